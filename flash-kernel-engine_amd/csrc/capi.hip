@@ -1,0 +1,190 @@
+// capi.hip — extern "C" boundary of libfke_qgemm.so: argument validation,
+// kernel-family dispatch and the drop-in entry points.
+//
+// Error contract: arguments are validated first and rejected with
+// hipErrorInvalidValue before any HIP runtime call, so the checks run (and are
+// tested) without a GPU.  Otherwise the return value is the status of this
+// call's hipLaunchKernel (the reference returned cudaGetLastError() after its
+// launch, src/quantized_gemm.cu:74,138, which could also surface an earlier
+// sticky error).  No state is kept between calls.
+#include <cstdio>
+
+#include "fke_internal.h"
+
+namespace {
+
+using fke::GemmArgs;
+
+bool common_args_ok(const void* A, const void* B, const void* C, int M, int N, int K,
+                    int b_layout) {
+    if (!A || !B || !C) return false;
+    if (M < 1 || N < 1 || K < 1) return false;
+    if (b_layout != FKE_B_NK && b_layout != FKE_B_KN) return false;
+    return true;
+}
+
+bool i8_args_ok(const void* A, const void* B, const void* C, int M, int N, int K, int out_dtype,
+                int b_layout) {
+    return common_args_ok(A, B, C, M, N, K, b_layout) && out_dtype >= FKE_OUT_F32 &&
+           out_dtype <= FKE_OUT_I32;
+}
+
+bool f8_args_ok(const void* A, const void* B, const void* C, int M, int N, int K, int out_dtype,
+                int b_layout) {
+    return common_args_ok(A, B, C, M, N, K, b_layout) &&
+           (out_dtype == FKE_OUT_F32 || out_dtype == FKE_OUT_BF16);
+}
+
+GemmArgs make_args(const void* A, const void* B, void* C, int M, int N, int K, const float* scale_a,
+                   const float* scale_b, float sa, float sb, const float* bias, int out_dtype,
+                   int b_layout) {
+    GemmArgs p;
+    p.A = A;
+    p.B = B;
+    p.C = C;
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    p.scale_a = scale_a;
+    p.scale_b = scale_b;
+    p.sa = sa;
+    p.sb = sb;
+    p.bias = bias;
+    p.out_dtype = out_dtype;
+    p.b_layout = b_layout;
+    return p;
+}
+
+int pick_i8(const GemmArgs& p) {
+    if (p.M <= 16 && fke::gemv_i8_supports(p)) return FKE_PATH_GEMV;
+    if (fke::mfma_supports(p, fke::ELEM_I8)) return FKE_PATH_MFMA;
+    return FKE_PATH_GENERIC;
+}
+
+int pick_f8(const GemmArgs& p) {
+    if (fke::mfma_supports(p, fke::ELEM_F8)) return FKE_PATH_MFMA;
+    return FKE_PATH_GENERIC;
+}
+
+int run_i8(int path, const GemmArgs& p, void* stream) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (path == FKE_PATH_AUTO) path = pick_i8(p);
+    switch (path) {
+        case FKE_PATH_GEMV:
+            if (!fke::gemv_i8_supports(p)) return hipErrorInvalidValue;
+            return fke::launch_gemv_i8(p, s);
+        case FKE_PATH_MFMA:
+            if (!fke::mfma_supports(p, fke::ELEM_I8)) return hipErrorInvalidValue;
+            return fke::launch_mfma(p, fke::ELEM_I8, s);
+        case FKE_PATH_GENERIC: return fke::launch_generic(p, fke::ELEM_I8, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+int run_f8(int path, const GemmArgs& p, void* stream) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (path == FKE_PATH_AUTO) path = pick_f8(p);
+    switch (path) {
+        case FKE_PATH_MFMA:
+            if (!fke::mfma_supports(p, fke::ELEM_F8)) return hipErrorInvalidValue;
+            return fke::launch_mfma(p, fke::ELEM_F8, s);
+        case FKE_PATH_GENERIC: return fke::launch_generic(p, fke::ELEM_F8, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+int fke_qgemm_i8_on_path(int path, const int8_t* A, const int8_t* B, void* C, int M, int N, int K,
+                         const float* scale_a, const float* scale_b, float sa, float sb,
+                         const float* bias, int out_dtype, int b_layout, void* stream) {
+    if (!i8_args_ok(A, B, C, M, N, K, out_dtype, b_layout)) return hipErrorInvalidValue;
+    return run_i8(path, make_args(A, B, C, M, N, K, scale_a, scale_b, sa, sb, bias, out_dtype, b_layout),
+                  stream);
+}
+
+int fke_qgemm_i8(const int8_t* A, const int8_t* B, void* C, int M, int N, int K, const float* scale_a,
+                 const float* scale_b, float sa, float sb, const float* bias, int out_dtype,
+                 int b_layout, void* stream) {
+    return fke_qgemm_i8_on_path(FKE_PATH_AUTO, A, B, C, M, N, K, scale_a, scale_b, sa, sb, bias,
+                                out_dtype, b_layout, stream);
+}
+
+int fke_qgemm_f8_on_path(int path, const uint8_t* A, const uint8_t* B, void* C, int M, int N, int K,
+                         float sa, float sb, const float* bias, int out_dtype, int b_layout,
+                         void* stream) {
+    if (!f8_args_ok(A, B, C, M, N, K, out_dtype, b_layout)) return hipErrorInvalidValue;
+    return run_f8(path, make_args(A, B, C, M, N, K, nullptr, nullptr, sa, sb, bias, out_dtype, b_layout),
+                  stream);
+}
+
+int fke_qgemm_f8(const uint8_t* A, const uint8_t* B, void* C, int M, int N, int K, float sa, float sb,
+                 const float* bias, int out_dtype, int b_layout, void* stream) {
+    return fke_qgemm_f8_on_path(FKE_PATH_AUTO, A, B, C, M, N, K, sa, sb, bias, out_dtype, b_layout,
+                                stream);
+}
+
+int fke_select_path_i8(const void* A, const void* B, const void* C, int M, int N, int K,
+                       int out_dtype, int b_layout) {
+    if (!i8_args_ok(A, B, C, M, N, K, out_dtype, b_layout)) return -1;
+    return pick_i8(make_args(A, B, const_cast<void*>(C), M, N, K, nullptr, nullptr, 1.f, 1.f, nullptr,
+                             out_dtype, b_layout));
+}
+
+int fke_select_path_f8(const void* A, const void* B, const void* C, int M, int N, int K,
+                       int out_dtype, int b_layout) {
+    if (!f8_args_ok(A, B, C, M, N, K, out_dtype, b_layout)) return -1;
+    return pick_f8(make_args(A, B, const_cast<void*>(C), M, N, K, nullptr, nullptr, 1.f, 1.f, nullptr,
+                             out_dtype, b_layout));
+}
+
+// Reference src/quantized_gemm.cu:56-75: B [N,K], fp32 out, alpha = sa*sb.
+int fke_launch_int8_gemm_dp4a(const int8_t* d_A, const int8_t* d_B, float* d_C, float scale_a,
+                              float scale_b, int M, int N, int K, void* stream) {
+    if (K % 4 != 0) return hipErrorInvalidValue;
+    return fke_qgemm_i8(d_A, d_B, d_C, M, N, K, nullptr, nullptr, scale_a, scale_b, nullptr,
+                        FKE_OUT_F32, FKE_B_NK, stream);
+}
+
+// Reference src/quantized_gemm.cu:120-139: B [K,N], fp32 out, alpha = sa*sb.
+int fke_launch_fp8_gemm_scaled(const uint8_t* d_A, const uint8_t* d_B, float* d_C, float scale_a,
+                               float scale_b, int M, int N, int K, void* stream) {
+    return fke_qgemm_f8(d_A, d_B, d_C, M, N, K, scale_a, scale_b, nullptr, FKE_OUT_F32, FKE_B_KN,
+                        stream);
+}
+
+// Reference src/flash_engine_api.cu:7-27, with the properties that matter on
+// CDNA (architecture name, CUs, wavefront size, LDS).
+int fke_print_device_info(int device_id) {
+    hipDeviceProp_t prop;
+    hipError_t err = hipGetDeviceProperties(&prop, device_id);
+    if (err != hipSuccess) return err;
+    printf("========================================================\n");
+    printf(" FlashKernel-Engine (MI355X build) GPU Diagnostics\n");
+    printf("========================================================\n");
+    printf(" Device:                        %s\n", prop.name);
+    printf(" Architecture:                  %s\n", prop.gcnArchName);
+    printf(" Compute Units:                 %d\n", prop.multiProcessorCount);
+    printf(" Wavefront Size:                %d\n", prop.warpSize);
+    printf(" Max Threads Per CU:            %d\n", prop.maxThreadsPerMultiProcessor);
+    printf(" Max Threads Per Block:         %d\n", prop.maxThreadsPerBlock);
+    printf(" LDS Per Block:                 %.1f KB\n", prop.sharedMemPerBlock / 1024.0);
+    printf(" LDS Per CU:                    %.1f KB\n", prop.maxSharedMemoryPerMultiProcessor / 1024.0);
+    printf(" Total Global Memory:           %.2f GB\n", prop.totalGlobalMem / (1024.0 * 1024.0 * 1024.0));
+    printf(" Memory Bus Width:              %d bits\n", prop.memoryBusWidth);
+    printf(" Peak Memory Clock:             %.1f MHz\n", prop.memoryClockRate * 1e-3);
+    printf(" Peak Engine Clock:             %.1f MHz\n", prop.clockRate * 1e-3);
+    printf("========================================================\n");
+    fflush(stdout);
+    return hipSuccess;
+}
+
+const char* fke_version(void) { return "1.2.0"; }
+
+const char* fke_status_string(int status) {
+    return hipGetErrorString(static_cast<hipError_t>(status));
+}
+
+}  // extern "C"

@@ -1,0 +1,94 @@
+// fke_internal.h — shared definitions of the gfx950 quantized GEMM kernels.
+//
+// Device code here is written for CDNA4 (gfx950) only: 64-lane wavefronts,
+// MFMA matrix cores, 160 KiB of LDS per CU.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "fke_qgemm.h"
+
+namespace fke {
+
+// Arguments of one GEMM call, passed by value to every kernel.
+struct GemmArgs {
+    const void* A;        // [M,K] int8 / e4m3 codes
+    const void* B;        // [N,K] (NK) or [K,N] (KN)
+    void* C;              // [M,N] fp32 / bf16 / int32
+    int M, N, K;
+    const float* scale_a; // [M] or null (then sa)
+    const float* scale_b; // [N] or null (then sb)
+    float sa, sb;
+    const float* bias;    // [N] or null
+    int out_dtype;        // FKE_OUT_*
+    int b_layout;         // FKE_B_*
+};
+
+enum Elem { ELEM_I8 = 0, ELEM_F8 = 1 };
+
+// Launchers (return this launch's status; arguments already validated).
+hipError_t launch_generic(const GemmArgs& p, int elem, hipStream_t stream);
+hipError_t launch_gemv_i8(const GemmArgs& p, hipStream_t stream);
+hipError_t launch_mfma(const GemmArgs& p, int elem, hipStream_t stream);
+
+// Shape/alignment predicates of the fast families (host side).
+bool gemv_i8_supports(const GemmArgs& p);
+bool mfma_supports(const GemmArgs& p, int elem);
+
+// ---------------------------------------------------------------------------
+// Device helpers
+// ---------------------------------------------------------------------------
+
+// fp32 -> bf16 bits, round to nearest even (quiet NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float y) {
+    uint32_t u = __float_as_uint(y);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+}
+
+// E4M3 code -> fp32 following reference src/quantized_gemm.cu:81-97, built
+// from IEEE bits: exp==0 -> m*2^-9; 0x7F/0xFF -> +0.0; else
+// (1+m/8)*2^(e-7), i.e. fp32 exponent field e+120 and mantissa m<<20.
+__device__ __forceinline__ float e4m3_decode(uint32_t x) {
+    const uint32_t e = (x >> 3) & 0xFu;
+    const uint32_t m = x & 7u;
+    float v;
+    if (e == 0) {
+        v = static_cast<float>(m) * 0.001953125f;
+    } else if (e == 15 && m == 7) {
+        return 0.0f;
+    } else {
+        v = __uint_as_float(((e + 120u) << 23) | (m << 20));
+    }
+    return (x & 0x80u) ? -v : v;
+}
+
+// Replace every 0x7F / 0xFF byte of a packed word by 0x00, so that the MFMA
+// (which reads those codes as NaN) sees the reference's 0.0.
+__device__ __forceinline__ uint32_t e4m3_sanitize(uint32_t w) {
+    const uint32_t t = (w & 0x7F7F7F7Fu) ^ 0x7F7F7F7Fu;          // byte==0 iff code was x7F
+    const uint32_t z = ~(((t & 0x7F7F7F7Fu) + 0x7F7F7F7Fu) | t | 0x7F7F7F7Fu);  // 0x80 per zero byte
+    const uint32_t mask = (z >> 7) * 0xFFu;
+    return w & ~mask;
+}
+
+// Canonical fused epilogue: s = fp32(sa_m*sb_n); y = bias ? fma(v,s,bias) : v*s.
+__device__ __forceinline__ float epilogue_value(float v, float s, const float* bias, int n) {
+    return bias ? __builtin_fmaf(v, s, bias[n]) : v * s;
+}
+
+template <int OUT>
+__device__ __forceinline__ void store_out(void* C, size_t idx, float y, int32_t acc) {
+    if constexpr (OUT == FKE_OUT_F32) {
+        static_cast<float*>(C)[idx] = y;
+    } else if constexpr (OUT == FKE_OUT_BF16) {
+        static_cast<uint16_t*>(C)[idx] = f32_to_bf16_rne(y);
+    } else {
+        static_cast<int32_t*>(C)[idx] = acc;
+    }
+}
+
+}  // namespace fke

@@ -1,0 +1,171 @@
+// gemm_generic.hip — any-shape fallback GEMM (INT8 and FP8, both B layouts).
+//
+// Used when a call does not meet the fast families' shape/alignment needs
+// (e.g. K % 128 != 0 for prefill, odd K, unaligned pointers).  It keeps the
+// reference's arithmetic exactly:
+//   INT8 — reference src/quantized_gemm.cu:33-52 (int32 sum of byte products,
+//          here over the full K like tests/test_quantized_gemm.cu:43-45);
+//   FP8  — reference src/quantized_gemm.cu:109-116: each output is summed in
+//          fp32 over k = 0..K-1 in increasing order, so the result is
+//          bit-identical to the reference's sequential loop.
+// 64x64 output tile per 256-thread workgroup, 4x4 outputs per thread, K staged
+// through LDS 64 bytes at a time with bounds-checked byte loads (zero fill
+// past M/N/K adds exact zeros).
+#include "fke_internal.h"
+
+namespace fke {
+namespace {
+
+constexpr int T = 64;   // tile edge
+constexpr int KC = 64;  // K bytes per LDS stage
+
+template <int ELEM, int OUT>
+__global__ __launch_bounds__(256) void gemm_generic_kernel(GemmArgs p) {
+    const int tid = threadIdx.x;
+    const int tx = tid & 15, ty = tid >> 4;
+    const int m0 = blockIdx.y * T, n0 = blockIdx.x * T;
+    const int M = p.M, N = p.N, K = p.K;
+    const uint8_t* A = static_cast<const uint8_t*>(p.A);
+    const uint8_t* B = static_cast<const uint8_t*>(p.B);
+    const bool kn = p.b_layout == FKE_B_KN;
+
+    // INT8: packed 4-byte words (KC/4 per row, +1 pad); FP8: decoded floats.
+    __shared__ int32_t Aw[ELEM == ELEM_I8 ? T : 1][KC / 4 + 1];
+    __shared__ int32_t Bw[ELEM == ELEM_I8 ? T : 1][KC / 4 + 1];
+    __shared__ float Af[ELEM == ELEM_F8 ? T : 1][KC + 1];
+    __shared__ float Bf[ELEM == ELEM_F8 ? T : 1][KC + 1];
+
+    int32_t iacc[4][4];
+    float facc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            iacc[i][j] = 0;
+            facc[i][j] = 0.0f;
+        }
+
+    for (int k0 = 0; k0 < K; k0 += KC) {
+        // Stage: thread t loads 16 bytes of A (row t/4, bytes 16*(t%4)..) and
+        // 16 bytes of B for one (n row, 16 k) slice.
+        {
+            const int r = tid >> 2, kq = (tid & 3) * 16;
+            const int m = m0 + r;
+            uint8_t a[16];
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const int k = k0 + kq + q;
+                a[q] = (m < M && k < K) ? A[static_cast<size_t>(m) * K + k] : 0;
+            }
+            uint8_t b[16];
+            int bn, bk;
+            if (kn) {  // coalesce along n: thread t -> column t%64, k block t/64
+                bn = tid & 63;
+                bk = (tid >> 6) * 16;
+            } else {
+                bn = r;
+                bk = kq;
+            }
+            const int n = n0 + bn;
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const int k = k0 + bk + q;
+                uint8_t v = 0;
+                if (n < N && k < K)
+                    v = kn ? B[static_cast<size_t>(k) * N + n] : B[static_cast<size_t>(n) * K + k];
+                b[q] = v;
+            }
+            if constexpr (ELEM == ELEM_I8) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    Aw[r][kq / 4 + q] = static_cast<int32_t>(a[4 * q] | (a[4 * q + 1] << 8) |
+                                                             (a[4 * q + 2] << 16) |
+                                                             (static_cast<uint32_t>(a[4 * q + 3]) << 24));
+                    Bw[bn][bk / 4 + q] = static_cast<int32_t>(b[4 * q] | (b[4 * q + 1] << 8) |
+                                                              (b[4 * q + 2] << 16) |
+                                                              (static_cast<uint32_t>(b[4 * q + 3]) << 24));
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < 16; ++q) {
+                    Af[r][kq + q] = e4m3_decode(a[q]);
+                    Bf[bn][bk + q] = e4m3_decode(b[q]);
+                }
+            }
+        }
+        __syncthreads();
+        if constexpr (ELEM == ELEM_I8) {
+#pragma unroll 4
+            for (int kw = 0; kw < KC / 4; ++kw) {
+                int32_t a[4], b[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) a[i] = Aw[ty * 4 + i][kw];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) b[j] = Bw[tx * 4 + j][kw];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        iacc[i][j] = __builtin_amdgcn_sdot4(a[i], b[j], iacc[i][j], false);
+            }
+        } else {
+            const int kend = min(KC, K - k0);  // reference order: k ascending, stop at K
+            for (int k = 0; k < kend; ++k) {
+                float a[4], b[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) a[i] = Af[ty * 4 + i][k];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) b[j] = Bf[tx * 4 + j][k];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) facc[i][j] += a[i] * b[j];  // exact product
+            }
+        }
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = m0 + ty * 4 + i;
+        if (m >= M) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int n = n0 + tx * 4 + j;
+            if (n >= N) continue;
+            const size_t idx = static_cast<size_t>(m) * N + n;
+            if constexpr (ELEM == ELEM_I8) {
+                const float s = (p.scale_a ? p.scale_a[m] : p.sa) * (p.scale_b ? p.scale_b[n] : p.sb);
+                store_out<OUT>(p.C, idx, epilogue_value(static_cast<float>(iacc[i][j]), s, p.bias, n),
+                               iacc[i][j]);
+            } else {
+                store_out<OUT>(p.C, idx, epilogue_value(facc[i][j], p.sa * p.sb, p.bias, n), 0);
+            }
+        }
+    }
+}
+
+template <int ELEM, int OUT>
+hipError_t launch_t(const GemmArgs& p, hipStream_t stream) {
+    GemmArgs a = p;
+    void* args[] = {&a};
+    const dim3 grid((p.N + T - 1) / T, (p.M + T - 1) / T);
+    return hipLaunchKernel(reinterpret_cast<const void*>(&gemm_generic_kernel<ELEM, OUT>), grid,
+                           dim3(256), args, 0, stream);
+}
+
+}  // namespace
+
+hipError_t launch_generic(const GemmArgs& p, int elem, hipStream_t s) {
+    if (elem == ELEM_I8) {
+        switch (p.out_dtype) {
+            case FKE_OUT_F32: return launch_t<ELEM_I8, FKE_OUT_F32>(p, s);
+            case FKE_OUT_BF16: return launch_t<ELEM_I8, FKE_OUT_BF16>(p, s);
+            default: return launch_t<ELEM_I8, FKE_OUT_I32>(p, s);
+        }
+    }
+    return p.out_dtype == FKE_OUT_F32 ? launch_t<ELEM_F8, FKE_OUT_F32>(p, s)
+                                      : launch_t<ELEM_F8, FKE_OUT_BF16>(p, s);
+}
+
+}  // namespace fke

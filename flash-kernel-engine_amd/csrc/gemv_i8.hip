@@ -1,0 +1,152 @@
+// gemv_i8.hip — W8A8 decode path (M <= 16, B stored [N,K]).
+//
+// Same arithmetic as reference src/quantized_gemm.cu:15-54 (exact int32 dot
+// products, the fused epilogue applied after), re-shaped for an HBM-bound
+// problem: the B panel is streamed once with 128-bit coalesced loads and no
+// MFMA is used.
+//
+// Workgroup = 4 waves = R consecutive B rows (output columns n0..n0+R-1).
+// The K bytes of a row are split in four quarters, one per wave (split-K);
+// lane l of a wave reads 16-byte chunks l, l+64, ... of its quarter, so each
+// load instruction of a wave covers 1 KiB of contiguous bytes of one row.
+// The wave keeps its A chunks (MT rows x 16 bytes) in registers and issues
+// the R row loads back to back before any arithmetic.
+// Partial int32 sums (R x MT per lane) are reduced across the 256 threads
+// through LDS: every thread writes its partials, then G = 256/(R*MT)
+// consecutive lanes sum one output's 256 partials and finish with a DPP/
+// swizzle butterfly inside the wave.  Integer addition is associative, so any
+// split and order is bit-exact.
+#include "fke_internal.h"
+
+namespace fke {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int32_t dot16(v4i a, v4i b, int32_t acc) {
+    acc = __builtin_amdgcn_sdot4(a[0], b[0], acc, false);
+    acc = __builtin_amdgcn_sdot4(a[1], b[1], acc, false);
+    acc = __builtin_amdgcn_sdot4(a[2], b[2], acc, false);
+    acc = __builtin_amdgcn_sdot4(a[3], b[3], acc, false);
+    return acc;
+}
+
+// Sum over groups of G consecutive lanes (G a power of two <= 64); every lane
+// of the group ends with the group sum.
+template <int G>
+__device__ __forceinline__ int32_t group_sum(int32_t v) {
+    if constexpr (G >= 2) v += __shfl_xor(v, 1);
+    if constexpr (G >= 4) v += __shfl_xor(v, 2);
+    if constexpr (G >= 8) v += __shfl_xor(v, 4);
+    if constexpr (G >= 16) v += __shfl_xor(v, 8);
+    if constexpr (G >= 32) v += __shfl_xor(v, 16);
+    if constexpr (G >= 64) v += __shfl_xor(v, 32);
+    return v;
+}
+
+template <int MT, int R, int OUT>
+__global__ __launch_bounds__(256) void gemv_i8_kernel(GemmArgs p) {
+    constexpr int V = R * MT;      // outputs per workgroup
+    constexpr int G = 256 / V;     // threads per output in the final sum
+    constexpr int S = 256 / G;     // partials each of those threads adds (= V)
+    static_assert(V >= 4 && V <= 64 && (V & (V - 1)) == 0, "R*MT must be a power of two in [4,64]");
+    __shared__ __attribute__((aligned(16))) int32_t red[4 * V * 64];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int M = p.M, N = p.N, K = p.K;
+    const int n0 = blockIdx.x * R;
+    const int8_t* A = static_cast<const int8_t*>(p.A);
+    const int8_t* B = static_cast<const int8_t*>(p.B);
+
+    const int cpw = K >> 6;  // 16-byte chunks per wave quarter (K % 64 == 0)
+    const int c_begin = wave * cpw, c_end = c_begin + cpw;
+
+    int32_t acc[R][MT];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[r][m] = 0;
+
+    for (int c = c_begin + lane; c < c_end; c += 64) {
+        v4i b[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int n = min(n0 + r, N - 1);  // rows past N repeat the last row; never stored
+            b[r] = __builtin_nontemporal_load(
+                reinterpret_cast<const v4i*>(B + static_cast<size_t>(n) * K) + c);
+        }
+        v4i a[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+            a[m] = (m < M) ? *(reinterpret_cast<const v4i*>(A + static_cast<size_t>(m) * K) + c)
+                           : v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int m = 0; m < MT; ++m) acc[r][m] = dot16(a[m], b[r], acc[r][m]);
+    }
+
+    // red[(wave*V + v)*64 + lane]: conflict-free writes, contiguous reads.
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) red[(wave * V + r * MT + m) * 64 + lane] = acc[r][m];
+    __syncthreads();
+
+    // Output v = tid / G sums partials e in [part*S, part*S+S) of the 256
+    // (wave, lane) partials; S divides 64, so a run stays inside one wave row.
+    const int v = tid / G, part = tid % G;
+    const int e0 = part * S;
+    const int w = e0 >> 6, l0 = e0 & 63;
+    const int32_t* src = red + (w * V + v) * 64 + l0;
+    int32_t s = 0;
+#pragma unroll
+    for (int q = 0; q < S; q += 4) {
+        const v4i x = *reinterpret_cast<const v4i*>(src + q);
+        s += x[0] + x[1] + x[2] + x[3];
+    }
+    s = group_sum<G>(s);
+
+    if (part == 0) {
+        const int r = v / MT, m = v % MT;
+        const int n = n0 + r;
+        if (m < M && n < N) {
+            const float sc = (p.scale_a ? p.scale_a[m] : p.sa) * (p.scale_b ? p.scale_b[n] : p.sb);
+            store_out<OUT>(p.C, static_cast<size_t>(m) * N + n,
+                           epilogue_value(static_cast<float>(s), sc, p.bias, n), s);
+        }
+    }
+}
+
+template <int MT, int R>
+hipError_t launch_t(const GemmArgs& p, hipStream_t stream) {
+    GemmArgs a = p;
+    void* args[] = {&a};
+    const dim3 grid((p.N + R - 1) / R);
+    const void* f;
+    switch (p.out_dtype) {
+        case FKE_OUT_F32: f = reinterpret_cast<const void*>(&gemv_i8_kernel<MT, R, FKE_OUT_F32>); break;
+        case FKE_OUT_BF16: f = reinterpret_cast<const void*>(&gemv_i8_kernel<MT, R, FKE_OUT_BF16>); break;
+        default: f = reinterpret_cast<const void*>(&gemv_i8_kernel<MT, R, FKE_OUT_I32>); break;
+    }
+    return hipLaunchKernel(f, grid, dim3(256), args, 0, stream);
+}
+
+}  // namespace
+
+bool gemv_i8_supports(const GemmArgs& p) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p.A), b = reinterpret_cast<uintptr_t>(p.B);
+    return p.M >= 1 && p.M <= 16 && p.N >= 1 && p.K >= 64 && p.K % 64 == 0 &&
+           p.b_layout == FKE_B_NK && ((a | b) & 15) == 0;
+}
+
+hipError_t launch_gemv_i8(const GemmArgs& p, hipStream_t s) {
+    if (p.M <= 1) return launch_t<1, 16>(p, s);
+    if (p.M <= 2) return launch_t<2, 16>(p, s);
+    if (p.M <= 4) return launch_t<4, 8>(p, s);
+    if (p.M <= 8) return launch_t<8, 8>(p, s);
+    return launch_t<16, 4>(p, s);
+}
+
+}  // namespace fke

@@ -1,0 +1,147 @@
+"""Quantized GEMM operations of the MI355X build (torch tensors on a ROCm GPU).
+
+`quantized_gemm_int8` keeps the signature and the arithmetic of reference
+python/flash_engine/ops.py:180-186 (C = (A_int8 @ B_int8) * (scale_a*scale_b),
+B stored [K,N], fp32 result) but runs the HIP kernels of libfke_qgemm.so
+through its C ABI; host (numpy) inputs are copied to the GPU and the result
+copied back.  The checks before each call follow the reference binding idiom
+(python/bindings.cpp:101-133: device/shape checks, a fresh output tensor, the
+current stream).  There is no CPU compute path: without the built library the
+import of the library raises.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import B_KN, B_NK, OUT_BF16, OUT_F32, OUT_I32, PATH_AUTO, PATH_GEMV, PATH_GENERIC, PATH_MFMA
+
+_OUT_CODES = {torch.float32: OUT_F32, torch.bfloat16: OUT_BF16, torch.int32: OUT_I32}
+_LAYOUTS = {"nk": B_NK, "kn": B_KN}
+_PATHS = {"auto": PATH_AUTO, "gemv": PATH_GEMV, "mfma": PATH_MFMA, "generic": PATH_GENERIC}
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _check_dev(name: str, t: torch.Tensor, dtype, device) -> None:
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise TypeError(f"{name} must be a GPU tensor")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if t.device != device:
+        raise ValueError(f"{name} is on {t.device}, expected {device}")
+
+
+def _check_vec(name: str, t, n: int, device) -> None:
+    if t is None:
+        return
+    _check_dev(name, t, torch.float32, device)
+    if t.numel() != n:
+        raise ValueError(f"{name} must have {n} elements, got {t.numel()}")
+
+
+def w8a8_gemm(A: torch.Tensor, B: torch.Tensor, scale_a=None, scale_b=None, bias=None,
+              out_dtype=torch.bfloat16, b_layout: str = "nk", sa: float = 1.0, sb: float = 1.0,
+              path: str = "auto", out: torch.Tensor | None = None) -> torch.Tensor:
+    """W8A8 INT8 GEMM with the fused epilogue.
+
+    acc = A[M,K] . B  (exact int32; B is [N,K] for b_layout="nk", [K,N] for "kn")
+    y   = fp32(acc) * fp32(scale_a[m] * scale_b[n])  (+ bias[n] via one fma)
+    out = y as fp32 / bf16 (round to nearest even), or acc as int32.
+    scale_a [M], scale_b [N], bias [N] are fp32 GPU tensors or None (then the
+    scalars sa / sb apply to every row / column).
+    """
+    dev = A.device
+    _check_dev("A", A, torch.int8, dev)
+    _check_dev("B", B, torch.int8, dev)
+    if A.dim() != 2 or B.dim() != 2:
+        raise ValueError("A and B must be 2-D")
+    layout = _LAYOUTS[b_layout]
+    M, K = A.shape
+    N, KB = (B.shape[0], B.shape[1]) if layout == B_NK else (B.shape[1], B.shape[0])
+    if KB != K:
+        raise ValueError(f"K mismatch: A has {K}, B has {KB}")
+    _check_vec("scale_a", scale_a, M, dev)
+    _check_vec("scale_b", scale_b, N, dev)
+    _check_vec("bias", bias, N, dev)
+    code = _OUT_CODES[out_dtype]
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=dev)
+    else:
+        _check_dev("out", out, out_dtype, dev)
+        if tuple(out.shape) != (M, N):
+            raise ValueError("out has the wrong shape")
+    st = _lib.lib().fke_qgemm_i8_on_path(
+        _PATHS[path], A.data_ptr(), B.data_ptr(), out.data_ptr(), M, N, K, _ptr(scale_a),
+        _ptr(scale_b), sa, sb, _ptr(bias), code, layout, _stream(A))
+    _lib.check(st, "fke_qgemm_i8")
+    return out
+
+
+def fp8_gemm_scaled(A: torch.Tensor, B: torch.Tensor, scale_a: float, scale_b: float, bias=None,
+                    out_dtype=torch.float32, b_layout: str = "kn", path: str = "auto",
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """Scaled FP8 E4M3 GEMM (reference src/quantized_gemm.cu:99-139).
+
+    sum = sum_k dec(A[m,k]) * dec(B(k,n)) in fp32, y = sum * fp32(scale_a*scale_b)
+    (+ bias[n] via one fma); codes 0x7F/0xFF decode to 0.0 like the reference.
+    A is [M,K] and B is [K,N] ("kn", the reference layout) or [N,K] ("nk"),
+    as torch.uint8 codes or torch.float8_e4m3fn.
+    """
+    dev = A.device
+    if A.dtype == torch.float8_e4m3fn:
+        A = A.view(torch.uint8)
+    if B.dtype == torch.float8_e4m3fn:
+        B = B.view(torch.uint8)
+    _check_dev("A", A, torch.uint8, dev)
+    _check_dev("B", B, torch.uint8, dev)
+    layout = _LAYOUTS[b_layout]
+    M, K = A.shape
+    N, KB = (B.shape[0], B.shape[1]) if layout == B_NK else (B.shape[1], B.shape[0])
+    if KB != K:
+        raise ValueError(f"K mismatch: A has {K}, B has {KB}")
+    _check_vec("bias", bias, N, dev)
+    if out_dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError("FP8 GEMM writes fp32 or bf16")
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=dev)
+    else:
+        _check_dev("out", out, out_dtype, dev)
+    st = _lib.lib().fke_qgemm_f8_on_path(
+        _PATHS[path], A.data_ptr(), B.data_ptr(), out.data_ptr(), M, N, K, scale_a, scale_b,
+        _ptr(bias), _OUT_CODES[out_dtype], layout, _stream(A))
+    _lib.check(st, "fke_qgemm_f8")
+    return out
+
+
+def quantized_gemm_int8(A, B, scale_a: float = 1.0, scale_b: float = 1.0):
+    """C = (A_int8 @ B_int8) * (scale_a * scale_b), B stored [K,N], fp32 out.
+
+    Same signature and result as reference python/flash_engine/ops.py:180-186:
+    the scale product is formed in double (Python floats) and applied as fp32,
+    the int32 product is exact.  GPU tensors stay on the GPU; numpy arrays are
+    copied to cuda:0 and the result is returned as a numpy array.
+    """
+    host = isinstance(A, np.ndarray)
+    if host:
+        A = torch.from_numpy(np.ascontiguousarray(A, dtype=np.int8)).cuda()
+        B = torch.from_numpy(np.ascontiguousarray(B, dtype=np.int8)).cuda()
+    alpha = float(np.float32(float(scale_a) * float(scale_b)))
+    out = w8a8_gemm(A.contiguous(), B.contiguous(), out_dtype=torch.float32, b_layout="kn",
+                    sa=alpha, sb=1.0)
+    if host:
+        return out.cpu().numpy()
+    return out
+
+
+def print_device_info(device_id: int = 0) -> None:
+    _lib.check(_lib.lib().fke_print_device_info(device_id), "fke_print_device_info")

@@ -1,0 +1,130 @@
+/*
+ * fke_qgemm.h — C ABI of the MI355X (gfx950) quantized GEMM library
+ * (libfke_qgemm.so).  Plain pointers, sizes and an opaque stream; no C++ or
+ * torch types.  Every entry point returns a hipError_t value as int:
+ * 0 = hipSuccess, 1 = hipErrorInvalidValue (argument rejected before any HIP
+ * call), otherwise the status of this call's kernel launch.
+ *
+ * Conventions shared by all GEMM entry points (reference:
+ * flash-kernel-engine include/quantized_gemm.cuh:6-41, src/quantized_gemm.cu):
+ *   - A, B, C, scale and bias pointers are caller-owned DEVICE buffers; the
+ *     library allocates nothing and frees nothing.  C is fully overwritten.
+ *   - All matrices are row-major.  A is [M,K].  B is [N,K] (FKE_B_NK,
+ *     K-contiguous per output column) or [K,N] (FKE_B_KN).  C is [M,N].
+ *   - The call is asynchronous on `stream` (a hipStream_t; NULL = the null
+ *     stream) and never synchronises.  No mutable global state: calls are
+ *     re-entrant from any host thread.
+ */
+#ifndef FKE_QGEMM_H
+#define FKE_QGEMM_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Output element type of the fused epilogue. */
+enum fke_out_dtype {
+    FKE_OUT_F32 = 0,  /* fp32 y                                  */
+    FKE_OUT_BF16 = 1, /* bf16, round-to-nearest-even of fp32 y   */
+    FKE_OUT_I32 = 2   /* raw int32 accumulator (INT8 GEMM only)  */
+};
+
+/* Storage order of B. */
+enum fke_b_layout {
+    FKE_B_NK = 0, /* B[n*K + k] */
+    FKE_B_KN = 1  /* B[k*N + n] */
+};
+
+/* Kernel family used by a call (for tests and benchmarks). */
+enum fke_path {
+    FKE_PATH_AUTO = 0,    /* dispatcher's choice                                */
+    FKE_PATH_GEMV = 1,    /* M<=16 split-K wavefront-reduction GEMV (INT8, NK)  */
+    FKE_PATH_MFMA = 2,    /* LDS-staged MFMA GEMM (INT8 i32 / FP8 f32 acc)      */
+    FKE_PATH_GENERIC = 3  /* any-shape tiled fallback (exact reference order)   */
+};
+
+/*
+ * Drop-in for flash_engine::quantized::launch_int8_gemm_dp4a
+ * (reference include/quantized_gemm.cuh:19-27, src/quantized_gemm.cu:56-75):
+ * C[m,n] = float(sum_k A[m,k]*B[n,k]) * fp32(scale_a*scale_b); B is [N,K]; C fp32.
+ * Rejects M,N,K <= 0, K % 4 != 0 (where the reference kernel truncates K and
+ * misaligns rows) and NULL pointers with hipErrorInvalidValue.
+ */
+int fke_launch_int8_gemm_dp4a(const int8_t* d_A, const int8_t* d_B, float* d_C,
+                              float scale_a, float scale_b, int M, int N, int K,
+                              void* stream);
+
+/*
+ * Drop-in for flash_engine::quantized::launch_fp8_gemm_scaled
+ * (reference include/quantized_gemm.cuh:30-38, src/quantized_gemm.cu:120-139):
+ * C[m,n] = (sum_k dec(A[m,k])*dec(B[k,n])) * fp32(scale_a*scale_b) with OCP
+ * E4M3 decode and the reference's 0x7F/0xFF -> 0.0 rule; B is [K,N]; C fp32;
+ * fp32 accumulation.
+ */
+int fke_launch_fp8_gemm_scaled(const uint8_t* d_A, const uint8_t* d_B, float* d_C,
+                               float scale_a, float scale_b, int M, int N, int K,
+                               void* stream);
+
+/*
+ * W8A8 INT8 GEMM with the fused epilogue (extends reference
+ * src/quantized_gemm.cu:15-75; per-row/per-column scales, bias and the bf16/i32
+ * outputs have no reference counterpart and reduce to it when uniform):
+ *   acc[m,n] = sum_{k<K} A[m,k]*B(n,k)                  (exact int32)
+ *   s        = fp32(sa_m * sb_n)   sa_m = scale_a ? scale_a[m] : sa
+ *                                  sb_n = scale_b ? scale_b[n] : sb
+ *   y        = bias ? fmaf(fp32(acc), s, bias[n]) : fp32(acc) * s
+ *   C        = y (F32) | bf16_rne(y) (BF16) | acc (I32)
+ * Any K >= 1.  scale_a is [M], scale_b and bias are [N] (fp32, device).
+ */
+int fke_qgemm_i8(const int8_t* A, const int8_t* B, void* C, int M, int N, int K,
+                 const float* scale_a, const float* scale_b, float sa, float sb,
+                 const float* bias, int out_dtype, int b_layout, void* stream);
+
+/* Same as fke_qgemm_i8 on an explicit kernel family (enum fke_path).  Returns
+ * hipErrorInvalidValue when that family cannot run the given shape/layout/
+ * alignment.  Used by tests to cross-check kernel families. */
+int fke_qgemm_i8_on_path(int path, const int8_t* A, const int8_t* B, void* C,
+                         int M, int N, int K, const float* scale_a, const float* scale_b,
+                         float sa, float sb, const float* bias, int out_dtype,
+                         int b_layout, void* stream);
+
+/*
+ * Scaled FP8 E4M3 GEMM with the fused epilogue (extends reference
+ * src/quantized_gemm.cu:99-139): sum = sum_k dec(A[m,k])*dec(B(k,n)) in fp32,
+ * y = bias ? fmaf(sum, fp32(sa*sb), bias[n]) : sum * fp32(sa*sb);
+ * C = y (F32) | bf16_rne(y) (BF16).  Codes 0x7F/0xFF decode to 0.0 as in the
+ * reference.  The MFMA family sums in a different order than the reference's
+ * sequential loop (each product is exact; only fp32 rounding of the sum
+ * differs); the GENERIC family keeps the reference's sequential k order.
+ */
+int fke_qgemm_f8(const uint8_t* A, const uint8_t* B, void* C, int M, int N, int K,
+                 float sa, float sb, const float* bias, int out_dtype, int b_layout,
+                 void* stream);
+
+int fke_qgemm_f8_on_path(int path, const uint8_t* A, const uint8_t* B, void* C,
+                         int M, int N, int K, float sa, float sb, const float* bias,
+                         int out_dtype, int b_layout, void* stream);
+
+/* The family fke_qgemm_i8 / fke_qgemm_f8 would pick (enum fke_path), or -1
+ * for arguments they would reject.  Pure host logic; needs no GPU. */
+int fke_select_path_i8(const void* A, const void* B, const void* C, int M, int N, int K,
+                       int out_dtype, int b_layout);
+int fke_select_path_f8(const void* A, const void* B, const void* C, int M, int N, int K,
+                       int out_dtype, int b_layout);
+
+/* Replaces flash_engine::print_device_info (reference include/flash_engine.h:29,
+ * src/flash_engine_api.cu:7-27): prints the device's properties to stdout. */
+int fke_print_device_info(int device_id);
+
+/* Replaces flash_engine::get_version (reference include/flash_engine.h:24-26). */
+const char* fke_version(void);
+
+/* Human-readable name for a status returned above. */
+const char* fke_status_string(int status);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FKE_QGEMM_H */

@@ -1,0 +1,92 @@
+/*
+ * fke_oracle.h — CPU restatement of flash-kernel-engine's quantized GEMM path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the shipped library links or calls this
+ * code; it is the checker used by tests/, by __graft_entry__.smoke() and by the
+ * cpu_baseline leg of bench.py.  Every function names the reference file:line
+ * it restates (paths relative to the reference repository root).
+ *
+ * Pinning (how each function is checked, see tests/test_oracle.py):
+ *   fko_ref_host_gemm_i8      KAT64 golden values from the reference test's
+ *                             closed-form inputs; brute force vs double math.
+ *   fko_ref_kernel_gemm_i8    equals fko_ref_host_gemm_i8 for K%4==0 (closed
+ *                             form); K%4!=0 truncation/misalignment by a
+ *                             hand-derived tiny case.
+ *   fko_e4m3_decode           exhaustive 256-code table vs the OCP E4M3 closed
+ *                             form (exact powers of two) incl. 0x7F/0xFF -> 0.
+ *   fko_ref_kernel_gemm_f8    brute force with exact (double) products, order
+ *                             check against a hand-computed rounding case.
+ *   fko_ref_py_gemm_i8        numpy int32 matmul closed form.
+ *   fko_w8a8_*                reduction to the reference when scales are
+ *                             uniform / bias absent / fp32 out; bf16 RNE known
+ *                             answers; exact-integer checksums.
+ *   generators                fixed known-answer streams (SplitMix64 KAT).
+ */
+#ifndef FKE_ORACLE_H
+#define FKE_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- seeded generators (synthetic inputs; no reference counterpart) ---- */
+uint64_t fko_splitmix64(uint64_t* state);
+void fko_gen_i8_uniform(int8_t* dst, size_t n, uint64_t seed);            /* (u%255)-127        */
+void fko_gen_i8_clipped_normal(int8_t* dst, size_t n, uint64_t seed,
+                               double sigma);                              /* clamp(rint(s*z))   */
+void fko_gen_f32_uniform(float* dst, size_t n, uint64_t seed, double lo, double hi);
+void fko_gen_f32_normal(float* dst, size_t n, uint64_t seed, double mu, double sigma);
+
+/* ---- reference restatements ---- */
+/* tests/test_quantized_gemm.cu:39-48 — full-K int32 triple loop, B is [N,K]. */
+void fko_ref_host_gemm_i8(const int8_t* A, const int8_t* B, float* C,
+                          int M, int N, int K, float scale_a, float scale_b);
+/* src/quantized_gemm.cu:15-54,68 — the device kernel's arithmetic, including
+ * its K/4 word truncation and int32 row reinterpretation. */
+void fko_ref_kernel_gemm_i8(const int8_t* A, const int8_t* B, float* C,
+                            int M, int N, int K, float scale_a, float scale_b);
+/* src/quantized_gemm.cu:81-97 */
+float fko_e4m3_decode(uint8_t x);
+/* src/quantized_gemm.cu:99-118,132 — sequential-k fp32 sum, B is [K,N]. */
+void fko_ref_kernel_gemm_f8(const uint8_t* A, const uint8_t* B, float* C,
+                            int M, int N, int K, float scale_a, float scale_b);
+/* python/flash_engine/ops.py:180-186 — B is [K,N]; scale product in double. */
+void fko_ref_py_gemm_i8(const int8_t* A, const int8_t* B, float* C,
+                        int M, int N, int K, double scale_a, double scale_b);
+
+/* ---- extended W8A8 path (per-token x per-channel scales, bias, out dtype) ---- */
+enum { FKO_OUT_F32 = 0, FKO_OUT_BF16 = 1, FKO_OUT_I32 = 2 };
+enum { FKO_B_NK = 0, FKO_B_KN = 1 };
+
+/* exact int32 accumulators acc[m,n] = sum_k A[m,k]*B(n,k) for the listed rows
+ * (rows==NULL -> all M rows, nrows ignored).  acc is [nrows or M, N]. */
+void fko_w8a8_acc(const int8_t* A, const int8_t* B, int32_t* acc,
+                  int M, int N, int K, int b_layout,
+                  const int* rows, int nrows, int nthreads);
+/* canonical epilogue: s = fp32(sa_m*sb_n); y = bias ? fmaf(fp32(acc),s,bias_n)
+ * : fp32(acc)*s; out = y (f32) | bf16_rne(y) | acc (i32).  scale_a/scale_b may
+ * be NULL (then the scalars sa/sb are used for every row/column). `rows`
+ * maps acc row r to problem row rows[r] for scale_a lookup (NULL: identity). */
+void fko_w8a8_epilogue(const int32_t* acc, void* out, int R, int N,
+                       const float* scale_a, const float* scale_b, float sa, float sb,
+                       const float* bias, int out_dtype, const int* rows);
+/* fp8 with the same epilogue over the reference's sequential fp32 sum:
+ * y = sum*fp32(sa*sb) (+bias via fmaf), out f32|bf16. */
+void fko_f8_gemm(const uint8_t* A, const uint8_t* B, void* out, int M, int N, int K,
+                 float sa, float sb, const float* bias, int out_dtype, int b_layout,
+                 const int* rows, int nrows, int nthreads);
+
+uint16_t fko_f32_to_bf16_rne(float x);
+float fko_bf16_to_f32(uint16_t h);
+/* saturating round-to-nearest-even fp32 -> OCP E4M3 (never emits 0x7F/0xFF) */
+uint8_t fko_f32_to_e4m3_sat(float x);
+/* per-tensor quantiser of the FP8 config: s = amax/448, q = e4m3_sat(x/s). */
+float fko_quantize_e4m3(const float* x, uint8_t* q, size_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,118 @@
+"""CPU tests of the C-ABI boundary (libfke_qgemm.so): it loads, exports every
+symbol include/fke_qgemm.h declares, rejects bad arguments with
+hipErrorInvalidValue before any HIP call, and dispatches shapes to the
+expected kernel family.  No GPU compute is issued here."""
+import os
+import re
+import subprocess
+
+import pytest
+
+from flash_engine import _lib
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "fke_qgemm.h")
+DROPIN = os.path.join(REPO, "flash-kernel-engine_amd", "_build", "test_quantized_gemm_dropin")
+INVALID = _lib.HIP_ERROR_INVALID_VALUE
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(fke_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_loads_and_exports_header_symbols():
+    L = _lib.lib()
+    syms = declared_symbols()
+    assert len(syms) >= 10
+    for s in syms:
+        assert hasattr(L, s), f"missing export {s}"
+    assert set(syms) == set(_lib.SIGNATURES), "ctypes table out of sync with the header"
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r" T (fke_\w+)", out))
+    assert set(syms) <= exported
+
+
+def test_version_and_status_strings():
+    assert _lib.version() == "1.2.0"
+    assert "invalid" in _lib.status_string(INVALID).lower()
+
+
+P = 4096  # a fake, 16-byte aligned "device" address: never dereferenced here
+
+
+@pytest.mark.parametrize("M,N,K", [(0, 8, 8), (8, 0, 8), (8, 8, 0), (-1, 8, 8), (8, -3, 8)])
+def test_rejects_bad_sizes(M, N, K):
+    L = _lib.lib()
+    assert L.fke_qgemm_i8(P, P, P, M, N, K, None, None, 1.0, 1.0, None, 0, 0, None) == INVALID
+    assert L.fke_qgemm_f8(P, P, P, M, N, K, 1.0, 1.0, None, 0, 1, None) == INVALID
+    assert L.fke_launch_int8_gemm_dp4a(P, P, P, 1.0, 1.0, M, N, K, None) == INVALID
+    assert L.fke_launch_fp8_gemm_scaled(P, P, P, 1.0, 1.0, M, N, K, None) == INVALID
+
+
+def test_rejects_null_pointers_and_bad_enums():
+    L = _lib.lib()
+    for a, b, c in [(None, P, P), (P, None, P), (P, P, None)]:
+        assert L.fke_qgemm_i8(a, b, c, 8, 8, 8, None, None, 1.0, 1.0, None, 0, 0, None) == INVALID
+        assert L.fke_qgemm_f8(a, b, c, 8, 8, 8, 1.0, 1.0, None, 0, 0, None) == INVALID
+    assert L.fke_qgemm_i8(P, P, P, 8, 8, 8, None, None, 1.0, 1.0, None, 3, 0, None) == INVALID
+    assert L.fke_qgemm_i8(P, P, P, 8, 8, 8, None, None, 1.0, 1.0, None, 0, 2, None) == INVALID
+    assert L.fke_qgemm_f8(P, P, P, 8, 8, 8, 1.0, 1.0, None, _lib.OUT_I32, 0, None) == INVALID
+    assert L.fke_qgemm_i8_on_path(9, P, P, P, 8, 8, 8, None, None, 1.0, 1.0, None, 0, 0, None) == INVALID
+
+
+def test_dropin_int8_rejects_k_not_multiple_of_4():
+    """The reference kernel silently drops the K tail and misaligns rows when
+    K % 4 != 0 (src/quantized_gemm.cu:28-30); the drop-in rejects it."""
+    L = _lib.lib()
+    for K in (1, 2, 3, 5, 4097):
+        assert L.fke_launch_int8_gemm_dp4a(P, P, P, 1.0, 1.0, 8, 8, K, None) == INVALID
+
+
+def test_path_unavailable_for_shape_is_rejected():
+    L = _lib.lib()
+    # GEMV needs M <= 16, K % 64 == 0, B [N,K]; MFMA needs K % 128 == 0
+    assert L.fke_qgemm_i8_on_path(_lib.PATH_GEMV, P, P, P, 17, 64, 4096, None, None, 1.0, 1.0, None,
+                                  0, 0, None) == INVALID
+    assert L.fke_qgemm_i8_on_path(_lib.PATH_GEMV, P, P, P, 4, 64, 4096, None, None, 1.0, 1.0, None,
+                                  0, 1, None) == INVALID
+    assert L.fke_qgemm_i8_on_path(_lib.PATH_MFMA, P, P, P, 64, 64, 100, None, None, 1.0, 1.0, None,
+                                  0, 0, None) == INVALID
+    assert L.fke_qgemm_f8_on_path(_lib.PATH_GEMV, P, P, P, 4, 64, 4096, 1.0, 1.0, None, 0, 0,
+                                  None) == INVALID
+
+
+@pytest.mark.parametrize("M,N,K,layout,expect", [
+    (1, 14336, 4096, 0, _lib.PATH_GEMV),
+    (4, 14336, 4096, 0, _lib.PATH_GEMV),
+    (16, 14336, 4096, 0, _lib.PATH_GEMV),
+    (17, 14336, 4096, 0, _lib.PATH_MFMA),
+    (4096, 11008, 4096, 0, _lib.PATH_MFMA),
+    (8192, 8192, 8192, 0, _lib.PATH_MFMA),
+    (8192, 8192, 8192, 1, _lib.PATH_MFMA),
+    (1, 14336, 4096, 1, _lib.PATH_MFMA),
+    (64, 64, 100, 0, _lib.PATH_GENERIC),
+    (64, 64, 4, 0, _lib.PATH_GENERIC),
+    (8, 64, 96, 0, _lib.PATH_GENERIC),
+])
+def test_dispatch_i8(M, N, K, layout, expect):
+    assert _lib.lib().fke_select_path_i8(P, P, P, M, N, K, 0, layout) == expect
+
+
+def test_dispatch_unaligned_pointer_falls_back():
+    L = _lib.lib()
+    assert L.fke_select_path_i8(P + 1, P, P, 1, 4096, 4096, 0, 0) == _lib.PATH_GENERIC
+    assert L.fke_select_path_i8(P, P + 4, P, 256, 4096, 4096, 0, 0) == _lib.PATH_GENERIC
+    assert L.fke_select_path_f8(P + 2, P, P, 256, 256, 256, 0, 1) == _lib.PATH_GENERIC
+    assert L.fke_select_path_f8(P, P, P, 8192, 8192, 8192, 1, 1) == _lib.PATH_MFMA
+    assert L.fke_select_path_i8(None, P, P, 8, 8, 8, 0, 0) == -1
+
+
+def test_dropin_header_program_host_checks():
+    """The drop-in C++ program (built by g++ against include/quantized_gemm.cuh)
+    passes its argument-validation checks without a GPU."""
+    assert os.path.exists(DROPIN), "build first: make -C flash-kernel-engine_amd/csrc"
+    r = subprocess.run([DROPIN, "--host-only"], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "[PASS]" in r.stdout

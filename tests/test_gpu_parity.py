@@ -1,0 +1,318 @@
+"""GPU parity tests: the HIP kernels, called through the C ABI, against the CPU
+oracle on the same seeded inputs.
+
+Bars: int32 accumulators bit-exact; the fp32 and bf16 epilogue outputs
+bit-exact against the oracle's canonical epilogue (which is the reference's
+float(acc)*fp32(sa*sb) when scales are uniform and there is no bias); FP8 on the
+MFMA family within 2e-2 max-norm relative error of the reference's sequential
+fp32 sum (and bit-exact on the GENERIC family, which keeps that order).
+Every test prints the case it is about to run before touching the GPU.
+"""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+from flash_engine import _lib, ops  # noqa: E402
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+DROPIN = os.path.join(REPO, "flash-kernel-engine_amd", "_build", "test_quantized_gemm_dropin")
+NTH = min(16, os.cpu_count() or 1)
+
+OUT_T = {"f32": torch.float32, "bf16": torch.bfloat16, "i32": torch.int32}
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+def dev_t(x):
+    return torch.from_numpy(np.ascontiguousarray(x)).cuda()
+
+
+def host(t: torch.Tensor) -> np.ndarray:
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).cpu().numpy().view(np.uint16)
+    return t.cpu().numpy()
+
+
+def oracle_out(oracle, acc, sa_vec, sb_vec, sa, sb, bias, out):
+    code = {"f32": oracle.OUT_F32, "bf16": oracle.OUT_BF16, "i32": oracle.OUT_I32}[out]
+    return oracle.w8a8_epilogue(acc, sa_vec, sb_vec, sa, sb, bias, code)
+
+
+def inputs_i8(oracle, M, N, K, seed, layout="nk", act="uniform"):
+    A = (oracle.gen_i8_uniform((M, K), seed) if act == "uniform"
+         else oracle.gen_i8_clipped_normal((M, K), seed, 30.0))
+    Bnk = oracle.gen_i8_uniform((N, K), seed + 1)
+    B = Bnk if layout == "nk" else np.ascontiguousarray(Bnk.T)
+    sa = oracle.gen_f32_uniform((M,), seed + 2, 0.001, 0.02)
+    sb = oracle.gen_f32_uniform((N,), seed + 3, 0.001, 0.02)
+    bias = oracle.gen_f32_normal((N,), seed + 4, 0.0, 0.02)
+    return A, B, sa, sb, bias
+
+
+def gpu_i8(A, B, layout, out, path="auto", sa_vec=None, sb_vec=None, sa=1.0, sb=1.0, bias=None):
+    r = ops.w8a8_gemm(dev_t(A), dev_t(B), None if sa_vec is None else dev_t(sa_vec),
+                      None if sb_vec is None else dev_t(sb_vec),
+                      None if bias is None else dev_t(bias), out_dtype=OUT_T[out],
+                      b_layout=layout, sa=sa, sb=sb, path=path)
+    torch.cuda.synchronize()
+    return host(r)
+
+
+def assert_same(got, ref, what):
+    if got.dtype == np.float32:
+        bad = got.view(np.uint32) != ref.view(np.uint32)
+    else:
+        bad = got != ref
+    n = int(bad.sum())
+    if n:
+        i = np.argwhere(bad)[0]
+        raise AssertionError(f"{what}: {n} mismatches, first at {tuple(i)}: {got[tuple(i)]} vs {ref[tuple(i)]}")
+
+
+# ------------------------------------------------------------- reference KAT
+
+def test_kat64_dropin_entry(oracle, dev):
+    """The reference test's own case through fke_launch_int8_gemm_dp4a."""
+    say("kat64 via fke_launch_int8_gemm_dp4a")
+    M = N = K = 64
+    A = (np.arange(M * K) % 7 - 3).astype(np.int8).reshape(M, K)
+    B = (np.arange(N * K) % 5 - 2).astype(np.int8).reshape(N, K)
+    dA, dB = dev_t(A), dev_t(B)
+    dC = torch.empty((M, N), dtype=torch.float32, device=dev)
+    st = _lib.lib().fke_launch_int8_gemm_dp4a(dA.data_ptr(), dB.data_ptr(), dC.data_ptr(), 0.05, 0.02,
+                                              M, N, K, None)
+    assert st == 0
+    torch.cuda.synchronize()
+    assert_same(host(dC), oracle.ref_host_gemm_i8(A, B, 0.05, 0.02), "kat64")
+
+
+def test_dropin_program_full(dev):
+    say("drop-in C++ program (reference test restated on the HIP API)")
+    r = subprocess.run([DROPIN], capture_output=True, text=True, timeout=120)
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr
+
+
+# ------------------------------------------------------------ C1 (config 0)
+
+@pytest.mark.parametrize("path", ["auto", "mfma", "generic"])
+def test_c1_golden(oracle, dev, path):
+    import json
+    g = json.load(open(os.path.join(REPO, "tests", "golden", "golden.json")))["c1"]
+    say("c1 golden", path)
+    M, N, K = g["M"], g["N"], g["K"]
+    A = oracle.gen_i8_uniform((M, K), g["seed_A"])
+    B = oracle.gen_i8_uniform((N, K), g["seed_B"])
+    sa = oracle.gen_f32_uniform((M,), g["seed_sa"], 0.001, 0.02)
+    sb = oracle.gen_f32_uniform((N,), g["seed_sb"], 0.001, 0.02)
+    acc = oracle.w8a8_acc(A, B)
+    for out in ("i32", "f32", "bf16"):
+        got = gpu_i8(A, B, "nk", out, path, sa, sb)
+        assert_same(got, oracle_out(oracle, acc, sa, sb, 1.0, 1.0, None, out), f"c1 {path} {out}")
+    for m, n, a, _, _ in g["samples"]:
+        assert acc[m, n] == a
+
+
+# ------------------------------------------------------- kernel families x options
+
+@pytest.mark.parametrize("path", ["mfma", "generic"])
+@pytest.mark.parametrize("layout", ["nk", "kn"])
+@pytest.mark.parametrize("out", ["f32", "bf16", "i32"])
+@pytest.mark.parametrize("opts", ["vec_bias", "scalar"])
+def test_i8_families_ragged(oracle, dev, path, layout, out, opts):
+    M, N, K = 300, 528, 384  # ragged in M and N against the 256x256 tile
+    say("i8", path, layout, out, opts, (M, N, K))
+    A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 100, layout)
+    acc = oracle.w8a8_acc(A, B, oracle.B_NK if layout == "nk" else oracle.B_KN)
+    if opts == "vec_bias":
+        got = gpu_i8(A, B, layout, out, path, sa, sb, bias=bias)
+        ref = oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, out)
+    else:
+        got = gpu_i8(A, B, layout, out, path, sa=0.05, sb=0.02)
+        ref = oracle_out(oracle, acc, None, None, 0.05, 0.02, None, out)
+    assert_same(got, ref, f"{path} {layout} {out} {opts}")
+
+
+@pytest.mark.parametrize("M", list(range(1, 17)))
+def test_gemv_every_m(oracle, dev, M):
+    N, K = 1000, 1024  # N ragged against every row-block size
+    say("gemv", M, N, K)
+    A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 200 + M, act="normal")
+    acc = oracle.w8a8_acc(A, B)
+    assert_same(gpu_i8(A, B, "nk", "i32", "gemv"), acc, f"gemv M={M} i32")
+    got = gpu_i8(A, B, "nk", "bf16", "gemv", sa, sb, bias=bias)
+    assert_same(got, oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, "bf16"), f"gemv M={M} bf16")
+
+
+@pytest.mark.parametrize("K", [64, 128, 4096 + 64, 14336])
+def test_gemv_k_variants(oracle, dev, K):
+    M, N = 3, 300
+    say("gemv K", K)
+    A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 300 + K)
+    acc = oracle.w8a8_acc(A, B)
+    assert_same(gpu_i8(A, B, "nk", "i32", "gemv"), acc, f"gemv K={K}")
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 1), (7, 13, 77), (65, 3, 5), (33, 70, 129), (2, 5, 4)])
+@pytest.mark.parametrize("layout", ["nk", "kn"])
+def test_generic_odd_shapes(oracle, dev, shape, layout):
+    M, N, K = shape
+    say("generic odd", shape, layout)
+    A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 400 + sum(shape), layout)
+    acc = oracle.w8a8_acc(A, B, oracle.B_NK if layout == "nk" else oracle.B_KN)
+    got = gpu_i8(A, B, layout, "f32", "auto", sa, sb, bias=bias)
+    assert_same(got, oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, "f32"), f"generic {shape}")
+
+
+def test_unaligned_pointers_use_generic(oracle, dev):
+    M, N, K = 40, 256, 256
+    say("unaligned A")
+    A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 500)
+    buf = torch.zeros(M * K + 1, dtype=torch.int8, device=dev)
+    buf[1:] = dev_t(A.ravel())
+    dA = buf[1:].view(M, K)
+    assert dA.data_ptr() % 16 == 1
+    assert _lib.lib().fke_select_path_i8(dA.data_ptr(), 4096, 4096, M, N, K, 0, 0) == _lib.PATH_GENERIC
+    r = ops.w8a8_gemm(dA, dev_t(B), dev_t(sa), dev_t(sb), None, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert_same(host(r), oracle_out(oracle, oracle.w8a8_acc(A, B), sa, sb, 1., 1., None, "f32"), "unaligned")
+
+
+# ------------------------------------------------------ BASELINE full sizes
+
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_c2_decode_full(oracle, dev, M):
+    """Config 1: M in {1,4,16}, N=14336, K=4096, clipped N(0,30^2) activations,
+    per-channel scales, fused bias, bf16 out; checked in full."""
+    N, K = 14336, 4096
+    say("c2 decode", M, N, K)
+    A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 1000 + M, act="normal")
+    assert _lib.lib().fke_select_path_i8(4096, 4096, 4096, M, N, K, 1, 0) == _lib.PATH_GEMV
+    acc = oracle.w8a8_acc(A, B, nthreads=NTH)
+    got = gpu_i8(A, B, "nk", "bf16", "auto", sa, sb, bias=bias)
+    assert_same(got, oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, "bf16"), f"c2 M={M}")
+
+
+def test_c3_prefill_full(oracle, dev):
+    """Config 2: 4096x11008x4096, bf16 out: every output checked."""
+    M, N, K = 4096, 11008, 4096
+    say("c3 prefill", M, N, K)
+    A, B, sa, sb, _ = inputs_i8(oracle, M, N, K, 2000)
+    acc_ref = oracle.w8a8_acc(A, B, nthreads=NTH)
+    got = gpu_i8(A, B, "nk", "bf16", "auto", sa, sb)
+    assert_same(got, oracle_out(oracle, acc_ref, sa, sb, 1.0, 1.0, None, "bf16"), "c3 bf16")
+
+
+def test_c4_square_full(oracle, dev):
+    """Config 3: 8192^3; the i32 result bit-exact in full against the oracle,
+    the fp32 output bit-exact against the epilogue of that i32, plus exact
+    int64 row/column checksums (a size-independent property)."""
+    M = N = K = 8192
+    say("c4 square", M, N, K)
+    A, B, sa, sb, _ = inputs_i8(oracle, M, N, K, 3000)
+    acc = gpu_i8(A, B, "nk", "i32", "auto")
+    colsum = acc.astype(np.int64).sum(0)
+    rowsum = acc.astype(np.int64).sum(1)
+    assert np.array_equal(colsum, B.astype(np.int64) @ A.astype(np.int64).sum(0))
+    assert np.array_equal(rowsum, A.astype(np.int64) @ B.astype(np.int64).sum(0))
+    acc_ref = oracle.w8a8_acc(A, B, nthreads=NTH)
+    assert_same(acc, acc_ref, "c4 i32")
+    f32 = gpu_i8(A, B, "nk", "f32", "auto", sa, sb)
+    assert_same(f32, oracle_out(oracle, acc_ref, sa, sb, 1.0, 1.0, None, "f32"), "c4 f32")
+
+
+# ---------------------------------------------------------------------- FP8
+
+def f8_inputs(oracle, M, N, K, seed, layout="kn", with_nan_codes=False):
+    xa = oracle.gen_f32_normal((M, K), seed)
+    xb = oracle.gen_f32_normal((K, N), seed + 1)
+    qa, sa = oracle.quantize_e4m3(xa)
+    qb, sb = oracle.quantize_e4m3(xb)
+    if with_nan_codes:  # the reference decodes these to 0.0
+        qa.ravel()[::97] = 0x7F
+        qb.ravel()[::89] = 0xFF
+    B = qb if layout == "kn" else np.ascontiguousarray(qb.T)
+    return qa, B, sa, sb
+
+
+def gpu_f8(A, B, sa, sb, layout, out="f32", path="auto", bias=None):
+    r = ops.fp8_gemm_scaled(dev_t(A), dev_t(B), sa, sb, None if bias is None else dev_t(bias),
+                            out_dtype=OUT_T[out], b_layout=layout, path=path)
+    torch.cuda.synchronize()
+    return host(r)
+
+
+def rel_errors(got, ref):
+    d = got.astype(np.float64) - ref.astype(np.float64)
+    return (np.abs(d).max() / max(np.abs(ref).max(), 1e-30),
+            np.linalg.norm(d) / max(np.linalg.norm(ref.astype(np.float64)), 1e-30))
+
+
+@pytest.mark.parametrize("layout", ["kn", "nk"])
+@pytest.mark.parametrize("shape", [(64, 64, 256), (37, 50, 131), (300, 272, 384)])
+def test_fp8_generic_bit_exact(oracle, dev, layout, shape):
+    M, N, K = shape
+    say("fp8 generic", shape, layout)
+    A, B, sa, sb = f8_inputs(oracle, M, N, K, 600 + K, layout, with_nan_codes=True)
+    code = oracle.B_KN if layout == "kn" else oracle.B_NK
+    ref = oracle.f8_gemm(A, B, sa, sb, b_layout=code)
+    assert_same(gpu_f8(A, B, sa, sb, layout, "f32", "generic"), ref, "fp8 generic")
+    if layout == "kn":
+        assert_same(ref, oracle.ref_kernel_gemm_f8(A, B, sa, sb), "oracle vs reference loop")
+
+
+@pytest.mark.parametrize("layout", ["kn", "nk"])
+@pytest.mark.parametrize("out", ["f32", "bf16"])
+@pytest.mark.parametrize("nan_codes", [False, True])
+def test_fp8_mfma_tolerance(oracle, dev, layout, out, nan_codes):
+    M, N, K = 300, 528, 1024
+    say("fp8 mfma", layout, out, nan_codes)
+    A, B, sa, sb = f8_inputs(oracle, M, N, K, 700, layout, with_nan_codes=nan_codes)
+    bias = oracle.gen_f32_normal((N,), 701, 0.0, 0.02)
+    code = oracle.B_KN if layout == "kn" else oracle.B_NK
+    ref = oracle.f8_gemm(A, B, sa, sb, bias=bias, b_layout=code)
+    got = gpu_f8(A, B, sa, sb, layout, out, "mfma", bias=bias)
+    if out == "bf16":
+        got = oracle.bf16_to_f32(got)
+    mx, fro = rel_errors(got, ref)
+    assert np.isfinite(got).all()
+    assert mx <= 2e-2 and fro <= 2e-2, (mx, fro)
+
+
+def test_c5_fp8_full(oracle, dev):
+    """Config 4: 8192^3 e4m3 (per-tensor amax/448 scales, B [K,N]), bf16 out,
+    against the reference's sequential fp32 sum on 64 sampled rows."""
+    M = N = K = 8192
+    say("c5 fp8", M, N, K)
+    A, B, sa, sb = f8_inputs(oracle, M, N, K, 4000, "kn")
+    got = oracle.bf16_to_f32(gpu_f8(A, B, sa, sb, "kn", "bf16"))
+    rows = np.linspace(0, M - 1, 64).astype(np.int32)
+    ref = oracle.f8_gemm(A, B, sa, sb, b_layout=oracle.B_KN, rows=rows, nthreads=NTH)
+    mx, fro = rel_errors(got[rows], ref)
+    print("c5 sampled rel errors: max-norm", mx, "frobenius", fro)
+    assert mx <= 2e-2 and fro <= 2e-2
+
+
+# --------------------------------------------------------------- python op
+
+def test_python_op_matches_reference_numpy_op(oracle, dev):
+    """flash_engine.quantized_gemm_int8 == reference python/flash_engine/ops.py:180-186."""
+    say("python op")
+    r = np.random.default_rng(5)
+    for (M, N, K) in [(32, 32, 64), (300, 256, 512)]:
+        A = r.integers(-127, 127, (M, K), dtype=np.int8)
+        B = r.integers(-127, 127, (K, N), dtype=np.int8)
+        for sa, sb in [(1.0, 1.0), (0.01, 0.02), (0.0123, 0.0456)]:
+            ref = oracle.ref_py_gemm_i8(A, B, sa, sb)
+            got_np = ops.quantized_gemm_int8(A, B, scale_a=sa, scale_b=sb)
+            assert isinstance(got_np, np.ndarray)
+            assert_same(got_np, ref, "python op (numpy in)")
+            got_t = ops.quantized_gemm_int8(dev_t(A), dev_t(B), sa, sb)
+            assert_same(host(got_t), ref, "python op (torch in)")

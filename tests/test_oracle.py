@@ -1,0 +1,311 @@
+"""CPU tests that pin the oracle (oracle/fke_oracle.c) before it is trusted.
+
+Each oracle function is checked against the reference's own known answers
+(the KAT64 case of tests/test_quantized_gemm.cu), against fixtures
+(tests/golden/golden.json), and against what the mathematics fixes: numpy
+int64 matmuls, exact rational arithmetic, torch's float8/bfloat16 casts
+(library routines), closed forms and hand-derived tiny cases.  Each check is
+chosen so that a plausible slip (transposed B, dropped K tail, wrong bias
+rounding, wrong decode exponent) fails it.
+"""
+import json
+import math
+import os
+from fractions import Fraction
+
+import numpy as np
+import pytest
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+GOLDEN = json.load(open(os.path.join(HERE, "golden", "golden.json")))
+
+
+def rng(seed):
+    return np.random.default_rng(seed)
+
+
+# ---------------------------------------------------------------- generators
+
+def test_splitmix64_published_vector(oracle):
+    g = GOLDEN["splitmix64"]
+    assert oracle.splitmix64_stream(g["seed"], 5) == g["first5"]
+
+
+def test_generators_ranges_and_moments(oracle):
+    a = oracle.gen_i8_uniform((1 << 16,), 1)
+    assert a.min() == -127 and a.max() == 127
+    assert abs(a.astype(np.float64).mean()) < 1.5
+    s = oracle.gen_f32_uniform((1 << 16,), 2, 0.001, 0.02)
+    assert s.min() >= 0.001 and s.max() < 0.02
+    z = oracle.gen_f32_normal((1 << 16,), 3, 0.0, 0.02)
+    assert abs(z.mean()) < 1e-3 and abs(z.std() - 0.02) < 1e-3
+    c = oracle.gen_i8_clipped_normal((1 << 16,), 4, 30.0)
+    assert c.min() >= -127 and c.max() <= 127 and abs(c.std() - 30.0) < 1.0
+    # deterministic per seed, different across seeds
+    assert np.array_equal(oracle.gen_i8_uniform((64,), 9), oracle.gen_i8_uniform((64,), 9))
+    assert not np.array_equal(oracle.gen_i8_uniform((64,), 9), oracle.gen_i8_uniform((64,), 10))
+
+
+# ------------------------------------------------------- INT8 reference GEMM
+
+def kat64_inputs():
+    M = N = K = 64
+    A = (np.arange(M * K) % 7 - 3).astype(np.int8).reshape(M, K)
+    B = (np.arange(N * K) % 5 - 2).astype(np.int8).reshape(N, K)
+    return A, B
+
+
+def test_kat64_reference_case(oracle):
+    """The reference test's closed-form case (tests/test_quantized_gemm.cu:19-48)."""
+    g = GOLDEN["kat64"]
+    A, B = kat64_inputs()
+    acc = oracle.w8a8_acc(A, B)
+    assert int(acc.sum()) == g["acc_sum"]
+    assert int(acc.min()) == g["acc_min"] and int(acc.max()) == g["acc_max"]
+    assert int((acc != 0).sum()) == g["acc_nonzero"]
+    assert acc[0, :8].tolist() == g["acc_row0_first8"]
+    assert int(acc[63, 63]) == g["acc_63_63"]
+    C = oracle.ref_host_gemm_i8(A, B, 0.05, 0.02)
+    alpha = np.array(g["alpha_bits"], dtype=np.uint32).view(np.float32)
+    assert np.array_equal(C, acc.astype(np.float32) * alpha)
+    assert C[0, 0] == np.float32(-6.0) * alpha
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 1), (3, 5, 7), (17, 9, 64), (8, 33, 130), (8, 8, 8)])
+def test_ref_host_gemm_vs_numpy(oracle, shape):
+    M, N, K = shape
+    r = rng(sum(shape))
+    A = r.integers(-127, 128, (M, K), dtype=np.int8)
+    B = r.integers(-127, 128, (N, K), dtype=np.int8)
+    sa, sb = np.float32(0.013), np.float32(0.0071)
+    C = oracle.ref_host_gemm_i8(A, B, float(sa), float(sb))
+    acc = A.astype(np.int64) @ B.astype(np.int64).T  # B is [N,K]: transposed here
+    assert np.array_equal(C, acc.astype(np.float32) * (sa * sb))
+    # a transposed-B mistake would not pass: B is not symmetric in these cases
+    if M == N == K and M > 1:
+        assert not np.array_equal(acc, A.astype(np.int64) @ B.astype(np.int64))
+
+
+def test_ref_kernel_equals_host_for_k_multiple_of_4(oracle):
+    r = rng(5)
+    A = r.integers(-127, 128, (13, 96), dtype=np.int8)
+    B = r.integers(-127, 128, (11, 96), dtype=np.int8)
+    assert np.array_equal(oracle.ref_kernel_gemm_i8(A, B, 0.5, 0.25),
+                          oracle.ref_host_gemm_i8(A, B, 0.5, 0.25))
+
+
+def test_ref_kernel_k_tail_truncation_hand_case(oracle):
+    """src/quantized_gemm.cu:28-35 with K=5: one int32 word per row, row r starting
+    at byte 4*r.  Row 0 sums bytes 0..3, row 1 bytes 4..7 (misaligned)."""
+    A = np.arange(1, 11, dtype=np.int8).reshape(2, 5)
+    B = np.ones((1, 5), dtype=np.int8)
+    C = oracle.ref_kernel_gemm_i8(A, B, 1.0, 1.0)
+    assert C.ravel().tolist() == [1 + 2 + 3 + 4, 5 + 6 + 7 + 8]
+    # the host loop of the reference test uses the full K instead
+    assert oracle.ref_host_gemm_i8(A, B, 1.0, 1.0).ravel().tolist() == [15, 40]
+
+
+def test_ref_py_gemm_matches_numpy_expression(oracle):
+    """python/flash_engine/ops.py:180-186, evaluated by numpy itself."""
+    r = rng(11)
+    A = r.integers(-127, 127, (32, 64), dtype=np.int8)
+    B = r.integers(-127, 127, (64, 32), dtype=np.int8)
+    for sa, sb in [(1.0, 1.0), (0.01, 0.02), (0.0123, 0.0456)]:
+        expect = np.matmul(A.astype(np.int32), B.astype(np.int32)).astype(np.float32) * (sa * sb)
+        got = oracle.ref_py_gemm_i8(A, B, sa, sb)
+        assert got.dtype == np.float32 and np.array_equal(got, expect)
+
+
+@pytest.mark.parametrize("layout", ["nk", "kn"])
+def test_w8a8_acc_vs_numpy(oracle, layout):
+    r = rng(21)
+    M, N, K = 19, 37, 200
+    A = r.integers(-127, 128, (M, K), dtype=np.int8)
+    Bnk = r.integers(-127, 128, (N, K), dtype=np.int8)
+    B = Bnk if layout == "nk" else np.ascontiguousarray(Bnk.T)
+    code = oracle.B_NK if layout == "nk" else oracle.B_KN
+    acc = oracle.w8a8_acc(A, B, code, nthreads=3)
+    assert np.array_equal(acc, (A.astype(np.int64) @ Bnk.astype(np.int64).T).astype(np.int32))
+    rows = np.array([18, 0, 7], dtype=np.int32)
+    assert np.array_equal(oracle.w8a8_acc(A, B, code, rows=rows), acc[rows])
+
+
+def test_w8a8_full_range_extremes(oracle):
+    """|acc| = K*127^2 at K=8192 (1.32e8) stays exact (no overflow)."""
+    K = 8192
+    A = np.full((2, K), -127, dtype=np.int8)
+    B = np.stack([np.full(K, -127, np.int8), np.full(K, 127, np.int8)])
+    acc = oracle.w8a8_acc(A, B)
+    assert acc[0].tolist() == [K * 127 * 127, -K * 127 * 127]
+
+
+# ------------------------------------------------------------------ epilogue
+
+def f32_rne(x: Fraction) -> np.float32:
+    """Exact round-to-nearest-even of a rational to fp32 (no double rounding)."""
+    c = np.float32(float(x))
+    cands = {c, np.nextafter(c, np.float32(np.inf)), np.nextafter(c, np.float32(-np.inf))}
+    best = sorted(cands, key=lambda v: (abs(Fraction(float(v)) - x),
+                                        int(np.array(v, np.float32).view(np.uint32)) & 1))
+    return best[0]
+
+
+def test_epilogue_reduces_to_reference(oracle):
+    """Uniform scales, no bias, fp32 out == tests/test_quantized_gemm.cu:46."""
+    r = rng(31)
+    A = r.integers(-127, 128, (24, 64), dtype=np.int8)
+    B = r.integers(-127, 128, (40, 64), dtype=np.int8)
+    acc = oracle.w8a8_acc(A, B)
+    ref = oracle.ref_host_gemm_i8(A, B, 0.05, 0.02)
+    y_scalar = oracle.w8a8_epilogue(acc, sa=0.05, sb=0.02)
+    y_vec = oracle.w8a8_epilogue(acc, np.full(24, 0.05, np.float32), np.full(40, 0.02, np.float32))
+    assert np.array_equal(y_scalar, ref) and np.array_equal(y_vec, ref)
+
+
+def test_epilogue_bias_is_one_rounding(oracle):
+    """y = round_f32(fp32(acc) * s + bias) exactly (fmaf), checked with exact
+    rationals; a two-rounding mul-then-add differs on some of these."""
+    r = rng(41)
+    acc = r.integers(-2_000_000, 2_000_000, (8, 64)).astype(np.int32)
+    sa = oracle.gen_f32_uniform((8,), 5, 0.001, 0.02)
+    sb = oracle.gen_f32_uniform((64,), 6, 0.001, 0.02)
+    bias = oracle.gen_f32_normal((64,), 7, 0.0, 0.02)
+    y = oracle.w8a8_epilogue(acc, sa, sb, bias=bias)
+    differs_from_two_roundings = 0
+    for m in range(8):
+        for n in range(64):
+            s = np.float32(sa[m] * sb[n])
+            exact = Fraction(float(np.float32(acc[m, n]))) * Fraction(float(s)) + Fraction(float(bias[n]))
+            assert y[m, n] == f32_rne(exact), (m, n)
+            two = np.float32(np.float32(np.float32(acc[m, n]) * s) + bias[n])
+            differs_from_two_roundings += int(two != y[m, n])
+    assert differs_from_two_roundings > 0
+
+
+def test_bf16_rne_known_answers(oracle):
+    assert oracle.f32_to_bf16_rne(1.0) == 0x3F80
+    assert oracle.f32_to_bf16_rne(1.0 + 2.0 ** -8) == 0x3F80       # tie -> even
+    assert oracle.f32_to_bf16_rne(1.0 + 3 * 2.0 ** -8) == 0x3F82   # tie -> even (up)
+    assert oracle.f32_to_bf16_rne(1.0 + 2.0 ** -8 + 2.0 ** -20) == 0x3F81
+    assert oracle.f32_to_bf16_rne(-2.5) == 0xC020
+    assert oracle.f32_to_bf16_rne(float("inf")) == 0x7F80
+
+
+def test_bf16_rne_matches_torch(oracle):
+    torch = pytest.importorskip("torch")
+    x = np.concatenate([oracle.gen_f32_normal((4096,), 8, 0, 3.0),
+                        oracle.gen_f32_uniform((4096,), 9, -1e-3, 1e-3)]).astype(np.float32)
+    acc = np.zeros((1, x.size), np.int32)
+    # route through the epilogue's bf16 store: acc=0 with bias=x gives y=x
+    got = oracle.w8a8_epilogue(acc, sa=1.0, sb=1.0, bias=x, out_dtype=oracle.OUT_BF16)[0]
+    ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, ref)
+
+
+# ----------------------------------------------------------------------- FP8
+
+def test_e4m3_decode_exhaustive(oracle):
+    table = oracle.e4m3_decode_table()
+    golden = np.array(GOLDEN["e4m3"], dtype=np.uint32).view(np.float32)
+    assert np.array_equal(table.view(np.uint32), golden.view(np.uint32))
+    for code in range(256):
+        s = -1.0 if code & 0x80 else 1.0
+        e, m = (code >> 3) & 15, code & 7
+        if e == 15 and m == 7:
+            assert table[code] == 0.0  # the reference's NaN clamp
+        elif e == 0:
+            assert table[code] == s * m / 512.0
+        else:
+            assert table[code] == s * (1 + m / 8) * 2.0 ** (e - 7)
+    assert table[0x7E] == 448.0 and table[0xFE] == -448.0 and table[0x01] == 2.0 ** -9
+
+
+def test_e4m3_decode_matches_torch_float8(oracle):
+    torch = pytest.importorskip("torch")
+    codes = np.array([c for c in range(256) if c not in (0x7F, 0xFF)], dtype=np.uint8)
+    ref = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    assert np.array_equal(oracle.e4m3_decode_table()[codes], ref)
+
+
+def test_e4m3_quantizer(oracle):
+    torch = pytest.importorskip("torch")
+    x = oracle.gen_f32_normal((1 << 15,), 12, 0.0, 1.0)
+    q, s = oracle.quantize_e4m3(x)
+    assert s == np.float32(np.abs(x).max()) / np.float32(448.0)
+    assert not np.isin(q, [0x7F, 0xFF]).any()
+    v = (x / np.float32(s)).astype(np.float32)
+    ref = torch.from_numpy(np.clip(v, -448, 448)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(q, ref)
+    # saturation instead of NaN, RNE ties to even, subnormals
+    assert oracle.f32_to_e4m3_sat(1e9) == 0x7E and oracle.f32_to_e4m3_sat(-500.0) == 0xFE
+    assert oracle.f32_to_e4m3_sat(1.0625) == 0x38   # 1 + 1/16: tie -> 1.0 (even)
+    assert oracle.f32_to_e4m3_sat(1.1875) == 0x3A   # 1 + 3/16: tie -> 1.25 (even)
+    assert oracle.f32_to_e4m3_sat(2.0 ** -9) == 0x01
+    assert oracle.f32_to_e4m3_sat(2.0 ** -10) == 0x00  # tie -> 0 (even)
+
+
+def f8_sequential(A, B_kn, table, alpha):
+    """Python float32 restatement of src/quantized_gemm.cu:109-116 (k in order)."""
+    M, K = A.shape
+    N = B_kn.shape[1]
+    C = np.zeros((M, N), np.float32)
+    for m in range(M):
+        for n in range(N):
+            s = np.float32(0.0)
+            for k in range(K):
+                s = np.float32(s + table[A[m, k]] * table[B_kn[k, n]])
+            C[m, n] = np.float32(s * alpha)
+    return C
+
+
+def test_f8_reference_sequential_order(oracle):
+    r = rng(51)
+    A = r.integers(0, 256, (5, 70), dtype=np.uint8)
+    B = r.integers(0, 256, (70, 6), dtype=np.uint8)
+    table = oracle.e4m3_decode_table()
+    alpha = np.float32(np.float32(0.3) * np.float32(0.7))
+    ref = f8_sequential(A, B, table, alpha)
+    assert np.array_equal(oracle.ref_kernel_gemm_f8(A, B, 0.3, 0.7), ref)
+    assert np.array_equal(oracle.f8_gemm(A, B, 0.3, 0.7, b_layout=oracle.B_KN), ref)
+    assert np.array_equal(oracle.f8_gemm(A, np.ascontiguousarray(B.T), 0.3, 0.7,
+                                         b_layout=oracle.B_NK), ref)
+    # exact double-precision sum differs only by fp32 rounding of the partial sums
+    exact = (table[A].astype(np.float64) @ table[B].astype(np.float64)) * float(alpha)
+    assert np.allclose(ref, exact, rtol=1e-5, atol=1e-6 * np.abs(exact).max())
+
+
+def test_f8_order_matters_case(oracle):
+    """A case where the sequential order is observable: 448*448 = 200704 has an
+    fp32 ulp of 2^-6, so each following 1.0 * 2^-9 product is rounded away one
+    at a time, while the exact (or a pairwise) sum of the eight keeps 2^-6."""
+    A = np.array([[0x7E] + [0x38] * 8], dtype=np.uint8)        # 448, then 1.0 x8
+    B = np.array([[0x7E]] + [[0x01]] * 8, dtype=np.uint8)      # 448, then 2^-9 x8
+    got = oracle.ref_kernel_gemm_f8(A, B, 1.0, 1.0)[0, 0]
+    assert got == np.float32(200704.0)
+    assert np.float32(200704.0 + 8 * 2.0 ** -9) == np.float32(200704.015625) != got
+
+
+# ------------------------------------------------------------------ fixtures
+
+def test_c1_golden_fixture(oracle):
+    import hashlib
+    g = GOLDEN["c1"]
+    M, N, K = g["M"], g["N"], g["K"]
+    A = oracle.gen_i8_uniform((M, K), g["seed_A"])
+    B = oracle.gen_i8_uniform((N, K), g["seed_B"])
+    sa = oracle.gen_f32_uniform((M,), g["seed_sa"], 0.001, 0.02)
+    sb = oracle.gen_f32_uniform((N,), g["seed_sb"], 0.001, 0.02)
+
+    def sha(a):
+        return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+    assert [sha(A), sha(B), sha(sa), sha(sb)] == [g["sha256"][k] for k in ("A", "B", "scale_a", "scale_b")]
+    acc = oracle.w8a8_acc(A, B)
+    assert np.array_equal(acc, (A.astype(np.int64) @ B.astype(np.int64).T).astype(np.int32))
+    f32 = oracle.w8a8_epilogue(acc, sa, sb)
+    bf16 = oracle.w8a8_epilogue(acc, sa, sb, out_dtype=oracle.OUT_BF16)
+    assert sha(acc) == g["sha256"]["acc"]
+    assert sha(f32) == g["sha256"]["f32"]
+    assert sha(bf16) == g["sha256"]["bf16"]
+    for m, n, a, fbits, h in g["samples"]:
+        assert acc[m, n] == a and f32[m:m + 1, n].view(np.uint32)[0] == fbits and bf16[m, n] == h
