@@ -160,14 +160,16 @@ def gemv_bench(torch, L, _lib, dev, gen, M, nbuf, launches, N=14336, K=4096):
         for i in range(launches):
             launch(i, s.cuda_stream)
     torch.cuda.synchronize()
-    g.replay()
+    with torch.cuda.stream(s):
+        g.replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     reps = 3
-    e0.record(s)
-    for _ in range(reps):
-        g.replay()
-    e1.record(s)
+    with torch.cuda.stream(s):  # replay on s, where the events are recorded
+        e0.record(s)
+        for _ in range(reps):
+            g.replay()
+        e1.record(s)
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) * 1e3 / (reps * launches)
     nbytes = gemv_bytes(M, N, K)

@@ -272,11 +272,15 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
     issue(0, lds0);
     finish(lds0);
     int kt = 0;
+    // sched_barrier after each issue: without it the scheduler sinks the
+    // loads below the stage's MFMAs, so they never overlap with compute.
     for (; kt + 2 < KT; kt += 2) {
         issue(kt + 1, lds1);
+        __builtin_amdgcn_sched_barrier(0);
         stage_compute<ELEM, BL>(lds0, lds0 + STAGE_A, acc, wm, wn, lane, true);
         finish(lds1);
         issue(kt + 2, lds0);
+        __builtin_amdgcn_sched_barrier(0);
         stage_compute<ELEM, BL>(lds1, lds1 + STAGE_A, acc, wm, wn, lane, true);
         finish(lds0);
     }
@@ -284,6 +288,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
     // lds1 stage re-reads stage kt (a valid address) and its B fragments are
     // zeroed, so it adds nothing.
     issue(min(kt + 1, KT - 1), lds1);
+    __builtin_amdgcn_sched_barrier(0);
     stage_compute<ELEM, BL>(lds0, lds0 + STAGE_A, acc, wm, wn, lane, true);
     finish(lds1);
     stage_compute<ELEM, BL>(lds1, lds1 + STAGE_A, acc, wm, wn, lane, kt + 1 < KT);

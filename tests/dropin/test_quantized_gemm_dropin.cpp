@@ -103,11 +103,14 @@ int main(int argc, char** argv) {
         std::cout << "[PASS] INT8 drop-in GEMM bit-exact vs the reference host loop\n";
     }
 
-    // ---- FP8: every code (incl. 0x7F/0xFF) over a 64x64x256 problem ----
+    // ---- FP8: every non-negative code (incl. 0x7F -> 0.0) over 64x64x256 ----
+    // Codes without the sign bit keep the sums free of cancellation, so the
+    // fp32 result of any summation order is within a few ulp of the exact sum
+    // (with both signs this closed form cancels to exactly 0.0).
     constexpr int FK = 256;
     std::vector<uint8_t> f_A(M * FK), f_B(FK * N);
-    for (int i = 0; i < M * FK; ++i) f_A[i] = static_cast<uint8_t>((i * 37 + 11) & 0xFF);
-    for (int i = 0; i < FK * N; ++i) f_B[i] = static_cast<uint8_t>((i * 101 + 5) & 0xFF);
+    for (int i = 0; i < M * FK; ++i) f_A[i] = static_cast<uint8_t>(((i * 37 + 11) ^ (i >> 7)) & 0x7F);
+    for (int i = 0; i < FK * N; ++i) f_B[i] = static_cast<uint8_t>(((i * 101 + 5) ^ (i >> 6)) & 0x7F);
     std::vector<float> f_C(M * N), f_ref(M * N);
     const float fa = 0.125f, fb = 0.5f;
     for (int m = 0; m < M; ++m)
