@@ -25,6 +25,17 @@ for p in (REPO, PKG):
 PEAK_INT8_TOPS = 5000.0   # MI355X dense INT8 MFMA, published (5.0 POP/s)
 PEAK_FP8_TFLOPS = 5000.0  # MI355X dense FP8 MFMA, published
 PEAK_HBM_GBS = 8000.0     # MI355X HBM3E, published (8 TB/s)
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic.json")
+
+
+def traffic(key):
+    """HBM bytes per launch measured by rocprofv3 FETCH_SIZE + WRITE_SIZE (calibrated
+    against a copy kernel), as recorded in profiles/traffic.json; None if absent."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return json.load(f).get(key)
+    except (OSError, ValueError):
+        return None
 
 
 def parse():
@@ -37,6 +48,8 @@ def parse():
     ap.add_argument("--extra", action="store_true", help="also time configs 2 and 4 and GEMV M=4,16")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run a 512 MiB device copy (reference kernel for FETCH_SIZE/WRITE_SIZE)")
     return ap.parse_args()
 
 
@@ -116,11 +129,19 @@ def main():
                                "fp32 scales, fp32 out (BASELINE config 3)",
                    "M": M, "N": N, "K": K, "out": "fp32", "kernel": "gemm_mfma_kernel<i8,NK,f32>"},
         "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": PEAK_INT8_TOPS,
-                     "unit": "TOP/s", "frac": round(tops / PEAK_INT8_TOPS, 4), "traffic": None,
+                     "unit": "TOP/s", "frac": round(tops / PEAK_INT8_TOPS, 4),
+                     "traffic": traffic("gemm_mfma_kernel<i8,NK,f32> M=N=K=8192"),
                      "algorithmic_ops_per_launch": ops_per},
         "decode_gemv": gemv,
         "timed_wall_s": round(wall, 3),
     }
+    if args.calibrate_copy:
+        src = torch.randint(0, 255, (512 << 20,), dtype=torch.uint8, device=dev, generator=gen)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     if args.extra:
         line["extra"] = extra_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args)
     if not args.no_cpu:
@@ -179,7 +200,8 @@ def gemv_bench(torch, L, _lib, dev, gen, M, nbuf, launches, N=14336, K=4096):
             "weight_buffers": nbuf, "weight_bytes_cycled": nbuf * N * K,
             "timing": f"HIP graph of {launches} launches x {reps} replays, events on the graph's stream",
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
-                         "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                         "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                         "traffic": traffic(f"gemv_i8_kernel M={M} N={N} K={K} bf16+bias"),
                          "algorithmic_bytes_per_launch": nbytes},
             "kernel": "gemv_i8_kernel"}
 
