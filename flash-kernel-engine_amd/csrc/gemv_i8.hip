@@ -5,7 +5,18 @@
 // problem: the B panel is streamed once with 128-bit coalesced loads and no
 // MFMA is used.
 //
-// Workgroup = 4 waves = R consecutive B rows (output columns n0..n0+R-1).
+// Two kernels:
+//  * gemv_rows_kernel (M == 1; instantiable up to 4 rows): one B row per wave
+//    over the full K.  Lane l
+//    reads 16-byte chunks l, l+64, l+128, l+192 of each 256-chunk block (one
+//    wave load = 1 KiB contiguous), keeps the M activation chunks in registers,
+//    and reduces its partial sums with DPP row rotations, one ds_swizzle and two
+//    readlanes - no LDS and no barrier, so a wave retires as soon as its row is
+//    done and the load queue never drains.
+//  * gemv_i8_kernel (2 <= M <= 16), described below; it amortises the
+//    activation chunks over R rows per wave, which the row kernel cannot.
+//
+// gemv_i8_kernel: workgroup = 4 waves = R consecutive B rows (output columns n0..n0+R-1).
 // The K bytes of a row are split in four quarters, one per wave (split-K);
 // lane l of a wave reads 16-byte chunks l, l+64, ... of its quarter, so each
 // load instruction of a wave covers 1 KiB of contiguous bytes of one row.
@@ -119,6 +130,98 @@ __global__ __launch_bounds__(256) void gemv_i8_kernel(GemmArgs p) {
     }
 }
 
+
+// Sum over all 64 lanes, result uniform: DPP quad swaps and row rotations inside
+// each 16-lane row, a ds_swizzle across row pairs (lane ^ 16), then the two
+// 32-lane halves through readlane.
+__device__ __forceinline__ int32_t wave_sum(int32_t v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+    v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+    v += __builtin_amdgcn_update_dpp(0, v, 0x124, 0xF, 0xF, false);  // row_ror:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x128, 0xF, 0xF, false);  // row_ror:8
+    v += __builtin_amdgcn_ds_swizzle(v, 0x401F);                     // bit mode, xor 16
+    return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 32);
+}
+
+constexpr int ROWS_WAVES = 2;  // waves (= B rows) per workgroup of gemv_rows_kernel
+
+template <int MT, int OUT>
+__global__ __launch_bounds__(ROWS_WAVES * 64) void gemv_rows_kernel(GemmArgs p) {
+    const int lane = threadIdx.x & 63;
+    const int n = blockIdx.x * ROWS_WAVES + (threadIdx.x >> 6);
+    if (n >= p.N) return;  // uniform per wave
+    const int M = p.M, K = p.K;
+    const int ck = K >> 4;  // 16-byte chunks per row (K % 64 == 0)
+    // per-row epilogue operands, fetched before the weight stream
+    const float sbn = p.scale_b ? p.scale_b[n] : p.sb;
+    const float biasn = p.bias ? p.bias[n] : 0.0f;
+    const v4i* brow = reinterpret_cast<const v4i*>(static_cast<const int8_t*>(p.B) + static_cast<size_t>(n) * K);
+    const int8_t* A = static_cast<const int8_t*>(p.A);
+    // Rows m >= M of the MT-row template read row 0 (cheap L2 hits) and are
+    // never stored, so the main loop has no per-row branches.
+    const v4i* arow[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+        arow[m] = reinterpret_cast<const v4i*>(A + static_cast<size_t>(m < M ? m : 0) * K);
+    int32_t acc[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc[m] = 0;
+    const int nfull = ck >> 8;  // full blocks of 256 chunks (4 KiB of the row)
+    for (int blk = 0; blk < nfull; ++blk) {
+        const int c = (blk << 8) + lane;
+        v4i a[MT][4], b[4];
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) a[m][u] = arow[m][c + 64 * u];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) b[u] = __builtin_nontemporal_load(brow + c + 64 * u);
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc[m] = dot16(a[m][u], b[u], acc[m]);
+    }
+    if (ck & 255) {  // tail: fewer than 256 chunks left (K % 4096 != 0)
+        const int c0 = nfull << 8;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int c = c0 + lane + 64 * u;
+            if (c < ck) {
+                const v4i b = brow[c];
+#pragma unroll
+                for (int m = 0; m < MT; ++m) acc[m] = dot16(arow[m][c], b, acc[m]);
+            }
+        }
+    }
+    int32_t tot[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) tot[m] = wave_sum(acc[m]);
+    // lane m stores output row m (all lanes hold every total)
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        if (lane == m && m < M) {
+            const float sc = (p.scale_a ? p.scale_a[m] : p.sa) * sbn;
+            const float y = p.bias ? __builtin_fmaf(static_cast<float>(tot[m]), sc, biasn)
+                                   : static_cast<float>(tot[m]) * sc;
+            store_out<OUT>(p.C, static_cast<size_t>(m) * p.N + n, y, tot[m]);
+        }
+    }
+}
+
+template <int MT>
+hipError_t launch_rows(const GemmArgs& p, hipStream_t stream) {
+    GemmArgs a = p;
+    void* args[] = {&a};
+    const dim3 grid((p.N + ROWS_WAVES - 1) / ROWS_WAVES);
+    const void* f;
+    switch (p.out_dtype) {
+        case FKE_OUT_F32: f = reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_F32>); break;
+        case FKE_OUT_BF16: f = reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_BF16>); break;
+        default: f = reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_I32>); break;
+    }
+    return hipLaunchKernel(f, grid, dim3(ROWS_WAVES * 64), args, 0, stream);
+}
+
 template <int MT, int R>
 hipError_t launch_t(const GemmArgs& p, hipStream_t stream) {
     GemmArgs a = p;
@@ -142,7 +245,7 @@ bool gemv_i8_supports(const GemmArgs& p) {
 }
 
 hipError_t launch_gemv_i8(const GemmArgs& p, hipStream_t s) {
-    if (p.M <= 1) return launch_t<1, 16>(p, s);
+    if (p.M <= 1) return launch_rows<1>(p, s);
     if (p.M <= 2) return launch_t<2, 16>(p, s);
     if (p.M <= 4) return launch_t<4, 8>(p, s);
     if (p.M <= 8) return launch_t<8, 8>(p, s);
