@@ -41,8 +41,10 @@ def traffic(key):
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # ~50 ms of warm-up: the first ~50-100 ms of sustained MFMA load run at a
+    # lower, still-settling clock (measured 558 us/step there vs 505 after).
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--gemv-buffers", type=int, default=8)
     ap.add_argument("--gemv-launches", type=int, default=400)
     ap.add_argument("--extra", action="store_true", help="also time configs 2 and 4 and GEMV M=4,16")
