@@ -68,11 +68,13 @@ __device__ __forceinline__ float e4m3_decode(uint32_t x) {
 
 // Replace every 0x7F / 0xFF byte of a packed word by 0x00, so that the MFMA
 // (which reads those codes as NaN) sees the reference's 0.0.
+// (w & 0x7F..) + 0x01.. sets bit 7 of a byte exactly when its low 7 bits are
+// all ones (no carry can cross bytes); that bit, moved to bit 2, turns the
+// byte's v_perm selector i into 4+i, which selects a byte of the zero operand.
 __device__ __forceinline__ uint32_t e4m3_sanitize(uint32_t w) {
-    const uint32_t t = (w & 0x7F7F7F7Fu) ^ 0x7F7F7F7Fu;          // byte==0 iff code was x7F
-    const uint32_t z = ~(((t & 0x7F7F7F7Fu) + 0x7F7F7F7Fu) | t | 0x7F7F7F7Fu);  // 0x80 per zero byte
-    const uint32_t mask = (z >> 7) * 0xFFu;
-    return w & ~mask;
+    const uint32_t hi = (w & 0x7F7F7F7Fu) + 0x01010101u;
+    const uint32_t sel = ((hi >> 5) & 0x04040404u) | 0x03020100u;
+    return __builtin_amdgcn_perm(0u, w, sel);
 }
 
 // Canonical fused epilogue: s = fp32(sa_m*sb_n); y = bias ? fma(v,s,bias) : v*s.

@@ -3,18 +3,26 @@
 // Replaces the arithmetic of reference src/quantized_gemm.cu:15-54 (INT8,
 // int8_gemm_dp4a_kernel) and :99-118 (FP8, fp8_gemm_scaled_kernel) for M > 16.
 //
-// Workgroup tile 256x256 with 8 waves (two per SIMD): wave w owns rows
-// 128*((w>>1)&1) .. +128 and columns 64*((w&1) + 2*(w>>2)) .. +64, i.e. 4x2
-// MFMA blocks of 32x32 held in 128 AGPRs.  Two waves per SIMD let one wave
-// issue MFMAs while the other waits on LDS or memory.
-//   INT8: v_mfma_i32_32x32x32_i8   (exact int32 accumulation)
-//   FP8 : v_mfma_f32_32x32x64_f8f6f4 with E4M3 operands (fp32 accumulation)
+// Workgroup tile 256x256, 4 waves (one per SIMD) in a 2x2 grid; each wave owns
+// 128x128 outputs as 4x4 MFMA blocks of 32x32 (256 accumulator AGPRs).
+//   INT8: v_mfma_i32_32x32x32_i8   (exact int32 accumulation), 4 k steps/stage
+//   FP8 : v_mfma_f32_32x32x64_f8f6f4 with E4M3 operands (fp32), 2 k steps/stage
 // K advances 128 bytes per stage; two LDS stages of (256+256)x128 bytes
 // (128 KiB of the CU's 160 KiB).  A (and B when stored [N,K]) is copied
-// global->LDS with 128-bit direct-to-LDS loads (global_load_lds_dwordx4),
+// global->LDS with 128-bit direct-to-LDS loads (buffer_load_dwordx4 ... lds),
 // eight lanes per 128-byte row segment, from per-lane 32-bit offsets computed
 // once.  B stored [K,N] goes through registers and is byte-transposed with
-// v_perm_b32 before a ds_write_b64.
+// v_perm_b32 into LDS.
+//
+// Schedule of one stage, per wave (steps 0..n-1 of the stage are in LDS):
+//   MFMAs of the previous stage's last step + first copies | read step 1 |
+//   MFMAs of step 0 + more copies | read step 2 | ... | MFMAs of step n-2 |
+//   wait for this wave's reads and copies, barrier | read step 0 of the next
+//   stage.
+// Fragment reads run one k step ahead of the MFMAs that use them; the reads
+// right after a barrier hide behind the MFMAs carried over from the previous
+// stage, and the global->LDS copies are spread over the stage instead of
+// bursting at its top.  sched_barrier fences keep the compiler to this order.
 //
 // LDS layout of a stage: row r (an M row of A or an N row of B) holds its 128
 // K-bytes as eight 16-byte chunks; logical chunk c is stored at physical
@@ -38,21 +46,18 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr int BM = 256;
 constexpr int BN = 256;
-constexpr int BK = 128;           // bytes of K per stage
-constexpr int NWAVES = 8;
+constexpr int BK = 128;                      // bytes of K per stage
+constexpr int NWAVES = 4;
 constexpr int NTHREADS = NWAVES * 64;
-constexpr int STAGE_A = BM * BK;  // 32 KiB
-constexpr int STAGE_B = BN * BK;  // 32 KiB
-constexpr int PW = BM * BK / 1024 / NWAVES;  // DMA loads per wave per panel (4)
+constexpr int STAGE_A = BM * BK;             // 32 KiB
+constexpr int STAGE = (BM + BN) * BK;        // 64 KiB
+constexpr int PW = BM * BK / 1024 / NWAVES;  // DMA loads per wave per panel (8)
 
 __device__ __forceinline__ int swz(int r) { return ((r & 31) ^ ((r & 31) >> 3)) & 7; }
 
-// s_waitcnt vmcnt(N) with expcnt/lgkmcnt left unconstrained (gfx9 encoding).
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
+// s_waitcnt vmcnt(0) / lgkmcnt(0), the other counters unconstrained (gfx9 encoding).
+__device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
 // Workgroup barrier without the LDS fence of __syncthreads: every LDS write a
 // stage depends on comes from LDS-DMA (ordered by the explicit vmcnt wait
@@ -65,8 +70,23 @@ __device__ __forceinline__ void barrier() {
     asm volatile("" ::: "memory");
 }
 
-__device__ __forceinline__ void dma16(const int8_t* g, uint8_t* l) {
-    __builtin_amdgcn_global_load_lds(g, l, 16, 0, 0);
+__device__ __forceinline__ void fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// Buffer resource over `bytes` bytes at `base` (raw buffer: stride 0, bounds
+// checked against num_records; gfx9 dword3).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+
+// 16 bytes per lane, buffer -> LDS (buffer_load_dwordx4 ... lds): lane l's
+// bytes land at lds + 16*l.  The MUBUF form rather than global_load_lds: the
+// compiler treats a FLAT-encoded LDS DMA as a pending access of both memory
+// kinds and then waits for every outstanding LDS read (lgkmcnt(0)) wherever
+// one result is needed, which would serialise the fragment reads.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, int soff, uint8_t* l) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        r, reinterpret_cast<__attribute__((address_space(3))) void*>(reinterpret_cast<uintptr_t>(l)), 16,
+        static_cast<int>(voff), soff, 0, 0);
 }
 
 // Workgroup -> output tile.  Consecutive workgroup ids are dispatched round
@@ -96,39 +116,39 @@ __device__ __forceinline__ void tile_of(int bid, int gm, int gn, int& tm, int& t
 // the swizzle assigns to that physical slot.  Rows past `rows` re-read the
 // last valid row (their outputs are never stored).
 struct Panel {
-    int off[PW];  // byte offset of this lane's 16-byte source at k = 0
-    __device__ void init(int ld, int row0, int rows, int wave, int lane) {
+    __amdgpu_buffer_rsrc_t rsrc;  // the whole operand, rows x ld bytes
+    uint32_t off[PW];             // byte offset of this lane's 16-byte source at k = 0
+    __device__ void init(const int8_t* base, int ld, int row0, int rows, int wave, int lane) {
+        rsrc = make_rsrc(base, rows * ld);
 #pragma unroll
         for (int i = 0; i < PW; ++i) {
             const int seg = wave * PW + i;
             const int r = seg * 8 + (lane >> 3);
             const int lc = (lane & 7) ^ swz(r);
-            off[i] = min(row0 + r, rows - 1) * ld + lc * 16;
+            off[i] = static_cast<uint32_t>(min(row0 + r, rows - 1) * ld + lc * 16);
         }
     }
-    // gk: uniform panel base at this stage's k; wave: uniform wave index.
-    __device__ __forceinline__ void issue(const int8_t* gk, uint8_t* lds, int wave) const {
-#pragma unroll
-        for (int i = 0; i < PW; ++i)
-            dma16(gk + static_cast<uint32_t>(off[i]), lds + (wave * PW + i) * 1024);
+    // Load i of this wave for the stage at K byte k0 (uniform).
+    __device__ __forceinline__ void issue(int i, int k0, uint8_t* lds, int wave) const {
+        dma16(rsrc, off[i], k0, lds + (wave * PW + i) * 1024);
     }
 };
 
-// B stored [K,N]: each thread owns an 8(k) x 8(n) byte block of the 128 x 256
-// stage tile (thread t: n group t%32, k group t/32), loaded as eight 8-byte
-// rows so that 32 lanes read 256 contiguous bytes of one k row.
+// B stored [K,N]: each thread owns an 8(k) x 16(n) byte block of the 128 x 256
+// stage tile (thread t: n block t%16, k block t/16), loaded as eight 16-byte
+// rows so that 16 lanes read 256 contiguous bytes of one k row.
 struct KNPlan {
-    const int8_t* base;  // B + n (column group start, clamped) at k = 8*(t/32)
+    const int8_t* base;  // B + n (column block start, clamped) at k = 8*(t/16)
     int N;
     __device__ void init(const int8_t* B, int N_, int n0, int tid) {
         N = N_;
-        const int n = min(n0 + (tid & 31) * 8, N_ - 8);  // ragged N: re-read the last group
-        base = B + n + static_cast<size_t>(tid >> 5) * 8 * N_;
+        const int n = min(n0 + (tid & 15) * 16, N_ - 16);  // ragged N: re-read the last block
+        base = B + n + static_cast<size_t>(tid >> 4) * 8 * N_;
     }
-    __device__ __forceinline__ void load(int k0, uint2 (&r)[8]) const {
+    __device__ __forceinline__ void load(int k0, v4i (&r)[8]) const {
         const int8_t* q = base + static_cast<size_t>(k0) * N;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) r[i] = *reinterpret_cast<const uint2*>(q + static_cast<size_t>(i) * N);
+        for (int i = 0; i < 8; ++i) r[i] = *reinterpret_cast<const v4i*>(q + static_cast<size_t>(i) * N);
     }
 };
 
@@ -145,134 +165,121 @@ __device__ __forceinline__ void t4x4(uint32_t x0, uint32_t x1, uint32_t x2, uint
     y3 = __builtin_amdgcn_perm(t3, t1, 0x07060302u);                 // a3 b3 c3 d3
 }
 
-// Transpose the thread's 8x8 block and store it as 8 bytes (k = 8*kg..+8) of
-// eight B^T rows (n = 8*ng + c).
+// Transpose the thread's 8(k) x 16(n) block and store, for each of its 16
+// columns n, the 8 bytes k = 8*kb..+8 of B^T row n.
 template <int ELEM>
-__device__ __forceinline__ void kn_store(const uint2 (&r)[8], uint8_t* lds_b, int tid) {
-    const int ng = tid & 31, kg = tid >> 5;
+__device__ __forceinline__ void kn_store(const v4i (&r)[8], uint8_t* lds_b, int tid) {
+    const int nb = tid & 15, kb = tid >> 4;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {  // column halves: bytes 0..3 (.x) and 4..7 (.y)
+    for (int q = 0; q < 4; ++q) {  // columns 4q..4q+3 of the block: word q of each row
         uint32_t lo[4], hi[4];
-        if (h == 0) {
-            t4x4(r[0].x, r[1].x, r[2].x, r[3].x, lo[0], lo[1], lo[2], lo[3]);
-            t4x4(r[4].x, r[5].x, r[6].x, r[7].x, hi[0], hi[1], hi[2], hi[3]);
-        } else {
-            t4x4(r[0].y, r[1].y, r[2].y, r[3].y, lo[0], lo[1], lo[2], lo[3]);
-            t4x4(r[4].y, r[5].y, r[6].y, r[7].y, hi[0], hi[1], hi[2], hi[3]);
-        }
+        t4x4(r[0][q], r[1][q], r[2][q], r[3][q], lo[0], lo[1], lo[2], lo[3]);
+        t4x4(r[4][q], r[5][q], r[6][q], r[7][q], hi[0], hi[1], hi[2], hi[3]);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            const int n = ng * 8 + h * 4 + c;
+            const int n = nb * 16 + q * 4 + c;
             uint32_t w0 = lo[c], w1 = hi[c];
             if constexpr (ELEM == ELEM_F8) {
                 w0 = e4m3_sanitize(w0);
                 w1 = e4m3_sanitize(w1);
             }
-            const int chunk = (kg >> 1) ^ swz(n);
-            *reinterpret_cast<uint2*>(lds_b + n * BK + chunk * 16 + (kg & 1) * 8) = make_uint2(w0, w1);
+            const int chunk = (kb >> 1) ^ swz(n);
+            *reinterpret_cast<uint2*>(lds_b + n * BK + chunk * 16 + (kb & 1) * 8) = make_uint2(w0, w1);
         }
     }
 }
 
-// FP8 operands staged by DMA cannot be rewritten on the way in; sanitize the
-// 0x7F/0xFF codes in the fragment registers instead.
+// Per element type: fragment and accumulator types, k steps per stage.
+template <int ELEM>
+struct Mma;
+template <>
+struct Mma<ELEM_I8> {
+    using Frag = v4i;  // 16 k bytes per lane
+    using AccT = v16i;
+    static constexpr int KSTEPS = BK / 32;
+};
+template <>
+struct Mma<ELEM_F8> {
+    using Frag = v8i;  // 32 k codes per lane
+    using AccT = v16f;
+    static constexpr int KSTEPS = BK / 64;
+};
+
+template <int ELEM>
+struct Frags {
+    typename Mma<ELEM>::Frag a[4], b[4];
+};
+
+// Issues the LDS reads of the wave's fragments of k step ks.  A rows
+// wm*128 + 32*i + lr and B^T rows wn*128 + 32*j + lr share swz(lr), so each
+// operand needs one address plus immediate offsets.  Nothing here waits for
+// the data: the MFMAs that consume it come one block later.
+template <int ELEM>
+__device__ __forceinline__ void read_frags(const uint8_t* buf, int ks, int wm, int wn, int lane,
+                                           Frags<ELEM>& f) {
+    const int lr = lane & 31, lh = lane >> 5, sw = swz(lr);
+    const uint8_t* Ab = buf + (wm * 128 + lr) * BK;
+    const uint8_t* Bb = buf + STAGE_A + (wn * 128 + lr) * BK;
+    if constexpr (ELEM == ELEM_I8) {
+        const int co = ((ks * 2 + lh) ^ sw) << 4;  // this lane's 16-byte chunk of the 32-byte step
+#pragma unroll
+        for (int i = 0; i < 4; ++i) f.a[i] = *reinterpret_cast<const v4i*>(Ab + i * 32 * BK + co);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) f.b[j] = *reinterpret_cast<const v4i*>(Bb + j * 32 * BK + co);
+    } else {
+        // two 16-byte chunks = 32 k codes per lane
+        const int cx = ((ks * 4 + lh * 2) ^ sw) << 4, cy = ((ks * 4 + lh * 2 + 1) ^ sw) << 4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const v4i x = *reinterpret_cast<const v4i*>(Ab + i * 32 * BK + cx);
+            const v4i y = *reinterpret_cast<const v4i*>(Ab + i * 32 * BK + cy);
+            f.a[i] = v8i{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const v4i x = *reinterpret_cast<const v4i*>(Bb + j * 32 * BK + cx);
+            const v4i y = *reinterpret_cast<const v4i*>(Bb + j * 32 * BK + cy);
+            f.b[j] = v8i{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+        }
+    }
+}
+
+// FP8 operands staged by DMA cannot be rewritten on the way in; their
+// 0x7F/0xFF codes are cleared in the fragment registers, just before use.
 __device__ __forceinline__ v8i sanitize8(v8i x) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) x[i] = static_cast<int>(e4m3_sanitize(static_cast<uint32_t>(x[i])));
     return x;
 }
 
-template <int ELEM>
-struct Acc;
-template <>
-struct Acc<ELEM_I8> {
-    using T = v16i;
-};
-template <>
-struct Acc<ELEM_F8> {
-    using T = v16f;
-};
-
-// One stage of MFMAs for this wave's 128x64 block: rows r0.. of the stage's A
-// rows (As) and columns c0.. of its B^T rows (Bs).  `live` false zeroes the B
-// fragments (a phantom stage that must add nothing).
+// The 16 MFMAs of one k step of the wave's 128x128 block.
 template <int ELEM, int BL>
-__device__ __forceinline__ void stage_compute(const uint8_t* As, const uint8_t* Bs,
-                                              typename Acc<ELEM>::T (&acc)[4][2], int r0, int c0,
-                                              int lane, bool live) {
-    const int lr = lane & 31;
-    const int lh = lane >> 5;
-    // Rows r0 + 32*i + lr share swz(lr): one base address per operand and k
-    // step, the 32-row blocks at immediate offsets of 32*BK bytes.
-    const int sw = swz(lr);
-    const uint8_t* Ab = As + (r0 + lr) * BK;
-    const uint8_t* Bb = Bs + (c0 + lr) * BK;
+__device__ __forceinline__ void mfma_step(const Frags<ELEM>& f, typename Mma<ELEM>::AccT (&acc)[4][4]) {
     if constexpr (ELEM == ELEM_I8) {
-        // Fragments of k step ks+1 are read while the MFMAs of step ks run.
-        auto rd = [&](int ks, v4i (&a)[4], v4i (&b)[2]) {
-            const int co = ((ks * 2 + lh) ^ sw) << 4;  // this lane's 16-byte chunk of the 32-byte step
 #pragma unroll
-            for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const v4i*>(Ab + i * 32 * BK + co);
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j) b[j] = *reinterpret_cast<const v4i*>(Bb + j * 32 * BK + co);
-        };
-        v4i a0[4], b0[2], a1[4], b1[2];
-        auto mm = [&](const v4i (&a)[4], const v4i (&b)[2]) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], live ? b[j] : v4i{0, 0, 0, 0},
-                                                                      acc[i][j], 0, 0, 0);
-        };
-        // Program order per step: reads of step ks+1, then the MFMAs of step
-        // ks (fenced, so the MFMAs only wait on reads issued a block earlier).
-        rd(0, a0, b0);
-#pragma unroll
-        for (int ks = 0; ks < BK / 32; ks += 2) {
-            rd(ks + 1, a1, b1);
-            __builtin_amdgcn_sched_barrier(0);
-            mm(a0, b0);
-            __builtin_amdgcn_sched_barrier(0);
-            if (ks + 2 < BK / 32) rd(ks + 2, a0, b0);
-            __builtin_amdgcn_sched_barrier(0);
-            mm(a1, b1);
-            __builtin_amdgcn_sched_barrier(0);
-        }
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
     } else {
+        v8i b[4];
 #pragma unroll
-        for (int ks = 0; ks < BK / 64; ++ks) {
-            const int cx = ((ks * 4 + lh * 2) ^ sw) << 4;      // two 16-byte chunks = 32 k codes per lane
-            const int cy = ((ks * 4 + lh * 2 + 1) ^ sw) << 4;
-            v8i a[4], b[2];
+        for (int j = 0; j < 4; ++j) b[j] = BL == FKE_B_NK ? sanitize8(f.b[j]) : f.b[j];  // KN: sanitized at staging
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const v4i x = *reinterpret_cast<const v4i*>(Ab + i * 32 * BK + cx);
-                const v4i y = *reinterpret_cast<const v4i*>(Ab + i * 32 * BK + cy);
-                a[i] = sanitize8(v8i{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]});
-            }
+        for (int i = 0; i < 4; ++i) {
+            const v8i a = sanitize8(f.a[i]);
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const v4i x = *reinterpret_cast<const v4i*>(Bb + j * 32 * BK + cx);
-                const v4i y = *reinterpret_cast<const v4i*>(Bb + j * 32 * BK + cy);
-                b[j] = v8i{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
-                if constexpr (BL == FKE_B_NK) b[j] = sanitize8(b[j]);  // KN was sanitized at staging
-                if (!live) b[j] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                        a[i], b[j], acc[i][j], 0, 0, 0, 0, 0, 0);
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b[j], acc[i][j], 0, 0, 0, 0, 0, 0);
         }
     }
 }
 
 template <int ELEM, int BL, int OUT>
 __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
-    __shared__ __attribute__((aligned(1024))) uint8_t lds0[STAGE_A + STAGE_B];
-    __shared__ __attribute__((aligned(1024))) uint8_t lds1[STAGE_A + STAGE_B];
+    constexpr int NKS = Mma<ELEM>::KSTEPS;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds0[STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds1[STAGE];
     __shared__ __attribute__((aligned(16))) float epi_sa[BM];    // scale of each tile row
     __shared__ __attribute__((aligned(16))) float epi_sb[BN];    // scale of each tile column
     __shared__ __attribute__((aligned(16))) float epi_bias[BN];  // bias of each tile column
@@ -280,8 +287,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar LDS/M0 math
-    const int r0 = ((wave >> 1) & 1) * 128;             // wave's rows within the tile
-    const int c0 = ((wave & 1) + 2 * (wave >> 2)) * 64;  // wave's columns within the tile
+    const int wm = wave >> 1, wn = wave & 1;                     // wave's 128x128 block
 
     const int M = p.M, N = p.N, K = p.K;
     const int gm = (M + BM - 1) / BM, gn = (N + BN - 1) / BN;
@@ -292,106 +298,137 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
     const int8_t* A = static_cast<const int8_t*>(p.A);
     const int8_t* B = static_cast<const int8_t*>(p.B);
 
-    // epilogue operands -> LDS (visible after the first barrier below)
-    if (tid < BM) {
+    // epilogue operands -> LDS (visible after the prologue barrier)
+    {
         const int m = min(m0 + tid, M - 1);
+        const int n = min(n0 + tid, N - 1);
         epi_sa[tid] = p.scale_a ? p.scale_a[m] : p.sa;
-    } else {
-        const int c = tid - BM;
-        const int n = min(n0 + c, N - 1);
-        epi_sb[c] = p.scale_b ? p.scale_b[n] : p.sb;
-        epi_bias[c] = p.bias ? p.bias[n] : 0.0f;
+        epi_sb[tid] = p.scale_b ? p.scale_b[n] : p.sb;
+        epi_bias[tid] = p.bias ? p.bias[n] : 0.0f;
     }
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the epilogue-operand ds_writes are done
 
-    typename Acc<ELEM>::T acc[4][2];
+    typename Mma<ELEM>::AccT acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
 
     const int KT = K / BK;
     Panel pa, pb;
-    pa.init(K, m0, M, wave, lane);
+    pa.init(A, K, m0, M, wave, lane);
     KNPlan kp;
-    if constexpr (BL == FKE_B_NK) pb.init(K, n0, N, wave, lane);
+    if constexpr (BL == FKE_B_NK) pb.init(B, K, n0, N, wave, lane);
     else kp.init(B, N, n0, tid);
-    uint2 knr[8];
+    v4i knr[8];
 
-    // Stage kt -> buffer: DMA for A (and B in NK order); B in KN order is
-    // loaded into registers here and transposed into LDS by finish().
-    // The DMA block is fenced on both sides: each global_load_lds needs its own
-    // M0 value, and an M0 write that the scheduler hoists into the MFMA stream
-    // costs an lgkmcnt(0) wait there.
-    auto issue = [&](int kt, uint8_t* buf) {
-        __builtin_amdgcn_sched_barrier(0);
-        pa.issue(A + kt * BK, buf, wave);
-        if constexpr (BL == FKE_B_NK) pb.issue(B + kt * BK, buf + STAGE_A, wave);
-        else kp.load(kt * BK, knr);
-        __builtin_amdgcn_sched_barrier(0);
-    };
-    auto finish = [&](uint8_t* buf) {
-        if constexpr (BL == FKE_B_KN) {
-            kn_store<ELEM>(knr, buf + STAGE_A, tid);
-            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): own ds_writes done
+    // Copy of stage kt into buffer b, slot q of NSLOT.  [N,K]: slots 0..PW-1
+    // copy A, PW..2PW-1 copy B, all by DMA.  [K,N]: slot 0 loads this
+    // thread's B block into registers (first, so the loads have the whole
+    // stage to land), slots 1..PW copy A; kn_commit() transposes the block
+    // into LDS before the barrier.
+    constexpr int NSLOT = BL == FKE_B_NK ? 2 * PW : PW + 1;
+    auto copy = [&](int q, int kt, uint8_t* b) {
+        if constexpr (BL == FKE_B_NK) {
+            if (q < PW) pa.issue(q, kt * BK, b, wave);
+            else pb.issue(q - PW, kt * BK, b + STAGE_A, wave);
+        } else {
+            if (q == 0) kp.load(kt * BK, knr);
+            else pa.issue(q - 1, kt * BK, b, wave);
         }
-        wait_vm<0>();
+    };
+    auto kn_commit = [&](uint8_t* b) {
+        if constexpr (BL == FKE_B_KN) kn_store<ELEM>(knr, b + STAGE_A, tid);
+    };
+    // Slots issued with MFMA group g (g = 0: the carried step, g = s + 1:
+    // step s), spread over all groups but the last so the copies have time
+    // to land before the end-of-stage wait.
+    constexpr int PER_GROUP = (NSLOT + NKS - 2) / (NKS - 1);
+
+    Frags<ELEM> f0, f1;
+    // Prologue: stage 0 -> lds0; f1 (the carried fragments) starts at zero.
+#pragma unroll
+    for (int q = 0; q < NSLOT; ++q) copy(q, 0, lds0);
+    kn_commit(lds0);
+    wait_lgkm0();
+    wait_vm0();
+    barrier();
+    read_frags<ELEM>(lds0, 0, wm, wn, lane, f0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        f1.a[i] = typename Mma<ELEM>::Frag{};
+        f1.b[i] = typename Mma<ELEM>::Frag{};
+    }
+
+    // One stage: `cur` holds stage kt, f0 its step-0 fragments (reads
+    // issued); `nxt` receives stage kt+1 (the last stage re-copies itself).
+    // f1 enters with the previous stage's last step and leaves with this
+    // stage's.
+    auto stage = [&](const uint8_t* cur, uint8_t* nxt, int kt) {
+        const int kc = min(kt + 1, KT - 1);
+        fence();
+        mfma_step<ELEM, BL>(f1, acc);
+#pragma unroll
+        for (int q = 0; q < PER_GROUP && q < NSLOT; ++q) copy(q, kc, nxt);
+        fence();
+#pragma unroll
+        for (int s = 0; s + 1 < NKS; ++s) {
+            Frags<ELEM>& rd = s % 2 == 0 ? f1 : f0;
+            Frags<ELEM>& mm = s % 2 == 0 ? f0 : f1;
+            read_frags<ELEM>(cur, s + 1, wm, wn, lane, rd);
+            fence();
+            mfma_step<ELEM, BL>(mm, acc);
+#pragma unroll
+            for (int q = (s + 1) * PER_GROUP; q < (s + 2) * PER_GROUP && q < NSLOT; ++q) copy(q, kc, nxt);
+            fence();
+        }
+        static_assert(NKS % 2 == 0, "the last step's fragments must land in f1");
+        kn_commit(nxt);
+        wait_lgkm0();  // last step's fragments in registers: cur may be overwritten after the barrier
+        wait_vm0();    // this wave's share of stage kt+1 has landed
         barrier();
+        fence();
     };
 
-    // Two-stage pipeline with static buffer roles (lds0 / lds1 are distinct
-    // objects, so the compiler can see that a stage's LDS DMA never aliases
-    // the other stage's fragment reads and need not wait on it early).  The
-    // sched_barrier after each issue keeps the loads ahead of the stage's
-    // MFMAs (the scheduler would otherwise sink them below), and the body has
-    // no data-dependent branches, so the accumulators stay in AGPRs.
-    issue(0, lds0);
-    finish(lds0);
+    // Buffer roles are static (lds0 / lds1 are distinct objects, so the
+    // compiler sees that a stage's DMA never aliases the other stage's
+    // reads), hence two stages per iteration; the body has no data-dependent
+    // branches, so the accumulators stay in AGPRs.
     int kt = 0;
-    for (; kt + 2 < KT; kt += 2) {
-        issue(kt + 1, lds1);
-        __builtin_amdgcn_sched_barrier(0);
-        stage_compute<ELEM, BL>(lds0, lds0 + STAGE_A, acc, r0, c0, lane, true);
-        finish(lds1);
-        issue(kt + 2, lds0);
-        __builtin_amdgcn_sched_barrier(0);
-        stage_compute<ELEM, BL>(lds1, lds1 + STAGE_A, acc, r0, c0, lane, true);
-        finish(lds0);
+    for (; kt + 2 <= KT; kt += 2) {
+        stage(lds0, lds1, kt);
+        read_frags<ELEM>(lds1, 0, wm, wn, lane, f0);
+        stage(lds1, lds0, kt + 1);
+        read_frags<ELEM>(lds0, 0, wm, wn, lane, f0);
     }
-    // Tail: one or two stages remain, stage kt is in lds0.  With one left, the
-    // lds1 stage re-reads stage kt (a valid address) and its B fragments are
-    // zeroed, so it adds nothing.
-    issue(min(kt + 1, KT - 1), lds1);
-    __builtin_amdgcn_sched_barrier(0);
-    stage_compute<ELEM, BL>(lds0, lds0 + STAGE_A, acc, r0, c0, lane, true);
-    finish(lds1);
-    stage_compute<ELEM, BL>(lds1, lds1 + STAGE_A, acc, r0, c0, lane, kt + 1 < KT);
+    if (kt < KT) stage(lds0, lds1, kt);  // odd stage count
+    mfma_step<ELEM, BL>(f1, acc);         // the last stage's carried step
 
     // Fused epilogue.  32x32 block layout of the accumulator: lane l holds
     // column l%32 and rows 8*(v/4) + 4*(l/32) + v%4 for v = 0..15.
     const int lr = lane & 31, lh = lane >> 5;
     const bool has_bias = p.bias != nullptr;
+    const bool full = m0 + BM <= M && n0 + BN <= N;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int cn = c0 + j * 32 + lr;  // column within the tile
+    for (int j = 0; j < 4; ++j) {
+        const int cn = wn * 128 + j * 32 + lr;  // column within the tile
         const int n = n0 + cn;
         const float sbn = epi_sb[cn];
         const float bn = epi_bias[cn];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            __builtin_amdgcn_sched_barrier(0);
+            fence();
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const int rm = r0 + i * 32 + 8 * g + 4 * lh;  // first of 4 consecutive tile rows
+                const int rm = wm * 128 + i * 32 + 8 * g + 4 * lh;  // first of 4 consecutive tile rows
                 const float4 sa4 = *reinterpret_cast<const float4*>(&epi_sa[rm]);
                 const float sav[4] = {sa4.x, sa4.y, sa4.z, sa4.w};
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int v = 4 * g + e;
                     const int m = m0 + rm + e;
-                    if (m >= M || n >= N) continue;
+                    if (!full && (m >= M || n >= N)) continue;
                     const size_t idx = static_cast<size_t>(m) * N + n;
                     if constexpr (ELEM == ELEM_I8) {
                         const int32_t a = acc[i][j][v];
