@@ -14,15 +14,15 @@
 // once.  B stored [K,N] goes through registers and is byte-transposed with
 // v_perm_b32 into LDS.
 //
-// Schedule of one stage, per wave (steps 0..n-1 of the stage are in LDS):
-//   MFMAs of the previous stage's last step + first copies | read step 1 |
-//   MFMAs of step 0 + more copies | read step 2 | ... | MFMAs of step n-2 |
-//   wait for this wave's reads and copies, barrier | read step 0 of the next
-//   stage.
-// Fragment reads run one k step ahead of the MFMAs that use them; the reads
-// right after a barrier hide behind the MFMAs carried over from the previous
-// stage, and the global->LDS copies are spread over the stage instead of
-// bursting at its top.  sched_barrier fences keep the compiler to this order.
+// Schedule of one stage, per wave (steps 0..n-1 of the stage are in LDS): n
+// groups of 16 MFMAs.  Group 0 runs the previous stage's last step, carried
+// across the barrier, while the reads of step 0 are issued; group g > 0 runs
+// step g-1 while the reads of step g are issued.  The global->LDS copies of
+// the next stage ride along in the first groups, one instruction per MFMA.
+// The stage ends with a wait for this wave's reads and copies and a barrier.
+// Fragment reads thus run one group ahead of their MFMAs and no memory
+// instruction waits in a queue of its own; sched_barrier / sched_group_barrier
+// keep the compiler to this order.
 //
 // LDS layout of a stage: row r (an M row of A or an N row of B) holds its 128
 // K-bytes as eight 16-byte chunks; logical chunk c is stored at physical
@@ -35,6 +35,8 @@
 // The per-row / per-column epilogue operands of the tile (scale_a, scale_b,
 // bias) are staged once in LDS beside the two stages.
 #include "fke_internal.h"
+
+#include <type_traits>
 
 namespace fke {
 namespace {
@@ -304,7 +306,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
         const int n = min(n0 + tid, N - 1);
         epi_sa[tid] = p.scale_a ? p.scale_a[m] : p.sa;
         epi_sb[tid] = p.scale_b ? p.scale_b[n] : p.sb;
-        epi_bias[tid] = p.bias ? p.bias[n] : 0.0f;
+        epi_bias[tid] = p.bias ? p.bias[n] : -0.0f;
     }
 
     typename Mma<ELEM>::AccT acc[4][4];
@@ -341,55 +343,76 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
     auto kn_commit = [&](uint8_t* b) {
         if constexpr (BL == FKE_B_KN) kn_store<ELEM>(knr, b + STAGE_A, tid);
     };
-    // Slots issued with MFMA group g (g = 0: the carried step, g = s + 1:
-    // step s), spread over all groups but the last so the copies have time
-    // to land before the end-of-stage wait.
+    // A stage is NKS groups of 16 MFMAs.  Group g runs the MFMAs of one
+    // fragment set (g = 0: the previous stage's last step, carried across
+    // the barrier; g > 0: step g-1) while the LDS reads of step g fill the
+    // other set, and carries copy slots of the next stage: slots are spread
+    // over all groups but the last, which instead takes the [K,N] transpose.
+    // Within a group every memory instruction is paired with an MFMA
+    // (sched_group_barrier), so it issues in the MFMA's shadow instead of
+    // stalling the matrix pipe.
     constexpr int PER_GROUP = (NSLOT + NKS - 2) / (NKS - 1);
-
     Frags<ELEM> f0, f1;
-    // Prologue: stage 0 -> lds0; f1 (the carried fragments) starts at zero.
+    constexpr int NREAD = ELEM == ELEM_I8 ? 8 : 16;  // ds_read_b128 per step
+    auto group = [&](auto q0c, auto q1c, auto commitc, const Frags<ELEM>& use, Frags<ELEM>& fill,
+                     const uint8_t* cur, int rks, uint8_t* nxt, int kc) {
+        constexpr int Q0 = decltype(q0c)::value, Q1 = decltype(q1c)::value;
+        constexpr bool COMMIT = decltype(commitc)::value;
+        // vector-memory instructions of slots [Q0, Q1): the [K,N] register load is 8
+        constexpr int NV = (Q1 - Q0) + (BL == FKE_B_KN && Q0 == 0 && Q1 > 0 ? 7 : 0);
+        static_assert(NV <= 16, "at most one vector-memory instruction per MFMA");
+        fence();
+        mfma_step<ELEM, BL>(use, acc);
+        read_frags<ELEM>(cur, rks, wm, wn, lane, fill);
+#pragma unroll
+        for (int q = Q0; q < Q1; ++q) copy(q, kc, nxt);
+        if constexpr (COMMIT) kn_commit(nxt);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);      // MFMA
+            if (i < NREAD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+            if (i >= 16 - NV) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+            if (COMMIT && i >= 8) __builtin_amdgcn_sched_group_barrier(0x200, 4, 0);  // DS write
+        }
+        fence();
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using F = std::false_type;
+    auto stage = [&](const uint8_t* cur, uint8_t* nxt, int kt) {
+        const int kc = min(kt + 1, KT - 1);  // the last stage re-copies itself
+        constexpr bool KN = BL == FKE_B_KN;
+        if constexpr (NKS == 4) {
+            constexpr int P = PER_GROUP;
+            group(I0{}, std::integral_constant<int, P>{}, F{}, f1, f0, cur, 0, nxt, kc);
+            group(std::integral_constant<int, P>{}, std::integral_constant<int, (2 * P < NSLOT ? 2 * P : NSLOT)>{}, F{},
+                  f0, f1, cur, 1, nxt, kc);
+            group(std::integral_constant<int, (2 * P < NSLOT ? 2 * P : NSLOT)>{}, std::integral_constant<int, NSLOT>{}, F{},
+                  f1, f0, cur, 2, nxt, kc);
+            group(std::integral_constant<int, NSLOT>{}, std::integral_constant<int, NSLOT>{},
+                  std::integral_constant<bool, KN>{}, f0, f1, cur, 3, nxt, kc);
+        } else {
+            static_assert(NKS == 2, "k steps per stage");
+            group(I0{}, std::integral_constant<int, NSLOT>{}, F{}, f1, f0, cur, 0, nxt, kc);
+            group(std::integral_constant<int, NSLOT>{}, std::integral_constant<int, NSLOT>{},
+                  std::integral_constant<bool, KN>{}, f0, f1, cur, 1, nxt, kc);
+        }
+        wait_lgkm0();  // last step's fragments in registers (f1): cur may be overwritten after the barrier
+        wait_vm0();    // this wave's share of stage kt+1 has landed
+        barrier();
+    };
+
+    // Prologue: stage 0 -> lds0; f1 (the carried set) starts at zero.
 #pragma unroll
     for (int q = 0; q < NSLOT; ++q) copy(q, 0, lds0);
     kn_commit(lds0);
     wait_lgkm0();
     wait_vm0();
     barrier();
-    read_frags<ELEM>(lds0, 0, wm, wn, lane, f0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         f1.a[i] = typename Mma<ELEM>::Frag{};
         f1.b[i] = typename Mma<ELEM>::Frag{};
     }
-
-    // One stage: `cur` holds stage kt, f0 its step-0 fragments (reads
-    // issued); `nxt` receives stage kt+1 (the last stage re-copies itself).
-    // f1 enters with the previous stage's last step and leaves with this
-    // stage's.
-    auto stage = [&](const uint8_t* cur, uint8_t* nxt, int kt) {
-        const int kc = min(kt + 1, KT - 1);
-        fence();
-        mfma_step<ELEM, BL>(f1, acc);
-#pragma unroll
-        for (int q = 0; q < PER_GROUP && q < NSLOT; ++q) copy(q, kc, nxt);
-        fence();
-#pragma unroll
-        for (int s = 0; s + 1 < NKS; ++s) {
-            Frags<ELEM>& rd = s % 2 == 0 ? f1 : f0;
-            Frags<ELEM>& mm = s % 2 == 0 ? f0 : f1;
-            read_frags<ELEM>(cur, s + 1, wm, wn, lane, rd);
-            fence();
-            mfma_step<ELEM, BL>(mm, acc);
-#pragma unroll
-            for (int q = (s + 1) * PER_GROUP; q < (s + 2) * PER_GROUP && q < NSLOT; ++q) copy(q, kc, nxt);
-            fence();
-        }
-        static_assert(NKS % 2 == 0, "the last step's fragments must land in f1");
-        kn_commit(nxt);
-        wait_lgkm0();  // last step's fragments in registers: cur may be overwritten after the barrier
-        wait_vm0();    // this wave's share of stage kt+1 has landed
-        barrier();
-        fence();
-    };
 
     // Buffer roles are static (lds0 / lds1 are distinct objects, so the
     // compiler sees that a stage's DMA never aliases the other stage's
@@ -398,24 +421,35 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
     int kt = 0;
     for (; kt + 2 <= KT; kt += 2) {
         stage(lds0, lds1, kt);
-        read_frags<ELEM>(lds1, 0, wm, wn, lane, f0);
         stage(lds1, lds0, kt + 1);
-        read_frags<ELEM>(lds0, 0, wm, wn, lane, f0);
     }
     if (kt < KT) stage(lds0, lds1, kt);  // odd stage count
     mfma_step<ELEM, BL>(f1, acc);         // the last stage's carried step
 
     // Fused epilogue.  32x32 block layout of the accumulator: lane l holds
     // column l%32 and rows 8*(v/4) + 4*(l/32) + v%4 for v = 0..15.
+    // y = fma(acc, sa_m*sb_n, bias_n) with bias_n = -0.0 when there is no
+    // bias, which is exactly acc*s (signed zeros included).
+    // The tile is written through a buffer resource based at row m0 whose
+    // range ends at the last valid row, so stores to rows >= M fall out of
+    // range and are dropped; a lane whose column is >= N adds 2^31 to its
+    // offsets and drops all of its stores.  One code path serves full and
+    // edge tiles.  Stores are non-temporal: the output is written once and
+    // should not evict the operand panels other workgroups still stream
+    // through L2.
+    constexpr int OB = OUT == FKE_OUT_BF16 ? 2 : 4;  // output bytes per element
     const int lr = lane & 31, lh = lane >> 5;
-    const bool has_bias = p.bias != nullptr;
-    const bool full = m0 + BM <= M && n0 + BN <= N;
+    const uint32_t row_bytes = static_cast<uint32_t>(N) * OB;
+    const __amdgpu_buffer_rsrc_t rc = make_rsrc(static_cast<char*>(p.C) + static_cast<size_t>(m0) * row_bytes,
+                                                min(M - m0, BM) * static_cast<int>(row_bytes));
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int cn = wn * 128 + j * 32 + lr;  // column within the tile
-        const int n = n0 + cn;
         const float sbn = epi_sb[cn];
         const float bn = epi_bias[cn];
+        const uint32_t lane_off = n0 + cn < N
+            ? static_cast<uint32_t>(wm * 128 + 4 * lh) * row_bytes + static_cast<uint32_t>(n0 + cn) * OB
+            : 0x80000000u;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             fence();
@@ -427,20 +461,21 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int v = 4 * g + e;
-                    const int m = m0 + rm + e;
-                    if (!full && (m >= M || n >= N)) continue;
-                    const size_t idx = static_cast<size_t>(m) * N + n;
+                    const int voff = static_cast<int>(lane_off + static_cast<uint32_t>(i * 32 + 8 * g + e) * row_bytes);
+                    float y;
+                    int32_t a = 0;
                     if constexpr (ELEM == ELEM_I8) {
-                        const int32_t a = acc[i][j][v];
-                        const float s = sav[e] * sbn;
-                        const float y = has_bias ? __builtin_fmaf(static_cast<float>(a), s, bn)
-                                                 : static_cast<float>(a) * s;
-                        store_out<OUT>(p.C, idx, y, a);
+                        a = acc[i][j][v];
+                        y = __builtin_fmaf(static_cast<float>(a), sav[e] * sbn, bn);
                     } else {
-                        const float s = p.sa * p.sb;
-                        const float y = has_bias ? __builtin_fmaf(acc[i][j][v], s, bn) : acc[i][j][v] * s;
-                        store_out<OUT>(p.C, idx, y, 0);
+                        y = __builtin_fmaf(acc[i][j][v], p.sa * p.sb, bn);
                     }
+                    if constexpr (OUT == FKE_OUT_F32)
+                        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(y), rc, voff, 0, 2);
+                    else if constexpr (OUT == FKE_OUT_BF16)
+                        __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_rne(y), rc, voff, 0, 2);
+                    else
+                        __builtin_amdgcn_raw_buffer_store_b32(static_cast<uint32_t>(a), rc, voff, 0, 2);
                 }
             }
         }
@@ -478,6 +513,8 @@ bool mfma_supports(const GemmArgs& p, int elem) {
     if (static_cast<int64_t>(p.M) * p.K > INT32_MAX) return false;
     if (p.b_layout == FKE_B_NK && static_cast<int64_t>(p.N) * p.K > INT32_MAX) return false;
     if (p.b_layout == FKE_B_KN && (p.N % 16 != 0)) return false;
+    // epilogue offsets are 32-bit: 256 output rows plus the 2^31 drop offset
+    if (p.N > (1 << 20)) return false;
     return true;
 }
 
