@@ -167,28 +167,31 @@ __device__ __forceinline__ void t4x4(uint32_t x0, uint32_t x1, uint32_t x2, uint
     y3 = __builtin_amdgcn_perm(t3, t1, 0x07060302u);                 // a3 b3 c3 d3
 }
 
-// Transpose the thread's 8(k) x 16(n) block and store, for each of its 16
-// columns n, the 8 bytes k = 8*kb..+8 of B^T row n.
+// Transpose columns 4q..4q+3 of the thread's 8(k) x 16(n) block and store,
+// for each such column n, the 8 bytes k = 8*kb..+8 of B^T row n.
+template <int ELEM>
+__device__ __forceinline__ void kn_store_part(const v4i (&r)[8], uint8_t* lds_b, int tid, int q) {
+    const int nb = tid & 15, kb = tid >> 4;
+    uint32_t lo[4], hi[4];  // word q of each row holds the 4 columns
+    t4x4(r[0][q], r[1][q], r[2][q], r[3][q], lo[0], lo[1], lo[2], lo[3]);
+    t4x4(r[4][q], r[5][q], r[6][q], r[7][q], hi[0], hi[1], hi[2], hi[3]);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int n = nb * 16 + q * 4 + c;
+        uint32_t w0 = lo[c], w1 = hi[c];
+        if constexpr (ELEM == ELEM_F8) {
+            w0 = e4m3_sanitize(w0);
+            w1 = e4m3_sanitize(w1);
+        }
+        const int chunk = (kb >> 1) ^ swz(n);
+        *reinterpret_cast<uint2*>(lds_b + n * BK + chunk * 16 + (kb & 1) * 8) = make_uint2(w0, w1);
+    }
+}
+
 template <int ELEM>
 __device__ __forceinline__ void kn_store(const v4i (&r)[8], uint8_t* lds_b, int tid) {
-    const int nb = tid & 15, kb = tid >> 4;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {  // columns 4q..4q+3 of the block: word q of each row
-        uint32_t lo[4], hi[4];
-        t4x4(r[0][q], r[1][q], r[2][q], r[3][q], lo[0], lo[1], lo[2], lo[3]);
-        t4x4(r[4][q], r[5][q], r[6][q], r[7][q], hi[0], hi[1], hi[2], hi[3]);
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const int n = nb * 16 + q * 4 + c;
-            uint32_t w0 = lo[c], w1 = hi[c];
-            if constexpr (ELEM == ELEM_F8) {
-                w0 = e4m3_sanitize(w0);
-                w1 = e4m3_sanitize(w1);
-            }
-            const int chunk = (kb >> 1) ^ swz(n);
-            *reinterpret_cast<uint2*>(lds_b + n * BK + chunk * 16 + (kb & 1) * 8) = make_uint2(w0, w1);
-        }
-    }
+    for (int q = 0; q < 4; ++q) kn_store_part<ELEM>(r, lds_b, tid, q);
 }
 
 // Per element type: fragment and accumulator types, k steps per stage.
@@ -212,69 +215,63 @@ struct Frags {
     typename Mma<ELEM>::Frag a[4], b[4];
 };
 
-// Issues the LDS reads of the wave's fragments of k step ks.  A rows
-// wm*128 + 32*i + lr and B^T rows wn*128 + 32*j + lr share swz(lr), so each
-// operand needs one address plus immediate offsets.  Nothing here waits for
-// the data: the MFMAs that consume it come one block later.
+// LDS read r of the wave's fragments of k step ks: one ds_read_b128.  INT8:
+// r = 0..3 -> A block r, 4..7 -> B block r-4 (16 k bytes per lane).  FP8:
+// r = 2f + h, f = 0..3 A blocks, 4..7 B blocks, h = which 16 of the lane's
+// 32 k codes.  A rows wm*128 + 32*i + lr and B^T rows wn*128 + 32*j + lr
+// share swz(lr), so every read of a step has one address plus an immediate
+// offset.  Nothing here waits for the data.
 template <int ELEM>
-__device__ __forceinline__ void read_frags(const uint8_t* buf, int ks, int wm, int wn, int lane,
-                                           Frags<ELEM>& f) {
+__device__ __forceinline__ void read_piece(const uint8_t* buf, int ks, int wm, int wn, int lane, Frags<ELEM>& f,
+                                           int r) {
     const int lr = lane & 31, lh = lane >> 5, sw = swz(lr);
     const uint8_t* Ab = buf + (wm * 128 + lr) * BK;
     const uint8_t* Bb = buf + STAGE_A + (wn * 128 + lr) * BK;
     if constexpr (ELEM == ELEM_I8) {
         const int co = ((ks * 2 + lh) ^ sw) << 4;  // this lane's 16-byte chunk of the 32-byte step
-#pragma unroll
-        for (int i = 0; i < 4; ++i) f.a[i] = *reinterpret_cast<const v4i*>(Ab + i * 32 * BK + co);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) f.b[j] = *reinterpret_cast<const v4i*>(Bb + j * 32 * BK + co);
+        if (r < 4) f.a[r] = *reinterpret_cast<const v4i*>(Ab + r * 32 * BK + co);
+        else f.b[r - 4] = *reinterpret_cast<const v4i*>(Bb + (r - 4) * 32 * BK + co);
     } else {
-        // two 16-byte chunks = 32 k codes per lane
-        const int cx = ((ks * 4 + lh * 2) ^ sw) << 4, cy = ((ks * 4 + lh * 2 + 1) ^ sw) << 4;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const v4i x = *reinterpret_cast<const v4i*>(Ab + i * 32 * BK + cx);
-            const v4i y = *reinterpret_cast<const v4i*>(Ab + i * 32 * BK + cy);
-            f.a[i] = v8i{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const v4i x = *reinterpret_cast<const v4i*>(Bb + j * 32 * BK + cx);
-            const v4i y = *reinterpret_cast<const v4i*>(Bb + j * 32 * BK + cy);
-            f.b[j] = v8i{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+        const int fi = r >> 1, h = r & 1;
+        const int co = ((ks * 4 + lh * 2 + h) ^ sw) << 4;
+        v8i& d = fi < 4 ? f.a[fi] : f.b[fi - 4];
+        const v4i x = *reinterpret_cast<const v4i*>((fi < 4 ? Ab + fi * 32 * BK : Bb + (fi - 4) * 32 * BK) + co);
+        if (h == 0) {
+            d[0] = x[0]; d[1] = x[1]; d[2] = x[2]; d[3] = x[3];
+        } else {
+            d[4] = x[0]; d[5] = x[1]; d[6] = x[2]; d[7] = x[3];
         }
     }
 }
 
-// FP8 operands staged by DMA cannot be rewritten on the way in; their
-// 0x7F/0xFF codes are cleared in the fragment registers, just before use.
+// Clears the 0x7F/0xFF codes of an FP8 fragment (DMA-staged operands cannot
+// be rewritten on the way into LDS).
 __device__ __forceinline__ v8i sanitize8(v8i x) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) x[i] = static_cast<int>(e4m3_sanitize(static_cast<uint32_t>(x[i])));
     return x;
 }
 
-// The 16 MFMAs of one k step of the wave's 128x128 block.
+// FP8: clear the 0x7F/0xFF codes of the operands not cleared at staging
+// (A always; B when it was copied by DMA).
 template <int ELEM, int BL>
-__device__ __forceinline__ void mfma_step(const Frags<ELEM>& f, typename Mma<ELEM>::AccT (&acc)[4][4]) {
-    if constexpr (ELEM == ELEM_I8) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
-    } else {
-        v8i b[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) b[j] = BL == FKE_B_NK ? sanitize8(f.b[j]) : f.b[j];  // KN: sanitized at staging
+__device__ __forceinline__ void sanitize_frags(Frags<ELEM>& f) {
+    if constexpr (ELEM == ELEM_F8) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const v8i a = sanitize8(f.a[i]);
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b[j], acc[i][j], 0, 0, 0, 0, 0, 0);
+            f.a[i] = sanitize8(f.a[i]);
+            if constexpr (BL == FKE_B_NK) f.b[i] = sanitize8(f.b[i]);
         }
     }
+}
+
+// MFMA (i, j) of one k step of the wave's 128x128 block.
+template <int ELEM>
+__device__ __forceinline__ void mfma_one(const Frags<ELEM>& f, typename Mma<ELEM>::AccT (&acc)[4][4], int i, int j) {
+    if constexpr (ELEM == ELEM_I8)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
+    else
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.a[i], f.b[j], acc[i][j], 0, 0, 0, 0, 0, 0);
 }
 
 template <int ELEM, int BL, int OUT>
@@ -285,6 +282,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
     __shared__ __attribute__((aligned(16))) float epi_sa[BM];    // scale of each tile row
     __shared__ __attribute__((aligned(16))) float epi_sb[BN];    // scale of each tile column
     __shared__ __attribute__((aligned(16))) float epi_bias[BN];  // bias of each tile column
+    __shared__ int redo;                                          // FP8: rerun with NaN codes cleared
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -307,6 +305,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
         epi_sa[tid] = p.scale_a ? p.scale_a[m] : p.sa;
         epi_sb[tid] = p.scale_b ? p.scale_b[n] : p.sb;
         epi_bias[tid] = p.bias ? p.bias[n] : -0.0f;
+        if (tid == 0) redo = 0;
     }
 
     typename Mma<ELEM>::AccT acc[4][4];
@@ -331,7 +330,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
     // stage to land), slots 1..PW copy A; kn_commit() transposes the block
     // into LDS before the barrier.
     constexpr int NSLOT = BL == FKE_B_NK ? 2 * PW : PW + 1;
-    auto copy = [&](int q, int kt, uint8_t* b) {
+    auto copy = [&](int q, int kt, uint8_t* b) __attribute__((always_inline)) {
         if constexpr (BL == FKE_B_NK) {
             if (q < PW) pa.issue(q, kt * BK, b, wave);
             else pb.issue(q - PW, kt * BK, b + STAGE_A, wave);
@@ -340,60 +339,65 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
             else pa.issue(q - 1, kt * BK, b, wave);
         }
     };
-    auto kn_commit = [&](uint8_t* b) {
+    auto kn_commit = [&](uint8_t* b) __attribute__((always_inline)) {
         if constexpr (BL == FKE_B_KN) kn_store<ELEM>(knr, b + STAGE_A, tid);
     };
     // A stage is NKS groups of 16 MFMAs.  Group g runs the MFMAs of one
     // fragment set (g = 0: the previous stage's last step, carried across
     // the barrier; g > 0: step g-1) while the LDS reads of step g fill the
-    // other set, and carries copy slots of the next stage: slots are spread
+    // other set, and carries copy slots of the next stage: INT8 spreads them
     // over all groups but the last, which instead takes the [K,N] transpose.
-    // Within a group every memory instruction is paired with an MFMA
-    // (sched_group_barrier), so it issues in the MFMA's shadow instead of
-    // stalling the matrix pipe.
+    // Within a group every memory instruction is paired with an MFMA, so it
+    // issues in the MFMA's shadow instead of stalling the matrix pipe.
     constexpr int PER_GROUP = (NSLOT + NKS - 2) / (NKS - 1);
     Frags<ELEM> f0, f1;
     constexpr int NREAD = ELEM == ELEM_I8 ? 8 : 16;  // ds_read_b128 per step
-    auto group = [&](auto q0c, auto q1c, auto commitc, const Frags<ELEM>& use, Frags<ELEM>& fill,
-                     const uint8_t* cur, int rks, uint8_t* nxt, int kc) {
+    auto group = [&](auto sanc, auto q0c, auto q1c, auto commitc, Frags<ELEM>& use, Frags<ELEM>& fill,
+                     const uint8_t* cur, int rks, uint8_t* nxt, int kc) __attribute__((always_inline)) {
+        constexpr bool SAN = decltype(sanc)::value;
         constexpr int Q0 = decltype(q0c)::value, Q1 = decltype(q1c)::value;
         constexpr bool COMMIT = decltype(commitc)::value;
-        // vector-memory instructions of slots [Q0, Q1): the [K,N] register load is 8
-        constexpr int NV = (Q1 - Q0) + (BL == FKE_B_KN && Q0 == 0 && Q1 > 0 ? 7 : 0);
-        static_assert(NV <= 16, "at most one vector-memory instruction per MFMA");
+        constexpr int NQ = Q1 - Q0;
+        static_assert(NQ <= 16, "at most one copy slot per MFMA");
         fence();
-        mfma_step<ELEM, BL>(use, acc);
-        read_frags<ELEM>(cur, rks, wm, wn, lane, fill);
+        if constexpr (SAN) sanitize_frags<ELEM, BL>(use);
+        // Piece t: MFMA (t/4, t%4), then read t of the next step, then copy
+        // slot Q0 + t - (16 - NQ) in the second half, then a quarter of the
+        // [K,N] transpose at t = 8, 10, 12, 14.  Each piece is fenced, so
+        // this is the issue order.
 #pragma unroll
-        for (int q = Q0; q < Q1; ++q) copy(q, kc, nxt);
-        if constexpr (COMMIT) kn_commit(nxt);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);      // MFMA
-            if (i < NREAD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-            if (i >= 16 - NV) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
-            if (COMMIT && i >= 8) __builtin_amdgcn_sched_group_barrier(0x200, 4, 0);  // DS write
+        for (int t = 0; t < 16; ++t) {
+            fence();
+            mfma_one<ELEM>(use, acc, t >> 2, t & 3);
+            if (t < NREAD) read_piece<ELEM>(cur, rks, wm, wn, lane, fill, t);
+            if (t >= 16 - NQ) copy(Q0 + t - (16 - NQ), kc, nxt);
+            if constexpr (COMMIT && BL == FKE_B_KN) {
+                if (t >= 8 && (t & 1) == 0) kn_store_part<ELEM>(knr, nxt + STAGE_A, tid, (t - 8) >> 1);
+            }
         }
         fence();
     };
     using I0 = std::integral_constant<int, 0>;
     using F = std::false_type;
-    auto stage = [&](const uint8_t* cur, uint8_t* nxt, int kt) {
+    auto stage = [&](auto sanc, const uint8_t* cur, uint8_t* nxt, int kt) __attribute__((always_inline)) {
         const int kc = min(kt + 1, KT - 1);  // the last stage re-copies itself
         constexpr bool KN = BL == FKE_B_KN;
+        using S = decltype(sanc);
         if constexpr (NKS == 4) {
-            constexpr int P = PER_GROUP;
-            group(I0{}, std::integral_constant<int, P>{}, F{}, f1, f0, cur, 0, nxt, kc);
-            group(std::integral_constant<int, P>{}, std::integral_constant<int, (2 * P < NSLOT ? 2 * P : NSLOT)>{}, F{},
-                  f0, f1, cur, 1, nxt, kc);
-            group(std::integral_constant<int, (2 * P < NSLOT ? 2 * P : NSLOT)>{}, std::integral_constant<int, NSLOT>{}, F{},
-                  f1, f0, cur, 2, nxt, kc);
-            group(std::integral_constant<int, NSLOT>{}, std::integral_constant<int, NSLOT>{},
+            constexpr int P = PER_GROUP, P2 = 2 * P < NSLOT ? 2 * P : NSLOT;
+            group(S{}, I0{}, std::integral_constant<int, P>{}, F{}, f1, f0, cur, 0, nxt, kc);
+            group(S{}, std::integral_constant<int, P>{}, std::integral_constant<int, P2>{}, F{}, f0, f1, cur, 1, nxt, kc);
+            group(S{}, std::integral_constant<int, P2>{}, std::integral_constant<int, NSLOT>{}, F{}, f1, f0, cur, 2, nxt,
+                  kc);
+            group(S{}, std::integral_constant<int, NSLOT>{}, std::integral_constant<int, NSLOT>{},
                   std::integral_constant<bool, KN>{}, f0, f1, cur, 3, nxt, kc);
         } else {
             static_assert(NKS == 2, "k steps per stage");
-            group(I0{}, std::integral_constant<int, NSLOT>{}, F{}, f1, f0, cur, 0, nxt, kc);
-            group(std::integral_constant<int, NSLOT>{}, std::integral_constant<int, NSLOT>{},
+            // FP8 steps are twice as long: the second group still leaves the
+            // copies it carries a full group of MFMAs to land.
+            constexpr int P = (NSLOT + 1) / 2;
+            group(S{}, I0{}, std::integral_constant<int, P>{}, F{}, f1, f0, cur, 0, nxt, kc);
+            group(S{}, std::integral_constant<int, P>{}, std::integral_constant<int, NSLOT>{},
                   std::integral_constant<bool, KN>{}, f0, f1, cur, 1, nxt, kc);
         }
         wait_lgkm0();  // last step's fragments in registers (f1): cur may be overwritten after the barrier
@@ -401,30 +405,67 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
         barrier();
     };
 
-    // Prologue: stage 0 -> lds0; f1 (the carried set) starts at zero.
+    // The whole K loop.  Buffer roles are static (lds0 / lds1 are distinct
+    // objects, so the compiler sees that a stage's DMA never aliases the
+    // other stage's reads), hence two stages per iteration; the body has no
+    // data-dependent branches, so the accumulators stay in AGPRs.
+    auto k_loop = [&](auto sanc) __attribute__((always_inline)) {
+        using S = decltype(sanc);
+        // Prologue: stage 0 -> lds0; f1 (the carried set) starts at zero.
 #pragma unroll
-    for (int q = 0; q < NSLOT; ++q) copy(q, 0, lds0);
-    kn_commit(lds0);
-    wait_lgkm0();
-    wait_vm0();
-    barrier();
+        for (int q = 0; q < NSLOT; ++q) copy(q, 0, lds0);
+        kn_commit(lds0);
+        wait_lgkm0();
+        wait_vm0();
+        barrier();
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        f1.a[i] = typename Mma<ELEM>::Frag{};
-        f1.b[i] = typename Mma<ELEM>::Frag{};
-    }
+        for (int i = 0; i < 4; ++i) {
+            f1.a[i] = typename Mma<ELEM>::Frag{};
+            f1.b[i] = typename Mma<ELEM>::Frag{};
+        }
+        int kt = 0;
+        for (; kt + 2 <= KT; kt += 2) {
+            stage(S{}, lds0, lds1, kt);
+            stage(S{}, lds1, lds0, kt + 1);
+        }
+        if (kt < KT) stage(S{}, lds0, lds1, kt);  // odd stage count
+        // the last stage's carried step
+        if constexpr (S::value) sanitize_frags<ELEM, BL>(f1);
+#pragma unroll
+        for (int t = 0; t < 16; ++t) mfma_one<ELEM>(f1, acc, t >> 2, t & 3);
+    };
 
-    // Buffer roles are static (lds0 / lds1 are distinct objects, so the
-    // compiler sees that a stage's DMA never aliases the other stage's
-    // reads), hence two stages per iteration; the body has no data-dependent
-    // branches, so the accumulators stay in AGPRs.
-    int kt = 0;
-    for (; kt + 2 <= KT; kt += 2) {
-        stage(lds0, lds1, kt);
-        stage(lds1, lds0, kt + 1);
+    if constexpr (ELEM == ELEM_I8) {
+        k_loop(F{});
+    } else {
+        // E4M3 0x7F/0xFF are NaN to the MFMA but 0.0 to the reference.
+        // Clearing them costs ~5 VALU per operand word, more than the MFMAs
+        // can hide, and real quantizers never emit them (they saturate at
+        // 448).  So run the K loop on the raw codes first: every product is
+        // finite and no sum can overflow, so a NaN accumulator proves a
+        // NaN code in the tile's rows or columns.  Only then does the
+        // workgroup run the loop again with the codes cleared.
+        k_loop(F{});
+        float t = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) t += acc[i][j][v];
+        if (__builtin_isnan(t)) redo = 1;  // benign race: every writer stores 1
+        wait_lgkm0();
+        barrier();
+        if (redo) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
+            k_loop(std::true_type{});
+        }
     }
-    if (kt < KT) stage(lds0, lds1, kt);  // odd stage count
-    mfma_step<ELEM, BL>(f1, acc);         // the last stage's carried step
 
     // Fused epilogue.  32x32 block layout of the accumulator: lane l holds
     // column l%32 and rows 8*(v/4) + 4*(l/32) + v%4 for v = 0..15.
