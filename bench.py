@@ -222,6 +222,16 @@ def extra_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
     res["prefill_4096x11008x4096_bf16"] = {"ms": round(ms, 4), "TOPS": round(t, 1),
                                            "frac": round(t / PEAK_INT8_TOPS, 4)}
     del A, B, C
+    # INT8 8192^3 with B [K,N] (the layout of the reference's Python op), fp32 out
+    M = N = K = 8192
+    A, B, sa, sb = rand_i8(M, K), rand_i8(K, N), rand_u(M), rand_u(N)
+    C = torch.empty((M, N), dtype=torch.float32, device=dev)
+    ms = timed(lambda: L.fke_qgemm_i8(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, sa.data_ptr(),
+                                      sb.data_ptr(), 1.0, 1.0, None, _lib.OUT_F32, _lib.B_KN, sh),
+               args.steps, args.warmup)
+    t = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+    res["int8_8192cubed_f32_Bkn"] = {"ms": round(ms, 4), "TOPS": round(t, 1), "frac": round(t / PEAK_INT8_TOPS, 4)}
+    del A, B, C
     # config 4: FP8 e4m3 8192^3, B [K,N] (reference layout) and [N,K], bf16 out
     M = N = K = 8192
     A8 = torch.randint(0, 256, (M, K), dtype=torch.uint8, device=dev, generator=gen)
@@ -235,6 +245,14 @@ def extra_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
         t = 2.0 * M * N * K / (ms * 1e-3) / 1e12
         res[f"fp8_8192cubed_bf16_B{name}"] = {"ms": round(ms, 4), "TFLOPS": round(t, 1),
                                               "frac": round(t / PEAK_FP8_TFLOPS, 4)}
+    # the same with 1 in 97 codes of A set to 0x7F: tiles rerun with NaN codes cleared
+    A8.view(-1)[::97] = 0x7F
+    C = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    ms = timed(lambda: L.fke_qgemm_f8(A8.data_ptr(), B8.data_ptr(), C.data_ptr(), M, N, K, 0.01, 0.01,
+                                      None, _lib.OUT_BF16, _lib.B_NK, sh), args.steps, args.warmup)
+    t = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+    res["fp8_8192cubed_bf16_Bnk_nan_codes"] = {"ms": round(ms, 4), "TFLOPS": round(t, 1),
+                                               "frac": round(t / PEAK_FP8_TFLOPS, 4)}
     del A8, B8, C
     for m in (4, 16):
         res[f"gemv_M{m}"] = gemv_bench(torch, L, _lib, dev, gen, m, args.gemv_buffers, args.gemv_launches)

@@ -136,62 +136,56 @@ struct Panel {
     }
 };
 
-// B stored [K,N]: each thread owns an 8(k) x 16(n) byte block of the 128 x 256
-// stage tile (thread t: n block t%16, k block t/16), loaded as eight 16-byte
-// rows so that 16 lanes read 256 contiguous bytes of one k row.
-struct KNPlan {
-    const int8_t* base;  // B + n (column block start, clamped) at k = 8*(t/16)
-    int N;
-    __device__ void init(const int8_t* B, int N_, int n0, int tid) {
-        N = N_;
-        const int n = min(n0 + (tid & 15) * 16, N_ - 16);  // ragged N: re-read the last block
-        base = B + n + static_cast<size_t>(tid >> 4) * 8 * N_;
-    }
-    __device__ __forceinline__ void load(int k0, v4i (&r)[8]) const {
-        const int8_t* q = base + static_cast<size_t>(k0) * N;
+// B stored [K,N]: a stage is 128 k rows of 256 n bytes, copied as they lie
+// in memory, four rows per 1-KiB load; 16-byte chunk c of row k is stored at
+// chunk c ^ (k & 15).  The MFMA fragments (one column n per lane, k bytes
+// consecutive) are then read with ds_read_b64_tr_b8, which transposes 8x8
+// byte blocks across lanes.  Columns past N read whatever follows them in
+// memory (those outputs are never stored); reads past the end of B fall out
+// of the buffer's range and return 0.
+struct KNPanel {
+    __amdgpu_buffer_rsrc_t rsrc;  // all of B, K x N bytes
+    uint32_t off[PW];             // byte offset of this lane's 16-byte source at stage 0
+    int stage_bytes;              // BK rows of B
+    __device__ void init(const int8_t* B, int N, int K, int n0, int wave, int lane) {
+        rsrc = make_rsrc(B, K * N);
+        stage_bytes = BK * N;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) r[i] = *reinterpret_cast<const v4i*>(q + static_cast<size_t>(i) * N);
+        for (int i = 0; i < PW; ++i) {
+            const int r = (wave * PW + i) * 4 + (lane >> 4);  // k row within the stage
+            const int c = (lane & 15) ^ (r & 15);             // logical chunk landing at physical lane & 15
+            off[i] = static_cast<uint32_t>(r * N + n0 + c * 16);
+        }
+    }
+    __device__ __forceinline__ void issue(int i, int kt, uint8_t* lds, int wave) const {
+        dma16(rsrc, off[i], kt * stage_bytes, lds + (wave * PW + i) * 1024);
     }
 };
 
-// 4x4 byte transpose of (x0..x3) rows -> columns with v_perm_b32.
-__device__ __forceinline__ void t4x4(uint32_t x0, uint32_t x1, uint32_t x2, uint32_t x3,
-                                     uint32_t& y0, uint32_t& y1, uint32_t& y2, uint32_t& y3) {
-    const uint32_t t0 = __builtin_amdgcn_perm(x1, x0, 0x05010400u);  // a0 b0 a1 b1
-    const uint32_t t1 = __builtin_amdgcn_perm(x1, x0, 0x07030602u);  // a2 b2 a3 b3
-    const uint32_t t2 = __builtin_amdgcn_perm(x3, x2, 0x05010400u);  // c0 d0 c1 d1
-    const uint32_t t3 = __builtin_amdgcn_perm(x3, x2, 0x07030602u);  // c2 d2 c3 d3
-    y0 = __builtin_amdgcn_perm(t2, t0, 0x05040100u);                 // a0 b0 c0 d0
-    y1 = __builtin_amdgcn_perm(t2, t0, 0x07060302u);                 // a1 b1 c1 d1
-    y2 = __builtin_amdgcn_perm(t3, t1, 0x05040100u);                 // a2 b2 c2 d2
-    y3 = __builtin_amdgcn_perm(t3, t1, 0x07060302u);                 // a3 b3 c3 d3
+// ds_read_b64_tr_b8 (gfx950): within each 16-lane group, lane 8h+i receives
+// byte i of the 8 bytes addressed by lanes 2b+h, b = 0..7, as its byte b.
+typedef int v2i __attribute__((ext_vector_type(2)));
+// The address-space cast keeps the pointer's provenance (lds0 or lds1), so
+// the compiler can tell these reads from the DMA writes into the other stage.
+__device__ __forceinline__ v2i ds_read_tr8(const uint8_t* p) {
+    typedef v2i __attribute__((address_space(3))) * lptr;
+    return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lptr)(p));
 }
 
-// Transpose columns 4q..4q+3 of the thread's 8(k) x 16(n) block and store,
-// for each such column n, the 8 bytes k = 8*kb..+8 of B^T row n.
+// Per-lane offsets (within a stage's B region) of the transposed reads of
+// B block j, k rows 8*rr..8*rr+7 of the lane's half of the first step.
+// Lane l = 16G + s reads row HS*(G>>1) + 8*rr + s/2 at column block
+// wn*128 + 32j + 16*(G&1) + 8*(s&1), so that after the transpose lane l
+// holds column wn*128 + 32j + l%32 with its k bytes in order.  Rows a
+// multiple of 16 apart share the chunk swizzle, so other steps (and, for
+// FP8, k rows 16..31 of the half) are immediate offsets away.
 template <int ELEM>
-__device__ __forceinline__ void kn_store_part(const v4i (&r)[8], uint8_t* lds_b, int tid, int q) {
-    const int nb = tid & 15, kb = tid >> 4;
-    uint32_t lo[4], hi[4];  // word q of each row holds the 4 columns
-    t4x4(r[0][q], r[1][q], r[2][q], r[3][q], lo[0], lo[1], lo[2], lo[3]);
-    t4x4(r[4][q], r[5][q], r[6][q], r[7][q], hi[0], hi[1], hi[2], hi[3]);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const int n = nb * 16 + q * 4 + c;
-        uint32_t w0 = lo[c], w1 = hi[c];
-        if constexpr (ELEM == ELEM_F8) {
-            w0 = e4m3_sanitize(w0);
-            w1 = e4m3_sanitize(w1);
-        }
-        const int chunk = (kb >> 1) ^ swz(n);
-        *reinterpret_cast<uint2*>(lds_b + n * BK + chunk * 16 + (kb & 1) * 8) = make_uint2(w0, w1);
-    }
-}
-
-template <int ELEM>
-__device__ __forceinline__ void kn_store(const v4i (&r)[8], uint8_t* lds_b, int tid) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) kn_store_part<ELEM>(r, lds_b, tid, q);
+__device__ __forceinline__ uint32_t kn_read_off(int lane, int wn, int j, int rr) {
+    constexpr int HS = ELEM == ELEM_I8 ? 16 : 32;  // k bytes of one lane-half per step
+    const int G = lane >> 4, sl = lane & 15, b = sl >> 1;
+    const int row = HS * (G >> 1) + 8 * rr + b;
+    const int chunk = (wn * 8 + 2 * j + (G & 1)) ^ (row & 15);
+    return static_cast<uint32_t>(row * 256 + chunk * 16 + 8 * (sl & 1));
 }
 
 // Per element type: fragment and accumulator types, k steps per stage.
@@ -215,18 +209,36 @@ struct Frags {
     typename Mma<ELEM>::Frag a[4], b[4];
 };
 
-// LDS read r of the wave's fragments of k step ks: one ds_read_b128.  INT8:
-// r = 0..3 -> A block r, 4..7 -> B block r-4 (16 k bytes per lane).  FP8:
-// r = 2f + h, f = 0..3 A blocks, 4..7 B blocks, h = which 16 of the lane's
-// 32 k codes.  A rows wm*128 + 32*i + lr and B^T rows wn*128 + 32*j + lr
-// share swz(lr), so every read of a step has one address plus an immediate
-// offset.  Nothing here waits for the data.
-template <int ELEM>
-__device__ __forceinline__ void read_piece(const uint8_t* buf, int ks, int wm, int wn, int lane, Frags<ELEM>& f,
-                                           int r) {
+// LDS reads of the wave's fragments of k step ks; read_piece issues read r
+// (one instruction, nothing waits for the data).
+//   A, and B in [N,K] order: ds_read_b128 of 16 k bytes.  INT8: r = 0..3 A
+//   block r, 4..7 B block r-4.  FP8: r = 2f + h, f = 0..3 A, 4..7 B, h =
+//   which 16 of the lane's 32 codes.  Rows wm*128 + 32*i + lr (A) and
+//   wn*128 + 32*j + lr (B^T) share swz(lr): one address plus immediates.
+//   B in [K,N] order: ds_read_b64_tr_b8 of 8 k bytes.  INT8: r = 4 + 2j + rr;
+//   FP8: r = 8 + 4j + rr, rr = which 8 of the lane's k bytes.
+template <int ELEM, int BL>
+struct Reads {
+    static constexpr int A = ELEM == ELEM_I8 ? 4 : 8;
+    static constexpr int N = BL == FKE_B_NK ? 2 * A : 3 * A;
+};
+
+template <int ELEM, int BL>
+__device__ __forceinline__ void read_piece(const uint8_t* buf, int ks, int wm, int wn, int lane,
+                                           const uint32_t (&kn_off)[4][2], Frags<ELEM>& f, int r) {
     const int lr = lane & 31, lh = lane >> 5, sw = swz(lr);
     const uint8_t* Ab = buf + (wm * 128 + lr) * BK;
     const uint8_t* Bb = buf + STAGE_A + (wn * 128 + lr) * BK;
+    constexpr int RA = Reads<ELEM, BL>::A;
+    if (BL == FKE_B_KN && r >= RA) {
+        constexpr int KSTEP = ELEM == ELEM_I8 ? 32 : 64;  // k rows per step
+        const int p = r - RA;
+        const int j = ELEM == ELEM_I8 ? p >> 1 : p >> 2, rr = ELEM == ELEM_I8 ? p & 1 : p & 3;
+        const v2i x = ds_read_tr8(buf + STAGE_A + kn_off[j][rr & 1] + (ks * KSTEP + (rr >> 1) * 16) * 256);
+        f.b[j][2 * rr] = x[0];
+        f.b[j][2 * rr + 1] = x[1];
+        return;
+    }
     if constexpr (ELEM == ELEM_I8) {
         const int co = ((ks * 2 + lh) ^ sw) << 4;  // this lane's 16-byte chunk of the 32-byte step
         if (r < 4) f.a[r] = *reinterpret_cast<const v4i*>(Ab + r * 32 * BK + co);
@@ -252,15 +264,14 @@ __device__ __forceinline__ v8i sanitize8(v8i x) {
     return x;
 }
 
-// FP8: clear the 0x7F/0xFF codes of the operands not cleared at staging
-// (A always; B when it was copied by DMA).
-template <int ELEM, int BL>
+// FP8: clear the 0x7F/0xFF codes of a fragment set.
+template <int ELEM>
 __device__ __forceinline__ void sanitize_frags(Frags<ELEM>& f) {
     if constexpr (ELEM == ELEM_F8) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             f.a[i] = sanitize8(f.a[i]);
-            if constexpr (BL == FKE_B_NK) f.b[i] = sanitize8(f.b[i]);
+            f.b[i] = sanitize8(f.b[i]);
         }
     }
 }
@@ -317,63 +328,57 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
 
     const int KT = K / BK;
-    Panel pa, pb;
+    Panel pa;
     pa.init(A, K, m0, M, wave, lane);
-    KNPlan kp;
-    if constexpr (BL == FKE_B_NK) pb.init(B, K, n0, N, wave, lane);
-    else kp.init(B, N, n0, tid);
-    v4i knr[8];
+    using BPanel = typename std::conditional<BL == FKE_B_NK, Panel, KNPanel>::type;
+    BPanel pb;
+    uint32_t kn_off[4][2] = {};
+    if constexpr (BL == FKE_B_NK) {
+        pb.init(B, K, n0, N, wave, lane);
+    } else {
+        pb.init(B, N, K, n0, wave, lane);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int rr = 0; rr < 2; ++rr) kn_off[j][rr] = kn_read_off<ELEM>(lane, wn, j, rr);
+    }
 
-    // Copy of stage kt into buffer b, slot q of NSLOT.  [N,K]: slots 0..PW-1
-    // copy A, PW..2PW-1 copy B, all by DMA.  [K,N]: slot 0 loads this
-    // thread's B block into registers (first, so the loads have the whole
-    // stage to land), slots 1..PW copy A; kn_commit() transposes the block
-    // into LDS before the barrier.
-    constexpr int NSLOT = BL == FKE_B_NK ? 2 * PW : PW + 1;
+    // Copy of stage kt into buffer b, slot q of NSLOT: slots 0..PW-1 copy
+    // A, PW..2PW-1 copy B, all buffer -> LDS.
+    constexpr int NSLOT = 2 * PW;
     auto copy = [&](int q, int kt, uint8_t* b) __attribute__((always_inline)) {
-        if constexpr (BL == FKE_B_NK) {
-            if (q < PW) pa.issue(q, kt * BK, b, wave);
-            else pb.issue(q - PW, kt * BK, b + STAGE_A, wave);
-        } else {
-            if (q == 0) kp.load(kt * BK, knr);
-            else pa.issue(q - 1, kt * BK, b, wave);
-        }
-    };
-    auto kn_commit = [&](uint8_t* b) __attribute__((always_inline)) {
-        if constexpr (BL == FKE_B_KN) kn_store<ELEM>(knr, b + STAGE_A, tid);
+        if (q < PW) pa.issue(q, kt * BK, b, wave);
+        else if constexpr (BL == FKE_B_NK) pb.issue(q - PW, kt * BK, b + STAGE_A, wave);
+        else pb.issue(q - PW, kt, b + STAGE_A, wave);
     };
     // A stage is NKS groups of 16 MFMAs.  Group g runs the MFMAs of one
     // fragment set (g = 0: the previous stage's last step, carried across
     // the barrier; g > 0: step g-1) while the LDS reads of step g fill the
-    // other set, and carries copy slots of the next stage: INT8 spreads them
-    // over all groups but the last, which instead takes the [K,N] transpose.
-    // Within a group every memory instruction is paired with an MFMA, so it
-    // issues in the MFMA's shadow instead of stalling the matrix pipe.
+    // other set, and carries copy slots of the next stage (INT8: spread over
+    // all groups but the last).  Within a group every memory instruction is
+    // paired with an MFMA, so it issues in the MFMA's shadow instead of
+    // stalling the matrix pipe.
     constexpr int PER_GROUP = (NSLOT + NKS - 2) / (NKS - 1);
     Frags<ELEM> f0, f1;
-    constexpr int NREAD = ELEM == ELEM_I8 ? 8 : 16;  // ds_read_b128 per step
-    auto group = [&](auto sanc, auto q0c, auto q1c, auto commitc, Frags<ELEM>& use, Frags<ELEM>& fill,
-                     const uint8_t* cur, int rks, uint8_t* nxt, int kc) __attribute__((always_inline)) {
+    constexpr int NREAD = Reads<ELEM, BL>::N;  // LDS reads per step
+    auto group = [&](auto sanc, auto q0c, auto q1c, Frags<ELEM>& use, Frags<ELEM>& fill, const uint8_t* cur,
+                     int rks, uint8_t* nxt, int kc) __attribute__((always_inline)) {
         constexpr bool SAN = decltype(sanc)::value;
         constexpr int Q0 = decltype(q0c)::value, Q1 = decltype(q1c)::value;
-        constexpr bool COMMIT = decltype(commitc)::value;
         constexpr int NQ = Q1 - Q0;
         static_assert(NQ <= 16, "at most one copy slot per MFMA");
         fence();
-        if constexpr (SAN) sanitize_frags<ELEM, BL>(use);
-        // Piece t: MFMA (t/4, t%4), then read t of the next step, then copy
-        // slot Q0 + t - (16 - NQ) in the second half, then a quarter of the
-        // [K,N] transpose at t = 8, 10, 12, 14.  Each piece is fenced, so
-        // this is the issue order.
+        if constexpr (SAN) sanitize_frags<ELEM>(use);
+        // Piece t: MFMA (t/4, t%4), then the reads r = t (mod 16) of the
+        // next step, then copy slot Q0 + t - (16 - NQ) in the second half.
+        // Each piece is fenced, so this is the issue order.
 #pragma unroll
         for (int t = 0; t < 16; ++t) {
             fence();
             mfma_one<ELEM>(use, acc, t >> 2, t & 3);
-            if (t < NREAD) read_piece<ELEM>(cur, rks, wm, wn, lane, fill, t);
+#pragma unroll
+            for (int r = t; r < NREAD; r += 16) read_piece<ELEM, BL>(cur, rks, wm, wn, lane, kn_off, fill, r);
             if (t >= 16 - NQ) copy(Q0 + t - (16 - NQ), kc, nxt);
-            if constexpr (COMMIT && BL == FKE_B_KN) {
-                if (t >= 8 && (t & 1) == 0) kn_store_part<ELEM>(knr, nxt + STAGE_A, tid, (t - 8) >> 1);
-            }
         }
         fence();
     };
@@ -381,24 +386,21 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
     using F = std::false_type;
     auto stage = [&](auto sanc, const uint8_t* cur, uint8_t* nxt, int kt) __attribute__((always_inline)) {
         const int kc = min(kt + 1, KT - 1);  // the last stage re-copies itself
-        constexpr bool KN = BL == FKE_B_KN;
         using S = decltype(sanc);
         if constexpr (NKS == 4) {
             constexpr int P = PER_GROUP, P2 = 2 * P < NSLOT ? 2 * P : NSLOT;
-            group(S{}, I0{}, std::integral_constant<int, P>{}, F{}, f1, f0, cur, 0, nxt, kc);
-            group(S{}, std::integral_constant<int, P>{}, std::integral_constant<int, P2>{}, F{}, f0, f1, cur, 1, nxt, kc);
-            group(S{}, std::integral_constant<int, P2>{}, std::integral_constant<int, NSLOT>{}, F{}, f1, f0, cur, 2, nxt,
+            group(S{}, I0{}, std::integral_constant<int, P>{}, f1, f0, cur, 0, nxt, kc);
+            group(S{}, std::integral_constant<int, P>{}, std::integral_constant<int, P2>{}, f0, f1, cur, 1, nxt, kc);
+            group(S{}, std::integral_constant<int, P2>{}, std::integral_constant<int, NSLOT>{}, f1, f0, cur, 2, nxt, kc);
+            group(S{}, std::integral_constant<int, NSLOT>{}, std::integral_constant<int, NSLOT>{}, f0, f1, cur, 3, nxt,
                   kc);
-            group(S{}, std::integral_constant<int, NSLOT>{}, std::integral_constant<int, NSLOT>{},
-                  std::integral_constant<bool, KN>{}, f0, f1, cur, 3, nxt, kc);
         } else {
             static_assert(NKS == 2, "k steps per stage");
             // FP8 steps are twice as long: the second group still leaves the
             // copies it carries a full group of MFMAs to land.
-            constexpr int P = (NSLOT + 1) / 2;
-            group(S{}, I0{}, std::integral_constant<int, P>{}, F{}, f1, f0, cur, 0, nxt, kc);
-            group(S{}, std::integral_constant<int, P>{}, std::integral_constant<int, NSLOT>{},
-                  std::integral_constant<bool, KN>{}, f0, f1, cur, 1, nxt, kc);
+            constexpr int P = NSLOT / 2;
+            group(S{}, I0{}, std::integral_constant<int, P>{}, f1, f0, cur, 0, nxt, kc);
+            group(S{}, std::integral_constant<int, P>{}, std::integral_constant<int, NSLOT>{}, f0, f1, cur, 1, nxt, kc);
         }
         wait_lgkm0();  // last step's fragments in registers (f1): cur may be overwritten after the barrier
         wait_vm0();    // this wave's share of stage kt+1 has landed
@@ -414,7 +416,6 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
         // Prologue: stage 0 -> lds0; f1 (the carried set) starts at zero.
 #pragma unroll
         for (int q = 0; q < NSLOT; ++q) copy(q, 0, lds0);
-        kn_commit(lds0);
         wait_lgkm0();
         wait_vm0();
         barrier();
@@ -430,7 +431,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
         }
         if (kt < KT) stage(S{}, lds0, lds1, kt);  // odd stage count
         // the last stage's carried step
-        if constexpr (S::value) sanitize_frags<ELEM, BL>(f1);
+        if constexpr (S::value) sanitize_frags<ELEM>(f1);
 #pragma unroll
         for (int t = 0; t < 16; ++t) mfma_one<ELEM>(f1, acc, t >> 2, t & 3);
     };
@@ -552,7 +553,7 @@ bool mfma_supports(const GemmArgs& p, int elem) {
     if ((a | b) & 15) return false;
     // per-lane DMA offsets are 32-bit: (rows - 1) * K + K must fit
     if (static_cast<int64_t>(p.M) * p.K > INT32_MAX) return false;
-    if (p.b_layout == FKE_B_NK && static_cast<int64_t>(p.N) * p.K > INT32_MAX) return false;
+    if (static_cast<int64_t>(p.N) * p.K > INT32_MAX) return false;
     if (p.b_layout == FKE_B_KN && (p.N % 16 != 0)) return false;
     // epilogue offsets are 32-bit: 256 output rows plus the 2^31 drop offset
     if (p.N > (1 << 20)) return false;
