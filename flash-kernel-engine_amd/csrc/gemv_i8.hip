@@ -7,14 +7,16 @@
 //
 // Two kernels:
 //  * gemv_rows_kernel (M == 1; instantiable up to 4 rows): one B row per wave
-//    over the full K.  Lane l
-//    reads 16-byte chunks l, l+64, l+128, l+192 of each 256-chunk block (one
-//    wave load = 1 KiB contiguous), keeps the M activation chunks in registers,
+//    over the full K.  Lane l reads 16-byte chunks l, l+64, l+128, l+192 of
+//    each 256-chunk block (one wave load = 1 KiB contiguous) with non-temporal
+//    buffer loads, keeps the M activation chunks in registers,
 //    and reduces its partial sums with DPP row rotations, one ds_swizzle and two
 //    readlanes - no LDS and no barrier, so a wave retires as soon as its row is
 //    done and the load queue never drains.
-//  * gemv_i8_kernel (2 <= M <= 16), described below; it amortises the
-//    activation chunks over R rows per wave, which the row kernel cannot.
+//  * gemv_i8_kernel (2 <= M <= 4, and larger M when the MFMA kernel's 32-bit
+//    offsets do not reach), described below; it amortises the activation
+//    chunks over R rows per wave, which the row kernel cannot.
+//  * gemv_mfma_kernel (5 <= M <= 16), described at its definition.
 //
 // gemv_i8_kernel: workgroup = 4 waves = R consecutive B rows (output columns n0..n0+R-1).
 // The K bytes of a row are split in four quarters, one per wave (split-K);
@@ -148,51 +150,53 @@ constexpr int ROWS_WAVES = 2;  // waves (= B rows) per workgroup of gemv_rows_ke
 template <int MT, int OUT>
 __global__ __launch_bounds__(ROWS_WAVES * 64) void gemv_rows_kernel(GemmArgs p) {
     const int lane = threadIdx.x & 63;
-    const int n = blockIdx.x * ROWS_WAVES + (threadIdx.x >> 6);
-    if (n >= p.N) return;  // uniform per wave
+    // uniform per wave; readfirstlane keeps the row's buffer resource in SGPRs
+    const int n = __builtin_amdgcn_readfirstlane(blockIdx.x * ROWS_WAVES + (threadIdx.x >> 6));
+    if (n >= p.N) return;
     const int M = p.M, K = p.K;
     const int ck = K >> 4;  // 16-byte chunks per row (K % 64 == 0)
-    // per-row epilogue operands, fetched before the weight stream
-    const float sbn = p.scale_b ? p.scale_b[n] : p.sb;
-    const float biasn = p.bias ? p.bias[n] : 0.0f;
-    const v4i* brow = reinterpret_cast<const v4i*>(static_cast<const int8_t*>(p.B) + static_cast<size_t>(n) * K);
-    const int8_t* A = static_cast<const int8_t*>(p.A);
-    // Rows m >= M of the MT-row template read row 0 (cheap L2 hits) and are
-    // never stored, so the main loop has no per-row branches.
-    const v4i* arow[MT];
+    // B row n and the M activation rows through buffer resources: 32-bit
+    // offsets, the weight stream non-temporal (read once, never re-used),
+    // and chunks past the row end pointed at offset 2^31, which lies outside
+    // every range and reads as zero - so the loop needs no guard.  Rows
+    // m >= M of the MT-row template read row 0 (never stored).
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int8_t*>(static_cast<const int8_t*>(p.B) + static_cast<size_t>(n) * K), 0, K, 0x00020000);
+    __amdgpu_buffer_rsrc_t ra[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m)
-        arow[m] = reinterpret_cast<const v4i*>(A + static_cast<size_t>(m < M ? m : 0) * K);
+        ra[m] = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<int8_t*>(static_cast<const int8_t*>(p.A) + static_cast<size_t>(m < M ? m : 0) * K), 0, K,
+            0x00020000);
     int32_t acc[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) acc[m] = 0;
-    const int nfull = ck >> 8;  // full blocks of 256 chunks (4 KiB of the row)
-    for (int blk = 0; blk < nfull; ++blk) {
-        const int c = (blk << 8) + lane;
+    const int nblk = (ck + 255) >> 8;  // blocks of 256 chunks (4 KiB of the row), the last one partial
+    for (int blk = 0; blk < nblk; ++blk) {
+        int off[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int c = (blk << 8) + lane + 64 * u;
+            off[u] = c < ck ? c * 16 : static_cast<int>(0x80000000u);
+        }
         v4i a[MT][4], b[4];
+        // the weight loads first: they are the ones that go to HBM
+#pragma unroll
+        for (int u = 0; u < 4; ++u) b[u] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rb, off[u], 0, 2));
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int m = 0; m < MT; ++m)
 #pragma unroll
-            for (int u = 0; u < 4; ++u) a[m][u] = arow[m][c + 64 * u];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) b[u] = __builtin_nontemporal_load(brow + c + 64 * u);
+            for (int u = 0; u < 4; ++u)
+                a[m][u] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(ra[m], off[u], 0, 0));
 #pragma unroll
         for (int m = 0; m < MT; ++m)
 #pragma unroll
             for (int u = 0; u < 4; ++u) acc[m] = dot16(a[m][u], b[u], acc[m]);
     }
-    if (ck & 255) {  // tail: fewer than 256 chunks left (K % 4096 != 0)
-        const int c0 = nfull << 8;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int c = c0 + lane + 64 * u;
-            if (c < ck) {
-                const v4i b = brow[c];
-#pragma unroll
-                for (int m = 0; m < MT; ++m) acc[m] = dot16(arow[m][c], b, acc[m]);
-            }
-        }
-    }
+    // per-row epilogue operands (small, L2-resident), fetched after the weight stream
+    const float sbn = p.scale_b ? p.scale_b[n] : p.sb;
+    const float biasn = p.bias ? p.bias[n] : 0.0f;
     int32_t tot[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) tot[m] = wave_sum(acc[m]);
@@ -206,6 +210,85 @@ __global__ __launch_bounds__(ROWS_WAVES * 64) void gemv_rows_kernel(GemmArgs p) 
             store_out<OUT>(p.C, static_cast<size_t>(m) * p.N + n, y, tot[m]);
         }
     }
+}
+
+// gemv_mfma_kernel (5 <= M <= 16): v_mfma_i32_16x16x64_i8 with the M
+// activation rows padded to 16.  The sdot kernel above re-reads every
+// activation chunk for each weight chunk it multiplies, which at M = 16
+// moves 4x more bytes through the caches than the weights themselves; here
+// one 16x16x64 MFMA consumes 64 k bytes of 16 weight rows against all 16
+// activation rows, so activations cost one 16-byte load per 16-byte weight
+// load per column block (halved with two blocks per wave).
+// Workgroup = KS waves over CB*16 consecutive weight rows (output columns);
+// wave w takes a contiguous 1/KS of the 64-byte k steps (split-K) and loads
+// T steps at a time.  Operand layouts (16x16x64 i8): lane l supplies row
+// l%16 (A) / column l%16 (B) with k bytes 16*(l/16)..+15 of the step; the
+// result holds column l%16, rows 4*(l/16)+v.  Activation rows >= M and
+// weight rows >= N are out of their buffers' ranges and read as zero.
+// Partials are summed over the KS waves through LDS (exact int32).
+constexpr int SK_CB = 2, SK_KS = 4, SK_T = 16;
+
+template <int OUT>
+__global__ __launch_bounds__(SK_KS * 64) void gemv_mfma_kernel(GemmArgs p) {
+    __shared__ int32_t red[SK_KS][SK_CB * 256];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int M = p.M, N = p.N, K = p.K;
+    const int n0 = blockIdx.x * SK_CB * 16;
+    const int steps = K >> 6, per = (steps + SK_KS - 1) / SK_KS;
+    const int s0 = wave * per, s1 = min(s0 + per, steps);
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.A), 0, M * K, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.B), 0, N * K, 0x00020000);
+    const int r16 = lane & 15, kq = (lane >> 4) * 16;
+    v4i acc[SK_CB];
+#pragma unroll
+    for (int c = 0; c < SK_CB; ++c) acc[c] = v4i{0, 0, 0, 0};
+    for (int s = s0; s < s1; s += SK_T) {
+        v4i a[SK_T], b[SK_CB][SK_T];
+#pragma unroll
+        for (int t = 0; t < SK_T; ++t) {
+            const bool ok = s + t < s1;  // steps past this wave's range read as zero
+            const int k = (s + t) * 64 + kq;
+#pragma unroll
+            for (int c = 0; c < SK_CB; ++c)
+                b[c][t] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                                                      rb, ok ? (n0 + 16 * c + r16) * K + k : int(0x80000000u), 0, 2));
+            a[t] = __builtin_bit_cast(
+                v4i, __builtin_amdgcn_raw_buffer_load_b128(ra, ok ? r16 * K + k : int(0x80000000u), 0, 0));
+        }
+#pragma unroll
+        for (int t = 0; t < SK_T; ++t)
+#pragma unroll
+            for (int c = 0; c < SK_CB; ++c) acc[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[t], b[c][t], acc[c], 0, 0, 0);
+    }
+#pragma unroll
+    for (int c = 0; c < SK_CB; ++c)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) red[wave][c * 256 + (4 * (lane >> 4) + v) * 16 + r16] = acc[c][v];
+    __syncthreads();
+    for (int o = tid; o < SK_CB * 256; o += SK_KS * 64) {
+        int32_t sum = 0;
+#pragma unroll
+        for (int w = 0; w < SK_KS; ++w) sum += red[w][o];
+        const int m = (o >> 4) & 15, n = n0 + 16 * (o >> 8) + (o & 15);
+        if (m < M && n < N) {
+            const float sc = (p.scale_a ? p.scale_a[m] : p.sa) * (p.scale_b ? p.scale_b[n] : p.sb);
+            store_out<OUT>(p.C, static_cast<size_t>(m) * N + n, epilogue_value(static_cast<float>(sum), sc, p.bias, n),
+                           sum);
+        }
+    }
+}
+
+hipError_t launch_mfma_skinny(const GemmArgs& p, hipStream_t stream) {
+    GemmArgs a = p;
+    void* args[] = {&a};
+    const dim3 grid((p.N + SK_CB * 16 - 1) / (SK_CB * 16));
+    const void* f;
+    switch (p.out_dtype) {
+        case FKE_OUT_F32: f = reinterpret_cast<const void*>(&gemv_mfma_kernel<FKE_OUT_F32>); break;
+        case FKE_OUT_BF16: f = reinterpret_cast<const void*>(&gemv_mfma_kernel<FKE_OUT_BF16>); break;
+        default: f = reinterpret_cast<const void*>(&gemv_mfma_kernel<FKE_OUT_I32>); break;
+    }
+    return hipLaunchKernel(f, grid, dim3(SK_KS * 64), args, 0, stream);
 }
 
 template <int MT>
@@ -248,6 +331,9 @@ hipError_t launch_gemv_i8(const GemmArgs& p, hipStream_t s) {
     if (p.M <= 1) return launch_rows<1>(p, s);
     if (p.M <= 2) return launch_t<2, 16>(p, s);
     if (p.M <= 4) return launch_t<4, 8>(p, s);
+    // the MFMA kernel addresses A and B with 32-bit buffer offsets, computed
+    // for up to 16 activation rows and 32 weight rows past N
+    if ((static_cast<int64_t>(p.N < 16 ? 16 : p.N) + 32) * p.K <= INT32_MAX) return launch_mfma_skinny(p, s);
     if (p.M <= 8) return launch_t<8, 8>(p, s);
     return launch_t<16, 4>(p, s);
 }

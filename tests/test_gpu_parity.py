@@ -152,9 +152,10 @@ def test_gemv_every_m(oracle, dev, M):
 
 
 @pytest.mark.parametrize("K", [64, 128, 4096 + 64, 14336])
-def test_gemv_k_variants(oracle, dev, K):
-    M, N = 3, 300
-    say("gemv K", K)
+@pytest.mark.parametrize("M", [1, 3, 9])  # row kernel, sdot split-K kernel, MFMA skinny kernel
+def test_gemv_k_variants(oracle, dev, M, K):
+    N = 300
+    say("gemv K", M, K)
     A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 300 + K)
     acc = oracle.w8a8_acc(A, B)
     assert_same(gpu_i8(A, B, "nk", "i32", "gemv"), acc, f"gemv K={K}")
