@@ -147,12 +147,16 @@ __device__ __forceinline__ int32_t wave_sum(int32_t v) {
 
 constexpr int ROWS_WAVES = 2;  // waves (= B rows) per workgroup of gemv_rows_kernel
 
-template <int MT, int OUT>
+// FULLK: K is a multiple of 4096, so every 256-chunk block is whole: the
+// activation chunks come with plain loads and no offset needs the 2^31 guard.
+template <int MT, int OUT, bool FULLK>
 __global__ __launch_bounds__(ROWS_WAVES * 64) void gemv_rows_kernel(GemmArgs p) {
     const int lane = threadIdx.x & 63;
-    // uniform per wave; readfirstlane keeps the row's buffer resource in SGPRs
-    const int n = __builtin_amdgcn_readfirstlane(blockIdx.x * ROWS_WAVES + (threadIdx.x >> 6));
-    if (n >= p.N) return;
+    // Uniform per wave; readfirstlane keeps the row's buffer resource in
+    // SGPRs.  A wave past the last row re-reads it and stores nothing, so
+    // nothing stands between the kernel arguments and the first weight load.
+    const int nw = __builtin_amdgcn_readfirstlane(blockIdx.x * ROWS_WAVES + (threadIdx.x >> 6));
+    const int n = min(nw, p.N - 1);
     const int M = p.M, K = p.K;
     const int ck = K >> 4;  // 16-byte chunks per row (K % 64 == 0)
     // B row n and the M activation rows through buffer resources: 32-bit
@@ -168,42 +172,47 @@ __global__ __launch_bounds__(ROWS_WAVES * 64) void gemv_rows_kernel(GemmArgs p) 
         ra[m] = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<int8_t*>(static_cast<const int8_t*>(p.A) + static_cast<size_t>(m < M ? m : 0) * K), 0, K,
             0x00020000);
+    // per-row epilogue operands: scalar loads (n is uniform) whose latency
+    // hides behind the weight stream
+    const float sbn = p.scale_b ? p.scale_b[n] : p.sb;
+    const float biasn = p.bias ? p.bias[n] : 0.0f;
     int32_t acc[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) acc[m] = 0;
-    const int nblk = (ck + 255) >> 8;  // blocks of 256 chunks (4 KiB of the row), the last one partial
-    for (int blk = 0; blk < nblk; ++blk) {
+    const int nblk = (ck + 255) >> 8;  // blocks of 256 chunks (4 KiB of the row), the last one partial; >= 1
+    int blk = 0;
+    do {
         int off[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int c = (blk << 8) + lane + 64 * u;
-            off[u] = c < ck ? c * 16 : static_cast<int>(0x80000000u);
+            off[u] = FULLK || c < ck ? c * 16 : static_cast<int>(0x80000000u);
         }
         v4i a[MT][4], b[4];
-        // the weight loads first: they are the ones that go to HBM
 #pragma unroll
         for (int u = 0; u < 4; ++u) b[u] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rb, off[u], 0, 2));
-        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int m = 0; m < MT; ++m)
 #pragma unroll
-            for (int u = 0; u < 4; ++u)
-                a[m][u] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(ra[m], off[u], 0, 0));
+            for (int u = 0; u < 4; ++u) {
+                if constexpr (FULLK)
+                    a[m][u] = *reinterpret_cast<const v4i*>(static_cast<const int8_t*>(p.A) +
+                                                            static_cast<size_t>(m < M ? m : 0) * K + off[u]);
+                else
+                    a[m][u] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(ra[m], off[u], 0, 0));
+            }
 #pragma unroll
         for (int m = 0; m < MT; ++m)
 #pragma unroll
             for (int u = 0; u < 4; ++u) acc[m] = dot16(a[m][u], b[u], acc[m]);
-    }
-    // per-row epilogue operands (small, L2-resident), fetched after the weight stream
-    const float sbn = p.scale_b ? p.scale_b[n] : p.sb;
-    const float biasn = p.bias ? p.bias[n] : 0.0f;
+    } while (++blk < nblk);
     int32_t tot[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) tot[m] = wave_sum(acc[m]);
     // lane m stores output row m (all lanes hold every total)
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
-        if (lane == m && m < M) {
+        if (lane == m && m < M && nw < p.N) {
             const float sc = (p.scale_a ? p.scale_a[m] : p.sa) * sbn;
             const float y = p.bias ? __builtin_fmaf(static_cast<float>(tot[m]), sc, biasn)
                                    : static_cast<float>(tot[m]) * sc;
@@ -291,16 +300,16 @@ hipError_t launch_mfma_skinny(const GemmArgs& p, hipStream_t stream) {
     return hipLaunchKernel(f, grid, dim3(SK_KS * 64), args, 0, stream);
 }
 
-template <int MT>
+template <int MT, bool FULLK>
 hipError_t launch_rows(const GemmArgs& p, hipStream_t stream) {
     GemmArgs a = p;
     void* args[] = {&a};
     const dim3 grid((p.N + ROWS_WAVES - 1) / ROWS_WAVES);
     const void* f;
     switch (p.out_dtype) {
-        case FKE_OUT_F32: f = reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_F32>); break;
-        case FKE_OUT_BF16: f = reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_BF16>); break;
-        default: f = reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_I32>); break;
+        case FKE_OUT_F32: f = reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_F32, FULLK>); break;
+        case FKE_OUT_BF16: f = reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_BF16, FULLK>); break;
+        default: f = reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_I32, FULLK>); break;
     }
     return hipLaunchKernel(f, grid, dim3(ROWS_WAVES * 64), args, 0, stream);
 }
@@ -328,7 +337,7 @@ bool gemv_i8_supports(const GemmArgs& p) {
 }
 
 hipError_t launch_gemv_i8(const GemmArgs& p, hipStream_t s) {
-    if (p.M <= 1) return launch_rows<1>(p, s);
+    if (p.M <= 1) return p.K % 4096 == 0 ? launch_rows<1, true>(p, s) : launch_rows<1, false>(p, s);
     if (p.M <= 2) return launch_t<2, 16>(p, s);
     if (p.M <= 4) return launch_t<4, 8>(p, s);
     // the MFMA kernel addresses A and B with 32-bit buffer offsets, computed
