@@ -28,6 +28,11 @@ PEAK_HBM_GBS = 8000.0     # MI355X HBM3E, published (8 TB/s)
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic.json")
 
 
+def gemv_kernel(M):
+    """Decode kernel the dispatcher picks for M rows (K % 4096 == 0, B [N,K])."""
+    return "gemv_rows_kernel" if M == 1 else "gemv_i8_kernel" if M <= 4 else "gemv_mfma_kernel"
+
+
 def traffic(key):
     """HBM bytes per launch measured by rocprofv3 FETCH_SIZE + WRITE_SIZE (calibrated
     against a copy kernel), as recorded in profiles/traffic.json; None if absent."""
@@ -203,9 +208,9 @@ def gemv_bench(torch, L, _lib, dev, gen, M, nbuf, launches, N=14336, K=4096):
             "timing": f"HIP graph of {launches} launches x {reps} replays, events on the graph's stream",
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
                          "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
-                         "traffic": traffic(f"gemv_i8_kernel M={M} N={N} K={K} bf16+bias"),
+                         "traffic": traffic(f"{gemv_kernel(M)} M={M} N={N} K={K} bf16+bias"),
                          "algorithmic_bytes_per_launch": nbytes},
-            "kernel": "gemv_i8_kernel"}
+            "kernel": gemv_kernel(M)}
 
 
 def extra_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
