@@ -160,6 +160,33 @@ def gemv_bytes(M, N, K, out_bytes=2, bias=True):
     return M * K + N * K + 4 * M + 4 * N + (4 * N if bias else 0) + out_bytes * M * N
 
 
+def graph_us(torch, dev, launch, launches, warm, reps=3):
+    """Per-launch microseconds of `launch(i, stream)` captured `launches` times in
+    one HIP graph, replayed `reps` times; events on the graph's stream."""
+    s = torch.cuda.Stream(device=dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):  # warm up outside the graph
+        for i in range(warm):
+            launch(i, s.cuda_stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for i in range(launches):
+            launch(i, s.cuda_stream)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(s):  # replay on s, where the events are recorded
+        e0.record(s)
+        for _ in range(reps):
+            g.replay()
+        e1.record(s)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (reps * launches)
+
+
 def gemv_bench(torch, L, _lib, dev, gen, M, nbuf, launches, N=14336, K=4096):
     """Launch-averaged duration of the decode GEMV from a HIP graph of `launches`
     calls cycling over `nbuf` distinct weight buffers (>= 448 MiB in total)."""
@@ -177,35 +204,13 @@ def gemv_bench(torch, L, _lib, dev, gen, M, nbuf, launches, N=14336, K=4096):
         if st:
             raise RuntimeError(f"gemv failed: {_lib.status_string(st)}")
 
-    s = torch.cuda.Stream(device=dev)
-    s.wait_stream(torch.cuda.current_stream(dev))
-    with torch.cuda.stream(s):  # warm up outside the graph
-        for i in range(2 * nbuf):
-            launch(i, s.cuda_stream)
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g, stream=s):
-        for i in range(launches):
-            launch(i, s.cuda_stream)
-    torch.cuda.synchronize()
-    with torch.cuda.stream(s):
-        g.replay()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    reps = 3
-    with torch.cuda.stream(s):  # replay on s, where the events are recorded
-        e0.record(s)
-        for _ in range(reps):
-            g.replay()
-        e1.record(s)
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1e3 / (reps * launches)
+    us = graph_us(torch, dev, launch, launches, 2 * nbuf)
     nbytes = gemv_bytes(M, N, K)
     gbs = nbytes / (us * 1e-6) / 1e9
     return {"metric": f"HBM GB/s, decode GEMV M={M} N={N} K={K} (bf16 out, fused bias)",
             "value": round(gbs, 1), "unit": "GB/s", "us_per_launch": round(us, 3),
             "weight_buffers": nbuf, "weight_bytes_cycled": nbuf * N * K,
-            "timing": f"HIP graph of {launches} launches x {reps} replays, events on the graph's stream",
+            "timing": f"HIP graph of {launches} launches x 3 replays, events on the graph's stream",
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
                          "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
                          "traffic": traffic(f"{gemv_kernel(M)} M={M} N={N} K={K} bf16+bias"),
@@ -261,6 +266,25 @@ def extra_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
     del A8, B8, C
     for m in (4, 16):
         res[f"gemv_M{m}"] = gemv_bench(torch, L, _lib, dev, gen, m, args.gemv_buffers, args.gemv_launches)
+    # per-token INT8 quantiser in front of the W8A8 GEMM: bf16 activations of C3 (4096 x 4096),
+    # 12 rotating inputs (384 MiB, more than the MALL), timed from a HIP graph like the GEMV
+    M, K, nx = 4096, 4096, 12
+    Xs = [torch.randn((M, K), device=dev, generator=gen).to(torch.bfloat16) for _ in range(nx)]
+    Q = torch.empty((M, K), dtype=torch.int8, device=dev)
+    S = torch.empty(M, dtype=torch.float32, device=dev)
+
+    def qlaunch(i, st):
+        r = L.fke_quantize_rows_i8(Xs[i % nx].data_ptr(), _lib.IN_BF16, M, K, Q.data_ptr(), S.data_ptr(), st)
+        if r:
+            raise RuntimeError(f"quantiser failed: {_lib.status_string(r)}")
+
+    us = graph_us(torch, dev, qlaunch, 240, 2 * nx)
+    nbytes = M * K * 2 + M * K + 4 * M
+    gbs = nbytes / (us * 1e-6) / 1e9
+    res["quantize_rows_4096x4096_bf16"] = {"us": round(us, 2), "GB/s": round(gbs, 1),
+                                           "frac": round(gbs / PEAK_HBM_GBS, 4), "bytes": nbytes,
+                                           "kernel": "quant_rows_kernel<bf16>"}
+    del Xs, Q, S
     return res
 
 

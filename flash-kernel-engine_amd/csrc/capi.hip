@@ -140,6 +140,13 @@ int fke_select_path_f8(const void* A, const void* B, const void* C, int M, int N
                              out_dtype, b_layout));
 }
 
+int fke_quantize_rows_i8(const void* X, int in_dtype, int M, int K, int8_t* Q, float* scale,
+                         void* stream) {
+    if (!X || !Q || !scale || M < 1 || K < 1) return hipErrorInvalidValue;
+    if (in_dtype != FKE_IN_F32 && in_dtype != FKE_IN_BF16) return hipErrorInvalidValue;
+    return fke::launch_quant_rows(X, in_dtype, M, K, Q, scale, static_cast<hipStream_t>(stream));
+}
+
 // Reference src/quantized_gemm.cu:56-75: B [N,K], fp32 out, alpha = sa*sb.
 int fke_launch_int8_gemm_dp4a(const int8_t* d_A, const int8_t* d_B, float* d_C, float scale_a,
                               float scale_b, int M, int N, int K, void* stream) {

@@ -32,6 +32,8 @@ enum Elem { ELEM_I8 = 0, ELEM_F8 = 1 };
 hipError_t launch_generic(const GemmArgs& p, int elem, hipStream_t stream);
 hipError_t launch_gemv_i8(const GemmArgs& p, hipStream_t stream);
 hipError_t launch_mfma(const GemmArgs& p, int elem, hipStream_t stream);
+hipError_t launch_quant_rows(const void* X, int in_dtype, int M, int K, int8_t* Q, float* S,
+                             hipStream_t stream);
 
 // Shape/alignment predicates of the fast families (host side).
 bool gemv_i8_supports(const GemmArgs& p);

@@ -3,7 +3,8 @@ on gfx950 HIP kernels.  Mirrors reference python/flash_engine/__init__.py for
 this path; the reference's attention / normalisation ops are not part of it.
 """
 from ._lib import version
-from .ops import fp8_gemm_scaled, print_device_info, quantized_gemm_int8, w8a8_gemm
+from .ops import (fp8_gemm_scaled, print_device_info, quantize_per_token, quantized_gemm_int8,
+                  w8a8_gemm, w8a8_linear)
 
 __version__ = "1.2.0"
 
@@ -11,6 +12,8 @@ __all__ = [
     "quantized_gemm_int8",
     "w8a8_gemm",
     "fp8_gemm_scaled",
+    "quantize_per_token",
+    "w8a8_linear",
     "print_device_info",
     "version",
 ]

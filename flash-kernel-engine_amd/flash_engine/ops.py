@@ -123,6 +123,51 @@ def fp8_gemm_scaled(A: torch.Tensor, B: torch.Tensor, scale_a: float, scale_b: f
     return out
 
 
+def quantize_per_token(x: torch.Tensor, q: torch.Tensor | None = None,
+                       scale: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-token symmetric INT8 quantisation of activations x [M,K] (fp32 or bf16).
+
+    scale[m] = fp32(max_k |x[m,k]| / 127), r = fp32(127 / max_k |x[m,k]|) (both 1
+    for an all-zero row) and q[m,k] = clamp(round_half_even(fp32(x[m,k] * r)), -127, 127),
+    so x ~= q * scale.
+    Returns (q int8 [M,K], scale fp32 [M]) on x's device, ready to be the A and
+    scale_a of `w8a8_gemm`.  No reference counterpart: the reference's quantized
+    GEMMs take int8 inputs with scalar scales.
+    """
+    dev = x.device
+    codes = {torch.float32: _lib.IN_F32, torch.bfloat16: _lib.IN_BF16}
+    if x.dtype not in codes:
+        raise TypeError(f"x must be float32 or bfloat16, got {x.dtype}")
+    _check_dev("x", x, x.dtype, dev)
+    if x.dim() != 2:
+        raise ValueError("x must be 2-D [M,K]")
+    M, K = x.shape
+    if q is None:
+        q = torch.empty((M, K), dtype=torch.int8, device=dev)
+    else:
+        _check_dev("q", q, torch.int8, dev)
+    if scale is None:
+        scale = torch.empty(M, dtype=torch.float32, device=dev)
+    else:
+        _check_vec("scale", scale, M, dev)
+    st = _lib.lib().fke_quantize_rows_i8(x.data_ptr(), codes[x.dtype], M, K, q.data_ptr(),
+                                         scale.data_ptr(), _stream(x))
+    _lib.check(st, "fke_quantize_rows_i8")
+    return q, scale
+
+
+def w8a8_linear(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor, bias=None,
+                out_dtype=torch.bfloat16) -> torch.Tensor:
+    """y = x . W^T with W8A8 quantisation: x [M,K] fp32/bf16 activations are
+    quantised per token (`quantize_per_token`), weight [N,K] int8 carries
+    per-channel scales weight_scale [N]; bias [N] fp32 optional.  Two launches
+    on the current stream: the quantiser, then `w8a8_gemm`.
+    """
+    q, sa = quantize_per_token(x)
+    return w8a8_gemm(q, weight, scale_a=sa, scale_b=weight_scale, bias=bias, out_dtype=out_dtype,
+                     b_layout="nk")
+
+
 def quantized_gemm_int8(A, B, scale_a: float = 1.0, scale_b: float = 1.0):
     """C = (A_int8 @ B_int8) * (scale_a * scale_b), B stored [K,N], fp32 out.
 

@@ -37,6 +37,12 @@ enum fke_b_layout {
     FKE_B_KN = 1  /* B[k*N + n] */
 };
 
+/* Element type of the activations given to the quantiser. */
+enum fke_in_dtype {
+    FKE_IN_F32 = 0,  /* fp32 */
+    FKE_IN_BF16 = 1  /* bf16 */
+};
+
 /* Kernel family used by a call (for tests and benchmarks). */
 enum fke_path {
     FKE_PATH_AUTO = 0,    /* dispatcher's choice                                */
@@ -106,6 +112,22 @@ int fke_qgemm_f8(const uint8_t* A, const uint8_t* B, void* C, int M, int N, int 
 int fke_qgemm_f8_on_path(int path, const uint8_t* A, const uint8_t* B, void* C,
                          int M, int N, int K, float sa, float sb, const float* bias,
                          int out_dtype, int b_layout, void* stream);
+
+/*
+ * Per-token (per-row) symmetric INT8 quantiser: the step that produces A and
+ * scale_a for fke_qgemm_i8 from fp32 or bf16 activations X [M,K].  No
+ * reference counterpart (the reference GEMMs take int8 inputs and scalar
+ * scales, src/quantized_gemm.cu:56-75):
+ *   amax_m = max_k |X[m,k]|             (NaN elements ignored)
+ *   s_m    = fp32(amax_m / 127) -> scale[m];  r_m = fp32(127 / amax_m)
+ *            (both 1 when amax_m == 0)
+ *   Q[m,k] = clamp(rne(fp32(X[m,k] * r_m)), -127, 127)       (NaN -> 0)
+ * The divisions are IEEE fp32, correctly rounded.  Q is int8 [M,K] row-major,
+ * scale fp32 [M]; device buffers.  Rejects NULL pointers, M,K <= 0 and bad
+ * dtypes with hipErrorInvalidValue.
+ */
+int fke_quantize_rows_i8(const void* X, int in_dtype, int M, int K, int8_t* Q, float* scale,
+                         void* stream);
 
 /* The family fke_qgemm_i8 / fke_qgemm_f8 would pick (enum fke_path), or -1
  * for arguments they would reject.  Pure host logic; needs no GPU. */

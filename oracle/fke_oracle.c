@@ -310,3 +310,32 @@ float fko_quantize_e4m3(const float* x, uint8_t* q, size_t n) {
     for (size_t i = 0; i < n; ++i) q[i] = fko_f32_to_e4m3_sat(x[i] / s);
     return s;
 }
+
+/* Per-token INT8 quantiser (no reference counterpart).  fp32 arithmetic as the
+ * kernel does it: the scale and its reciprocal are single correctly rounded
+ * fp32 divisions, each code one fp32 product (the file is built with
+ * -ffp-contract=off); nearbyintf rounds half to even in the default mode. */
+void fko_quantize_rows_i8(const void* x, int in_dtype, int M, int K, int8_t* q, float* scale) {
+    for (int m = 0; m < M; ++m) {
+        float amax = 0.0f;
+        for (int k = 0; k < K; ++k) {
+            const size_t i = (size_t)m * K + k;
+            const float v = in_dtype == 0 ? ((const float*)x)[i] : fko_bf16_to_f32(((const uint16_t*)x)[i]);
+            const float a = fabsf(v);
+            if (a > amax) amax = a;
+        }
+        const float s = amax == 0.0f ? 1.0f : amax / 127.0f;
+        const float r = amax == 0.0f ? 1.0f : 127.0f / amax;
+        scale[m] = s;
+        for (int k = 0; k < K; ++k) {
+            const size_t i = (size_t)m * K + k;
+            const float v = in_dtype == 0 ? ((const float*)x)[i] : fko_bf16_to_f32(((const uint16_t*)x)[i]);
+            if (v != v) { q[i] = 0; continue; }
+            const float p = v * r;
+            float t = nearbyintf(p);
+            if (t > 127.0f) t = 127.0f;
+            if (t < -127.0f) t = -127.0f;
+            q[i] = (int8_t)t;
+        }
+    }
+}

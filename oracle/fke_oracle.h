@@ -21,6 +21,9 @@
  *                             uniform / bias absent / fp32 out; bf16 RNE known
  *                             answers; exact-integer checksums.
  *   generators                fixed known-answer streams (SplitMix64 KAT).
+ *   fko_quantize_rows_i8      hand-derived rows (ties to even, exact scales),
+ *                             invariants (the amax element maps to +-127,
+ *                             |q*s - x| <= s/2), brute force in exact rationals.
  */
 #ifndef FKE_ORACLE_H
 #define FKE_ORACLE_H
@@ -85,6 +88,12 @@ float fko_bf16_to_f32(uint16_t h);
 uint8_t fko_f32_to_e4m3_sat(float x);
 /* per-tensor quantiser of the FP8 config: s = amax/448, q = e4m3_sat(x/s). */
 float fko_quantize_e4m3(const float* x, uint8_t* q, size_t n);
+/* per-token INT8 activation quantiser (no reference counterpart; the step in
+ * front of the W8A8 GEMM): per row m, amax = max|x| over non-NaN elements,
+ * s = fp32(amax/127), r = fp32(127/amax) (both 1 when amax == 0),
+ * q = clamp(rne(fp32(x*r)), -127, 127), NaN -> 0; scale[m] = s.
+ * x is fp32 (in_dtype 0) or bf16 bits (in_dtype 1), [M,K]. */
+void fko_quantize_rows_i8(const void* x, int in_dtype, int M, int K, int8_t* q, float* scale);
 
 #ifdef __cplusplus
 }

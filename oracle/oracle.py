@@ -67,6 +67,8 @@ def _declare(L):
     L.fko_f32_to_e4m3_sat.argtypes = [_f]
     L.fko_f32_to_e4m3_sat.restype = ct.c_uint8
     L.fko_quantize_e4m3.argtypes = [_p, _p, _sz]
+    L.fko_quantize_rows_i8.argtypes = [_p, _i, _i, _i, _p, _p]
+    L.fko_quantize_rows_i8.restype = None
     L.fko_quantize_e4m3.restype = _f
 
 
@@ -223,3 +225,17 @@ def quantize_e4m3(x) -> tuple[np.ndarray, float]:
     q = np.empty(x.shape, dtype=np.uint8)
     s = lib().fko_quantize_e4m3(_ptr(x), _ptr(q), x.size)
     return q, float(s)
+
+
+IN_F32, IN_BF16 = 0, 1
+
+
+def quantize_rows_i8(x, in_dtype: int = IN_F32) -> tuple[np.ndarray, np.ndarray]:
+    """Per-token INT8 quantiser: x [M,K] fp32 (IN_F32) or bf16 bits as uint16
+    (IN_BF16) -> (q int8 [M,K], scale fp32 [M])."""
+    x = _c(x, np.float32 if in_dtype == IN_F32 else np.uint16)
+    M, K = x.shape
+    q = np.empty((M, K), dtype=np.int8)
+    s = np.empty(M, dtype=np.float32)
+    lib().fko_quantize_rows_i8(_ptr(x), in_dtype, M, K, _ptr(q), _ptr(s))
+    return q, s

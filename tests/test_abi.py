@@ -62,6 +62,18 @@ def test_rejects_null_pointers_and_bad_enums():
     assert L.fke_qgemm_i8_on_path(9, P, P, P, 8, 8, 8, None, None, 1.0, 1.0, None, 0, 0, None) == INVALID
 
 
+def test_quantizer_rejects_bad_arguments():
+    L = _lib.lib()
+    q = L.fke_quantize_rows_i8
+    assert q(None, 0, 4, 8, P, P, None) == INVALID
+    assert q(P, 0, 4, 8, None, P, None) == INVALID
+    assert q(P, 0, 4, 8, P, None, None) == INVALID
+    for M, K in [(0, 8), (4, 0), (-1, 8)]:
+        assert q(P, 0, M, K, P, P, None) == INVALID
+    for dt in (-1, 2):
+        assert q(P, dt, 4, 8, P, P, None) == INVALID
+
+
 def test_dropin_int8_rejects_k_not_multiple_of_4():
     """The reference kernel silently drops the K tail and misaligns rows when
     K % 4 != 0 (src/quantized_gemm.cu:28-30); the drop-in rejects it."""

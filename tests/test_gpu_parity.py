@@ -317,3 +317,67 @@ def test_python_op_matches_reference_numpy_op(oracle, dev):
             assert_same(got_np, ref, "python op (numpy in)")
             got_t = ops.quantized_gemm_int8(dev_t(A), dev_t(B), sa, sb)
             assert_same(host(got_t), ref, "python op (torch in)")
+
+
+# ------------------------------------------------- per-token INT8 quantiser
+
+def quant_inputs(oracle, M, K, seed, dtype):
+    x = oracle.gen_f32_normal((M, K), seed, 0.0, 1.0)
+    x *= oracle.gen_f32_uniform((M, 1), seed + 1, 0.01, 100.0)   # row scales over four decades
+    if M > 2:
+        x[1, :] = 0.0                                            # an all-zero row
+        x[2, ::5] = np.float32(x[2, 0])                          # repeated values, ties
+    if dtype == "bf16":
+        bits = (torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16))
+        return bits, oracle.IN_BF16
+    return x, oracle.IN_F32
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("M,K", [(1, 4096), (16, 4096), (300, 1024), (7, 10000), (33, 8 * 1337), (5, 100), (3, 1)])
+def test_quantize_rows_bit_exact(oracle, dev, M, K, dtype):
+    """Chunked kernel (K % 8 == 0), rows longer than the register cache
+    (K = 10000, 10696) and the element-wise kernel (K = 100, K = 1) against the
+    oracle: codes and scales bit-exact."""
+    say("quantize rows", M, K, dtype)
+    x, code = quant_inputs(oracle, M, K, 900 + M + K, dtype)
+    q_ref, s_ref = oracle.quantize_rows_i8(x, code)
+    xt = dev_t(x) if dtype == "f32" else dev_t(x.view(np.int16)).view(torch.bfloat16)
+    q, s = ops.quantize_per_token(xt)
+    torch.cuda.synchronize()
+    assert np.array_equal(s.cpu().numpy(), s_ref)
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+
+
+def test_quantize_rows_unaligned_input(oracle, dev):
+    """A row base that is not 16-byte aligned takes the element-wise kernel."""
+    M, K = 9, 512
+    say("quantize rows unaligned", M, K)
+    x, _ = quant_inputs(oracle, M, K + 1, 950, "f32")
+    xs = np.ascontiguousarray(x.reshape(-1)[1:1 + M * K].reshape(M, K))
+    q_ref, s_ref = oracle.quantize_rows_i8(xs)
+    big = dev_t(x.reshape(-1))
+    xt = big[1:1 + M * K].view(M, K)            # 4-byte offset from the allocation
+    assert xt.data_ptr() % 16 != 0
+    q, s = ops.quantize_per_token(xt)
+    torch.cuda.synchronize()
+    assert np.array_equal(s.cpu().numpy(), s_ref) and np.array_equal(q.cpu().numpy(), q_ref)
+
+
+@pytest.mark.parametrize("M", [1, 9, 300])
+def test_w8a8_linear_end_to_end(oracle, dev, M):
+    """bf16 activations -> per-token quantiser -> W8A8 GEMM with per-channel
+    weight scales and bias, bf16 out: bit-exact against the oracle's quantiser
+    followed by the oracle's GEMM (exercises GEMV, MFMA-skinny and MFMA GEMM)."""
+    N, K = 640, 4096
+    say("w8a8_linear", M, N, K)
+    x, code = quant_inputs(oracle, M, K, 970 + M, "bf16")
+    W = oracle.gen_i8_uniform((N, K), 971)
+    ws = oracle.gen_f32_uniform((N,), 972, 0.001, 0.02)
+    bias = oracle.gen_f32_normal((N,), 973, 0.0, 0.02)
+    q_ref, s_ref = oracle.quantize_rows_i8(x, code)
+    acc = oracle.w8a8_acc(q_ref, W)
+    ref = oracle.w8a8_epilogue(acc, s_ref, ws, 1.0, 1.0, bias, oracle.OUT_BF16)
+    xt = dev_t(x.view(np.int16)).view(torch.bfloat16)
+    y = ops.w8a8_linear(xt, dev_t(W), dev_t(ws), dev_t(bias), out_dtype=torch.bfloat16)
+    assert_same(host(y), ref, f"w8a8_linear M={M}")

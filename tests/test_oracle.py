@@ -309,3 +309,78 @@ def test_c1_golden_fixture(oracle):
     assert sha(bf16) == g["sha256"]["bf16"]
     for m, n, a, fbits, h in g["samples"]:
         assert acc[m, n] == a and f32[m:m + 1, n].view(np.uint32)[0] == fbits and bf16[m, n] == h
+
+
+# ------------------------------------------------- per-token INT8 quantiser
+
+def test_quantize_rows_known_answers(oracle):
+    """Hand-derived rows.  Row 1 has amax 127, so r = 1 exactly and x*r = x:
+    2.5 -> 2 and 3.5 -> 4 (ties to even), -2.5 -> -2.  Row 0: r = 127/2 = 63.5
+    exactly, so 1 -> 63.5 -> 64 (tie to even), 0.5 -> 31.75 -> 32, and the amax
+    element -2 -> -127.  An all-zero row gets scale 1 and zero codes."""
+    x = np.array([[1.0, -2.0, 0.5, 0.0],
+                  [127.0, 2.5, 3.5, -2.5],
+                  [0.0, 0.0, 0.0, 0.0],
+                  [-0.25, 0.125, 0.0625, 1e-9]], dtype=np.float32)
+    q, s = oracle.quantize_rows_i8(x)
+    assert s[0] == np.float32(2.0) / np.float32(127.0)
+    assert s[1] == 1.0 and s[2] == 1.0
+    assert s[3] == np.float32(0.25) / np.float32(127.0)
+    assert q[0].tolist() == [64, -127, 32, 0]
+    assert q[1].tolist() == [127, 2, 4, -2]
+    assert q[2].tolist() == [0, 0, 0, 0]
+    assert q[3].tolist() == [-127, 64, 32, 0]     # r = 508: 0.125 -> 63.5 -> 64, 0.0625 -> 31.75
+
+
+def test_quantize_rows_invariants(oracle):
+    """On random rows: the scale is fp32(amax/127); the amax element maps to
+    +-127; every code is within [-127, 127]; and the dequantised value is within
+    half a step of x (plus the one rounding of the quotient), checked in exact
+    rationals."""
+    r = rng(21)
+    x = (r.standard_normal((64, 300)) * r.uniform(1e-3, 1e3, (64, 1))).astype(np.float32)
+    q, s = oracle.quantize_rows_i8(x)
+    amax = np.abs(x).max(axis=1)
+    assert np.array_equal(s, amax / np.float32(127.0))
+    assert np.all(np.abs(q.astype(np.int32)) <= 127)
+    for m in range(x.shape[0]):
+        k = int(np.argmax(np.abs(x[m])))
+        assert q[m, k] == (127 if x[m, k] > 0 else -127)
+        sm = Fraction(float(s[m]))
+        for k in range(0, x.shape[1], 7):
+            err = abs(Fraction(int(q[m, k])) * sm - Fraction(float(x[m, k])))
+            assert err <= sm / 2 * Fraction(1 + 2**-20), (m, k)
+
+
+def test_quantize_rows_matches_numpy_fp32_semantics(oracle):
+    """numpy's float32 division and product are IEEE correctly rounded and
+    np.rint rounds half to even: an independent evaluation of the same fp32
+    arithmetic.  A C slip such as a double-precision product, dividing by s
+    instead of multiplying by r, or truncation instead of rint fails."""
+    r = rng(22)
+    x = (r.standard_normal((40, 1000)) * 3).astype(np.float32)
+    x[5, :] = 0.0
+    x[6, ::3] = np.float32(1.5)     # exact ties once s is a power of two
+    x[6, 0] = np.float32(127.0)
+    q, s = oracle.quantize_rows_i8(x)
+    amax = np.abs(x).max(axis=1)
+    zero = amax == 0
+    s_np = np.where(zero, np.float32(1.0), amax / np.float32(127.0)).astype(np.float32)
+    with np.errstate(divide="ignore"):
+        r_np = np.where(zero, np.float32(1.0), np.float32(127.0) / amax).astype(np.float32)
+    q_np = np.clip(np.rint(x * r_np[:, None]), -127, 127).astype(np.int8)
+    assert np.array_equal(s, s_np)
+    assert np.array_equal(q, q_np)
+    assert q[6, 3] == 2                # 1.5 with s = 1 -> 2 (even)
+
+
+def test_quantize_rows_bf16_input(oracle):
+    """bf16 inputs quantise exactly like their fp32 values (bf16 -> fp32 is
+    exact: the bits shifted left by 16)."""
+    r = rng(23)
+    x32 = r.standard_normal((8, 256)).astype(np.float32)
+    bits = np.array([oracle.f32_to_bf16_rne(float(v)) for v in x32.ravel()], dtype=np.uint16).reshape(x32.shape)
+    xb = oracle.bf16_to_f32(bits)
+    qb, sb = oracle.quantize_rows_i8(bits, oracle.IN_BF16)
+    qf, sf = oracle.quantize_rows_i8(xb)
+    assert np.array_equal(qb, qf) and np.array_equal(sb, sf)
