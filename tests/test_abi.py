@@ -128,3 +128,23 @@ def test_dropin_header_program_host_checks():
     r = subprocess.run([DROPIN, "--host-only"], capture_output=True, text=True, timeout=60)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "[PASS]" in r.stdout
+
+
+def test_torch_extension_loads_and_binds_the_ops():
+    """The torch extension (bindings.cpp idiom) imports and exposes its three
+    entries; it links libfke_qgemm.so, whose exports are checked above."""
+    from flash_engine import _ext
+    m = _ext.ext()
+    for name in ("quantized_gemm_int8_forward", "fp8_gemm_scaled_forward", "quantize_per_token_forward"):
+        assert hasattr(m, name), name
+
+
+def test_torch_extension_rejects_host_tensors():
+    import torch
+    from flash_engine import _ext
+    m = _ext.ext()
+    a = torch.zeros((4, 8), dtype=torch.int8)
+    with pytest.raises(RuntimeError, match="GPU tensor"):
+        m.quantized_gemm_int8_forward(a, a)
+    with pytest.raises(RuntimeError, match="GPU tensor"):
+        m.quantize_per_token_forward(torch.zeros((4, 8)))

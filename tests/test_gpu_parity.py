@@ -381,3 +381,39 @@ def test_w8a8_linear_end_to_end(oracle, dev, M):
     xt = dev_t(x.view(np.int16)).view(torch.bfloat16)
     y = ops.w8a8_linear(xt, dev_t(W), dev_t(ws), dev_t(bias), out_dtype=torch.bfloat16)
     assert_same(host(y), ref, f"w8a8_linear M={M}")
+
+
+# ------------------------------------------------- torch extension binding
+
+@pytest.mark.parametrize("layout", ["nk", "kn"])
+def test_torch_extension_i8_bit_exact(oracle, dev, layout):
+    """flash_engine_hip.quantized_gemm_int8_forward (bindings.cpp idiom) on the
+    MFMA and decode families, every output type, against the oracle."""
+    from flash_engine import _ext
+    m = _ext.ext()
+    for (M, N, K) in [(300, 528, 384), (3, 300, 1024)]:
+        if layout == "kn" and M <= 16:
+            continue  # the decode family takes [N,K] only (the generic family covers it)
+        say("torch ext i8", layout, M, N, K)
+        A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 990 + M, layout)
+        acc = oracle.w8a8_acc(A, B, oracle.B_NK if layout == "nk" else oracle.B_KN)
+        for out in ("f32", "bf16", "i32"):
+            y = m.quantized_gemm_int8_forward(dev_t(A), dev_t(B), dev_t(sa), dev_t(sb), dev_t(bias),
+                                              OUT_T[out], layout, 1.0, 1.0)
+            assert_same(host(y), oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, out), f"ext {layout} {out}")
+
+
+def test_torch_extension_f8_and_quantizer(oracle, dev):
+    from flash_engine import _ext
+    m = _ext.ext()
+    M, N, K = 256, 256, 512
+    say("torch ext f8 + quantizer", M, N, K)
+    A, B, sa, sb = f8_inputs(oracle, M, N, K, 995, "kn")
+    y = m.fp8_gemm_scaled_forward(dev_t(A), dev_t(B), sa, sb, None, torch.float32, "kn")
+    ref = oracle.f8_gemm(A, B, sa, sb, None, oracle.OUT_F32, oracle.B_KN, nthreads=NTH)
+    err = np.abs(y.cpu().numpy() - ref).max() / max(np.abs(ref).max(), 1e-30)
+    assert err <= 2e-2, err
+    x, code = quant_inputs(oracle, 20, 4096, 996, "f32")
+    q, s = m.quantize_per_token_forward(dev_t(x))
+    q_ref, s_ref = oracle.quantize_rows_i8(x, code)
+    assert np.array_equal(q.cpu().numpy(), q_ref) and np.array_equal(s.cpu().numpy(), s_ref)
