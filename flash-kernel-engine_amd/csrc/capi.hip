@@ -52,6 +52,21 @@ GemmArgs make_args(const void* A, const void* B, void* C, int M, int N, int K, c
     p.bias = bias;
     p.out_dtype = out_dtype;
     p.b_layout = b_layout;
+    p.swiglu = 0;
+    return p;
+}
+
+// SwiGLU GEMM: B is the merged [2I, K] weight; the kernels see N = 2I.
+bool swiglu_args_ok(const void* A, const void* W, const void* H, int M, int I, int K, int out_dtype) {
+    if (I < 1 || I > INT32_MAX / 2) return false;
+    return common_args_ok(A, W, H, M, 2 * I, K, FKE_B_NK) &&
+           (out_dtype == FKE_OUT_F32 || out_dtype == FKE_OUT_BF16);
+}
+
+GemmArgs make_swiglu_args(const void* A, const void* W, void* H, int M, int I, int K, const float* scale_a,
+                          const float* scale_b, float sa, float sb, const float* bias, int out_dtype) {
+    GemmArgs p = make_args(A, W, H, M, 2 * I, K, scale_a, scale_b, sa, sb, bias, out_dtype, FKE_B_NK);
+    p.swiglu = 1;
     return p;
 }
 
@@ -124,6 +139,34 @@ int fke_qgemm_f8(const uint8_t* A, const uint8_t* B, void* C, int M, int N, int 
                  const float* bias, int out_dtype, int b_layout, void* stream) {
     return fke_qgemm_f8_on_path(FKE_PATH_AUTO, A, B, C, M, N, K, sa, sb, bias, out_dtype, b_layout,
                                 stream);
+}
+
+int fke_qgemm_i8_swiglu_on_path(int path, const int8_t* A, const int8_t* W, void* H, int M, int I, int K,
+                                const float* scale_a, const float* scale_b, float sa, float sb,
+                                const float* bias, int out_dtype, void* stream) {
+    if (!swiglu_args_ok(A, W, H, M, I, K, out_dtype)) return hipErrorInvalidValue;
+    return run_i8(path, make_swiglu_args(A, W, H, M, I, K, scale_a, scale_b, sa, sb, bias, out_dtype), stream);
+}
+
+int fke_qgemm_i8_swiglu(const int8_t* A, const int8_t* W, void* H, int M, int I, int K, const float* scale_a,
+                        const float* scale_b, float sa, float sb, const float* bias, int out_dtype,
+                        void* stream) {
+    return fke_qgemm_i8_swiglu_on_path(FKE_PATH_AUTO, A, W, H, M, I, K, scale_a, scale_b, sa, sb, bias,
+                                       out_dtype, stream);
+}
+
+int fke_select_path_i8_swiglu(const void* A, const void* W, const void* H, int M, int I, int K,
+                              int out_dtype) {
+    if (!swiglu_args_ok(A, W, H, M, I, K, out_dtype)) return -1;
+    return pick_i8(make_swiglu_args(A, W, const_cast<void*>(H), M, I, K, nullptr, nullptr, 1.f, 1.f, nullptr,
+                                    out_dtype));
+}
+
+int fke_swiglu(const void* gate, const void* up, void* out, int64_t n, int dtype, void* stream) {
+    if (!gate || !up || !out || n < 0) return hipErrorInvalidValue;
+    if (dtype != FKE_IN_F32 && dtype != FKE_IN_BF16 && dtype != FKE_IN_F16) return hipErrorInvalidValue;
+    if (n == 0) return hipSuccess;
+    return fke::launch_swiglu(gate, up, out, n, dtype, static_cast<hipStream_t>(stream));
 }
 
 int fke_select_path_i8(const void* A, const void* B, const void* C, int M, int N, int K,

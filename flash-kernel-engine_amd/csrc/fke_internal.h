@@ -24,6 +24,7 @@ struct GemmArgs {
     const float* bias;    // [N] or null
     int out_dtype;        // FKE_OUT_*
     int b_layout;         // FKE_B_*
+    int swiglu;           // 1: B is [gate; up] (N = 2I rows, NK), C is [M, I] = SwiGLU of the pairs
 };
 
 enum Elem { ELEM_I8 = 0, ELEM_F8 = 1 };
@@ -34,6 +35,8 @@ hipError_t launch_gemv_i8(const GemmArgs& p, hipStream_t stream);
 hipError_t launch_mfma(const GemmArgs& p, int elem, hipStream_t stream);
 hipError_t launch_quant_rows(const void* X, int in_dtype, int M, int K, int8_t* Q, float* S,
                              hipStream_t stream);
+hipError_t launch_swiglu(const void* gate, const void* up, void* out, int64_t n, int dtype,
+                         hipStream_t stream);
 
 // Shape/alignment predicates of the fast families (host side).
 bool gemv_i8_supports(const GemmArgs& p);
@@ -82,6 +85,16 @@ __device__ __forceinline__ uint32_t e4m3_sanitize(uint32_t w) {
 // Canonical fused epilogue: s = fp32(sa_m*sb_n); y = bias ? fma(v,s,bias) : v*s.
 __device__ __forceinline__ float epilogue_value(float v, float s, const float* bias, int n) {
     return bias ? __builtin_fmaf(v, s, bias[n]) : v * s;
+}
+
+// SwiGLU of one (gate, up) pair: (g * sigmoid(g)) * u with sigmoid(g) =
+// 1 / (1 + exp(-g)), in that order (reference src/fused_activations.cu:9-11,
+// :30-33).  exp is the device library's expf (within 1 ulp; the reference
+// uses the fast __expf) and the reciprocal is v_rcp_f32 (1 ulp).  exp(-g)
+// overflows to +inf for g < -88.7, which gives sigmoid = 0 and h = +-0.
+__device__ __forceinline__ float swiglu_pair(float g, float u) {
+    const float s = __builtin_amdgcn_rcpf(1.0f + expf(-g));
+    return (g * s) * u;
 }
 
 template <int OUT>

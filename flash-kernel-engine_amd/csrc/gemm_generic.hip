@@ -11,6 +11,11 @@
 // 64x64 output tile per 256-thread workgroup, 4x4 outputs per thread, K staged
 // through LDS 64 bytes at a time with bounds-checked byte loads (zero fill
 // past M/N/K adds exact zeros).
+//
+// SwiGLU (INT8, B = [gate; up] of 2I rows): a tile covers 32 outputs; its
+// B column c = 4t + j holds gate row o (j = 0, 1) or up row I + o (j = 2, 3)
+// of output o = n0 + 2t + (j & 1), so each thread's columns j and j + 2 are
+// the two operands of one output.
 #include "fke_internal.h"
 
 namespace fke {
@@ -19,12 +24,14 @@ namespace {
 constexpr int T = 64;   // tile edge
 constexpr int KC = 64;  // K bytes per LDS stage
 
-template <int ELEM, int OUT>
+template <int ELEM, int OUT, bool SWI = false>
 __global__ __launch_bounds__(256) void gemm_generic_kernel(GemmArgs p) {
+    static_assert(!SWI || (ELEM == ELEM_I8 && OUT != FKE_OUT_I32), "SwiGLU: INT8, float out");
     const int tid = threadIdx.x;
     const int tx = tid & 15, ty = tid >> 4;
-    const int m0 = blockIdx.y * T, n0 = blockIdx.x * T;
+    const int m0 = blockIdx.y * T, n0 = blockIdx.x * (SWI ? T / 2 : T);  // n0: first output column
     const int M = p.M, N = p.N, K = p.K;
+    const int NO = SWI ? N >> 1 : N;  // output columns
     const uint8_t* A = static_cast<const uint8_t*>(p.A);
     const uint8_t* B = static_cast<const uint8_t*>(p.B);
     const bool kn = p.b_layout == FKE_B_KN;
@@ -66,12 +73,18 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(GemmArgs p) {
                 bn = r;
                 bk = kq;
             }
-            const int n = n0 + bn;
+            int n = n0 + bn;  // B row (NK) / column (KN) of tile column bn
+            bool n_ok = n < N;
+            if constexpr (SWI) {
+                const int o = n0 + 2 * (bn >> 2) + (bn & 1);
+                n = (bn & 2) ? NO + o : o;
+                n_ok = o < NO;
+            }
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
                 const int k = k0 + bk + q;
                 uint8_t v = 0;
-                if (n < N && k < K)
+                if (n_ok && k < K)
                     v = kn ? B[static_cast<size_t>(k) * N + n] : B[static_cast<size_t>(n) * K + k];
                 b[q] = v;
             }
@@ -125,6 +138,25 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(GemmArgs p) {
         __syncthreads();
     }
 
+    if constexpr (SWI) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int m = m0 + ty * 4 + i;
+            if (m >= M) continue;
+            const float sam = p.scale_a ? p.scale_a[m] : p.sa;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int n = n0 + 2 * tx + j;
+                if (n >= NO) continue;
+                const float yg = epilogue_value(static_cast<float>(iacc[i][j]),
+                                                sam * (p.scale_b ? p.scale_b[n] : p.sb), p.bias, n);
+                const float yu = epilogue_value(static_cast<float>(iacc[i][j + 2]),
+                                                sam * (p.scale_b ? p.scale_b[NO + n] : p.sb), p.bias, NO + n);
+                store_out<OUT>(p.C, static_cast<size_t>(m) * NO + n, swiglu_pair(yg, yu), 0);
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int m = m0 + ty * 4 + i;
@@ -157,6 +189,15 @@ hipError_t launch_t(const GemmArgs& p, hipStream_t stream) {
 }  // namespace
 
 hipError_t launch_generic(const GemmArgs& p, int elem, hipStream_t s) {
+    if (p.swiglu) {
+        GemmArgs a = p;
+        void* args[] = {&a};
+        const dim3 grid((p.N / 2 + T / 2 - 1) / (T / 2), (p.M + T - 1) / T);
+        const void* f = p.out_dtype == FKE_OUT_F32
+            ? reinterpret_cast<const void*>(&gemm_generic_kernel<ELEM_I8, FKE_OUT_F32, true>)
+            : reinterpret_cast<const void*>(&gemm_generic_kernel<ELEM_I8, FKE_OUT_BF16, true>);
+        return hipLaunchKernel(f, grid, dim3(256), args, 0, s);
+    }
     if (elem == ELEM_I8) {
         switch (p.out_dtype) {
             case FKE_OUT_F32: return launch_t<ELEM_I8, FKE_OUT_F32>(p, s);

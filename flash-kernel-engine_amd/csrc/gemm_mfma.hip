@@ -112,14 +112,27 @@ __device__ __forceinline__ void tile_of(int bid, int gm, int gn, int& tm, int& t
     tn = in_group / gsize;
 }
 
+// Weight row held by column c (0..255) of a SwiGLU tile whose 128 outputs
+// start at column o0; B is [gate; up] with I = rows / 2.  Each wave's 128 B
+// columns are 64 gate columns then the 64 up columns of the same outputs, so
+// MFMA block j (gate) and block j + 2 (up) of a wave hold the two operands of
+// one output in the same lane.
+__device__ __forceinline__ int swiglu_b_row(int c, int o0, int I) {
+    const int jj = (c >> 5) & 3;
+    const int o = o0 + (c >> 7) * 64 + (jj & 1) * 32 + (c & 31);
+    return jj >= 2 ? I + o : o;
+}
+
 // Direct-to-LDS copy plan of one 256-row x 128-byte K-contiguous panel (A, or
 // B in [N,K] order).  Each wave issues PW loads of 1 KiB (8 rows x 128 B);
 // lane l lands at byte 16*l of its KiB, so it fetches the logical chunk that
 // the swizzle assigns to that physical slot.  Rows past `rows` re-read the
-// last valid row (their outputs are never stored).
+// last valid row (their outputs are never stored).  SWI: panel row r holds
+// weight row swiglu_b_row(r, row0, rows / 2).
 struct Panel {
     __amdgpu_buffer_rsrc_t rsrc;  // the whole operand, rows x ld bytes
     uint32_t off[PW];             // byte offset of this lane's 16-byte source at k = 0
+    template <bool SWI = false>
     __device__ void init(const int8_t* base, int ld, int row0, int rows, int wave, int lane) {
         rsrc = make_rsrc(base, rows * ld);
 #pragma unroll
@@ -127,7 +140,8 @@ struct Panel {
             const int seg = wave * PW + i;
             const int r = seg * 8 + (lane >> 3);
             const int lc = (lane & 7) ^ swz(r);
-            off[i] = static_cast<uint32_t>(min(row0 + r, rows - 1) * ld + lc * 16);
+            const int src = SWI ? swiglu_b_row(r, row0, rows >> 1) : row0 + r;
+            off[i] = static_cast<uint32_t>(min(src, rows - 1) * ld + lc * 16);
         }
     }
     // Load i of this wave for the stage at K byte k0 (uniform).
@@ -285,8 +299,13 @@ __device__ __forceinline__ void mfma_one(const Frags<ELEM>& f, typename Mma<ELEM
         acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.a[i], f.b[j], acc[i][j], 0, 0, 0, 0, 0, 0);
 }
 
-template <int ELEM, int BL, int OUT>
+// Output columns of one workgroup tile: 256, or 128 SwiGLU outputs (256 B rows).
+template <bool SWI>
+constexpr int tile_cols() { return SWI ? BN / 2 : BN; }
+
+template <int ELEM, int BL, int OUT, bool SWI>
 __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
+    static_assert(!SWI || (ELEM == ELEM_I8 && BL == FKE_B_NK && OUT != FKE_OUT_I32), "SwiGLU: INT8, B [N,K], float out");
     constexpr int NKS = Mma<ELEM>::KSTEPS;
     __shared__ __attribute__((aligned(1024))) uint8_t lds0[STAGE];
     __shared__ __attribute__((aligned(1024))) uint8_t lds1[STAGE];
@@ -301,10 +320,12 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
     const int wm = wave >> 1, wn = wave & 1;                     // wave's 128x128 block
 
     const int M = p.M, N = p.N, K = p.K;
-    const int gm = (M + BM - 1) / BM, gn = (N + BN - 1) / BN;
+    constexpr int TC = tile_cols<SWI>();
+    const int NO = SWI ? N >> 1 : N;  // output columns
+    const int gm = (M + BM - 1) / BM, gn = (NO + TC - 1) / TC;
     int tm, tn;
     tile_of(blockIdx.x, gm, gn, tm, tn);
-    const int m0 = tm * BM, n0 = tn * BN;
+    const int m0 = tm * BM, n0 = tn * TC;  // n0: first output column
 
     const int8_t* A = static_cast<const int8_t*>(p.A);
     const int8_t* B = static_cast<const int8_t*>(p.B);
@@ -312,7 +333,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
     // epilogue operands -> LDS (visible after the prologue barrier)
     {
         const int m = min(m0 + tid, M - 1);
-        const int n = min(n0 + tid, N - 1);
+        const int n = min(SWI ? swiglu_b_row(tid, n0, NO) : n0 + tid, N - 1);  // B row of tile column tid
         epi_sa[tid] = p.scale_a ? p.scale_a[m] : p.sa;
         epi_sb[tid] = p.scale_b ? p.scale_b[n] : p.sb;
         epi_bias[tid] = p.bias ? p.bias[n] : -0.0f;
@@ -334,7 +355,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
     BPanel pb;
     uint32_t kn_off[4][2] = {};
     if constexpr (BL == FKE_B_NK) {
-        pb.init(B, K, n0, N, wave, lane);
+        pb.template init<SWI>(B, K, n0, N, wave, lane);
     } else {
         pb.init(B, N, K, n0, wave, lane);
 #pragma unroll
@@ -481,9 +502,48 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
     // through L2.
     constexpr int OB = OUT == FKE_OUT_BF16 ? 2 : 4;  // output bytes per element
     const int lr = lane & 31, lh = lane >> 5;
-    const uint32_t row_bytes = static_cast<uint32_t>(N) * OB;
+    const uint32_t row_bytes = static_cast<uint32_t>(NO) * OB;
     const __amdgpu_buffer_rsrc_t rc = make_rsrc(static_cast<char*>(p.C) + static_cast<size_t>(m0) * row_bytes,
                                                 min(M - m0, BM) * static_cast<int>(row_bytes));
+    if constexpr (SWI) {
+        // SwiGLU: block j (gate) and j + 2 (up) of the wave hold output column
+        // n0 + 64*wn + 32*j + lane%32; h = swiglu_pair(g, u) of the two
+        // canonical epilogue values.
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int cg = wn * 128 + j * 32 + lr, cu = cg + 64;  // tile columns of the gate / up rows
+            const float sbg = epi_sb[cg], sbu = epi_sb[cu];
+            const float bg = epi_bias[cg], bu = epi_bias[cu];
+            const int o = n0 + wn * 64 + j * 32 + lr;
+            const uint32_t lane_off = o < NO
+                ? static_cast<uint32_t>(wm * 128 + 4 * lh) * row_bytes + static_cast<uint32_t>(o) * OB
+                : 0x80000000u;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                fence();
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int rm = wm * 128 + i * 32 + 8 * g + 4 * lh;
+                    const float4 sa4 = *reinterpret_cast<const float4*>(&epi_sa[rm]);
+                    const float sav[4] = {sa4.x, sa4.y, sa4.z, sa4.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int v = 4 * g + e;
+                        const int voff =
+                            static_cast<int>(lane_off + static_cast<uint32_t>(i * 32 + 8 * g + e) * row_bytes);
+                        const float yg = __builtin_fmaf(static_cast<float>(acc[i][j][v]), sav[e] * sbg, bg);
+                        const float yu = __builtin_fmaf(static_cast<float>(acc[i][j + 2][v]), sav[e] * sbu, bu);
+                        const float h = swiglu_pair(yg, yu);
+                        if constexpr (OUT == FKE_OUT_F32)
+                            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(h), rc, voff, 0, 2);
+                        else
+                            __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_rne(h), rc, voff, 0, 2);
+                    }
+                }
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int cn = wn * 128 + j * 32 + lr;  // column within the tile
@@ -524,12 +584,13 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
     }
 }
 
-template <int ELEM, int BL, int OUT>
+template <int ELEM, int BL, int OUT, bool SWI = false>
 hipError_t launch_t(const GemmArgs& p, hipStream_t stream) {
-    const int gm = (p.M + BM - 1) / BM, gn = (p.N + BN - 1) / BN;
+    constexpr int TC = tile_cols<SWI>();
+    const int gm = (p.M + BM - 1) / BM, gn = ((SWI ? p.N / 2 : p.N) + TC - 1) / TC;
     GemmArgs a = p;
     void* args[] = {&a};
-    return hipLaunchKernel(reinterpret_cast<const void*>(&gemm_mfma_kernel<ELEM, BL, OUT>),
+    return hipLaunchKernel(reinterpret_cast<const void*>(&gemm_mfma_kernel<ELEM, BL, OUT, SWI>),
                            dim3(gm * gn), dim3(NTHREADS), args, 0, stream);
 }
 
@@ -555,12 +616,16 @@ bool mfma_supports(const GemmArgs& p, int elem) {
     if (static_cast<int64_t>(p.M) * p.K > INT32_MAX) return false;
     if (static_cast<int64_t>(p.N) * p.K > INT32_MAX) return false;
     if (p.b_layout == FKE_B_KN && (p.N % 16 != 0)) return false;
+    if (p.swiglu && (elem != ELEM_I8 || p.b_layout != FKE_B_NK)) return false;
     // epilogue offsets are 32-bit: 256 output rows plus the 2^31 drop offset
     if (p.N > (1 << 20)) return false;
     return true;
 }
 
 hipError_t launch_mfma(const GemmArgs& p, int elem, hipStream_t s) {
+    if (p.swiglu)
+        return p.out_dtype == FKE_OUT_F32 ? launch_t<ELEM_I8, FKE_B_NK, FKE_OUT_F32, true>(p, s)
+                                          : launch_t<ELEM_I8, FKE_B_NK, FKE_OUT_BF16, true>(p, s);
     if (elem == ELEM_I8)
         return p.b_layout == FKE_B_NK ? launch_out<ELEM_I8, FKE_B_NK>(p, s)
                                       : launch_out<ELEM_I8, FKE_B_KN>(p, s);

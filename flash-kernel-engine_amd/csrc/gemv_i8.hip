@@ -149,14 +149,18 @@ constexpr int ROWS_WAVES = 2;  // waves (= B rows) per workgroup of gemv_rows_ke
 
 // FULLK: K is a multiple of 4096, so every 256-chunk block is whole: the
 // activation chunks come with plain loads and no offset needs the 2^31 guard.
-template <int MT, int OUT, bool FULLK>
+// SWI: B is [gate; up] (N = 2I rows); the wave streams gate row n and up row
+// I + n side by side and stores swiglu_pair of the two epilogue values.
+template <int MT, int OUT, bool FULLK, bool SWI = false>
 __global__ __launch_bounds__(ROWS_WAVES * 64) void gemv_rows_kernel(GemmArgs p) {
+    constexpr int NB = SWI ? 2 : 1;  // weight rows per wave
     const int lane = threadIdx.x & 63;
+    const int NO = SWI ? p.N >> 1 : p.N;  // output columns
     // Uniform per wave; readfirstlane keeps the row's buffer resource in
     // SGPRs.  A wave past the last row re-reads it and stores nothing, so
     // nothing stands between the kernel arguments and the first weight load.
     const int nw = __builtin_amdgcn_readfirstlane(blockIdx.x * ROWS_WAVES + (threadIdx.x >> 6));
-    const int n = min(nw, p.N - 1);
+    const int n = min(nw, NO - 1);
     const int M = p.M, K = p.K;
     const int ck = K >> 4;  // 16-byte chunks per row (K % 64 == 0)
     // B row n and the M activation rows through buffer resources: 32-bit
@@ -164,8 +168,12 @@ __global__ __launch_bounds__(ROWS_WAVES * 64) void gemv_rows_kernel(GemmArgs p) 
     // and chunks past the row end pointed at offset 2^31, which lies outside
     // every range and reads as zero - so the loop needs no guard.  Rows
     // m >= M of the MT-row template read row 0 (never stored).
-    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<int8_t*>(static_cast<const int8_t*>(p.B) + static_cast<size_t>(n) * K), 0, K, 0x00020000);
+    __amdgpu_buffer_rsrc_t rb[NB];
+#pragma unroll
+    for (int q = 0; q < NB; ++q)
+        rb[q] = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<int8_t*>(static_cast<const int8_t*>(p.B) + static_cast<size_t>(n + q * NO) * K), 0, K,
+            0x00020000);
     __amdgpu_buffer_rsrc_t ra[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m)
@@ -174,11 +182,17 @@ __global__ __launch_bounds__(ROWS_WAVES * 64) void gemv_rows_kernel(GemmArgs p) 
             0x00020000);
     // per-row epilogue operands: scalar loads (n is uniform) whose latency
     // hides behind the weight stream
-    const float sbn = p.scale_b ? p.scale_b[n] : p.sb;
-    const float biasn = p.bias ? p.bias[n] : 0.0f;
-    int32_t acc[MT];
+    float sbn[NB], biasn[NB];
 #pragma unroll
-    for (int m = 0; m < MT; ++m) acc[m] = 0;
+    for (int q = 0; q < NB; ++q) {
+        sbn[q] = p.scale_b ? p.scale_b[n + q * NO] : p.sb;
+        biasn[q] = p.bias ? p.bias[n + q * NO] : 0.0f;
+    }
+    int32_t acc[NB][MT];
+#pragma unroll
+    for (int q = 0; q < NB; ++q)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[q][m] = 0;
     const int nblk = (ck + 255) >> 8;  // blocks of 256 chunks (4 KiB of the row), the last one partial; >= 1
     int blk = 0;
     do {
@@ -188,9 +202,12 @@ __global__ __launch_bounds__(ROWS_WAVES * 64) void gemv_rows_kernel(GemmArgs p) 
             const int c = (blk << 8) + lane + 64 * u;
             off[u] = FULLK || c < ck ? c * 16 : static_cast<int>(0x80000000u);
         }
-        v4i a[MT][4], b[4];
+        v4i a[MT][4], b[NB][4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) b[u] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rb, off[u], 0, 2));
+        for (int q = 0; q < NB; ++q)
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                b[q][u] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rb[q], off[u], 0, 2));
 #pragma unroll
         for (int m = 0; m < MT; ++m)
 #pragma unroll
@@ -202,21 +219,31 @@ __global__ __launch_bounds__(ROWS_WAVES * 64) void gemv_rows_kernel(GemmArgs p) 
                     a[m][u] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(ra[m], off[u], 0, 0));
             }
 #pragma unroll
-        for (int m = 0; m < MT; ++m)
+        for (int q = 0; q < NB; ++q)
 #pragma unroll
-            for (int u = 0; u < 4; ++u) acc[m] = dot16(a[m][u], b[u], acc[m]);
+            for (int m = 0; m < MT; ++m)
+#pragma unroll
+                for (int u = 0; u < 4; ++u) acc[q][m] = dot16(a[m][u], b[q][u], acc[q][m]);
     } while (++blk < nblk);
-    int32_t tot[MT];
+    int32_t tot[NB][MT];
 #pragma unroll
-    for (int m = 0; m < MT; ++m) tot[m] = wave_sum(acc[m]);
+    for (int q = 0; q < NB; ++q)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) tot[q][m] = wave_sum(acc[q][m]);
     // lane m stores output row m (all lanes hold every total)
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
-        if (lane == m && m < M && nw < p.N) {
-            const float sc = (p.scale_a ? p.scale_a[m] : p.sa) * sbn;
-            const float y = p.bias ? __builtin_fmaf(static_cast<float>(tot[m]), sc, biasn)
-                                   : static_cast<float>(tot[m]) * sc;
-            store_out<OUT>(p.C, static_cast<size_t>(m) * p.N + n, y, tot[m]);
+        if (lane == m && m < M && nw < NO) {
+            const float sam = p.scale_a ? p.scale_a[m] : p.sa;
+            float y[NB];
+#pragma unroll
+            for (int q = 0; q < NB; ++q) {
+                const float sc = sam * sbn[q];
+                y[q] = p.bias ? __builtin_fmaf(static_cast<float>(tot[q][m]), sc, biasn[q])
+                              : static_cast<float>(tot[q][m]) * sc;
+            }
+            const float h = SWI ? swiglu_pair(y[0], y[NB - 1]) : y[0];
+            store_out<OUT>(p.C, static_cast<size_t>(m) * NO + n, h, tot[0][m]);
         }
     }
 }
@@ -237,12 +264,17 @@ __global__ __launch_bounds__(ROWS_WAVES * 64) void gemv_rows_kernel(GemmArgs p) 
 // Partials are summed over the KS waves through LDS (exact int32).
 constexpr int SK_CB = 2, SK_KS = 4, SK_T = 16;
 
-template <int OUT>
+// SWI: B is [gate; up] (N = 2I rows); column block 0 holds gate rows
+// n0..n0+15 and block 1 the up rows I+n0.., and each output is swiglu_pair of
+// the two epilogue values.
+template <int OUT, bool SWI = false>
 __global__ __launch_bounds__(SK_KS * 64) void gemv_mfma_kernel(GemmArgs p) {
+    static_assert(!SWI || SK_CB == 2, "SwiGLU pairs one gate and one up block");
     __shared__ int32_t red[SK_KS][SK_CB * 256];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int M = p.M, N = p.N, K = p.K;
-    const int n0 = blockIdx.x * SK_CB * 16;
+    const int NO = SWI ? N >> 1 : N;                       // output columns
+    const int n0 = blockIdx.x * (SWI ? 16 : SK_CB * 16);  // first output column
     const int steps = K >> 6, per = (steps + SK_KS - 1) / SK_KS;
     const int s0 = wave * per, s1 = min(s0 + per, steps);
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.A), 0, M * K, 0x00020000);
@@ -259,8 +291,9 @@ __global__ __launch_bounds__(SK_KS * 64) void gemv_mfma_kernel(GemmArgs p) {
             const int k = (s + t) * 64 + kq;
 #pragma unroll
             for (int c = 0; c < SK_CB; ++c)
-                b[c][t] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
-                                                      rb, ok ? (n0 + 16 * c + r16) * K + k : int(0x80000000u), 0, 2));
+                b[c][t] = __builtin_bit_cast(
+                    v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                             rb, ok ? ((SWI ? c * NO : 16 * c) + n0 + r16) * K + k : int(0x80000000u), 0, 2));
             a[t] = __builtin_bit_cast(
                 v4i, __builtin_amdgcn_raw_buffer_load_b128(ra, ok ? r16 * K + k : int(0x80000000u), 0, 0));
         }
@@ -274,6 +307,26 @@ __global__ __launch_bounds__(SK_KS * 64) void gemv_mfma_kernel(GemmArgs p) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) red[wave][c * 256 + (4 * (lane >> 4) + v) * 16 + r16] = acc[c][v];
     __syncthreads();
+    if constexpr (SWI) {
+        for (int o = tid; o < 256; o += SK_KS * 64) {
+            int32_t sg = 0, su = 0;
+#pragma unroll
+            for (int w = 0; w < SK_KS; ++w) {
+                sg += red[w][o];
+                su += red[w][256 + o];
+            }
+            const int m = o >> 4, n = n0 + (o & 15);
+            if (m < M && n < NO) {
+                const float sam = p.scale_a ? p.scale_a[m] : p.sa;
+                const float yg = epilogue_value(static_cast<float>(sg), sam * (p.scale_b ? p.scale_b[n] : p.sb),
+                                                p.bias, n);
+                const float yu = epilogue_value(static_cast<float>(su),
+                                                sam * (p.scale_b ? p.scale_b[NO + n] : p.sb), p.bias, NO + n);
+                store_out<OUT>(p.C, static_cast<size_t>(m) * NO + n, swiglu_pair(yg, yu), 0);
+            }
+        }
+        return;
+    }
     for (int o = tid; o < SK_CB * 256; o += SK_KS * 64) {
         int32_t sum = 0;
 #pragma unroll
@@ -290,8 +343,14 @@ __global__ __launch_bounds__(SK_KS * 64) void gemv_mfma_kernel(GemmArgs p) {
 hipError_t launch_mfma_skinny(const GemmArgs& p, hipStream_t stream) {
     GemmArgs a = p;
     void* args[] = {&a};
-    const dim3 grid((p.N + SK_CB * 16 - 1) / (SK_CB * 16));
     const void* f;
+    if (p.swiglu) {
+        const dim3 grid((p.N / 2 + 15) / 16);
+        f = p.out_dtype == FKE_OUT_F32 ? reinterpret_cast<const void*>(&gemv_mfma_kernel<FKE_OUT_F32, true>)
+                                       : reinterpret_cast<const void*>(&gemv_mfma_kernel<FKE_OUT_BF16, true>);
+        return hipLaunchKernel(f, grid, dim3(SK_KS * 64), args, 0, stream);
+    }
+    const dim3 grid((p.N + SK_CB * 16 - 1) / (SK_CB * 16));
     switch (p.out_dtype) {
         case FKE_OUT_F32: f = reinterpret_cast<const void*>(&gemv_mfma_kernel<FKE_OUT_F32>); break;
         case FKE_OUT_BF16: f = reinterpret_cast<const void*>(&gemv_mfma_kernel<FKE_OUT_BF16>); break;
@@ -304,8 +363,15 @@ template <int MT, bool FULLK>
 hipError_t launch_rows(const GemmArgs& p, hipStream_t stream) {
     GemmArgs a = p;
     void* args[] = {&a};
-    const dim3 grid((p.N + ROWS_WAVES - 1) / ROWS_WAVES);
     const void* f;
+    if (p.swiglu) {
+        const dim3 grid((p.N / 2 + ROWS_WAVES - 1) / ROWS_WAVES);
+        f = p.out_dtype == FKE_OUT_F32
+            ? reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_F32, FULLK, true>)
+            : reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_BF16, FULLK, true>);
+        return hipLaunchKernel(f, grid, dim3(ROWS_WAVES * 64), args, 0, stream);
+    }
+    const dim3 grid((p.N + ROWS_WAVES - 1) / ROWS_WAVES);
     switch (p.out_dtype) {
         case FKE_OUT_F32: f = reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_F32, FULLK>); break;
         case FKE_OUT_BF16: f = reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_BF16, FULLK>); break;
@@ -328,21 +394,39 @@ hipError_t launch_t(const GemmArgs& p, hipStream_t stream) {
     return hipLaunchKernel(f, grid, dim3(256), args, 0, stream);
 }
 
+// The skinny MFMA kernel addresses A and B with 32-bit buffer offsets,
+// computed for up to 16 activation rows and 32 weight rows past N.
+bool skinny_offsets_fit(const GemmArgs& p) {
+    return (static_cast<int64_t>(p.N < 16 ? 16 : p.N) + 32) * p.K <= INT32_MAX;
+}
+
+template <bool FULLK>
+hipError_t launch_rows_m(const GemmArgs& p, hipStream_t s) {
+    if (p.M <= 1) return launch_rows<1, FULLK>(p, s);
+    if (p.M <= 2) return launch_rows<2, FULLK>(p, s);
+    return launch_rows<4, FULLK>(p, s);
+}
+
 }  // namespace
 
 bool gemv_i8_supports(const GemmArgs& p) {
     const uintptr_t a = reinterpret_cast<uintptr_t>(p.A), b = reinterpret_cast<uintptr_t>(p.B);
-    return p.M >= 1 && p.M <= 16 && p.N >= 1 && p.K >= 64 && p.K % 64 == 0 &&
-           p.b_layout == FKE_B_NK && ((a | b) & 15) == 0;
+    if (!(p.M >= 1 && p.M <= 16 && p.N >= 1 && p.K >= 64 && p.K % 64 == 0 && p.b_layout == FKE_B_NK &&
+          ((a | b) & 15) == 0))
+        return false;
+    // SwiGLU pairs: the row kernel up to M = 4, the skinny MFMA kernel above
+    return !p.swiglu || p.M <= 4 || skinny_offsets_fit(p);
 }
 
 hipError_t launch_gemv_i8(const GemmArgs& p, hipStream_t s) {
+    if (p.swiglu) {
+        if (p.M <= 4) return p.K % 4096 == 0 ? launch_rows_m<true>(p, s) : launch_rows_m<false>(p, s);
+        return launch_mfma_skinny(p, s);
+    }
     if (p.M <= 1) return p.K % 4096 == 0 ? launch_rows<1, true>(p, s) : launch_rows<1, false>(p, s);
     if (p.M <= 2) return launch_t<2, 16>(p, s);
     if (p.M <= 4) return launch_t<4, 8>(p, s);
-    // the MFMA kernel addresses A and B with 32-bit buffer offsets, computed
-    // for up to 16 activation rows and 32 weight rows past N
-    if ((static_cast<int64_t>(p.N < 16 ? 16 : p.N) + 32) * p.K <= INT32_MAX) return launch_mfma_skinny(p, s);
+    if (skinny_offsets_fit(p)) return launch_mfma_skinny(p, s);
     if (p.M <= 8) return launch_t<8, 8>(p, s);
     return launch_t<16, 4>(p, s);
 }

@@ -1,5 +1,5 @@
 // torch_ext.cpp — torch C++ extension `flash_engine_hip`: the quantized GEMM
-// path in the binding idiom of reference python/bindings.cpp:101-140
+// path (and the SwiGLU it feeds) in the binding idiom of reference python/bindings.cpp:101-140
 // (TORCH_CHECKs on device / dtype / shape, a fresh output tensor, the current
 // stream, one `*_forward` function per op).  The reference module
 // (flash_engine_cuda) exposes no quantized GEMM; these are the entries its
@@ -109,6 +109,54 @@ std::vector<torch::Tensor> quantize_per_token_forward(torch::Tensor x) {
     return {q, s};
 }
 
+// Gate/up GEMM with SwiGLU in the epilogue: W [2I, K] = [gate; up], out [M, I].
+torch::Tensor quantized_gemm_int8_swiglu_forward(torch::Tensor A, torch::Tensor W,
+                                                 c10::optional<torch::Tensor> scale_a,
+                                                 c10::optional<torch::Tensor> scale_b,
+                                                 c10::optional<torch::Tensor> bias, at::ScalarType out_dtype,
+                                                 double sa, double sb) {
+    const auto dev = A.device();
+    check_dev(A, "A", at::kChar, dev);
+    check_dev(W, "W", at::kChar, dev);
+    TORCH_CHECK(A.dim() == 2 && W.dim() == 2, "A and W must be 2-D");
+    const int64_t M = A.size(0), K = A.size(1);
+    TORCH_CHECK(W.size(1) == K && W.size(0) % 2 == 0, "W must be [2I, K]");
+    const int64_t I = W.size(0) / 2;
+    TORCH_CHECK(out_dtype == at::kFloat || out_dtype == at::kBFloat16, "SwiGLU GEMM writes float32 or bfloat16");
+    const float* pa = vec_ptr(scale_a, "scale_a", M, dev);
+    const float* pb = vec_ptr(scale_b, "scale_b", 2 * I, dev);
+    const float* pbias = vec_ptr(bias, "bias", 2 * I, dev);
+    auto out = torch::empty({M, I}, A.options().dtype(out_dtype));
+    check_status(fke_qgemm_i8_swiglu(A.data_ptr<int8_t>(), W.data_ptr<int8_t>(), out.data_ptr(),
+                                     static_cast<int>(M), static_cast<int>(I), static_cast<int>(K), pa, pb,
+                                     static_cast<float>(sa), static_cast<float>(sb), pbias,
+                                     out_dtype == at::kFloat ? FKE_OUT_F32 : FKE_OUT_BF16, current_stream(A)),
+                 "fke_qgemm_i8_swiglu");
+    return out;
+}
+
+// Reference python/bindings.cpp:101-133 (fused_swiglu_forward): float32 and
+// float16 as there, bfloat16 added.
+torch::Tensor fused_swiglu_forward(torch::Tensor gate, torch::Tensor up) {
+    TORCH_CHECK(gate.is_cuda() && up.is_cuda(), "Inputs must be GPU tensors");
+    TORCH_CHECK(gate.sizes() == up.sizes(), "Gate and Up tensors must match shapes");
+    TORCH_CHECK(gate.scalar_type() == up.scalar_type(), "Gate and Up tensors must have one dtype");
+    TORCH_CHECK(gate.device() == up.device(), "Gate and Up tensors must be on one device");
+    TORCH_CHECK(gate.is_contiguous() && up.is_contiguous(), "Gate and Up tensors must be contiguous");
+    int code;
+    switch (gate.scalar_type()) {
+        case at::kFloat: code = FKE_IN_F32; break;
+        case at::kHalf: code = FKE_IN_F16; break;
+        case at::kBFloat16: code = FKE_IN_BF16; break;
+        default: TORCH_CHECK(false, "Unsupported tensor type for SwiGLU");
+    }
+    auto out = torch::empty_like(gate);
+    check_status(fke_swiglu(gate.data_ptr(), up.data_ptr(), out.data_ptr(), gate.numel(), code,
+                            current_stream(gate)),
+                 "fke_swiglu");
+    return out;
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
@@ -121,4 +169,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("scale_a"), py::arg("scale_b"), py::arg("bias") = py::none(), py::arg("out_dtype") = at::kFloat,
           py::arg("b_layout") = "kn");
     m.def("quantize_per_token_forward", &quantize_per_token_forward, "Per-token INT8 quantiser", py::arg("x"));
+    m.def("quantized_gemm_int8_swiglu_forward", &quantized_gemm_int8_swiglu_forward,
+          "W8A8 gate/up GEMM with SwiGLU fused into the epilogue", py::arg("A"), py::arg("W"),
+          py::arg("scale_a") = py::none(), py::arg("scale_b") = py::none(), py::arg("bias") = py::none(),
+          py::arg("out_dtype") = at::kBFloat16, py::arg("sa") = 1.0, py::arg("sb") = 1.0);
+    m.def("fused_swiglu_forward", &fused_swiglu_forward, "Fused SwiGLU", py::arg("gate"), py::arg("up"));
 }

@@ -16,7 +16,7 @@ LIB_PATH = os.path.join(_PKG, "lib", "libfke_qgemm.so")
 OUT_F32, OUT_BF16, OUT_I32 = 0, 1, 2
 B_NK, B_KN = 0, 1
 PATH_AUTO, PATH_GEMV, PATH_MFMA, PATH_GENERIC = 0, 1, 2, 3
-IN_F32, IN_BF16 = 0, 1
+IN_F32, IN_BF16, IN_F16 = 0, 1, 2
 HIP_SUCCESS, HIP_ERROR_INVALID_VALUE = 0, 1
 
 # Every exported symbol with its (argtypes, restype).
@@ -29,6 +29,10 @@ SIGNATURES = {
     "fke_qgemm_f8": ([_p, _p, _p, _i, _i, _i, _f, _f, _p, _i, _i, _p], _i),
     "fke_qgemm_f8_on_path": ([_i, _p, _p, _p, _i, _i, _i, _f, _f, _p, _i, _i, _p], _i),
     "fke_quantize_rows_i8": ([_p, _i, _i, _i, _p, _p, _p], _i),
+    "fke_swiglu": ([_p, _p, _p, ct.c_int64, _i, _p], _i),
+    "fke_qgemm_i8_swiglu": ([_p, _p, _p, _i, _i, _i, _p, _p, _f, _f, _p, _i, _p], _i),
+    "fke_qgemm_i8_swiglu_on_path": ([_i, _p, _p, _p, _i, _i, _i, _p, _p, _f, _f, _p, _i, _p], _i),
+    "fke_select_path_i8_swiglu": ([_p, _p, _p, _i, _i, _i, _i], _i),
     "fke_select_path_i8": ([_p, _p, _p, _i, _i, _i, _i, _i], _i),
     "fke_select_path_f8": ([_p, _p, _p, _i, _i, _i, _i, _i], _i),
     "fke_print_device_info": ([_i], _i),

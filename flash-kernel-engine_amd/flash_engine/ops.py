@@ -168,6 +168,66 @@ def w8a8_linear(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tenso
                      b_layout="nk")
 
 
+def w8a8_swiglu(A: torch.Tensor, W: torch.Tensor, scale_a=None, scale_b=None, bias=None,
+                out_dtype=torch.bfloat16, sa: float = 1.0, sb: float = 1.0, path: str = "auto",
+                out: torch.Tensor | None = None) -> torch.Tensor:
+    """Gate/up projection with SwiGLU fused into the GEMM epilogue.
+
+    W is the merged int8 weight [2I, K]: rows 0..I-1 project the gate, rows
+    I..2I-1 the up branch (nn.Linear layout).  With the `w8a8_gemm` epilogue
+    g = y(A, W[n]) and u = y(A, W[I+n]) (scale_b / bias [2I], indexed by
+    weight row), out[m, n] = (g * sigmoid(g)) * u for n < I, fp32 or bf16
+    [M, I]; equal to `fused_swiglu` of the two fp32 GEMM outputs.
+    """
+    dev = A.device
+    _check_dev("A", A, torch.int8, dev)
+    _check_dev("W", W, torch.int8, dev)
+    if A.dim() != 2 or W.dim() != 2:
+        raise ValueError("A and W must be 2-D")
+    M, K = A.shape
+    if W.shape[1] != K or W.shape[0] % 2:
+        raise ValueError(f"W must be [2I, {K}], got {tuple(W.shape)}")
+    I = W.shape[0] // 2
+    _check_vec("scale_a", scale_a, M, dev)
+    _check_vec("scale_b", scale_b, 2 * I, dev)
+    _check_vec("bias", bias, 2 * I, dev)
+    if out_dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError("the SwiGLU GEMM writes fp32 or bf16")
+    if out is None:
+        out = torch.empty((M, I), dtype=out_dtype, device=dev)
+    else:
+        _check_dev("out", out, out_dtype, dev)
+        if tuple(out.shape) != (M, I):
+            raise ValueError("out has the wrong shape")
+    st = _lib.lib().fke_qgemm_i8_swiglu_on_path(
+        _PATHS[path], A.data_ptr(), W.data_ptr(), out.data_ptr(), M, I, K, _ptr(scale_a), _ptr(scale_b),
+        sa, sb, _ptr(bias), _OUT_CODES[out_dtype], _stream(A))
+    _lib.check(st, "fke_qgemm_i8_swiglu")
+    return out
+
+
+def w8a8_gate_up_swiglu(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor, bias=None,
+                        out_dtype=torch.bfloat16) -> torch.Tensor:
+    """The gate/up half of a SwiGLU MLP in W8A8: x [M,K] fp32/bf16 is quantised
+    per token, then one launch computes silu(x W_gate^T) * (x W_up^T) from the
+    merged weight [2I, K] with per-channel scales weight_scale [2I]."""
+    q, sa = quantize_per_token(x)
+    return w8a8_swiglu(q, weight, scale_a=sa, scale_b=weight_scale, bias=bias, out_dtype=out_dtype)
+
+
+def fused_swiglu(gate, up):
+    """(gate * sigmoid(gate)) * up, elementwise (reference python/flash_engine/ops.py:218-230,
+    src/fused_activations.cu).  float32, float16 or bfloat16 GPU tensors of one
+    shape; computed in fp32 and rounded once to the input type.  numpy inputs
+    are copied to cuda:0 and the result returned as numpy."""
+    host = isinstance(gate, np.ndarray)
+    if host:
+        gate = torch.from_numpy(np.ascontiguousarray(gate)).cuda()
+        up = torch.from_numpy(np.ascontiguousarray(up)).cuda()
+    out = _ext.ext().fused_swiglu_forward(gate.contiguous(), up.contiguous())
+    return out.cpu().numpy() if host else out
+
+
 def quantized_gemm_int8(A, B, scale_a: float = 1.0, scale_b: float = 1.0):
     """C = (A_int8 @ B_int8) * (scale_a * scale_b), B stored [K,N], fp32 out.
 

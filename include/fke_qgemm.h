@@ -37,10 +37,12 @@ enum fke_b_layout {
     FKE_B_KN = 1  /* B[k*N + n] */
 };
 
-/* Element type of the activations given to the quantiser. */
+/* Element type of floating-point activations (quantiser input: F32, BF16;
+ * elementwise SwiGLU: all three). */
 enum fke_in_dtype {
     FKE_IN_F32 = 0,  /* fp32 */
-    FKE_IN_BF16 = 1  /* bf16 */
+    FKE_IN_BF16 = 1, /* bf16 */
+    FKE_IN_F16 = 2   /* IEEE fp16 */
 };
 
 /* Kernel family used by a call (for tests and benchmarks). */
@@ -129,12 +131,47 @@ int fke_qgemm_f8_on_path(int path, const uint8_t* A, const uint8_t* B, void* C,
 int fke_quantize_rows_i8(const void* X, int in_dtype, int M, int K, int8_t* Q, float* scale,
                          void* stream);
 
+/*
+ * Elementwise SwiGLU, drop-in for flash_engine::activation::launch_fused_swiglu_fp32
+ * / _fp16 (reference include/fused_activations.cuh:11-25, src/fused_activations.cu:17-118),
+ * with bf16 added:
+ *   out[i] = (g * sigmoid(g)) * u,  sigmoid(g) = 1 / (1 + exp(-g)),
+ * computed in fp32 from g = gate[i], u = up[i] and rounded to the element type
+ * (dtype: enum fke_in_dtype) to nearest even.  n elements, device buffers (out
+ * may alias gate or up).  exp within 1 ulp, reciprocal within 1 ulp.  Rejects
+ * NULL pointers, n < 0 and bad dtypes; n == 0 launches nothing.
+ */
+int fke_swiglu(const void* gate, const void* up, void* out, int64_t n, int dtype, void* stream);
+
+/*
+ * W8A8 gate/up projection with SwiGLU fused into the GEMM epilogue (fuses
+ * reference src/fused_activations.cu:17-35 behind the quantized GEMM; no
+ * single reference call).  W is the merged weight [2I, K] int8 row-major (the
+ * B [N,K] layout): rows 0..I-1 are the gate projection, rows I..2I-1 the up
+ * projection.  With epi() the fke_qgemm_i8 epilogue (fp32 y):
+ *   g = epi(A . W[n]),   using scale_b[n],   bias[n]
+ *   u = epi(A . W[I+n]), using scale_b[I+n], bias[I+n]
+ *   H[m,n] = (g * sigmoid(g)) * u   as in fke_swiglu, for n < I
+ * H is [M, I], fp32 or bf16 (out_dtype).  scale_b and bias are [2I] or NULL;
+ * scale_a [M] or NULL.  Equals fke_swiglu applied to the two fp32 GEMM
+ * outputs, bit for bit.  Rejects I < 1, 2I > INT32_MAX and FKE_OUT_I32.
+ */
+int fke_qgemm_i8_swiglu(const int8_t* A, const int8_t* W, void* H, int M, int I, int K,
+                        const float* scale_a, const float* scale_b, float sa, float sb,
+                        const float* bias, int out_dtype, void* stream);
+
+int fke_qgemm_i8_swiglu_on_path(int path, const int8_t* A, const int8_t* W, void* H, int M, int I,
+                                int K, const float* scale_a, const float* scale_b, float sa,
+                                float sb, const float* bias, int out_dtype, void* stream);
+
 /* The family fke_qgemm_i8 / fke_qgemm_f8 would pick (enum fke_path), or -1
  * for arguments they would reject.  Pure host logic; needs no GPU. */
 int fke_select_path_i8(const void* A, const void* B, const void* C, int M, int N, int K,
                        int out_dtype, int b_layout);
 int fke_select_path_f8(const void* A, const void* B, const void* C, int M, int N, int K,
                        int out_dtype, int b_layout);
+int fke_select_path_i8_swiglu(const void* A, const void* W, const void* H, int M, int I, int K,
+                              int out_dtype);
 
 /* Replaces flash_engine::print_device_info (reference include/flash_engine.h:29,
  * src/flash_engine_api.cu:7-27): prints the device's properties to stdout. */

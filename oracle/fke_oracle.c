@@ -339,3 +339,35 @@ void fko_quantize_rows_i8(const void* x, int in_dtype, int M, int K, int8_t* q, 
         }
     }
 }
+
+/* src/fused_activations.cu:9-11 (fast_sigmoid) and :30-33 / :48 (the pair).
+ * Built with -ffp-contract=off: every operation rounds once, as written. */
+float fko_swiglu1(float g, float u) {
+    const float s = 1.0f / (1.0f + expf(-g));
+    return (g * s) * u;
+}
+
+void fko_swiglu_f32(const float* g, const float* u, float* h, size_t n) {
+    for (size_t i = 0; i < n; ++i) h[i] = fko_swiglu1(g[i], u[i]);
+}
+
+void fko_w8a8_swiglu(const int8_t* A, const int8_t* W, void* out, int M, int I, int K,
+                     const float* scale_a, const float* scale_b, float sa, float sb,
+                     const float* bias, int out_dtype, const int* rows, int nrows, int nthreads) {
+    const int R = rows ? nrows : M;
+    const int N = 2 * I;
+    int32_t* acc = (int32_t*)malloc((size_t)R * N * sizeof(int32_t));
+    if (!acc) return;
+    fko_w8a8_acc(A, W, acc, M, N, K, FKO_B_NK, rows, nrows, nthreads);
+    for (int r = 0; r < R; ++r) {
+        const int m = rows ? rows[r] : r;
+        const float am = scale_a ? scale_a[m] : sa;
+        for (int n = 0; n < I; ++n) {
+            const int32_t* a = acc + (size_t)r * N;
+            const float g = epi((float)a[n], am * (scale_b ? scale_b[n] : sb), bias, n);
+            const float u = epi((float)a[I + n], am * (scale_b ? scale_b[I + n] : sb), bias, I + n);
+            store_out(out, (size_t)r * I + n, out_dtype, fko_swiglu1(g, u), 0);
+        }
+    }
+    free(acc);
+}

@@ -24,6 +24,12 @@
  *   fko_quantize_rows_i8      hand-derived rows (ties to even, exact scales),
  *                             invariants (the amax element maps to +-127,
  *                             |q*s - x| <= s/2), brute force in exact rationals.
+ *   fko_swiglu1 / _f32        the reference test's vector (python/tests/
+ *                             test_correctness.py:166-176), float64 closed
+ *                             form over a sweep, silu(g) - silu(-g) = g,
+ *                             exact special values (g = 0, saturation).
+ *   fko_w8a8_swiglu           equals fko_w8a8_gemm on the gate rows and on the
+ *                             up rows followed by fko_swiglu_f32, bit for bit.
  */
 #ifndef FKE_ORACLE_H
 #define FKE_ORACLE_H
@@ -94,6 +100,22 @@ float fko_quantize_e4m3(const float* x, uint8_t* q, size_t n);
  * q = clamp(rne(fp32(x*r)), -127, 127), NaN -> 0; scale[m] = s.
  * x is fp32 (in_dtype 0) or bf16 bits (in_dtype 1), [M,K]. */
 void fko_quantize_rows_i8(const void* x, int in_dtype, int M, int K, int8_t* q, float* scale);
+
+/* SwiGLU of one pair, src/fused_activations.cu:9-11,30-33:
+ * (g * sigmoid(g)) * u with sigmoid(g) = 1 / (1 + exp(-g)), fp32, in that
+ * order (the reference's __expf is a fast approximation; here expf and the
+ * division are the C library's / IEEE, so this is the function's value within
+ * about one ulp). */
+float fko_swiglu1(float g, float u);
+/* elementwise over n fp32 pairs (src/fused_activations.cu:17-83) */
+void fko_swiglu_f32(const float* g, const float* u, float* h, size_t n);
+/* W8A8 gate/up GEMM with SwiGLU (no reference counterpart as one call): W is
+ * [2I, K] (rows 0..I-1 gate, I..2I-1 up); g, u = canonical epilogue values of
+ * rows n and I+n (scale_b / bias indexed the same way, [2I] or NULL);
+ * out[r, n] = fko_swiglu1(g, u) as f32 or bf16_rne, [nrows or M, I]. */
+void fko_w8a8_swiglu(const int8_t* A, const int8_t* W, void* out, int M, int I, int K,
+                     const float* scale_a, const float* scale_b, float sa, float sb,
+                     const float* bias, int out_dtype, const int* rows, int nrows, int nthreads);
 
 #ifdef __cplusplus
 }

@@ -70,6 +70,12 @@ def _declare(L):
     L.fko_quantize_rows_i8.argtypes = [_p, _i, _i, _i, _p, _p]
     L.fko_quantize_rows_i8.restype = None
     L.fko_quantize_e4m3.restype = _f
+    L.fko_swiglu1.argtypes = [_f, _f]
+    L.fko_swiglu1.restype = _f
+    L.fko_swiglu_f32.argtypes = [_p, _p, _p, _sz]
+    L.fko_swiglu_f32.restype = None
+    L.fko_w8a8_swiglu.argtypes = [_p, _p, _p, _i, _i, _i, _p, _p, _f, _f, _p, _i, _p, _i, _i]
+    L.fko_w8a8_swiglu.restype = None
 
 
 def _ptr(a):
@@ -239,3 +245,30 @@ def quantize_rows_i8(x, in_dtype: int = IN_F32) -> tuple[np.ndarray, np.ndarray]
     s = np.empty(M, dtype=np.float32)
     lib().fko_quantize_rows_i8(_ptr(x), in_dtype, M, K, _ptr(q), _ptr(s))
     return q, s
+
+
+# ---- SwiGLU --------------------------------------------------------------------
+
+def swiglu_f32(gate, up) -> np.ndarray:
+    """src/fused_activations.cu:9-35: (g * sigmoid(g)) * u elementwise, fp32."""
+    g = _c(gate, np.float32); u = _c(up, np.float32)
+    assert g.shape == u.shape
+    h = np.empty_like(g)
+    lib().fko_swiglu_f32(_ptr(g), _ptr(u), _ptr(h), g.size)
+    return h
+
+
+def w8a8_swiglu(A, W, scale_a=None, scale_b=None, sa: float = 1.0, sb: float = 1.0, bias=None,
+                out_dtype: int = OUT_F32, rows=None, nthreads: int = 0) -> np.ndarray:
+    """W8A8 gate/up GEMM + SwiGLU: W is [2I, K] (gate rows, then up rows); out [R, I]."""
+    A = _c(A, np.int8); W = _c(W, np.int8)
+    M, K = A.shape
+    I = W.shape[0] // 2
+    r = None if rows is None else np.ascontiguousarray(rows, dtype=np.int32)
+    R = M if r is None else r.size
+    out = np.empty((R, I), dtype=np.float32 if out_dtype == OUT_F32 else np.uint16)
+    sa_arr, sb_arr, b_arr = _c(scale_a, np.float32), _c(scale_b, np.float32), _c(bias, np.float32)
+    nt = nthreads or (os.cpu_count() or 1)
+    lib().fko_w8a8_swiglu(_ptr(A), _ptr(W), _ptr(out), M, I, K, _ptr(sa_arr), _ptr(sb_arr), sa, sb,
+                          _ptr(b_arr), out_dtype, _ptr(r), 0 if r is None else r.size, nt)
+    return out

@@ -74,6 +74,42 @@ def test_quantizer_rejects_bad_arguments():
         assert q(P, dt, 4, 8, P, P, None) == INVALID
 
 
+def test_swiglu_rejects_bad_arguments():
+    L = _lib.lib()
+    sw = L.fke_swiglu
+    assert sw(None, P, P, 16, 0, None) == INVALID
+    assert sw(P, None, P, 16, 0, None) == INVALID
+    assert sw(P, P, None, 16, 0, None) == INVALID
+    assert sw(P, P, P, -1, 0, None) == INVALID
+    for dt in (-1, 3):
+        assert sw(P, P, P, 16, dt, None) == INVALID
+    assert sw(P, P, P, 0, 0, None) == _lib.HIP_SUCCESS  # nothing to do, nothing launched
+    g = L.fke_qgemm_i8_swiglu
+    assert g(None, P, P, 4, 8, 64, None, None, 1.0, 1.0, None, 0, None) == INVALID
+    assert g(P, P, None, 4, 8, 64, None, None, 1.0, 1.0, None, 0, None) == INVALID
+    for M, I, K in [(0, 8, 64), (4, 0, 64), (4, 8, 0), (4, 1 << 30, 64)]:
+        assert g(P, P, P, M, I, K, None, None, 1.0, 1.0, None, 0, None) == INVALID
+    assert g(P, P, P, 4, 8, 64, None, None, 1.0, 1.0, None, _lib.OUT_I32, None) == INVALID
+    assert L.fke_qgemm_i8_swiglu_on_path(_lib.PATH_GEMV, P, P, P, 17, 64, 4096, None, None, 1.0, 1.0,
+                                         None, 0, None) == INVALID
+    assert L.fke_qgemm_i8_swiglu_on_path(_lib.PATH_MFMA, P, P, P, 64, 64, 100, None, None, 1.0, 1.0,
+                                         None, 0, None) == INVALID
+
+
+@pytest.mark.parametrize("M,I,K,expect", [
+    (1, 14336, 4096, _lib.PATH_GEMV),
+    (3, 14336, 4096, _lib.PATH_GEMV),
+    (16, 14336, 4096, _lib.PATH_GEMV),
+    (17, 14336, 4096, _lib.PATH_MFMA),
+    (4096, 14336, 4096, _lib.PATH_MFMA),
+    (64, 64, 100, _lib.PATH_GENERIC),
+    (2, 300000, 4096, _lib.PATH_GEMV),     # row kernel: 64-bit row bases
+    (8, 300000, 4096, _lib.PATH_GENERIC),  # 2I*K past the 32-bit offsets of the MFMA kernels
+])
+def test_dispatch_i8_swiglu(M, I, K, expect):
+    assert _lib.lib().fke_select_path_i8_swiglu(P, P, P, M, I, K, 0) == expect
+
+
 def test_dropin_int8_rejects_k_not_multiple_of_4():
     """The reference kernel silently drops the K tail and misaligns rows when
     K % 4 != 0 (src/quantized_gemm.cu:28-30); the drop-in rejects it."""
@@ -131,11 +167,12 @@ def test_dropin_header_program_host_checks():
 
 
 def test_torch_extension_loads_and_binds_the_ops():
-    """The torch extension (bindings.cpp idiom) imports and exposes its three
+    """The torch extension (bindings.cpp idiom) imports and exposes its
     entries; it links libfke_qgemm.so, whose exports are checked above."""
     from flash_engine import _ext
     m = _ext.ext()
-    for name in ("quantized_gemm_int8_forward", "fp8_gemm_scaled_forward", "quantize_per_token_forward"):
+    for name in ("quantized_gemm_int8_forward", "fp8_gemm_scaled_forward", "quantize_per_token_forward",
+                 "quantized_gemm_int8_swiglu_forward", "fused_swiglu_forward"):
         assert hasattr(m, name), name
 
 
@@ -148,3 +185,7 @@ def test_torch_extension_rejects_host_tensors():
         m.quantized_gemm_int8_forward(a, a)
     with pytest.raises(RuntimeError, match="GPU tensor"):
         m.quantize_per_token_forward(torch.zeros((4, 8)))
+    with pytest.raises(RuntimeError, match="GPU tensors"):
+        m.fused_swiglu_forward(torch.zeros(8), torch.zeros(8))
+    with pytest.raises(RuntimeError, match="GPU tensor"):
+        m.quantized_gemm_int8_swiglu_forward(a, a)

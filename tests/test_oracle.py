@@ -384,3 +384,96 @@ def test_quantize_rows_bf16_input(oracle):
     qb, sb = oracle.quantize_rows_i8(bits, oracle.IN_BF16)
     qf, sf = oracle.quantize_rows_i8(xb)
     assert np.array_equal(qb, qf) and np.array_equal(sb, sf)
+
+
+# ---------------------------------------------------------------- SwiGLU
+
+def test_swiglu_reference_test_vector(oracle):
+    """The reference's own check (python/tests/test_correctness.py:166-176):
+    gate [-2,-0.5,0,0.5,2], up [1..5], against numpy fp32
+    (gate / (1 + exp(-gate))) * up, max abs difference < 1e-6."""
+    gate = np.array([-2.0, -0.5, 0.0, 0.5, 2.0], dtype=np.float32)
+    up = np.array([1.0, 2.0, 3.0, 4.0, 5.0], dtype=np.float32)
+    ref = (gate / (np.float32(1.0) + np.exp(-gate))) * up
+    out = oracle.swiglu_f32(gate, up)
+    assert np.max(np.abs(out - ref)) < 1e-6
+
+
+def test_swiglu_float64_closed_form_sweep(oracle):
+    """Against g*u/(1+e^-g) in float64 over g in [-90, 90]: within 4 fp32 ulps
+    of the exact value wherever sigmoid(g) and the result are normal numbers
+    (g > -87: below that 1/(1+e^-g) leaves the normal range and e^-g overflows
+    fp32 past -88.7, so the fp32 formula flushes towards zero - there |h| is
+    checked to be tiny).  A sign slip (e^+g), a dropped factor (silu without
+    u, sigmoid without g) or a wrong operand order is off by far more."""
+    r = rng(31)
+    g = np.concatenate([np.linspace(-90, 90, 20001), r.standard_normal(5000) * 4]).astype(np.float32)
+    u = (r.standard_normal(g.size) * 2).astype(np.float32)
+    h = oracle.swiglu_f32(g, u).astype(np.float64)
+    g64, u64 = g.astype(np.float64), u.astype(np.float64)
+    exact = g64 * u64 / (1.0 + np.exp(-g64))
+    tiny = float(np.finfo(np.float32).tiny)
+    inr = g > -87.0
+    normal = inr & (np.abs(exact) >= tiny)
+    ulp = np.spacing(np.abs(exact[normal]).astype(np.float32)).astype(np.float64)
+    assert np.all(np.abs(h[normal] - exact[normal]) <= 4 * ulp)
+    sub = inr & ~normal  # subnormal results: a few steps of 2^-149
+    assert np.all(np.abs(h[sub] - exact[sub]) <= 8 * 2.0**-149 + 4 * 2.0**-23 * np.abs(exact[sub]))
+    low = ~inr           # sigmoid(g) <= e^g < 2^-125
+    assert np.all(np.abs(h[low]) <= np.abs(g64 * u64)[low] * 2.0**-124)
+
+
+def test_swiglu_odd_part_identity(oracle):
+    """silu(g) - silu(-g) = g(sigmoid(g) + sigmoid(-g)) = g exactly in real
+    arithmetic; with u = 1 the fp32 values agree to a few ulps of |g|."""
+    g = np.linspace(-20, 20, 4001).astype(np.float32)
+    one = np.ones_like(g)
+    d = oracle.swiglu_f32(g, one).astype(np.float64) - oracle.swiglu_f32(-g, one).astype(np.float64)
+    assert np.all(np.abs(d - g.astype(np.float64)) <= 4 * np.spacing(np.abs(g)).astype(np.float64) + 1e-30)
+
+
+def test_swiglu_special_values(oracle):
+    """g = 0 gives 0 (sigmoid(0) = 1/2 exactly); g = 100 gives g*u exactly
+    (e^-100 < 2^-24, so 1 + e^-100 rounds to 1); g = -100 overflows e^100 to
+    inf and gives a signed zero; the pair order is (gate, up): swapping them
+    changes the value."""
+    assert oracle.lib().fko_swiglu1(0.0, 7.0) == 0.0
+    assert oracle.lib().fko_swiglu1(1.0, 0.0) == 0.0
+    assert oracle.lib().fko_swiglu1(100.0, 3.0) == 300.0
+    v = oracle.lib().fko_swiglu1(-100.0, 3.0)
+    assert v == 0.0 and math.copysign(1.0, v) == -1.0
+    # sigmoid(ln 3) = 3/4: h = 0.75 * ln3 * u up to the rounding of ln 3 itself
+    g = np.float32(math.log(3.0))
+    assert abs(oracle.lib().fko_swiglu1(float(g), 2.0) - 1.5 * float(g)) <= 2e-7 * 1.5 * float(g)
+    assert oracle.lib().fko_swiglu1(2.0, 0.5) != oracle.lib().fko_swiglu1(0.5, 2.0)
+
+
+def test_w8a8_swiglu_is_gemm_then_swiglu(oracle):
+    """The fused oracle equals the pinned GEMM oracle on W's gate rows
+    (0..I-1) and up rows (I..2I-1), each with its own slice of scale_b and
+    bias, followed by the pinned elementwise SwiGLU: bit for bit, in fp32 and
+    bf16, for all rows and a row subset.  Swapping the halves, indexing
+    scale_b / bias by the output column for the up rows, or applying SwiGLU
+    to bf16-rounded values fails."""
+    r = rng(32)
+    M, I, K = 9, 37, 72
+    A = r.integers(-127, 128, (M, K), dtype=np.int8)
+    W = r.integers(-127, 128, (2 * I, K), dtype=np.int8)
+    sa = r.uniform(0.001, 0.02, M).astype(np.float32)
+    sb = r.uniform(0.001, 0.02, 2 * I).astype(np.float32)
+    bias = (r.standard_normal(2 * I) * 0.5).astype(np.float32)
+    for b in (None, bias):
+        g = oracle.w8a8_gemm(A, W[:I], sa, sb[:I], bias=None if b is None else b[:I])
+        u = oracle.w8a8_gemm(A, W[I:], sa, sb[I:], bias=None if b is None else b[I:])
+        h = oracle.swiglu_f32(g, u)
+        fused = oracle.w8a8_swiglu(A, W, sa, sb, bias=b)
+        assert np.array_equal(fused.view(np.uint32), h.view(np.uint32))
+        fb = oracle.w8a8_swiglu(A, W, sa, sb, bias=b, out_dtype=oracle.OUT_BF16)
+        hb = np.array([oracle.f32_to_bf16_rne(float(v)) for v in h.ravel()], dtype=np.uint16).reshape(h.shape)
+        assert np.array_equal(fb, hb)
+        rows = np.array([8, 0, 3], dtype=np.int32)
+        assert np.array_equal(oracle.w8a8_swiglu(A, W, sa, sb, bias=b, rows=rows), fused[rows])
+    # scalar scales
+    g = oracle.w8a8_gemm(A, W[:I], sa=0.5, sb=0.25)
+    u = oracle.w8a8_gemm(A, W[I:], sa=0.5, sb=0.25)
+    assert np.array_equal(oracle.w8a8_swiglu(A, W, sa=0.5, sb=0.25), oracle.swiglu_f32(g, u))
