@@ -8,7 +8,7 @@ over 8 distinct 56 MiB buffers so the 256 MiB MALL cannot hold them) is timed in
 the same run and reported under "decode_gemv".  Inputs are random (torch RNG on
 the device), never zero-filled.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--extra] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--extra | --swiglu] [--no-cpu]
 """
 import argparse
 import json
@@ -53,6 +53,7 @@ def parse():
     ap.add_argument("--gemv-buffers", type=int, default=8)
     ap.add_argument("--gemv-launches", type=int, default=400)
     ap.add_argument("--extra", action="store_true", help="also time configs 2 and 4 and GEMV M=4,16")
+    ap.add_argument("--swiglu", action="store_true", help="also time the SwiGLU configs (part of --extra)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -151,6 +152,8 @@ def main():
         del src, dst
     if args.extra:
         line["extra"] = extra_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args)
+    elif args.swiglu:
+        line["extra"] = swiglu_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(line), flush=True)
@@ -285,6 +288,84 @@ def extra_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
                                            "frac": round(gbs / PEAK_HBM_GBS, 4), "bytes": nbytes,
                                            "kernel": "quant_rows_kernel<bf16>"}
     del Xs, Q, S
+    res.update(swiglu_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args))
+    return res
+
+
+def swiglu_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
+    """The MLP gate/up projection of a Llama-3-8B-shaped layer (K = 4096,
+    I = 14336) with SwiGLU fused into the GEMM epilogue, against the unfused
+    pipeline (two GEMMs to bf16, then the elementwise op), plus the elementwise
+    op alone and the decode (M = 1) fused kernel."""
+    res = {}
+    sh = torch.cuda.current_stream(dev).cuda_stream
+    M, I, K = 4096, 14336, 4096
+    A, W, sa, sb = rand_i8(M, K), rand_i8(2 * I, K), rand_u(M), rand_u(2 * I)
+    H = torch.empty((M, I), dtype=torch.bfloat16, device=dev)
+    G = torch.empty((M, I), dtype=torch.bfloat16, device=dev)
+    U = torch.empty((M, I), dtype=torch.bfloat16, device=dev)
+    ms = timed(lambda: L.fke_qgemm_i8_swiglu(A.data_ptr(), W.data_ptr(), H.data_ptr(), M, I, K, sa.data_ptr(),
+                                             sb.data_ptr(), 1.0, 1.0, None, _lib.OUT_BF16, sh),
+               args.steps, args.warmup)
+    Wu = W[I:]
+    sbu = sb[I:]
+
+    def unfused():
+        L.fke_qgemm_i8(A.data_ptr(), W.data_ptr(), G.data_ptr(), M, I, K, sa.data_ptr(), sb.data_ptr(), 1.0, 1.0,
+                       None, _lib.OUT_BF16, _lib.B_NK, sh)
+        L.fke_qgemm_i8(A.data_ptr(), Wu.data_ptr(), U.data_ptr(), M, I, K, sa.data_ptr(), sbu.data_ptr(), 1.0,
+                       1.0, None, _lib.OUT_BF16, _lib.B_NK, sh)
+        L.fke_swiglu(G.data_ptr(), U.data_ptr(), H.data_ptr(), M * I, _lib.IN_BF16, sh)
+
+    ms_u = timed(unfused, args.steps, args.warmup)
+    t = 2.0 * M * 2 * I * K / (ms * 1e-3) / 1e12
+    res["swiglu_gate_up_4096x14336x4096_bf16"] = {
+        "ms": round(ms, 4), "TOPS": round(t, 1), "frac": round(t / PEAK_INT8_TOPS, 4),
+        "unfused_ms": round(ms_u, 4), "speedup_vs_unfused": round(ms_u / ms, 3),
+        "kernel": "gemm_mfma_kernel<i8, nk, bf16, swiglu>",
+        "unfused": "two gemm_mfma_kernel launches to bf16 [4096,14336] + swiglu_kernel<bf16>"}
+    # the elementwise op alone on those bf16 tensors, two rotating sets (704 MiB)
+    G2, U2, H2 = torch.empty_like(G), torch.empty_like(U), torch.empty_like(H)
+    G.copy_(torch.randn((M, I), device=dev, generator=gen))
+    U.copy_(torch.randn((M, I), device=dev, generator=gen))
+    G2.copy_(G)
+    U2.copy_(U)
+    sets = [(G, U, H), (G2, U2, H2)]
+
+    def elaunch(i, st):
+        g, u, h = sets[i % 2]
+        r = L.fke_swiglu(g.data_ptr(), u.data_ptr(), h.data_ptr(), M * I, _lib.IN_BF16, st)
+        if r:
+            raise RuntimeError(f"swiglu failed: {_lib.status_string(r)}")
+
+    us = graph_us(torch, dev, elaunch, 40, 4)
+    nbytes = 3 * 2 * M * I
+    gbs = nbytes / (us * 1e-6) / 1e9
+    res["swiglu_elementwise_4096x14336_bf16"] = {"us": round(us, 2), "GB/s": round(gbs, 1),
+                                                 "frac": round(gbs / PEAK_HBM_GBS, 4), "bytes": nbytes,
+                                                 "kernel": "swiglu_kernel<bf16, vec>"}
+    del A, W, H, G, U, G2, U2, H2, sets
+    # decode: M = 1, fused gate/up + SwiGLU, 4 rotating weights of 112 MiB (448 MiB)
+    M, nbuf = 1, 4
+    A = torch.clamp(torch.round(torch.randn((M, K), device=dev, generator=gen) * 30), -127, 127).to(torch.int8)
+    Ws = [torch.randint(-127, 128, (2 * I, K), dtype=torch.int8, device=dev, generator=gen) for _ in range(nbuf)]
+    sa, sb = rand_u(M), rand_u(2 * I)
+    bias = torch.randn(2 * I, device=dev, generator=gen) * 0.02
+    H = torch.empty((M, I), dtype=torch.bfloat16, device=dev)
+
+    def dlaunch(i, st):
+        r = L.fke_qgemm_i8_swiglu(A.data_ptr(), Ws[i % nbuf].data_ptr(), H.data_ptr(), M, I, K, sa.data_ptr(),
+                                  sb.data_ptr(), 1.0, 1.0, bias.data_ptr(), _lib.OUT_BF16, st)
+        if r:
+            raise RuntimeError(f"swiglu decode failed: {_lib.status_string(r)}")
+
+    us = graph_us(torch, dev, dlaunch, 200, 2 * nbuf)
+    nbytes = M * K + 2 * I * K + 4 * M + 8 * 2 * I + 2 * M * I
+    gbs = nbytes / (us * 1e-6) / 1e9
+    res["swiglu_gate_up_decode_M1_14336x4096_bf16"] = {
+        "us": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4), "bytes": nbytes,
+        "kernel": "gemv_rows_kernel<1, bf16, fullk, swiglu>"}
+    del A, Ws, H
     return res
 
 

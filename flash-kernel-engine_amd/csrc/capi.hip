@@ -96,6 +96,31 @@ int run_i8(int path, const GemmArgs& p, void* stream) {
     }
 }
 
+bool half_args_ok(const void* A, const void* B, const void* C, int M, int N, int K, int in_dtype, int out_dtype,
+                  int b_layout) {
+    return common_args_ok(A, B, C, M, N, K, b_layout) && (in_dtype == FKE_IN_F16 || in_dtype == FKE_IN_BF16) &&
+           (out_dtype == FKE_OUT_F32 || out_dtype == FKE_OUT_BF16);
+}
+
+int half_elem(int in_dtype) { return in_dtype == FKE_IN_F16 ? fke::ELEM_F16 : fke::ELEM_BF16; }
+
+int pick_half(const GemmArgs& p, int elem) {
+    if (fke::mfma_supports(p, elem)) return FKE_PATH_MFMA;
+    return FKE_PATH_GENERIC;
+}
+
+int run_half(int path, const GemmArgs& p, int elem, void* stream) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (path == FKE_PATH_AUTO) path = pick_half(p, elem);
+    switch (path) {
+        case FKE_PATH_MFMA:
+            if (!fke::mfma_supports(p, elem)) return hipErrorInvalidValue;
+            return fke::launch_mfma(p, elem, s);
+        case FKE_PATH_GENERIC: return fke::launch_generic(p, elem, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
 int run_f8(int path, const GemmArgs& p, void* stream) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (path == FKE_PATH_AUTO) path = pick_f8(p);
@@ -167,6 +192,39 @@ int fke_swiglu(const void* gate, const void* up, void* out, int64_t n, int dtype
     if (dtype != FKE_IN_F32 && dtype != FKE_IN_BF16 && dtype != FKE_IN_F16) return hipErrorInvalidValue;
     if (n == 0) return hipSuccess;
     return fke::launch_swiglu(gate, up, out, n, dtype, static_cast<hipStream_t>(stream));
+}
+
+int fke_gemm_half_on_path(int path, const void* A, const void* B, void* C, int M, int N, int K, int in_dtype,
+                          const float* scale_a, const float* scale_b, float sa, float sb, const float* bias,
+                          int out_dtype, int b_layout, void* stream) {
+    if (!half_args_ok(A, B, C, M, N, K, in_dtype, out_dtype, b_layout)) return hipErrorInvalidValue;
+    return run_half(path, make_args(A, B, C, M, N, K, scale_a, scale_b, sa, sb, bias, out_dtype, b_layout),
+                    half_elem(in_dtype), stream);
+}
+
+int fke_gemm_half(const void* A, const void* B, void* C, int M, int N, int K, int in_dtype, const float* scale_a,
+                  const float* scale_b, float sa, float sb, const float* bias, int out_dtype, int b_layout,
+                  void* stream) {
+    return fke_gemm_half_on_path(FKE_PATH_AUTO, A, B, C, M, N, K, in_dtype, scale_a, scale_b, sa, sb, bias,
+                                 out_dtype, b_layout, stream);
+}
+
+int fke_select_path_half(const void* A, const void* B, const void* C, int M, int N, int K, int in_dtype,
+                         int out_dtype, int b_layout) {
+    if (!half_args_ok(A, B, C, M, N, K, in_dtype, out_dtype, b_layout)) return -1;
+    return pick_half(make_args(A, B, const_cast<void*>(C), M, N, K, nullptr, nullptr, 1.f, 1.f, nullptr, out_dtype,
+                               b_layout),
+                     half_elem(in_dtype));
+}
+
+// Reference src/tensor_core_attention.cu:13-86 (launch_wmma_gemm_fp16): A fp16
+// [M,K], B fp16 [N,K] ("column-major K x N"), C fp32 = alpha * A.B^T; beta is
+// accepted and, as there, unused (C is overwritten).
+int fke_launch_wmma_gemm_fp16(const void* d_A, const void* d_B, float* d_C, int M, int N, int K, float alpha,
+                              float beta, void* stream) {
+    (void)beta;
+    return fke_gemm_half(d_A, d_B, d_C, M, N, K, FKE_IN_F16, nullptr, nullptr, alpha, 1.0f, nullptr, FKE_OUT_F32,
+                         FKE_B_NK, stream);
 }
 
 int fke_select_path_i8(const void* A, const void* B, const void* C, int M, int N, int K,

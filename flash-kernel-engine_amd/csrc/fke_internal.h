@@ -27,7 +27,10 @@ struct GemmArgs {
     int swiglu;           // 1: B is [gate; up] (N = 2I rows, NK), C is [M, I] = SwiGLU of the pairs
 };
 
-enum Elem { ELEM_I8 = 0, ELEM_F8 = 1 };
+// Operand element types.  ELEM_F16 / ELEM_BF16: GemmArgs::K counts elements
+// at the C ABI; the MFMA kernel works on K bytes (2K).
+enum Elem { ELEM_I8 = 0, ELEM_F8 = 1, ELEM_F16 = 2, ELEM_BF16 = 3 };
+constexpr int elem_bytes(int elem) { return elem >= ELEM_F16 ? 2 : 1; }
 
 // Launchers (return this launch's status; arguments already validated).
 hipError_t launch_generic(const GemmArgs& p, int elem, hipStream_t stream);

@@ -1,4 +1,4 @@
-// gemm_generic.hip — any-shape fallback GEMM (INT8 and FP8, both B layouts).
+// gemm_generic.hip — any-shape fallback GEMM (INT8, FP8, fp16, bf16; both B layouts).
 //
 // Used when a call does not meet the fast families' shape/alignment needs
 // (e.g. K % 128 != 0 for prefill, odd K, unaligned pointers).  It keeps the
@@ -8,9 +8,11 @@
 //   FP8  — reference src/quantized_gemm.cu:109-116: each output is summed in
 //          fp32 over k = 0..K-1 in increasing order, so the result is
 //          bit-identical to the reference's sequential loop.
+//   fp16 / bf16 — the same sequential fp32 sum of exact products (reference
+//          src/tensor_core_attention.cu:13-66 leaves the order to the WMMA unit).
 // 64x64 output tile per 256-thread workgroup, 4x4 outputs per thread, K staged
-// through LDS 64 bytes at a time with bounds-checked byte loads (zero fill
-// past M/N/K adds exact zeros).
+// through LDS 64 elements at a time with bounds-checked element loads (zero
+// fill past M/N/K adds exact zeros).
 //
 // SwiGLU (INT8, B = [gate; up] of 2I rows): a tile covers 32 outputs; its
 // B column c = 4t + j holds gate row o (j = 0, 1) or up row I + o (j = 2, 3)
@@ -22,7 +24,22 @@ namespace fke {
 namespace {
 
 constexpr int T = 64;   // tile edge
-constexpr int KC = 64;  // K bytes per LDS stage
+constexpr int KC = 64;  // K elements per LDS stage
+
+// Raw bits of element idx (a byte, or 16 bits for fp16 / bf16).
+template <int ELEM>
+__device__ __forceinline__ uint32_t load_raw(const void* base, size_t idx) {
+    if constexpr (elem_bytes(ELEM) == 2) return static_cast<const uint16_t*>(base)[idx];
+    else return static_cast<const uint8_t*>(base)[idx];
+}
+
+// Value of a float-type element (FP8, fp16, bf16), exact in fp32.
+template <int ELEM>
+__device__ __forceinline__ float decode(uint32_t raw) {
+    if constexpr (ELEM == ELEM_F8) return e4m3_decode(raw);
+    else if constexpr (ELEM == ELEM_F16) return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(raw)));
+    else return __uint_as_float(raw << 16);
+}
 
 template <int ELEM, int OUT, bool SWI = false>
 __global__ __launch_bounds__(256) void gemm_generic_kernel(GemmArgs p) {
@@ -32,15 +49,14 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(GemmArgs p) {
     const int m0 = blockIdx.y * T, n0 = blockIdx.x * (SWI ? T / 2 : T);  // n0: first output column
     const int M = p.M, N = p.N, K = p.K;
     const int NO = SWI ? N >> 1 : N;  // output columns
-    const uint8_t* A = static_cast<const uint8_t*>(p.A);
-    const uint8_t* B = static_cast<const uint8_t*>(p.B);
     const bool kn = p.b_layout == FKE_B_KN;
 
-    // INT8: packed 4-byte words (KC/4 per row, +1 pad); FP8: decoded floats.
-    __shared__ int32_t Aw[ELEM == ELEM_I8 ? T : 1][KC / 4 + 1];
-    __shared__ int32_t Bw[ELEM == ELEM_I8 ? T : 1][KC / 4 + 1];
-    __shared__ float Af[ELEM == ELEM_F8 ? T : 1][KC + 1];
-    __shared__ float Bf[ELEM == ELEM_F8 ? T : 1][KC + 1];
+    // INT8: packed 4-byte words (KC/4 per row, +1 pad); FP8 / fp16 / bf16: decoded floats.
+    constexpr bool INT = ELEM == ELEM_I8;
+    __shared__ int32_t Aw[INT ? T : 1][KC / 4 + 1];
+    __shared__ int32_t Bw[INT ? T : 1][KC / 4 + 1];
+    __shared__ float Af[INT ? 1 : T][KC + 1];
+    __shared__ float Bf[INT ? 1 : T][KC + 1];
 
     int32_t iacc[4][4];
     float facc[4][4];
@@ -53,18 +69,18 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(GemmArgs p) {
         }
 
     for (int k0 = 0; k0 < K; k0 += KC) {
-        // Stage: thread t loads 16 bytes of A (row t/4, bytes 16*(t%4)..) and
-        // 16 bytes of B for one (n row, 16 k) slice.
+        // Stage: thread t loads 16 elements of A (row t/4, k 16*(t%4)..) and
+        // 16 elements of B for one (n row, 16 k) slice.
         {
             const int r = tid >> 2, kq = (tid & 3) * 16;
             const int m = m0 + r;
-            uint8_t a[16];
+            uint32_t a[16];
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
                 const int k = k0 + kq + q;
-                a[q] = (m < M && k < K) ? A[static_cast<size_t>(m) * K + k] : 0;
+                a[q] = (m < M && k < K) ? load_raw<ELEM>(p.A, static_cast<size_t>(m) * K + k) : 0;
             }
-            uint8_t b[16];
+            uint32_t b[16];
             int bn, bk;
             if (kn) {  // coalesce along n: thread t -> column t%64, k block t/64
                 bn = tid & 63;
@@ -83,12 +99,12 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(GemmArgs p) {
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
                 const int k = k0 + bk + q;
-                uint8_t v = 0;
+                uint32_t v = 0;
                 if (n_ok && k < K)
-                    v = kn ? B[static_cast<size_t>(k) * N + n] : B[static_cast<size_t>(n) * K + k];
+                    v = load_raw<ELEM>(p.B, kn ? static_cast<size_t>(k) * N + n : static_cast<size_t>(n) * K + k);
                 b[q] = v;
             }
-            if constexpr (ELEM == ELEM_I8) {
+            if constexpr (INT) {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     Aw[r][kq / 4 + q] = static_cast<int32_t>(a[4 * q] | (a[4 * q + 1] << 8) |
@@ -101,8 +117,8 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(GemmArgs p) {
             } else {
 #pragma unroll
                 for (int q = 0; q < 16; ++q) {
-                    Af[r][kq + q] = e4m3_decode(a[q]);
-                    Bf[bn][bk + q] = e4m3_decode(b[q]);
+                    Af[r][kq + q] = decode<ELEM>(a[q]);
+                    Bf[bn][bk + q] = decode<ELEM>(b[q]);
                 }
             }
         }
@@ -166,13 +182,13 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(GemmArgs p) {
             const int n = n0 + tx * 4 + j;
             if (n >= N) continue;
             const size_t idx = static_cast<size_t>(m) * N + n;
-            if constexpr (ELEM == ELEM_I8) {
-                const float s = (p.scale_a ? p.scale_a[m] : p.sa) * (p.scale_b ? p.scale_b[n] : p.sb);
+            // (FP8 calls carry no scale vectors: s = fp32(sa * sb))
+            const float s = (p.scale_a ? p.scale_a[m] : p.sa) * (p.scale_b ? p.scale_b[n] : p.sb);
+            if constexpr (ELEM == ELEM_I8)
                 store_out<OUT>(p.C, idx, epilogue_value(static_cast<float>(iacc[i][j]), s, p.bias, n),
                                iacc[i][j]);
-            } else {
-                store_out<OUT>(p.C, idx, epilogue_value(facc[i][j], p.sa * p.sb, p.bias, n), 0);
-            }
+            else
+                store_out<OUT>(p.C, idx, epilogue_value(facc[i][j], s, p.bias, n), 0);
         }
     }
 }
@@ -205,6 +221,12 @@ hipError_t launch_generic(const GemmArgs& p, int elem, hipStream_t s) {
             default: return launch_t<ELEM_I8, FKE_OUT_I32>(p, s);
         }
     }
+    if (elem == ELEM_F16)
+        return p.out_dtype == FKE_OUT_F32 ? launch_t<ELEM_F16, FKE_OUT_F32>(p, s)
+                                          : launch_t<ELEM_F16, FKE_OUT_BF16>(p, s);
+    if (elem == ELEM_BF16)
+        return p.out_dtype == FKE_OUT_F32 ? launch_t<ELEM_BF16, FKE_OUT_F32>(p, s)
+                                          : launch_t<ELEM_BF16, FKE_OUT_BF16>(p, s);
     return p.out_dtype == FKE_OUT_F32 ? launch_t<ELEM_F8, FKE_OUT_F32>(p, s)
                                       : launch_t<ELEM_F8, FKE_OUT_BF16>(p, s);
 }

@@ -202,7 +202,11 @@ __device__ __forceinline__ uint32_t kn_read_off(int lane, int wn, int j, int rr)
     return static_cast<uint32_t>(row * 256 + chunk * 16 + 8 * (sl & 1));
 }
 
-// Per element type: fragment and accumulator types, k steps per stage.
+// Per element type: fragment and accumulator types, k steps per stage, and
+// FB, the operand bytes per lane of one MFMA.  FB = 16 (INT8, fp16, bf16):
+// lane l supplies row l%32 with bytes 16*(l/32)..+15 of a 32-byte k step
+// (32 int8 or 16 fp16/bf16 values per row); FB = 32 (FP8): 32 codes per lane
+// of a 64-byte step.
 template <int ELEM>
 struct Mma;
 template <>
@@ -210,13 +214,26 @@ struct Mma<ELEM_I8> {
     using Frag = v4i;  // 16 k bytes per lane
     using AccT = v16i;
     static constexpr int KSTEPS = BK / 32;
+    static constexpr int FB = 16;
 };
 template <>
 struct Mma<ELEM_F8> {
     using Frag = v8i;  // 32 k codes per lane
     using AccT = v16f;
     static constexpr int KSTEPS = BK / 64;
+    static constexpr int FB = 32;
 };
+template <int ELEM>
+struct Mma16 {
+    using Frag = v4i;  // 8 fp16 / bf16 k values per lane
+    using AccT = v16f;
+    static constexpr int KSTEPS = BK / 32;
+    static constexpr int FB = 16;
+};
+template <>
+struct Mma<ELEM_F16> : Mma16<ELEM_F16> {};
+template <>
+struct Mma<ELEM_BF16> : Mma16<ELEM_BF16> {};
 
 template <int ELEM>
 struct Frags {
@@ -233,7 +250,7 @@ struct Frags {
 //   FP8: r = 8 + 4j + rr, rr = which 8 of the lane's k bytes.
 template <int ELEM, int BL>
 struct Reads {
-    static constexpr int A = ELEM == ELEM_I8 ? 4 : 8;
+    static constexpr int A = Mma<ELEM>::FB == 16 ? 4 : 8;
     static constexpr int N = BL == FKE_B_NK ? 2 * A : 3 * A;
 };
 
@@ -244,7 +261,7 @@ __device__ __forceinline__ void read_piece(const uint8_t* buf, int ks, int wm, i
     const uint8_t* Ab = buf + (wm * 128 + lr) * BK;
     const uint8_t* Bb = buf + STAGE_A + (wn * 128 + lr) * BK;
     constexpr int RA = Reads<ELEM, BL>::A;
-    if (BL == FKE_B_KN && r >= RA) {
+    if constexpr (BL == FKE_B_KN) if (r >= RA) {
         constexpr int KSTEP = ELEM == ELEM_I8 ? 32 : 64;  // k rows per step
         const int p = r - RA;
         const int j = ELEM == ELEM_I8 ? p >> 1 : p >> 2, rr = ELEM == ELEM_I8 ? p & 1 : p & 3;
@@ -253,7 +270,7 @@ __device__ __forceinline__ void read_piece(const uint8_t* buf, int ks, int wm, i
         f.b[j][2 * rr + 1] = x[1];
         return;
     }
-    if constexpr (ELEM == ELEM_I8) {
+    if constexpr (Mma<ELEM>::FB == 16) {
         const int co = ((ks * 2 + lh) ^ sw) << 4;  // this lane's 16-byte chunk of the 32-byte step
         if (r < 4) f.a[r] = *reinterpret_cast<const v4i*>(Ab + r * 32 * BK + co);
         else f.b[r - 4] = *reinterpret_cast<const v4i*>(Bb + (r - 4) * 32 * BK + co);
@@ -293,10 +310,18 @@ __device__ __forceinline__ void sanitize_frags(Frags<ELEM>& f) {
 // MFMA (i, j) of one k step of the wave's 128x128 block.
 template <int ELEM>
 __device__ __forceinline__ void mfma_one(const Frags<ELEM>& f, typename Mma<ELEM>::AccT (&acc)[4][4], int i, int j) {
+    typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+    typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
     if constexpr (ELEM == ELEM_I8)
         acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
-    else
+    else if constexpr (ELEM == ELEM_F8)
         acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.a[i], f.b[j], acc[i][j], 0, 0, 0, 0, 0, 0);
+    else if constexpr (ELEM == ELEM_F16)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, f.a[i]),
+                                                           __builtin_bit_cast(v8h, f.b[j]), acc[i][j], 0, 0, 0);
+    else
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, f.a[i]),
+                                                            __builtin_bit_cast(v8bf, f.b[j]), acc[i][j], 0, 0, 0);
 }
 
 // Output columns of one workgroup tile: 256, or 128 SwiGLU outputs (256 B rows).
@@ -457,7 +482,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
         for (int t = 0; t < 16; ++t) mfma_one<ELEM>(f1, acc, t >> 2, t & 3);
     };
 
-    if constexpr (ELEM == ELEM_I8) {
+    if constexpr (ELEM != ELEM_F8) {
         k_loop(F{});
     } else {
         // E4M3 0x7F/0xFF are NaN to the MFMA but 0.0 to the reference.
@@ -569,8 +594,10 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
                     if constexpr (ELEM == ELEM_I8) {
                         a = acc[i][j][v];
                         y = __builtin_fmaf(static_cast<float>(a), sav[e] * sbn, bn);
-                    } else {
+                    } else if constexpr (ELEM == ELEM_F8) {
                         y = __builtin_fmaf(acc[i][j][v], p.sa * p.sb, bn);
+                    } else {
+                        y = __builtin_fmaf(acc[i][j][v], sav[e] * sbn, bn);
                     }
                     if constexpr (OUT == FKE_OUT_F32)
                         __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(y), rc, voff, 0, 2);
@@ -608,13 +635,15 @@ hipError_t launch_out(const GemmArgs& p, hipStream_t s) {
 }  // namespace
 
 bool mfma_supports(const GemmArgs& p, int elem) {
-    (void)elem;
     const uintptr_t a = reinterpret_cast<uintptr_t>(p.A), b = reinterpret_cast<uintptr_t>(p.B);
-    if (p.M < 1 || p.N < 1 || p.K < BK || p.K % BK != 0) return false;
+    const int64_t kb = static_cast<int64_t>(p.K) * elem_bytes(elem);  // K bytes per row
+    if (p.M < 1 || p.N < 1 || kb < BK || kb % BK != 0) return false;
     if ((a | b) & 15) return false;
     // per-lane DMA offsets are 32-bit: (rows - 1) * K + K must fit
-    if (static_cast<int64_t>(p.M) * p.K > INT32_MAX) return false;
-    if (static_cast<int64_t>(p.N) * p.K > INT32_MAX) return false;
+    if (p.M * kb > INT32_MAX) return false;
+    if (p.N * kb > INT32_MAX) return false;
+    // 16-bit operands: B [N,K] only (the transposed LDS reads are byte-wise)
+    if (elem_bytes(elem) == 2 && p.b_layout != FKE_B_NK) return false;
     if (p.b_layout == FKE_B_KN && (p.N % 16 != 0)) return false;
     if (p.swiglu && (elem != ELEM_I8 || p.b_layout != FKE_B_NK)) return false;
     // epilogue offsets are 32-bit: 256 output rows plus the 2^31 drop offset
@@ -623,6 +652,11 @@ bool mfma_supports(const GemmArgs& p, int elem) {
 }
 
 hipError_t launch_mfma(const GemmArgs& p, int elem, hipStream_t s) {
+    if (elem == ELEM_F16 || elem == ELEM_BF16) {
+        GemmArgs q = p;
+        q.K = 2 * p.K;  // the kernel walks K bytes
+        return elem == ELEM_F16 ? launch_out<ELEM_F16, FKE_B_NK>(q, s) : launch_out<ELEM_BF16, FKE_B_NK>(q, s);
+    }
     if (p.swiglu)
         return p.out_dtype == FKE_OUT_F32 ? launch_t<ELEM_I8, FKE_B_NK, FKE_OUT_F32, true>(p, s)
                                           : launch_t<ELEM_I8, FKE_B_NK, FKE_OUT_BF16, true>(p, s);

@@ -145,22 +145,30 @@ __device__ __forceinline__ int32_t wave_sum(int32_t v) {
     return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 32);
 }
 
-constexpr int ROWS_WAVES = 2;  // waves (= B rows) per workgroup of gemv_rows_kernel
+constexpr int ROWS_WAVES = 2;  // waves per workgroup of gemv_rows_kernel
+// Weight rows per wave of the plain kernel.  One: at N = 14336, K = 4096 the
+// launch is bounded by its ramp and drain, and 2 / 4 / 8 rows per wave
+// (fewer, longer waves) measured 10.3 / 10.8 / 13.0 us against 9.8 us.
+constexpr int ROWS_NB = 1;
 
+// Wave w streams NB weight rows side by side: rows NB*w .. NB*w+NB-1 (plain),
+// or gate row w and up row I + w (SWI: B is [gate; up], N = 2I rows, and the
+// wave stores swiglu_pair of the two epilogue values).
 // FULLK: K is a multiple of 4096, so every 256-chunk block is whole: the
 // activation chunks come with plain loads and no offset needs the 2^31 guard.
-// SWI: B is [gate; up] (N = 2I rows); the wave streams gate row n and up row
-// I + n side by side and stores swiglu_pair of the two epilogue values.
-template <int MT, int OUT, bool FULLK, bool SWI = false>
+template <int MT, int OUT, bool FULLK, int NB, bool SWI = false>
 __global__ __launch_bounds__(ROWS_WAVES * 64) void gemv_rows_kernel(GemmArgs p) {
-    constexpr int NB = SWI ? 2 : 1;  // weight rows per wave
+    static_assert(!SWI || NB == 2, "SwiGLU streams one gate and one up row");
+    static_assert(MT * NB <= 64, "one storing lane per output");
     const int lane = threadIdx.x & 63;
-    const int NO = SWI ? p.N >> 1 : p.N;  // output columns
-    // Uniform per wave; readfirstlane keeps the row's buffer resource in
+    const int NO = SWI ? p.N >> 1 : p.N;           // output columns
+    const int NU = SWI ? NO : (p.N + NB - 1) / NB;  // waves with work
+    // Uniform per wave; readfirstlane keeps the rows' buffer resources in
     // SGPRs.  A wave past the last row re-reads it and stores nothing, so
     // nothing stands between the kernel arguments and the first weight load.
     const int nw = __builtin_amdgcn_readfirstlane(blockIdx.x * ROWS_WAVES + (threadIdx.x >> 6));
-    const int n = min(nw, NO - 1);
+    const int n = min(nw, NU - 1);
+    auto row_of = [&](int q) __attribute__((always_inline)) { return SWI ? n + q * NO : min(n * NB + q, p.N - 1); };
     const int M = p.M, K = p.K;
     const int ck = K >> 4;  // 16-byte chunks per row (K % 64 == 0)
     // B row n and the M activation rows through buffer resources: 32-bit
@@ -172,7 +180,7 @@ __global__ __launch_bounds__(ROWS_WAVES * 64) void gemv_rows_kernel(GemmArgs p) 
 #pragma unroll
     for (int q = 0; q < NB; ++q)
         rb[q] = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<int8_t*>(static_cast<const int8_t*>(p.B) + static_cast<size_t>(n + q * NO) * K), 0, K,
+            const_cast<int8_t*>(static_cast<const int8_t*>(p.B) + static_cast<size_t>(row_of(q)) * K), 0, K,
             0x00020000);
     __amdgpu_buffer_rsrc_t ra[MT];
 #pragma unroll
@@ -185,8 +193,8 @@ __global__ __launch_bounds__(ROWS_WAVES * 64) void gemv_rows_kernel(GemmArgs p) 
     float sbn[NB], biasn[NB];
 #pragma unroll
     for (int q = 0; q < NB; ++q) {
-        sbn[q] = p.scale_b ? p.scale_b[n + q * NO] : p.sb;
-        biasn[q] = p.bias ? p.bias[n + q * NO] : 0.0f;
+        sbn[q] = p.scale_b ? p.scale_b[row_of(q)] : p.sb;
+        biasn[q] = p.bias ? p.bias[row_of(q)] : 0.0f;
     }
     int32_t acc[NB][MT];
 #pragma unroll
@@ -230,20 +238,26 @@ __global__ __launch_bounds__(ROWS_WAVES * 64) void gemv_rows_kernel(GemmArgs p) 
     for (int q = 0; q < NB; ++q)
 #pragma unroll
         for (int m = 0; m < MT; ++m) tot[q][m] = wave_sum(acc[q][m]);
-    // lane m stores output row m (all lanes hold every total)
+    // All lanes hold every total.  SWI: lane m stores output (m, n); plain:
+    // lane m*NB + q stores output (m, NB*n + q).
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
-        if (lane == m && m < M && nw < NO) {
-            const float sam = p.scale_a ? p.scale_a[m] : p.sa;
-            float y[NB];
+        const float sam = p.scale_a ? p.scale_a[m] : p.sa;
+        float y[NB];
 #pragma unroll
-            for (int q = 0; q < NB; ++q) {
-                const float sc = sam * sbn[q];
-                y[q] = p.bias ? __builtin_fmaf(static_cast<float>(tot[q][m]), sc, biasn[q])
-                              : static_cast<float>(tot[q][m]) * sc;
-            }
-            const float h = SWI ? swiglu_pair(y[0], y[NB - 1]) : y[0];
-            store_out<OUT>(p.C, static_cast<size_t>(m) * NO + n, h, tot[0][m]);
+        for (int q = 0; q < NB; ++q) {
+            const float sc = sam * sbn[q];
+            y[q] = p.bias ? __builtin_fmaf(static_cast<float>(tot[q][m]), sc, biasn[q])
+                          : static_cast<float>(tot[q][m]) * sc;
+        }
+        if constexpr (SWI) {
+            if (lane == m && m < M && nw < NO)
+                store_out<OUT>(p.C, static_cast<size_t>(m) * NO + n, swiglu_pair(y[0], y[1]), 0);
+        } else {
+#pragma unroll
+            for (int q = 0; q < NB; ++q)
+                if (lane == m * NB + q && m < M && nw < NU && n * NB + q < p.N)
+                    store_out<OUT>(p.C, static_cast<size_t>(m) * p.N + n * NB + q, y[q], tot[q][m]);
         }
     }
 }
@@ -359,7 +373,7 @@ hipError_t launch_mfma_skinny(const GemmArgs& p, hipStream_t stream) {
     return hipLaunchKernel(f, grid, dim3(SK_KS * 64), args, 0, stream);
 }
 
-template <int MT, bool FULLK>
+template <int MT, bool FULLK, int NB = ROWS_NB>
 hipError_t launch_rows(const GemmArgs& p, hipStream_t stream) {
     GemmArgs a = p;
     void* args[] = {&a};
@@ -367,15 +381,16 @@ hipError_t launch_rows(const GemmArgs& p, hipStream_t stream) {
     if (p.swiglu) {
         const dim3 grid((p.N / 2 + ROWS_WAVES - 1) / ROWS_WAVES);
         f = p.out_dtype == FKE_OUT_F32
-            ? reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_F32, FULLK, true>)
-            : reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_BF16, FULLK, true>);
+            ? reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_F32, FULLK, 2, true>)
+            : reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_BF16, FULLK, 2, true>);
         return hipLaunchKernel(f, grid, dim3(ROWS_WAVES * 64), args, 0, stream);
     }
-    const dim3 grid((p.N + ROWS_WAVES - 1) / ROWS_WAVES);
+    const int units = (p.N + NB - 1) / NB;
+    const dim3 grid((units + ROWS_WAVES - 1) / ROWS_WAVES);
     switch (p.out_dtype) {
-        case FKE_OUT_F32: f = reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_F32, FULLK>); break;
-        case FKE_OUT_BF16: f = reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_BF16, FULLK>); break;
-        default: f = reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_I32, FULLK>); break;
+        case FKE_OUT_F32: f = reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_F32, FULLK, NB>); break;
+        case FKE_OUT_BF16: f = reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_BF16, FULLK, NB>); break;
+        default: f = reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_I32, FULLK, NB>); break;
     }
     return hipLaunchKernel(f, grid, dim3(ROWS_WAVES * 64), args, 0, stream);
 }

@@ -33,6 +33,10 @@ SIGNATURES = {
     "fke_qgemm_i8_swiglu": ([_p, _p, _p, _i, _i, _i, _p, _p, _f, _f, _p, _i, _p], _i),
     "fke_qgemm_i8_swiglu_on_path": ([_i, _p, _p, _p, _i, _i, _i, _p, _p, _f, _f, _p, _i, _p], _i),
     "fke_select_path_i8_swiglu": ([_p, _p, _p, _i, _i, _i, _i], _i),
+    "fke_gemm_half": ([_p, _p, _p, _i, _i, _i, _i, _p, _p, _f, _f, _p, _i, _i, _p], _i),
+    "fke_gemm_half_on_path": ([_i, _p, _p, _p, _i, _i, _i, _i, _p, _p, _f, _f, _p, _i, _i, _p], _i),
+    "fke_launch_wmma_gemm_fp16": ([_p, _p, _p, _i, _i, _i, _f, _f, _p], _i),
+    "fke_select_path_half": ([_p, _p, _p, _i, _i, _i, _i, _i, _i], _i),
     "fke_select_path_i8": ([_p, _p, _p, _i, _i, _i, _i, _i], _i),
     "fke_select_path_f8": ([_p, _p, _p, _i, _i, _i, _i, _i], _i),
     "fke_print_device_info": ([_i], _i),

@@ -215,6 +215,48 @@ def w8a8_gate_up_swiglu(x: torch.Tensor, weight: torch.Tensor, weight_scale: tor
     return w8a8_swiglu(q, weight, scale_a=sa, scale_b=weight_scale, bias=bias, out_dtype=out_dtype)
 
 
+def gemm_half(A: torch.Tensor, B: torch.Tensor, scale_a=None, scale_b=None, bias=None,
+              out_dtype=torch.float32, b_layout: str = "nk", sa: float = 1.0, sb: float = 1.0,
+              path: str = "auto", out: torch.Tensor | None = None) -> torch.Tensor:
+    """fp16 / bf16 GEMM on the MFMA tile engine (extends reference
+    src/tensor_core_attention.cu:13-86, launch_wmma_gemm_fp16).
+
+    acc = A[M,K] . B in fp32 (B [N,K] for "nk", [K,N] for "kn"; A and B both
+    float16 or both bfloat16), y = acc * fp32(scale_a[m] * scale_b[n]) (+ bias[n]
+    via one fma), out fp32 or bf16 [M,N].  With sa = alpha and no vectors this is
+    the reference's C = alpha * A B^T.
+    """
+    dev = A.device
+    codes = {torch.float16: _lib.IN_F16, torch.bfloat16: _lib.IN_BF16}
+    if A.dtype not in codes:
+        raise TypeError(f"A must be float16 or bfloat16, got {A.dtype}")
+    _check_dev("A", A, A.dtype, dev)
+    _check_dev("B", B, A.dtype, dev)
+    if A.dim() != 2 or B.dim() != 2:
+        raise ValueError("A and B must be 2-D")
+    layout = _LAYOUTS[b_layout]
+    M, K = A.shape
+    N, KB = (B.shape[0], B.shape[1]) if layout == B_NK else (B.shape[1], B.shape[0])
+    if KB != K:
+        raise ValueError(f"K mismatch: A has {K}, B has {KB}")
+    _check_vec("scale_a", scale_a, M, dev)
+    _check_vec("scale_b", scale_b, N, dev)
+    _check_vec("bias", bias, N, dev)
+    if out_dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError("the half GEMM writes fp32 or bf16")
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=dev)
+    else:
+        _check_dev("out", out, out_dtype, dev)
+        if tuple(out.shape) != (M, N):
+            raise ValueError("out has the wrong shape")
+    st = _lib.lib().fke_gemm_half_on_path(
+        _PATHS[path], A.data_ptr(), B.data_ptr(), out.data_ptr(), M, N, K, codes[A.dtype], _ptr(scale_a),
+        _ptr(scale_b), sa, sb, _ptr(bias), _OUT_CODES[out_dtype], layout, _stream(A))
+    _lib.check(st, "fke_gemm_half")
+    return out
+
+
 def fused_swiglu(gate, up):
     """(gate * sigmoid(gate)) * up, elementwise (reference python/flash_engine/ops.py:218-230,
     src/fused_activations.cu).  float32, float16 or bfloat16 GPU tensors of one

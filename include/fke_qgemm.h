@@ -164,6 +164,36 @@ int fke_qgemm_i8_swiglu_on_path(int path, const int8_t* A, const int8_t* W, void
                                 int K, const float* scale_a, const float* scale_b, float sa,
                                 float sb, const float* bias, int out_dtype, void* stream);
 
+/*
+ * fp16 / bf16 GEMM on the MFMA tile engine (extends reference
+ * src/tensor_core_attention.cu:13-86, whose WMMA kernel computes fp16 A [M,K]
+ * times B stored [N,K] into fp32; per-row/per-column scales, bias and the
+ * bf16 operands and output have no reference counterpart):
+ *   acc[m,n] = sum_k A[m,k]*B(n,k) in fp32       (each product exact in fp32)
+ *   y        = bias ? fmaf(acc, s, bias[n]) : acc * s,  s = fp32(sa_m * sb_n)
+ *   C        = y (F32) | bf16_rne(y) (BF16)
+ * in_dtype: FKE_IN_F16 or FKE_IN_BF16 (A and B alike); K counts elements.
+ * The MFMA family (K % 64 == 0, B [N,K], 16-byte aligned) sums in its own
+ * order; the GENERIC family sums k = 0..K-1 in order.  Any M, N, K >= 1.
+ */
+int fke_gemm_half(const void* A, const void* B, void* C, int M, int N, int K, int in_dtype,
+                  const float* scale_a, const float* scale_b, float sa, float sb,
+                  const float* bias, int out_dtype, int b_layout, void* stream);
+
+int fke_gemm_half_on_path(int path, const void* A, const void* B, void* C, int M, int N, int K,
+                          int in_dtype, const float* scale_a, const float* scale_b, float sa,
+                          float sb, const float* bias, int out_dtype, int b_layout, void* stream);
+
+/*
+ * Drop-in for flash_engine::tensor_core::launch_wmma_gemm_fp16 (reference
+ * include/tensor_core_gemm.cuh:27-35, src/tensor_core_attention.cu:68-86):
+ * C[m,n] = alpha * sum_k A[m,k]*B[n*K+k], A and B fp16, C fp32 [M,N].  beta
+ * is accepted and unused, as in the reference (C is overwritten).  Any M, N,
+ * K >= 1 (the reference kernel needs multiples of 16).
+ */
+int fke_launch_wmma_gemm_fp16(const void* d_A, const void* d_B, float* d_C, int M, int N, int K,
+                              float alpha, float beta, void* stream);
+
 /* The family fke_qgemm_i8 / fke_qgemm_f8 would pick (enum fke_path), or -1
  * for arguments they would reject.  Pure host logic; needs no GPU. */
 int fke_select_path_i8(const void* A, const void* B, const void* C, int M, int N, int K,
@@ -172,6 +202,8 @@ int fke_select_path_f8(const void* A, const void* B, const void* C, int M, int N
                        int out_dtype, int b_layout);
 int fke_select_path_i8_swiglu(const void* A, const void* W, const void* H, int M, int I, int K,
                               int out_dtype);
+int fke_select_path_half(const void* A, const void* B, const void* C, int M, int N, int K,
+                         int in_dtype, int out_dtype, int b_layout);
 
 /* Replaces flash_engine::print_device_info (reference include/flash_engine.h:29,
  * src/flash_engine_api.cu:7-27): prints the device's properties to stdout. */

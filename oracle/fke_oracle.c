@@ -371,3 +371,60 @@ void fko_w8a8_swiglu(const int8_t* A, const int8_t* W, void* out, int M, int I, 
     }
     free(acc);
 }
+
+/* IEEE binary16 -> fp32, exact, from the bit fields. */
+float fko_f16_to_f32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h >> 15) << 31;
+    const uint32_t e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
+    uint32_t bits;
+    if (e == 0) {
+        float v = ldexpf((float)m, -24);
+        memcpy(&bits, &v, 4);
+        bits |= sign;
+    } else if (e == 31) {
+        bits = sign | 0x7F800000u | (m << 13);
+    } else {
+        bits = sign | ((e + 112u) << 23) | (m << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+void fko_gemm_half(const uint16_t* A, const uint16_t* B, void* out, int M, int N, int K, int in_dtype,
+                   const float* scale_a, const float* scale_b, float sa, float sb, const float* bias,
+                   int out_dtype, int b_layout, const int* rows, int nrows, int nthreads) {
+    const int R = rows ? nrows : M;
+    float* dec = (float*)malloc(sizeof(float) * 65536);
+    if (!dec) return;
+    for (uint32_t i = 0; i < 65536; ++i) dec[i] = in_dtype == 2 ? fko_f16_to_f32((uint16_t)i) : fko_bf16_to_f32((uint16_t)i);
+    if (nthreads < 1) nthreads = 1;
+#pragma omp parallel for schedule(dynamic, 1) num_threads(nthreads)
+    for (int r = 0; r < R; ++r) {
+        const int m = rows ? rows[r] : r;
+        const uint16_t* a = A + (size_t)m * K;
+        const float am = scale_a ? scale_a[m] : sa;
+        float* sums = (float*)malloc(sizeof(float) * (size_t)N);
+        for (int n = 0; n < N; ++n) sums[n] = 0.0f;
+        if (b_layout == FKO_B_KN) {
+            for (int k = 0; k < K; ++k) { /* each sums[n] still adds k = 0..K-1 in order */
+                const float av = dec[a[k]];
+                const uint16_t* b = B + (size_t)k * N;
+                for (int n = 0; n < N; ++n) sums[n] += av * dec[b[n]];
+            }
+        } else {
+            for (int n = 0; n < N; ++n) {
+                const uint16_t* b = B + (size_t)n * K;
+                float sum = 0.0f;
+                for (int k = 0; k < K; ++k) sum += dec[a[k]] * dec[b[k]];
+                sums[n] = sum;
+            }
+        }
+        for (int n = 0; n < N; ++n) {
+            const float s = am * (scale_b ? scale_b[n] : sb);
+            store_out(out, (size_t)r * N + n, out_dtype, epi(sums[n], s, bias, n), 0);
+        }
+        free(sums);
+    }
+    free(dec);
+}

@@ -30,6 +30,11 @@
  *                             exact special values (g = 0, saturation).
  *   fko_w8a8_swiglu           equals fko_w8a8_gemm on the gate rows and on the
  *                             up rows followed by fko_swiglu_f32, bit for bit.
+ *   fko_f16_to_f32            exhaustive 65536 codes vs numpy's float16 cast.
+ *   fko_gemm_half             exact small-integer products vs int64 matmul;
+ *                             float64 matmul within the sequential-sum error
+ *                             bound; a hand case whose value depends on the
+ *                             summation order (pins k ascending).
  */
 #ifndef FKE_ORACLE_H
 #define FKE_ORACLE_H
@@ -100,6 +105,19 @@ float fko_quantize_e4m3(const float* x, uint8_t* q, size_t n);
  * q = clamp(rne(fp32(x*r)), -127, 127), NaN -> 0; scale[m] = s.
  * x is fp32 (in_dtype 0) or bf16 bits (in_dtype 1), [M,K]. */
 void fko_quantize_rows_i8(const void* x, int in_dtype, int M, int K, int8_t* q, float* scale);
+
+/* IEEE binary16 -> fp32 (exact): e = 0 -> m * 2^-24; e = 31 -> inf / NaN;
+ * else (1 + m/1024) * 2^(e-15).  The operand type of the reference's WMMA
+ * GEMM (src/tensor_core_attention.cu:13-18, half). */
+float fko_f16_to_f32(uint16_t h);
+/* fp16 / bf16 GEMM (extends src/tensor_core_attention.cu:13-66, which
+ * accumulates fp16 products into fp32 with alpha applied at the end):
+ * acc = sum over k = 0..K-1, in order, of the exact fp32 products; then the
+ * W8A8 canonical epilogue (s = fp32(sa_m*sb_n), fmaf with bias) and f32 /
+ * bf16 output.  A, B are raw 16-bit codes; in_dtype 2 = fp16, 1 = bf16. */
+void fko_gemm_half(const uint16_t* A, const uint16_t* B, void* out, int M, int N, int K, int in_dtype,
+                   const float* scale_a, const float* scale_b, float sa, float sb, const float* bias,
+                   int out_dtype, int b_layout, const int* rows, int nrows, int nthreads);
 
 /* SwiGLU of one pair, src/fused_activations.cu:9-11,30-33:
  * (g * sigmoid(g)) * u with sigmoid(g) = 1 / (1 + exp(-g)), fp32, in that

@@ -18,6 +18,7 @@ _SO = os.path.join(_HERE, "liboracle.so")
 
 OUT_F32, OUT_BF16, OUT_I32 = 0, 1, 2
 B_NK, B_KN = 0, 1
+HALF_BF16, HALF_F16 = 1, 2  # in_dtype codes of gemm_half (fke_in_dtype values)
 
 _lib = None
 
@@ -76,6 +77,10 @@ def _declare(L):
     L.fko_swiglu_f32.restype = None
     L.fko_w8a8_swiglu.argtypes = [_p, _p, _p, _i, _i, _i, _p, _p, _f, _f, _p, _i, _p, _i, _i]
     L.fko_w8a8_swiglu.restype = None
+    L.fko_f16_to_f32.argtypes = [ct.c_uint16]
+    L.fko_f16_to_f32.restype = _f
+    L.fko_gemm_half.argtypes = [_p, _p, _p, _i, _i, _i, _i, _p, _p, _f, _f, _p, _i, _i, _p, _i, _i]
+    L.fko_gemm_half.restype = None
 
 
 def _ptr(a):
@@ -271,4 +276,29 @@ def w8a8_swiglu(A, W, scale_a=None, scale_b=None, sa: float = 1.0, sb: float = 1
     nt = nthreads or (os.cpu_count() or 1)
     lib().fko_w8a8_swiglu(_ptr(A), _ptr(W), _ptr(out), M, I, K, _ptr(sa_arr), _ptr(sb_arr), sa, sb,
                           _ptr(b_arr), out_dtype, _ptr(r), 0 if r is None else r.size, nt)
+    return out
+
+
+# ---- fp16 / bf16 GEMM ------------------------------------------------------------
+
+def f16_to_f32(bits) -> np.ndarray:
+    """IEEE binary16 codes -> fp32 (exact)."""
+    b = np.ascontiguousarray(bits, dtype=np.uint16)
+    return np.array([lib().fko_f16_to_f32(int(v)) for v in b.ravel()], dtype=np.float32).reshape(b.shape)
+
+
+def gemm_half(A, B, in_dtype: int, scale_a=None, scale_b=None, sa: float = 1.0, sb: float = 1.0, bias=None,
+              out_dtype: int = OUT_F32, b_layout: int = B_NK, rows=None, nthreads: int = 0) -> np.ndarray:
+    """fp16 (in_dtype HALF_F16) / bf16 (HALF_BF16) GEMM on raw uint16 codes,
+    sequential fp32 sum (src/tensor_core_attention.cu:13-66 restated)."""
+    A = _c(A, np.uint16); B = _c(B, np.uint16)
+    M, K = A.shape
+    N = B.shape[0] if b_layout == B_NK else B.shape[1]
+    r = None if rows is None else np.ascontiguousarray(rows, dtype=np.int32)
+    R = M if r is None else r.size
+    out = np.empty((R, N), dtype=np.float32 if out_dtype == OUT_F32 else np.uint16)
+    sa_arr, sb_arr, b_arr = _c(scale_a, np.float32), _c(scale_b, np.float32), _c(bias, np.float32)
+    nt = nthreads or (os.cpu_count() or 1)
+    lib().fko_gemm_half(_ptr(A), _ptr(B), _ptr(out), M, N, K, in_dtype, _ptr(sa_arr), _ptr(sb_arr), sa, sb,
+                        _ptr(b_arr), out_dtype, b_layout, _ptr(r), 0 if r is None else r.size, nt)
     return out

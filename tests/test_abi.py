@@ -110,6 +110,29 @@ def test_dispatch_i8_swiglu(M, I, K, expect):
     assert _lib.lib().fke_select_path_i8_swiglu(P, P, P, M, I, K, 0) == expect
 
 
+def test_half_gemm_rejects_bad_arguments_and_dispatch():
+    L = _lib.lib()
+    g = L.fke_gemm_half
+    F16, BF16 = _lib.IN_F16, _lib.IN_BF16
+    assert g(None, P, P, 4, 4, 64, F16, None, None, 1.0, 1.0, None, 0, 0, None) == INVALID
+    for dt in (_lib.IN_F32, -1, 3):
+        assert g(P, P, P, 4, 4, 64, dt, None, None, 1.0, 1.0, None, 0, 0, None) == INVALID
+    assert g(P, P, P, 4, 4, 64, F16, None, None, 1.0, 1.0, None, _lib.OUT_I32, 0, None) == INVALID
+    for M, N, K in [(0, 4, 64), (4, 0, 64), (4, 4, 0)]:
+        assert g(P, P, P, M, N, K, BF16, None, None, 1.0, 1.0, None, 0, 0, None) == INVALID
+    assert L.fke_launch_wmma_gemm_fp16(P, P, None, 4, 4, 64, 1.0, 0.0, None) == INVALID
+    sel = L.fke_select_path_half
+    assert sel(P, P, P, 8192, 8192, 8192, BF16, 0, 0) == _lib.PATH_MFMA
+    assert sel(P, P, P, 1, 4096, 4096, F16, 1, 0) == _lib.PATH_MFMA
+    assert sel(P, P, P, 256, 256, 96, F16, 0, 0) == _lib.PATH_GENERIC      # K % 64
+    assert sel(P, P, P, 256, 256, 256, F16, 0, 1) == _lib.PATH_GENERIC     # B [K,N]
+    assert sel(P + 2, P, P, 256, 256, 256, F16, 0, 0) == _lib.PATH_GENERIC
+    assert L.fke_gemm_half_on_path(_lib.PATH_MFMA, P, P, P, 64, 64, 96, F16, None, None, 1.0, 1.0, None, 0, 0,
+                                   None) == INVALID
+    assert L.fke_gemm_half_on_path(_lib.PATH_GEMV, P, P, P, 1, 64, 64, F16, None, None, 1.0, 1.0, None, 0, 0,
+                                   None) == INVALID
+
+
 def test_dropin_int8_rejects_k_not_multiple_of_4():
     """The reference kernel silently drops the K tail and misaligns rows when
     K % 4 != 0 (src/quantized_gemm.cu:28-30); the drop-in rejects it."""

@@ -477,3 +477,81 @@ def test_w8a8_swiglu_is_gemm_then_swiglu(oracle):
     g = oracle.w8a8_gemm(A, W[:I], sa=0.5, sb=0.25)
     u = oracle.w8a8_gemm(A, W[I:], sa=0.5, sb=0.25)
     assert np.array_equal(oracle.w8a8_swiglu(A, W, sa=0.5, sb=0.25), oracle.swiglu_f32(g, u))
+
+
+# ---------------------------------------------------------------- fp16 / bf16 GEMM
+
+def f16_bits(x):
+    return np.ascontiguousarray(x, dtype=np.float32).astype(np.float16).view(np.uint16)
+
+
+def bf16_bits_np(x):
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def test_f16_decode_exhaustive(oracle):
+    """All 65536 binary16 codes against numpy's float16 -> float32 cast (a
+    library routine): same bits, NaN for NaN codes."""
+    codes = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = oracle.f16_to_f32(codes)
+    want = codes.view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+    assert oracle.lib().fko_f16_to_f32(0x0001) == 2.0**-24   # smallest subnormal
+    assert oracle.lib().fko_f16_to_f32(0x7BFF) == 65504.0    # largest finite
+
+
+@pytest.mark.parametrize("in_dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("layout", [0, 1])
+def test_gemm_half_small_integers_exact(oracle, in_dtype, layout):
+    """Integer operands in [-8, 8] are exact in both formats and every partial
+    sum is an integer below 2^24, so any summation order gives the int64
+    matmul exactly.  A transposed B, a dropped K tail or a decode slip fails."""
+    r = rng(41)
+    M, N, K = 13, 21, 300
+    a = r.integers(-8, 9, (M, K)).astype(np.float32)
+    b = r.integers(-8, 9, (N, K)).astype(np.float32)
+    enc = f16_bits if in_dtype == "f16" else bf16_bits_np
+    code = oracle.HALF_F16 if in_dtype == "f16" else oracle.HALF_BF16
+    B = enc(b) if layout == 0 else np.ascontiguousarray(enc(b).T)
+    got = oracle.gemm_half(enc(a), B, code, b_layout=layout)
+    want = a.astype(np.int64) @ b.astype(np.int64).T
+    assert np.array_equal(got, want.astype(np.float32))
+
+
+def test_gemm_half_float64_bound_and_epilogue(oracle):
+    """Random fp16 operands: within the sequential-sum bound K * 2^-24 *
+    sum|a b| of the float64 product; with scales and bias, each output is
+    fmaf(acc, fp32(sa_m * sb_n), bias_n) of the unscaled result."""
+    r = rng(42)
+    M, N, K = 17, 29, 1000
+    a = f16_bits(r.standard_normal((M, K)))
+    b = f16_bits(r.standard_normal((N, K)))
+    af, bf = a.view(np.float16).astype(np.float64), b.view(np.float16).astype(np.float64)
+    acc = oracle.gemm_half(a, b, oracle.HALF_F16)
+    exact = af @ bf.T
+    bound = K * 2.0**-24 * (np.abs(af) @ np.abs(bf).T)
+    assert np.all(np.abs(acc - exact) <= bound)
+    sa = r.uniform(0.5, 2, M).astype(np.float32)
+    sb = r.uniform(0.5, 2, N).astype(np.float32)
+    bias = r.standard_normal(N).astype(np.float32)
+    y = oracle.gemm_half(a, b, oracle.HALF_F16, sa, sb, bias=bias)
+    s = (sa[:, None] * sb[None, :]).astype(np.float32)
+    want = (acc.astype(np.float64) * s.astype(np.float64) + bias.astype(np.float64)).astype(np.float32)
+    assert np.array_equal(y, want)
+    yb = oracle.gemm_half(a, b, oracle.HALF_F16, sa, sb, bias=bias, out_dtype=oracle.OUT_BF16)
+    assert np.array_equal(yb, bf16_bits_np(y))
+
+
+def test_gemm_half_sequential_order_case(oracle):
+    """Products 1, 2^24, -2^24 summed k = 0, 1, 2: 1 + 2^24 rounds to 2^24
+    (ties to even), so the sequential fp32 sum is 0 (any order that adds the
+    two large products first gives 1).  Pins the oracle's k-ascending order."""
+    a = f16_bits(np.array([[1.0, 4096.0, -4096.0]]))
+    b = f16_bits(np.array([[1.0, 4096.0, 4096.0]]))
+    assert oracle.gemm_half(a, b, oracle.HALF_F16)[0, 0] == 0.0
+    a2 = f16_bits(np.array([[4096.0, -4096.0, 1.0]]))
+    b2 = f16_bits(np.array([[4096.0, 4096.0, 1.0]]))
+    assert oracle.gemm_half(a2, b2, oracle.HALF_F16)[0, 0] == 1.0
