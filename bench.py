@@ -8,7 +8,7 @@ over 8 distinct 56 MiB buffers so the 256 MiB MALL cannot hold them) is timed in
 the same run and reported under "decode_gemv".  Inputs are random (torch RNG on
 the device), never zero-filled.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--extra | --swiglu] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--extra | --swiglu --half] [--vendor] [--no-cpu]
 """
 import argparse
 import json
@@ -24,6 +24,7 @@ for p in (REPO, PKG):
 
 PEAK_INT8_TOPS = 5000.0   # MI355X dense INT8 MFMA, published (5.0 POP/s)
 PEAK_FP8_TFLOPS = 5000.0  # MI355X dense FP8 MFMA, published
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 / fp16 MFMA, published
 PEAK_HBM_GBS = 8000.0     # MI355X HBM3E, published (8 TB/s)
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic.json")
 
@@ -54,6 +55,9 @@ def parse():
     ap.add_argument("--gemv-launches", type=int, default=400)
     ap.add_argument("--extra", action="store_true", help="also time configs 2 and 4 and GEMV M=4,16")
     ap.add_argument("--swiglu", action="store_true", help="also time the SwiGLU configs (part of --extra)")
+    ap.add_argument("--half", action="store_true", help="also time the fp16/bf16 GEMM (part of --extra)")
+    ap.add_argument("--vendor", action="store_true",
+                    help="also time the vendor library (hipBLASLt through torch) on the 8192^3 GEMMs, for context")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -152,8 +156,14 @@ def main():
         del src, dst
     if args.extra:
         line["extra"] = extra_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args)
-    elif args.swiglu:
-        line["extra"] = swiglu_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args)
+    elif args.swiglu or args.half:
+        line["extra"] = {}
+        if args.swiglu:
+            line["extra"].update(swiglu_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args))
+        if args.half:
+            line["extra"].update(half_configs(torch, L, _lib, dev, gen, timed, args))
+    if args.vendor:
+        line["vendor_context"] = vendor_configs(torch, dev, gen, timed, args)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(line), flush=True)
@@ -267,6 +277,7 @@ def extra_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
     res["fp8_8192cubed_bf16_Bnk_nan_codes"] = {"ms": round(ms, 4), "TFLOPS": round(t, 1),
                                                "frac": round(t / PEAK_FP8_TFLOPS, 4)}
     del A8, B8, C
+    res.update(half_configs(torch, L, _lib, dev, gen, timed, args))
     for m in (4, 16):
         res[f"gemv_M{m}"] = gemv_bench(torch, L, _lib, dev, gen, m, args.gemv_buffers, args.gemv_launches)
     # per-token INT8 quantiser in front of the W8A8 GEMM: bf16 activations of C3 (4096 x 4096),
@@ -289,6 +300,56 @@ def extra_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
                                            "kernel": "quant_rows_kernel<bf16>"}
     del Xs, Q, S
     res.update(swiglu_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args))
+    return res
+
+
+def vendor_configs(torch, dev, gen, timed, args):
+    """The vendor library (hipBLASLt through torch) on the 8192^3 GEMMs, timed like
+    this library's: INT8 (torch._int_mm, int32 out), FP8 e4m3 (torch._scaled_mm,
+    bf16 out), bf16 and fp16 (A @ B^T, same-type out).  Context only, not a bench figure."""
+    res = {}
+    M = N = K = 8192
+    A = torch.randint(-127, 128, (M, K), dtype=torch.int8, device=dev, generator=gen)
+    B = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=gen)
+    ms = timed(lambda: torch._int_mm(A, B.t()), args.steps, args.warmup)
+    res["int8_8192cubed_i32out_torch_int_mm"] = {"ms": round(ms, 4), "TOPS": round(2.0 * M * N * K / ms / 1e9, 1)}
+    del A, B
+    try:
+        a8 = torch.randn((M, K), device=dev, generator=gen).to(torch.float8_e4m3fn)
+        b8 = torch.randn((N, K), device=dev, generator=gen).to(torch.float8_e4m3fn)
+        one = torch.tensor(1.0, device=dev)
+        ms = timed(lambda: torch._scaled_mm(a8, b8.t(), scale_a=one, scale_b=one, out_dtype=torch.bfloat16),
+                   args.steps, args.warmup)
+        res["fp8_8192cubed_bf16out_torch_scaled_mm"] = {"ms": round(ms, 4),
+                                                       "TFLOPS": round(2.0 * M * N * K / ms / 1e9, 1)}
+        del a8, b8
+    except (RuntimeError, AttributeError) as e:  # the op may be absent for this device / build
+        res["fp8_8192cubed_bf16out_torch_scaled_mm"] = {"error": str(e)[:200]}
+    for name, dt in (("bf16", torch.bfloat16), ("f16", torch.float16)):
+        Ah = torch.randn((M, K), device=dev, generator=gen).to(dt)
+        Bh = torch.randn((N, K), device=dev, generator=gen).to(dt)
+        ms = timed(lambda: Ah @ Bh.t(), args.steps, args.warmup)
+        res[f"{name}_8192cubed_torch_matmul"] = {"ms": round(ms, 4), "TFLOPS": round(2.0 * M * N * K / ms / 1e9, 1)}
+        del Ah, Bh
+    return res
+
+
+def half_configs(torch, L, _lib, dev, gen, timed, args):
+    """fp16 / bf16 GEMM 8192^3 on the MFMA engine (B [N,K], bf16 out)."""
+    res = {}
+    sh = torch.cuda.current_stream(dev).cuda_stream
+    M = N = K = 8192
+    for name, dt, code in (("bf16", torch.bfloat16, _lib.IN_BF16), ("f16", torch.float16, _lib.IN_F16)):
+        Ah = torch.randn((M, K), device=dev, generator=gen).to(dt)
+        Bh = torch.randn((N, K), device=dev, generator=gen).to(dt)
+        C = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        ms = timed(lambda: L.fke_gemm_half(Ah.data_ptr(), Bh.data_ptr(), C.data_ptr(), M, N, K, code, None, None,
+                                           1.0, 1.0, None, _lib.OUT_BF16, _lib.B_NK, sh), args.steps, args.warmup)
+        t = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+        res[f"{name}_gemm_8192cubed_bf16out"] = {"ms": round(ms, 4), "TFLOPS": round(t, 1),
+                                                 "frac": round(t / PEAK_BF16_TFLOPS, 4),
+                                                 "kernel": f"gemm_mfma_kernel<{name}, nk, bf16>"}
+        del Ah, Bh, C
     return res
 
 

@@ -400,8 +400,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
     // A stage is NKS groups of 16 MFMAs.  Group g runs the MFMAs of one
     // fragment set (g = 0: the previous stage's last step, carried across
     // the barrier; g > 0: step g-1) while the LDS reads of step g fill the
-    // other set, and carries copy slots of the next stage (INT8: spread over
-    // all groups but the last).  Within a group every memory instruction is
+    // other set, and carries copy slots of the next stage (INT8, fp16, bf16:
+    // 6 / 6 / 4 / 0 over the four groups; FP8: all in the first of its
+    // two).  Within a group every memory instruction is
     // paired with an MFMA, so it issues in the MFMA's shadow instead of
     // stalling the matrix pipe.
     constexpr int PER_GROUP = (NSLOT + NKS - 2) / (NKS - 1);
@@ -442,11 +443,15 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
                   kc);
         } else {
             static_assert(NKS == 2, "k steps per stage");
-            // FP8 steps are twice as long: the second group still leaves the
-            // copies it carries a full group of MFMAs to land.
-            constexpr int P = NSLOT / 2;
-            group(S{}, I0{}, std::integral_constant<int, P>{}, f1, f0, cur, 0, nxt, kc);
-            group(S{}, std::integral_constant<int, P>{}, std::integral_constant<int, NSLOT>{}, f0, f1, cur, 1, nxt, kc);
+            // FP8 steps are twice as long (64-cycle MFMAs): all copies ride
+            // in the first group, one per MFMA, and the whole second group
+            // (16 x 64 cycles) is left for them to land before the stage's
+            // vmcnt(0).  Splitting them 8 / 8 left the last copies one MFMA
+            // before that wait and measured 5 % slower (438-444 us against
+            // 416-422 us at 8192^3, both B layouts).
+            group(S{}, I0{}, std::integral_constant<int, NSLOT>{}, f1, f0, cur, 0, nxt, kc);
+            group(S{}, std::integral_constant<int, NSLOT>{}, std::integral_constant<int, NSLOT>{}, f0, f1, cur, 1, nxt,
+                  kc);
         }
         wait_lgkm0();  // last step's fragments in registers (f1): cur may be overwritten after the barrier
         wait_vm0();    // this wave's share of stage kt+1 has landed

@@ -1,13 +1,17 @@
 /*
  * flash_engine.h — umbrella header of the MI355X build of the quantized GEMM
  * path.  Mirrors reference include/flash_engine.h:17-31 (version constants,
- * get_version, print_device_info).  The reference's other module headers
- * (attention, decoding, RMSNorm, ...) are not part of this library.
+ * get_version, print_device_info).  Of the reference's module headers it
+ * carries quantized_gemm.cuh, tensor_core_gemm.cuh (the GEMM) and
+ * fused_activations.cuh (SwiGLU); attention, decoding, RMSNorm and the others
+ * are not part of this library.
  */
 #pragma once
 
+#include "fused_activations.cuh"
 #include "hip_utils.h"
 #include "quantized_gemm.cuh"
+#include "tensor_core_gemm.cuh"
 
 namespace flash_engine {
 

@@ -1,7 +1,10 @@
 // Drop-in check of the C++ host API (include/quantized_gemm.cuh,
+// include/tensor_core_gemm.cuh, include/fused_activations.cuh,
 // include/flash_engine.h): the reference's own GEMM test
 // (tests/test_quantized_gemm.cu:9-86 of flash-kernel-engine) restated against
-// the HIP API, plus the FP8 launcher and the argument-validation contract.
+// the HIP API, plus the FP8 launcher, the fp16 WMMA-GEMM launcher, SwiGLU on
+// the reference's Python test vector (python/tests/test_correctness.py:166-176)
+// and the argument-validation contract.
 // Built by the host compiler alone and linked against libfke_qgemm.so.
 //
 //   test_quantized_gemm_dropin --host-only   validation checks only (no GPU)
@@ -15,6 +18,9 @@
 
 using namespace flash_engine;
 using namespace flash_engine::quantized;
+using flash_engine::activation::launch_fused_swiglu_fp16;
+using flash_engine::activation::launch_fused_swiglu_fp32;
+using flash_engine::tensor_core::launch_wmma_gemm_fp16;
 
 static int host_checks() {
     int bad = 0;
@@ -34,6 +40,11 @@ static int host_checks() {
     expect_invalid(launch_int8_gemm_dp4a(nullptr, p8, pf, 1.f, 1.f, QuantGEMMConfig(8, 8, 8)), "A=null");
     expect_invalid(launch_fp8_gemm_scaled(pu, nullptr, pf, 1.f, 1.f, QuantGEMMConfig(8, 8, 8)), "B=null");
     expect_invalid(launch_fp8_gemm_scaled(pu, pu, pf, 1.f, 1.f, QuantGEMMConfig(-1, 8, 8)), "M<0");
+    const half* ph = reinterpret_cast<const half*>(16);
+    expect_invalid(launch_wmma_gemm_fp16(ph, nullptr, pf, 8, 8, 8), "wmma B=null");
+    expect_invalid(launch_wmma_gemm_fp16(ph, ph, pf, 8, 8, 0), "wmma K=0");
+    expect_invalid(launch_fused_swiglu_fp32(pf, nullptr, pf, 8), "swiglu up=null");
+    expect_invalid(launch_fused_swiglu_fp32(pf, pf, pf, -1), "swiglu n<0");
     if (std::strcmp(get_version(), "1.2.0") != 0 || VERSION_MAJOR != 1 || VERSION_MINOR != 2 ||
         VERSION_PATCH != 0) {
         std::cerr << "[FAIL] version\n";
@@ -140,10 +151,70 @@ int main(int argc, char** argv) {
     } else {
         std::cout << "[PASS] FP8 drop-in GEMM within 2e-2 of the reference loop\n";
     }
+
+    // ---- fp16 WMMA-GEMM launcher: small-integer operands (exact sums), alpha
+    // ---- applied, beta ignored, C overwritten ----
+    constexpr int HM = 48, HN = 80, HK = 192;
+    std::vector<half> hA(HM * HK), hB(HN * HK);
+    std::vector<float> hC(HM * HN), href(HM * HN);
+    for (int i = 0; i < HM * HK; ++i) hA[i] = __float2half(static_cast<float>((i * 7 + 3) % 11 - 5));
+    for (int i = 0; i < HN * HK; ++i) hB[i] = __float2half(static_cast<float>((i * 5 + 1) % 9 - 4));
+    for (int m = 0; m < HM; ++m)
+        for (int n = 0; n < HN; ++n) {
+            long acc = 0;
+            for (int k = 0; k < HK; ++k)
+                acc += static_cast<long>((( (m * HK + k) * 7 + 3) % 11) - 5) *
+                       static_cast<long>((((n * HK + k) * 5 + 1) % 9) - 4);
+            href[m * HN + n] = static_cast<float>(acc) * 0.25f;
+        }
+    half *d_hA, *d_hB;
+    float* d_hC;
+    HIP_CHECK(hipMalloc(&d_hA, hA.size() * sizeof(half)));
+    HIP_CHECK(hipMalloc(&d_hB, hB.size() * sizeof(half)));
+    HIP_CHECK(hipMalloc(&d_hC, hC.size() * sizeof(float)));
+    HIP_CHECK(hipMemcpy(d_hA, hA.data(), hA.size() * sizeof(half), hipMemcpyHostToDevice));
+    HIP_CHECK(hipMemcpy(d_hB, hB.data(), hB.size() * sizeof(half), hipMemcpyHostToDevice));
+    HIP_CHECK(hipMemset(d_hC, 0xFF, hC.size() * sizeof(float)));  // NaN: must be overwritten
+    HIP_CHECK(launch_wmma_gemm_fp16(d_hA, d_hB, d_hC, HM, HN, HK, 0.25f, 2.0f));
+    HIP_CHECK(hipDeviceSynchronize());
+    HIP_CHECK(hipMemcpy(hC.data(), d_hC, hC.size() * sizeof(float), hipMemcpyDeviceToHost));
+    size_t hmis = 0;
+    for (size_t i = 0; i < hC.size(); ++i)
+        if (std::memcmp(&hC[i], &href[i], 4) != 0) ++hmis;
+    if (hmis) {
+        std::cerr << "[FAIL] fp16 WMMA-GEMM drop-in: " << hmis << " mismatches\n";
+        ++bad;
+    } else {
+        std::cout << "[PASS] fp16 WMMA-GEMM drop-in exact on integer operands (alpha applied, beta ignored)\n";
+    }
+
+    // ---- SwiGLU fp32 on the reference's test vector: max abs diff < 1e-6 ----
+    const float gate[5] = {-2.0f, -0.5f, 0.0f, 0.5f, 2.0f}, up[5] = {1.0f, 2.0f, 3.0f, 4.0f, 5.0f};
+    float sw[5];
+    float* d_sw;
+    HIP_CHECK(hipMalloc(&d_sw, 3 * 5 * sizeof(float)));
+    HIP_CHECK(hipMemcpy(d_sw, gate, sizeof(gate), hipMemcpyHostToDevice));
+    HIP_CHECK(hipMemcpy(d_sw + 5, up, sizeof(up), hipMemcpyHostToDevice));
+    HIP_CHECK(launch_fused_swiglu_fp32(d_sw, d_sw + 5, d_sw + 10, 5));
+    HIP_CHECK(hipDeviceSynchronize());
+    HIP_CHECK(hipMemcpy(sw, d_sw + 10, sizeof(sw), hipMemcpyDeviceToHost));
+    float sdiff = 0.0f;
+    for (int i = 0; i < 5; ++i)
+        sdiff = std::fmax(sdiff, std::fabs(sw[i] - (gate[i] / (1.0f + std::exp(-gate[i]))) * up[i]));
+    if (!(sdiff < 1e-6f)) {
+        std::cerr << "[FAIL] SwiGLU drop-in: max abs diff " << sdiff << "\n";
+        ++bad;
+    } else {
+        std::cout << "[PASS] SwiGLU drop-in on the reference test vector (max abs diff " << sdiff << ")\n";
+    }
     HIP_CHECK(hipFree(d_A));
     HIP_CHECK(hipFree(d_B));
     HIP_CHECK(hipFree(d_C));
     HIP_CHECK(hipFree(d_fA));
     HIP_CHECK(hipFree(d_fB));
+    HIP_CHECK(hipFree(d_hA));
+    HIP_CHECK(hipFree(d_hB));
+    HIP_CHECK(hipFree(d_hC));
+    HIP_CHECK(hipFree(d_sw));
     return bad ? 1 : 0;
 }
