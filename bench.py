@@ -8,7 +8,7 @@ over 8 distinct 56 MiB buffers so the 256 MiB MALL cannot hold them) is timed in
 the same run and reported under "decode_gemv".  Inputs are random (torch RNG on
 the device), never zero-filled.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--extra | --swiglu --half] [--vendor] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--extra | --fp8 --swiglu --half] [--vendor] [--no-cpu]
 """
 import argparse
 import json
@@ -56,6 +56,7 @@ def parse():
     ap.add_argument("--extra", action="store_true", help="also time configs 2 and 4 and GEMV M=4,16")
     ap.add_argument("--swiglu", action="store_true", help="also time the SwiGLU configs (part of --extra)")
     ap.add_argument("--half", action="store_true", help="also time the fp16/bf16 GEMM (part of --extra)")
+    ap.add_argument("--fp8", action="store_true", help="also time the FP8 e4m3 GEMM 8192^3 (part of --extra)")
     ap.add_argument("--vendor", action="store_true",
                     help="also time the vendor library (hipBLASLt through torch) on the 8192^3 GEMMs, for context")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -156,8 +157,10 @@ def main():
         del src, dst
     if args.extra:
         line["extra"] = extra_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args)
-    elif args.swiglu or args.half:
+    elif args.swiglu or args.half or args.fp8:
         line["extra"] = {}
+        if args.fp8:
+            line["extra"].update(fp8_configs(torch, L, _lib, dev, gen, timed, args))
         if args.swiglu:
             line["extra"].update(swiglu_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args))
         if args.half:
@@ -255,20 +258,13 @@ def extra_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
     t = 2.0 * M * N * K / (ms * 1e-3) / 1e12
     res["int8_8192cubed_f32_Bkn"] = {"ms": round(ms, 4), "TOPS": round(t, 1), "frac": round(t / PEAK_INT8_TOPS, 4)}
     del A, B, C
-    # config 4: FP8 e4m3 8192^3, B [K,N] (reference layout) and [N,K], bf16 out
+    res.update(fp8_configs(torch, L, _lib, dev, gen, timed, args))
+    # FP8 with 1 in 97 codes of A set to 0x7F: tiles rerun with NaN codes cleared
     M = N = K = 8192
     A8 = torch.randint(0, 256, (M, K), dtype=torch.uint8, device=dev, generator=gen)
     A8[(A8 & 0x7F) == 0x7F] = 0
     B8 = torch.randint(0, 256, (K, N), dtype=torch.uint8, device=dev, generator=gen)
     B8[(B8 & 0x7F) == 0x7F] = 0
-    C = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
-    for name, lay in (("kn", _lib.B_KN), ("nk", _lib.B_NK)):
-        ms = timed(lambda: L.fke_qgemm_f8(A8.data_ptr(), B8.data_ptr(), C.data_ptr(), M, N, K, 0.01, 0.01,
-                                          None, _lib.OUT_BF16, lay, sh), args.steps, args.warmup)
-        t = 2.0 * M * N * K / (ms * 1e-3) / 1e12
-        res[f"fp8_8192cubed_bf16_B{name}"] = {"ms": round(ms, 4), "TFLOPS": round(t, 1),
-                                              "frac": round(t / PEAK_FP8_TFLOPS, 4)}
-    # the same with 1 in 97 codes of A set to 0x7F: tiles rerun with NaN codes cleared
     A8.view(-1)[::97] = 0x7F
     C = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
     ms = timed(lambda: L.fke_qgemm_f8(A8.data_ptr(), B8.data_ptr(), C.data_ptr(), M, N, K, 0.01, 0.01,
@@ -300,6 +296,26 @@ def extra_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
                                            "kernel": "quant_rows_kernel<bf16>"}
     del Xs, Q, S
     res.update(swiglu_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args))
+    return res
+
+
+def fp8_configs(torch, L, _lib, dev, gen, timed, args):
+    """Config 4: FP8 e4m3 8192^3, B [K,N] (reference layout) and [N,K], bf16 out."""
+    res = {}
+    sh = torch.cuda.current_stream(dev).cuda_stream
+    M = N = K = 8192
+    A8 = torch.randint(0, 256, (M, K), dtype=torch.uint8, device=dev, generator=gen)
+    A8[(A8 & 0x7F) == 0x7F] = 0
+    B8 = torch.randint(0, 256, (K, N), dtype=torch.uint8, device=dev, generator=gen)
+    B8[(B8 & 0x7F) == 0x7F] = 0
+    C = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    for name, lay in (("kn", _lib.B_KN), ("nk", _lib.B_NK)):
+        ms = timed(lambda: L.fke_qgemm_f8(A8.data_ptr(), B8.data_ptr(), C.data_ptr(), M, N, K, 0.01, 0.01,
+                                          None, _lib.OUT_BF16, lay, sh), args.steps, args.warmup)
+        t = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+        res[f"fp8_8192cubed_bf16_B{name}"] = {"ms": round(ms, 4), "TFLOPS": round(t, 1),
+                                              "frac": round(t / PEAK_FP8_TFLOPS, 4)}
+    del A8, B8, C
     return res
 
 
