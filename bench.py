@@ -31,7 +31,7 @@ TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic.json")
 
 def gemv_kernel(M):
     """Decode kernel the dispatcher picks for M rows (K % 4096 == 0, B [N,K])."""
-    return "gemv_rows_kernel" if M == 1 else "gemv_i8_kernel" if M <= 4 else "gemv_mfma_kernel"
+    return "gemv_rows_kernel" if M <= 4 else "gemv_mfma_kernel"
 
 
 def traffic(key):

@@ -5,17 +5,18 @@
 // problem: the B panel is streamed once with 128-bit coalesced loads and no
 // MFMA is used.
 //
-// Two kernels:
-//  * gemv_rows_kernel (M == 1; instantiable up to 4 rows): one B row per wave
-//    over the full K.  Lane l reads 16-byte chunks l, l+64, l+128, l+192 of
-//    each 256-chunk block (one wave load = 1 KiB contiguous) with non-temporal
-//    buffer loads, keeps the M activation chunks in registers,
-//    and reduces its partial sums with DPP row rotations, one ds_swizzle and two
-//    readlanes - no LDS and no barrier, so a wave retires as soon as its row is
-//    done and the load queue never drains.
-//  * gemv_i8_kernel (2 <= M <= 4, and larger M when the MFMA kernel's 32-bit
-//    offsets do not reach), described below; it amortises the activation
-//    chunks over R rows per wave, which the row kernel cannot.
+// Three kernels:
+//  * gemv_rows_kernel (M <= 4): NB B rows per wave (one at M = 1, two for
+//    M = 2..4 and for SwiGLU's gate/up pairs) over the full K.  Lane l reads
+//    16-byte chunks l, l+64, l+128, l+192 of each 256-chunk block (one wave
+//    load = 1 KiB contiguous) with non-temporal buffer loads, keeps the M
+//    activation chunks in registers for the NB rows, and reduces its partial
+//    sums with DPP row rotations, one ds_swizzle and two readlanes - no LDS
+//    and no barrier, so a wave retires as soon as its rows are done and the
+//    load queue never drains.
+//  * gemv_i8_kernel (5 <= M <= 16 when the MFMA kernel's 32-bit offsets do
+//    not reach), described below; it amortises the activation chunks over R
+//    rows per wave.
 //  * gemv_mfma_kernel (5 <= M <= 16), described at its definition.
 //
 // gemv_i8_kernel: workgroup = 4 waves = R consecutive B rows (output columns n0..n0+R-1).
@@ -415,11 +416,14 @@ bool skinny_offsets_fit(const GemmArgs& p) {
     return (static_cast<int64_t>(p.N < 16 ? 16 : p.N) + 32) * p.K <= INT32_MAX;
 }
 
+// M = 2..4 (and SwiGLU up to 4): the row kernel with two weight rows per
+// wave, which reuses each activation chunk for both rows; measured 4-8 %
+// faster than the split-K kernel at N = 14336, K = 4096.
 template <bool FULLK>
 hipError_t launch_rows_m(const GemmArgs& p, hipStream_t s) {
     if (p.M <= 1) return launch_rows<1, FULLK>(p, s);
-    if (p.M <= 2) return launch_rows<2, FULLK>(p, s);
-    return launch_rows<4, FULLK>(p, s);
+    if (p.M <= 2) return launch_rows<2, FULLK, 2>(p, s);
+    return launch_rows<4, FULLK, 2>(p, s);
 }
 
 }  // namespace
@@ -438,9 +442,7 @@ hipError_t launch_gemv_i8(const GemmArgs& p, hipStream_t s) {
         if (p.M <= 4) return p.K % 4096 == 0 ? launch_rows_m<true>(p, s) : launch_rows_m<false>(p, s);
         return launch_mfma_skinny(p, s);
     }
-    if (p.M <= 1) return p.K % 4096 == 0 ? launch_rows<1, true>(p, s) : launch_rows<1, false>(p, s);
-    if (p.M <= 2) return launch_t<2, 16>(p, s);
-    if (p.M <= 4) return launch_t<4, 8>(p, s);
+    if (p.M <= 4) return p.K % 4096 == 0 ? launch_rows_m<true>(p, s) : launch_rows_m<false>(p, s);
     if (skinny_offsets_fit(p)) return launch_mfma_skinny(p, s);
     if (p.M <= 8) return launch_t<8, 8>(p, s);
     return launch_t<16, 4>(p, s);

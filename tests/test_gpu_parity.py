@@ -201,6 +201,33 @@ def test_c2_decode_full(oracle, dev, M):
     assert_same(got, oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, "bf16"), f"c2 M={M}")
 
 
+@pytest.mark.parametrize("M", [6, 9])
+def test_decode_weight_past_2gib(oracle, dev, M):
+    """A 2.1 GB weight (N*K > 2^31): the skinny MFMA kernel's 32-bit offsets do
+    not reach, so 5 <= M <= 16 runs the split-K sdot kernel (64-bit row bases).
+    The weight is generated on the device; sampled output columns (both ends and
+    the middle) are checked against the oracle on host copies of those rows."""
+    N, K = (1 << 31) // 4096 + 64, 4096
+    say("decode weight past 2 GiB", M, N, K)
+    assert _lib.lib().fke_select_path_i8(4096, 4096, 4096, M, N, K, 1, 0) == _lib.PATH_GEMV
+    g = torch.Generator(device=dev)
+    g.manual_seed(77 + M)
+    Bd = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g)
+    A = oracle.gen_i8_clipped_normal((M, K), 500 + M, 30.0)
+    sa = oracle.gen_f32_uniform((M,), 501, 0.001, 0.02)
+    sb = oracle.gen_f32_uniform((N,), 502, 0.001, 0.02)
+    bias = oracle.gen_f32_normal((N,), 503, 0.0, 0.02)
+    out = ops.w8a8_gemm(dev_t(A), Bd, dev_t(sa), dev_t(sb), dev_t(bias), out_dtype=torch.float32, path="gemv")
+    torch.cuda.synchronize()
+    cols = np.concatenate([np.arange(0, 64), np.arange(N // 2, N // 2 + 64), np.arange(N - 64, N)])
+    Bs = Bd[torch.from_numpy(cols).long().cuda()].cpu().numpy()
+    del Bd
+    acc = oracle.w8a8_acc(A, Bs, nthreads=NTH)
+    ref = oracle.w8a8_epilogue(acc, sa, sb[cols], 1.0, 1.0, bias[cols], oracle.OUT_F32)
+    got = out[:, torch.from_numpy(cols).long().cuda()].cpu().numpy()
+    assert_same(got, ref, f"decode past 2 GiB M={M}")
+
+
 def test_c3_prefill_full(oracle, dev):
     """Config 2: 4096x11008x4096, bf16 out: every output checked."""
     M, N, K = 4096, 11008, 4096
