@@ -8,7 +8,7 @@ over 8 distinct 56 MiB buffers so the 256 MiB MALL cannot hold them) is timed in
 the same run and reported under "decode_gemv".  Inputs are random (torch RNG on
 the device), never zero-filled.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--extra | --fp8 --swiglu --half] [--vendor] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--extra | --fp8 --swiglu --half] [--vendor] [--data-sweep] [--no-cpu]
 """
 import argparse
 import json
@@ -57,6 +57,8 @@ def parse():
     ap.add_argument("--swiglu", action="store_true", help="also time the SwiGLU configs (part of --extra)")
     ap.add_argument("--half", action="store_true", help="also time the fp16/bf16 GEMM (part of --extra)")
     ap.add_argument("--fp8", action="store_true", help="also time the FP8 e4m3 GEMM 8192^3 (part of --extra)")
+    ap.add_argument("--data-sweep", action="store_true",
+                    help="also time the headline GEMM on zero, constant and narrow-range operands (clock vs data)")
     ap.add_argument("--vendor", action="store_true",
                     help="also time the vendor library (hipBLASLt through torch) on the 8192^3 GEMMs, for context")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -167,6 +169,8 @@ def main():
             line["extra"].update(half_configs(torch, L, _lib, dev, gen, timed, args))
     if args.vendor:
         line["vendor_context"] = vendor_configs(torch, dev, gen, timed, args)
+    if args.data_sweep:
+        line["data_sweep"] = data_sweep(torch, L, _lib, dev, gen, timed, args)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(line), flush=True)
@@ -296,6 +300,31 @@ def extra_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
                                            "kernel": "quant_rows_kernel<bf16>"}
     del Xs, Q, S
     res.update(swiglu_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args))
+    return res
+
+
+def data_sweep(torch, L, _lib, dev, gen, timed, args):
+    """The headline INT8 GEMM (8192^3, fp32 out, scalar scales) on all-zero, all-one,
+    uniform [-3,3] and uniform [-127,127] operands, in that order: the same
+    instructions on data of different switching activity, to show the power-limited
+    clock (pair with rocprofv3 --pmc GRBM_GUI_ACTIVE for the cycle counts)."""
+    res = {}
+    sh = torch.cuda.current_stream(dev).cuda_stream
+    M = N = K = 8192
+    C = torch.empty((M, N), dtype=torch.float32, device=dev)
+    kinds = (("zeros", None), ("ones", None), ("uniform_-3_3", 3), ("uniform_-127_127", 127))
+    for name, r in kinds:
+        if r is None:
+            fill = 0 if name == "zeros" else 1
+            A = torch.full((M, K), fill, dtype=torch.int8, device=dev)
+            B = torch.full((N, K), fill, dtype=torch.int8, device=dev)
+        else:
+            A = torch.randint(-r, r + 1, (M, K), dtype=torch.int8, device=dev, generator=gen)
+            B = torch.randint(-r, r + 1, (N, K), dtype=torch.int8, device=dev, generator=gen)
+        ms = timed(lambda: L.fke_qgemm_i8(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, None, None, 1.0, 1.0,
+                                          None, _lib.OUT_F32, _lib.B_NK, sh), args.steps, args.warmup)
+        res[name] = {"ms": round(ms, 4), "TOPS": round(2.0 * M * N * K / ms / 1e9, 1)}
+        del A, B
     return res
 
 
