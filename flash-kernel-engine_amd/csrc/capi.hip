@@ -15,6 +15,8 @@ namespace {
 
 using fke::GemmArgs;
 
+int run_i8(int path, const GemmArgs& p, void* stream);
+
 bool common_args_ok(const void* A, const void* B, const void* C, int M, int N, int K,
                     int b_layout) {
     if (!A || !B || !C) return false;
@@ -54,6 +56,28 @@ GemmArgs make_args(const void* A, const void* B, void* C, int M, int N, int K, c
     p.b_layout = b_layout;
     p.swiglu = 0;
     return p;
+}
+
+// Workspace of the unfused W8A8 linear: int8 codes [M,K] at offset 0, then the
+// fp32 row scales [M] at the next 256-byte boundary.
+size_t w8a8_ws_scale_offset(int M, int K) {
+    return (static_cast<size_t>(M) * static_cast<size_t>(K) + 255) & ~static_cast<size_t>(255);
+}
+size_t w8a8_ws_bytes(int M, int K) { return w8a8_ws_scale_offset(M, K) + 4 * static_cast<size_t>(M); }
+
+// Shared body of fke_w8a8_linear / fke_w8a8_swiglu_linear.  p describes the
+// GEMM on the int8 codes with A = X: the quantiser writes X's codes and row
+// scales into the workspace, then the GEMM reads them there.
+int run_w8a8_from_float(GemmArgs p, int in_dtype, void* workspace, size_t workspace_bytes, void* stream) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (!workspace || workspace_bytes < w8a8_ws_bytes(p.M, p.K)) return hipErrorInvalidValue;
+    int8_t* Q = static_cast<int8_t*>(workspace);
+    float* S = reinterpret_cast<float*>(static_cast<char*>(workspace) + w8a8_ws_scale_offset(p.M, p.K));
+    const hipError_t st = fke::launch_quant_rows(p.A, in_dtype, p.M, p.K, Q, S, s);
+    if (st != hipSuccess) return st;
+    p.A = Q;
+    p.scale_a = S;
+    return run_i8(FKE_PATH_AUTO, p, stream);
 }
 
 // SwiGLU GEMM: B is the merged [2I, K] weight; the kernels see N = 2I.
@@ -185,6 +209,30 @@ int fke_select_path_i8_swiglu(const void* A, const void* W, const void* H, int M
     if (!swiglu_args_ok(A, W, H, M, I, K, out_dtype)) return -1;
     return pick_i8(make_swiglu_args(A, W, const_cast<void*>(H), M, I, K, nullptr, nullptr, 1.f, 1.f, nullptr,
                                     out_dtype));
+}
+
+size_t fke_w8a8_linear_workspace_size(int M, int K) {
+    if (M < 1 || K < 1) return 0;
+    return w8a8_ws_bytes(M, K);
+}
+
+int fke_w8a8_linear(const void* X, int in_dtype, const int8_t* W, void* Y, int M, int N, int K, const float* w_scale,
+                    float sb, const float* bias, int out_dtype, void* workspace, size_t workspace_bytes,
+                    void* stream) {
+    if (!common_args_ok(X, W, Y, M, N, K, FKE_B_NK)) return hipErrorInvalidValue;
+    if (in_dtype != FKE_IN_F32 && in_dtype != FKE_IN_BF16) return hipErrorInvalidValue;
+    if (out_dtype != FKE_OUT_F32 && out_dtype != FKE_OUT_BF16) return hipErrorInvalidValue;
+    return run_w8a8_from_float(make_args(X, W, Y, M, N, K, nullptr, w_scale, 1.0f, sb, bias, out_dtype, FKE_B_NK),
+                               in_dtype, workspace, workspace_bytes, stream);
+}
+
+int fke_w8a8_swiglu_linear(const void* X, int in_dtype, const int8_t* W, void* H, int M, int I, int K,
+                           const float* w_scale, float sb, const float* bias, int out_dtype, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+    if (!swiglu_args_ok(X, W, H, M, I, K, out_dtype)) return hipErrorInvalidValue;
+    if (in_dtype != FKE_IN_F32 && in_dtype != FKE_IN_BF16) return hipErrorInvalidValue;
+    return run_w8a8_from_float(make_swiglu_args(X, W, H, M, I, K, nullptr, w_scale, 1.0f, sb, bias, out_dtype),
+                               in_dtype, workspace, workspace_bytes, stream);
 }
 
 int fke_swiglu(const void* gate, const void* up, void* out, int64_t n, int dtype, void* stream) {

@@ -100,6 +100,47 @@ __device__ __forceinline__ float swiglu_pair(float g, float u) {
     return (g * s) * u;
 }
 
+// ---- per-token INT8 quantisation (quant_i8.hip) ----
+
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, __shfl_xor(v, 1));
+    v = fmaxf(v, __shfl_xor(v, 2));
+    v = fmaxf(v, __shfl_xor(v, 4));
+    v = fmaxf(v, __shfl_xor(v, 8));
+    v = fmaxf(v, __shfl_xor(v, 16));
+    v = fmaxf(v, __shfl_xor(v, 32));
+    return v;
+}
+
+// Row scale s (stored / applied in the epilogue) and its reciprocal r
+// (applied to the elements), both 1 for an all-zero row.
+struct RowScale {
+    float s, r;
+};
+__device__ __forceinline__ RowScale scale_of(float amax) {
+    if (amax == 0.0f) return {1.0f, 1.0f};
+    return {amax / 127.0f, 127.0f / amax};
+}
+
+// Code of x, clamp(rne(fp32(x * r)), -127, 127), in the low byte of the
+// result, in a few VALU operations: for finite x, |x*r| <= 127*(1+2^-23) <
+// 2^22, so adding 1.5*2^23 (a separate, correctly rounded fp32 add - the
+// product is rounded first) rounds x*r to an integer half to even and leaves
+// it, two's complement, in the low mantissa bits; it never reaches +-128, so
+// no clamp is needed.  NaN selects 0.
+__device__ __forceinline__ uint32_t q8_bits(float x, float r) {
+#pragma clang fp contract(off)  // the product must be rounded before the add
+    const float p = x * r;
+    const uint32_t t = __float_as_uint(p + 12582912.0f);
+    return x != x ? 0u : t;
+}
+
+// Low bytes of t0..t3 -> bytes 0..3 of one word.
+__device__ __forceinline__ uint32_t pack_q8(uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3) {
+    return __builtin_amdgcn_perm(__builtin_amdgcn_perm(t3, t2, 0x0C0C0400u), __builtin_amdgcn_perm(t1, t0, 0x0C0C0400u),
+                                 0x05040100u);
+}
+
 template <int OUT>
 __device__ __forceinline__ void store_out(void* C, size_t idx, float y, int32_t acc) {
     if constexpr (OUT == FKE_OUT_F32) {

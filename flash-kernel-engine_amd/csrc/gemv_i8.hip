@@ -189,6 +189,7 @@ __global__ __launch_bounds__(ROWS_WAVES * 64) void gemv_rows_kernel(GemmArgs p) 
         ra[m] = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<int8_t*>(static_cast<const int8_t*>(p.A) + static_cast<size_t>(m < M ? m : 0) * K), 0, K,
             0x00020000);
+    const int nblk = (ck + 255) >> 8;  // blocks of 256 chunks (4 KiB of the row), the last one partial; >= 1
     // per-row epilogue operands: scalar loads (n is uniform) whose latency
     // hides behind the weight stream
     float sbn[NB], biasn[NB];
@@ -202,7 +203,6 @@ __global__ __launch_bounds__(ROWS_WAVES * 64) void gemv_rows_kernel(GemmArgs p) 
     for (int q = 0; q < NB; ++q)
 #pragma unroll
         for (int m = 0; m < MT; ++m) acc[q][m] = 0;
-    const int nblk = (ck + 255) >> 8;  // blocks of 256 chunks (4 KiB of the row), the last one partial; >= 1
     int blk = 0;
     do {
         int off[4];
@@ -221,11 +221,12 @@ __global__ __launch_bounds__(ROWS_WAVES * 64) void gemv_rows_kernel(GemmArgs p) 
         for (int m = 0; m < MT; ++m)
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                if constexpr (FULLK)
+                if constexpr (FULLK) {
                     a[m][u] = *reinterpret_cast<const v4i*>(static_cast<const int8_t*>(p.A) +
                                                             static_cast<size_t>(m < M ? m : 0) * K + off[u]);
-                else
+                } else {
                     a[m][u] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(ra[m], off[u], 0, 0));
+                }
             }
 #pragma unroll
         for (int q = 0; q < NB; ++q)
@@ -436,6 +437,7 @@ bool gemv_i8_supports(const GemmArgs& p) {
     // SwiGLU pairs: the row kernel up to M = 4, the skinny MFMA kernel above
     return !p.swiglu || p.M <= 4 || skinny_offsets_fit(p);
 }
+
 
 hipError_t launch_gemv_i8(const GemmArgs& p, hipStream_t s) {
     if (p.swiglu) {

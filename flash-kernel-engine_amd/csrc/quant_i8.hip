@@ -40,16 +40,6 @@ __device__ __forceinline__ float elem(const v4i& c, int e) {
     }
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-    v = fmaxf(v, __shfl_xor(v, 1));
-    v = fmaxf(v, __shfl_xor(v, 2));
-    v = fmaxf(v, __shfl_xor(v, 4));
-    v = fmaxf(v, __shfl_xor(v, 8));
-    v = fmaxf(v, __shfl_xor(v, 16));
-    v = fmaxf(v, __shfl_xor(v, 32));
-    return v;
-}
-
 // Maximum of v over the workgroup, returned to every thread.
 __device__ __forceinline__ float block_max(float v, float* red) {
     v = wave_max(v);
@@ -63,28 +53,6 @@ __device__ __forceinline__ int8_t q8(float x, float r) {
     if (x != x) return 0;
     const float v = __builtin_rintf(x * r);
     return static_cast<int8_t>(fminf(fmaxf(v, -127.0f), 127.0f));
-}
-
-// The same code as q8, in the low byte of the result, in a few VALU
-// operations: for finite x, |x*r| <= 127*(1+2^-23) < 2^22, so adding 1.5*2^23
-// (a separate, correctly rounded fp32 add - the product is rounded first, as
-// in q8) rounds x*r to an integer half to even and leaves it, two's
-// complement, in the low mantissa bits; it never reaches +-128, so no clamp
-// is needed.  NaN selects 0.
-__device__ __forceinline__ uint32_t q8_bits(float x, float r) {
-#pragma clang fp contract(off)  // the product must be rounded before the add
-    const float p = x * r;
-    const uint32_t t = __float_as_uint(p + 12582912.0f);
-    return x != x ? 0u : t;
-}
-
-// Row scale s (stored) and its reciprocal r (applied), both 1 for an all-zero row.
-struct RowScale {
-    float s, r;
-};
-__device__ __forceinline__ RowScale scale_of(float amax) {
-    if (amax == 0.0f) return {1.0f, 1.0f};
-    return {amax / 127.0f, 127.0f / amax};
 }
 
 template <int IN>
@@ -122,9 +90,7 @@ __global__ __launch_bounds__(QT) void quant_rows_kernel(const void* X, int M, in
         for (int j = 0; j < EPC / 4; ++j) {
             const uint32_t t0 = q8_bits(elem<IN>(v, 4 * j + 0), rs.r), t1 = q8_bits(elem<IN>(v, 4 * j + 1), rs.r);
             const uint32_t t2 = q8_bits(elem<IN>(v, 4 * j + 2), rs.r), t3 = q8_bits(elem<IN>(v, 4 * j + 3), rs.r);
-            // low bytes of t0..t3 -> bytes 0..3
-            w[j] = __builtin_amdgcn_perm(__builtin_amdgcn_perm(t3, t2, 0x0C0C0400u),
-                                         __builtin_amdgcn_perm(t1, t0, 0x0C0C0400u), 0x05040100u);
+            w[j] = pack_q8(t0, t1, t2, t3);
         }
         if constexpr (EPC == 4) *reinterpret_cast<uint32_t*>(qr + c * 4) = w[0];
         else *reinterpret_cast<uint2*>(qr + c * 8) = make_uint2(w[0], w[1]);

@@ -156,16 +156,44 @@ def quantize_per_token(x: torch.Tensor, q: torch.Tensor | None = None,
     return q, scale
 
 
+_IN_CODES = {torch.float32: _lib.IN_F32, torch.bfloat16: _lib.IN_BF16}
+
+
+def _float_linear(fn: str, x, weight, weight_scale, bias, out_dtype, n_vec: int, out_cols: int) -> torch.Tensor:
+    """Shared body of w8a8_linear / w8a8_gate_up_swiglu: one C call
+    (fke_w8a8_linear / fke_w8a8_swiglu_linear) that quantises x per token into
+    a workspace and runs the W8A8 GEMM on it."""
+    dev = x.device
+    if x.dtype not in _IN_CODES:
+        raise TypeError(f"x must be float32 or bfloat16, got {x.dtype}")
+    _check_dev("x", x, x.dtype, dev)
+    _check_dev("weight", weight, torch.int8, dev)
+    if x.dim() != 2 or weight.dim() != 2 or weight.shape[1] != x.shape[1]:
+        raise ValueError("x must be [M,K] and weight [N,K]")
+    _check_vec("weight_scale", weight_scale, n_vec, dev)
+    _check_vec("bias", bias, n_vec, dev)
+    if out_dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError("out_dtype must be float32 or bfloat16")
+    M, K = x.shape
+    L = _lib.lib()
+    out = torch.empty((M, out_cols), dtype=out_dtype, device=dev)
+    ws = torch.empty(L.fke_w8a8_linear_workspace_size(M, K), dtype=torch.uint8, device=dev)
+    st = getattr(L, fn)(x.data_ptr(), _IN_CODES[x.dtype], weight.data_ptr(), out.data_ptr(), M, out_cols, K,
+                        _ptr(weight_scale), 1.0, _ptr(bias), _OUT_CODES[out_dtype], ws.data_ptr(), ws.numel(),
+                        _stream(x))
+    _lib.check(st, fn)
+    return out
+
+
 def w8a8_linear(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor, bias=None,
                 out_dtype=torch.bfloat16) -> torch.Tensor:
     """y = x . W^T with W8A8 quantisation: x [M,K] fp32/bf16 activations are
-    quantised per token (`quantize_per_token`), weight [N,K] int8 carries
-    per-channel scales weight_scale [N]; bias [N] fp32 optional.  Two launches
-    on the current stream: the quantiser, then `w8a8_gemm`.
-    """
-    q, sa = quantize_per_token(x)
-    return w8a8_gemm(q, weight, scale_a=sa, scale_b=weight_scale, bias=bias, out_dtype=out_dtype,
-                     b_layout="nk")
+    quantised per token (as `quantize_per_token`), weight [N,K] int8 carries
+    per-channel scales weight_scale [N]; bias [N] fp32 optional.  Equal, bit for
+    bit, to `w8a8_gemm(*quantize_per_token(x), ...)`: the quantiser and the GEMM,
+    two launches on the current stream through one C call."""
+    return _float_linear("fke_w8a8_linear", x, weight, weight_scale, bias, out_dtype, weight.shape[0],
+                         weight.shape[0])
 
 
 def w8a8_swiglu(A: torch.Tensor, W: torch.Tensor, scale_a=None, scale_b=None, bias=None,
@@ -209,10 +237,13 @@ def w8a8_swiglu(A: torch.Tensor, W: torch.Tensor, scale_a=None, scale_b=None, bi
 def w8a8_gate_up_swiglu(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor, bias=None,
                         out_dtype=torch.bfloat16) -> torch.Tensor:
     """The gate/up half of a SwiGLU MLP in W8A8: x [M,K] fp32/bf16 is quantised
-    per token, then one launch computes silu(x W_gate^T) * (x W_up^T) from the
-    merged weight [2I, K] with per-channel scales weight_scale [2I]."""
-    q, sa = quantize_per_token(x)
-    return w8a8_swiglu(q, weight, scale_a=sa, scale_b=weight_scale, bias=bias, out_dtype=out_dtype)
+    per token and silu(x W_gate^T) * (x W_up^T) is computed from the merged
+    weight [2I, K] with per-channel scales weight_scale [2I]: the quantiser, then
+    the fused gate/up GEMM."""
+    if weight.dim() != 2 or weight.shape[0] % 2:
+        raise ValueError("weight must be [2I, K]")
+    return _float_linear("fke_w8a8_swiglu_linear", x, weight, weight_scale, bias, out_dtype, weight.shape[0],
+                         weight.shape[0] // 2)
 
 
 def gemm_half(A: torch.Tensor, B: torch.Tensor, scale_a=None, scale_b=None, bias=None,

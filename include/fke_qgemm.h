@@ -18,6 +18,7 @@
 #ifndef FKE_QGEMM_H
 #define FKE_QGEMM_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -193,6 +194,29 @@ int fke_gemm_half_on_path(int path, const void* A, const void* B, void* C, int M
  */
 int fke_launch_wmma_gemm_fp16(const void* d_A, const void* d_B, float* d_C, int M, int N, int K,
                               float alpha, float beta, void* stream);
+
+/*
+ * W8A8 linear layer from float activations in one call: the per-token
+ * quantisation of fke_quantize_rows_i8 applied to X [M,K] (fp32 or bf16,
+ * in_dtype), then the fke_qgemm_i8 GEMM with B = W [N,K] int8, scale_a = the
+ * row scales, scale_b = w_scale ([N] or NULL for the scalar sb) and bias:
+ *   Y = fke_qgemm_i8(quantize(X), W, ...)   bit for bit, fp32 or bf16 [M,N].
+ * No reference counterpart (its GEMMs take int8 inputs).  Two launches on
+ * `stream`: the quantiser writes the codes and scales into the caller's
+ * device `workspace` (at least fke_w8a8_linear_workspace_size(M, K) bytes,
+ * else hipErrorInvalidValue), the GEMM reads them there; calls that share a
+ * workspace must be ordered (same stream).
+ */
+size_t fke_w8a8_linear_workspace_size(int M, int K);
+int fke_w8a8_linear(const void* X, int in_dtype, const int8_t* W, void* Y, int M, int N, int K,
+                    const float* w_scale, float sb, const float* bias, int out_dtype,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* The same with the fused SwiGLU gate/up GEMM (fke_qgemm_i8_swiglu): W is
+ * [2I, K], w_scale and bias [2I], H [M, I]. */
+int fke_w8a8_swiglu_linear(const void* X, int in_dtype, const int8_t* W, void* H, int M, int I,
+                           int K, const float* w_scale, float sb, const float* bias,
+                           int out_dtype, void* workspace, size_t workspace_bytes, void* stream);
 
 /* The family fke_qgemm_i8 / fke_qgemm_f8 would pick (enum fke_path), or -1
  * for arguments they would reject.  Pure host logic; needs no GPU. */

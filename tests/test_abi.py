@@ -133,6 +133,26 @@ def test_half_gemm_rejects_bad_arguments_and_dispatch():
                                    None) == INVALID
 
 
+def test_w8a8_linear_from_float_arguments():
+    L = _lib.lib()
+    F32, BF16 = _lib.IN_F32, _lib.IN_BF16
+    lin = L.fke_w8a8_linear
+    need = L.fke_w8a8_linear_workspace_size(8, 4096)
+    assert need == 8 * 4096 + 4 * 8
+    assert L.fke_w8a8_linear_workspace_size(3, 100) == 512 + 12   # codes padded to 256 bytes
+    assert L.fke_w8a8_linear_workspace_size(0, 100) == 0
+    assert lin(None, BF16, P, P, 1, 64, 4096, None, 1.0, None, 1, P, need, None) == INVALID
+    for dt in (-1, _lib.IN_F16, 5):
+        assert lin(P, dt, P, P, 1, 64, 4096, None, 1.0, None, 1, P, need, None) == INVALID
+    assert lin(P, BF16, P, P, 1, 64, 4096, None, 1.0, None, _lib.OUT_I32, P, need, None) == INVALID
+    # the workspace is required and must be large enough: rejected before any launch
+    assert lin(P, BF16, P, P, 8, 64, 4096, None, 1.0, None, 1, None, 0, None) == INVALID
+    assert lin(P, BF16, P, P, 8, 64, 4096, None, 1.0, None, 1, P, need - 1, None) == INVALID
+    assert lin(P, BF16, P, P, 1, 64, 4096, None, 1.0, None, 1, None, 0, None) == INVALID
+    assert L.fke_w8a8_swiglu_linear(P, F32, P, P, 9, 64, 4096, None, 1.0, None, 1, None, 0, None) == INVALID
+    assert L.fke_w8a8_swiglu_linear(P, F32, P, P, 9, 64, 4096, None, 1.0, None, 2, P, 1 << 20, None) == INVALID
+
+
 def test_dropin_int8_rejects_k_not_multiple_of_4():
     """The reference kernel silently drops the K tail and misaligns rows when
     K % 4 != 0 (src/quantized_gemm.cu:28-30); the drop-in rejects it."""
