@@ -1,6 +1,6 @@
 """Benchmark of the quantized GEMM path on one MI355X.
 
-Metric: INT8 TOPS at M=N=K=8192 + HBM GB/s of the M=1 decode
+Headline metric: INT8 TOPS at M=N=K=8192 + HBM GB/s of the M=1 decode
 GEMV (N=14336, K=4096).  One "step" is one W8A8 INT8 GEMM at 8192^3 (per-token x
 per-channel fp32 scales, fp32 out) with inputs resident in HBM; `value` is its
 throughput in TOPS.  The decode GEMV (bf16 out + fused bias, weights rotated
@@ -141,7 +141,7 @@ def main():
         "dtype": "int8",
         "data": "synthetic (uniform int8 [-127,127], fp32 scales U[0.001,0.02], device RNG)",
         "config": {"workload": "W8A8 INT8 GEMM M=N=K=8192, B [N,K], per-token x per-channel "
-                               "fp32 scales, fp32 out (BASELINE config 3)",
+                               "fp32 scales, fp32 out (the square headline workload)",
                    "M": M, "N": N, "K": K, "out": "fp32", "kernel": "gemm_mfma_kernel<i8,NK,f32>"},
         "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": PEAK_INT8_TOPS,
                      "unit": "TOP/s", "frac": round(tops / PEAK_INT8_TOPS, 4),
@@ -260,7 +260,7 @@ def gemv_bench(torch, L, _lib, dev, gen, M, nbuf, launches, N=14336, K=4096):
 
 def extra_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
     res = {}
-    # config 2: prefill 4096 x 11008 x 4096, bf16 out
+    # prefill 4096 x 11008 x 4096, bf16 out
     M, N, K = 4096, 11008, 4096
     A, B, sa, sb = rand_i8(M, K), rand_i8(N, K), rand_u(M), rand_u(N)
     C = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
@@ -349,7 +349,7 @@ def data_sweep(torch, L, _lib, dev, gen, timed, args):
 
 
 def fp8_configs(torch, L, _lib, dev, gen, timed, args):
-    """Config 4: FP8 e4m3 8192^3, B [K,N] (reference layout) and [N,K], bf16 out."""
+    """FP8 e4m3 8192^3, B [K,N] (reference layout) and [N,K], bf16 out."""
     res = {}
     sh = torch.cuda.current_stream(dev).cuda_stream
     M = N = K = 8192

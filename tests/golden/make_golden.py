@@ -12,7 +12,7 @@ Contents (all data, no code):
   e4m3        the 256-entry E4M3 decode table (fp32 bit patterns) from the OCP
               closed form with exact powers of two, with the reference's
               0x7F/0xFF -> 0.0 rule (src/quantized_gemm.cu:81-97);
-  c1          BASELINE config 0 (M=128 N=128 K=256, seeded uniform int8,
+  c1          the CPU-sized config (M=128 N=128 K=256, seeded uniform int8,
               per-row/per-column scales U[0.001,0.02]): SHA-256 of the seeded
               inputs and of the oracle's int32 / fp32 / bf16 outputs, plus
               sampled entries.

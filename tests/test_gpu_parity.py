@@ -100,7 +100,7 @@ def test_dropin_program_full(dev):
     assert r.returncode == 0, r.stdout + r.stderr
 
 
-# ------------------------------------------------------------ C1 (config 0)
+# ------------------------------------------------------------ C1 (the CPU-sized config)
 
 @pytest.mark.parametrize("path", ["auto", "mfma", "generic"])
 def test_c1_golden(oracle, dev, path):
@@ -186,11 +186,11 @@ def test_unaligned_pointers_use_generic(oracle, dev):
     assert_same(host(r), oracle_out(oracle, oracle.w8a8_acc(A, B), sa, sb, 1., 1., None, "f32"), "unaligned")
 
 
-# ------------------------------------------------------ BASELINE full sizes
+# ------------------------------------------------------ full-size workloads
 
 @pytest.mark.parametrize("M", [1, 4, 16])
 def test_c2_decode_full(oracle, dev, M):
-    """Config 1: M in {1,4,16}, N=14336, K=4096, clipped N(0,30^2) activations,
+    """Decode: M in {1,4,16}, N=14336, K=4096, clipped N(0,30^2) activations,
     per-channel scales, fused bias, bf16 out; checked in full."""
     N, K = 14336, 4096
     say("c2 decode", M, N, K)
@@ -229,7 +229,7 @@ def test_decode_weight_past_2gib(oracle, dev, M):
 
 
 def test_c3_prefill_full(oracle, dev):
-    """Config 2: 4096x11008x4096, bf16 out: every output checked."""
+    """Prefill: 4096x11008x4096, bf16 out: every output checked."""
     M, N, K = 4096, 11008, 4096
     say("c3 prefill", M, N, K)
     A, B, sa, sb, _ = inputs_i8(oracle, M, N, K, 2000)
@@ -315,7 +315,7 @@ def test_fp8_mfma_tolerance(oracle, dev, layout, out, nan_codes):
 
 
 def test_c5_fp8_full(oracle, dev):
-    """Config 4: 8192^3 e4m3 (per-tensor amax/448 scales, B [K,N]), bf16 out,
+    """FP8 square: 8192^3 e4m3 (per-tensor amax/448 scales, B [K,N]), bf16 out,
     against the reference's sequential fp32 sum on 64 sampled rows."""
     M = N = K = 8192
     say("c5 fp8", M, N, K)
