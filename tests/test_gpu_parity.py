@@ -228,6 +228,72 @@ def test_decode_weight_past_2gib(oracle, dev, M):
     assert_same(got, ref, f"decode past 2 GiB M={M}")
 
 
+def _sampled_rows_check(oracle, A_dev, B_dev, sa, sb, rows, what):
+    """Oracle check of the listed output rows of C = A . B^T (B [N,K] on the device)."""
+    out = ops.w8a8_gemm(A_dev, B_dev, dev_t(sa), dev_t(sb), None, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    Ah = A_dev[torch.from_numpy(rows).long().cuda()].cpu().numpy()
+    acc = oracle.w8a8_acc(Ah, B_dev.cpu().numpy(), nthreads=NTH)
+    ref = oracle.w8a8_epilogue(acc, sa[rows], sb, 1.0, 1.0, None, oracle.OUT_F32)
+    assert_same(out[torch.from_numpy(rows).long().cuda()].cpu().numpy(), ref, what)
+
+
+def test_mfma_largest_activation_panel(oracle, dev):
+    """M*K = 2^31 - 8192, the largest A the MFMA kernel's 32-bit offsets take
+    (2 GiB of activations): first, middle and last rows against the oracle."""
+    M, N, K = (1 << 31) // 8192 - 1, 256, 8192
+    say("mfma largest A", M, N, K)
+    L = _lib.lib()
+    assert L.fke_select_path_i8(4096, 4096, 4096, M, N, K, 0, 0) == _lib.PATH_MFMA
+    assert L.fke_select_path_i8(4096, 4096, 4096, M + 2, N, K, 0, 0) == _lib.PATH_GENERIC
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    A = torch.randint(-127, 128, (M, K), dtype=torch.int8, device=dev, generator=g)
+    B = dev_t(oracle.gen_i8_uniform((N, K), 6))
+    sa = oracle.gen_f32_uniform((M,), 7, 0.001, 0.02)
+    sb = oracle.gen_f32_uniform((N,), 8, 0.001, 0.02)
+    rows = np.array([0, 1, 255, 256, M // 2, M - 257, M - 2, M - 1], dtype=np.int32)
+    _sampled_rows_check(oracle, A, B, sa, sb, rows, "largest A panel")
+
+
+def test_generic_past_the_mfma_offsets(oracle, dev):
+    """M*K just above 2^31: the dispatcher sends it to the generic kernel
+    (64-bit indexing), which must give the same exact results."""
+    M, N, K = (1 << 31) // 8192 + 1, 64, 8192
+    say("generic past the MFMA offsets", M, N, K)
+    assert _lib.lib().fke_select_path_i8(4096, 4096, 4096, M, N, K, 0, 0) == _lib.PATH_GENERIC
+    g = torch.Generator(device=dev)
+    g.manual_seed(9)
+    A = torch.randint(-127, 128, (M, K), dtype=torch.int8, device=dev, generator=g)
+    B = dev_t(oracle.gen_i8_uniform((N, K), 10))
+    sa = oracle.gen_f32_uniform((M,), 11, 0.001, 0.02)
+    sb = oracle.gen_f32_uniform((N,), 12, 0.001, 0.02)
+    rows = np.array([0, 63, 64, M // 2, M - 65, M - 1], dtype=np.int32)
+    _sampled_rows_check(oracle, A, B, sa, sb, rows, "generic past 2^31")
+
+
+def test_mfma_largest_weight_panel(oracle, dev):
+    """N*K = 2^31 - 8192 (2 GiB of weights, B [N,K]): sampled output columns
+    against the oracle on host copies of those weight rows."""
+    M, N, K = 300, (1 << 31) // 8192 - 1, 8192
+    say("mfma largest B", M, N, K)
+    assert _lib.lib().fke_select_path_i8(4096, 4096, 4096, M, N, K, 0, 0) == _lib.PATH_MFMA
+    g = torch.Generator(device=dev)
+    g.manual_seed(13)
+    Bd = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g)
+    A = oracle.gen_i8_uniform((M, K), 14)
+    sa = oracle.gen_f32_uniform((M,), 15, 0.001, 0.02)
+    sb = oracle.gen_f32_uniform((N,), 16, 0.001, 0.02)
+    out = ops.w8a8_gemm(dev_t(A), Bd, dev_t(sa), dev_t(sb), None, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    cols = np.array([0, 1, 255, 256, N // 2, N - 257, N - 2, N - 1])
+    Bs = Bd[torch.from_numpy(cols).long().cuda()].cpu().numpy()
+    del Bd
+    acc = oracle.w8a8_acc(A, Bs, nthreads=NTH)
+    ref = oracle.w8a8_epilogue(acc, sa, sb[cols], 1.0, 1.0, None, oracle.OUT_F32)
+    assert_same(out[:, torch.from_numpy(cols).long().cuda()].cpu().numpy(), ref, "largest B panel")
+
+
 def test_c3_prefill_full(oracle, dev):
     """Prefill: 4096x11008x4096, bf16 out: every output checked."""
     M, N, K = 4096, 11008, 4096
