@@ -185,3 +185,34 @@ def test_full_8192_cubed_sampled_rows(oracle, dev, dt):
     rows = np.array([0, 1, 255, 256, 4095, 8191], dtype=np.int32)
     ref = oracle.gemm_half(A, B, code(dt, oracle), rows=rows, nthreads=NTH)
     same_bits(C[torch.from_numpy(rows).long().cuda()].cpu().numpy(), ref, f"{dt} 8192^3 sampled rows")
+
+
+def _device_int_codes(shape, dt, seed, dev):
+    """Small-integer operands made on the device (exact in fp16 and bf16)."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    return torch.randint(-4, 5, shape, dtype=torch.int8, device=dev, generator=g).to(TD[dt])
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("M,want_path", [((1 << 31) // 16384 - 1, "mfma"), ((1 << 31) // 16384 + 1, "generic")])
+def test_largest_activation_panel(oracle, dev, dt, M, want_path):
+    """M * 2K at the MFMA kernel's 32-bit byte-offset limit (2 GiB of A), and
+    just past it, where the dispatcher sends the call to the generic kernel:
+    sampled rows against the oracle (integer operands: exact)."""
+    N, K = 128, 8192
+    say("half gemm largest A", dt, M, want_path)
+    path = {"mfma": _lib.PATH_MFMA, "generic": _lib.PATH_GENERIC}[want_path]
+    Ad = _device_int_codes((M, K), dt, 21, dev)
+    B = enc(int_operands(1, N, K, 22)[1], dt)
+    Bd = dev_codes(B, dt)
+    C = torch.empty((M, N), dtype=torch.float32, device=dev)
+    sel = _lib.lib().fke_select_path_half(Ad.data_ptr(), Bd.data_ptr(), C.data_ptr(), M, N, K,
+                                         _lib.IN_F16 if dt == "f16" else _lib.IN_BF16, _lib.OUT_F32, _lib.B_NK)
+    assert sel == path
+    C = ops.gemm_half(Ad, Bd, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    rows = torch.tensor([0, 1, 255, 256, M // 2, M - 257, M - 2, M - 1], device=dev)
+    A = host(Ad[rows]).view(np.uint16)
+    ref = oracle.gemm_half(A, B, code(dt, oracle), nthreads=NTH)
+    same_bits(C[rows].cpu().numpy(), ref, f"{dt} M={M}")
