@@ -31,7 +31,7 @@ TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic.json")
 
 def gemv_kernel(M):
     """Decode kernel the dispatcher picks for M rows (K % 4096 == 0, B [N,K])."""
-    return "gemv_rows_kernel" if M <= 4 else "gemv_mfma_kernel"
+    return "gemv_rows_kernel" if M <= 2 else "gemv_lds_kernel"
 
 
 def traffic(key):
@@ -471,27 +471,30 @@ def swiglu_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
                                                  "frac": round(gbs / PEAK_HBM_GBS, 4), "bytes": nbytes,
                                                  "kernel": "swiglu_kernel<bf16, vec>"}
     del A, W, H, G, U, G2, U2, H2, sets
-    # decode: M = 1, fused gate/up + SwiGLU, 4 rotating weights of 112 MiB (448 MiB)
-    M, nbuf = 1, 4
-    A = torch.clamp(torch.round(torch.randn((M, K), device=dev, generator=gen) * 30), -127, 127).to(torch.int8)
+    # decode: M = 1 and 16, fused gate/up + SwiGLU, 4 rotating weights of 112 MiB (448 MiB)
+    nbuf = 4
     Ws = [torch.randint(-127, 128, (2 * I, K), dtype=torch.int8, device=dev, generator=gen) for _ in range(nbuf)]
-    sa, sb = rand_u(M), rand_u(2 * I)
+    sb = rand_u(2 * I)
     bias = torch.randn(2 * I, device=dev, generator=gen) * 0.02
-    H = torch.empty((M, I), dtype=torch.bfloat16, device=dev)
+    for M in (1, 16):
+        A = torch.clamp(torch.round(torch.randn((M, K), device=dev, generator=gen) * 30), -127, 127).to(torch.int8)
+        sa = rand_u(M)
+        H = torch.empty((M, I), dtype=torch.bfloat16, device=dev)
 
-    def dlaunch(i, st):
-        r = L.fke_qgemm_i8_swiglu(A.data_ptr(), Ws[i % nbuf].data_ptr(), H.data_ptr(), M, I, K, sa.data_ptr(),
-                                  sb.data_ptr(), 1.0, 1.0, bias.data_ptr(), _lib.OUT_BF16, st)
-        if r:
-            raise RuntimeError(f"swiglu decode failed: {_lib.status_string(r)}")
+        def dlaunch(i, st):
+            r = L.fke_qgemm_i8_swiglu(A.data_ptr(), Ws[i % nbuf].data_ptr(), H.data_ptr(), M, I, K, sa.data_ptr(),
+                                      sb.data_ptr(), 1.0, 1.0, bias.data_ptr(), _lib.OUT_BF16, st)
+            if r:
+                raise RuntimeError(f"swiglu decode failed: {_lib.status_string(r)}")
 
-    us = graph_us(torch, dev, dlaunch, 200, 2 * nbuf)
-    nbytes = M * K + 2 * I * K + 4 * M + 8 * 2 * I + 2 * M * I
-    gbs = nbytes / (us * 1e-6) / 1e9
-    res["swiglu_gate_up_decode_M1_14336x4096_bf16"] = {
-        "us": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4), "bytes": nbytes,
-        "kernel": "gemv_rows_kernel<1, bf16, fullk, swiglu>"}
-    del A, Ws, H
+        us = graph_us(torch, dev, dlaunch, 200, 2 * nbuf)
+        nbytes = M * K + 2 * I * K + 4 * M + 8 * 2 * I + 2 * M * I
+        gbs = nbytes / (us * 1e-6) / 1e9
+        res[f"swiglu_gate_up_decode_M{M}_14336x4096_bf16"] = {
+            "us": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4), "bytes": nbytes,
+            "kernel": "gemv_rows_kernel<1, bf16, fullk, swiglu>" if M <= 2 else "gemv_lds_kernel<bf16, swiglu>"}
+        del A, H
+    del Ws
     return res
 
 

@@ -100,6 +100,51 @@ __device__ __forceinline__ float swiglu_pair(float g, float u) {
     return (g * s) * u;
 }
 
+// ---- memory-pipeline helpers shared by the LDS-staged kernels ----
+
+// s_waitcnt vmcnt(N) with the other counters unconstrained (gfx9 encoding:
+// vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+__device__ __forceinline__ void wait_vm0() { wait_vm<0>(); }
+// s_waitcnt lgkmcnt(0), the other counters unconstrained.
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+// Workgroup barrier without the LDS fence of __syncthreads: every LDS write a
+// stage depends on comes from LDS-DMA (ordered by an explicit vmcnt wait
+// before the barrier) or from ds_writes followed by an explicit lgkmcnt wait.
+// The empty asm statements keep the compiler from moving memory operations
+// across the barrier.
+__device__ __forceinline__ void barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ void fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// Buffer resource over `bytes` bytes at `base` (raw buffer: stride 0, bounds
+// checked against num_records; gfx9 dword3).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+
+// 16 bytes per lane, buffer -> LDS (buffer_load_dwordx4 ... lds): lane l's
+// bytes land at lds + 16*l.  The MUBUF form rather than global_load_lds: the
+// compiler treats a FLAT-encoded LDS DMA as a pending access of both memory
+// kinds and then waits for every outstanding LDS read (lgkmcnt(0)) wherever
+// one result is needed, which would serialise the fragment reads.
+// aux = 2 marks the load non-temporal (a stream read once).
+template <int AUX = 0>
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, int soff, uint8_t* l) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        r, reinterpret_cast<__attribute__((address_space(3))) void*>(reinterpret_cast<uintptr_t>(l)), 16,
+        static_cast<int>(voff), soff, 0, AUX);
+}
+
 // ---- per-token INT8 quantisation (quant_i8.hip) ----
 
 __device__ __forceinline__ float wave_max(float v) {

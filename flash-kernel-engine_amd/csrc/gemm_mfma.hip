@@ -57,40 +57,6 @@ constexpr int PW = BM * BK / 1024 / NWAVES;  // DMA loads per wave per panel (8)
 
 __device__ __forceinline__ int swz(int r) { return ((r & 31) ^ ((r & 31) >> 3)) & 7; }
 
-// s_waitcnt vmcnt(0) / lgkmcnt(0), the other counters unconstrained (gfx9 encoding).
-__device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
-__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
-
-// Workgroup barrier without the LDS fence of __syncthreads: every LDS write a
-// stage depends on comes from LDS-DMA (ordered by the explicit vmcnt wait
-// before the barrier) or from ds_writes followed by an explicit lgkmcnt wait.
-// The empty asm statements keep the compiler from moving memory operations
-// across the barrier.
-__device__ __forceinline__ void barrier() {
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
-
-__device__ __forceinline__ void fence() { __builtin_amdgcn_sched_barrier(0); }
-
-// Buffer resource over `bytes` bytes at `base` (raw buffer: stride 0, bounds
-// checked against num_records; gfx9 dword3).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
-}
-
-// 16 bytes per lane, buffer -> LDS (buffer_load_dwordx4 ... lds): lane l's
-// bytes land at lds + 16*l.  The MUBUF form rather than global_load_lds: the
-// compiler treats a FLAT-encoded LDS DMA as a pending access of both memory
-// kinds and then waits for every outstanding LDS read (lgkmcnt(0)) wherever
-// one result is needed, which would serialise the fragment reads.
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, int soff, uint8_t* l) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        r, reinterpret_cast<__attribute__((address_space(3))) void*>(reinterpret_cast<uintptr_t>(l)), 16,
-        static_cast<int>(voff), soff, 0, 0);
-}
-
 // Workgroup -> output tile.  Consecutive workgroup ids are dispatched round
 // robin over the 8 XCDs; give each XCD a contiguous range of tile ids and walk
 // that range in groups of GROUP_M tile rows so the workgroups an XCD runs at

@@ -2,10 +2,11 @@
 //
 // Same arithmetic as reference src/quantized_gemm.cu:15-54 (exact int32 dot
 // products, the fused epilogue applied after), re-shaped for an HBM-bound
-// problem: the B panel is streamed once with 128-bit coalesced loads and no
-// MFMA is used.
+// problem: the B panel is streamed once with 128-bit coalesced loads.
 //
-// Three kernels:
+// Four kernels:
+//  * gemv_lds_kernel (3 <= M <= 16, K >= 4096), described at its definition:
+//    the weight panel streamed through LDS by one workgroup per CU.
 //  * gemv_rows_kernel (M <= 4): NB B rows per wave (one at M = 1, two for
 //    M = 2..4 and for SwiGLU's gate/up pairs) over the full K.  Lane l reads
 //    16-byte chunks l, l+64, l+128, l+192 of each 256-chunk block (one wave
@@ -14,10 +15,10 @@
 //    sums with DPP row rotations, one ds_swizzle and two readlanes - no LDS
 //    and no barrier, so a wave retires as soon as its rows are done and the
 //    load queue never drains.
-//  * gemv_i8_kernel (5 <= M <= 16 when the MFMA kernel's 32-bit offsets do
-//    not reach), described below; it amortises the activation chunks over R
+//  * gemv_i8_kernel (5 <= M <= 16 when neither MFMA kernel's 32-bit offsets
+//    reach), described below; it amortises the activation chunks over R
 //    rows per wave.
-//  * gemv_mfma_kernel (5 <= M <= 16), described at its definition.
+//  * gemv_mfma_kernel (5 <= M <= 16, K < 4096), described at its definition.
 //
 // gemv_i8_kernel: workgroup = 4 waves = R consecutive B rows (output columns n0..n0+R-1).
 // The K bytes of a row are split in four quarters, one per wave (split-K);
@@ -356,6 +357,311 @@ __global__ __launch_bounds__(SK_KS * 64) void gemv_mfma_kernel(GemmArgs p) {
     }
 }
 
+// gemv_lds_kernel (M <= 16): the weight panel streamed through LDS.  One
+// workgroup per CU owns an even share of R = ceil(NO / G) weight rows
+// (output columns), so every CU reads the same number of bytes, and keeps
+// its HBM reads in flight from its first instruction to its last.
+// The K bytes are cut into pieces of PIECE bytes; wave w owns pieces w, w+4,
+// ...  An item is 16 rows x PIECE bytes of one piece: the wave copies it into
+// LDS with buffer_load_dwordx4 ... lds instructions of 1 KiB each (one or two
+// rows' contiguous bytes), keeps NS items in flight in a ring of NS slots, and
+// multiplies a landed item from LDS with PIECE/64 v_mfma_i32_16x16x64_i8
+// against the piece's activation rows.  Those arrive the same way (an item of
+// activation rows 0..15, read into registers once per piece and tile chunk).
+// The wave walks its pieces for LK_TMAX tiles at a time (a tile chunk),
+// accumulating each tile; at the end of a chunk the four waves' partial sums
+// meet in LDS and the chunk's outputs are finished (exact int32 sums, so any
+// split is bit-exact).
+// k order: a dot product is a sum, so the MFMA's k positions may map to any
+// permutation of a piece's bytes as long as both operands use the same one.
+// With S = PIECE/64 steps, step s of lane group g = l/16 takes 16-byte chunk
+// S*g + s; LDS row i of an item holds chunk c at slot c ^ z(i), z(i) =
+// (i / (1024/PIECE)) mod S, so the 64 lanes of every ds_read_b128 touch 64
+// distinct 16-byte slots of a 1 KiB span.  Activation rows >= M, bytes >= K
+// and tile rows past the workgroup's share read as zero (offset 2^31 is
+// outside every range); weight bytes past K in the last piece meet zero
+// activations.
+// SWI: B is [gate; up]; tile t of a chunk is gate tile t/2 (t even) or the
+// matching up tile (t odd), and each output is swiglu_pair of the two.
+constexpr int LK_TMAX = 4;    // tiles accumulated between two reductions
+constexpr int LK_RMAX = 512;  // weight rows (of each half) of one workgroup
+
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+
+// Position in a wave's item sequence: tile chunk tc (nt tiles), the wave's
+// j-th piece, and u = -1 (the piece's activation rows) or tile u of the chunk.
+struct LkPos {
+    int tc, nt, j, u;
+};
+
+// s_waitcnt vmcnt(n) / lgkmcnt(n) for an n known after unrolling; the lgkm
+// form is tied to the register it guards so the consumer cannot move above it.
+__device__ __forceinline__ void wait_vm_n(int n) {
+    switch (n) {
+        case 0: wait_vm<0>(); break;
+        case 1: wait_vm<8>(); break;
+        case 2: wait_vm<16>(); break;
+        case 3: wait_vm<24>(); break;
+        default: wait_vm<32>(); break;
+    }
+}
+__device__ __forceinline__ void wait_lgkm_tied(int n, v4i& r) {
+    switch (n) {
+        case 0: asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r)); break;
+        case 1: asm volatile("s_waitcnt lgkmcnt(1)" : "+v"(r)); break;
+        case 2: asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(r)); break;
+        case 3: asm volatile("s_waitcnt lgkmcnt(3)" : "+v"(r)); break;
+        case 4: asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(r)); break;
+        case 5: asm volatile("s_waitcnt lgkmcnt(5)" : "+v"(r)); break;
+        case 6: asm volatile("s_waitcnt lgkmcnt(6)" : "+v"(r)); break;
+        default: asm volatile("s_waitcnt lgkmcnt(7)" : "+v"(r)); break;
+    }
+}
+
+template <int OUT, bool SWI, int PIECE, int NS>
+__global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
+    constexpr int H = SWI ? 2 : 1;
+    constexpr int RPW = 1024 / PIECE;  // rows per 1 KiB copy instruction
+    constexpr int DI = 16 / RPW;       // copy instructions per item
+    constexpr int S = PIECE / 64;      // MFMA steps per item
+    constexpr int LA = S < 8 ? S : 8;  // fragment reads ahead of their MFMA
+    static_assert(PIECE == 512 || PIECE == 1024, "piece of 512 or 1024 bytes");
+    static_assert(DI == 8 || DI == 16, "vmcnt steps of wait_vm_n are 8 copies");
+    static_assert((NS - 1) * DI <= 32, "wait_vm_n covers up to 32 copies");
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[NS][4][16 * PIECE];
+    __shared__ __attribute__((aligned(16))) int32_t red[LK_TMAX][4][256];
+    __shared__ __attribute__((aligned(16))) float esb[H * LK_RMAX], ebias[H * LK_RMAX], esa[64];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int M = p.M, K = p.K;
+    const int NO = SWI ? p.N >> 1 : p.N;  // output columns
+    const int R = (NO + static_cast<int>(gridDim.x) - 1) / static_cast<int>(gridDim.x);
+    const int r0 = blockIdx.x * R;
+    if (r0 >= NO) return;  // uniform over the workgroup
+    const int nr = min(R, NO - r0);  // rows of each half
+    const int th = (nr + 15) >> 4;   // 16-row tiles of each half
+    const int T = H * th;
+    const int TC = (T + LK_TMAX - 1) / LK_TMAX;
+    const int P = (K + PIECE - 1) / PIECE;  // >= 4
+    const int np = (P - 1 - wave) / 4 + 1;  // pieces of this wave, >= 1
+
+    // Epilogue operands (scale_b and bias of the workgroup's rows, scale_a of
+    // the activation rows) go straight to LDS with dword LDS-DMA copies issued
+    // by wave 0 before its stream.  No register then holds a value loaded
+    // outside the main loop, which would make the compiler drain every copy in
+    // flight before entering it; being older than every item's copies, they
+    // have landed once the first item has.
+    if (wave == 0) {
+        const int nq = (nr + 63) >> 6;  // 64 rows per copy instruction
+#pragma unroll
+        for (int h = 0; h < H; ++h) {
+            if (p.scale_b) {
+                const __amdgpu_buffer_rsrc_t r = make_rsrc(p.scale_b + h * NO + r0, nr * 4);
+                for (int q = 0; q < nq; ++q)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_u8*)(esb + h * LK_RMAX + 64 * q), 4,
+                                                             256 * q + 4 * lane, 0, 0, 0);
+            }
+            if (p.bias) {
+                const __amdgpu_buffer_rsrc_t r = make_rsrc(p.bias + h * NO + r0, nr * 4);
+                for (int q = 0; q < nq; ++q)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_u8*)(ebias + h * LK_RMAX + 64 * q), 4,
+                                                             256 * q + 4 * lane, 0, 0, 0);
+            }
+        }
+        if (p.scale_a)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(p.scale_a, M * 4), (lds_u8*)esa, 4, 4 * lane, 0, 0, 0);
+    }
+
+    const int8_t* B = static_cast<const int8_t*>(p.B);
+    const __amdgpu_buffer_rsrc_t rb0 = make_rsrc(B + static_cast<size_t>(r0) * K, nr * K);
+    const __amdgpu_buffer_rsrc_t rb1 = make_rsrc(B + static_cast<size_t>(SWI ? NO + r0 : r0) * K, nr * K);
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, M * K);
+    lds_u8* const lring = (lds_u8*)(&ring[0][wave][0]);  // slot q at + q * 4 * 16 * PIECE
+
+    // copy lanes: lane l fills slot l % (64/RPW) of row d*RPW + l / (64/RPW)
+    const int crow = lane / (64 / RPW), cslot = lane % (64 / RPW);
+    auto z = [](int i) __attribute__((always_inline)) { return (i / RPW) & (S - 1); };
+    auto issue = [&](const LkPos& it, lds_u8* dst) __attribute__((always_inline)) {
+        const int pc = (wave + 4 * it.j) * PIECE;  // first k byte of the piece
+        if (it.u < 0) {
+#pragma unroll
+            for (int d = 0; d < DI; ++d) {
+                const int i = d * RPW + crow;
+                const int k = pc + ((cslot ^ z(i)) << 4);
+                const uint32_t off = i < M && k < K ? static_cast<uint32_t>(i * K + k) : 0x80000000u;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, dst + d * 1024, 16, static_cast<int>(off), 0, 0, 0);
+            }
+        } else {
+            const int t = it.tc * LK_TMAX + it.u;
+            const int row0 = 16 * (SWI ? t >> 1 : t);
+            const __amdgpu_buffer_rsrc_t rb = SWI && (t & 1) ? rb1 : rb0;
+#pragma unroll
+            for (int d = 0; d < DI; ++d) {
+                const int i = d * RPW + crow, r = row0 + i;
+                const uint32_t off =
+                    r < nr ? static_cast<uint32_t>(r * K + pc + ((cslot ^ z(i)) << 4)) : 0x80000000u;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, dst + d * 1024, 16, static_cast<int>(off), 0, 0, 2);
+            }
+        }
+    };
+    // advance to the next item; false past the last one
+    auto advance = [&](LkPos& it) __attribute__((always_inline)) {
+        if (++it.u < it.nt) return true;
+        it.u = -1;
+        if (++it.j < np) return true;
+        it.j = 0;
+        ++it.tc;
+        it.nt = min(LK_TMAX, T - it.tc * LK_TMAX);
+        return it.tc < TC;
+    };
+
+    // lane l = 16g + i reads row i, chunk S*g + s at slot (S*g + s) ^ z(i)
+    const int li = lane & 15;
+    const uint32_t lb = static_cast<uint32_t>(li * PIECE + (lane >> 4) * (PIECE / 4) + z(li) * 16);
+    v4i act[S];
+    v4i acc[LK_TMAX];
+#pragma unroll
+    for (int q = 0; q < LK_TMAX; ++q) acc[q] = v4i{0, 0, 0, 0};
+
+    // Fragment reads are inline ds_read_b128: the compiler does not know
+    // which ring slot an LDS-DMA copy writes, and before any LDS read it can
+    // see it would wait for every copy in flight (the next items' too).  Each
+    // wait below is tied to the registers it guards; LDS operations complete
+    // in order, so lgkmcnt(n) means all but the last n reads have landed.
+    auto rd = [&](const lds_u8* src, int s) __attribute__((always_inline)) {
+        v4i r;
+        asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(src + (lb ^ (s << 4))));
+        return r;
+    };
+    // An item's fragments go to registers first, so its slot can be refilled
+    // before the MFMAs run (the slot's copy is then in flight during them).
+    // At most LA reads are in flight (lgkmcnt's field is 4 bits).
+    auto read_all = [&](const lds_u8* src, v4i (&f)[S]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int s = 0; s < LA; ++s) f[s] = rd(src, s);
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            wait_lgkm_tied(min(S, s + LA) - s - 1, f[s]);
+            if (s + LA < S) f[s + LA] = rd(src, s + LA);
+        }
+    };
+    auto mma = [&](v4i& c, const v4i (&w)[S]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) c = __builtin_amdgcn_mfma_i32_16x16x64_i8(act[s], w[s], c, 0, 0, 0);
+    };
+
+    // End of a tile chunk: the four waves' partials meet in LDS; thread
+    // (m, nl) = (tid / 16, tid % 16) finishes output column nl of each tile.
+    // Lane l of a wave holds tile column l%16, rows 4*(l/16)+v.  The LDS
+    // accesses are inline for the reason given at the fragment reads.
+    auto ld = [](const void* a) __attribute__((always_inline)) {
+        int v;
+        asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"((lds_u8*)(const_cast<void*>(a))));
+        return v;
+    };
+    auto finish = [&](int tc, int nt) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < LK_TMAX; ++q) {
+            if (q < nt) asm volatile("ds_write_b128 %0, %1" : : "v"((lds_u8*)&red[q][wave][lane * 4]), "v"(acc[q]) : "memory");
+            acc[q] = v4i{0, 0, 0, 0};
+        }
+        wait_lgkm0();
+        barrier();
+        const int m = tid >> 4, nl = tid & 15;
+        const int ri = ((m >> 2) * 16 + nl) * 4 + (m & 3);
+        if (m < M) {
+            int xa = ld(esa + m);
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(xa));
+            const float sam = p.scale_a ? __int_as_float(xa) : p.sa;
+            if constexpr (SWI) {
+                for (int q = 0; q < nt; q += 2) {
+                    const int r = 16 * ((tc * LK_TMAX + q) >> 1) + nl;
+                    int g0 = ld(&red[q][0][ri]), g1 = ld(&red[q][1][ri]), g2 = ld(&red[q][2][ri]), g3 = ld(&red[q][3][ri]);
+                    int u0 = ld(&red[q + 1][0][ri]), u1 = ld(&red[q + 1][1][ri]), u2 = ld(&red[q + 1][2][ri]),
+                        u3 = ld(&red[q + 1][3][ri]);
+                    int bg = ld(esb + r), bu = ld(esb + LK_RMAX + r), cg = ld(ebias + r), cu = ld(ebias + LK_RMAX + r);
+                    asm volatile("s_waitcnt lgkmcnt(0)"
+                                 : "+v"(g0), "+v"(g1), "+v"(g2), "+v"(g3), "+v"(u0), "+v"(u1), "+v"(u2), "+v"(u3),
+                                   "+v"(bg), "+v"(bu), "+v"(cg), "+v"(cu));
+                    if (r < nr) {
+                        const float sg = sam * (p.scale_b ? __int_as_float(bg) : p.sb);
+                        const float su = sam * (p.scale_b ? __int_as_float(bu) : p.sb);
+                        const float ag = static_cast<float>(g0 + g1 + g2 + g3), au = static_cast<float>(u0 + u1 + u2 + u3);
+                        const float yg = p.bias ? __builtin_fmaf(ag, sg, __int_as_float(cg)) : ag * sg;
+                        const float yu = p.bias ? __builtin_fmaf(au, su, __int_as_float(cu)) : au * su;
+                        store_out<OUT>(p.C, static_cast<size_t>(m) * NO + r0 + r, swiglu_pair(yg, yu), 0);
+                    }
+                }
+            } else {
+                for (int q = 0; q < nt; ++q) {
+                    const int r = 16 * (tc * LK_TMAX + q) + nl;
+                    int a0 = ld(&red[q][0][ri]), a1 = ld(&red[q][1][ri]), a2 = ld(&red[q][2][ri]), a3 = ld(&red[q][3][ri]);
+                    int b = ld(esb + r), cb = ld(ebias + r);
+                    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a0), "+v"(a1), "+v"(a2), "+v"(a3), "+v"(b), "+v"(cb));
+                    if (r < nr) {
+                        const int32_t sum = a0 + a1 + a2 + a3;
+                        const float sc = sam * (p.scale_b ? __int_as_float(b) : p.sb);
+                        const float y = p.bias ? __builtin_fmaf(static_cast<float>(sum), sc, __int_as_float(cb))
+                                               : static_cast<float>(sum) * sc;
+                        store_out<OUT>(p.C, static_cast<size_t>(m) * NO + r0 + r, y, sum);
+                    }
+                }
+            }
+        }
+        barrier();  // the partials of the next chunk overwrite red
+    };
+
+    // Prologue: the first NS items in flight.
+    LkPos pi{0, min(LK_TMAX, T), 0, -1};
+    int issued = 0;
+    bool more = true;
+#pragma unroll
+    for (int q = 0; q < NS; ++q)
+        if (more) {
+            issue(pi, lring + q * (4 * 16 * PIECE));
+            ++issued;
+            more = advance(pi);
+        }
+
+    // Consumer: the same item order as the producer, spelled out as loops so
+    // that every register array is indexed by constants.  Item c sits in
+    // slot c % NS; once its fragments are in registers, item c + NS goes there.
+    int c = 0;
+    auto next_slot = [&]() __attribute__((always_inline)) {
+        lds_u8* const slot = lring + (c % NS) * (4 * 16 * PIECE);
+        wait_vm_n((issued - c - 1) * DI / 8);  // all but the later items' copies have landed
+        return slot;
+    };
+    auto refill = [&](lds_u8* slot) __attribute__((always_inline)) {
+        if (more) {
+            issue(pi, slot);
+            ++issued;
+            more = advance(pi);
+        }
+        ++c;
+    };
+    for (int tc = 0; tc < TC; ++tc) {
+        const int nt = min(LK_TMAX, T - tc * LK_TMAX);
+        for (int j = 0; j < np; ++j) {
+            lds_u8* slot = next_slot();
+            read_all(slot, act);
+            refill(slot);
+#pragma unroll
+            for (int u = 0; u < LK_TMAX; ++u) {
+                if (u < nt) {
+                    slot = next_slot();
+                    v4i w[S];
+                    read_all(slot, w);
+                    refill(slot);
+                    mma(acc[u], w);
+                }
+            }
+        }
+        finish(tc, nt);
+    }
+}
+
 hipError_t launch_mfma_skinny(const GemmArgs& p, hipStream_t stream) {
     GemmArgs a = p;
     void* args[] = {&a};
@@ -373,6 +679,46 @@ hipError_t launch_mfma_skinny(const GemmArgs& p, hipStream_t stream) {
         default: f = reinterpret_cast<const void*>(&gemv_mfma_kernel<FKE_OUT_I32>); break;
     }
     return hipLaunchKernel(f, grid, dim3(SK_KS * 64), args, 0, stream);
+}
+
+// Workgroups of gemv_lds_kernel: one per CU, fewer when the rows run out
+// (at least 16 rows each), more when a share would exceed LK_RMAX rows.
+int lds_grid(const GemmArgs& p) {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+        cus = 256;
+    const int no = p.swiglu ? p.N / 2 : p.N;
+    int g = min(cus, (no + 15) / 16);
+    if ((no + g - 1) / g > LK_RMAX) g = (no + LK_RMAX - 1) / LK_RMAX;
+    return g;
+}
+
+template <int PIECE>
+bool lds_fits(const GemmArgs& p) {
+    if (p.K < 4 * PIECE || static_cast<int64_t>(p.M) * p.K > INT32_MAX) return false;
+    const int no = p.swiglu ? p.N / 2 : p.N;
+    const int g = lds_grid(p);
+    const int64_t r = (no + g - 1) / g;
+    return r * p.K + PIECE <= INT32_MAX;
+}
+
+template <int PIECE, int NS>
+hipError_t launch_lds_t(const GemmArgs& p, hipStream_t stream) {
+    GemmArgs a = p;
+    void* args[] = {&a};
+    const void* f;
+    if (p.swiglu) {
+        f = p.out_dtype == FKE_OUT_F32 ? reinterpret_cast<const void*>(&gemv_lds_kernel<FKE_OUT_F32, true, PIECE, NS>)
+                                       : reinterpret_cast<const void*>(&gemv_lds_kernel<FKE_OUT_BF16, true, PIECE, NS>);
+    } else {
+        switch (p.out_dtype) {
+            case FKE_OUT_F32: f = reinterpret_cast<const void*>(&gemv_lds_kernel<FKE_OUT_F32, false, PIECE, NS>); break;
+            case FKE_OUT_BF16: f = reinterpret_cast<const void*>(&gemv_lds_kernel<FKE_OUT_BF16, false, PIECE, NS>); break;
+            default: f = reinterpret_cast<const void*>(&gemv_lds_kernel<FKE_OUT_I32, false, PIECE, NS>); break;
+        }
+    }
+    return hipLaunchKernel(f, dim3(lds_grid(p)), dim3(256), args, 0, stream);
 }
 
 template <int MT, bool FULLK, int NB = ROWS_NB>
@@ -434,12 +780,18 @@ bool gemv_i8_supports(const GemmArgs& p) {
     if (!(p.M >= 1 && p.M <= 16 && p.N >= 1 && p.K >= 64 && p.K % 64 == 0 && p.b_layout == FKE_B_NK &&
           ((a | b) & 15) == 0))
         return false;
-    // SwiGLU pairs: the row kernel up to M = 4, the skinny MFMA kernel above
-    return !p.swiglu || p.M <= 4 || skinny_offsets_fit(p);
+    // SwiGLU pairs: the row kernel up to M = 4, the LDS-streamed kernel from
+    // M = 3 when K >= 4 KiB, the skinny MFMA kernel otherwise
+    return !p.swiglu || p.M <= 4 || lds_fits<1024>(p) || skinny_offsets_fit(p);
 }
 
 
 hipError_t launch_gemv_i8(const GemmArgs& p, hipStream_t s) {
+    // M >= 3 with K >= 4 KiB: the LDS-streamed kernel (11.4-11.8 us at
+    // N = 14336, K = 4096 for every M in 3..16, against 12.5-18.1 us for the
+    // row and skinny kernels; SwiGLU 20.3-20.9 us against 21.5-34.3 us).  At
+    // M = 1, 2 the row kernel is faster (9.8 / 11.0 us against 11.6 us).
+    if (p.M >= 3 && lds_fits<1024>(p)) return launch_lds_t<1024, 2>(p, s);
     if (p.swiglu) {
         if (p.M <= 4) return p.K % 4096 == 0 ? launch_rows_m<true>(p, s) : launch_rows_m<false>(p, s);
         return launch_mfma_skinny(p, s);

@@ -104,7 +104,8 @@ def test_swiglu_rejects_bad_arguments():
     (4096, 14336, 4096, _lib.PATH_MFMA),
     (64, 64, 100, _lib.PATH_GENERIC),
     (2, 300000, 4096, _lib.PATH_GEMV),     # row kernel: 64-bit row bases
-    (8, 300000, 4096, _lib.PATH_GENERIC),  # 2I*K past the 32-bit offsets of the MFMA kernels
+    (8, 300000, 4096, _lib.PATH_GEMV),     # LDS-streamed kernel: buffer bases per workgroup
+    (8, 600000, 2048, _lib.PATH_GENERIC),  # K < 4096 and 2I*K past the skinny kernel's 32-bit offsets
 ])
 def test_dispatch_i8_swiglu(M, I, K, expect):
     assert _lib.lib().fke_select_path_i8_swiglu(P, P, P, M, I, K, 0) == expect

@@ -161,6 +161,49 @@ def test_gemv_k_variants(oracle, dev, M, K):
     assert_same(gpu_i8(A, B, "nk", "i32", "gemv"), acc, f"gemv K={K}")
 
 
+# The LDS-streamed decode kernel (3 <= M <= 16, K >= 4096): small N (fewer
+# workgroups than CUs), N not a multiple of 16, K with a partial last 1 KiB
+# piece, K = 14336 (waves own 4 or 3 pieces), several tile chunks per
+# workgroup (N = 20000), every output type, scales as vectors or scalars,
+# with and without bias.
+STREAM_SHAPES = [(100, 4096), (1000, 4160), (777, 5056), (4096, 14336), (20000, 4096), (129, 8192)]
+
+
+@pytest.mark.parametrize("shape", STREAM_SHAPES)
+@pytest.mark.parametrize("M", [3, 8, 16])
+def test_gemv_streamed_shapes(oracle, dev, M, shape):
+    N, K = shape
+    say("gemv streamed", M, N, K)
+    A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 700 + M + N + K, act="normal")
+    acc = oracle.w8a8_acc(A, B, nthreads=NTH)
+    assert_same(gpu_i8(A, B, "nk", "i32", "gemv"), acc, f"streamed M={M} {shape} i32")
+    got = gpu_i8(A, B, "nk", "bf16", "gemv", sa, sb, bias=bias)
+    assert_same(got, oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, "bf16"), f"streamed M={M} {shape} bf16")
+    got = gpu_i8(A, B, "nk", "f32", "gemv", sa=0.013, sb=0.007)
+    assert_same(got, oracle_out(oracle, acc, None, None, 0.013, 0.007, None, "f32"), f"streamed M={M} {shape} f32")
+
+
+def test_gemv_streamed_more_workgroups_than_cus(oracle, dev):
+    """N = 140000 rows: a share would pass 512 rows per CU, so the launch takes
+    more workgroups than CUs; sampled columns against the oracle."""
+    M, N, K = 5, 140000, 4096
+    say("gemv streamed, N > 512 rows per CU", M, N, K)
+    g = torch.Generator(device=dev)
+    g.manual_seed(4242)
+    Bd = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=g)
+    A = oracle.gen_i8_clipped_normal((M, K), 4243, 30.0)
+    sa = oracle.gen_f32_uniform((M,), 4244, 0.001, 0.02)
+    sb = oracle.gen_f32_uniform((N,), 4245, 0.001, 0.02)
+    bias = oracle.gen_f32_normal((N,), 4246, 0.0, 0.02)
+    out = ops.w8a8_gemm(dev_t(A), Bd, dev_t(sa), dev_t(sb), dev_t(bias), out_dtype=torch.float32, path="gemv")
+    torch.cuda.synchronize()
+    cols = np.concatenate([np.arange(0, 600), np.arange(N // 2 - 300, N // 2 + 300), np.arange(N - 600, N)])
+    Bs = Bd[torch.from_numpy(cols).long().cuda()].cpu().numpy()
+    acc = oracle.w8a8_acc(A, Bs, nthreads=NTH)
+    ref = oracle.w8a8_epilogue(acc, sa, sb[cols], 1.0, 1.0, bias[cols], oracle.OUT_F32)
+    assert_same(out[:, torch.from_numpy(cols).long().cuda()].cpu().numpy(), ref, "streamed N=140000")
+
+
 @pytest.mark.parametrize("shape", [(1, 1, 1), (7, 13, 77), (65, 3, 5), (33, 70, 129), (2, 5, 4)])
 @pytest.mark.parametrize("layout", ["nk", "kn"])
 def test_generic_odd_shapes(oracle, dev, shape, layout):

@@ -220,6 +220,34 @@ def test_w8a8_swiglu_decode_full(oracle, dev, M):
     check_f32(h.cpu().numpy(), oracle.w8a8_swiglu(A, W, sa, sb, bias=bias, nthreads=NTH), f"decode M={M}")
 
 
+def test_w8a8_swiglu_decode_weight_past_2gib(oracle, dev):
+    """M = 8, I = 300000, K = 4096: the [gate; up] weight is 2.46 GB, past
+    32-bit offsets from its base; the LDS-streamed kernel addresses each
+    workgroup's rows from their own base.  Sampled output columns (both ends,
+    the middle) against the oracle on host copies of their gate and up rows."""
+    M, I, K = 8, 300000, 4096
+    say("w8a8_swiglu decode, weight past 2 GiB", M, I, K)
+    assert _lib.lib().fke_select_path_i8_swiglu(4096, 4096, 4096, M, I, K, 0) == _lib.PATH_GEMV
+    g = torch.Generator(device=dev)
+    g.manual_seed(31337)
+    Wd = torch.randint(-127, 128, (2 * I, K), dtype=torch.int8, device=dev, generator=g)
+    A = oracle.gen_i8_clipped_normal((M, K), 31338, 30.0)
+    sa = oracle.gen_f32_uniform((M,), 31339, 0.001, 0.02)
+    sb = oracle.gen_f32_uniform((2 * I,), 31340, 0.0005, 0.005)
+    bias = oracle.gen_f32_normal((2 * I,), 31341, 0.0, 0.5)
+    h = ops.w8a8_swiglu(dev_t(A), Wd, dev_t(sa), dev_t(sb), dev_t(bias), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    cols = np.concatenate([np.arange(0, 300), np.arange(I // 2 - 150, I // 2 + 150), np.arange(I - 300, I)])
+    rows = np.concatenate([cols, I + cols])
+    Ws = Wd[torch.from_numpy(rows).long().cuda()].cpu().numpy()
+    del Wd
+    ns = len(cols)
+    ref = oracle.w8a8_swiglu(A, Ws, sa, np.concatenate([sb[cols], sb[I + cols]]),
+                             bias=np.concatenate([bias[cols], bias[I + cols]]), nthreads=NTH)
+    check_f32(h[:, torch.from_numpy(cols).long().cuda()].cpu().numpy(), ref, "decode past 2 GiB")
+    assert ref.shape == (M, ns)
+
+
 def test_w8a8_swiglu_prefill_full(oracle, dev):
     """M = 4096 tokens, I = 14336, K = 4096: all rows against the unfused GPU
     pipeline (bit for bit), sampled rows against the oracle."""
