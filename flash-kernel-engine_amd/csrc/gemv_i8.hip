@@ -551,65 +551,79 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
         for (int s = 0; s < S; ++s) c = __builtin_amdgcn_mfma_i32_16x16x64_i8(act[s], w[s], c, 0, 0, 0);
     };
 
-    // End of a tile chunk: the four waves' partials meet in LDS; thread
-    // (m, nl) = (tid / 16, tid % 16) finishes output column nl of each tile.
-    // Lane l of a wave holds tile column l%16, rows 4*(l/16)+v.  The LDS
-    // accesses are inline for the reason given at the fragment reads.
+    // Lane l of a wave holds tile column l%16, rows 4*(l/16)+v of an MFMA
+    // tile.  The LDS accesses of the reduction are inline for the reason
+    // given at the fragment reads.
     auto ld = [](const void* a) __attribute__((always_inline)) {
         int v;
         asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"((lds_u8*)(const_cast<void*>(a))));
         return v;
     };
-    auto finish = [&](int tc, int nt) __attribute__((always_inline)) {
+    // Finishing tile u of chunk tc (SWI: the pair u-1, u): the waves' partial
+    // sums go to red, and after a barrier thread (m, nl) = (tid/16, tid%16)
+    // computes output column nl into yv[u] / sv[u].  Called by every wave once
+    // its share of the tile is summed, so a chunk's early tiles are reduced
+    // while the later tiles' copies stream in; the stores wait for the end of
+    // the chunk (8 % faster at M = 4 than one reduction at the chunk's end).
+    float yv[LK_TMAX];
+    int32_t sv[LK_TMAX];
+    auto finish_tile = [&](int tc, int u) __attribute__((always_inline)) {
+        constexpr int NQ = SWI ? 2 : 1;  // tiles finished together
 #pragma unroll
-        for (int q = 0; q < LK_TMAX; ++q) {
-            if (q < nt) asm volatile("ds_write_b128 %0, %1" : : "v"((lds_u8*)&red[q][wave][lane * 4]), "v"(acc[q]) : "memory");
-            acc[q] = v4i{0, 0, 0, 0};
+        for (int q = 0; q < NQ; ++q) {
+            // The MFMA result passes through a VALU move first: the compiler
+            // puts the wait states an MFMA result needs before a VALU reads
+            // it, but not before an inline-asm store does.
+            v4i a;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                a[e] = __builtin_amdgcn_update_dpp(0, acc[u - NQ + 1 + q][e], 0xE4, 0xF, 0xF, false);
+            asm volatile("ds_write_b128 %0, %1" : : "v"((lds_u8*)&red[u - NQ + 1 + q][wave][lane * 4]), "v"(a)
+                         : "memory");
         }
         wait_lgkm0();
         barrier();
         const int m = tid >> 4, nl = tid & 15;
+        if (m >= M) return;
         const int ri = ((m >> 2) * 16 + nl) * 4 + (m & 3);
-        if (m < M) {
-            int xa = ld(esa + m);
-            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(xa));
-            const float sam = p.scale_a ? __int_as_float(xa) : p.sa;
-            if constexpr (SWI) {
-                for (int q = 0; q < nt; q += 2) {
-                    const int r = 16 * ((tc * LK_TMAX + q) >> 1) + nl;
-                    int g0 = ld(&red[q][0][ri]), g1 = ld(&red[q][1][ri]), g2 = ld(&red[q][2][ri]), g3 = ld(&red[q][3][ri]);
-                    int u0 = ld(&red[q + 1][0][ri]), u1 = ld(&red[q + 1][1][ri]), u2 = ld(&red[q + 1][2][ri]),
-                        u3 = ld(&red[q + 1][3][ri]);
-                    int bg = ld(esb + r), bu = ld(esb + LK_RMAX + r), cg = ld(ebias + r), cu = ld(ebias + LK_RMAX + r);
-                    asm volatile("s_waitcnt lgkmcnt(0)"
-                                 : "+v"(g0), "+v"(g1), "+v"(g2), "+v"(g3), "+v"(u0), "+v"(u1), "+v"(u2), "+v"(u3),
-                                   "+v"(bg), "+v"(bu), "+v"(cg), "+v"(cu));
-                    if (r < nr) {
-                        const float sg = sam * (p.scale_b ? __int_as_float(bg) : p.sb);
-                        const float su = sam * (p.scale_b ? __int_as_float(bu) : p.sb);
-                        const float ag = static_cast<float>(g0 + g1 + g2 + g3), au = static_cast<float>(u0 + u1 + u2 + u3);
-                        const float yg = p.bias ? __builtin_fmaf(ag, sg, __int_as_float(cg)) : ag * sg;
-                        const float yu = p.bias ? __builtin_fmaf(au, su, __int_as_float(cu)) : au * su;
-                        store_out<OUT>(p.C, static_cast<size_t>(m) * NO + r0 + r, swiglu_pair(yg, yu), 0);
-                    }
-                }
-            } else {
-                for (int q = 0; q < nt; ++q) {
-                    const int r = 16 * (tc * LK_TMAX + q) + nl;
-                    int a0 = ld(&red[q][0][ri]), a1 = ld(&red[q][1][ri]), a2 = ld(&red[q][2][ri]), a3 = ld(&red[q][3][ri]);
-                    int b = ld(esb + r), cb = ld(ebias + r);
-                    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a0), "+v"(a1), "+v"(a2), "+v"(a3), "+v"(b), "+v"(cb));
-                    if (r < nr) {
-                        const int32_t sum = a0 + a1 + a2 + a3;
-                        const float sc = sam * (p.scale_b ? __int_as_float(b) : p.sb);
-                        const float y = p.bias ? __builtin_fmaf(static_cast<float>(sum), sc, __int_as_float(cb))
-                                               : static_cast<float>(sum) * sc;
-                        store_out<OUT>(p.C, static_cast<size_t>(m) * NO + r0 + r, y, sum);
-                    }
-                }
-            }
+        const int t = tc * LK_TMAX + u;  // SWI: the up tile of the pair
+        const int r = 16 * (SWI ? t >> 1 : t) + nl;
+        int x[4 * NQ];
+#pragma unroll
+        for (int q = 0; q < NQ; ++q)
+#pragma unroll
+            for (int w = 0; w < 4; ++w) x[4 * q + w] = ld(&red[u - NQ + 1 + q][w][ri]);
+        int xa = ld(esa + m), b0 = ld(esb + r), c0 = ld(ebias + r);
+        int b1 = SWI ? ld(esb + LK_RMAX + r) : 0, c1 = SWI ? ld(ebias + LK_RMAX + r) : 0;
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(xa), "+v"(b0), "+v"(c0), "+v"(b1), "+v"(c1));
+#pragma unroll
+        for (int q = 0; q < 4 * NQ; ++q) asm volatile("" : "+v"(x[q]));
+        const float sam = p.scale_a ? __int_as_float(xa) : p.sa;
+        const int32_t s0 = x[0] + x[1] + x[2] + x[3];
+        const float sc0 = sam * (p.scale_b ? __int_as_float(b0) : p.sb);
+        const float y0 = p.bias ? __builtin_fmaf(static_cast<float>(s0), sc0, __int_as_float(c0))
+                                : static_cast<float>(s0) * sc0;
+        if constexpr (SWI) {
+            const int32_t s1 = x[4] + x[5] + x[6] + x[7];
+            const float sc1 = sam * (p.scale_b ? __int_as_float(b1) : p.sb);
+            const float y1 = p.bias ? __builtin_fmaf(static_cast<float>(s1), sc1, __int_as_float(c1))
+                                    : static_cast<float>(s1) * sc1;
+            yv[u] = swiglu_pair(y0, y1);
+        } else {
+            yv[u] = y0;
+            sv[u] = s0;
         }
-        barrier();  // the partials of the next chunk overwrite red
+    };
+    // The chunk's stores: thread (m, nl) holds output column nl of each tile.
+    auto store_chunk = [&](int tc, int nt) __attribute__((always_inline)) {
+        const int m = tid >> 4, nl = tid & 15;
+        if (m >= M) return;
+#pragma unroll
+        for (int u = SWI ? 1 : 0; u < LK_TMAX; u += SWI ? 2 : 1) {
+            const int t = tc * LK_TMAX + u;
+            const int r = 16 * (SWI ? t >> 1 : t) + nl;
+            if (u < nt && r < nr) store_out<OUT>(p.C, static_cast<size_t>(m) * NO + r0 + r, yv[u], sv[u]);
+        }
     };
 
     // Prologue: the first NS items in flight.
@@ -655,10 +669,14 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
                     read_all(slot, w);
                     refill(slot);
                     mma(acc[u], w);
+                    if (j == np - 1 && (!SWI || (u & 1))) finish_tile(tc, u);
                 }
             }
         }
-        finish(tc, nt);
+        store_chunk(tc, nt);
+#pragma unroll
+        for (int q = 0; q < LK_TMAX; ++q) acc[q] = v4i{0, 0, 0, 0};
+        barrier();  // every read of red for this chunk precedes the next chunk's writes
     }
 }
 
