@@ -57,6 +57,8 @@ def parse():
     ap.add_argument("--swiglu", action="store_true", help="also time the SwiGLU configs (part of --extra)")
     ap.add_argument("--half", action="store_true", help="also time the fp16/bf16 GEMM (part of --extra)")
     ap.add_argument("--fp8", action="store_true", help="also time the FP8 e4m3 GEMM 8192^3 (part of --extra)")
+    ap.add_argument("--shards", action="store_true",
+                    help="also time the per-GPU shards of 8-way tensor parallelism (part of --extra)")
     ap.add_argument("--data-sweep", action="store_true",
                     help="also time the headline GEMM on zero, constant and narrow-range operands (clock vs data)")
     ap.add_argument("--vendor", action="store_true",
@@ -160,8 +162,10 @@ def main():
         del src, dst
     if args.extra:
         line["extra"] = extra_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args)
-    elif args.swiglu or args.half or args.fp8:
+    elif args.swiglu or args.half or args.fp8 or args.shards:
         line["extra"] = {}
+        if args.shards:
+            line["extra"].update(shard_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args))
         if args.fp8:
             line["extra"].update(fp8_configs(torch, L, _lib, dev, gen, timed, args))
         if args.swiglu:
@@ -258,6 +262,32 @@ def gemv_bench(torch, L, _lib, dev, gen, M, nbuf, launches, N=14336, K=4096):
             "kernel": gemv_kernel(M)}
 
 
+def shard_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
+    """One GPU's shard of 8-way tensor parallelism, at real size: the decode and prefill
+    weights split by output columns (no exchange), and the 8192^3 problem split by columns
+    (fp32 out) and by K (int32 partial sums, the exact all-reduce form)."""
+    res = {}
+    for m in (1, 16):
+        r = gemv_bench(torch, L, _lib, dev, gen, m, 48, args.gemv_launches, N=1792, K=4096)
+        res[f"tp8_decode_colshard_M{m}_1792x4096_bf16"] = {
+            "us": r["us_per_launch"], "GB/s": r["value"], "frac": r["roofline"]["frac"],
+            "bytes": r["roofline"]["algorithmic_bytes_per_launch"], "kernel": r["kernel"]}
+    sh = torch.cuda.current_stream(dev).cuda_stream
+    for name, (M, N, K, out, tdt) in {
+            "tp8_prefill_colshard_4096x1376x4096_bf16": (4096, 1376, 4096, _lib.OUT_BF16, torch.bfloat16),
+            "tp8_int8_colshard_8192x1024x8192_f32": (8192, 1024, 8192, _lib.OUT_F32, torch.float32),
+            "tp8_int8_kshard_8192x8192x1024_i32": (8192, 8192, 1024, _lib.OUT_I32, torch.int32)}.items():
+        A, B, sa, sb = rand_i8(M, K), rand_i8(N, K), rand_u(M), rand_u(N)
+        C = torch.empty((M, N), dtype=tdt, device=dev)
+        ms = timed(lambda: L.fke_qgemm_i8(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, sa.data_ptr(),
+                                          sb.data_ptr(), 1.0, 1.0, None, out, _lib.B_NK, sh),
+                   args.steps, args.warmup)
+        t = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+        res[name] = {"ms": round(ms, 4), "TOPS": round(t, 1), "frac": round(t / PEAK_INT8_TOPS, 4)}
+        del A, B, C
+    return res
+
+
 def extra_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
     res = {}
     # prefill 4096 x 11008 x 4096, bf16 out
@@ -298,6 +328,7 @@ def extra_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
                                                "frac": round(t / PEAK_FP8_TFLOPS, 4)}
     del A8, B8, C
     res.update(half_configs(torch, L, _lib, dev, gen, timed, args))
+    res.update(shard_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args))
     for m in (4, 16):
         res[f"gemv_M{m}"] = gemv_bench(torch, L, _lib, dev, gen, m, args.gemv_buffers, args.gemv_launches)
     # per-token INT8 quantiser in front of the W8A8 GEMM: bf16 activations of C3 (4096 x 4096),
