@@ -369,9 +369,10 @@ __global__ __launch_bounds__(SK_KS * 64) void gemv_mfma_kernel(GemmArgs p) {
 // against the piece's activation rows.  Those arrive the same way (an item of
 // activation rows 0..15, read into registers once per piece and tile chunk).
 // The wave walks its pieces for LK_TMAX tiles at a time (a tile chunk),
-// accumulating each tile; at the end of a chunk the four waves' partial sums
-// meet in LDS and the chunk's outputs are finished (exact int32 sums, so any
-// split is bit-exact).
+// accumulating each tile; as soon as every wave has summed its share of a
+// tile, the four partial sums meet in LDS and the tile's outputs are computed
+// (exact int32 sums, so any split is bit-exact), while later tiles stream in;
+// the outputs are stored at the end of the chunk.
 // k order: a dot product is a sum, so the MFMA's k positions may map to any
 // permutation of a piece's bytes as long as both operands use the same one.
 // With S = PIECE/64 steps, step s of lane group g = l/16 takes 16-byte chunk
