@@ -5,8 +5,9 @@ GEMV (N=14336, K=4096).  One "step" is one W8A8 INT8 GEMM at 8192^3 (per-token x
 per-channel fp32 scales, fp32 out) with inputs resident in HBM; `value` is its
 throughput in TOPS.  The decode GEMV (bf16 out + fused bias, weights rotated
 over 8 distinct 56 MiB buffers so the 256 MiB MALL cannot hold them) is timed in
-the same run and reported under "decode_gemv".  Inputs are random (torch RNG on
-the device), never zero-filled.
+the same run and reported under "decode_gemv", and the M=16 decode (the other
+end of the decode configs) under "decode_gemv_m16".  Inputs are random (torch RNG
+on the device), never zero-filled.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--extra | --fp8 --swiglu --half] [--vendor] [--data-sweep] [--no-cpu]
 """
@@ -126,8 +127,9 @@ def main():
     tops = ops_per / (ms * 1e-3) / 1e12
     del C
 
-    # ---- decode GEMV M=1, N=14336, K=4096, bf16 out + bias ---------------------
+    # ---- decode GEMV M=1 and M=16, N=14336, K=4096, bf16 out + bias -------------
     gemv = gemv_bench(torch, L, _lib, dev, gen, 1, args.gemv_buffers, args.gemv_launches)
+    gemv16 = gemv_bench(torch, L, _lib, dev, gen, 16, args.gemv_buffers, args.gemv_launches)
 
     line = {
         "metric": "INT8 TOPS at 8192^3 + HBM GB/s at M=1 decode GEMV (N=14336,K=4096)",
@@ -150,6 +152,7 @@ def main():
                      "traffic": traffic("gemm_mfma_kernel<i8,NK,f32> M=N=K=8192"),
                      "algorithmic_ops_per_launch": ops_per},
         "decode_gemv": gemv,
+        "decode_gemv_m16": gemv16,
         "timed_wall_s": round(wall, 3),
     }
     line["hbm_copy_GBps"] = copy_bandwidth(torch, dev, gen)
@@ -329,7 +332,7 @@ def extra_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
     del A8, B8, C
     res.update(half_configs(torch, L, _lib, dev, gen, timed, args))
     res.update(shard_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args))
-    for m in (4, 16):
+    for m in (4,):
         res[f"gemv_M{m}"] = gemv_bench(torch, L, _lib, dev, gen, m, args.gemv_buffers, args.gemv_launches)
     # per-token INT8 quantiser in front of the W8A8 GEMM: bf16 activations of C3 (4096 x 4096),
     # 12 rotating inputs (384 MiB, more than the MALL), timed from a HIP graph like the GEMV
