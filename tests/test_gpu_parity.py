@@ -181,6 +181,8 @@ def test_gemv_streamed_shapes(oracle, dev, M, shape):
     assert_same(got, oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, "bf16"), f"streamed M={M} {shape} bf16")
     got = gpu_i8(A, B, "nk", "f32", "gemv", sa=0.013, sb=0.007)
     assert_same(got, oracle_out(oracle, acc, None, None, 0.013, 0.007, None, "f32"), f"streamed M={M} {shape} f32")
+    got = gpu_i8(A, B, "nk", "f32", "gemv", sa_vec=sa, sb=0.007, bias=bias)
+    assert_same(got, oracle_out(oracle, acc, sa, None, 1.0, 0.007, bias, "f32"), f"streamed M={M} {shape} mixed")
 
 
 def test_gemv_streamed_more_workgroups_than_cus(oracle, dev):
