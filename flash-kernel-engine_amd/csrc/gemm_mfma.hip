@@ -4,7 +4,9 @@
 // int8_gemm_dp4a_kernel) and :99-118 (FP8, fp8_gemm_scaled_kernel) for M > 16.
 //
 // Workgroup tile 256x256, 4 waves (one per SIMD) in a 2x2 grid; each wave owns
-// 128x128 outputs as 4x4 MFMA blocks of 32x32 (256 accumulator AGPRs).
+// 128x128 outputs as 4x4 MFMA blocks of 32x32 (256 accumulator AGPRs).  The
+// launch is persistent: one workgroup per CU (a multiple of the XCD count)
+// walks its tiles without a relaunch between them.
 //   INT8: v_mfma_i32_32x32x32_i8   (exact int32 accumulation), 4 k steps/stage
 //   FP8 : v_mfma_f32_32x32x64_f8f6f4 with E4M3 operands (fp32), 2 k steps/stage
 // K advances 128 bytes per stage; two LDS stages of (256+256)x128 bytes
@@ -314,8 +316,15 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
     constexpr int TC = tile_cols<SWI>();
     const int NO = SWI ? N >> 1 : N;  // output columns
     const int gm = (M + BM - 1) / BM, gn = (NO + TC - 1) / TC;
+    // Persistent: workgroup b takes tiles b, b + G, b + 2G, ... (G = grid size,
+    // a multiple of the XCD count, so every tile of a workgroup stays on its
+    // XCD and each XCD walks its tile range in the same order as a one-tile-
+    // per-workgroup launch would), so a CU moves to its next tile without a
+    // workgroup relaunch.
+    for (int slot = blockIdx.x; slot < gm * gn; slot += gridDim.x) {
+    if (slot != static_cast<int>(blockIdx.x)) barrier();  // the last tile's epilogue read epi_* from LDS
     int tm, tn;
-    tile_of(blockIdx.x, gm, gn, tm, tn);
+    tile_of(slot, gm, gn, tm, tn);
     const int m0 = tm * BM, n0 = tn * TC;  // n0: first output column
 
     const int8_t* A = static_cast<const int8_t*>(p.A);
@@ -540,7 +549,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
                 }
             }
         }
-        return;
+        continue;
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -582,16 +591,22 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
             }
         }
     }
+    }
 }
 
 template <int ELEM, int BL, int OUT, bool SWI = false>
 hipError_t launch_t(const GemmArgs& p, hipStream_t stream) {
     constexpr int TC = tile_cols<SWI>();
     const int gm = (p.M + BM - 1) / BM, gn = ((SWI ? p.N / 2 : p.N) + TC - 1) / TC;
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < NXCD)
+        cus = 256;
+    const int grid = min(gm * gn, cus / NXCD * NXCD);
     GemmArgs a = p;
     void* args[] = {&a};
     return hipLaunchKernel(reinterpret_cast<const void*>(&gemm_mfma_kernel<ELEM, BL, OUT, SWI>),
-                           dim3(gm * gn), dim3(NTHREADS), args, 0, stream);
+                           dim3(grid), dim3(NTHREADS), args, 0, stream);
 }
 
 template <int ELEM, int BL>
