@@ -95,7 +95,10 @@ GemmArgs make_swiglu_args(const void* A, const void* W, void* H, int M, int I, i
 }
 
 int pick_i8(const GemmArgs& p) {
-    if (p.M <= 16 && fke::gemv_i8_supports(p)) return FKE_PATH_GEMV;
+    // decode and batches up to FKE_GEMV_MAX_M rows: the decode family where
+    // its cost model beats the MFMA GEMM's, or where that GEMM cannot run
+    if (fke::gemv_i8_supports(p) && (fke::gemv_i8_batch_pays(p) || !fke::mfma_supports(p, fke::ELEM_I8)))
+        return FKE_PATH_GEMV;
     if (fke::mfma_supports(p, fke::ELEM_I8)) return FKE_PATH_MFMA;
     return FKE_PATH_GENERIC;
 }

@@ -41,8 +41,13 @@ hipError_t launch_quant_rows(const void* X, int in_dtype, int M, int K, int8_t* 
 hipError_t launch_swiglu(const void* gate, const void* up, void* out, int64_t n, int dtype,
                          hipStream_t stream);
 
+// Largest batch the decode family takes: past 16 rows only its LDS-streamed
+// kernel, 64 activation rows per workgroup and more workgroups beyond that.
+constexpr int FKE_GEMV_MAX_M = 512;
+
 // Shape/alignment predicates of the fast families (host side).
 bool gemv_i8_supports(const GemmArgs& p);
+bool gemv_i8_batch_pays(const GemmArgs& p);  // M > 16: the decode family beats the MFMA GEMM
 bool mfma_supports(const GemmArgs& p, int elem);
 
 // ---------------------------------------------------------------------------

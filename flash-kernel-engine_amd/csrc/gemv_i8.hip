@@ -357,7 +357,7 @@ __global__ __launch_bounds__(SK_KS * 64) void gemv_mfma_kernel(GemmArgs p) {
     }
 }
 
-// gemv_lds_kernel (M <= 16): the weight panel streamed through LDS.  One
+// gemv_lds_kernel (M <= 64 per workgroup): the weight panel streamed through LDS.  One
 // workgroup per CU owns an even share of R = ceil(NO / G) weight rows
 // (output columns), so every CU reads the same number of bytes, and keeps
 // its HBM reads in flight from its first instruction to its last.
@@ -366,8 +366,11 @@ __global__ __launch_bounds__(SK_KS * 64) void gemv_mfma_kernel(GemmArgs p) {
 // LDS with buffer_load_dwordx4 ... lds instructions of 1 KiB each (one or two
 // rows' contiguous bytes), keeps NS items in flight in a ring of NS slots, and
 // multiplies a landed item from LDS with PIECE/64 v_mfma_i32_16x16x64_i8
-// against the piece's activation rows.  Those arrive the same way (an item of
-// activation rows 0..15, read into registers once per piece and tile chunk).
+// against the piece's activation rows.  Those arrive the same way (MB items
+// of 16 activation rows, read into registers once per piece and tile chunk;
+// each weight fragment then feeds MB MFMAs).  Batches past 16*MB rows run
+// as more workgroups along y, one 16*MB-row chunk of A each: their copies of
+// a weight share find it in the last-level cache.
 // The wave walks its pieces for LK_TMAX tiles at a time (a tile chunk),
 // accumulating each tile; as soon as every wave has summed its share of a
 // tile, the four partial sums meet in LDS and the tile's outputs are computed
@@ -390,7 +393,8 @@ constexpr int LK_RMAX = 512;  // weight rows (of each half) of one workgroup
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
 // Position in a wave's item sequence: tile chunk tc (nt tiles), the wave's
-// j-th piece, and u = -1 (the piece's activation rows) or tile u of the chunk.
+// j-th piece, and u < 0 (activation rows 16*(u+MB).. of the piece) or tile u
+// of the chunk.
 struct LkPos {
     int tc, nt, j, u;
 };
@@ -419,7 +423,7 @@ __device__ __forceinline__ void wait_lgkm_tied(int n, v4i& r) {
     }
 }
 
-template <int OUT, bool SWI, int PIECE, int NS>
+template <int OUT, bool SWI, int PIECE, int NS, int MB>
 __global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
     constexpr int H = SWI ? 2 : 1;
     constexpr int RPW = 1024 / PIECE;  // rows per 1 KiB copy instruction
@@ -429,13 +433,21 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
     static_assert(PIECE == 512 || PIECE == 1024, "piece of 512 or 1024 bytes");
     static_assert(DI == 8 || DI == 16, "vmcnt steps of wait_vm_n are 8 copies");
     static_assert((NS - 1) * DI <= 32, "wait_vm_n covers up to 32 copies");
+    static_assert(MB >= 1 && MB <= 4, "up to 64 activation rows per workgroup (esa, one dword copy per lane)");
+    // Partial sums of the tiles being finished: all tiles of a chunk for one
+    // activation block (no barrier between two finishes), or with more blocks
+    // only the tile (SWI: pair) at hand, which leaves the LDS to a deeper ring.
+    constexpr int NQ = SWI ? 2 : 1;  // tiles finished together
+    constexpr int RT = MB == 1 ? LK_TMAX : NQ;
     __shared__ __attribute__((aligned(1024))) uint8_t ring[NS][4][16 * PIECE];
-    __shared__ __attribute__((aligned(16))) int32_t red[LK_TMAX][4][256];
+    __shared__ __attribute__((aligned(16))) int32_t red[RT][4][MB * 256];
     __shared__ __attribute__((aligned(16))) float esb[H * LK_RMAX], ebias[H * LK_RMAX], esa[64];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int M = p.M, K = p.K;
+    const int K = p.K;
+    const int mc = blockIdx.y * 16 * MB;  // first activation row of this workgroup
+    const int M = min(16 * MB, p.M - mc);
     const int NO = SWI ? p.N >> 1 : p.N;  // output columns
     const int R = (NO + static_cast<int>(gridDim.x) - 1) / static_cast<int>(gridDim.x);
     const int r0 = blockIdx.x * R;
@@ -471,13 +483,14 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
             }
         }
         if (p.scale_a)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(p.scale_a, M * 4), (lds_u8*)esa, 4, 4 * lane, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(p.scale_a + mc, M * 4), (lds_u8*)esa, 4, 4 * lane, 0,
+                                                     0, 0);
     }
 
     const int8_t* B = static_cast<const int8_t*>(p.B);
     const __amdgpu_buffer_rsrc_t rb0 = make_rsrc(B + static_cast<size_t>(r0) * K, nr * K);
     const __amdgpu_buffer_rsrc_t rb1 = make_rsrc(B + static_cast<size_t>(SWI ? NO + r0 : r0) * K, nr * K);
-    const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, M * K);
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(static_cast<const int8_t*>(p.A) + static_cast<size_t>(mc) * K, M * K);
     lds_u8* const lring = (lds_u8*)(&ring[0][wave][0]);  // slot q at + q * 4 * 16 * PIECE
 
     // copy lanes: lane l fills slot l % (64/RPW) of row d*RPW + l / (64/RPW)
@@ -486,11 +499,12 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
     auto issue = [&](const LkPos& it, lds_u8* dst) __attribute__((always_inline)) {
         const int pc = (wave + 4 * it.j) * PIECE;  // first k byte of the piece
         if (it.u < 0) {
+            const int a0 = 16 * (it.u + MB);  // first activation row of the item
 #pragma unroll
             for (int d = 0; d < DI; ++d) {
                 const int i = d * RPW + crow;
                 const int k = pc + ((cslot ^ z(i)) << 4);
-                const uint32_t off = i < M && k < K ? static_cast<uint32_t>(i * K + k) : 0x80000000u;
+                const uint32_t off = a0 + i < M && k < K ? static_cast<uint32_t>((a0 + i) * K + k) : 0x80000000u;
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, dst + d * 1024, 16, static_cast<int>(off), 0, 0, 0);
             }
         } else {
@@ -509,7 +523,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
     // advance to the next item; false past the last one
     auto advance = [&](LkPos& it) __attribute__((always_inline)) {
         if (++it.u < it.nt) return true;
-        it.u = -1;
+        it.u = -MB;
         if (++it.j < np) return true;
         it.j = 0;
         ++it.tc;
@@ -520,10 +534,12 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
     // lane l = 16g + i reads row i, chunk S*g + s at slot (S*g + s) ^ z(i)
     const int li = lane & 15;
     const uint32_t lb = static_cast<uint32_t>(li * PIECE + (lane >> 4) * (PIECE / 4) + z(li) * 16);
-    v4i act[S];
-    v4i acc[LK_TMAX];
+    v4i act[MB][S];
+    v4i acc[LK_TMAX][MB];
 #pragma unroll
-    for (int q = 0; q < LK_TMAX; ++q) acc[q] = v4i{0, 0, 0, 0};
+    for (int q = 0; q < LK_TMAX; ++q)
+#pragma unroll
+        for (int b = 0; b < MB; ++b) acc[q][b] = v4i{0, 0, 0, 0};
 
     // Fragment reads are inline ds_read_b128: the compiler does not know
     // which ring slot an LDS-DMA copy writes, and before any LDS read it can
@@ -547,9 +563,11 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
             if (s + LA < S) f[s + LA] = rd(src, s + LA);
         }
     };
-    auto mma = [&](v4i& c, const v4i (&w)[S]) __attribute__((always_inline)) {
+    auto mma = [&](v4i (&c)[MB], const v4i (&w)[S]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int s = 0; s < S; ++s) c = __builtin_amdgcn_mfma_i32_16x16x64_i8(act[s], w[s], c, 0, 0, 0);
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+            for (int b = 0; b < MB; ++b) c[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(act[b][s], w[s], c[b], 0, 0, 0);
     };
 
     // Lane l of a wave holds tile column l%16, rows 4*(l/16)+v of an MFMA
@@ -562,26 +580,33 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
     };
     // Finishing tile u of chunk tc (SWI: the pair u-1, u): the waves' partial
     // sums go to red, and after a barrier thread (m, nl) = (tid/16, tid%16)
-    // computes output column nl into yv[u] / sv[u].  Called by every wave once
+    // computes output column nl of activation rows m + 16b into yv[u][b] /
+    // sv[u][b].  Called by every wave once
     // its share of the tile is summed, so a chunk's early tiles are reduced
     // while the later tiles' copies stream in; the stores wait for the end of
     // the chunk (8 % faster at M = 4 than one reduction at the chunk's end).
-    float yv[LK_TMAX];
-    int32_t sv[LK_TMAX];
+    float yv[LK_TMAX][MB];
+    int32_t sv[LK_TMAX][MB];
     auto finish_tile = [&](int tc, int u) __attribute__((always_inline)) {
-        constexpr int NQ = SWI ? 2 : 1;  // tiles finished together
+        // red slot of tile u - NQ + 1 + q
+        auto rs = [&](int q) __attribute__((always_inline)) { return RT == LK_TMAX ? u - NQ + 1 + q : q; };
+        if constexpr (RT < LK_TMAX) barrier();  // the previous finish has read red
 #pragma unroll
-        for (int q = 0; q < NQ; ++q) {
-            // The MFMA result passes through a VALU move first: the compiler
-            // puts the wait states an MFMA result needs before a VALU reads
-            // it, but not before an inline-asm store does.
-            v4i a;
+        for (int q = 0; q < NQ; ++q)
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                a[e] = __builtin_amdgcn_update_dpp(0, acc[u - NQ + 1 + q][e], 0xE4, 0xF, 0xF, false);
-            asm volatile("ds_write_b128 %0, %1" : : "v"((lds_u8*)&red[u - NQ + 1 + q][wave][lane * 4]), "v"(a)
-                         : "memory");
-        }
+            for (int b = 0; b < MB; ++b) {
+                // The MFMA result passes through a VALU move first: the
+                // compiler puts the wait states an MFMA result needs before a
+                // VALU reads it, but not before an inline-asm store does.
+                v4i a;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    a[e] = __builtin_amdgcn_update_dpp(0, acc[u - NQ + 1 + q][b][e], 0xE4, 0xF, 0xF, false);
+                asm volatile("ds_write_b128 %0, %1"
+                             :
+                             : "v"((lds_u8*)&red[rs(q)][wave][b * 256 + lane * 4]), "v"(a)
+                             : "memory");
+            }
         wait_lgkm0();
         barrier();
         const int m = tid >> 4, nl = tid & 15;
@@ -589,46 +614,59 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
         const int ri = ((m >> 2) * 16 + nl) * 4 + (m & 3);
         const int t = tc * LK_TMAX + u;  // SWI: the up tile of the pair
         const int r = 16 * (SWI ? t >> 1 : t) + nl;
-        int x[4 * NQ];
-#pragma unroll
-        for (int q = 0; q < NQ; ++q)
-#pragma unroll
-            for (int w = 0; w < 4; ++w) x[4 * q + w] = ld(&red[u - NQ + 1 + q][w][ri]);
-        int xa = ld(esa + m), b0 = ld(esb + r), c0 = ld(ebias + r);
+        int b0 = ld(esb + r), c0 = ld(ebias + r);
         int b1 = SWI ? ld(esb + LK_RMAX + r) : 0, c1 = SWI ? ld(ebias + LK_RMAX + r) : 0;
-        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(xa), "+v"(b0), "+v"(c0), "+v"(b1), "+v"(c1));
+        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(b0), "+v"(c0), "+v"(b1), "+v"(c1));
+        const float sb0 = p.scale_b ? __int_as_float(b0) : p.sb, sb1 = p.scale_b ? __int_as_float(b1) : p.sb;
 #pragma unroll
-        for (int q = 0; q < 4 * NQ; ++q) asm volatile("" : "+v"(x[q]));
-        const float sam = p.scale_a ? __int_as_float(xa) : p.sa;
-        const int32_t s0 = x[0] + x[1] + x[2] + x[3];
-        const float sc0 = sam * (p.scale_b ? __int_as_float(b0) : p.sb);
-        const float y0 = p.bias ? __builtin_fmaf(static_cast<float>(s0), sc0, __int_as_float(c0))
-                                : static_cast<float>(s0) * sc0;
-        if constexpr (SWI) {
-            const int32_t s1 = x[4] + x[5] + x[6] + x[7];
-            const float sc1 = sam * (p.scale_b ? __int_as_float(b1) : p.sb);
-            const float y1 = p.bias ? __builtin_fmaf(static_cast<float>(s1), sc1, __int_as_float(c1))
-                                    : static_cast<float>(s1) * sc1;
-            yv[u] = swiglu_pair(y0, y1);
-        } else {
-            yv[u] = y0;
-            sv[u] = s0;
+        for (int b = 0; b < MB; ++b) {
+            if (b > 0 && m + 16 * b >= M) break;
+            // at most 4 * NQ + 1 reads in flight (lgkmcnt's field is 4 bits)
+            int x[4 * NQ];
+#pragma unroll
+            for (int q = 0; q < NQ; ++q)
+#pragma unroll
+                for (int w = 0; w < 4; ++w) x[4 * q + w] = ld(&red[rs(q)][w][b * 256 + ri]);
+            int xa = ld(esa + m + 16 * b);
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(xa));
+#pragma unroll
+            for (int q = 0; q < 4 * NQ; ++q) asm volatile("" : "+v"(x[q]));
+            const float sam = p.scale_a ? __int_as_float(xa) : p.sa;
+            const int32_t s0 = x[0] + x[1] + x[2] + x[3];
+            const float sc0 = sam * sb0;
+            const float y0 = p.bias ? __builtin_fmaf(static_cast<float>(s0), sc0, __int_as_float(c0))
+                                    : static_cast<float>(s0) * sc0;
+            if constexpr (SWI) {
+                const int32_t s1 = x[4] + x[5] + x[6] + x[7];
+                const float sc1 = sam * sb1;
+                const float y1 = p.bias ? __builtin_fmaf(static_cast<float>(s1), sc1, __int_as_float(c1))
+                                        : static_cast<float>(s1) * sc1;
+                yv[u][b] = swiglu_pair(y0, y1);
+            } else {
+                yv[u][b] = y0;
+                sv[u][b] = s0;
+            }
         }
     };
-    // The chunk's stores: thread (m, nl) holds output column nl of each tile.
+    // The chunk's stores: thread (m, nl) holds output column nl of each tile
+    // for activation rows m + 16b.
     auto store_chunk = [&](int tc, int nt) __attribute__((always_inline)) {
         const int m = tid >> 4, nl = tid & 15;
-        if (m >= M) return;
 #pragma unroll
-        for (int u = SWI ? 1 : 0; u < LK_TMAX; u += SWI ? 2 : 1) {
-            const int t = tc * LK_TMAX + u;
-            const int r = 16 * (SWI ? t >> 1 : t) + nl;
-            if (u < nt && r < nr) store_out<OUT>(p.C, static_cast<size_t>(m) * NO + r0 + r, yv[u], sv[u]);
+        for (int b = 0; b < MB; ++b) {
+            if (m + 16 * b >= M) break;
+#pragma unroll
+            for (int u = SWI ? 1 : 0; u < LK_TMAX; u += SWI ? 2 : 1) {
+                const int t = tc * LK_TMAX + u;
+                const int r = 16 * (SWI ? t >> 1 : t) + nl;
+                if (u < nt && r < nr)
+                    store_out<OUT>(p.C, static_cast<size_t>(mc + m + 16 * b) * NO + r0 + r, yv[u][b], sv[u][b]);
+            }
         }
     };
 
     // Prologue: the first NS items in flight.
-    LkPos pi{0, min(LK_TMAX, T), 0, -1};
+    LkPos pi{0, min(LK_TMAX, T), 0, -MB};
     int issued = 0;
     bool more = true;
 #pragma unroll
@@ -659,13 +697,16 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
     for (int tc = 0; tc < TC; ++tc) {
         const int nt = min(LK_TMAX, T - tc * LK_TMAX);
         for (int j = 0; j < np; ++j) {
-            lds_u8* slot = next_slot();
-            read_all(slot, act);
-            refill(slot);
+#pragma unroll
+            for (int b = 0; b < MB; ++b) {
+                lds_u8* const slot = next_slot();
+                read_all(slot, act[b]);
+                refill(slot);
+            }
 #pragma unroll
             for (int u = 0; u < LK_TMAX; ++u) {
                 if (u < nt) {
-                    slot = next_slot();
+                    lds_u8* const slot = next_slot();
                     v4i w[S];
                     read_all(slot, w);
                     refill(slot);
@@ -676,7 +717,9 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
         }
         store_chunk(tc, nt);
 #pragma unroll
-        for (int q = 0; q < LK_TMAX; ++q) acc[q] = v4i{0, 0, 0, 0};
+        for (int q = 0; q < LK_TMAX; ++q)
+#pragma unroll
+            for (int b = 0; b < MB; ++b) acc[q][b] = v4i{0, 0, 0, 0};
         barrier();  // every read of red for this chunk precedes the next chunk's writes
     }
 }
@@ -700,13 +743,18 @@ hipError_t launch_mfma_skinny(const GemmArgs& p, hipStream_t stream) {
     return hipLaunchKernel(f, grid, dim3(SK_KS * 64), args, 0, stream);
 }
 
-// Workgroups of gemv_lds_kernel: one per CU, fewer when the rows run out
-// (at least 16 rows each), more when a share would exceed LK_RMAX rows.
-int lds_grid(const GemmArgs& p) {
+int cu_count() {
     int dev = 0, cus = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
         cus = 256;
+    return cus;
+}
+
+// Workgroups of gemv_lds_kernel: one per CU, fewer when the rows run out
+// (at least 16 rows each), more when a share would exceed LK_RMAX rows.
+int lds_grid(const GemmArgs& p) {
+    const int cus = cu_count();
     const int no = p.swiglu ? p.N / 2 : p.N;
     int g = min(cus, (no + 15) / 16);
     if ((no + g - 1) / g > LK_RMAX) g = (no + LK_RMAX - 1) / LK_RMAX;
@@ -715,29 +763,37 @@ int lds_grid(const GemmArgs& p) {
 
 template <int PIECE>
 bool lds_fits(const GemmArgs& p) {
-    if (p.K < 4 * PIECE || static_cast<int64_t>(p.M) * p.K > INT32_MAX) return false;
+    // offsets within one workgroup's activation rows (at most 64) and weight rows
+    if (p.K < 4 * PIECE || static_cast<int64_t>(min(p.M, 64)) * p.K > INT32_MAX) return false;
     const int no = p.swiglu ? p.N / 2 : p.N;
     const int g = lds_grid(p);
     const int64_t r = (no + g - 1) / g;
     return r * p.K + PIECE <= INT32_MAX;
 }
 
-template <int PIECE, int NS>
+// grid.y: one workgroup row per 16*MB activation rows; NSW: ring slots of
+// the SwiGLU instantiation (its two-tile reduction buffer takes LDS)
+template <int PIECE, int NS, int MB, int NSW = NS>
 hipError_t launch_lds_t(const GemmArgs& p, hipStream_t stream) {
     GemmArgs a = p;
     void* args[] = {&a};
     const void* f;
     if (p.swiglu) {
-        f = p.out_dtype == FKE_OUT_F32 ? reinterpret_cast<const void*>(&gemv_lds_kernel<FKE_OUT_F32, true, PIECE, NS>)
-                                       : reinterpret_cast<const void*>(&gemv_lds_kernel<FKE_OUT_BF16, true, PIECE, NS>);
+        f = p.out_dtype == FKE_OUT_F32
+            ? reinterpret_cast<const void*>(&gemv_lds_kernel<FKE_OUT_F32, true, PIECE, NSW, MB>)
+            : reinterpret_cast<const void*>(&gemv_lds_kernel<FKE_OUT_BF16, true, PIECE, NSW, MB>);
     } else {
         switch (p.out_dtype) {
-            case FKE_OUT_F32: f = reinterpret_cast<const void*>(&gemv_lds_kernel<FKE_OUT_F32, false, PIECE, NS>); break;
-            case FKE_OUT_BF16: f = reinterpret_cast<const void*>(&gemv_lds_kernel<FKE_OUT_BF16, false, PIECE, NS>); break;
-            default: f = reinterpret_cast<const void*>(&gemv_lds_kernel<FKE_OUT_I32, false, PIECE, NS>); break;
+            case FKE_OUT_F32:
+                f = reinterpret_cast<const void*>(&gemv_lds_kernel<FKE_OUT_F32, false, PIECE, NS, MB>);
+                break;
+            case FKE_OUT_BF16:
+                f = reinterpret_cast<const void*>(&gemv_lds_kernel<FKE_OUT_BF16, false, PIECE, NS, MB>);
+                break;
+            default: f = reinterpret_cast<const void*>(&gemv_lds_kernel<FKE_OUT_I32, false, PIECE, NS, MB>); break;
         }
     }
-    return hipLaunchKernel(f, dim3(lds_grid(p)), dim3(256), args, 0, stream);
+    return hipLaunchKernel(f, dim3(lds_grid(p), (p.M + 16 * MB - 1) / (16 * MB)), dim3(256), args, 0, stream);
 }
 
 template <int MT, bool FULLK, int NB = ROWS_NB>
@@ -794,11 +850,39 @@ hipError_t launch_rows_m(const GemmArgs& p, hipStream_t s) {
 
 }  // namespace
 
+// Batches of 17..FKE_GEMV_MAX_M rows: whether the LDS-streamed kernel beats
+// the MFMA GEMM, from cost models fitted to measurements on MI355X (N of 4096
+// and 14336, K of 4096 and 14336, M of 17..512; each model within ~15 %):
+//  * streamed, per 64-row chunk of A: 5 us + cw us per KiB of the
+//    workgroup's weight share + 0.007 us per KiB of the chunk's activation
+//    rows (L2 hits), with cw = 0.054 (two 16-row blocks) or 0.068 (four): the
+//    weight stream slows as more MFMAs and activation items sit between its
+//    items;
+//  * MFMA GEMM: per round of 256x256 tiles over the CUs, 1.35 us per 128-byte
+//    K stage + 11 us.
+// Past 16 rows the MFMA GEMM has fewer tiles than CUs up to the hundreds of
+// rows (one 256-row tile row), so it takes a whole tile's time for any M.
+bool gemv_i8_batch_pays(const GemmArgs& p) {
+    if (p.M <= 16 || p.M > FKE_GEMV_MAX_M) return p.M <= 16;
+    const double kib = p.K / 1024.0;
+    const int g = lds_grid(p), no = p.swiglu ? p.N / 2 : p.N;
+    const double share = static_cast<double>((no + g - 1) / g) * (p.swiglu ? 2 : 1) * kib;
+    const double cw = p.M > 32 ? 0.068 : 0.054;
+    const double chunk = 5.0 + cw * share + 0.007 * min(p.M, 64) * kib;
+    const double t_lds = ((p.M + 63) / 64) * chunk;
+    const int64_t tiles = static_cast<int64_t>((p.M + 255) / 256) * ((p.N + 255) / 256);
+    const int64_t rounds = (tiles + cu_count() - 1) / cu_count();
+    const double t_mfma = rounds * (p.K / 128.0 * 1.35 + 11.0);
+    return t_lds < t_mfma;
+}
+
 bool gemv_i8_supports(const GemmArgs& p) {
     const uintptr_t a = reinterpret_cast<uintptr_t>(p.A), b = reinterpret_cast<uintptr_t>(p.B);
-    if (!(p.M >= 1 && p.M <= 16 && p.N >= 1 && p.K >= 64 && p.K % 64 == 0 && p.b_layout == FKE_B_NK &&
-          ((a | b) & 15) == 0))
+    if (!(p.M >= 1 && p.M <= FKE_GEMV_MAX_M && p.N >= 1 && p.K >= 64 && p.K % 64 == 0 &&
+          p.b_layout == FKE_B_NK && ((a | b) & 15) == 0))
         return false;
+    // batches past 16 rows: the LDS-streamed kernel only (K >= 2 KiB)
+    if (p.M > 16) return lds_fits<512>(p);
     // SwiGLU pairs: the row kernel up to M = 4, the LDS-streamed kernel from
     // M = 3 when K >= 4 KiB, the skinny MFMA kernel otherwise
     return !p.swiglu || p.M <= 4 || lds_fits<1024>(p) || skinny_offsets_fit(p);
@@ -810,7 +894,9 @@ hipError_t launch_gemv_i8(const GemmArgs& p, hipStream_t s) {
     // N = 14336, K = 4096 for every M in 3..16, against 12.5-18.1 us for the
     // row and skinny kernels; SwiGLU 20.3-20.9 us against 21.5-34.3 us).  At
     // M = 1, 2 the row kernel is faster (9.8 / 11.0 us against 11.6 us).
-    if (p.M >= 3 && lds_fits<1024>(p)) return launch_lds_t<1024, 2>(p, s);
+    if (p.M > 32) return launch_lds_t<512, 4, 4, 3>(p, s);
+    if (p.M > 16) return launch_lds_t<512, 4, 2>(p, s);
+    if (p.M >= 3 && lds_fits<1024>(p)) return launch_lds_t<1024, 2, 1>(p, s);
     if (p.swiglu) {
         if (p.M <= 4) return p.K % 4096 == 0 ? launch_rows_m<true>(p, s) : launch_rows_m<false>(p, s);
         return launch_mfma_skinny(p, s);

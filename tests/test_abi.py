@@ -90,7 +90,10 @@ def test_swiglu_rejects_bad_arguments():
     for M, I, K in [(0, 8, 64), (4, 0, 64), (4, 8, 0), (4, 1 << 30, 64)]:
         assert g(P, P, P, M, I, K, None, None, 1.0, 1.0, None, 0, None) == INVALID
     assert g(P, P, P, 4, 8, 64, None, None, 1.0, 1.0, None, _lib.OUT_I32, None) == INVALID
-    assert L.fke_qgemm_i8_swiglu_on_path(_lib.PATH_GEMV, P, P, P, 17, 64, 4096, None, None, 1.0, 1.0,
+    # past 16 rows the decode family needs K >= 2048 and at most 512 rows
+    assert L.fke_qgemm_i8_swiglu_on_path(_lib.PATH_GEMV, P, P, P, 17, 64, 1024, None, None, 1.0, 1.0,
+                                         None, 0, None) == INVALID
+    assert L.fke_qgemm_i8_swiglu_on_path(_lib.PATH_GEMV, P, P, P, 513, 64, 4096, None, None, 1.0, 1.0,
                                          None, 0, None) == INVALID
     assert L.fke_qgemm_i8_swiglu_on_path(_lib.PATH_MFMA, P, P, P, 64, 64, 100, None, None, 1.0, 1.0,
                                          None, 0, None) == INVALID
@@ -100,7 +103,9 @@ def test_swiglu_rejects_bad_arguments():
     (1, 14336, 4096, _lib.PATH_GEMV),
     (3, 14336, 4096, _lib.PATH_GEMV),
     (16, 14336, 4096, _lib.PATH_GEMV),
-    (17, 14336, 4096, _lib.PATH_MFMA),
+    (17, 14336, 4096, _lib.PATH_GEMV),     # batches: the LDS-streamed kernel while its cost model wins
+    (64, 14336, 4096, _lib.PATH_GEMV),
+    (128, 14336, 4096, _lib.PATH_MFMA),
     (4096, 14336, 4096, _lib.PATH_MFMA),
     (64, 64, 100, _lib.PATH_GENERIC),
     (2, 300000, 4096, _lib.PATH_GEMV),     # row kernel: 64-bit row bases
@@ -164,8 +169,10 @@ def test_dropin_int8_rejects_k_not_multiple_of_4():
 
 def test_path_unavailable_for_shape_is_rejected():
     L = _lib.lib()
-    # GEMV needs M <= 16, K % 64 == 0, B [N,K]; MFMA needs K % 128 == 0
-    assert L.fke_qgemm_i8_on_path(_lib.PATH_GEMV, P, P, P, 17, 64, 4096, None, None, 1.0, 1.0, None,
+    # GEMV needs M <= 512 (K >= 2048 past 16 rows), K % 64 == 0, B [N,K]; MFMA needs K % 128 == 0
+    assert L.fke_qgemm_i8_on_path(_lib.PATH_GEMV, P, P, P, 17, 64, 1024, None, None, 1.0, 1.0, None,
+                                  0, 0, None) == INVALID
+    assert L.fke_qgemm_i8_on_path(_lib.PATH_GEMV, P, P, P, 513, 64, 4096, None, None, 1.0, 1.0, None,
                                   0, 0, None) == INVALID
     assert L.fke_qgemm_i8_on_path(_lib.PATH_GEMV, P, P, P, 4, 64, 4096, None, None, 1.0, 1.0, None,
                                   0, 1, None) == INVALID
@@ -179,7 +186,16 @@ def test_path_unavailable_for_shape_is_rejected():
     (1, 14336, 4096, 0, _lib.PATH_GEMV),
     (4, 14336, 4096, 0, _lib.PATH_GEMV),
     (16, 14336, 4096, 0, _lib.PATH_GEMV),
-    (17, 14336, 4096, 0, _lib.PATH_MFMA),
+    (17, 14336, 4096, 0, _lib.PATH_GEMV),    # batches: LDS-streamed kernel against the MFMA GEMM's cost
+    (128, 14336, 4096, 0, _lib.PATH_GEMV),
+    (192, 14336, 4096, 0, _lib.PATH_MFMA),
+    (192, 4096, 4096, 0, _lib.PATH_GEMV),
+    (384, 4096, 4096, 0, _lib.PATH_MFMA),
+    (384, 4096, 14336, 0, _lib.PATH_GEMV),
+    (512, 4096, 14336, 0, _lib.PATH_MFMA),
+    (17, 14336, 1024, 0, _lib.PATH_MFMA),    # K < 2048: no streamed batch kernel
+    (100, 4096, 2112, 0, _lib.PATH_GEMV),    # K % 128 != 0: no MFMA GEMM, the streamed kernel takes it
+    (17, 14336, 4096, 1, _lib.PATH_MFMA),
     (4096, 11008, 4096, 0, _lib.PATH_MFMA),
     (8192, 8192, 8192, 0, _lib.PATH_MFMA),
     (8192, 8192, 8192, 1, _lib.PATH_MFMA),

@@ -185,6 +185,28 @@ def test_gemv_streamed_shapes(oracle, dev, M, shape):
     assert_same(got, oracle_out(oracle, acc, sa, None, 1.0, 0.007, bias, "f32"), f"streamed M={M} {shape} mixed")
 
 
+MID_SHAPES = [(100, 4096), (777, 5056), (1000, 2048), (4096, 14336), (129, 8192)]
+
+
+@pytest.mark.parametrize("shape", MID_SHAPES)
+@pytest.mark.parametrize("M", [17, 32, 33, 64, 65, 130, 200])
+def test_gemv_streamed_batches(oracle, dev, M, shape):
+    """Batches past 16 rows on the LDS-streamed kernel: 2 or 4 activation
+    blocks per workgroup, and workgroup rows along y past 64 rows (ragged
+    last chunk at 65, 130, 200)."""
+    N, K = shape
+    say("gemv streamed batch", M, N, K)
+    A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 900 + M + N + K, act="normal")
+    acc = oracle.w8a8_acc(A, B, nthreads=NTH)
+    assert_same(gpu_i8(A, B, "nk", "i32", "gemv"), acc, f"batch M={M} {shape} i32")
+    got = gpu_i8(A, B, "nk", "bf16", "gemv", sa, sb, bias=bias)
+    assert_same(got, oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, "bf16"), f"batch M={M} {shape} bf16")
+    got = gpu_i8(A, B, "nk", "f32", "gemv", sa=0.013, sb=0.007)
+    assert_same(got, oracle_out(oracle, acc, None, None, 0.013, 0.007, None, "f32"), f"batch M={M} {shape} f32")
+    got = gpu_i8(A, B, "nk", "f32", "gemv", sa_vec=sa, sb=0.007, bias=bias)
+    assert_same(got, oracle_out(oracle, acc, sa, None, 1.0, 0.007, bias, "f32"), f"batch M={M} {shape} mixed")
+
+
 def test_gemv_streamed_more_workgroups_than_cus(oracle, dev):
     """N = 140000 rows: a share would pass 512 rows per CU, so the launch takes
     more workgroups than CUs; sampled columns against the oracle."""

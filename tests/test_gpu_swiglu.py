@@ -174,6 +174,8 @@ CASES = [
     # (M, I, K, path)
     (1, 200, 4096, "gemv"), (1, 130, 192, "gemv"), (2, 77, 320, "gemv"), (3, 64, 4096, "gemv"),
     (4, 33, 128, "gemv"), (5, 100, 256, "gemv"), (9, 300, 1024, "gemv"), (16, 47, 4096, "gemv"),
+    (17, 130, 2048, "gemv"), (40, 300, 4096, "gemv"), (64, 100, 2048, "gemv"), (100, 77, 4096, "gemv"),
+    (200, 513, 2048, "gemv"),
     (17, 130, 256, "mfma"), (300, 200, 512, "mfma"), (256, 128, 128, "mfma"), (513, 333, 384, "mfma"),
     (33, 40, 100, "generic"), (7, 9, 77, "generic"), (1, 5, 3, "generic"), (70, 100, 256, "generic"),
 ]
@@ -210,7 +212,7 @@ def test_w8a8_swiglu_scalar_scales_and_extension(oracle, dev):
     check_f32(out.cpu().numpy(), oracle.w8a8_swiglu(A, W, sa=0.01, sb=0.002, nthreads=NTH), "scalar scales")
 
 
-@pytest.mark.parametrize("M", [1, 4, 16])
+@pytest.mark.parametrize("M", [1, 4, 16, 64])
 def test_w8a8_swiglu_decode_full(oracle, dev, M):
     """Llama-3-8B MLP gate/up at decode: K = 4096, I = 14336 (W is 112 MiB)."""
     say("w8a8_swiglu decode full", M)
