@@ -1,12 +1,15 @@
-// gemv_i8.hip — W8A8 decode path (M <= 16, B stored [N,K]).
+// gemv_i8.hip — W8A8 decode path (M <= 16, and batches up to
+// FKE_GEMV_MAX_M rows where it beats the MFMA GEMM; B stored [N,K]).
 //
 // Same arithmetic as reference src/quantized_gemm.cu:15-54 (exact int32 dot
 // products, the fused epilogue applied after), re-shaped for an HBM-bound
 // problem: the B panel is streamed once with 128-bit coalesced loads.
 //
 // Four kernels:
-//  * gemv_lds_kernel (3 <= M <= 16, K >= 4096), described at its definition:
-//    the weight panel streamed through LDS by one workgroup per CU.
+//  * gemv_lds_kernel (3 <= M <= 16 with K >= 4096; 17 <= M <= 512 with
+//    K >= 2048), described at its definition: the weight panel streamed
+//    through LDS by one workgroup per CU, each weight fragment multiplied
+//    with up to four 16-row activation blocks.
 //  * gemv_rows_kernel (M <= 4): NB B rows per wave (one at M = 1, two for
 //    M = 2..4 and for SwiGLU's gate/up pairs) over the full K.  Lane l reads
 //    16-byte chunks l, l+64, l+128, l+192 of each 256-chunk block (one wave

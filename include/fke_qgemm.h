@@ -49,7 +49,7 @@ enum fke_in_dtype {
 /* Kernel family used by a call (for tests and benchmarks). */
 enum fke_path {
     FKE_PATH_AUTO = 0,    /* dispatcher's choice                                */
-    FKE_PATH_GEMV = 1,    /* M<=16 split-K wavefront-reduction GEMV (INT8, NK)  */
+    FKE_PATH_GEMV = 1,    /* decode family, M<=512 (INT8, NK): weight streamed  */
     FKE_PATH_MFMA = 2,    /* LDS-staged MFMA GEMM (INT8 i32 / FP8 f32 acc)      */
     FKE_PATH_GENERIC = 3  /* any-shape tiled fallback (exact reference order)   */
 };
