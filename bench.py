@@ -9,7 +9,7 @@ the same run and reported under "decode_gemv", and the M=16 decode (the other
 end of the decode configs) under "decode_gemv_m16".  Inputs are random (torch RNG
 on the device), never zero-filled.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--extra | --fp8 --swiglu --half] [--vendor] [--data-sweep] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--extra | --fp8 --swiglu --half --batch --shards] [--vendor] [--data-sweep] [--no-cpu]
 """
 import argparse
 import json
@@ -54,10 +54,12 @@ def parse():
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--gemv-buffers", type=int, default=8)
     ap.add_argument("--gemv-launches", type=int, default=400)
-    ap.add_argument("--extra", action="store_true", help="also time configs 2 and 4 and GEMV M=4,16")
+    ap.add_argument("--extra", action="store_true", help="also time configs 2 and 4, decode M=4 and batched decode M=32,64,128")
     ap.add_argument("--swiglu", action="store_true", help="also time the SwiGLU configs (part of --extra)")
     ap.add_argument("--half", action="store_true", help="also time the fp16/bf16 GEMM (part of --extra)")
     ap.add_argument("--fp8", action="store_true", help="also time the FP8 e4m3 GEMM 8192^3 (part of --extra)")
+    ap.add_argument("--batch", action="store_true",
+                    help="also time batched decode M=32,64,128 on the decode weights (part of --extra)")
     ap.add_argument("--shards", action="store_true",
                     help="also time the per-GPU shards of 8-way tensor parallelism (part of --extra)")
     ap.add_argument("--data-sweep", action="store_true",
@@ -165,8 +167,10 @@ def main():
         del src, dst
     if args.extra:
         line["extra"] = extra_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args)
-    elif args.swiglu or args.half or args.fp8 or args.shards:
+    elif args.swiglu or args.half or args.fp8 or args.shards or args.batch:
         line["extra"] = {}
+        if args.batch:
+            line["extra"].update(batch_configs(torch, L, _lib, dev, gen, args))
         if args.shards:
             line["extra"].update(shard_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args))
         if args.fp8:
@@ -291,6 +295,14 @@ def shard_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
     return res
 
 
+def batch_configs(torch, L, _lib, dev, gen, args):
+    """Batched decode on the decode weights (N = 14336, K = 4096): 32, 64 and 128 rows, which
+    the dispatcher gives to the LDS-streamed kernel with 2 / 4 activation blocks (128 rows as
+    two 64-row workgroup rows)."""
+    return {f"gemv_M{m}": gemv_bench(torch, L, _lib, dev, gen, m, args.gemv_buffers, args.gemv_launches)
+            for m in (32, 64, 128)}
+
+
 def extra_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
     res = {}
     # prefill 4096 x 11008 x 4096, bf16 out
@@ -332,8 +344,8 @@ def extra_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
     del A8, B8, C
     res.update(half_configs(torch, L, _lib, dev, gen, timed, args))
     res.update(shard_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args))
-    for m in (4,):
-        res[f"gemv_M{m}"] = gemv_bench(torch, L, _lib, dev, gen, m, args.gemv_buffers, args.gemv_launches)
+    res["gemv_M4"] = gemv_bench(torch, L, _lib, dev, gen, 4, args.gemv_buffers, args.gemv_launches)
+    res.update(batch_configs(torch, L, _lib, dev, gen, args))
     # per-token INT8 quantiser in front of the W8A8 GEMM: bf16 activations of C3 (4096 x 4096),
     # 12 rotating inputs (384 MiB, more than the MALL), timed from a HIP graph like the GEMV
     M, K, nx = 4096, 4096, 12
