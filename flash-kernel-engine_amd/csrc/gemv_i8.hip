@@ -461,6 +461,10 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
     const int TC = (T + LK_TMAX - 1) / LK_TMAX;
     const int P = (K + PIECE - 1) / PIECE;  // >= 4
     const int np = (P - 1 - wave) / 4 + 1;  // pieces of this wave, >= 1
+    // The wave walks its pieces starting at a different one in each
+    // workgroup, so the CUs' concurrent reads spread over the whole K span
+    // of their rows rather than all reading the same byte range at once.
+    const int jo = static_cast<int>(blockIdx.x) % np;
 
     // Epilogue operands (scale_b and bias of the workgroup's rows, scale_a of
     // the activation rows) go straight to LDS with dword LDS-DMA copies issued
@@ -500,7 +504,8 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
     const int crow = lane / (64 / RPW), cslot = lane % (64 / RPW);
     auto z = [](int i) __attribute__((always_inline)) { return (i / RPW) & (S - 1); };
     auto issue = [&](const LkPos& it, lds_u8* dst) __attribute__((always_inline)) {
-        const int pc = (wave + 4 * it.j) * PIECE;  // first k byte of the piece
+        const int jr = it.j + jo < np ? it.j + jo : it.j + jo - np;
+        const int pc = (wave + 4 * jr) * PIECE;  // first k byte of the piece
         if (it.u < 0) {
             const int a0 = 16 * (it.u + MB);  // first activation row of the item
 #pragma unroll
@@ -746,6 +751,8 @@ hipError_t launch_mfma_skinny(const GemmArgs& p, hipStream_t stream) {
     return hipLaunchKernel(f, grid, dim3(SK_KS * 64), args, 0, stream);
 }
 
+bool pieces_even(int K, int piece) { return ((K + piece - 1) / piece) % 4 == 0; }
+
 int cu_count() {
     int dev = 0, cus = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
@@ -897,8 +904,16 @@ hipError_t launch_gemv_i8(const GemmArgs& p, hipStream_t s) {
     // N = 14336, K = 4096 for every M in 3..16, against 12.5-18.1 us for the
     // row and skinny kernels; SwiGLU 20.3-20.9 us against 21.5-34.3 us).  At
     // M = 1, 2 the row kernel is faster (9.8 / 11.0 us against 11.6 us).
+    // Two activation blocks: 1 KiB pieces unless that leaves the four waves
+    // uneven piece counts and 512 bytes does not (the workgroup waits for its
+    // slowest wave: at K = 14336, 1 KiB pieces go 4/4/3/3 and took 8 % longer
+    // at M = 17..32; at K = 4096 they are 4-6 % faster than 512).  One block
+    // keeps 1 KiB pieces (512 at K = 14336 measured within 3 % either way).
     if (p.M > 32) return launch_lds_t<512, 4, 4, 3>(p, s);
-    if (p.M > 16) return launch_lds_t<512, 4, 2>(p, s);
+    if (p.M > 16) {
+        const bool big = lds_fits<1024>(p) && (pieces_even(p.K, 1024) || !pieces_even(p.K, 512));
+        return big ? launch_lds_t<1024, 2, 2>(p, s) : launch_lds_t<512, 4, 2>(p, s);
+    }
     if (p.M >= 3 && lds_fits<1024>(p)) return launch_lds_t<1024, 2, 1>(p, s);
     if (p.swiglu) {
         if (p.M <= 4) return p.K % 4096 == 0 ? launch_rows_m<true>(p, s) : launch_rows_m<false>(p, s);
