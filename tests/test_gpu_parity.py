@@ -207,6 +207,18 @@ def test_gemv_streamed_batches(oracle, dev, M, shape):
     assert_same(got, oracle_out(oracle, acc, sa, None, 1.0, 0.007, bias, "f32"), f"batch M={M} {shape} mixed")
 
 
+@pytest.mark.parametrize("M,N,K", [(512, 300, 2048), (449, 1000, 4096), (257, 70, 14336)])
+def test_gemv_streamed_batch_largest(oracle, dev, M, N, K):
+    """The largest batches the decode family takes (up to 512 rows: 8 workgroup
+    rows of 64 activation rows), ragged last chunks, 512-byte and 1 KiB pieces."""
+    say("gemv streamed largest batch", M, N, K)
+    A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 950 + M + N + K, act="normal")
+    acc = oracle.w8a8_acc(A, B, nthreads=NTH)
+    assert_same(gpu_i8(A, B, "nk", "i32", "gemv"), acc, f"batch M={M} i32")
+    got = gpu_i8(A, B, "nk", "bf16", "gemv", sa, sb, bias=bias)
+    assert_same(got, oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, "bf16"), f"batch M={M} bf16")
+
+
 def test_gemv_streamed_more_workgroups_than_cus(oracle, dev):
     """N = 140000 rows: a share would pass 512 rows per CU, so the launch takes
     more workgroups than CUs; sampled columns against the oracle."""
