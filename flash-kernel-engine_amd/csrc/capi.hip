@@ -104,6 +104,9 @@ int pick_i8(const GemmArgs& p) {
 }
 
 int pick_f8(const GemmArgs& p) {
+    // decode and small batches (B [N,K]): the streamed kernel, by the same cost model as INT8
+    if (fke::gemv_f8_supports(p) && (fke::gemv_i8_batch_pays(p) || !fke::mfma_supports(p, fke::ELEM_F8)))
+        return FKE_PATH_GEMV;
     if (fke::mfma_supports(p, fke::ELEM_F8)) return FKE_PATH_MFMA;
     return FKE_PATH_GENERIC;
 }
@@ -152,6 +155,9 @@ int run_f8(int path, const GemmArgs& p, void* stream) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (path == FKE_PATH_AUTO) path = pick_f8(p);
     switch (path) {
+        case FKE_PATH_GEMV:
+            if (!fke::gemv_f8_supports(p)) return hipErrorInvalidValue;
+            return fke::launch_gemv_f8(p, s);
         case FKE_PATH_MFMA:
             if (!fke::mfma_supports(p, fke::ELEM_F8)) return hipErrorInvalidValue;
             return fke::launch_mfma(p, fke::ELEM_F8, s);

@@ -48,6 +48,8 @@ constexpr int FKE_GEMV_MAX_M = 512;
 // Shape/alignment predicates of the fast families (host side).
 bool gemv_i8_supports(const GemmArgs& p);
 bool gemv_i8_batch_pays(const GemmArgs& p);  // M > 16: the decode family beats the MFMA GEMM
+bool gemv_f8_supports(const GemmArgs& p);
+hipError_t launch_gemv_f8(const GemmArgs& p, hipStream_t stream);
 bool mfma_supports(const GemmArgs& p, int elem);
 
 // ---------------------------------------------------------------------------

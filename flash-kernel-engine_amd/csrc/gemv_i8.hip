@@ -390,6 +390,15 @@ __global__ __launch_bounds__(SK_KS * 64) void gemv_mfma_kernel(GemmArgs p) {
 // activations.
 // SWI: B is [gate; up]; tile t of a chunk is gate tile t/2 (t even) or the
 // matching up tile (t odd), and each output is swiglu_pair of the two.
+// EL = ELEM_F8 (E4M3 codes, fp32 sums): v_mfma_scale_f32_16x16x128_f8f6f4
+// takes 32 k bytes per lane, so each MFMA pairs two of the 16-byte reads
+// (chunks 2t and 2t+1 of the lane's step sequence; both operands pair the
+// same chunks, so the k permutation argument holds).  Codes 0x7F / 0xFF are
+// NaN to the MFMA but 0.0 to the reference (src/quantized_gemm.cu:90-91):
+// every operand word is cleared of them on the VALU before its MFMA, which
+// also keeps the weight bytes past K in the last piece (the next row's
+// codes) finite against their zero activations.  The four waves' partial
+// sums meet in the fixed order w = 0..3.
 constexpr int LK_TMAX = 4;    // tiles accumulated between two reductions
 constexpr int LK_RMAX = 512;  // weight rows (of each half) of one workgroup
 
@@ -426,7 +435,10 @@ __device__ __forceinline__ void wait_lgkm_tied(int n, v4i& r) {
     }
 }
 
-template <int OUT, bool SWI, int PIECE, int NS, int MB>
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+
+template <int OUT, bool SWI, int PIECE, int NS, int MB, int EL = ELEM_I8>
 __global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
     constexpr int H = SWI ? 2 : 1;
     constexpr int RPW = 1024 / PIECE;  // rows per 1 KiB copy instruction
@@ -437,6 +449,10 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
     static_assert(DI == 8 || DI == 16, "vmcnt steps of wait_vm_n are 8 copies");
     static_assert((NS - 1) * DI <= 32, "wait_vm_n covers up to 32 copies");
     static_assert(MB >= 1 && MB <= 4, "up to 64 activation rows per workgroup (esa, one dword copy per lane)");
+    static_assert(EL == ELEM_I8 || (EL == ELEM_F8 && !SWI && OUT != FKE_OUT_I32 && S % 2 == 0),
+                  "FP8: plain GEMM, fp32 or bf16 out, pairs of 16-byte reads");
+    constexpr bool F8 = EL == ELEM_F8;
+    using AccV = typename std::conditional<F8, v4f, v4i>::type;
     // Partial sums of the tiles being finished: all tiles of a chunk for one
     // activation block (no barrier between two finishes), or with more blocks
     // only the tile (SWI: pair) at hand, which leaves the LDS to a deeper ring.
@@ -543,11 +559,11 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
     const int li = lane & 15;
     const uint32_t lb = static_cast<uint32_t>(li * PIECE + (lane >> 4) * (PIECE / 4) + z(li) * 16);
     v4i act[MB][S];
-    v4i acc[LK_TMAX][MB];
+    AccV acc[LK_TMAX][MB];
 #pragma unroll
     for (int q = 0; q < LK_TMAX; ++q)
 #pragma unroll
-        for (int b = 0; b < MB; ++b) acc[q][b] = v4i{0, 0, 0, 0};
+        for (int b = 0; b < MB; ++b) acc[q][b] = AccV{0, 0, 0, 0};
 
     // Fragment reads are inline ds_read_b128: the compiler does not know
     // which ring slot an LDS-DMA copy writes, and before any LDS read it can
@@ -571,11 +587,29 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
             if (s + LA < S) f[s + LA] = rd(src, s + LA);
         }
     };
-    auto mma = [&](v4i (&c)[MB], const v4i (&w)[S]) __attribute__((always_inline)) {
+    auto san = [](v4i x) __attribute__((always_inline)) {
 #pragma unroll
-        for (int s = 0; s < S; ++s)
+        for (int e = 0; e < 4; ++e) x[e] = static_cast<int>(e4m3_sanitize(static_cast<uint32_t>(x[e])));
+        return x;
+    };
+    auto mma = [&](AccV (&c)[MB], const v4i (&w)[S]) __attribute__((always_inline)) {
+        if constexpr (F8) {
 #pragma unroll
-            for (int b = 0; b < MB; ++b) c[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(act[b][s], w[s], c[b], 0, 0, 0);
+            for (int t = 0; t < S / 2; ++t) {
+                const v8i wv = __builtin_shufflevector(san(w[2 * t]), san(w[2 * t + 1]), 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+                for (int b = 0; b < MB; ++b)
+                    c[b] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                        __builtin_shufflevector(act[b][2 * t], act[b][2 * t + 1], 0, 1, 2, 3, 4, 5, 6, 7), wv, c[b],
+                        0, 0, 0, 0, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int s = 0; s < S; ++s)
+#pragma unroll
+                for (int b = 0; b < MB; ++b)
+                    c[b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(act[b][s], w[s], c[b], 0, 0, 0);
+        }
     };
 
     // Lane l of a wave holds tile column l%16, rows 4*(l/16)+v of an MFMA
@@ -606,10 +640,12 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
                 // The MFMA result passes through a VALU move first: the
                 // compiler puts the wait states an MFMA result needs before a
                 // VALU reads it, but not before an inline-asm store does.
+                // (The whole accumulator is reinterpreted as integers first:
+                // a bit cast of one vector element reads element 0.)
+                const v4i ai = __builtin_bit_cast(v4i, acc[u - NQ + 1 + q][b]);
                 v4i a;
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    a[e] = __builtin_amdgcn_update_dpp(0, acc[u - NQ + 1 + q][b][e], 0xE4, 0xF, 0xF, false);
+                for (int e = 0; e < 4; ++e) a[e] = __builtin_amdgcn_update_dpp(0, ai[e], 0xE4, 0xF, 0xF, false);
                 asm volatile("ds_write_b128 %0, %1"
                              :
                              : "v"((lds_u8*)&red[rs(q)][wave][b * 256 + lane * 4]), "v"(a)
@@ -640,10 +676,16 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
 #pragma unroll
             for (int q = 0; q < 4 * NQ; ++q) asm volatile("" : "+v"(x[q]));
             const float sam = p.scale_a ? __int_as_float(xa) : p.sa;
-            const int32_t s0 = x[0] + x[1] + x[2] + x[3];
+            int32_t s0 = 0;
+            float v0;
+            if constexpr (F8) {
+                v0 = ((__int_as_float(x[0]) + __int_as_float(x[1])) + __int_as_float(x[2])) + __int_as_float(x[3]);
+            } else {
+                s0 = x[0] + x[1] + x[2] + x[3];
+                v0 = static_cast<float>(s0);
+            }
             const float sc0 = sam * sb0;
-            const float y0 = p.bias ? __builtin_fmaf(static_cast<float>(s0), sc0, __int_as_float(c0))
-                                    : static_cast<float>(s0) * sc0;
+            const float y0 = p.bias ? __builtin_fmaf(v0, sc0, __int_as_float(c0)) : v0 * sc0;
             if constexpr (SWI) {
                 const int32_t s1 = x[4] + x[5] + x[6] + x[7];
                 const float sc1 = sam * sb1;
@@ -710,6 +752,9 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
                 lds_u8* const slot = next_slot();
                 read_all(slot, act[b]);
                 refill(slot);
+                if constexpr (F8)
+#pragma unroll
+                    for (int q = 0; q < S; ++q) act[b][q] = san(act[b][q]);
             }
 #pragma unroll
             for (int u = 0; u < LK_TMAX; ++u) {
@@ -727,7 +772,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
 #pragma unroll
         for (int q = 0; q < LK_TMAX; ++q)
 #pragma unroll
-            for (int b = 0; b < MB; ++b) acc[q][b] = v4i{0, 0, 0, 0};
+            for (int b = 0; b < MB; ++b) acc[q][b] = AccV{0, 0, 0, 0};
         barrier();  // every read of red for this chunk precedes the next chunk's writes
     }
 }
@@ -803,6 +848,16 @@ hipError_t launch_lds_t(const GemmArgs& p, hipStream_t stream) {
             default: f = reinterpret_cast<const void*>(&gemv_lds_kernel<FKE_OUT_I32, false, PIECE, NS, MB>); break;
         }
     }
+    return hipLaunchKernel(f, dim3(lds_grid(p), (p.M + 16 * MB - 1) / (16 * MB)), dim3(256), args, 0, stream);
+}
+
+template <int PIECE, int NS, int MB>
+hipError_t launch_lds_f8(const GemmArgs& p, hipStream_t stream) {
+    GemmArgs a = p;
+    void* args[] = {&a};
+    const void* f = p.out_dtype == FKE_OUT_F32
+                        ? reinterpret_cast<const void*>(&gemv_lds_kernel<FKE_OUT_F32, false, PIECE, NS, MB, ELEM_F8>)
+                        : reinterpret_cast<const void*>(&gemv_lds_kernel<FKE_OUT_BF16, false, PIECE, NS, MB, ELEM_F8>);
     return hipLaunchKernel(f, dim3(lds_grid(p), (p.M + 16 * MB - 1) / (16 * MB)), dim3(256), args, 0, stream);
 }
 
@@ -923,6 +978,21 @@ hipError_t launch_gemv_i8(const GemmArgs& p, hipStream_t s) {
     if (skinny_offsets_fit(p)) return launch_mfma_skinny(p, s);
     if (p.M <= 8) return launch_t<8, 8>(p, s);
     return launch_t<16, 4>(p, s);
+}
+
+// FP8 decode and batches: the LDS-streamed kernel on E4M3 codes (B [N,K]).
+bool gemv_f8_supports(const GemmArgs& p) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p.A), b = reinterpret_cast<uintptr_t>(p.B);
+    return p.M >= 1 && p.M <= FKE_GEMV_MAX_M && p.N >= 1 && p.K % 64 == 0 && p.b_layout == FKE_B_NK &&
+           !p.swiglu && (p.out_dtype == FKE_OUT_F32 || p.out_dtype == FKE_OUT_BF16) && ((a | b) & 15) == 0 &&
+           lds_fits<512>(p);
+}
+
+hipError_t launch_gemv_f8(const GemmArgs& p, hipStream_t s) {
+    const bool big = lds_fits<1024>(p) && (pieces_even(p.K, 1024) || !pieces_even(p.K, 512));
+    if (p.M > 32) return launch_lds_f8<512, 4, 4>(p, s);
+    if (p.M > 16) return big ? launch_lds_f8<1024, 2, 2>(p, s) : launch_lds_f8<512, 4, 2>(p, s);
+    return lds_fits<1024>(p) ? launch_lds_f8<1024, 2, 1>(p, s) : launch_lds_f8<512, 4, 1>(p, s);
 }
 
 }  // namespace fke

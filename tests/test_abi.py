@@ -178,7 +178,12 @@ def test_path_unavailable_for_shape_is_rejected():
                                   0, 1, None) == INVALID
     assert L.fke_qgemm_i8_on_path(_lib.PATH_MFMA, P, P, P, 64, 64, 100, None, None, 1.0, 1.0, None,
                                   0, 0, None) == INVALID
-    assert L.fke_qgemm_f8_on_path(_lib.PATH_GEMV, P, P, P, 4, 64, 4096, 1.0, 1.0, None, 0, 0,
+    # FP8 decode family: B [N,K], fp32 / bf16 out, K >= 2048
+    assert L.fke_qgemm_f8_on_path(_lib.PATH_GEMV, P, P, P, 4, 64, 4096, 1.0, 1.0, None, 0, 1,
+                                  None) == INVALID
+    assert L.fke_qgemm_f8_on_path(_lib.PATH_GEMV, P, P, P, 4, 64, 1024, 1.0, 1.0, None, 0, 0,
+                                  None) == INVALID
+    assert L.fke_qgemm_f8_on_path(_lib.PATH_GEMV, P, P, P, 4, 64, 4096, 1.0, 1.0, None, _lib.OUT_I32, 0,
                                   None) == INVALID
 
 
@@ -215,6 +220,19 @@ def test_dispatch_unaligned_pointer_falls_back():
     assert L.fke_select_path_f8(P + 2, P, P, 256, 256, 256, 0, 1) == _lib.PATH_GENERIC
     assert L.fke_select_path_f8(P, P, P, 8192, 8192, 8192, 1, 1) == _lib.PATH_MFMA
     assert L.fke_select_path_i8(None, P, P, 8, 8, 8, 0, 0) == -1
+
+
+@pytest.mark.parametrize("M,N,K,layout,expect", [
+    (1, 14336, 4096, 0, _lib.PATH_GEMV),      # FP8 decode: the LDS-streamed kernel
+    (16, 14336, 4096, 0, _lib.PATH_GEMV),
+    (64, 14336, 4096, 0, _lib.PATH_GEMV),
+    (1, 14336, 4096, 1, _lib.PATH_MFMA),      # B [K,N] (the reference layout): no streamed kernel
+    (8192, 8192, 8192, 0, _lib.PATH_MFMA),
+    (4, 14336, 1024, 0, _lib.PATH_MFMA),      # K < 2048
+    (4, 300, 2112, 0, _lib.PATH_GEMV),        # K % 128 != 0: no MFMA GEMM
+])
+def test_dispatch_f8(M, N, K, layout, expect):
+    assert _lib.lib().fke_select_path_f8(P, P, P, M, N, K, 0, layout) == expect
 
 
 def test_dropin_header_program_host_checks():

@@ -459,6 +459,26 @@ def test_fp8_mfma_tolerance(oracle, dev, layout, out, nan_codes):
     assert mx <= 2e-2 and fro <= 2e-2, (mx, fro)
 
 
+@pytest.mark.parametrize("M,N,K", [(1, 300, 4096), (3, 1000, 2048), (16, 777, 5056), (16, 4096, 14336),
+                                   (17, 129, 4096), (40, 500, 2048), (64, 1000, 14336), (130, 300, 8192)])
+@pytest.mark.parametrize("nan_codes", [False, True])
+def test_fp8_streamed_tolerance(oracle, dev, M, N, K, nan_codes):
+    """FP8 decode and batches (B [N,K]) on the LDS-streamed kernel: fp32 sums in
+    another order than the reference's sequential loop, so the FP8 bar (2e-2
+    relative); codes 0x7F / 0xFF count as 0.0 like the reference."""
+    say("fp8 streamed", M, N, K, nan_codes)
+    A, B, sa, sb = f8_inputs(oracle, M, N, K, 800 + M + K, "nk", with_nan_codes=nan_codes)
+    bias = oracle.gen_f32_normal((N,), 801 + N, 0.0, 0.02)
+    ref = oracle.f8_gemm(A, B, sa, sb, bias=bias, b_layout=oracle.B_NK, nthreads=NTH)
+    for out in ("f32", "bf16"):
+        got = gpu_f8(A, B, sa, sb, "nk", out, "gemv", bias=bias)
+        if out == "bf16":
+            got = oracle.bf16_to_f32(got)
+        mx, fro = rel_errors(got, ref)
+        assert np.isfinite(got).all(), f"fp8 streamed {out}: non-finite output"
+        assert mx <= 2e-2 and fro <= 2e-2, (out, mx, fro)
+
+
 def test_c5_fp8_full(oracle, dev):
     """FP8 square: 8192^3 e4m3 (per-tensor amax/448 scales, B [K,N]), bf16 out,
     against the reference's sequential fp32 sum on 64 sampled rows."""
