@@ -395,7 +395,7 @@ def data_sweep(torch, L, _lib, dev, gen, timed, args):
 
 
 def fp8_configs(torch, L, _lib, dev, gen, timed, args):
-    """FP8 e4m3 8192^3, B [K,N] (reference layout) and [N,K], bf16 out."""
+    """FP8 e4m3 8192^3, B [K,N] (reference layout) and [N,K], bf16 out; FP8 decode M=1,16."""
     res = {}
     sh = torch.cuda.current_stream(dev).cuda_stream
     M = N = K = 8192
@@ -411,6 +411,33 @@ def fp8_configs(torch, L, _lib, dev, gen, timed, args):
         res[f"fp8_8192cubed_bf16_B{name}"] = {"ms": round(ms, 4), "TFLOPS": round(t, 1),
                                               "frac": round(t / PEAK_FP8_TFLOPS, 4)}
     del A8, B8, C
+    # FP8 decode on the decode weights (N = 14336, K = 4096, B [N,K], bf16 out + bias): the
+    # LDS-streamed kernel, 8 rotating weights, HIP-graph timed like the INT8 decode lines
+    N, K, nbuf = 14336, 4096, args.gemv_buffers
+    Bs = []
+    for _ in range(nbuf):
+        b = torch.randint(0, 256, (N, K), dtype=torch.uint8, device=dev, generator=gen)
+        b[(b & 0x7F) == 0x7F] = 0
+        Bs.append(b)
+    bias = torch.randn(N, device=dev, generator=gen) * 0.02
+    for M in (1, 16):
+        A8 = torch.randint(0, 256, (M, K), dtype=torch.uint8, device=dev, generator=gen)
+        A8[(A8 & 0x7F) == 0x7F] = 0
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+
+        def launch(i, st):
+            r = L.fke_qgemm_f8(A8.data_ptr(), Bs[i % nbuf].data_ptr(), out.data_ptr(), M, N, K, 0.01, 0.01,
+                               bias.data_ptr(), _lib.OUT_BF16, _lib.B_NK, st)
+            if r:
+                raise RuntimeError(f"fp8 decode failed: {_lib.status_string(r)}")
+
+        us = graph_us(torch, dev, launch, args.gemv_launches, 2 * nbuf)
+        nbytes = M * K + N * K + 4 * N + 2 * M * N
+        gbs = nbytes / (us * 1e-6) / 1e9
+        res[f"fp8_decode_M{M}_14336x4096_bf16"] = {"us": round(us, 3), "GB/s": round(gbs, 1),
+                                                   "frac": round(gbs / PEAK_HBM_GBS, 4), "bytes": nbytes,
+                                                   "kernel": "gemv_lds_kernel (FP8)"}
+    del Bs
     return res
 
 
