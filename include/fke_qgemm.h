@@ -104,9 +104,10 @@ int fke_qgemm_i8_on_path(int path, const int8_t* A, const int8_t* B, void* C,
  * src/quantized_gemm.cu:99-139): sum = sum_k dec(A[m,k])*dec(B(k,n)) in fp32,
  * y = bias ? fmaf(sum, fp32(sa*sb), bias[n]) : sum * fp32(sa*sb);
  * C = y (F32) | bf16_rne(y) (BF16).  Codes 0x7F/0xFF decode to 0.0 as in the
- * reference.  The MFMA family sums in a different order than the reference's
- * sequential loop (each product is exact; only fp32 rounding of the sum
- * differs); the GENERIC family keeps the reference's sequential k order.
+ * reference.  The MFMA family and the decode family (B [N,K], M <= 512, K >= 2048,
+ * picked for decode and small batches) sum in a different order than the
+ * reference's sequential loop (each product is exact; only fp32 rounding of the
+ * sum differs); the GENERIC family keeps the reference's sequential k order.
  */
 int fke_qgemm_f8(const uint8_t* A, const uint8_t* B, void* C, int M, int N, int K,
                  float sa, float sb, const float* bias, int out_dtype, int b_layout,
@@ -219,7 +220,8 @@ int fke_w8a8_swiglu_linear(const void* X, int in_dtype, const int8_t* W, void* H
                            int out_dtype, void* workspace, size_t workspace_bytes, void* stream);
 
 /* The family fke_qgemm_i8 / fke_qgemm_f8 would pick (enum fke_path), or -1
- * for arguments they would reject.  Pure host logic; needs no GPU. */
+ * for arguments they would reject.  Host logic only: launches nothing; the
+ * batch cost model reads the current device's CU count (256 without a device). */
 int fke_select_path_i8(const void* A, const void* B, const void* C, int M, int N, int K,
                        int out_dtype, int b_layout);
 int fke_select_path_f8(const void* A, const void* B, const void* C, int M, int N, int K,
