@@ -394,11 +394,15 @@ __global__ __launch_bounds__(SK_KS * 64) void gemv_mfma_kernel(GemmArgs p) {
 // takes 32 k bytes per lane, so each MFMA pairs two of the 16-byte reads
 // (chunks 2t and 2t+1 of the lane's step sequence; both operands pair the
 // same chunks, so the k permutation argument holds).  Codes 0x7F / 0xFF are
-// NaN to the MFMA but 0.0 to the reference (src/quantized_gemm.cu:90-91):
-// every operand word is cleared of them on the VALU before its MFMA, which
-// also keeps the weight bytes past K in the last piece (the next row's
-// codes) finite against their zero activations.  The four waves' partial
-// sums meet in the fixed order w = 0..3.
+// NaN to the MFMA but 0.0 to the reference (src/quantized_gemm.cu:90-91).
+// The stream runs on the raw codes: E4M3 has no infinity, every product of
+// finite codes is finite and no sum of them can overflow fp32, so a NaN sum
+// proves a NaN code in its activation row or weight row, and that output
+// alone is recomputed from global memory by its finishing thread in the
+// reference's sequential k order (bit-exact with the reference there).
+// Weight bytes past K in the last piece read as zero (they would be the
+// next row's codes).  The four waves' partial sums meet in the fixed order
+// w = 0..3.
 constexpr int LK_TMAX = 4;    // tiles accumulated between two reductions
 constexpr int LK_RMAX = 512;  // weight rows (of each half) of one workgroup
 
@@ -538,8 +542,9 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
 #pragma unroll
             for (int d = 0; d < DI; ++d) {
                 const int i = d * RPW + crow, r = row0 + i;
-                const uint32_t off =
-                    r < nr ? static_cast<uint32_t>(r * K + pc + ((cslot ^ z(i)) << 4)) : 0x80000000u;
+                const int k = pc + ((cslot ^ z(i)) << 4);
+                // FP8: bytes past K read as zero (the next row's codes may be NaN codes)
+                const uint32_t off = r < nr && (!F8 || k < K) ? static_cast<uint32_t>(r * K + k) : 0x80000000u;
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, dst + d * 1024, 16, static_cast<int>(off), 0, 0, 2);
             }
         }
@@ -587,16 +592,11 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
             if (s + LA < S) f[s + LA] = rd(src, s + LA);
         }
     };
-    auto san = [](v4i x) __attribute__((always_inline)) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) x[e] = static_cast<int>(e4m3_sanitize(static_cast<uint32_t>(x[e])));
-        return x;
-    };
     auto mma = [&](AccV (&c)[MB], const v4i (&w)[S]) __attribute__((always_inline)) {
         if constexpr (F8) {
 #pragma unroll
             for (int t = 0; t < S / 2; ++t) {
-                const v8i wv = __builtin_shufflevector(san(w[2 * t]), san(w[2 * t + 1]), 0, 1, 2, 3, 4, 5, 6, 7);
+                const v8i wv = __builtin_shufflevector(w[2 * t], w[2 * t + 1], 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
                 for (int b = 0; b < MB; ++b)
                     c[b] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
@@ -680,6 +680,16 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
             float v0;
             if constexpr (F8) {
                 v0 = ((__int_as_float(x[0]) + __int_as_float(x[1])) + __int_as_float(x[2])) + __int_as_float(x[3]);
+                // A NaN code took part: the reference's sequential sum, 0x7F / 0xFF as 0.  Only for
+                // rows of this workgroup's share (padding rows of the last tile are never stored,
+                // and their weight row would lie past the share).
+                if (v0 != v0 && r < nr) {
+                    const uint8_t* ar = static_cast<const uint8_t*>(p.A) + static_cast<size_t>(mc + m + 16 * b) * K;
+                    const uint8_t* br = static_cast<const uint8_t*>(p.B) + static_cast<size_t>(r0 + r) * K;
+                    float acc1 = 0.0f;
+                    for (int k = 0; k < K; ++k) acc1 += e4m3_decode(ar[k]) * e4m3_decode(br[k]);
+                    v0 = acc1;
+                }
             } else {
                 s0 = x[0] + x[1] + x[2] + x[3];
                 v0 = static_cast<float>(s0);
@@ -752,9 +762,6 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
                 lds_u8* const slot = next_slot();
                 read_all(slot, act[b]);
                 refill(slot);
-                if constexpr (F8)
-#pragma unroll
-                    for (int q = 0; q < S; ++q) act[b][q] = san(act[b][q]);
             }
 #pragma unroll
             for (int u = 0; u < LK_TMAX; ++u) {
