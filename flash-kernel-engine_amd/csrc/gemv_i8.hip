@@ -397,11 +397,13 @@ __global__ __launch_bounds__(SK_KS * 64) void gemv_mfma_kernel(GemmArgs p) {
 // NaN to the MFMA but 0.0 to the reference (src/quantized_gemm.cu:90-91).
 // The stream runs on the raw codes: E4M3 has no infinity, every product of
 // finite codes is finite and no sum of them can overflow fp32, so a NaN sum
-// proves a NaN code in its activation row or weight row, and that output
-// alone is recomputed from global memory by its finishing thread in the
-// reference's sequential k order (bit-exact with the reference there).
-// Weight bytes past K in the last piece read as zero (they would be the
-// next row's codes).  The four waves' partial sums meet in the fixed order
+// proves a NaN code in its activation row or weight row.  A workgroup that
+// saw one replays its whole stream once with every fragment cleared of the
+// codes on the VALU after its LDS read (clean tiles give the same bits
+// either way, so the replay simply overwrites): at most twice the time,
+// where clearing every fragment always cost ~20 % of the decode.  Weight
+// bytes past K in the last piece read as zero (they would be the next
+// row's codes).  The four waves' partial sums meet in the fixed order
 // w = 0..3.
 constexpr int LK_TMAX = 4;    // tiles accumulated between two reductions
 constexpr int LK_RMAX = 512;  // weight rows (of each half) of one workgroup
@@ -627,6 +629,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
     // its share of the tile is summed, so a chunk's early tiles are reduced
     // while the later tiles' copies stream in; the stores wait for the end of
     // the chunk (8 % faster at M = 4 than one reduction at the chunk's end).
+    int nan_seen = 0;  // FP8: a NaN sum in this thread's outputs (a 0x7F / 0xFF code took part)
     float yv[LK_TMAX][MB];
     int32_t sv[LK_TMAX][MB];
     auto finish_tile = [&](int tc, int u) __attribute__((always_inline)) {
@@ -680,16 +683,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
             float v0;
             if constexpr (F8) {
                 v0 = ((__int_as_float(x[0]) + __int_as_float(x[1])) + __int_as_float(x[2])) + __int_as_float(x[3]);
-                // A NaN code took part: the reference's sequential sum, 0x7F / 0xFF as 0.  Only for
-                // rows of this workgroup's share (padding rows of the last tile are never stored,
-                // and their weight row would lie past the share).
-                if (v0 != v0 && r < nr) {
-                    const uint8_t* ar = static_cast<const uint8_t*>(p.A) + static_cast<size_t>(mc + m + 16 * b) * K;
-                    const uint8_t* br = static_cast<const uint8_t*>(p.B) + static_cast<size_t>(r0 + r) * K;
-                    float acc1 = 0.0f;
-                    for (int k = 0; k < K; ++k) acc1 += e4m3_decode(ar[k]) * e4m3_decode(br[k]);
-                    v0 = acc1;
-                }
+                if (v0 != v0 && r < nr) nan_seen = 1;  // rows of the share only (padding rows are not stored)
             } else {
                 s0 = x[0] + x[1] + x[2] + x[3];
                 v0 = static_cast<float>(s0);
@@ -725,6 +719,16 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
         }
     };
 
+    auto san = [](v4i (&f)[S]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < S; ++q)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) f[q][e] = static_cast<int>(e4m3_sanitize(static_cast<uint32_t>(f[q][e])));
+    };
+    // The whole stream; CLEAR (FP8 replay only) clears the codes from every
+    // fragment after its LDS read.
+    auto stream = [&](auto clear_c) __attribute__((always_inline)) {
+    constexpr bool clear = decltype(clear_c)::value;
     // Prologue: the first NS items in flight.
     LkPos pi{0, min(LK_TMAX, T), 0, -MB};
     int issued = 0;
@@ -762,6 +766,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
                 lds_u8* const slot = next_slot();
                 read_all(slot, act[b]);
                 refill(slot);
+                if constexpr (clear) san(act[b]);
             }
 #pragma unroll
             for (int u = 0; u < LK_TMAX; ++u) {
@@ -770,6 +775,7 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
                     v4i w[S];
                     read_all(slot, w);
                     refill(slot);
+                    if constexpr (clear) san(w);
                     mma(acc[u], w);
                     if (j == np - 1 && (!SWI || (u & 1))) finish_tile(tc, u);
                 }
@@ -782,6 +788,12 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
             for (int b = 0; b < MB; ++b) acc[q][b] = AccV{0, 0, 0, 0};
         barrier();  // every read of red for this chunk precedes the next chunk's writes
     }
+    };
+    // Raw codes first; FP8 only: a workgroup with a NaN output replays the
+    // stream with the codes cleared (no copy is in flight between the two).
+    stream(std::false_type{});
+    if constexpr (F8)
+        if (__syncthreads_or(nan_seen)) stream(std::true_type{});
 }
 
 hipError_t launch_mfma_skinny(const GemmArgs& p, hipStream_t stream) {
