@@ -479,6 +479,24 @@ def test_fp8_streamed_tolerance(oracle, dev, M, N, K, nan_codes):
         assert mx <= 2e-2 and fro <= 2e-2, (out, mx, fro)
 
 
+@pytest.mark.parametrize("M", [1, 16, 64])
+def test_fp8_streamed_isolated_nan_codes(oracle, dev, M):
+    """One weight row and one activation element hold NaN codes: only the
+    workgroups whose outputs come out NaN replay their stream with the codes
+    cleared; every output still matches the reference (codes as 0.0)."""
+    N, K = 5000, 4096
+    say("fp8 streamed isolated NaN codes", M, N, K)
+    A, B, sa, sb = f8_inputs(oracle, M, N, K, 870 + M, "nk")
+    B[1234, 77] = 0x7F
+    B[4999, K - 1] = 0xFF
+    A[M - 1, 300] = 0xFF
+    ref = oracle.f8_gemm(A, B, sa, sb, b_layout=oracle.B_NK, nthreads=NTH)
+    got = gpu_f8(A, B, sa, sb, "nk", "f32", "gemv")
+    mx, fro = rel_errors(got, ref)
+    assert np.isfinite(got).all()
+    assert mx <= 2e-2 and fro <= 2e-2, (mx, fro)
+
+
 def test_c5_fp8_full(oracle, dev):
     """FP8 square: 8192^3 e4m3 (per-tensor amax/448 scales, B [K,N]), bf16 out,
     against the reference's sequential fp32 sum on 64 sampled rows."""
