@@ -400,8 +400,9 @@ __global__ __launch_bounds__(SK_KS * 64) void gemv_mfma_kernel(GemmArgs p) {
 // proves a NaN code in its activation row or weight row.  A workgroup that
 // saw one replays its whole stream once with every fragment cleared of the
 // codes on the VALU after its LDS read (clean tiles give the same bits
-// either way, so the replay simply overwrites): at most twice the time,
-// where clearing every fragment always cost ~20 % of the decode.  Weight
+// either way, so the replay simply overwrites).  Inputs holding such codes
+// take about twice the time; clearing every fragment on every call instead
+// cost ~20 % of the decode.  Weight
 // bytes past K in the last piece read as zero (they would be the next
 // row's codes).  The four waves' partial sums meet in the fixed order
 // w = 0..3.
@@ -725,8 +726,8 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemmArgs p) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) f[q][e] = static_cast<int>(e4m3_sanitize(static_cast<uint32_t>(f[q][e])));
     };
-    // The whole stream; CLEAR (FP8 replay only) clears the codes from every
-    // fragment after its LDS read.
+    // The whole stream; with clear_c true (the FP8 replay) every fragment is
+    // cleared of the codes after its LDS read.
     auto stream = [&](auto clear_c) __attribute__((always_inline)) {
     constexpr bool clear = decltype(clear_c)::value;
     // Prologue: the first NS items in flight.
