@@ -627,3 +627,31 @@ def test_torch_extension_f8_and_quantizer(oracle, dev):
     q, s = m.quantize_per_token_forward(dev_t(x))
     q_ref, s_ref = oracle.quantize_rows_i8(x, code)
     assert np.array_equal(q.cpu().numpy(), q_ref) and np.array_equal(s.cpu().numpy(), s_ref)
+
+
+def _random_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for _ in range(n):
+        M = int(rng.choice([1, 2, 3, 5, 15, 16, 17, 31, 32, 33, 47, 63, 64, 65, 100, 129, 200, 300]))
+        N = int(rng.integers(1, 1500))
+        K = int(rng.choice([64, 192, 1024, 1984, 2048, 2112, 3008, 4096, 4160, 6144]))
+        layout = str(rng.choice(["nk", "nk", "kn"]))
+        out = str(rng.choice(["i32", "bf16", "f32"]))
+        cases.append((M, N, K, layout, out))
+    return cases
+
+
+@pytest.mark.parametrize("M,N,K,layout,out", _random_cases(40, 20261201))
+def test_auto_dispatch_random_shapes(oracle, dev, M, N, K, layout, out):
+    """Seeded random shapes through the automatic dispatch (every family and
+    block-count boundary of the decode, batch, MFMA and generic paths),
+    bit-exact against the oracle."""
+    say("auto random", M, N, K, layout, out)
+    A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 5000 + M + N + K, layout)
+    acc = oracle.w8a8_acc(A, B, oracle.B_NK if layout == "nk" else oracle.B_KN, nthreads=NTH)
+    if out == "i32":
+        assert_same(gpu_i8(A, B, layout, "i32"), acc, f"auto {M, N, K, layout} i32")
+    else:
+        got = gpu_i8(A, B, layout, out, "auto", sa, sb, bias=bias)
+        assert_same(got, oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, out), f"auto {M, N, K, layout} {out}")
