@@ -655,3 +655,20 @@ def test_auto_dispatch_random_shapes(oracle, dev, M, N, K, layout, out):
     else:
         got = gpu_i8(A, B, layout, out, "auto", sa, sb, bias=bias)
         assert_same(got, oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, out), f"auto {M, N, K, layout} {out}")
+
+
+@pytest.mark.parametrize("M,N,K,layout,out", _random_cases(20, 20261202))
+def test_fp8_auto_dispatch_random_shapes(oracle, dev, M, N, K, layout, out):
+    """Seeded random shapes through the FP8 automatic dispatch (decode family
+    for B [N,K], MFMA and generic families), within the FP8 bar of the
+    reference's sequential sum, with a few NaN codes."""
+    out = "f32" if out == "i32" else out
+    say("fp8 auto random", M, N, K, layout, out)
+    A, B, sa, sb = f8_inputs(oracle, M, N, K, 6000 + M + N + K, layout, with_nan_codes=(M + N) % 3 == 0)
+    ref = oracle.f8_gemm(A, B, sa, sb, b_layout=oracle.B_NK if layout == "nk" else oracle.B_KN, nthreads=NTH)
+    got = gpu_f8(A, B, sa, sb, layout, out)
+    if out == "bf16":
+        got = oracle.bf16_to_f32(got)
+    mx, fro = rel_errors(got, ref)
+    assert np.isfinite(got).all()
+    assert mx <= 2e-2 and fro <= 2e-2, (mx, fro)
