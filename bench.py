@@ -6,8 +6,9 @@ per-channel fp32 scales, fp32 out) with inputs resident in HBM; `value` is its
 throughput in TOPS.  The decode GEMV (bf16 out + fused bias, weights rotated
 over 8 distinct 56 MiB buffers so the 256 MiB MALL cannot hold them) is timed in
 the same run and reported under "decode_gemv", and the M=16 decode (the other
-end of the decode configs) under "decode_gemv_m16".  Inputs are random (torch RNG
-on the device), never zero-filled.
+end of the decode configs) under "decode_gemv_m16", and a 64-row batch on the
+same weights (the batched decode kernel) under "decode_batch_m64".  Inputs are
+random (torch RNG on the device), never zero-filled.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--extra | --fp8 --swiglu --half --batch --shards] [--vendor] [--data-sweep] [--no-cpu]
 """
@@ -132,6 +133,7 @@ def main():
     # ---- decode GEMV M=1 and M=16, N=14336, K=4096, bf16 out + bias -------------
     gemv = gemv_bench(torch, L, _lib, dev, gen, 1, args.gemv_buffers, args.gemv_launches)
     gemv16 = gemv_bench(torch, L, _lib, dev, gen, 16, args.gemv_buffers, args.gemv_launches)
+    batch64 = gemv_bench(torch, L, _lib, dev, gen, 64, args.gemv_buffers, args.gemv_launches)
 
     line = {
         "metric": "INT8 TOPS at 8192^3 + HBM GB/s at M=1 decode GEMV (N=14336,K=4096)",
@@ -155,6 +157,7 @@ def main():
                      "algorithmic_ops_per_launch": ops_per},
         "decode_gemv": gemv,
         "decode_gemv_m16": gemv16,
+        "decode_batch_m64": batch64,
         "timed_wall_s": round(wall, 3),
     }
     line["hbm_copy_GBps"] = copy_bandwidth(torch, dev, gen)
