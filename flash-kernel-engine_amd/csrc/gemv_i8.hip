@@ -937,12 +937,13 @@ hipError_t launch_rows_m(const GemmArgs& p, hipStream_t s) {
 
 // Batches of 17..FKE_GEMV_MAX_M rows: whether the LDS-streamed kernel beats
 // the MFMA GEMM, from cost models fitted to measurements on MI355X (N of 4096
-// and 14336, K of 4096 and 14336, M of 17..512; each model within ~15 %):
-//  * streamed, per 64-row chunk of A: 5 us + cw us per KiB of the
-//    workgroup's weight share + 0.007 us per KiB of the chunk's activation
-//    rows (L2 hits), with cw = 0.054 (two 16-row blocks) or 0.068 (four): the
-//    weight stream slows as more MFMAs and activation items sit between its
-//    items;
+// and 14336, K of 4096 and 14336, M of 17..512):
+//  * streamed, per 64-row chunk of A: c0 + cw us per KiB of the workgroup's
+//    weight share + ca us per KiB of the chunk's activation rows (L2 hits),
+//    with (c0, cw, ca) = (4.0, 0.046, 0.004) for two 16-row blocks and
+//    (5.2, 0.056, 0.0078) for four (each fit within 1 % of its three shapes;
+//    chunks after the first measured up to 8 % faster): the weight stream
+//    slows as more MFMAs and activation items sit between its items;
 //  * MFMA GEMM: per round of 256x256 tiles over the CUs, 1.35 us per 128-byte
 //    K stage + 11 us.
 // Past 16 rows the MFMA GEMM has fewer tiles than CUs up to the hundreds of
@@ -952,8 +953,8 @@ bool gemv_i8_batch_pays(const GemmArgs& p) {
     const double kib = p.K / 1024.0;
     const int g = lds_grid(p), no = p.swiglu ? p.N / 2 : p.N;
     const double share = static_cast<double>((no + g - 1) / g) * (p.swiglu ? 2 : 1) * kib;
-    const double cw = p.M > 32 ? 0.068 : 0.054;
-    const double chunk = 5.0 + cw * share + 0.007 * min(p.M, 64) * kib;
+    const bool four = p.M > 32;
+    const double chunk = (four ? 5.2 : 4.0) + (four ? 0.056 : 0.046) * share + (four ? 0.0078 : 0.004) * min(p.M, 64) * kib;
     const double t_lds = ((p.M + 63) / 64) * chunk;
     const int64_t tiles = static_cast<int64_t>((p.M + 255) / 256) * ((p.N + 255) / 256);
     const int64_t rounds = (tiles + cu_count() - 1) / cu_count();
