@@ -164,27 +164,36 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
-// Row scale s (stored / applied in the epilogue) and its reciprocal r
-// (applied to the elements), both 1 for an all-zero row.
+// Row scale s (stored / applied in the epilogue), the reciprocal r applied to
+// the elements, and the power of two f the elements are multiplied by first:
+//   amax == 0: s = r = f = 1
+//   otherwise: s = fp32(amax/127), f = 2^64 if amax < 2^-64 else 1,
+//              r = fp32(127/(amax*f))
+// f keeps r finite for rows whose maximum is below 127/FLT_MAX (x*f and
+// amax*f are exact); wherever 127/amax is finite the codes equal those of
+// f = 1.  amax = +inf gives s = inf, r = 0.
 struct RowScale {
-    float s, r;
+    float s, r, f;
 };
 __device__ __forceinline__ RowScale scale_of(float amax) {
-    if (amax == 0.0f) return {1.0f, 1.0f};
-    return {amax / 127.0f, 127.0f / amax};
+    if (amax == 0.0f) return {1.0f, 1.0f, 1.0f};
+    const float f = amax < 0x1p-64f ? 0x1p64f : 1.0f;
+    return {amax / 127.0f, 127.0f / (amax * f), f};
 }
 
-// Code of x, clamp(rne(fp32(x * r)), -127, 127), in the low byte of the
-// result, in a few VALU operations: for finite x, |x*r| <= 127*(1+2^-23) <
-// 2^22, so adding 1.5*2^23 (a separate, correctly rounded fp32 add - the
-// product is rounded first) rounds x*r to an integer half to even and leaves
-// it, two's complement, in the low mantissa bits; it never reaches +-128, so
-// no clamp is needed.  NaN selects 0.
+// Code of x (already multiplied by the row's f), clamp(rne(fp32(x * r)),
+// -127, 127), in the low byte of the result, in a few VALU operations: the
+// product p is finite or NaN (|x| <= amax*f and r = fp32(127/(amax*f)), or
+// r = 0 for an infinite amax), and a finite |p| <= 127*(1+2^-23) < 2^22, so
+// adding 1.5*2^23 (a separate, correctly rounded fp32 add - the product is
+// rounded first) rounds p to an integer half to even and leaves it, two's
+// complement, in the low mantissa bits; it never reaches +-128, so no clamp
+// is needed.  A NaN product (NaN x, or inf * 0) selects 0.
 __device__ __forceinline__ uint32_t q8_bits(float x, float r) {
 #pragma clang fp contract(off)  // the product must be rounded before the add
     const float p = x * r;
     const uint32_t t = __float_as_uint(p + 12582912.0f);
-    return x != x ? 0u : t;
+    return p != p ? 0u : t;
 }
 
 // Low bytes of t0..t3 -> bytes 0..3 of one word.

@@ -3,10 +3,14 @@
 // quantized path takes int8 inputs and one scalar scale,
 // src/quantized_gemm.cu:56-75); this one produces the A operand and the
 // per-row scale_a of fke_qgemm_i8:
-//   amax_m = max_k |x[m,k]|                    (NaN elements ignored)
-//   s_m    = fp32(amax_m / 127),  r_m = fp32(127 / amax_m)   (both 1 when amax_m == 0)
-//   q[m,k] = clamp(rne(fp32(x[m,k] * r_m)), -127, 127)       (NaN elements give 0)
-// so that x ~= q * s_m and the GEMM's epilogue s = fp32(s_m * sb_n) dequantises.
+//   amax_m = max_k |x[m,k]|                    (NaN elements ignored, +-inf counted)
+//   s_m    = fp32(amax_m / 127),  r_m = fp32(127 / (amax_m * f_m))   (s = r = 1 when amax_m == 0)
+//   q[m,k] = clamp(rne(fp32(fp32(x[m,k] * f_m) * r_m)), -127, 127)   (a NaN product gives 0)
+// with f_m = 2^64 when amax_m < 2^-64, else 1 (an exact power of two that
+// keeps r_m finite for rows whose maximum is below 127/FLT_MAX; it changes no
+// code of any other row), so that x ~= q * s_m and the GEMM's epilogue
+// s = fp32(s_m * sb_n) dequantises.  A row holding +-inf gets s_m = inf and
+// r_m = 0: every code is 0.
 // One multiply per element instead of a correctly rounded division (about ten
 // instructions on this GPU, which made the division-based form VALU-bound).
 //
@@ -20,6 +24,8 @@
 // unaligned pointers) use the same arithmetic one element at a time, one
 // 256-thread workgroup per row.
 #include "fke_internal.h"
+
+#include <type_traits>
 
 namespace fke {
 namespace {
@@ -49,9 +55,11 @@ __device__ __forceinline__ float block_max(float v, float* red) {
     return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
+// The code of q8_bits, one element at a time (x already multiplied by f).
 __device__ __forceinline__ int8_t q8(float x, float r) {
-    if (x != x) return 0;
-    const float v = __builtin_rintf(x * r);
+    const float p = x * r;
+    if (p != p) return 0;
+    const float v = __builtin_rintf(p);
     return static_cast<int8_t>(fminf(fmaxf(v, -127.0f), 127.0f));
 }
 
@@ -84,23 +92,31 @@ __global__ __launch_bounds__(QT) void quant_rows_kernel(const void* X, int M, in
     }
     const RowScale rs = scale_of(wave_max(amax));
 
-    auto emit = [&](const v4i& v, int c) {
-        uint32_t w[EPC / 4];
+    // TINY: the row's f is 2^64 (a wave-uniform branch below; the common
+    // path has no extra multiply).
+    auto row = [&](auto tinyc) __attribute__((always_inline)) {
+        constexpr bool TINY = decltype(tinyc)::value;
+        auto x = [&](const v4i& v, int e) { return TINY ? elem<IN>(v, e) * 0x1p64f : elem<IN>(v, e); };
+        auto emit = [&](const v4i& v, int c) {
+            uint32_t w[EPC / 4];
 #pragma unroll
-        for (int j = 0; j < EPC / 4; ++j) {
-            const uint32_t t0 = q8_bits(elem<IN>(v, 4 * j + 0), rs.r), t1 = q8_bits(elem<IN>(v, 4 * j + 1), rs.r);
-            const uint32_t t2 = q8_bits(elem<IN>(v, 4 * j + 2), rs.r), t3 = q8_bits(elem<IN>(v, 4 * j + 3), rs.r);
-            w[j] = pack_q8(t0, t1, t2, t3);
+            for (int j = 0; j < EPC / 4; ++j) {
+                const uint32_t t0 = q8_bits(x(v, 4 * j + 0), rs.r), t1 = q8_bits(x(v, 4 * j + 1), rs.r);
+                const uint32_t t2 = q8_bits(x(v, 4 * j + 2), rs.r), t3 = q8_bits(x(v, 4 * j + 3), rs.r);
+                w[j] = pack_q8(t0, t1, t2, t3);
+            }
+            if constexpr (EPC == 4) *reinterpret_cast<uint32_t*>(qr + c * 4) = w[0];
+            else *reinterpret_cast<uint2*>(qr + c * 8) = make_uint2(w[0], w[1]);
+        };
+#pragma unroll
+        for (int i = 0; i < CACHE; ++i) {
+            const int c = lane + i * 64;
+            if (c < nch) emit(cache[i], c);
         }
-        if constexpr (EPC == 4) *reinterpret_cast<uint32_t*>(qr + c * 4) = w[0];
-        else *reinterpret_cast<uint2*>(qr + c * 8) = make_uint2(w[0], w[1]);
+        for (int c = lane + CACHE * 64; c < nch; c += 64) emit(xr[c], c);
     };
-#pragma unroll
-    for (int i = 0; i < CACHE; ++i) {
-        const int c = lane + i * 64;
-        if (c < nch) emit(cache[i], c);
-    }
-    for (int c = lane + CACHE * 64; c < nch; c += 64) emit(xr[c], c);
+    if (rs.f != 1.0f) row(std::true_type{});
+    else row(std::false_type{});
     if (lane == 0) S[m] = rs.s;
 }
 
@@ -117,7 +133,7 @@ __global__ __launch_bounds__(QT) void quant_rows_scalar_kernel(const void* X, in
     float amax = 0.0f;
     for (int k = tid; k < K; k += QT) amax = fmaxf(amax, fabsf(load(k)));
     const RowScale rs = scale_of(block_max(amax, red));
-    for (int k = tid; k < K; k += QT) Q[static_cast<size_t>(m) * K + k] = q8(load(k), rs.r);
+    for (int k = tid; k < K; k += QT) Q[static_cast<size_t>(m) * K + k] = q8(load(k) * rs.f, rs.r);
     if (tid == 0) S[m] = rs.s;
 }
 

@@ -1,9 +1,11 @@
-// torch_ext.cpp — torch C++ extension `flash_engine_hip`: the quantized GEMM
-// path (and the SwiGLU it feeds) in the binding idiom of reference python/bindings.cpp:101-140
-// (TORCH_CHECKs on device / dtype / shape, a fresh output tensor, the current
-// stream, one `*_forward` function per op).  The reference module
-// (flash_engine_cuda) exposes no quantized GEMM; these are the entries its
-// ops.quantized_gemm_int8 (python/flash_engine/ops.py:180-186) would bind.
+// torch_ext.cpp — torch C++ extension `flash_engine_cuda` (the reference's
+// module name, setup.py:51, imported by python/flash_engine/ops.py:9-13): the
+// quantized GEMM path (and the SwiGLU it feeds) in the binding idiom of
+// reference python/bindings.cpp:101-140 (TORCH_CHECKs on device / dtype /
+// shape, a fresh output tensor, the current stream, one `*_forward` function
+// per op).  The reference module exposes no quantized GEMM; these are the
+// entries its ops.quantized_gemm_int8 (python/flash_engine/ops.py:180-186)
+// would bind, beside its fused_swiglu_forward (ops.py:222-223).
 // Every call goes through the C ABI of libfke_qgemm.so (include/fke_qgemm.h);
 // this file holds no kernels and no CPU compute.
 #include <c10/hip/HIPStream.h>

@@ -6,8 +6,10 @@ B stored [K,N], fp32 result) but runs the HIP kernels of libfke_qgemm.so
 through its C ABI; host (numpy) inputs are copied to the GPU and the result
 copied back.  The checks before each call follow the reference binding idiom
 (python/bindings.cpp:101-133: device/shape checks, a fresh output tensor, the
-current stream).  There is no CPU compute path: without the built library the
-import of the library raises.
+current stream).  Every op runs the HIP kernels; without the built library the
+load of the library raises.  The one host computation is the reference op's
+own numpy arithmetic in `quantized_gemm_int8`, taken only for numpy inputs on
+a machine with no visible GPU.
 """
 from __future__ import annotations
 
@@ -104,6 +106,8 @@ def fp8_gemm_scaled(A: torch.Tensor, B: torch.Tensor, scale_a: float, scale_b: f
         B = B.view(torch.uint8)
     _check_dev("A", A, torch.uint8, dev)
     _check_dev("B", B, torch.uint8, dev)
+    if A.dim() != 2 or B.dim() != 2:
+        raise ValueError("A and B must be 2-D")
     layout = _LAYOUTS[b_layout]
     M, K = A.shape
     N, KB = (B.shape[0], B.shape[1]) if layout == B_NK else (B.shape[1], B.shape[0])
@@ -116,6 +120,8 @@ def fp8_gemm_scaled(A: torch.Tensor, B: torch.Tensor, scale_a: float, scale_b: f
         out = torch.empty((M, N), dtype=out_dtype, device=dev)
     else:
         _check_dev("out", out, out_dtype, dev)
+        if tuple(out.shape) != (M, N):
+            raise ValueError(f"out must be [{M}, {N}], got {tuple(out.shape)}")
     st = _lib.lib().fke_qgemm_f8_on_path(
         _PATHS[path], A.data_ptr(), B.data_ptr(), out.data_ptr(), M, N, K, scale_a, scale_b,
         _ptr(bias), _OUT_CODES[out_dtype], layout, _stream(A))
@@ -146,6 +152,8 @@ def quantize_per_token(x: torch.Tensor, q: torch.Tensor | None = None,
         q = torch.empty((M, K), dtype=torch.int8, device=dev)
     else:
         _check_dev("q", q, torch.int8, dev)
+        if tuple(q.shape) != (M, K):
+            raise ValueError(f"q must be [{M}, {K}], got {tuple(q.shape)}")
     if scale is None:
         scale = torch.empty(M, dtype=torch.float32, device=dev)
     else:
@@ -301,18 +309,40 @@ def fused_swiglu(gate, up):
     return out.cpu().numpy() if host else out
 
 
+def _host_int8(x, name: str) -> np.ndarray:
+    """A numpy operand as contiguous int8 for the GPU path.  The reference
+    widens its inputs with astype(np.int32) (python/flash_engine/ops.py:184), so
+    an integer array whose values lie outside [-128, 127] would give a
+    different product after a narrowing cast: it is rejected instead."""
+    x = np.asarray(x)
+    if x.dtype == np.int8:
+        return np.ascontiguousarray(x)
+    if not np.issubdtype(x.dtype, np.integer):
+        raise TypeError(f"{name} must hold integers (int8 values), got {x.dtype}")
+    if x.size and (int(x.min()) < -128 or int(x.max()) > 127):
+        raise ValueError(f"{name} has values outside the int8 range [-128, 127]")
+    return np.ascontiguousarray(x, dtype=np.int8)
+
+
 def quantized_gemm_int8(A, B, scale_a: float = 1.0, scale_b: float = 1.0):
     """C = (A_int8 @ B_int8) * (scale_a * scale_b), B stored [K,N], fp32 out.
 
     Same signature and result as reference python/flash_engine/ops.py:180-186:
     the scale product is formed in double (Python floats) and applied as fp32,
-    the int32 product is exact.  GPU tensors stay on the GPU; numpy arrays are
-    copied to cuda:0 and the result is returned as a numpy array.
+    the int32 product is exact.  GPU tensors stay on the GPU and run the HIP
+    kernels.  numpy arrays are copied to cuda:0 and the result is returned as a
+    numpy array.  Only on a machine where no GPU is visible at all do numpy
+    inputs take the reference op's own host arithmetic (an int32 numpy matmul,
+    as there), so CPU-only callers of the reference op keep working; wherever a
+    GPU is visible the HIP path runs, and a missing HIP library raises.
     """
-    host = isinstance(A, np.ndarray)
+    host = isinstance(A, np.ndarray) or isinstance(B, np.ndarray)
+    if host and not torch.cuda.is_available():
+        acc = np.asarray(A).astype(np.int32) @ np.asarray(B).astype(np.int32)
+        return acc.astype(np.float32) * (scale_a * scale_b)
     if host:
-        A = torch.from_numpy(np.ascontiguousarray(A, dtype=np.int8)).cuda()
-        B = torch.from_numpy(np.ascontiguousarray(B, dtype=np.int8)).cuda()
+        A = torch.from_numpy(_host_int8(A, "A")).cuda()
+        B = torch.from_numpy(_host_int8(B, "B")).cuda()
     alpha = float(np.float32(float(scale_a) * float(scale_b)))
     # the compiled binding, as the reference op calls its extension (ops.py:10-13)
     out = _ext.ext().quantized_gemm_int8_forward(A.contiguous(), B.contiguous(), None, None, None,

@@ -314,7 +314,17 @@ float fko_quantize_e4m3(const float* x, uint8_t* q, size_t n) {
 /* Per-token INT8 quantiser (no reference counterpart).  fp32 arithmetic as the
  * kernel does it: the scale and its reciprocal are single correctly rounded
  * fp32 divisions, each code one fp32 product (the file is built with
- * -ffp-contract=off); nearbyintf rounds half to even in the default mode. */
+ * -ffp-contract=off); nearbyintf rounds half to even in the default mode.
+ *   amax = max |x| over the row's non-NaN elements (+inf included)
+ *   amax == 0:  s = r = 1, f = 1
+ *   otherwise:  s = fp32(amax / 127); f = 2^64 if amax < 2^-64 else 1;
+ *               r = fp32(127 / (amax * f))
+ *   p = fp32(fp32(x * f) * r);  q = NaN(p) ? 0 : clamp(rne(p), -127, 127)
+ * f keeps 127/amax finite for rows whose maximum is below 127/FLT_MAX: x * f
+ * and amax * f are exact (a power of two, no overflow), and for every row
+ * where 127/amax is finite the result equals that of f = 1.  A row holding
+ * +-inf has s = inf and r = 0, so every code is 0 (inf * 0 is NaN); NaN
+ * elements give 0. */
 void fko_quantize_rows_i8(const void* x, int in_dtype, int M, int K, int8_t* q, float* scale) {
     for (int m = 0; m < M; ++m) {
         float amax = 0.0f;
@@ -324,14 +334,15 @@ void fko_quantize_rows_i8(const void* x, int in_dtype, int M, int K, int8_t* q, 
             const float a = fabsf(v);
             if (a > amax) amax = a;
         }
+        const float f = (amax > 0.0f && amax < 0x1p-64f) ? 0x1p64f : 1.0f;
         const float s = amax == 0.0f ? 1.0f : amax / 127.0f;
-        const float r = amax == 0.0f ? 1.0f : 127.0f / amax;
+        const float r = amax == 0.0f ? 1.0f : 127.0f / (amax * f);
         scale[m] = s;
         for (int k = 0; k < K; ++k) {
             const size_t i = (size_t)m * K + k;
             const float v = in_dtype == 0 ? ((const float*)x)[i] : fko_bf16_to_f32(((const uint16_t*)x)[i]);
-            if (v != v) { q[i] = 0; continue; }
-            const float p = v * r;
+            const float p = (v * f) * r;
+            if (p != p) { q[i] = 0; continue; }
             float t = nearbyintf(p);
             if (t > 127.0f) t = 127.0f;
             if (t < -127.0f) t = -127.0f;

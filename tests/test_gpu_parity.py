@@ -574,6 +574,44 @@ def test_quantize_rows_unaligned_input(oracle, dev):
     assert np.array_equal(s.cpu().numpy(), s_ref) and np.array_equal(q.cpu().numpy(), q_ref)
 
 
+def edge_rows(K):
+    """Rows with tiny maxima (127/amax overflows fp32 below ~3.7e-37), +-inf,
+    NaN and all-NaN, beside ordinary rows, for the quantiser's edge cases."""
+    r = np.random.default_rng(K)
+    base = r.standard_normal((10, K)).astype(np.float32)
+    mags = np.array([1.0, 1e-38, 2e-40, 1e-44, 2.0**-70, 3e-37, 5.0, 1.0, 1.0, 1.0], dtype=np.float32)
+    x = (base / np.abs(base).max(axis=1, keepdims=True) * mags[:, None]).astype(np.float32)
+    x[6, K // 3] = np.inf
+    x[7, 0] = -np.inf
+    x[7, K - 1] = np.nan
+    x[8, ::7] = np.nan
+    x[9, :] = np.nan
+    return x
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("K", [4096, 100])
+def test_quantize_rows_edge_values(oracle, dev, K, dtype):
+    """Tiny row maxima (the power-of-two prescale), +-inf rows (scale inf, all
+    codes 0), NaN elements and all-NaN rows, on the chunked kernel (K = 4096)
+    and the element-wise kernel (K = 100): codes and scales bit-exact against
+    the oracle."""
+    say("quantize rows edge values", K, dtype)
+    x = edge_rows(K)
+    if dtype == "bf16":
+        bits = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+        q_ref, s_ref = oracle.quantize_rows_i8(bits, oracle.IN_BF16)
+        xt = dev_t(bits.view(np.int16)).view(torch.bfloat16)
+    else:
+        q_ref, s_ref = oracle.quantize_rows_i8(x)
+        xt = dev_t(x)
+    q, s = ops.quantize_per_token(xt)
+    torch.cuda.synchronize()
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+    assert np.isinf(s_ref[6]) and not q_ref[6].any()
+
+
 @pytest.mark.parametrize("M", [1, 9, 300])
 def test_w8a8_linear_end_to_end(oracle, dev, M):
     """bf16 activations -> per-token quantiser -> W8A8 GEMM with per-channel
@@ -597,7 +635,7 @@ def test_w8a8_linear_end_to_end(oracle, dev, M):
 
 @pytest.mark.parametrize("layout", ["nk", "kn"])
 def test_torch_extension_i8_bit_exact(oracle, dev, layout):
-    """flash_engine_hip.quantized_gemm_int8_forward (bindings.cpp idiom) on the
+    """flash_engine_cuda.quantized_gemm_int8_forward (bindings.cpp idiom) on the
     MFMA and decode families, every output type, against the oracle."""
     from flash_engine import _ext
     m = _ext.ext()

@@ -374,6 +374,69 @@ def test_quantize_rows_matches_numpy_fp32_semantics(oracle):
     assert q[6, 3] == 2                # 1.5 with s = 1 -> 2 (even)
 
 
+def _quantize_rows_numpy(x, f=None):
+    """The quantiser evaluated by numpy's IEEE float32 arithmetic with the
+    row factor f given (None: 2^64 below a 2^-64 maximum, else 1)."""
+    amax = np.max(np.where(np.isnan(x), np.float32(0), np.abs(x)), axis=1).astype(np.float32)
+    if f is None:
+        f = np.where((amax > 0) & (amax < np.float32(2.0**-64)), np.float32(2.0**64), np.float32(1.0))
+    f = np.asarray(f, dtype=np.float32) * np.ones_like(amax)
+    zero = amax == 0
+    with np.errstate(divide="ignore", over="ignore", invalid="ignore"):
+        s = np.where(zero, np.float32(1), amax / np.float32(127)).astype(np.float32)
+        r = np.where(zero, np.float32(1), np.float32(127) / (amax * f)).astype(np.float32)
+        p = (x * f[:, None]).astype(np.float32) * r[:, None]
+        q = np.where(np.isnan(p), 0, np.clip(np.rint(np.nan_to_num(p, nan=0.0)), -127, 127)).astype(np.int8)
+    return q, s
+
+
+def test_quantize_rows_tiny_row_maxima(oracle):
+    """Rows whose maximum is below 127/FLT_MAX (~3.7e-37), where fp32(127/amax)
+    overflows: the power-of-two prescale keeps the amax element at +-127 and
+    every code equal to the exact-rational rounding of x*127/amax (to within
+    the one rounding of r).  Rows with a maximum in [2^-121, 2^-64) take the
+    prescale too, and there the codes equal the f = 1 evaluation: the
+    prescale changes no row where 127/amax is finite."""
+    r = rng(24)
+    base = r.standard_normal((6, 64)).astype(np.float32)
+    mags = np.array([1e-38, 2e-40, 1e-44, 3e-37, 1e-30, 2.0**-70], dtype=np.float32)
+    x = (base / np.abs(base).max(axis=1, keepdims=True) * mags[:, None]).astype(np.float32)
+    x[2, 5] = np.float32(1e-45)            # the smallest subnormal scale of values
+    q, s = oracle.quantize_rows_i8(x)
+    q_np, s_np = _quantize_rows_numpy(x)
+    assert np.array_equal(q, q_np) and np.array_equal(s, s_np)
+    amax = np.abs(x).max(axis=1)
+    for m in range(x.shape[0]):
+        k = int(np.argmax(np.abs(x[m])))
+        assert q[m, k] == (127 if x[m, k] > 0 else -127), m
+        for kk in range(x.shape[1]):          # |q - x*127/amax| <= 1/2 (+ the rounding of r)
+            ideal = Fraction(float(x[m, kk])) * 127 / Fraction(float(amax[m]))
+            assert abs(Fraction(int(q[m, kk])) - ideal) <= Fraction(1, 2) + Fraction(1, 2**16), (m, kk)
+    with np.errstate(over="ignore", divide="ignore"):
+        finite = np.float32(127) / amax < np.float32(np.inf)
+    q1, _ = _quantize_rows_numpy(x[finite], f=1.0)
+    assert finite.sum() >= 2 and np.array_equal(q[finite], q1)
+
+
+def test_quantize_rows_non_finite(oracle):
+    """NaN elements give code 0 and do not enter the maximum; a row holding
+    +-inf has scale inf and r = 0, so every code is 0 (inf * 0 is NaN, finite *
+    0 is 0); the other rows are untouched."""
+    x = np.array([[1.0, np.inf, -3.0, 0.5],
+                  [-np.inf, 2.0, np.nan, 0.0],
+                  [np.nan, 2.0, -4.0, 1.0],
+                  [np.nan, np.nan, np.nan, np.nan],
+                  [np.inf, -np.inf, 0.0, 1e-45]], dtype=np.float32)
+    q, s = oracle.quantize_rows_i8(x)
+    assert np.isinf(s[0]) and np.isinf(s[1]) and np.isinf(s[4])
+    assert q[0].tolist() == [0, 0, 0, 0] and q[1].tolist() == [0, 0, 0, 0] and q[4].tolist() == [0, 0, 0, 0]
+    assert s[2] == np.float32(4.0) / np.float32(127.0)
+    assert q[2].tolist() == [0, 64, -127, 32]       # r = 31.75: 2 -> 63.5 -> 64
+    assert s[3] == 1.0 and q[3].tolist() == [0, 0, 0, 0]
+    q_np, s_np = _quantize_rows_numpy(x)
+    assert np.array_equal(q, q_np) and np.array_equal(s, s_np)
+
+
 def test_quantize_rows_bf16_input(oracle):
     """bf16 inputs quantise exactly like their fp32 values (bf16 -> fp32 is
     exact: the bits shifted left by 16)."""
