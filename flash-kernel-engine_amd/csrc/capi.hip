@@ -6,12 +6,40 @@
 // tested) without a GPU.  Otherwise the return value is the status of this
 // call's hipLaunchKernel (the reference returned cudaGetLastError() after its
 // launch, src/quantized_gemm.cu:74,138, which could also surface an earlier
-// sticky error).  No state is kept between calls.
+// sticky error).  No state is kept between calls, apart from the device
+// scratch of fke_w8a8_linear_noalloc (and its per-device address, set once).
 #include <cstdio>
+#include <mutex>
 
 #include "fke_internal.h"
 
+// Device scratch of fke_w8a8_linear_noalloc: the quantised activations and
+// their row scales between its two launches (the layout of the workspace of
+// fke_w8a8_linear).  Each GPU the library runs on holds its own copy for the
+// life of the process.  In host code `scratch` is only a handle: its device
+// address on the current device comes from hipGetSymbolAddress (below).
+static __device__ __align__(256) uint8_t scratch[FKE_W8A8_NOALLOC_SCRATCH_BYTES];
+
 namespace {
+
+// Per-device address of `scratch`, looked up once per device with that device
+// current (the first allocation-free call on it) and immutable afterwards.
+constexpr int kMaxDevices = 64;
+std::once_flag g_scratch_once[kMaxDevices];
+void* g_scratch_ptr[kMaxDevices];
+hipError_t g_scratch_status[kMaxDevices];
+
+hipError_t scratch_of_device(int dev, void** out) {
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::call_once(g_scratch_once[dev], [dev] {
+        void* ptr = nullptr;
+        g_scratch_status[dev] = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        g_scratch_ptr[dev] = ptr;
+    });
+    if (g_scratch_status[dev] != hipSuccess) return g_scratch_status[dev];
+    *out = g_scratch_ptr[dev];
+    return hipSuccess;
+}
 
 using fke::GemmArgs;
 
@@ -233,6 +261,30 @@ int fke_w8a8_linear(const void* X, int in_dtype, const int8_t* W, void* Y, int M
     if (out_dtype != FKE_OUT_F32 && out_dtype != FKE_OUT_BF16) return hipErrorInvalidValue;
     return run_w8a8_from_float(make_args(X, W, Y, M, N, K, nullptr, w_scale, 1.0f, sb, bias, out_dtype, FKE_B_NK),
                                in_dtype, workspace, workspace_bytes, stream);
+}
+
+int fke_w8a8_linear_noalloc(const void* X, int in_dtype, const int8_t* W, void* Y, int M, int N, int K,
+                            const float* w_scale, float sb, const float* bias, int out_dtype, void* stream) {
+    if (!common_args_ok(X, W, Y, M, N, K, FKE_B_NK)) return hipErrorInvalidValue;
+    if (in_dtype != FKE_IN_F32 && in_dtype != FKE_IN_BF16) return hipErrorInvalidValue;
+    if (out_dtype != FKE_OUT_F32 && out_dtype != FKE_OUT_BF16) return hipErrorInvalidValue;
+    if (w8a8_ws_bytes(M, K) > FKE_W8A8_NOALLOC_SCRATCH_BYTES) return hipErrorInvalidValue;
+    // The scratch must be the copy on the stream's device, looked up with
+    // that device current: a stream of another device is refused.
+    int dev = 0;
+    hipError_t st = hipGetDevice(&dev);
+    if (st != hipSuccess) return st;
+    if (stream) {
+        hipDevice_t sdev = 0;
+        st = hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev);
+        if (st != hipSuccess) return st;
+        if (sdev != dev) return hipErrorInvalidValue;
+    }
+    void* ptr = nullptr;
+    st = scratch_of_device(dev, &ptr);
+    if (st != hipSuccess) return st;
+    return run_w8a8_from_float(make_args(X, W, Y, M, N, K, nullptr, w_scale, 1.0f, sb, bias, out_dtype, FKE_B_NK),
+                               in_dtype, ptr, FKE_W8A8_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 int fke_w8a8_swiglu_linear(const void* X, int in_dtype, const int8_t* W, void* H, int M, int I, int K,

@@ -18,6 +18,7 @@ B_NK, B_KN = 0, 1
 PATH_AUTO, PATH_GEMV, PATH_MFMA, PATH_GENERIC = 0, 1, 2, 3
 IN_F32, IN_BF16, IN_F16 = 0, 1, 2
 HIP_SUCCESS, HIP_ERROR_INVALID_VALUE = 0, 1
+W8A8_NOALLOC_SCRATCH_BYTES = 32 << 20  # FKE_W8A8_NOALLOC_SCRATCH_BYTES
 
 # Every exported symbol with its (argtypes, restype).
 _p, _i, _f = ct.c_void_p, ct.c_int, ct.c_float
@@ -39,6 +40,7 @@ SIGNATURES = {
     "fke_select_path_half": ([_p, _p, _p, _i, _i, _i, _i, _i, _i], _i),
     "fke_w8a8_linear_workspace_size": ([_i, _i], ct.c_size_t),
     "fke_w8a8_linear": ([_p, _i, _p, _p, _i, _i, _i, _p, _f, _p, _i, _p, ct.c_size_t, _p], _i),
+    "fke_w8a8_linear_noalloc": ([_p, _i, _p, _p, _i, _i, _i, _p, _f, _p, _i, _p], _i),
     "fke_w8a8_swiglu_linear": ([_p, _i, _p, _p, _i, _i, _i, _p, _f, _p, _i, _p, ct.c_size_t, _p], _i),
     "fke_select_path_i8": ([_p, _p, _p, _i, _i, _i, _i, _i], _i),
     "fke_select_path_f8": ([_p, _p, _p, _i, _i, _i, _i, _i], _i),

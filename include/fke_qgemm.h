@@ -13,7 +13,8 @@
  *     K-contiguous per output column) or [K,N] (FKE_B_KN).  C is [M,N].
  *   - The call is asynchronous on `stream` (a hipStream_t; NULL = the null
  *     stream) and never synchronises.  No mutable global state: calls are
- *     re-entrant from any host thread.
+ *     re-entrant from any host thread.  (The one exception is the device
+ *     scratch of fke_w8a8_linear_noalloc, shared by its calls on one GPU.)
  */
 #ifndef FKE_QGEMM_H
 #define FKE_QGEMM_H
@@ -212,6 +213,26 @@ size_t fke_w8a8_linear_workspace_size(int M, int K);
 int fke_w8a8_linear(const void* X, int in_dtype, const int8_t* W, void* Y, int M, int N, int K,
                     const float* w_scale, float sb, const float* bias, int out_dtype,
                     void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * fke_w8a8_linear without the caller's workspace, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  Same
+ * arguments and result as fke_w8a8_linear, bit for bit; the quantised
+ * activations and row scales go to a library-owned device array of
+ * FKE_W8A8_NOALLOC_SCRATCH_BYTES bytes per GPU (held until the process ends;
+ * its address is looked up once per device).  The call allocates nothing.
+ * Rejects, with hipErrorInvalidValue, shapes whose workspace
+ * (fke_w8a8_linear_workspace_size(M, K)) exceeds the array, and a stream of a
+ * device other than the current one.  Every call on one GPU shares that GPU's
+ * array: calls that overlap on one GPU (other streams, other host threads
+ * without ordering) race; calls ordered on one stream are safe.  Nothing in
+ * the array needs to start at zero (each call writes what it reads).
+ */
+#define FKE_W8A8_NOALLOC_SCRATCH_BYTES (32u << 20)
+int fke_w8a8_linear_noalloc(const void* X, int in_dtype, const int8_t* W, void* Y, int M, int N, int K,
+                            const float* w_scale, float sb, const float* bias, int out_dtype,
+                            void* stream);
 
 /* The same with the fused SwiGLU gate/up GEMM (fke_qgemm_i8_swiglu): W is
  * [2I, K], w_scale and bias [2I], H [M, I]. */

@@ -159,6 +159,26 @@ def test_w8a8_linear_from_float_arguments():
     assert L.fke_w8a8_swiglu_linear(P, F32, P, P, 9, 64, 4096, None, 1.0, None, 2, P, 1 << 20, None) == INVALID
 
 
+def test_w8a8_linear_noalloc_arguments():
+    """The allocation-free linear takes no workspace and rejects, before any
+    HIP call, shapes whose workspace would not fit its device scratch, as well
+    as everything fke_w8a8_linear rejects."""
+    L = _lib.lib()
+    BF16 = _lib.IN_BF16
+    na = L.fke_w8a8_linear_noalloc
+    cap = _lib.W8A8_NOALLOC_SCRATCH_BYTES
+    assert cap == 32 << 20
+    M, K = 4096, 8192                       # codes exactly fill the array: the scales do not fit
+    assert L.fke_w8a8_linear_workspace_size(M, K) > cap
+    assert na(P, BF16, P, P, M, 64, K, None, 1.0, None, 1, None) == INVALID
+    assert na(P, BF16, P, P, 1, 64, cap, None, 1.0, None, 1, None) == INVALID
+    assert L.fke_w8a8_linear_workspace_size(4096, 8000) <= cap   # fits (checked on the GPU)
+    assert na(None, BF16, P, P, 1, 64, 4096, None, 1.0, None, 1, None) == INVALID
+    assert na(P, _lib.IN_F16, P, P, 1, 64, 4096, None, 1.0, None, 1, None) == INVALID
+    assert na(P, BF16, P, P, 1, 64, 4096, None, 1.0, None, _lib.OUT_I32, None) == INVALID
+    assert na(P, BF16, P, P, 0, 64, 4096, None, 1.0, None, 1, None) == INVALID
+
+
 def test_dropin_int8_rejects_k_not_multiple_of_4():
     """The reference kernel silently drops the K tail and misaligns rows when
     K % 4 != 0 (src/quantized_gemm.cu:28-30); the drop-in rejects it."""
