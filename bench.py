@@ -7,8 +7,20 @@ throughput in TOPS.  The decode GEMV (bf16 out + fused bias, weights rotated
 over 8 distinct 56 MiB buffers so the 256 MiB MALL cannot hold them) is timed in
 the same run and reported under "decode_gemv", and the M=16 decode (the other
 end of the decode configs) under "decode_gemv_m16", and a 64-row batch on the
-same weights (the batched decode kernel) under "decode_batch_m64".  Inputs are
-random (torch RNG on the device), never zero-filled.
+same weights (the batched decode kernel) under "decode_batch_m64".  The other
+two GEMM configurations of the benchmark set sit in the same line with their
+own rooflines: "c3" (prefill 4096x11008x4096, bf16 out) and "c5" (FP8 e4m3
+8192^3, B [K,N] as the reference's launcher reads it, operands drawn as fp32
+N(0,1) and quantised at per-tensor amax/448).  Inputs are random (torch RNG
+on the device), never zero-filled.
+
+Each GEMM configuration first runs back to back for a fixed wall time
+(--preheat-ms): the shader clock settles over the first ~50 ms of sustained
+MFMA load (measured: 481 us per launch over the first 100 launches of the
+headline GEMM, 430 us after), and the counted warm-up steps alone are too few
+to cover that.  The shader clock under the headline load is read through
+amdsmi and reported as "sclk_mhz" (with the socket power: this GEMM runs at
+the board's power limit, so the clock is the box-to-box variable).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--extra | --fp8 --swiglu --half --batch --shards] [--vendor] [--data-sweep] [--no-cpu]
 """
@@ -53,6 +65,8 @@ def parse():
     # lower, still-settling clock (measured 558 us/step there vs 505 after).
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--preheat-ms", type=float, default=250.0,
+                    help="wall time each GEMM configuration runs back to back before its counted warm-up")
     ap.add_argument("--gemv-buffers", type=int, default=8)
     ap.add_argument("--gemv-launches", type=int, default=400)
     ap.add_argument("--extra", action="store_true", help="also time configs 2 and 4, decode M=4 and batched decode M=32,64,128")
@@ -98,7 +112,9 @@ def main():
     def rand_u(n, lo=0.001, hi=0.02):
         return torch.rand(n, device=dev, generator=gen) * (hi - lo) + lo
 
-    def timed(fn, n, warm):
+    def timed(fn, n, warm, preheat_ms=0.0):
+        if preheat_ms > 0:
+            preheat(torch, fn, preheat_ms)
         for _ in range(warm):
             fn()
         torch.cuda.synchronize()
@@ -123,12 +139,21 @@ def main():
             raise RuntimeError(f"fke_qgemm_i8 failed: {_lib.status_string(st)}")
 
     torch.cuda.synchronize()
+    clock = ClockSampler()
+    clock.start()
+    pre_n, pre_ms = preheat(torch, gemm, args.preheat_ms)
     t0 = time.perf_counter()
     ms = timed(gemm, args.steps, args.warmup)
     wall = time.perf_counter() - t0
+    preheat(torch, gemm, 1100.0)  # the same load a while longer: the metrics refresh once a second
+    sclk = clock.stop()
     ops_per = 2.0 * M * N * K
     tops = ops_per / (ms * 1e-3) / 1e12
     del C
+
+    # ---- C3 prefill and C5 FP8 square, each with its own roofline -------------
+    c3 = c3_line(torch, L, _lib, dev, rand_i8, rand_u, timed, args)
+    c5 = c5_line(torch, L, _lib, dev, gen, timed, args)
 
     # ---- decode GEMV M=1 and M=16, N=14336, K=4096, bf16 out + bias -------------
     gemv = gemv_bench(torch, L, _lib, dev, gen, 1, args.gemv_buffers, args.gemv_launches)
@@ -155,6 +180,11 @@ def main():
                      "unit": "TOP/s", "frac": round(tops / PEAK_INT8_TOPS, 4),
                      "traffic": traffic("gemm_mfma_kernel<i8,NK,f32> M=N=K=8192"),
                      "algorithmic_ops_per_launch": ops_per},
+        "preheat_ms": round(pre_ms, 1),
+        "preheat_launches": pre_n,
+        "sclk_mhz": sclk,
+        "c3": c3,
+        "c5": c5,
         "decode_gemv": gemv,
         "decode_gemv_m16": gemv16,
         "decode_batch_m64": batch64,
@@ -189,6 +219,154 @@ def main():
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(line), flush=True)
+
+
+def preheat(torch, fn, ms, chunk=16):
+    """Run fn back to back until `ms` milliseconds of wall time have passed
+    (synchronising every `chunk` launches); returns (launches, wall ms)."""
+    t0 = time.perf_counter()
+    n = 0
+    while True:
+        for _ in range(chunk):
+            fn()
+        torch.cuda.synchronize()
+        n += chunk
+        el = (time.perf_counter() - t0) * 1e3
+        if el >= ms:
+            return n, el
+
+
+class ClockSampler:
+    """Reads the GPU's shader clock and socket power through amdsmi on a
+    background thread (every 5 ms) while the headline GEMM runs.  The
+    firmware refreshes its metrics table about once a second (measured: the
+    table's system_clock_counter steps by 1e9 ns), so only readings whose
+    counter advanced while the load ran - at least 100 ms after it started -
+    count; the clock is the mean over the XCDs of current_gfxclks."""
+
+    def __init__(self, period=0.005):
+        self.period = period
+        self.fresh = []
+        self.t_load = None
+        self.err = None
+        self._stop = False
+        self._th = None
+        self._last = None
+        try:
+            import amdsmi
+            amdsmi.amdsmi_init()
+            self.smi = amdsmi
+            self.h = amdsmi.amdsmi_get_processor_handles()[0]
+            self._last = self._read()[0]
+        except Exception as e:  # no amdsmi or no permission: report why
+            self.smi = None
+            self.err = repr(e)[:160]
+
+    def _read(self):
+        m = self.smi.amdsmi_get_gpu_metrics_info(self.h)
+        xs = [v for v in m.get("current_gfxclks", []) if isinstance(v, (int, float))]
+        power = m.get("current_socket_power")
+        return (m.get("system_clock_counter"), sum(xs) / len(xs) if xs else None, min(xs) if xs else None,
+                max(xs) if xs else None, power if isinstance(power, (int, float)) else None)
+
+    def _run(self):
+        while not self._stop:
+            try:
+                r = self._read()
+                if r[0] != self._last:
+                    self._last = r[0]
+                    if r[1] is not None and time.perf_counter() - self.t_load >= 0.1:
+                        self.fresh.append(r)
+            except Exception as e:
+                self.err = repr(e)[:160]
+            time.sleep(self.period)
+
+    def start(self):
+        self.t_load = time.perf_counter()
+        if self.smi is not None:
+            import threading
+            self._th = threading.Thread(target=self._run, daemon=True)
+            self._th.start()
+
+    def stop(self):
+        self._stop = True
+        if self._th is not None:
+            self._th.join()
+        if self.smi is None or not self.fresh:
+            return {"value": None, "error": self.err or "no metrics refresh during the load"}
+        clk = [r[1] for r in self.fresh]
+        pw = [r[4] for r in self.fresh if r[4] is not None]
+        return {"value": round(sum(clk) / len(clk), 1),
+                "xcd_min": min(r[2] for r in self.fresh), "xcd_max": max(r[3] for r in self.fresh),
+                "socket_power_w": round(sum(pw) / len(pw), 1) if pw else None, "readings": len(clk),
+                "source": "amdsmi gpu_metrics current_gfxclks (mean over XCDs), readings refreshed while the "
+                          "headline GEMM ran back to back (pre-heat, timed steps, then 1.1 s more)"}
+
+
+def c3_line(torch, L, _lib, dev, rand_i8, rand_u, timed, args):
+    """W8A8 prefill M=4096 N=11008 K=4096 (MLP up), int8
+    uniform, per-token x per-channel scales U[0.001,0.02], bf16 out."""
+    M, N, K = 4096, 11008, 4096
+    sh = torch.cuda.current_stream(dev).cuda_stream
+    A, B, sa, sb = rand_i8(M, K), rand_i8(N, K), rand_u(M), rand_u(N)
+    C = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+
+    def run():
+        st = L.fke_qgemm_i8(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, sa.data_ptr(), sb.data_ptr(), 1.0,
+                            1.0, None, _lib.OUT_BF16, _lib.B_NK, sh)
+        if st:
+            raise RuntimeError(f"fke_qgemm_i8 failed: {_lib.status_string(st)}")
+
+    ms = timed(run, args.steps, args.warmup, args.preheat_ms)
+    ops = 2.0 * M * N * K
+    t = ops / (ms * 1e-3) / 1e12
+    del A, B, C
+    return {"metric": "INT8 TOPS, prefill W8A8 GEMM M=4096 N=11008 K=4096 (bf16 out)", "value": round(t, 1),
+            "unit": "TOPS", "ms_per_launch": round(ms, 4), "steps": args.steps,
+            "roofline": {"bound": "mfma", "achieved": round(t, 1), "peak": PEAK_INT8_TOPS, "unit": "TOP/s",
+                         "frac": round(t / PEAK_INT8_TOPS, 4),
+                         "traffic": traffic("gemm_mfma_kernel<i8,NK,bf16> M=4096 N=11008 K=4096"),
+                         "algorithmic_ops_per_launch": ops},
+            "kernel": "gemm_mfma_kernel<i8,NK,bf16>"}
+
+
+def c5_line(torch, L, _lib, dev, gen, timed, args):
+    """FP8 e4m3 8192^3.  A and B are drawn as fp32 N(0,1) and
+    quantised to e4m3 with per-tensor scales amax/448 (saturating; the largest
+    element maps to 448), B stored [K,N] as the reference's launcher reads it
+    (src/quantized_gemm.cu:113), fp32 accumulation, bf16 out."""
+    M = N = K = 8192
+    sh = torch.cuda.current_stream(dev).cuda_stream
+
+    def quant(shape):
+        x = torch.randn(shape, device=dev, generator=gen)
+        s = float(x.abs().max()) / 448.0
+        q = torch.clamp(x / s, -448.0, 448.0).to(torch.float8_e4m3fn).view(torch.uint8)
+        del x
+        return q.contiguous(), s
+
+    A8, s_a = quant((M, K))
+    B8, s_b = quant((K, N))
+    C = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+
+    def run():
+        st = L.fke_qgemm_f8(A8.data_ptr(), B8.data_ptr(), C.data_ptr(), M, N, K, s_a, s_b, None, _lib.OUT_BF16,
+                            _lib.B_KN, sh)
+        if st:
+            raise RuntimeError(f"fke_qgemm_f8 failed: {_lib.status_string(st)}")
+
+    ms = timed(run, args.steps, args.warmup, args.preheat_ms)
+    flops = 2.0 * M * N * K
+    t = flops / (ms * 1e-3) / 1e12
+    del A8, B8, C
+    return {"metric": "FP8 TFLOPS, scaled e4m3 GEMM M=N=K=8192, B [K,N] (bf16 out)", "value": round(t, 1),
+            "unit": "TFLOPS", "ms_per_launch": round(ms, 4), "steps": args.steps,
+            "data": "fp32 N(0,1) quantised to e4m3 at per-tensor amax/448 on the device",
+            "roofline": {"bound": "mfma", "achieved": round(t, 1), "peak": PEAK_FP8_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(t / PEAK_FP8_TFLOPS, 4),
+                         "traffic": traffic("gemm_mfma_kernel<f8,KN,bf16> M=N=K=8192"),
+                         "algorithmic_flops_per_launch": flops},
+            "kernel": "gemm_mfma_kernel<f8,KN,bf16>"}
 
 
 def copy_bandwidth(torch, dev, gen):
@@ -241,6 +419,24 @@ def graph_us(torch, dev, launch, launches, warm, reps=3):
     return e0.elapsed_time(e1) * 1e3 / (reps * launches)
 
 
+def eager_us(torch, dev, launch, launches):
+    """Per-call microseconds of `launches` eager calls through the C ABI (ctypes
+    call, argument checks, dispatch and launch on the current stream, no graph),
+    events around them as in the reference's benchmark idiom
+    (benchmarks/bench_decoding.cu:33-58)."""
+    sh = torch.cuda.current_stream(dev).cuda_stream
+    for i in range(16):
+        launch(i, sh)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(launches):
+        launch(i, sh)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / launches
+
+
 def gemv_bench(torch, L, _lib, dev, gen, M, nbuf, launches, N=14336, K=4096):
     """Launch-averaged duration of the decode GEMV from a HIP graph of `launches`
     calls cycling over `nbuf` distinct weight buffers (>= 448 MiB in total)."""
@@ -259,10 +455,12 @@ def gemv_bench(torch, L, _lib, dev, gen, M, nbuf, launches, N=14336, K=4096):
             raise RuntimeError(f"gemv failed: {_lib.status_string(st)}")
 
     us = graph_us(torch, dev, launch, launches, 2 * nbuf)
+    eager = eager_us(torch, dev, launch, launches)
     nbytes = gemv_bytes(M, N, K)
     gbs = nbytes / (us * 1e-6) / 1e9
     return {"metric": f"HBM GB/s, decode GEMV M={M} N={N} K={K} (bf16 out, fused bias)",
             "value": round(gbs, 1), "unit": "GB/s", "us_per_launch": round(us, 3),
+            "us_per_call_eager": round(eager, 3),
             "weight_buffers": nbuf, "weight_bytes_cycled": nbuf * N * K,
             "timing": f"HIP graph of {launches} launches x 3 replays, events on the graph's stream",
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,

@@ -123,10 +123,15 @@ int fke_qgemm_f8_on_path(int path, const uint8_t* A, const uint8_t* B, void* C,
  * scale_a for fke_qgemm_i8 from fp32 or bf16 activations X [M,K].  No
  * reference counterpart (the reference GEMMs take int8 inputs and scalar
  * scales, src/quantized_gemm.cu:56-75):
- *   amax_m = max_k |X[m,k]|             (NaN elements ignored)
- *   s_m    = fp32(amax_m / 127) -> scale[m];  r_m = fp32(127 / amax_m)
- *            (both 1 when amax_m == 0)
- *   Q[m,k] = clamp(rne(fp32(X[m,k] * r_m)), -127, 127)       (NaN -> 0)
+ *   amax_m = max_k |X[m,k]|             (NaN elements ignored, +-inf counted)
+ *   s_m    = fp32(amax_m / 127) -> scale[m]
+ *   f_m    = 2^64 if amax_m < 2^-64 else 1;  r_m = fp32(127 / (amax_m * f_m))
+ *            (s_m = r_m = 1 when amax_m == 0)
+ *   p      = fp32(fp32(X[m,k] * f_m) * r_m)
+ *   Q[m,k] = NaN(p) ? 0 : clamp(rne(p), -127, 127)
+ * f_m (exact) keeps r_m finite when 127/amax_m would overflow fp32 and changes
+ * no code where it would not.  A row holding +-inf gets scale inf and all
+ * codes 0; NaN elements give 0.
  * The divisions are IEEE fp32, correctly rounded.  Q is int8 [M,K] row-major,
  * scale fp32 [M]; device buffers.  Rejects NULL pointers, M,K <= 0 and bad
  * dtypes with hipErrorInvalidValue.

@@ -250,29 +250,47 @@ void fko_f8_gemm(const uint8_t* A, const uint8_t* B, void* out, int M, int N, in
     float dec[256];
     for (int i = 0; i < 256; ++i) dec[i] = fko_e4m3_decode((uint8_t)i);
     if (nthreads < 1) nthreads = 1;
+    if (b_layout == FKO_B_KN) {
+        /* B decoded once; rows in blocks of RB, k outer and n inner, so each
+         * decoded B row serves RB rows from cache.  Every sums[i][n] still
+         * adds k = 0..K-1 in order, one product and one sum per step. */
+        enum { RB = 8 };
+        float* bf = (float*)malloc(sizeof(float) * (size_t)K * N);
+#pragma omp parallel for schedule(static) num_threads(nthreads)
+        for (int k = 0; k < K; ++k)
+            for (int n = 0; n < N; ++n) bf[(size_t)k * N + n] = dec[B[(size_t)k * N + n]];
+#pragma omp parallel for schedule(dynamic, 1) num_threads(nthreads)
+        for (int r0 = 0; r0 < R; r0 += RB) {
+            const int nr = R - r0 < RB ? R - r0 : RB;
+            float* sums = (float*)malloc(sizeof(float) * (size_t)RB * N);
+            for (size_t i = 0; i < (size_t)RB * N; ++i) sums[i] = 0.0f;
+            for (int k = 0; k < K; ++k) {
+                const float* b = bf + (size_t)k * N;
+                for (int i = 0; i < nr; ++i) {
+                    const int m = rows ? rows[r0 + i] : r0 + i;
+                    const float av = dec[A[(size_t)m * K + k]];
+                    float* s = sums + (size_t)i * N;
+                    for (int n = 0; n < N; ++n) s[n] += av * b[n];
+                }
+            }
+            for (int i = 0; i < nr; ++i)
+                for (int n = 0; n < N; ++n)
+                    store_out(out, (size_t)(r0 + i) * N + n, out_dtype, epi(sums[(size_t)i * N + n], alpha, bias, n),
+                              0);
+            free(sums);
+        }
+        free(bf);
+        return;
+    }
 #pragma omp parallel for schedule(dynamic, 1) num_threads(nthreads)
     for (int r = 0; r < R; ++r) {
         const int m = rows ? rows[r] : r;
         const uint8_t* a = A + (size_t)m * K;
-        if (b_layout == FKO_B_KN) {
-            /* k outer, n inner: each sums[n] still adds k = 0..K-1 in order */
-            float* sums = (float*)malloc(sizeof(float) * (size_t)N);
-            for (int n = 0; n < N; ++n) sums[n] = 0.0f;
-            for (int k = 0; k < K; ++k) {
-                const float av = dec[a[k]];
-                const uint8_t* b = B + (size_t)k * N;
-                for (int n = 0; n < N; ++n) sums[n] += av * dec[b[n]];
-            }
-            for (int n = 0; n < N; ++n)
-                store_out(out, (size_t)r * N + n, out_dtype, epi(sums[n], alpha, bias, n), 0);
-            free(sums);
-        } else {
-            for (int n = 0; n < N; ++n) {
-                const uint8_t* b = B + (size_t)n * K;
-                float sum = 0.0f;
-                for (int k = 0; k < K; ++k) sum += dec[a[k]] * dec[b[k]];
-                store_out(out, (size_t)r * N + n, out_dtype, epi(sum, alpha, bias, n), 0);
-            }
+        for (int n = 0; n < N; ++n) {
+            const uint8_t* b = B + (size_t)n * K;
+            float sum = 0.0f;
+            for (int k = 0; k < K; ++k) sum += dec[a[k]] * dec[b[k]];
+            store_out(out, (size_t)r * N + n, out_dtype, epi(sum, alpha, bias, n), 0);
         }
     }
 }

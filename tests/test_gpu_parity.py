@@ -428,6 +428,31 @@ def rel_errors(got, ref):
             np.linalg.norm(d) / max(np.linalg.norm(ref.astype(np.float64)), 1e-30))
 
 
+# Measured-level bounds beside the FP8 bar (2e-2, max-norm and Frobenius
+# relative to the reference's sequential fp32 sum).  Another fp32 summation
+# order moves a sum by a few units of fp32 rounding of its partial sums: fp32
+# outputs measured 1e-5..3e-5 (max-norm) and ~1.5e-5 (Frobenius), held to
+# 2e-4 / 1e-4.  A bf16 output is the rounding of such a sum, so each element
+# must lie within bf16's half unit (at most 2^-8 of the element) plus 2e-4 of
+# the largest element.  A regression to a lower-precision accumulation fails
+# these long before it reaches 2e-2.
+FP8_F32_TIGHT = (2e-4, 1e-4)
+
+
+def assert_fp8_close(got, ref, out, what=""):
+    mx, fro = rel_errors(got, ref)
+    print(f"[fp8 error] {what} {out}: max-norm {mx:.3e} frobenius {fro:.3e}", flush=True)
+    assert np.isfinite(got).all(), f"{what} {out}: non-finite output"
+    assert mx <= 2e-2 and fro <= 2e-2, (what, out, mx, fro)
+    if out == "f32":
+        assert mx <= FP8_F32_TIGHT[0] and fro <= FP8_F32_TIGHT[1], ("measured-level bound", what, mx, fro)
+    else:
+        r = ref.astype(np.float64)
+        allowed = 2.0**-8 * np.abs(r) + 2e-4 * max(np.abs(r).max(), 1e-30)
+        bad = np.abs(got.astype(np.float64) - r) > allowed
+        assert not bad.any(), ("bf16 beyond its rounding of an fp32-level sum", what, int(bad.sum()))
+
+
 @pytest.mark.parametrize("layout", ["kn", "nk"])
 @pytest.mark.parametrize("shape", [(64, 64, 256), (37, 50, 131), (300, 272, 384)])
 def test_fp8_generic_bit_exact(oracle, dev, layout, shape):
@@ -454,9 +479,7 @@ def test_fp8_mfma_tolerance(oracle, dev, layout, out, nan_codes):
     got = gpu_f8(A, B, sa, sb, layout, out, "mfma", bias=bias)
     if out == "bf16":
         got = oracle.bf16_to_f32(got)
-    mx, fro = rel_errors(got, ref)
-    assert np.isfinite(got).all()
-    assert mx <= 2e-2 and fro <= 2e-2, (mx, fro)
+    assert_fp8_close(got, ref, out, f"mfma {layout} nan={nan_codes}")
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 300, 4096), (3, 1000, 2048), (16, 777, 5056), (16, 4096, 14336),
@@ -474,9 +497,7 @@ def test_fp8_streamed_tolerance(oracle, dev, M, N, K, nan_codes):
         got = gpu_f8(A, B, sa, sb, "nk", out, "gemv", bias=bias)
         if out == "bf16":
             got = oracle.bf16_to_f32(got)
-        mx, fro = rel_errors(got, ref)
-        assert np.isfinite(got).all(), f"fp8 streamed {out}: non-finite output"
-        assert mx <= 2e-2 and fro <= 2e-2, (out, mx, fro)
+        assert_fp8_close(got, ref, out, f"streamed {M, N, K} nan={nan_codes}")
 
 
 @pytest.mark.parametrize("M", [1, 16, 64])
@@ -492,23 +513,21 @@ def test_fp8_streamed_isolated_nan_codes(oracle, dev, M):
     A[M - 1, 300] = 0xFF
     ref = oracle.f8_gemm(A, B, sa, sb, b_layout=oracle.B_NK, nthreads=NTH)
     got = gpu_f8(A, B, sa, sb, "nk", "f32", "gemv")
-    mx, fro = rel_errors(got, ref)
-    assert np.isfinite(got).all()
-    assert mx <= 2e-2 and fro <= 2e-2, (mx, fro)
+    assert_fp8_close(got, ref, "f32", f"streamed isolated NaN codes M={M}")
 
 
 def test_c5_fp8_full(oracle, dev):
     """FP8 square: 8192^3 e4m3 (per-tensor amax/448 scales, B [K,N]), bf16 out,
-    against the reference's sequential fp32 sum on 64 sampled rows."""
+    against the reference's sequential fp32 sum on 1024 rows spread over M
+    (every 8th row: each of the 32 row tiles contributes 32 rows)."""
     M = N = K = 8192
     say("c5 fp8", M, N, K)
     A, B, sa, sb = f8_inputs(oracle, M, N, K, 4000, "kn")
     got = oracle.bf16_to_f32(gpu_f8(A, B, sa, sb, "kn", "bf16"))
-    rows = np.linspace(0, M - 1, 64).astype(np.int32)
+    rows = np.arange(3, M, 8, dtype=np.int32)
+    assert rows.size == 1024
     ref = oracle.f8_gemm(A, B, sa, sb, b_layout=oracle.B_KN, rows=rows, nthreads=NTH)
-    mx, fro = rel_errors(got[rows], ref)
-    print("c5 sampled rel errors: max-norm", mx, "frobenius", fro)
-    assert mx <= 2e-2 and fro <= 2e-2
+    assert_fp8_close(got[rows], ref, "bf16", "c5 1024 rows")
 
 
 # --------------------------------------------------------------- python op
@@ -659,8 +678,7 @@ def test_torch_extension_f8_and_quantizer(oracle, dev):
     A, B, sa, sb = f8_inputs(oracle, M, N, K, 995, "kn")
     y = m.fp8_gemm_scaled_forward(dev_t(A), dev_t(B), sa, sb, None, torch.float32, "kn")
     ref = oracle.f8_gemm(A, B, sa, sb, None, oracle.OUT_F32, oracle.B_KN, nthreads=NTH)
-    err = np.abs(y.cpu().numpy() - ref).max() / max(np.abs(ref).max(), 1e-30)
-    assert err <= 2e-2, err
+    assert_fp8_close(y.cpu().numpy(), ref, "f32", "torch ext")
     x, code = quant_inputs(oracle, 20, 4096, 996, "f32")
     q, s = m.quantize_per_token_forward(dev_t(x))
     q_ref, s_ref = oracle.quantize_rows_i8(x, code)
@@ -707,6 +725,4 @@ def test_fp8_auto_dispatch_random_shapes(oracle, dev, M, N, K, layout, out):
     got = gpu_f8(A, B, sa, sb, layout, out)
     if out == "bf16":
         got = oracle.bf16_to_f32(got)
-    mx, fro = rel_errors(got, ref)
-    assert np.isfinite(got).all()
-    assert mx <= 2e-2 and fro <= 2e-2, (mx, fro)
+    assert_fp8_close(got, ref, out, f"auto {M, N, K, layout}")
