@@ -159,6 +159,9 @@ def main():
     gemv = gemv_bench(torch, L, _lib, dev, gen, 1, args.gemv_buffers, args.gemv_launches)
     gemv16 = gemv_bench(torch, L, _lib, dev, gen, 16, args.gemv_buffers, args.gemv_launches)
     batch64 = gemv_bench(torch, L, _lib, dev, gen, 64, args.gemv_buffers, args.gemv_launches)
+    # the same decode with B stored [K,N], the layout of the reference's Python op
+    gemv_kn1 = gemv_bench(torch, L, _lib, dev, gen, 1, args.gemv_buffers, args.gemv_launches, layout="kn")
+    gemv_kn16 = gemv_bench(torch, L, _lib, dev, gen, 16, args.gemv_buffers, args.gemv_launches, layout="kn")
 
     line = {
         "metric": "INT8 TOPS at 8192^3 + HBM GB/s at M=1 decode GEMV (N=14336,K=4096)",
@@ -188,6 +191,8 @@ def main():
         "decode_gemv": gemv,
         "decode_gemv_m16": gemv16,
         "decode_batch_m64": batch64,
+        "decode_gemv_b_kn": gemv_kn1,
+        "decode_gemv_m16_b_kn": gemv_kn16,
         "timed_wall_s": round(wall, 3),
     }
     line["hbm_copy_GBps"] = copy_bandwidth(torch, dev, gen)
@@ -437,11 +442,14 @@ def eager_us(torch, dev, launch, launches):
     return e0.elapsed_time(e1) * 1e3 / launches
 
 
-def gemv_bench(torch, L, _lib, dev, gen, M, nbuf, launches, N=14336, K=4096):
+def gemv_bench(torch, L, _lib, dev, gen, M, nbuf, launches, N=14336, K=4096, layout="nk"):
     """Launch-averaged duration of the decode GEMV from a HIP graph of `launches`
-    calls cycling over `nbuf` distinct weight buffers (>= 448 MiB in total)."""
+    calls cycling over `nbuf` distinct weight buffers (>= 448 MiB in total);
+    B stored [N,K] ("nk") or [K,N] ("kn", the reference's Python-op layout)."""
     A = torch.clamp(torch.round(torch.randn((M, K), device=dev, generator=gen) * 30), -127, 127).to(torch.int8)
-    Bs = [torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=gen) for _ in range(nbuf)]
+    shape = (N, K) if layout == "nk" else (K, N)
+    code = _lib.B_NK if layout == "nk" else _lib.B_KN
+    Bs = [torch.randint(-127, 128, shape, dtype=torch.int8, device=dev, generator=gen) for _ in range(nbuf)]
     sa = torch.rand(M, device=dev, generator=gen) * 0.019 + 0.001
     sb = torch.rand(N, device=dev, generator=gen) * 0.019 + 0.001
     bias = torch.randn(N, device=dev, generator=gen) * 0.02
@@ -450,7 +458,7 @@ def gemv_bench(torch, L, _lib, dev, gen, M, nbuf, launches, N=14336, K=4096):
     def launch(i, sh):
         st = L.fke_qgemm_i8(A.data_ptr(), Bs[i % nbuf].data_ptr(), out.data_ptr(), M, N, K,
                             sa.data_ptr(), sb.data_ptr(), 1.0, 1.0, bias.data_ptr(), _lib.OUT_BF16,
-                            _lib.B_NK, sh)
+                            code, sh)
         if st:
             raise RuntimeError(f"gemv failed: {_lib.status_string(st)}")
 
@@ -458,16 +466,18 @@ def gemv_bench(torch, L, _lib, dev, gen, M, nbuf, launches, N=14336, K=4096):
     eager = eager_us(torch, dev, launch, launches)
     nbytes = gemv_bytes(M, N, K)
     gbs = nbytes / (us * 1e-6) / 1e9
-    return {"metric": f"HBM GB/s, decode GEMV M={M} N={N} K={K} (bf16 out, fused bias)",
+    kernel = gemv_kernel(M) if layout == "nk" else "gemv_kn_kernel<i8,bf16>"
+    return {"metric": f"HBM GB/s, decode GEMV M={M} N={N} K={K}, B {'[N,K]' if layout == 'nk' else '[K,N]'} "
+                      f"(bf16 out, fused bias)",
             "value": round(gbs, 1), "unit": "GB/s", "us_per_launch": round(us, 3),
             "us_per_call_eager": round(eager, 3),
             "weight_buffers": nbuf, "weight_bytes_cycled": nbuf * N * K,
             "timing": f"HIP graph of {launches} launches x 3 replays, events on the graph's stream",
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
                          "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
-                         "traffic": traffic(f"{gemv_kernel(M)} M={M} N={N} K={K} bf16+bias"),
+                         "traffic": traffic(f"{kernel} M={M} N={N} K={K} bf16+bias"),
                          "algorithmic_bytes_per_launch": nbytes},
-            "kernel": gemv_kernel(M)}
+            "kernel": kernel}
 
 
 def shard_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
@@ -621,23 +631,25 @@ def fp8_configs(torch, L, _lib, dev, gen, timed, args):
         b[(b & 0x7F) == 0x7F] = 0
         Bs.append(b)
     bias = torch.randn(N, device=dev, generator=gen) * 0.02
-    for M in (1, 16):
-        A8 = torch.randint(0, 256, (M, K), dtype=torch.uint8, device=dev, generator=gen)
-        A8[(A8 & 0x7F) == 0x7F] = 0
-        out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    # the same bytes read as B [K,N] (the reference launcher's layout) run the transposing decode kernel
+    for lname, lay, kname in (("", _lib.B_NK, "gemv_lds_kernel (FP8)"), ("_Bkn", _lib.B_KN, "gemv_kn_kernel<f8>")):
+        for M in (1, 16):
+            A8 = torch.randint(0, 256, (M, K), dtype=torch.uint8, device=dev, generator=gen)
+            A8[(A8 & 0x7F) == 0x7F] = 0
+            out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
 
-        def launch(i, st):
-            r = L.fke_qgemm_f8(A8.data_ptr(), Bs[i % nbuf].data_ptr(), out.data_ptr(), M, N, K, 0.01, 0.01,
-                               bias.data_ptr(), _lib.OUT_BF16, _lib.B_NK, st)
-            if r:
-                raise RuntimeError(f"fp8 decode failed: {_lib.status_string(r)}")
+            def launch(i, st):
+                r = L.fke_qgemm_f8(A8.data_ptr(), Bs[i % nbuf].data_ptr(), out.data_ptr(), M, N, K, 0.01, 0.01,
+                                   bias.data_ptr(), _lib.OUT_BF16, lay, st)
+                if r:
+                    raise RuntimeError(f"fp8 decode failed: {_lib.status_string(r)}")
 
-        us = graph_us(torch, dev, launch, args.gemv_launches, 2 * nbuf)
-        nbytes = M * K + N * K + 4 * N + 2 * M * N
-        gbs = nbytes / (us * 1e-6) / 1e9
-        res[f"fp8_decode_M{M}_14336x4096_bf16"] = {"us": round(us, 3), "GB/s": round(gbs, 1),
-                                                   "frac": round(gbs / PEAK_HBM_GBS, 4), "bytes": nbytes,
-                                                   "kernel": "gemv_lds_kernel (FP8)"}
+            us = graph_us(torch, dev, launch, args.gemv_launches, 2 * nbuf)
+            nbytes = M * K + N * K + 4 * N + 2 * M * N
+            gbs = nbytes / (us * 1e-6) / 1e9
+            res[f"fp8_decode_M{M}_14336x4096_bf16{lname}"] = {"us": round(us, 3), "GB/s": round(gbs, 1),
+                                                              "frac": round(gbs / PEAK_HBM_GBS, 4),
+                                                              "bytes": nbytes, "kernel": kname}
     del Bs
     return res
 

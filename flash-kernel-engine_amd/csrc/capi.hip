@@ -123,6 +123,8 @@ GemmArgs make_swiglu_args(const void* A, const void* W, void* H, int M, int I, i
 }
 
 int pick_i8(const GemmArgs& p) {
+    // decode with B [K,N]: the transposing LDS-streamed kernel
+    if (fke::gemv_kn_supports(p, fke::ELEM_I8)) return FKE_PATH_GEMV;
     // decode and batches up to FKE_GEMV_MAX_M rows: the decode family where
     // its cost model beats the MFMA GEMM's, or where that GEMM cannot run
     if (fke::gemv_i8_supports(p) && (fke::gemv_i8_batch_pays(p) || !fke::mfma_supports(p, fke::ELEM_I8)))
@@ -132,6 +134,7 @@ int pick_i8(const GemmArgs& p) {
 }
 
 int pick_f8(const GemmArgs& p) {
+    if (fke::gemv_kn_supports(p, fke::ELEM_F8)) return FKE_PATH_GEMV;  // decode with B [K,N]
     // decode and small batches (B [N,K]): the streamed kernel, by the same cost model as INT8
     if (fke::gemv_f8_supports(p) && (fke::gemv_i8_batch_pays(p) || !fke::mfma_supports(p, fke::ELEM_F8)))
         return FKE_PATH_GEMV;
@@ -144,6 +147,7 @@ int run_i8(int path, const GemmArgs& p, void* stream) {
     if (path == FKE_PATH_AUTO) path = pick_i8(p);
     switch (path) {
         case FKE_PATH_GEMV:
+            if (fke::gemv_kn_supports(p, fke::ELEM_I8)) return fke::launch_gemv_kn(p, fke::ELEM_I8, s);
             if (!fke::gemv_i8_supports(p)) return hipErrorInvalidValue;
             return fke::launch_gemv_i8(p, s);
         case FKE_PATH_MFMA:
@@ -184,6 +188,7 @@ int run_f8(int path, const GemmArgs& p, void* stream) {
     if (path == FKE_PATH_AUTO) path = pick_f8(p);
     switch (path) {
         case FKE_PATH_GEMV:
+            if (fke::gemv_kn_supports(p, fke::ELEM_F8)) return fke::launch_gemv_kn(p, fke::ELEM_F8, s);
             if (!fke::gemv_f8_supports(p)) return hipErrorInvalidValue;
             return fke::launch_gemv_f8(p, s);
         case FKE_PATH_MFMA:

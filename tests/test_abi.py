@@ -194,12 +194,19 @@ def test_path_unavailable_for_shape_is_rejected():
                                   0, 0, None) == INVALID
     assert L.fke_qgemm_i8_on_path(_lib.PATH_GEMV, P, P, P, 513, 64, 4096, None, None, 1.0, 1.0, None,
                                   0, 0, None) == INVALID
-    assert L.fke_qgemm_i8_on_path(_lib.PATH_GEMV, P, P, P, 4, 64, 4096, None, None, 1.0, 1.0, None,
+    # GEMV with B [K,N]: M <= 16, N % 16 == 0, K % 64 == 0
+    assert L.fke_qgemm_i8_on_path(_lib.PATH_GEMV, P, P, P, 17, 64, 4096, None, None, 1.0, 1.0, None,
+                                  0, 1, None) == INVALID
+    assert L.fke_qgemm_i8_on_path(_lib.PATH_GEMV, P, P, P, 4, 72, 4096, None, None, 1.0, 1.0, None,
+                                  0, 1, None) == INVALID
+    assert L.fke_qgemm_i8_on_path(_lib.PATH_GEMV, P, P, P, 4, 64, 4000, None, None, 1.0, 1.0, None,
                                   0, 1, None) == INVALID
     assert L.fke_qgemm_i8_on_path(_lib.PATH_MFMA, P, P, P, 64, 64, 100, None, None, 1.0, 1.0, None,
                                   0, 0, None) == INVALID
-    # FP8 decode family: B [N,K], fp32 / bf16 out, K >= 2048
-    assert L.fke_qgemm_f8_on_path(_lib.PATH_GEMV, P, P, P, 4, 64, 4096, 1.0, 1.0, None, 0, 1,
+    # FP8 decode family: B [N,K] with K >= 2048, or B [K,N] with M <= 16; fp32 / bf16 out
+    assert L.fke_qgemm_f8_on_path(_lib.PATH_GEMV, P, P, P, 17, 64, 4096, 1.0, 1.0, None, 0, 1,
+                                  None) == INVALID
+    assert L.fke_qgemm_f8_on_path(_lib.PATH_GEMV, P, P, P, 4, 72, 4096, 1.0, 1.0, None, 0, 1,
                                   None) == INVALID
     assert L.fke_qgemm_f8_on_path(_lib.PATH_GEMV, P, P, P, 4, 64, 1024, 1.0, 1.0, None, 0, 0,
                                   None) == INVALID
@@ -224,7 +231,11 @@ def test_path_unavailable_for_shape_is_rejected():
     (4096, 11008, 4096, 0, _lib.PATH_MFMA),
     (8192, 8192, 8192, 0, _lib.PATH_MFMA),
     (8192, 8192, 8192, 1, _lib.PATH_MFMA),
-    (1, 14336, 4096, 1, _lib.PATH_MFMA),
+    (1, 14336, 4096, 1, _lib.PATH_GEMV),     # B [K,N] decode: the transposing streamed kernel
+    (16, 14336, 4096, 1, _lib.PATH_GEMV),
+    (4, 4096, 64, 1, _lib.PATH_GEMV),
+    (4, 4104, 4096, 1, _lib.PATH_GENERIC),   # B [K,N] with N % 16 != 0: neither fast kernel
+    (17, 4096, 4096, 1, _lib.PATH_MFMA),
     (64, 64, 100, 0, _lib.PATH_GENERIC),
     (64, 64, 4, 0, _lib.PATH_GENERIC),
     (8, 64, 96, 0, _lib.PATH_GENERIC),
@@ -246,7 +257,10 @@ def test_dispatch_unaligned_pointer_falls_back():
     (1, 14336, 4096, 0, _lib.PATH_GEMV),      # FP8 decode: the LDS-streamed kernel
     (16, 14336, 4096, 0, _lib.PATH_GEMV),
     (64, 14336, 4096, 0, _lib.PATH_GEMV),
-    (1, 14336, 4096, 1, _lib.PATH_MFMA),      # B [K,N] (the reference layout): no streamed kernel
+    (1, 14336, 4096, 1, _lib.PATH_GEMV),      # B [K,N] (the reference layout): transposing decode kernel
+    (16, 14336, 4096, 1, _lib.PATH_GEMV),
+    (17, 14336, 4096, 1, _lib.PATH_MFMA),
+    (4, 14336, 4000, 1, _lib.PATH_GENERIC),   # K % 64 != 0
     (8192, 8192, 8192, 0, _lib.PATH_MFMA),
     (4, 14336, 1024, 0, _lib.PATH_MFMA),      # K < 2048
     (4, 300, 2112, 0, _lib.PATH_GEMV),        # K % 128 != 0: no MFMA GEMM

@@ -280,6 +280,78 @@ def test_c2_decode_full(oracle, dev, M):
     assert_same(got, oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, "bf16"), f"c2 M={M}")
 
 
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_c2_decode_full_b_kn(oracle, dev, M):
+    """C2 with B stored [K,N] (the layout of the reference's Python op and FP8
+    launcher): the transposing decode kernel, checked in full."""
+    N, K = 14336, 4096
+    say("c2 decode B [K,N]", M, N, K)
+    A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 1000 + M, layout="kn", act="normal")
+    assert _lib.lib().fke_select_path_i8(4096, 4096, 4096, M, N, K, 1, 1) == _lib.PATH_GEMV
+    acc = oracle.w8a8_acc(A, B, oracle.B_KN, nthreads=NTH)
+    got = gpu_i8(A, B, "kn", "bf16", "auto", sa, sb, bias=bias)
+    assert_same(got, oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, "bf16"), f"c2 kn M={M}")
+
+
+# (M, N, K): one 64-column block and a ragged last block (N % 64 != 0), a K
+# that ends in half an item (K % 128 == 64), K below one item per wave (waves
+# without items), K = 14336 (28 items per wave), more blocks than CUs
+KN_SHAPES = [(1, 16, 4096), (3, 304, 1024), (16, 1040, 192), (5, 4096, 64), (2, 4096, 14336),
+             (16, 20016, 2048), (8, 1008, 4160)]
+
+
+@pytest.mark.parametrize("M,N,K", KN_SHAPES)
+@pytest.mark.parametrize("out,opts", [("i32", "none"), ("f32", "vec"), ("bf16", "vec"), ("f32", "scalar")])
+def test_gemv_kn_i8_bit_exact(oracle, dev, M, N, K, out, opts):
+    """INT8 decode with B [K,N] on the transposing kernel: every output type,
+    per-row / per-column scales with bias and scalar scales, bit-exact."""
+    say("gemv kn i8", M, N, K, out, opts)
+    A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 7000 + M + N + K, layout="kn")
+    acc = oracle.w8a8_acc(A, B, oracle.B_KN, nthreads=NTH)
+    if out == "i32":
+        assert_same(gpu_i8(A, B, "kn", "i32", "gemv"), acc, f"kn i32 {M, N, K}")
+    elif opts == "vec":
+        got = gpu_i8(A, B, "kn", out, "gemv", sa, sb, bias=bias)
+        assert_same(got, oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, out), f"kn {out} {M, N, K}")
+    else:
+        got = gpu_i8(A, B, "kn", out, "gemv", sa=0.013, sb=0.021)
+        assert_same(got, oracle_out(oracle, acc, None, None, 0.013, 0.021, None, out), f"kn scalar {M, N, K}")
+
+
+@pytest.mark.parametrize("M,N,K", KN_SHAPES + [(16, 14336, 4096)])
+@pytest.mark.parametrize("nan_codes", [False, True])
+def test_gemv_kn_f8_tolerance(oracle, dev, M, N, K, nan_codes):
+    """FP8 decode with B [K,N] (the reference launcher's layout) on the
+    transposing kernel: fp32 sums in another order than the reference's
+    sequential loop, codes 0x7F / 0xFF counted as 0.0."""
+    say("gemv kn f8", M, N, K, nan_codes)
+    A, B, sa, sb = f8_inputs(oracle, M, N, K, 7500 + M + N + K, "kn", with_nan_codes=nan_codes)
+    bias = oracle.gen_f32_normal((N,), 7501 + N, 0.0, 0.02)
+    ref = oracle.f8_gemm(A, B, sa, sb, bias=bias, b_layout=oracle.B_KN, nthreads=NTH)
+    for out in ("f32", "bf16"):
+        got = gpu_f8(A, B, sa, sb, "kn", out, "gemv", bias=bias)
+        if out == "bf16":
+            got = oracle.bf16_to_f32(got)
+        assert_fp8_close(got, ref, out, f"kn {M, N, K} nan={nan_codes}")
+
+
+@pytest.mark.parametrize("M", [1, 7, 16])
+def test_fp8_dropin_launcher_decode(oracle, dev, M):
+    """The drop-in fke_launch_fp8_gemm_scaled (B [K,N], fp32 out, alpha =
+    sa*sb; src/quantized_gemm.cu:120-139) at decode shapes, against the
+    reference's own sequential loop."""
+    N, K = 2048, 4096
+    say("fp8 drop-in decode", M, N, K)
+    A, B, sa, sb = f8_inputs(oracle, M, N, K, 7600 + M, "kn", with_nan_codes=True)
+    ref = oracle.ref_kernel_gemm_f8(A, B, sa, sb)
+    C = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    st = _lib.lib().fke_launch_fp8_gemm_scaled(dev_t(A).data_ptr(), dev_t(B).data_ptr(), C.data_ptr(), sa, sb,
+                                               M, N, K, None)
+    _lib.check(st, "fke_launch_fp8_gemm_scaled")
+    torch.cuda.synchronize()
+    assert_fp8_close(C.cpu().numpy(), ref, "f32", f"drop-in M={M}")
+
+
 @pytest.mark.parametrize("M", [6, 9])
 def test_decode_weight_past_2gib(oracle, dev, M):
     """A 2.1 GB weight (N*K > 2^31): the skinny MFMA kernel's 32-bit offsets do
