@@ -13,7 +13,16 @@
 //
 //  * Workgroup = 64 consecutive columns (64-byte row segments of B) over the
 //    whole K; 4 waves split K: wave w takes the 128-row pieces w, w+4, ...
-//    Grid = ceil(N / 64) workgroups.
+//    Grid = ceil(N / 64) workgroups; the two 64-column halves of each
+//    128-byte line go to workgroups on one XCD.
+//  * Bound by its access pattern, not by consumption: the same copies with
+//    nothing consumed take as long (17 us at N = 14336, K = 4096).  Each CU
+//    streams strided row segments at a rate that grows with the segment
+//    width (64 / 128 / 256 / 512 bytes: 12 / 31 / 43 / 53 GB/s per CU), so
+//    only a K split across workgroups (wider segments and every CU busy)
+//    reaches the row-contiguous rate: copies of 512-byte segments in 8 K
+//    ranges ran 9.8 us.  That needs a cross-workgroup reduction of the
+//    partial sums, which this entry point (no workspace) cannot hold.
 //  * Item = one piece: 128 k rows x 64 bytes of B (8 KiB, eight 1-KiB
 //    buffer_load_dwordx4 ... lds copies of 16 rows each, four lanes per row)
 //    plus the matching 128 k bytes of the 16 activation rows (2 KiB, two
@@ -114,7 +123,16 @@ __global__ __launch_bounds__(256) void gemv_kn_kernel(GemmArgs p) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int M = p.M, N = p.N, K = p.K;
-    const int n0 = blockIdx.x * KN_W;
+    // Column block of this workgroup.  Workgroups are dispatched round robin
+    // over the 8 XCDs (b on XCD b % 8); blocks 2j and 2j+1, the two 64-byte
+    // halves of every 128-byte line of their rows, go to workgroups b and
+    // b + 8, which run at the same time on one XCD, so each line is fetched
+    // into that XCD's L2 once and both halves are used (23 -> 17 us at
+    // N = 14336, K = 4096; wider groups of blocks per XCD measured no better).
+    int blk = blockIdx.x;
+    const int G16 = static_cast<int>(gridDim.x) / 16 * 16;
+    if (blk < G16) blk = ((blk / 16) * 8 + (blk % 8)) * 2 + ((blk / 8) % 2);
+    const int n0 = blk * KN_W;
     const int P = (K + KN_ROWS - 1) / KN_ROWS;         // pieces along K
     const int np = wave < P ? (P - 1 - wave) / 4 + 1 : 0;  // pieces of this wave
 
