@@ -67,6 +67,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--preheat-ms", type=float, default=250.0,
                     help="wall time each GEMM configuration runs back to back before its counted warm-up")
+    ap.add_argument("--clock-ms", type=float, default=1100.0,
+                    help="wall time the headline GEMM keeps running after its timed steps for the clock readings "
+                         "(the metrics refresh once a second; 0 skips them)")
     ap.add_argument("--gemv-buffers", type=int, default=8)
     ap.add_argument("--gemv-launches", type=int, default=400)
     ap.add_argument("--extra", action="store_true", help="also time configs 2 and 4, decode M=4 and batched decode M=32,64,128")
@@ -139,14 +142,16 @@ def main():
             raise RuntimeError(f"fke_qgemm_i8 failed: {_lib.status_string(st)}")
 
     torch.cuda.synchronize()
-    clock = ClockSampler()
-    clock.start()
-    pre_n, pre_ms = preheat(torch, gemm, args.preheat_ms)
+    clock = ClockSampler() if args.clock_ms > 0 else None
+    if clock:
+        clock.start()
+    pre_n, pre_ms = preheat(torch, gemm, args.preheat_ms) if args.preheat_ms > 0 else (0, 0.0)
     t0 = time.perf_counter()
     ms = timed(gemm, args.steps, args.warmup)
     wall = time.perf_counter() - t0
-    preheat(torch, gemm, 1100.0)  # the same load a while longer: the metrics refresh once a second
-    sclk = clock.stop()
+    if clock:
+        preheat(torch, gemm, args.clock_ms)  # the same load a while longer: the metrics refresh once a second
+    sclk = clock.stop() if clock else {"value": None, "error": "not sampled (--clock-ms 0)"}
     ops_per = 2.0 * M * N * K
     tops = ops_per / (ms * 1e-3) / 1e12
     del C
