@@ -36,6 +36,8 @@
 // split and order is bit-exact.
 #include "fke_internal.h"
 
+#include <algorithm>
+
 namespace fke {
 namespace {
 
@@ -828,20 +830,21 @@ int cu_count() {
 
 // Workgroups of gemv_lds_kernel: one per CU, fewer when the rows run out
 // (at least 16 rows each), more when a share would exceed LK_RMAX rows.
+// (64-bit arithmetic: N may be anything up to INT32_MAX here.)
 int lds_grid(const GemmArgs& p) {
-    const int cus = cu_count();
-    const int no = p.swiglu ? p.N / 2 : p.N;
-    int g = min(cus, (no + 15) / 16);
+    const int64_t cus = cu_count();
+    const int64_t no = p.swiglu ? p.N / 2 : p.N;
+    int64_t g = std::min(cus, (no + 15) / 16);
     if ((no + g - 1) / g > LK_RMAX) g = (no + LK_RMAX - 1) / LK_RMAX;
-    return g;
+    return static_cast<int>(g);
 }
 
 template <int PIECE>
 bool lds_fits(const GemmArgs& p) {
     // offsets within one workgroup's activation rows (at most 64) and weight rows
     if (p.K < 4 * PIECE || static_cast<int64_t>(min(p.M, 64)) * p.K > INT32_MAX) return false;
-    const int no = p.swiglu ? p.N / 2 : p.N;
-    const int g = lds_grid(p);
+    const int64_t no = p.swiglu ? p.N / 2 : p.N;
+    const int64_t g = lds_grid(p);
     const int64_t r = (no + g - 1) / g;
     return r * p.K + PIECE <= INT32_MAX;
 }
@@ -951,12 +954,12 @@ hipError_t launch_rows_m(const GemmArgs& p, hipStream_t s) {
 bool gemv_i8_batch_pays(const GemmArgs& p) {
     if (p.M <= 16 || p.M > FKE_GEMV_MAX_M) return p.M <= 16;
     const double kib = p.K / 1024.0;
-    const int g = lds_grid(p), no = p.swiglu ? p.N / 2 : p.N;
+    const int64_t g = lds_grid(p), no = p.swiglu ? p.N / 2 : p.N;
     const double share = static_cast<double>((no + g - 1) / g) * (p.swiglu ? 2 : 1) * kib;
     const bool four = p.M > 32;
     const double chunk = (four ? 5.2 : 4.0) + (four ? 0.056 : 0.046) * share + (four ? 0.0078 : 0.004) * min(p.M, 64) * kib;
     const double t_lds = ((p.M + 63) / 64) * chunk;
-    const int64_t tiles = static_cast<int64_t>((p.M + 255) / 256) * ((p.N + 255) / 256);
+    const int64_t tiles = ((static_cast<int64_t>(p.M) + 255) / 256) * ((static_cast<int64_t>(p.N) + 255) / 256);
     const int64_t rounds = (tiles + cu_count() - 1) / cu_count();
     const double t_mfma = rounds * (p.K / 128.0 * 1.35 + 11.0);
     return t_lds < t_mfma;

@@ -101,8 +101,9 @@ uint8_t fko_f32_to_e4m3_sat(float x);
 float fko_quantize_e4m3(const float* x, uint8_t* q, size_t n);
 /* per-token INT8 activation quantiser (no reference counterpart; the step in
  * front of the W8A8 GEMM): per row m, amax = max|x| over non-NaN elements,
- * s = fp32(amax/127), r = fp32(127/amax) (both 1 when amax == 0),
- * q = clamp(rne(fp32(x*r)), -127, 127), NaN -> 0; scale[m] = s.
+ * s = fp32(amax/127), f = 2^64 if amax < 2^-64 else 1, r = fp32(127/(amax*f))
+ * (s = r = 1 when amax == 0), p = fp32(fp32(x*f)*r),
+ * q = NaN(p) ? 0 : clamp(rne(p), -127, 127); scale[m] = s.
  * x is fp32 (in_dtype 0) or bf16 bits (in_dtype 1), [M,K]. */
 void fko_quantize_rows_i8(const void* x, int in_dtype, int M, int K, int8_t* q, float* scale);
 
