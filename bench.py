@@ -22,7 +22,8 @@ to cover that.  The shader clock under the headline load is read through
 amdsmi and reported as "sclk_mhz" (with the socket power: this GEMM runs at
 the board's power limit, so the clock is the box-to-box variable).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--extra | --fp8 --swiglu --half --batch --shards] [--vendor] [--data-sweep] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--extra | --fp8 --swiglu --half --batch --shards
+       --decode-families] [--vendor] [--data-sweep] [--no-cpu] [--preheat-ms MS] [--clock-ms MS]
 """
 import argparse
 import json
@@ -78,6 +79,9 @@ def parse():
     ap.add_argument("--fp8", action="store_true", help="also time the FP8 e4m3 GEMM 8192^3 (part of --extra)")
     ap.add_argument("--batch", action="store_true",
                     help="also time batched decode M=32,64,128 on the decode weights (part of --extra)")
+    ap.add_argument("--decode-families", action="store_true",
+                    help="also time decode M=1,2,4,8,16 on the MFMA kernels the dispatcher picks and on the "
+                         "VALU dot-product kernels (FKE_PATH_GEMV_DOT), for the choice between them")
     ap.add_argument("--shards", action="store_true",
                     help="also time the per-GPU shards of 8-way tensor parallelism (part of --extra)")
     ap.add_argument("--data-sweep", action="store_true",
@@ -210,8 +214,10 @@ def main():
         del src, dst
     if args.extra:
         line["extra"] = extra_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args)
-    elif args.swiglu or args.half or args.fp8 or args.shards or args.batch:
+    elif args.swiglu or args.half or args.fp8 or args.shards or args.batch or args.decode_families:
         line["extra"] = {}
+        if args.decode_families:
+            line["extra"].update(decode_family_configs(torch, L, _lib, dev, gen, args))
         if args.batch:
             line["extra"].update(batch_configs(torch, L, _lib, dev, gen, args))
         if args.shards:
@@ -445,6 +451,34 @@ def eager_us(torch, dev, launch, launches):
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) * 1e3 / launches
+
+
+def decode_family_configs(torch, L, _lib, dev, gen, args, N=14336, K=4096):
+    """Decode on the C2 weights (N = 14336, K = 4096, bf16 out + bias, 8 rotating weights) on the
+    family the dispatcher picks (row kernel for M <= 2, LDS-streamed MFMA kernel above) and on the
+    VALU dot-product family (row kernel for M <= 4, split-K sdot kernel above), HIP-graph timed."""
+    res = {}
+    nbuf = args.gemv_buffers
+    Bs = [torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=gen) for _ in range(nbuf)]
+    sb = torch.rand(N, device=dev, generator=gen) * 0.019 + 0.001
+    bias = torch.randn(N, device=dev, generator=gen) * 0.02
+    for M in (1, 2, 4, 8, 16):
+        A = torch.clamp(torch.round(torch.randn((M, K), device=dev, generator=gen) * 30), -127, 127).to(torch.int8)
+        sa = torch.rand(M, device=dev, generator=gen) * 0.019 + 0.001
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        for name, path in (("auto", _lib.PATH_AUTO), ("dot", _lib.PATH_GEMV_DOT)):
+            def launch(i, st, path=path):
+                r = L.fke_qgemm_i8_on_path(path, A.data_ptr(), Bs[i % nbuf].data_ptr(), out.data_ptr(), M, N, K,
+                                           sa.data_ptr(), sb.data_ptr(), 1.0, 1.0, bias.data_ptr(), _lib.OUT_BF16,
+                                           _lib.B_NK, st)
+                if r:
+                    raise RuntimeError(f"decode failed: {_lib.status_string(r)}")
+            us = graph_us(torch, dev, launch, args.gemv_launches, 2 * nbuf)
+            nbytes = gemv_bytes(M, N, K)
+            res[f"decode_M{M}_{name}"] = {"us": round(us, 3), "GB/s": round(nbytes / us / 1e3, 1),
+                                          "frac": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4)}
+    del Bs
+    return res
 
 
 def gemv_bench(torch, L, _lib, dev, gen, M, nbuf, launches, N=14336, K=4096, layout="nk"):

@@ -154,6 +154,9 @@ int run_i8(int path, const GemmArgs& p, void* stream) {
             if (!fke::mfma_supports(p, fke::ELEM_I8)) return hipErrorInvalidValue;
             return fke::launch_mfma(p, fke::ELEM_I8, s);
         case FKE_PATH_GENERIC: return fke::launch_generic(p, fke::ELEM_I8, s);
+        case FKE_PATH_GEMV_DOT:
+            if (!fke::gemv_dot_supports(p)) return hipErrorInvalidValue;
+            return fke::launch_gemv_dot(p, s);
         default: return hipErrorInvalidValue;
     }
 }

@@ -51,6 +51,9 @@ bool gemv_i8_batch_pays(const GemmArgs& p);  // M > 16: the decode family beats 
 bool gemv_f8_supports(const GemmArgs& p);
 hipError_t launch_gemv_f8(const GemmArgs& p, hipStream_t stream);
 bool mfma_supports(const GemmArgs& p, int elem);
+// The VALU dot-product decode kernels (no MFMA), M <= 16, INT8, B [N,K].
+bool gemv_dot_supports(const GemmArgs& p);
+hipError_t launch_gemv_dot(const GemmArgs& p, hipStream_t stream);
 // Decode (M <= 16) with B stored [K,N], INT8 or FP8 (gemv_kn.hip).
 bool gemv_kn_supports(const GemmArgs& p, int elem);
 hipError_t launch_gemv_kn(const GemmArgs& p, int elem, hipStream_t stream);

@@ -978,6 +978,25 @@ bool gemv_i8_supports(const GemmArgs& p) {
 }
 
 
+// The VALU dot-product decode kernels alone, with no MFMA: the row kernel
+// (v_dot4 + DPP / ds_swizzle wave reduction) for M <= 4 and the split-K sdot
+// kernel (LDS + group reduction) for 5 <= M <= 16.  The dispatcher prefers the
+// MFMA kernels from M = 3 by measurement; this family stays selectable
+// (FKE_PATH_GEMV_DOT) to cross-check and to measure that choice.
+bool gemv_dot_supports(const GemmArgs& p) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p.A), b = reinterpret_cast<uintptr_t>(p.B);
+    if (!(p.M >= 1 && p.M <= 16 && p.N >= 1 && p.K >= 64 && p.K % 64 == 0 && p.b_layout == FKE_B_NK &&
+          ((a | b) & 15) == 0))
+        return false;
+    return !p.swiglu || p.M <= 4;
+}
+
+hipError_t launch_gemv_dot(const GemmArgs& p, hipStream_t s) {
+    if (p.M <= 4) return p.K % 4096 == 0 ? launch_rows_m<true>(p, s) : launch_rows_m<false>(p, s);
+    if (p.M <= 8) return launch_t<8, 8>(p, s);
+    return launch_t<16, 4>(p, s);
+}
+
 hipError_t launch_gemv_i8(const GemmArgs& p, hipStream_t s) {
     // M >= 3 with K >= 4 KiB: the LDS-streamed kernel (11.4-11.8 us at
     // N = 14336, K = 4096 for every M in 3..16, against 12.5-18.1 us for the

@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(_PKG, "lib", "libfke_qgemm.so")
 # enum values of include/fke_qgemm.h
 OUT_F32, OUT_BF16, OUT_I32 = 0, 1, 2
 B_NK, B_KN = 0, 1
-PATH_AUTO, PATH_GEMV, PATH_MFMA, PATH_GENERIC = 0, 1, 2, 3
+PATH_AUTO, PATH_GEMV, PATH_MFMA, PATH_GENERIC, PATH_GEMV_DOT = 0, 1, 2, 3, 4
 IN_F32, IN_BF16, IN_F16 = 0, 1, 2
 HIP_SUCCESS, HIP_ERROR_INVALID_VALUE = 0, 1
 W8A8_NOALLOC_SCRATCH_BYTES = 32 << 20  # FKE_W8A8_NOALLOC_SCRATCH_BYTES

@@ -52,7 +52,9 @@ enum fke_path {
     FKE_PATH_AUTO = 0,    /* dispatcher's choice                                */
     FKE_PATH_GEMV = 1,    /* decode family, M<=512 (INT8, NK): weight streamed  */
     FKE_PATH_MFMA = 2,    /* LDS-staged MFMA GEMM (INT8 i32 / FP8 f32 acc)      */
-    FKE_PATH_GENERIC = 3  /* any-shape tiled fallback (exact reference order)   */
+    FKE_PATH_GENERIC = 3, /* any-shape tiled fallback (exact reference order)   */
+    FKE_PATH_GEMV_DOT = 4 /* decode, VALU dot products only (no MFMA): INT8,    */
+                          /* B [N,K], M <= 16, K % 64 == 0 (fke_qgemm_i8*_on_path) */
 };
 
 /*

@@ -194,6 +194,15 @@ def test_path_unavailable_for_shape_is_rejected():
                                   0, 0, None) == INVALID
     assert L.fke_qgemm_i8_on_path(_lib.PATH_GEMV, P, P, P, 513, 64, 4096, None, None, 1.0, 1.0, None,
                                   0, 0, None) == INVALID
+    # the dot-product decode family: INT8, B [N,K], M <= 16, K % 64 == 0
+    assert L.fke_qgemm_i8_on_path(_lib.PATH_GEMV_DOT, P, P, P, 17, 64, 4096, None, None, 1.0, 1.0, None,
+                                  0, 0, None) == INVALID
+    assert L.fke_qgemm_i8_on_path(_lib.PATH_GEMV_DOT, P, P, P, 4, 64, 4096, None, None, 1.0, 1.0, None,
+                                  0, 1, None) == INVALID
+    assert L.fke_qgemm_i8_on_path(_lib.PATH_GEMV_DOT, P, P, P, 4, 64, 4000, None, None, 1.0, 1.0, None,
+                                  0, 0, None) == INVALID
+    assert L.fke_qgemm_i8_swiglu_on_path(_lib.PATH_GEMV_DOT, P, P, P, 5, 64, 4096, None, None, 1.0, 1.0, None,
+                                         1, None) == INVALID
     # GEMV with B [K,N]: M <= 16, N % 16 == 0, K % 64 == 0
     assert L.fke_qgemm_i8_on_path(_lib.PATH_GEMV, P, P, P, 17, 64, 4096, None, None, 1.0, 1.0, None,
                                   0, 1, None) == INVALID

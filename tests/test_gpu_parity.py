@@ -352,6 +352,21 @@ def test_fp8_dropin_launcher_decode(oracle, dev, M):
     assert_fp8_close(C.cpu().numpy(), ref, "f32", f"drop-in M={M}")
 
 
+@pytest.mark.parametrize("M", list(range(1, 17)))
+def test_gemv_dot_family_bit_exact(oracle, dev, M):
+    """The VALU dot-product decode kernels (row kernel for M <= 4, split-K sdot
+    kernel above; FKE_PATH_GEMV_DOT) at every M up to 16: bit-exact, and equal
+    to the dispatcher's (MFMA) choice."""
+    N, K = 1000, 4096
+    say("gemv dot family", M, N, K)
+    A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 7800 + M, act="normal")
+    acc = oracle.w8a8_acc(A, B, nthreads=NTH)
+    got = gpu_i8(A, B, "nk", "bf16", "gemv_dot", sa, sb, bias=bias)
+    assert_same(got, oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, "bf16"), f"dot M={M}")
+    assert_same(gpu_i8(A, B, "nk", "i32", "gemv_dot"), acc, f"dot i32 M={M}")
+    assert_same(got, gpu_i8(A, B, "nk", "bf16", "auto", sa, sb, bias=bias), f"dot vs auto M={M}")
+
+
 @pytest.mark.parametrize("M", [6, 9])
 def test_decode_weight_past_2gib(oracle, dev, M):
     """A 2.1 GB weight (N*K > 2^31): the skinny MFMA kernel's 32-bit offsets do
