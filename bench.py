@@ -505,7 +505,7 @@ def gemv_bench(torch, L, _lib, dev, gen, M, nbuf, launches, N=14336, K=4096, lay
     eager = eager_us(torch, dev, launch, launches)
     nbytes = gemv_bytes(M, N, K)
     gbs = nbytes / (us * 1e-6) / 1e9
-    kernel = gemv_kernel(M) if layout == "nk" else "gemv_kn_kernel<i8,bf16>"
+    kernel = gemv_kernel(M) if layout == "nk" else "gemv_kn_split_kernel<i8>+kn_reduce_kernel<i8,bf16>"
     return {"metric": f"HBM GB/s, decode GEMV M={M} N={N} K={K}, B {'[N,K]' if layout == 'nk' else '[K,N]'} "
                       f"(bf16 out, fused bias)",
             "value": round(gbs, 1), "unit": "GB/s", "us_per_launch": round(us, 3),
@@ -671,7 +671,7 @@ def fp8_configs(torch, L, _lib, dev, gen, timed, args):
         Bs.append(b)
     bias = torch.randn(N, device=dev, generator=gen) * 0.02
     # the same bytes read as B [K,N] (the reference launcher's layout) run the transposing decode kernel
-    for lname, lay, kname in (("", _lib.B_NK, "gemv_lds_kernel (FP8)"), ("_Bkn", _lib.B_KN, "gemv_kn_kernel<f8>")):
+    for lname, lay, kname in (("", _lib.B_NK, "gemv_lds_kernel (FP8)"), ("_Bkn", _lib.B_KN, "gemv_kn_split_kernel<f8>+kn_reduce_kernel<f8>")):
         for M in (1, 16):
             A8 = torch.randint(0, 256, (M, K), dtype=torch.uint8, device=dev, generator=gen)
             A8[(A8 & 0x7F) == 0x7F] = 0

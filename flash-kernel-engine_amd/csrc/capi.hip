@@ -7,9 +7,12 @@
 // call's hipLaunchKernel (the reference returned cudaGetLastError() after its
 // launch, src/quantized_gemm.cu:74,138, which could also surface an earlier
 // sticky error).  No state is kept between calls, apart from the device
-// scratch of fke_w8a8_linear_noalloc (and its per-device address, set once).
+// scratch of fke_w8a8_linear_noalloc (and its per-device address, set once)
+// and the per-stream workspaces of the [K,N] decode's K splits (below).
 #include <cstdio>
 #include <mutex>
+#include <utility>
+#include <vector>
 
 #include "fke_internal.h"
 
@@ -43,7 +46,62 @@ hipError_t scratch_of_device(int dev, void** out) {
 
 using fke::GemmArgs;
 
-int run_i8(int path, const GemmArgs& p, void* stream);
+// Workspaces of the [K,N] decode's K splits (the partial sums its second
+// kernel adds), one per (device, stream): calls on one stream run in order,
+// so they can share one; calls on different streams never do.  Allocated the
+// first time a stream needs one and then held until the process ends.  A
+// stream that is being captured into a graph gets no new allocation: it uses
+// what it already has, and the decode runs with fewer splits (or unsplit)
+// when that is too small or absent.  A workspace outgrown by a larger shape
+// is replaced, and the old one kept (a launch queued on it may not have run
+// yet).
+struct KnWorkspace {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+constexpr size_t kKnWsMinBytes = size_t{8} << 20;  // covers M = 16 at N = 14336 (7.3 MiB)
+constexpr size_t kKnWsMaxStreams = 64;              // beyond this many streams: unsplit
+std::mutex g_kn_mu;
+std::vector<std::pair<std::pair<int, hipStream_t>, KnWorkspace>> g_kn_ws;
+std::vector<void*> g_kn_retired;
+
+KnWorkspace kn_workspace(hipStream_t s, size_t need) {
+    if (need == 0) return {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return {};
+    if (s) {  // the workspace must live on the stream's device, which must be current
+        hipDevice_t sdev = 0;
+        if (hipStreamGetDevice(s, &sdev) != hipSuccess || sdev != dev) return {};
+    }
+    std::lock_guard<std::mutex> lock(g_kn_mu);
+    KnWorkspace* have = nullptr;
+    for (auto& e : g_kn_ws)
+        if (e.first.first == dev && e.first.second == s) have = &e.second;
+    if (have && have->bytes >= need) return *have;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+        return have ? *have : KnWorkspace{};
+    if (!have && g_kn_ws.size() >= kKnWsMaxStreams) return {};
+    KnWorkspace ws;
+    ws.bytes = need > kKnWsMinBytes ? need : kKnWsMinBytes;
+    if (hipMalloc(&ws.ptr, ws.bytes) != hipSuccess) return have ? *have : KnWorkspace{};
+    if (have) {
+        g_kn_retired.push_back(have->ptr);
+        *have = ws;
+    } else {
+        g_kn_ws.push_back({{dev, s}, ws});
+    }
+    return ws;
+}
+
+// The [K,N] decode on the caller's workspace (`given`), or else on the
+// stream's own.
+hipError_t run_kn(const GemmArgs& p, int elem, hipStream_t s, const KnWorkspace* given) {
+    const KnWorkspace ws = given ? *given : kn_workspace(s, fke::gemv_kn_workspace_bytes(p));
+    return fke::launch_gemv_kn(p, elem, fke::gemv_kn_plan(p, ws.ptr, ws.bytes), s);
+}
+
+int run_i8(int path, const GemmArgs& p, void* stream, const KnWorkspace* ws = nullptr);
 
 bool common_args_ok(const void* A, const void* B, const void* C, int M, int N, int K,
                     int b_layout) {
@@ -142,12 +200,12 @@ int pick_f8(const GemmArgs& p) {
     return FKE_PATH_GENERIC;
 }
 
-int run_i8(int path, const GemmArgs& p, void* stream) {
+int run_i8(int path, const GemmArgs& p, void* stream, const KnWorkspace* ws) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (path == FKE_PATH_AUTO) path = pick_i8(p);
     switch (path) {
         case FKE_PATH_GEMV:
-            if (fke::gemv_kn_supports(p, fke::ELEM_I8)) return fke::launch_gemv_kn(p, fke::ELEM_I8, s);
+            if (fke::gemv_kn_supports(p, fke::ELEM_I8)) return run_kn(p, fke::ELEM_I8, s, ws);
             if (!fke::gemv_i8_supports(p)) return hipErrorInvalidValue;
             return fke::launch_gemv_i8(p, s);
         case FKE_PATH_MFMA:
@@ -186,12 +244,12 @@ int run_half(int path, const GemmArgs& p, int elem, void* stream) {
     }
 }
 
-int run_f8(int path, const GemmArgs& p, void* stream) {
+int run_f8(int path, const GemmArgs& p, void* stream, const KnWorkspace* ws = nullptr) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (path == FKE_PATH_AUTO) path = pick_f8(p);
     switch (path) {
         case FKE_PATH_GEMV:
-            if (fke::gemv_kn_supports(p, fke::ELEM_F8)) return fke::launch_gemv_kn(p, fke::ELEM_F8, s);
+            if (fke::gemv_kn_supports(p, fke::ELEM_F8)) return run_kn(p, fke::ELEM_F8, s, ws);
             if (!fke::gemv_f8_supports(p)) return hipErrorInvalidValue;
             return fke::launch_gemv_f8(p, s);
         case FKE_PATH_MFMA:
@@ -233,6 +291,37 @@ int fke_qgemm_f8(const uint8_t* A, const uint8_t* B, void* C, int M, int N, int 
                  const float* bias, int out_dtype, int b_layout, void* stream) {
     return fke_qgemm_f8_on_path(FKE_PATH_AUTO, A, B, C, M, N, K, sa, sb, bias, out_dtype, b_layout,
                                 stream);
+}
+
+size_t fke_qgemm_workspace_size(int M, int N, int K, int b_layout) {
+    if (M < 1 || N < 1 || K < 1 || (b_layout != FKE_B_NK && b_layout != FKE_B_KN)) return 0;
+    // alignment-independent: the decode's shape rules with aligned stand-in pointers
+    const void* a = reinterpret_cast<const void*>(uintptr_t{4096});
+    const GemmArgs p = make_args(a, a, const_cast<void*>(a), M, N, K, nullptr, nullptr, 1.f, 1.f, nullptr, FKE_OUT_F32,
+                                 b_layout);
+    return fke::gemv_kn_supports(p, fke::ELEM_I8) ? fke::gemv_kn_workspace_bytes(p) : 0;
+}
+
+int fke_qgemm_i8_ws(const int8_t* A, const int8_t* B, void* C, int M, int N, int K, const float* scale_a,
+                    const float* scale_b, float sa, float sb, const float* bias, int out_dtype, int b_layout,
+                    void* workspace, size_t workspace_bytes, void* stream) {
+    if (!i8_args_ok(A, B, C, M, N, K, out_dtype, b_layout)) return hipErrorInvalidValue;
+    KnWorkspace ws;
+    ws.ptr = workspace;
+    ws.bytes = workspace ? workspace_bytes : 0;
+    return run_i8(FKE_PATH_AUTO, make_args(A, B, C, M, N, K, scale_a, scale_b, sa, sb, bias, out_dtype, b_layout),
+                  stream, &ws);
+}
+
+int fke_qgemm_f8_ws(const uint8_t* A, const uint8_t* B, void* C, int M, int N, int K, float sa, float sb,
+                    const float* bias, int out_dtype, int b_layout, void* workspace, size_t workspace_bytes,
+                    void* stream) {
+    if (!f8_args_ok(A, B, C, M, N, K, out_dtype, b_layout)) return hipErrorInvalidValue;
+    KnWorkspace ws;
+    ws.ptr = workspace;
+    ws.bytes = workspace ? workspace_bytes : 0;
+    return run_f8(FKE_PATH_AUTO, make_args(A, B, C, M, N, K, nullptr, nullptr, sa, sb, bias, out_dtype, b_layout),
+                  stream, &ws);
 }
 
 int fke_qgemm_i8_swiglu_on_path(int path, const int8_t* A, const int8_t* W, void* H, int M, int I, int K,

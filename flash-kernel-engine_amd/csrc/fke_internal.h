@@ -54,9 +54,19 @@ bool mfma_supports(const GemmArgs& p, int elem);
 // The VALU dot-product decode kernels (no MFMA), M <= 16, INT8, B [N,K].
 bool gemv_dot_supports(const GemmArgs& p);
 hipError_t launch_gemv_dot(const GemmArgs& p, hipStream_t stream);
-// Decode (M <= 16) with B stored [K,N], INT8 or FP8 (gemv_kn.hip).
+// Decode (M <= 16) with B stored [K,N], INT8 or FP8 (gemv_kn.hip): with a
+// workspace for partial sums, S K splits of 512-column workgroups and a
+// second kernel that adds the splits; without one (S = 1), one workgroup per
+// 64-column block over all of K.
+struct KnSplit {
+    int S;       // K splits (1: no workspace)
+    int PS;      // 128-row pieces per split
+    void* part;  // [ceil(N/128)][S][M][128] partial sums (int32 / fp32)
+};
 bool gemv_kn_supports(const GemmArgs& p, int elem);
-hipError_t launch_gemv_kn(const GemmArgs& p, int elem, hipStream_t stream);
+size_t gemv_kn_workspace_bytes(const GemmArgs& p);  // 0: runs unsplit
+KnSplit gemv_kn_plan(const GemmArgs& p, void* ws, size_t ws_bytes);
+hipError_t launch_gemv_kn(const GemmArgs& p, int elem, const KnSplit& sp, hipStream_t stream);
 
 // ---------------------------------------------------------------------------
 // Device helpers

@@ -7,50 +7,40 @@
 //
 // HBM-bound: the weight panel is streamed once.  In [K,N] order a weight row
 // is one k and an output column is a byte column, so the k bytes an MFMA
-// lane needs for one column are N bytes apart in memory.  The kernel copies
-// the panel into LDS as it lies and lets the LDS transpose it:
+// lane needs for one column are N bytes apart in memory.  The kernels copy
+// the panel into LDS as it lies and let the LDS transpose it:
 // ds_read_b64_tr_b8 gives each lane 8 consecutive k bytes of one column.
+// INT8 runs v_mfma_i32_16x16x64_i8 (two k steps per 128-row item); FP8
+// v_mfma_scale_f32_16x16x128_f8f6f4 (one step), its fragments cleared of the
+// 0x7F / 0xFF codes on the VALU (the MFMA reads them as NaN).
 //
-//  * Workgroup = 64 consecutive columns (64-byte row segments of B) over the
-//    whole K; 4 waves split K: wave w takes the 128-row pieces w, w+4, ...
-//    Grid = ceil(N / 64) workgroups; the two 64-column halves of each
-//    128-byte line go to workgroups on one XCD.
-//  * Bound by its access pattern, not by consumption: the same copies with
-//    nothing consumed take as long (17 us at N = 14336, K = 4096).  Each CU
-//    streams strided row segments at a rate that grows with the segment
-//    width (64 / 128 / 256 / 512 bytes: 12 / 31 / 43 / 53 GB/s per CU), so
-//    only a K split across workgroups (wider segments and every CU busy)
-//    reaches the row-contiguous rate: copies of 512-byte segments in 8 K
-//    ranges ran 9.8 us.  That needs a cross-workgroup reduction of the
-//    partial sums, which this entry point (no workspace) cannot hold.
-//  * Item = one piece: 128 k rows x 64 bytes of B (8 KiB, eight 1-KiB
-//    buffer_load_dwordx4 ... lds copies of 16 rows each, four lanes per row)
-//    plus the matching 128 k bytes of the 16 activation rows (2 KiB, two
-//    copies; rows >= M and bytes >= K read as zero).  Each wave keeps NS
-//    items in flight in its own ring slots.
-//  * A landed item is read with ds_read_b128 (activations, in MFMA operand
-//    order) and ds_read_b64_tr_b8 (weights): within each 16-lane group, lane
-//    8h+i receives byte i of the 8 bytes addressed by lanes 2b+h (b = 0..7)
-//    as its byte b, so lanes 2b+h addressing row k0+b at column c0+8h hand
-//    lane j column c0+j with its k bytes in order - the MFMA's B operand.
-//    INT8: v_mfma_i32_16x16x64_i8, two k steps per item; FP8:
-//    v_mfma_scale_f32_16x16x128_f8f6f4, one step, fragments cleared of the
-//    0x7F / 0xFF codes on the VALU (the MFMA reads them as NaN).
-//  * The four waves' partial sums meet in LDS in the fixed order w = 0..3
-//    (exact for INT8, deterministic for FP8), then the workgroup applies the
-//    epilogue and stores 64 consecutive columns per activation row.
+// A CU streams strided row segments at a rate that grows with the segment
+// width, and the chip needs most CUs streaming, so the panel is cut along K
+// as well as N when a workspace holds the partial sums:
 //
-// LDS layouts (16-byte chunks, swizzled so that the 16-lane groups of one
-// read instruction touch distinct banks whether the LDS serves 128 or 256
-// bytes per cycle):
-//  * weights: item row r (64 bytes, four chunks) keeps logical chunk c at
-//    physical chunk c ^ kn_swz(r);
-//  * activations: row m (128 bytes, eight chunks) keeps chunk c at
-//    c ^ (m & 7) ^ ((m >> 3) & 1).
-// The reads are inline ds_read instructions with lgkmcnt waits tied to their
-// registers: the compiler cannot tell which ring slot an LDS-DMA copy
-// writes, and before an LDS read it can see it would wait for every copy in
-// flight.
+//  * Split kernel (gemv_kn_split_kernel + kn_reduce_kernel).  Workgroup =
+//    512 consecutive columns x one of S K ranges (grid ceil(N/512) x S, S <=
+//    8: 224 workgroups at N = 14336, K = 4096); wave w streams the 128-column
+//    block 4*blockIdx/S + w over the range, so the workgroup reads 512
+//    contiguous bytes of every row it touches.  Each wave writes its block's
+//    partial sums ([M][128], int32 / fp32) to the workspace; a second kernel
+//    adds the S partials of each output in the fixed order s = 0..S-1 (exact
+//    for INT8, deterministic for FP8) and applies the epilogue.  Summing in
+//    the same kernel (the last split to arrive, counted by an atomic) cost
+//    ~8 us more at that shape: its store / count / load round trips queue
+//    behind the other workgroups' streams, where the second kernel's run
+//    after them (13.2 against 19 us for M = 1).
+//  * Full kernel (gemv_kn_full_kernel), when there is no workspace or K is
+//    too short to split: one workgroup per 64-column block over all of K,
+//    blocks 2j and 2j+1 (the two halves of each 128-byte line) on one XCD.
+//
+// Item = 128 k rows x the block's bytes of B plus the matching 128 k bytes
+// of the 16 activation rows (rows >= M and bytes >= K read as zero), copied
+// by buffer_load_dwordx4 ... lds; each wave keeps its items in flight in its
+// own ring slots.  The reads are inline ds_read instructions with lgkmcnt
+// waits tied to their registers: the compiler cannot tell which ring slot an
+// LDS-DMA copy writes, and before an LDS read it can see it would wait for
+// every copy in flight.
 #include "fke_internal.h"
 
 #include <type_traits>
@@ -64,29 +54,311 @@ typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
-constexpr int KN_W = 64;                 // columns (bytes of a B row) per workgroup
-constexpr int KN_ROWS = 128;             // k rows per item
-constexpr int KN_BI = KN_ROWS * KN_W;    // weight bytes per item (8 KiB)
-constexpr int KN_AI = 16 * KN_ROWS;      // activation bytes per item (2 KiB)
-constexpr int KN_ITEM = KN_BI + KN_AI;   // 10 KiB
-constexpr int KN_DB = KN_BI / 1024;      // weight copies per item
-constexpr int KN_DA = KN_AI / 1024;      // activation copies per item
-constexpr int KN_DI = KN_DB + KN_DA;     // copies per item
-constexpr int KN_NS = 3;                 // ring slots per wave (120 KiB of LDS per workgroup)
+// ===========================================================================
+// Split kernel: 128 columns per wave, four waves (512 columns) per workgroup.
+// ===========================================================================
+constexpr int KS_W = 128;                // columns (bytes of a B row) per wave
+constexpr int KS_CB = KS_W / 16;         // 16-column MFMA blocks per wave
+constexpr int KS_ROWS = 128;             // k rows per item
+constexpr int KS_BI = KS_ROWS * KS_W;    // weight bytes per item (16 KiB)
+constexpr int KS_AI = 16 * KS_ROWS;      // activation bytes per item (2 KiB)
+constexpr int KS_ITEM = KS_BI + KS_AI;   // 18 KiB
+constexpr int KS_DB = KS_BI / 1024;      // weight copies per item
+constexpr int KS_DA = KS_AI / 1024;      // activation copies per item
+constexpr int KS_DI = KS_DB + KS_DA;     // copies per item
+constexpr int KS_NS = 2;                 // ring slots per wave (144 KiB of LDS per workgroup)
+constexpr int KS_SMAX = 8;               // K splits at most
+
+// LDS layouts (16-byte chunks, swizzled so that every 16-lane group of a read
+// touches 32 distinct banks and every 32-lane half 64, whether the LDS serves
+// 128 or 256 bytes per cycle):
+//  * weights: item row r (128 bytes, eight chunks) keeps logical chunk c at
+//    physical chunk c ^ ks_swz(r): bits 0..2 of r spread the eight rows a
+//    16-lane group reads over eight chunks; bits 4 and 5 flip it between the
+//    two 16-lane groups of a half wave (rows 16 apart for INT8, 32 apart for
+//    FP8), whose rows share bit 0 and would otherwise meet mod 256 bytes;
+//  * activations: row m (128 bytes) keeps chunk c at c ^ ks_aswz(m).
+__device__ __forceinline__ int ks_swz(int r) { return (r & 7) ^ ((r >> 4) & 1) ^ ((r >> 5) & 1); }
+__device__ __forceinline__ int ks_aswz(int m) { return (m & 7) ^ ((m >> 3) & 1); }
+
+__device__ __forceinline__ v4i ks_rd128(const lds_u8* a) {
+    v4i r;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(a));
+    return r;
+}
+template <int OFF>
+__device__ __forceinline__ v2i ks_rdtr(const lds_u8* a) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset is 16 bits");
+    v2i r;
+    asm volatile("ds_read_b64_tr_b8 %0, %1 offset:%2" : "=v"(r) : "v"(a), "i"(OFF));
+    return r;
+}
+// Every LDS read has landed; the registers they wrote are tied to the wait,
+// so nothing reads (or copies) them before it.
+__device__ __forceinline__ void ks_lgkm_wait_all(v4i (&a)[2], v2i (&t)[32]) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    asm volatile("" : "+v"(a[0]), "+v"(a[1]));
+#pragma unroll
+    for (int i = 0; i < 32; ++i) asm volatile("" : "+v"(t[i]));
+}
+// s_waitcnt vmcnt(KS_DI * n): every copy but those of the n latest items has landed.
+__device__ __forceinline__ void ks_wait_items(int n) {
+    static_assert(KS_DI == 18 && KS_NS == 2, "vmcnt steps below: 18 copies, at most one later item");
+    if (n == 0) wait_vm<0>();
+    else wait_vm<18>();
+}
+
+// Weight read of item fragment X (compile-time), at an immediate offset from
+// the lane's column-block address wadr[]:
+//  INT8: X = 16s + 2cb + t -> rows 64s + 16G + 8t + b of block cb;
+//  FP8:  X = 4cb + t       -> rows 32G + 8t + b of block cb (the swizzle
+//        flips bit 0 of the chunk for t >= 2, i.e. block cb ^ 1's address).
+// At most 14 LDS reads are in flight when one is issued (lgkmcnt is 4 bits;
+// the two activation reads come first).
+template <bool F8, int X>
+__device__ __forceinline__ void ks_read_w(const lds_u8* slot, const uint32_t (&wadr)[KS_CB], v2i (&tr)[32]) {
+    if constexpr (X < 32) {
+        if constexpr (X + 2 >= 14) asm volatile("s_waitcnt lgkmcnt(13)" ::: "memory");
+        if constexpr (F8) {
+            constexpr int cb = X >> 2, t = X & 3;
+            tr[X] = ks_rdtr<8 * t * KS_W>(slot + wadr[t >= 2 ? (cb ^ 1) : cb]);
+        } else {
+            constexpr int s = X >> 4, cb = (X >> 1) & 7, t = X & 1;
+            tr[X] = ks_rdtr<(64 * s + 8 * t) * KS_W>(slot + wadr[cb]);
+        }
+        ks_read_w<F8, X + 1>(slot, wadr, tr);
+    }
+}
+
+// Wave w of workgroup b streams column block 4*(b/S) + w (128 columns) over
+// the 128-row pieces [s*PS, min(P, (s+1)*PS)) of split s = b % S and writes
+// its sums to part[block][s][m][column] for m < M.
+template <int EL>
+__global__ __launch_bounds__(256) void gemv_kn_split_kernel(GemmArgs p, KnSplit sp) {
+    constexpr bool F8 = EL == ELEM_F8;
+    using AccV = typename std::conditional<F8, v4f, v4i>::type;
+    using AccE = typename std::conditional<F8, float, int32_t>::type;
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[KS_NS][4][KS_ITEM];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int M = p.M, N = p.N, K = p.K;
+    const int S = sp.S;
+    const int split = static_cast<int>(blockIdx.x) % S;
+    const int cbg = 4 * (static_cast<int>(blockIdx.x) / S) + wave;  // this wave's column block
+    const int n0 = cbg * KS_W;
+    if (n0 >= N) return;  // no barrier below: the other waves go on alone
+    const int P = (K + KS_ROWS - 1) / KS_ROWS;
+    const int pb = split * sp.PS, np = min(P, pb + sp.PS) - pb;
+
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.B, K * N);
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, M * K);
+    lds_u8* const lring = (lds_u8*)(&ring[0][wave][0]);  // slot q at + q * SLOT
+    constexpr int SLOT = 4 * KS_ITEM;
+
+    // Copy geometry.  Weights, copy d: item row i = 8d + l/8 at physical
+    // chunk l%8, holding logical chunk (l%8) ^ ks_swz(i); ks_swz(i) is
+    // (l/8) ^ f(d) with f(d) = bit 1 ^ bit 2 of d, so two lane offsets serve
+    // all sixteen copies.  Activations, copy d: row m = 8d + l/8, physical
+    // chunk l%8 holding logical chunk (l%8) ^ ks_aswz(m).
+    const int lr = lane >> 3, lc = lane & 7;
+    const uint32_t bbase0 = static_cast<uint32_t>(lr * N + n0 + 16 * (lc ^ lr));
+    const uint32_t bbase1 = static_cast<uint32_t>(lr * N + n0 + 16 * (lc ^ lr ^ 1));
+    uint32_t aoff[KS_DA];
+    int akb[KS_DA];
+    bool arow[KS_DA];
+#pragma unroll
+    for (int d = 0; d < KS_DA; ++d) {
+        const int m = 8 * d + lr;
+        const int c = lc ^ ks_aswz(m);
+        arow[d] = m < M;
+        akb[d] = 16 * c;
+        aoff[d] = static_cast<uint32_t>(m * K + 16 * c);
+    }
+    auto issue = [&](int j, lds_u8* dst) __attribute__((always_inline)) {
+        const int k0 = (pb + j) * KS_ROWS;
+#pragma unroll
+        for (int d = 0; d < KS_DB; ++d) {
+            const uint32_t base = (((d >> 1) ^ (d >> 2)) & 1) ? bbase1 : bbase0;
+            const uint32_t off = k0 + 8 * d < K ? base + static_cast<uint32_t>((k0 + 8 * d) * N) : 0x80000000u;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, dst + d * 1024, 16, static_cast<int>(off), 0, 0, 2);
+        }
+#pragma unroll
+        for (int d = 0; d < KS_DA; ++d) {
+            const uint32_t off = arow[d] && k0 + akb[d] < K ? aoff[d] + static_cast<uint32_t>(k0) : 0x80000000u;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, dst + KS_BI + d * 1024, 16, static_cast<int>(off), 0, 0, 0);
+        }
+    };
+
+    // Read geometry.  Lane l = 16G + 2b + h addresses item row R0 + b at
+    // column block cb's 8-byte half h; R0 = 16G (INT8) / 32G (FP8) plus the
+    // read's immediate rows, which leave the row's swizzle unchanged.
+    // Activation reads: row m = l % 16, logical chunk (INT8) 4s + G for step
+    // s, (FP8) 2G + e for half e.
+    const int G = lane >> 4, b8 = (lane & 15) >> 1, hh = lane & 1;
+    uint32_t wadr[KS_CB];
+#pragma unroll
+    for (int cb = 0; cb < KS_CB; ++cb) {
+        const int r = (F8 ? 32 : 16) * G + b8;
+        wadr[cb] = static_cast<uint32_t>(r * KS_W + 16 * (cb ^ ks_swz(r)) + 8 * hh);
+    }
+    const int am = lane & 15;
+    uint32_t aadr[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const int c = F8 ? 2 * G + e : 4 * e + G;
+        aadr[e] = static_cast<uint32_t>(KS_BI + am * KS_ROWS + 16 * (c ^ ks_aswz(am)));
+    }
+
+    AccV acc[KS_CB];
+#pragma unroll
+    for (int cb = 0; cb < KS_CB; ++cb) acc[cb] = AccV{0, 0, 0, 0};
+
+    int issued = 0;
+#pragma unroll
+    for (int q = 0; q < KS_NS; ++q)
+        if (issued < np) {
+            issue(issued, lring + q * SLOT);
+            ++issued;
+        }
+    for (int c = 0; c < np; ++c) {
+        lds_u8* const slot = lring + (c % KS_NS) * SLOT;
+        ks_wait_items(issued - c - 1);
+        // Fragments to registers, then the slot is refilled before the MFMAs.
+        v4i af[2];
+        v2i tr[32];
+        af[0] = ks_rd128(slot + aadr[0]);
+        af[1] = ks_rd128(slot + aadr[1]);
+        ks_read_w<F8, 0>(slot, wadr, tr);
+        ks_lgkm_wait_all(af, tr);
+        v4i wf[16];  // INT8: [2 steps][8 blocks] of 16 k bytes; FP8: [8 blocks][2 halves] of 16 k bytes
+#pragma unroll
+        for (int x = 0; x < 16; ++x) wf[x] = v4i{tr[2 * x][0], tr[2 * x][1], tr[2 * x + 1][0], tr[2 * x + 1][1]};
+        if (issued < np) {
+            issue(issued, slot);
+            ++issued;
+        }
+        if constexpr (F8) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) af[h][e] = static_cast<int>(e4m3_sanitize(static_cast<uint32_t>(af[h][e])));
+#pragma unroll
+            for (int x = 0; x < 16; ++x)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) wf[x][e] = static_cast<int>(e4m3_sanitize(static_cast<uint32_t>(wf[x][e])));
+            const v8i a8 = __builtin_shufflevector(af[0], af[1], 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+            for (int cb = 0; cb < KS_CB; ++cb)
+                acc[cb] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                    a8, __builtin_shufflevector(wf[2 * cb], wf[2 * cb + 1], 0, 1, 2, 3, 4, 5, 6, 7), acc[cb], 0, 0,
+                    0, 0, 0, 0);
+        } else {
+#pragma unroll
+            for (int s = 0; s < 2; ++s)
+#pragma unroll
+                for (int cb = 0; cb < KS_CB; ++cb)
+                    acc[cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[s], wf[8 * s + cb], acc[cb], 0, 0, 0);
+        }
+    }
+
+    // Lane l of block cb holds column 16cb + l%16, rows 4(l/16) + v.
+    AccE* const part = static_cast<AccE*>(sp.part) + (static_cast<size_t>(cbg) * S + split) * M * KS_W;
+    const int j = lane & 15, mb = 4 * G;
+#pragma unroll
+    for (int cb = 0; cb < KS_CB; ++cb)
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+            if (mb + v < M) part[(mb + v) * KS_W + 16 * cb + j] = acc[cb][v];
+}
+
+// One thread per output: the S partials of (m, n) in split order, then the
+// epilogue.
+template <int EL, int OUT>
+__global__ __launch_bounds__(256) void kn_reduce_kernel(GemmArgs p, KnSplit sp) {
+    constexpr bool F8 = EL == ELEM_F8;
+    using AccE = typename std::conditional<F8, float, int32_t>::type;
+    const int N = p.N, S = sp.S;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (idx >= static_cast<int64_t>(p.M) * N) return;
+    const int m = static_cast<int>(idx / N), n = static_cast<int>(idx % N);
+    const AccE* part = static_cast<const AccE*>(sp.part) + static_cast<size_t>(n / KS_W) * S * p.M * KS_W +
+                       static_cast<size_t>(m) * KS_W + (n % KS_W);
+    AccE v[KS_SMAX];
+#pragma unroll
+    for (int t = 0; t < KS_SMAX; ++t) v[t] = t < S ? part[static_cast<size_t>(t) * p.M * KS_W] : AccE(0);
+    AccE s = v[0];
+#pragma unroll
+    for (int t = 1; t < KS_SMAX; ++t)
+        if (t < S) s += v[t];
+    float y;
+    if constexpr (F8) {
+        const float sab = p.sa * p.sb;
+        y = p.bias ? __builtin_fmaf(s, sab, p.bias[n]) : s * sab;
+    } else {
+        const float sc = (p.scale_a ? p.scale_a[m] : p.sa) * (p.scale_b ? p.scale_b[n] : p.sb);
+        y = p.bias ? __builtin_fmaf(static_cast<float>(s), sc, p.bias[n]) : static_cast<float>(s) * sc;
+    }
+    int32_t si = 0;
+    if constexpr (!F8) si = s;
+    store_out<OUT>(p.C, static_cast<size_t>(idx), y, si);
+}
+
+template <int EL, int OUT>
+hipError_t launch_kn_split_out(const GemmArgs& p, const KnSplit& sp, hipStream_t stream) {
+    GemmArgs a = p;
+    KnSplit s = sp;
+    void* args[] = {&a, &s};
+    const int nblk = (p.N + 4 * KS_W - 1) / (4 * KS_W);
+    hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(&gemv_kn_split_kernel<EL>), dim3(nblk * sp.S),
+                                   dim3(256), args, 0, stream);
+    if (e != hipSuccess) return e;
+    const int64_t outs = static_cast<int64_t>(p.M) * p.N;
+    return hipLaunchKernel(reinterpret_cast<const void*>(&kn_reduce_kernel<EL, OUT>),
+                           dim3(static_cast<unsigned>((outs + 255) / 256)), dim3(256), args, 0, stream);
+}
+
+template <int EL>
+hipError_t launch_kn_split(const GemmArgs& p, const KnSplit& sp, hipStream_t stream) {
+    switch (p.out_dtype) {
+        case FKE_OUT_F32: return launch_kn_split_out<EL, FKE_OUT_F32>(p, sp, stream);
+        case FKE_OUT_BF16: return launch_kn_split_out<EL, FKE_OUT_BF16>(p, sp, stream);
+        default:
+            if constexpr (EL == ELEM_I8) return launch_kn_split_out<ELEM_I8, FKE_OUT_I32>(p, sp, stream);
+            return hipErrorInvalidValue;
+    }
+}
+
+// ===========================================================================
+// Full kernel: one workgroup per 64-column block over all of K (no workspace).
+// Four waves split K: wave w takes the 128-row pieces w, w+4, ...; items of
+// 128 rows x 64 bytes (8 KiB, sixteen rows per 1-KiB copy, four lanes per
+// row) plus 2 KiB of activations, three ring slots per wave (120 KiB); the
+// four waves' sums meet in LDS in the fixed order w = 0..3.
+// ===========================================================================
+constexpr int KF_W = 64;                 // columns (bytes of a B row) per workgroup
+constexpr int KF_ROWS = 128;             // k rows per item
+constexpr int KF_BI = KF_ROWS * KF_W;    // weight bytes per item (8 KiB)
+constexpr int KF_AI = 16 * KF_ROWS;      // activation bytes per item (2 KiB)
+constexpr int KF_ITEM = KF_BI + KF_AI;   // 10 KiB
+constexpr int KF_DB = KF_BI / 1024;      // weight copies per item
+constexpr int KF_DA = KF_AI / 1024;      // activation copies per item
+constexpr int KF_DI = KF_DB + KF_DA;     // copies per item
+constexpr int KF_NS = 3;                 // ring slots per wave (120 KiB of LDS per workgroup)
 
 // Physical chunk offset of item row r: bijective on r bits 1..2 within each
 // 8-row group (a 16-lane group reads 8 rows x 16 bytes = 128 bytes), and
 // with bit 4 ^ bit 5 flipping it, rows of the two 16-lane groups of a half
 // wave that share r mod 4 land in different chunks too.
-__device__ __forceinline__ int kn_swz(int r) { return ((r >> 1) & 3) ^ ((((r >> 4) ^ (r >> 5)) & 1) * 3); }
-__device__ __forceinline__ int kn_aswz(int m) { return (m & 7) ^ ((m >> 3) & 1); }
+__device__ __forceinline__ int kf_swz(int r) { return ((r >> 1) & 3) ^ ((((r >> 4) ^ (r >> 5)) & 1) * 3); }
+__device__ __forceinline__ int kf_aswz(int m) { return (m & 7) ^ ((m >> 3) & 1); }
 
-__device__ __forceinline__ v4i rd128(const lds_u8* a) {
+__device__ __forceinline__ v4i kf_rd128(const lds_u8* a) {
     v4i r;
     asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(a));
     return r;
 }
-__device__ __forceinline__ v2i rdtr(const lds_u8* a) {
+__device__ __forceinline__ v2i kf_rdtr(const lds_u8* a) {
     v2i r;
     asm volatile("ds_read_b64_tr_b8 %0, %1" : "=v"(r) : "v"(a));
     return r;
@@ -94,16 +366,16 @@ __device__ __forceinline__ v2i rdtr(const lds_u8* a) {
 // Every LDS read has landed; the registers they wrote are tied to the wait,
 // so nothing reads (or copies) them before it.
 template <int N>
-__device__ __forceinline__ void lgkm_wait_all(v4i (&a)[2], v2i (&t)[N]) {
+__device__ __forceinline__ void kf_lgkm_wait_all(v4i (&a)[2], v2i (&t)[N]) {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     asm volatile("" : "+v"(a[0]), "+v"(a[1]));
 #pragma unroll
     for (int i = 0; i < N; ++i) asm volatile("" : "+v"(t[i]));
 }
 
-// s_waitcnt vmcnt(KN_DI * n): every copy but those of the n latest items has landed.
-__device__ __forceinline__ void wait_items(int n) {
-    static_assert(KN_DI == 10, "vmcnt steps below are 10 copies");
+// s_waitcnt vmcnt(KF_DI * n): every copy but those of the n latest items has landed.
+__device__ __forceinline__ void kf_wait_items(int n) {
+    static_assert(KF_DI == 10, "vmcnt steps below are 10 copies");
     switch (n) {
         case 0: wait_vm<0>(); break;
         case 1: wait_vm<10>(); break;
@@ -112,13 +384,13 @@ __device__ __forceinline__ void wait_items(int n) {
 }
 
 template <int EL, int OUT>
-__global__ __launch_bounds__(256) void gemv_kn_kernel(GemmArgs p) {
+__global__ __launch_bounds__(256) void gemv_kn_full_kernel(GemmArgs p) {
     constexpr bool F8 = EL == ELEM_F8;
     static_assert(EL == ELEM_I8 || (F8 && OUT != FKE_OUT_I32), "FP8: fp32 or bf16 out");
-    static_assert(KN_NS == 3, "wait_items covers up to two later items");
+    static_assert(KF_NS == 3, "kf_wait_items covers up to two later items");
     using AccV = typename std::conditional<F8, v4f, v4i>::type;
-    __shared__ __attribute__((aligned(1024))) uint8_t ring[KN_NS][4][KN_ITEM];
-    __shared__ __attribute__((aligned(16))) float esb[KN_W], ebias[KN_W], esa[64];
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[KF_NS][4][KF_ITEM];
+    __shared__ __attribute__((aligned(16))) float esb[KF_W], ebias[KF_W], esa[64];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -132,14 +404,14 @@ __global__ __launch_bounds__(256) void gemv_kn_kernel(GemmArgs p) {
     int blk = blockIdx.x;
     const int G16 = static_cast<int>(gridDim.x) / 16 * 16;
     if (blk < G16) blk = ((blk / 16) * 8 + (blk % 8)) * 2 + ((blk / 8) % 2);
-    const int n0 = blk * KN_W;
-    const int P = (K + KN_ROWS - 1) / KN_ROWS;         // pieces along K
+    const int n0 = blk * KF_W;
+    const int P = (K + KF_ROWS - 1) / KF_ROWS;         // pieces along K
     const int np = wave < P ? (P - 1 - wave) / 4 + 1 : 0;  // pieces of this wave
 
     // Epilogue operands straight to LDS (dword LDS-DMA by wave 0 before its
     // stream; older than every item's copies, so landed with the first item).
     if (wave == 0) {
-        const int nc = min(KN_W, N - n0);
+        const int nc = min(KF_W, N - n0);
         if (p.scale_b)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(p.scale_b + n0, nc * 4), (lds_u8*)esb, 4, 4 * lane, 0,
                                                      0, 0);
@@ -153,43 +425,43 @@ __global__ __launch_bounds__(256) void gemv_kn_kernel(GemmArgs p) {
 
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.B, K * N);
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, M * K);
-    lds_u8* const lring = (lds_u8*)(&ring[0][wave][0]);  // slot q at + q * 4 * KN_ITEM
-    constexpr int SLOT = 4 * KN_ITEM;
+    lds_u8* const lring = (lds_u8*)(&ring[0][wave][0]);  // slot q at + q * 4 * KF_ITEM
+    constexpr int SLOT = 4 * KF_ITEM;
 
     // Copy geometry (k-independent part of each lane's source offsets).
     // Weights, copy d: row i = 16d + l/4 of the item, physical chunk l%4
-    // holding logical chunk (l%4) ^ kn_swz(i).  Activations, copy d: row
-    // m = 8d + l/8, physical chunk l%8 holding logical chunk (l%8) ^ kn_aswz(m).
-    uint32_t boff[KN_DB];
-    int brow[KN_DB];
+    // holding logical chunk (l%4) ^ kf_swz(i).  Activations, copy d: row
+    // m = 8d + l/8, physical chunk l%8 holding logical chunk (l%8) ^ kf_aswz(m).
+    uint32_t boff[KF_DB];
+    int brow[KF_DB];
 #pragma unroll
-    for (int d = 0; d < KN_DB; ++d) {
+    for (int d = 0; d < KF_DB; ++d) {
         const int i = 16 * d + (lane >> 2);
         brow[d] = i;
-        boff[d] = static_cast<uint32_t>(i * N + n0 + 16 * ((lane & 3) ^ kn_swz(i)));
+        boff[d] = static_cast<uint32_t>(i * N + n0 + 16 * ((lane & 3) ^ kf_swz(i)));
     }
-    uint32_t aoff[KN_DA];
-    int akb[KN_DA];
-    bool arow[KN_DA];
+    uint32_t aoff[KF_DA];
+    int akb[KF_DA];
+    bool arow[KF_DA];
 #pragma unroll
-    for (int d = 0; d < KN_DA; ++d) {
+    for (int d = 0; d < KF_DA; ++d) {
         const int m = 8 * d + (lane >> 3);
-        const int c = (lane & 7) ^ kn_aswz(m);
+        const int c = (lane & 7) ^ kf_aswz(m);
         arow[d] = m < M;
         akb[d] = 16 * c;
         aoff[d] = static_cast<uint32_t>(m * K + 16 * c);
     }
     auto issue = [&](int j, lds_u8* dst) __attribute__((always_inline)) {
-        const int k0 = (wave + 4 * j) * KN_ROWS;
+        const int k0 = (wave + 4 * j) * KF_ROWS;
 #pragma unroll
-        for (int d = 0; d < KN_DB; ++d) {
+        for (int d = 0; d < KF_DB; ++d) {
             const uint32_t off = k0 + brow[d] < K ? boff[d] + static_cast<uint32_t>(k0 * N) : 0x80000000u;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, dst + d * 1024, 16, static_cast<int>(off), 0, 0, 2);
         }
 #pragma unroll
-        for (int d = 0; d < KN_DA; ++d) {
+        for (int d = 0; d < KF_DA; ++d) {
             const uint32_t off = arow[d] && k0 + akb[d] < K ? aoff[d] + static_cast<uint32_t>(k0) : 0x80000000u;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, dst + KN_BI + d * 1024, 16, static_cast<int>(off), 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, dst + KF_BI + d * 1024, 16, static_cast<int>(off), 0, 0, 0);
         }
     };
 
@@ -204,7 +476,7 @@ __global__ __launch_bounds__(256) void gemv_kn_kernel(GemmArgs p) {
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb) {
         const int r = (F8 ? 32 : 16) * G + b8;
-        wadr[cb] = static_cast<uint32_t>(r * KN_W + 16 * (cb ^ kn_swz(r)) + 8 * hh);
+        wadr[cb] = static_cast<uint32_t>(r * KF_W + 16 * (cb ^ kf_swz(r)) + 8 * hh);
     }
     // Activation reads: row m = l % 16, logical chunk (INT8) 4s + G for step
     // s, (FP8) 2G + e for half e.
@@ -213,7 +485,7 @@ __global__ __launch_bounds__(256) void gemv_kn_kernel(GemmArgs p) {
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
         const int c = F8 ? 2 * G + e : 4 * e + G;
-        aadr[e] = static_cast<uint32_t>(KN_BI + am * KN_ROWS + 16 * (c ^ kn_aswz(am)));
+        aadr[e] = static_cast<uint32_t>(KF_BI + am * KF_ROWS + 16 * (c ^ kf_aswz(am)));
     }
 
     AccV acc[4];
@@ -222,34 +494,34 @@ __global__ __launch_bounds__(256) void gemv_kn_kernel(GemmArgs p) {
 
     int issued = 0;
 #pragma unroll
-    for (int q = 0; q < KN_NS; ++q)
+    for (int q = 0; q < KF_NS; ++q)
         if (issued < np) {
             issue(issued, lring + q * SLOT);
             ++issued;
         }
     for (int c = 0; c < np; ++c) {
-        lds_u8* const slot = lring + (c % KN_NS) * SLOT;
-        wait_items(issued - c - 1);
+        lds_u8* const slot = lring + (c % KF_NS) * SLOT;
+        kf_wait_items(issued - c - 1);
         // Fragments to registers, then the slot is refilled before the MFMAs.
         // 18 reads: at most 12 in flight (lgkmcnt's field is 4 bits).
         v4i af[2];
         v2i tr[16];  // INT8: [2 steps][4 blocks][2 eighths]; FP8: [4 blocks][4 eighths]
-        af[0] = rd128(slot + aadr[0]);
-        af[1] = rd128(slot + aadr[1]);
+        af[0] = kf_rd128(slot + aadr[0]);
+        af[1] = kf_rd128(slot + aadr[1]);
 #pragma unroll
         for (int x = 0; x < 16; ++x) {
             uint32_t a;
             if constexpr (F8) {
                 const int cb = x >> 2, t = x & 3;  // eighth t of block cb: rows 32G + 8t ..
-                a = (t >= 2 ? wadr[cb ^ 3] : wadr[cb]) + (8 * t) * KN_W;
+                a = (t >= 2 ? wadr[cb ^ 3] : wadr[cb]) + (8 * t) * KF_W;
             } else {
                 const int s = x >> 3, cb = (x >> 1) & 3, t = x & 1;  // rows 64s + 16G + 8t ..
-                a = wadr[cb] + (64 * s + 8 * t) * KN_W;
+                a = wadr[cb] + (64 * s + 8 * t) * KF_W;
             }
             if (x + 2 >= 12) asm volatile("s_waitcnt lgkmcnt(11)" ::: "memory");
-            tr[x] = rdtr(slot + a);
+            tr[x] = kf_rdtr(slot + a);
         }
-        lgkm_wait_all(af, tr);
+        kf_lgkm_wait_all(af, tr);
         v4i wf[8];  // INT8: [2 steps][4 blocks] of 16 k bytes; FP8: [4 blocks][2 halves] of 16 k bytes
 #pragma unroll
         for (int x = 0; x < 8; ++x) wf[x] = v4i{tr[2 * x][0], tr[2 * x][1], tr[2 * x + 1][0], tr[2 * x + 1][1]};
@@ -314,21 +586,21 @@ __global__ __launch_bounds__(256) void gemv_kn_kernel(GemmArgs p) {
 }
 
 template <int EL>
-hipError_t launch_kn(const GemmArgs& p, hipStream_t stream) {
+hipError_t launch_kn_full(const GemmArgs& p, hipStream_t stream) {
     GemmArgs a = p;
     void* args[] = {&a};
     const void* f;
     switch (p.out_dtype) {
-        case FKE_OUT_F32: f = reinterpret_cast<const void*>(&gemv_kn_kernel<EL, FKE_OUT_F32>); break;
-        case FKE_OUT_BF16: f = reinterpret_cast<const void*>(&gemv_kn_kernel<EL, FKE_OUT_BF16>); break;
+        case FKE_OUT_F32: f = reinterpret_cast<const void*>(&gemv_kn_full_kernel<EL, FKE_OUT_F32>); break;
+        case FKE_OUT_BF16: f = reinterpret_cast<const void*>(&gemv_kn_full_kernel<EL, FKE_OUT_BF16>); break;
         default:
             if constexpr (EL == ELEM_I8) {
-                f = reinterpret_cast<const void*>(&gemv_kn_kernel<ELEM_I8, FKE_OUT_I32>);
+                f = reinterpret_cast<const void*>(&gemv_kn_full_kernel<ELEM_I8, FKE_OUT_I32>);
                 break;
             }
             return hipErrorInvalidValue;
     }
-    return hipLaunchKernel(f, dim3((p.N + KN_W - 1) / KN_W), dim3(256), args, 0, stream);
+    return hipLaunchKernel(f, dim3((p.N + KF_W - 1) / KF_W), dim3(256), args, 0, stream);
 }
 
 }  // namespace
@@ -344,8 +616,51 @@ bool gemv_kn_supports(const GemmArgs& p, int elem) {
     return static_cast<int64_t>(p.K) * p.N <= INT32_MAX && static_cast<int64_t>(p.M) * p.K <= INT32_MAX;
 }
 
-hipError_t launch_gemv_kn(const GemmArgs& p, int elem, hipStream_t stream) {
-    return elem == ELEM_F8 ? launch_kn<ELEM_F8>(p, stream) : launch_kn<ELEM_I8>(p, stream);
+// Partial sums of the split kernel: [ceil(N/128)][S][M][128], 4 bytes each.
+static size_t kn_ws_bytes(int M, int N, int S) {
+    return static_cast<size_t>((N + KS_W - 1) / KS_W) * static_cast<size_t>(S) * static_cast<size_t>(M) * KS_W * 4;
+}
+
+// K splits: as many as fill the CUs with one 512-column workgroup each
+// (kCUs; S <= 8, at least one 128-row piece per split, and no more than a
+// workspace of ws_bytes holds), with no empty split.  S = 1: the full kernel.
+static void kn_splits(const GemmArgs& p, size_t ws_bytes, int* S_out, int* PS_out) {
+    constexpr int kCUs = 256;
+    const int P = (p.K + KS_ROWS - 1) / KS_ROWS;
+    const int nblk = (p.N + 4 * KS_W - 1) / (4 * KS_W);
+    int S = kCUs / nblk;
+    if (S > KS_SMAX) S = KS_SMAX;
+    if (S > P) S = P;
+    while (S > 1 && kn_ws_bytes(p.M, p.N, S) > ws_bytes) --S;
+    if (S < 2) {
+        *S_out = 1;
+        *PS_out = P;
+        return;
+    }
+    const int PS = (P + S - 1) / S;
+    *S_out = (P + PS - 1) / PS;
+    *PS_out = PS;
+}
+
+size_t gemv_kn_workspace_bytes(const GemmArgs& p) {
+    int S, PS;
+    kn_splits(p, SIZE_MAX, &S, &PS);
+    return S > 1 ? kn_ws_bytes(p.M, p.N, S) : 0;
+}
+
+KnSplit gemv_kn_plan(const GemmArgs& p, void* ws, size_t ws_bytes) {
+    KnSplit sp;
+    kn_splits(p, ws ? ws_bytes : 0, &sp.S, &sp.PS);
+    sp.part = sp.S > 1 ? ws : nullptr;
+    return sp;
+}
+
+hipError_t launch_gemv_kn(const GemmArgs& p, int elem, const KnSplit& sp, hipStream_t stream) {
+    if (sp.S > 1) {
+        if (!sp.part) return hipErrorInvalidValue;
+        return elem == ELEM_F8 ? launch_kn_split<ELEM_F8>(p, sp, stream) : launch_kn_split<ELEM_I8>(p, sp, stream);
+    }
+    return elem == ELEM_F8 ? launch_kn_full<ELEM_F8>(p, stream) : launch_kn_full<ELEM_I8>(p, stream);
 }
 
 }  // namespace fke

@@ -29,6 +29,9 @@ SIGNATURES = {
     "fke_qgemm_i8_on_path": ([_i, _p, _p, _p, _i, _i, _i, _p, _p, _f, _f, _p, _i, _i, _p], _i),
     "fke_qgemm_f8": ([_p, _p, _p, _i, _i, _i, _f, _f, _p, _i, _i, _p], _i),
     "fke_qgemm_f8_on_path": ([_i, _p, _p, _p, _i, _i, _i, _f, _f, _p, _i, _i, _p], _i),
+    "fke_qgemm_workspace_size": ([_i, _i, _i, _i], ct.c_size_t),
+    "fke_qgemm_i8_ws": ([_p, _p, _p, _i, _i, _i, _p, _p, _f, _f, _p, _i, _i, _p, ct.c_size_t, _p], _i),
+    "fke_qgemm_f8_ws": ([_p, _p, _p, _i, _i, _i, _f, _f, _p, _i, _i, _p, ct.c_size_t, _p], _i),
     "fke_quantize_rows_i8": ([_p, _i, _i, _i, _p, _p, _p], _i),
     "fke_swiglu": ([_p, _p, _p, ct.c_int64, _i, _p], _i),
     "fke_qgemm_i8_swiglu": ([_p, _p, _p, _i, _i, _i, _p, _p, _f, _f, _p, _i, _p], _i),

@@ -7,14 +7,20 @@
  *
  * Conventions shared by all GEMM entry points (reference:
  * flash-kernel-engine include/quantized_gemm.cuh:6-41, src/quantized_gemm.cu):
- *   - A, B, C, scale and bias pointers are caller-owned DEVICE buffers; the
- *     library allocates nothing and frees nothing.  C is fully overwritten.
+ *   - A, B, C, scale and bias pointers are caller-owned DEVICE buffers.  C is
+ *     fully overwritten.  The library allocates nothing for them; the one
+ *     device memory it allocates itself is the workspace of the B [K,N] decode
+ *     (M <= 16) on each stream that runs it (see fke_qgemm_workspace_size),
+ *     held until the process ends, and the fke_qgemm_*_ws entry points take
+ *     the caller's instead.
  *   - All matrices are row-major.  A is [M,K].  B is [N,K] (FKE_B_NK,
  *     K-contiguous per output column) or [K,N] (FKE_B_KN).  C is [M,N].
  *   - The call is asynchronous on `stream` (a hipStream_t; NULL = the null
- *     stream) and never synchronises.  No mutable global state: calls are
- *     re-entrant from any host thread.  (The one exception is the device
- *     scratch of fke_w8a8_linear_noalloc, shared by its calls on one GPU.)
+ *     stream) and never synchronises.  Calls are re-entrant from any host
+ *     thread.  Global state: the device scratch of fke_w8a8_linear_noalloc,
+ *     shared by its calls on one GPU, and the per-(device, stream) [K,N]
+ *     decode workspaces (calls on one stream run in order; different streams
+ *     never share one).
  */
 #ifndef FKE_QGEMM_H
 #define FKE_QGEMM_H
@@ -119,6 +125,31 @@ int fke_qgemm_f8(const uint8_t* A, const uint8_t* B, void* C, int M, int N, int 
 int fke_qgemm_f8_on_path(int path, const uint8_t* A, const uint8_t* B, void* C,
                          int M, int N, int K, float sa, float sb, const float* bias,
                          int out_dtype, int b_layout, void* stream);
+
+/*
+ * Workspace of the B [K,N] decode (M <= 16, INT8 and FP8; no reference
+ * counterpart: the reference kernels sum all of K in one thread,
+ * src/quantized_gemm.cu:29-37, :106-116).  The decode splits K over up to 8
+ * workgroups per 512-column block and adds the splits' partial sums in a
+ * second kernel, in split order (exact for INT8, deterministic for FP8); the
+ * partial sums need fke_qgemm_workspace_size(M, N, K, b_layout) bytes of
+ * device memory (0 for shapes the decode does not run or does not split).
+ * fke_qgemm_i8 / fke_qgemm_f8 use a workspace the library allocates per
+ * (device, stream) on first need (not while that stream is being captured
+ * into a graph: a capture then runs the decode unsplit, or on the workspace
+ * the stream already has).  fke_qgemm_i8_ws / fke_qgemm_f8_ws are the same
+ * calls on the caller's workspace: NULL or fewer bytes run the decode with
+ * fewer splits or unsplit (same results); calls that can overlap in time must
+ * not share one.  Other kernel families ignore the workspace.
+ */
+size_t fke_qgemm_workspace_size(int M, int N, int K, int b_layout);
+int fke_qgemm_i8_ws(const int8_t* A, const int8_t* B, void* C, int M, int N, int K,
+                    const float* scale_a, const float* scale_b, float sa, float sb,
+                    const float* bias, int out_dtype, int b_layout,
+                    void* workspace, size_t workspace_bytes, void* stream);
+int fke_qgemm_f8_ws(const uint8_t* A, const uint8_t* B, void* C, int M, int N, int K,
+                    float sa, float sb, const float* bias, int out_dtype, int b_layout,
+                    void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Per-token (per-row) symmetric INT8 quantiser: the step that produces A and

@@ -65,7 +65,7 @@ int main(void) {
     const int dims[] = {1, 2, 3, 15, 16, 17, 63, 64, 65, 127, 128, 129, 512, 513, 2047, 2048, 4095, 4096,
                         4104, 8192, 14336, 65536, 1 << 20, (1 << 20) + 16, 1 << 24, INT_MAX / 2, INT_MAX};
     const int nd = (int)(sizeof dims / sizeof *dims);
-    long n_paths[5] = {0};
+    long n_paths[5] = {0}, n_ws = 0;
     for (int a = 0; a < nd; ++a)
         for (int b = 0; b < nd; ++b)
             for (int c = 0; c < nd; ++c)
@@ -84,6 +84,11 @@ int main(void) {
                     }
                     const int ps = fke_select_path_i8_swiglu(P, P, P, M, N, K, FKE_OUT_BF16);
                     CHECK(ps == -1 || (ps >= FKE_PATH_GEMV && ps <= FKE_PATH_GENERIC));
+                    /* B [K,N] decode workspace: M*N*4 bytes per split (N rounded to 128), at most 8 splits */
+                    const size_t ws = fke_qgemm_workspace_size(M, N, K, lay);
+                    const size_t row = (size_t)((N + 127LL) / 128) * 128 * 4 * (size_t)M;
+                    CHECK(ws == 0 || (lay == FKE_B_KN && M <= 16 && ws % row == 0 && ws / row >= 2 && ws / row <= 8));
+                    ++n_ws;
                 }
     CHECK(n_paths[FKE_PATH_GEMV + 1] > 0 && n_paths[FKE_PATH_MFMA + 1] > 0 && n_paths[FKE_PATH_GENERIC + 1] > 0);
     CHECK(fke_select_path_i8(NULL, P, P, 8, 8, 8, 0, 0) == -1);
@@ -93,7 +98,7 @@ int main(void) {
         printf("[FAIL] %d checks\n", failures);
         return 1;
     }
-    printf("[PASS] C ABI host code under AddressSanitizer + UndefinedBehaviorSanitizer (%ld dispatch queries)\n",
-           n_paths[1] + n_paths[2] + n_paths[3] + n_paths[4]);
+    printf("[PASS] C ABI host code under AddressSanitizer + UndefinedBehaviorSanitizer (%ld dispatch queries, "
+           "%ld workspace sizes)\n", n_paths[1] + n_paths[2] + n_paths[3] + n_paths[4], n_ws);
     return 0;
 }

@@ -62,6 +62,37 @@ def test_rejects_null_pointers_and_bad_enums():
     assert L.fke_qgemm_i8_on_path(9, P, P, P, 8, 8, 8, None, None, 1.0, 1.0, None, 0, 0, None) == INVALID
 
 
+def test_workspace_entry_points_reject_bad_arguments():
+    L = _lib.lib()
+    for a, b, c in [(None, P, P), (P, None, P), (P, P, None)]:
+        assert L.fke_qgemm_i8_ws(a, b, c, 1, 16, 64, None, None, 1.0, 1.0, None, 0, 1, P, 1 << 20, None) == INVALID
+        assert L.fke_qgemm_f8_ws(a, b, c, 1, 16, 64, 1.0, 1.0, None, 0, 1, P, 1 << 20, None) == INVALID
+    for M, N, K in [(0, 16, 64), (1, 0, 64), (1, 16, 0)]:
+        assert L.fke_qgemm_i8_ws(P, P, P, M, N, K, None, None, 1.0, 1.0, None, 0, 1, None, 0, None) == INVALID
+        assert L.fke_qgemm_f8_ws(P, P, P, M, N, K, 1.0, 1.0, None, 0, 1, None, 0, None) == INVALID
+    assert L.fke_qgemm_i8_ws(P, P, P, 1, 16, 64, None, None, 1.0, 1.0, None, 3, 1, None, 0, None) == INVALID
+    assert L.fke_qgemm_f8_ws(P, P, P, 1, 16, 64, 1.0, 1.0, None, _lib.OUT_I32, 1, None, 0, None) == INVALID
+    assert L.fke_qgemm_f8_ws(P, P, P, 1, 16, 64, 1.0, 1.0, None, 0, 2, None, 0, None) == INVALID
+
+
+@pytest.mark.parametrize("M,N,K,layout,expect", [
+    # C2 with B [K,N]: 28 workgroups of 512 columns x 8 K splits, [M][N] int32 partials each
+    (1, 14336, 4096, 1, 8 * 1 * 14336 * 4),
+    (16, 14336, 4096, 1, 8 * 16 * 14336 * 4),
+    # splits capped by the 128-row pieces of K: K = 512 -> 4 splits
+    (4, 14336, 512, 1, 4 * 4 * 14336 * 4),
+    # N = 2^16: 128 blocks of 512 columns -> 2 splits
+    (2, 65536, 4096, 1, 2 * 2 * 65536 * 4),
+    # N rounded up to 128-column blocks
+    (3, 1040, 4096, 1, 8 * 3 * 1152 * 4),
+    # unsplit: K of one piece, the decode not taken (M > 16, B [N,K], N % 16 != 0, K % 64 != 0)
+    (1, 14336, 128, 1, 0), (17, 14336, 4096, 1, 0), (1, 14336, 4096, 0, 0), (1, 1000, 4096, 1, 0),
+    (1, 14336, 4000, 1, 0), (0, 14336, 4096, 1, 0), (1, 14336, 4096, 2, 0),
+])
+def test_workspace_size(M, N, K, layout, expect):
+    assert _lib.lib().fke_qgemm_workspace_size(M, N, K, layout) == expect
+
+
 def test_quantizer_rejects_bad_arguments():
     L = _lib.lib()
     q = L.fke_quantize_rows_i8

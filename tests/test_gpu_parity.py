@@ -335,6 +335,125 @@ def test_gemv_kn_f8_tolerance(oracle, dev, M, N, K, nan_codes):
         assert_fp8_close(got, ref, out, f"kn {M, N, K} nan={nan_codes}")
 
 
+def kn_i8_ws(A, B, sa, sb, bias, out, ws, ws_bytes, stream=None):
+    """fke_qgemm_i8_ws (B [K,N]) on device inputs, with the caller's workspace."""
+    M, K = A.shape
+    N = B.shape[1]
+    C = torch.empty((M, N), dtype=OUT_T[out], device=A.device)
+    st = _lib.lib().fke_qgemm_i8_ws(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, sa.data_ptr(),
+                                    sb.data_ptr(), 1.0, 1.0, bias.data_ptr(),
+                                    {"f32": _lib.OUT_F32, "bf16": _lib.OUT_BF16, "i32": _lib.OUT_I32}[out],
+                                    _lib.B_KN, None if ws is None else ws.data_ptr(), ws_bytes,
+                                    stream if stream is not None else torch.cuda.current_stream().cuda_stream)
+    _lib.check(st, "fke_qgemm_i8_ws")
+    return C
+
+
+@pytest.mark.parametrize("M", [1, 16])
+def test_gemv_kn_split_full_and_fewer_splits(oracle, dev, M):
+    """C2 with B [K,N] through fke_qgemm_i8_ws: the K-split kernels on a
+    workspace of fke_qgemm_workspace_size bytes, on a third of it (fewer
+    splits) and on none (the one-kernel full-K decode), every output dtype
+    bit-exact against the oracle."""
+    N, K = 14336, 4096
+    say("c2 kn split/full", M, N, K)
+    A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 9100 + M, layout="kn", act="normal")
+    acc = oracle.w8a8_acc(A, B, oracle.B_KN, nthreads=NTH)
+    need = _lib.lib().fke_qgemm_workspace_size(M, N, K, _lib.B_KN)
+    assert need == 4 * 8 * M * N  # 8 splits of [M][N] int32 partial sums
+    dA, dB, dsa, dsb, dbias = dev_t(A), dev_t(B), dev_t(sa), dev_t(sb), dev_t(bias)
+    for nbytes in (need, need // 3, 0):
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev) if nbytes else None
+        for out in ("i32", "f32", "bf16"):
+            got = kn_i8_ws(dA, dB, dsa, dsb, dbias, out, ws, nbytes)
+            torch.cuda.synchronize()
+            assert_same(host(got), oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, out),
+                        f"kn ws={nbytes} {out} M={M}")
+
+
+def test_gemv_kn_graph_replays(oracle, dev):
+    """The split [K,N] decode captured into a HIP graph (on the stream's own
+    workspace, and on a caller's workspace): three replays with other [K,N]
+    decodes run eagerly between them, each replay bit-exact."""
+    M, N, K = 4, 14336, 4096
+    say("kn graph replays", M, N, K)
+    A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 9200, layout="kn", act="normal")
+    ref = oracle_out(oracle, oracle.w8a8_acc(A, B, oracle.B_KN, nthreads=NTH), sa, sb, 1.0, 1.0, bias, "bf16")
+    A2, B2, sa2, sb2, bias2 = inputs_i8(oracle, M, N, K, 9300, layout="kn", act="normal")
+    dA, dB, dsa, dsb, dbias = dev_t(A), dev_t(B), dev_t(sa), dev_t(sb), dev_t(bias)
+    d2 = [dev_t(x) for x in (A2, B2, sa2, sb2, bias2)]
+    s = torch.cuda.Stream()
+    ws = torch.empty(_lib.lib().fke_qgemm_workspace_size(M, N, K, _lib.B_KN), dtype=torch.uint8, device=dev)
+    with torch.cuda.stream(s):  # the stream's own workspace exists before the capture
+        ops.w8a8_gemm(dA, dB, dsa, dsb, dbias, out_dtype=torch.bfloat16, b_layout="kn")
+    s.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        out_a = ops.w8a8_gemm(dA, dB, dsa, dsb, dbias, out_dtype=torch.bfloat16, b_layout="kn")
+        out_b = kn_i8_ws(dA, dB, dsa, dsb, dbias, "bf16", ws, ws.numel(), stream=s.cuda_stream)
+    for r in range(3):
+        out_a.zero_()
+        out_b.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert_same(host(out_a), ref, f"replay {r} (stream workspace)")
+        assert_same(host(out_b), ref, f"replay {r} (caller workspace)")
+        other = ops.w8a8_gemm(*d2[:2], d2[2], d2[3], d2[4], out_dtype=torch.bfloat16, b_layout="kn")
+        other2 = kn_i8_ws(*d2, "bf16", ws, ws.numel())
+        torch.cuda.synchronize()
+        assert torch.equal(other, other2)
+
+
+def test_gemv_kn_two_streams(oracle, dev):
+    """[K,N] decodes of different inputs on two streams at once, each on its
+    stream's own workspace: both bit-exact."""
+    M, N, K = 8, 14336, 4096
+    say("kn two streams", M, N, K)
+    ins = [inputs_i8(oracle, M, N, K, 9400 + 10 * i, layout="kn", act="normal") for i in range(2)]
+    refs = [oracle_out(oracle, oracle.w8a8_acc(A, B, oracle.B_KN, nthreads=NTH), sa, sb, 1.0, 1.0, bias, "bf16")
+            for A, B, sa, sb, bias in ins]
+    dins = [[dev_t(x) for x in t] for t in ins]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = [[], []]
+    for _ in range(20):
+        for i in range(2):
+            with torch.cuda.stream(streams[i]):
+                A, B, sa, sb, bias = dins[i]
+                outs[i].append(ops.w8a8_gemm(A, B, sa, sb, bias, out_dtype=torch.bfloat16, b_layout="kn"))
+    torch.cuda.synchronize()
+    for i in range(2):
+        for o in outs[i]:
+            assert_same(host(o), refs[i], f"stream {i}")
+
+
+@pytest.mark.parametrize("M", [1, 16])
+def test_gemv_kn_f8_split_deterministic(oracle, dev, M):
+    """FP8 decode with B [K,N] at the C2 shape on the K-split kernels and on
+    the full-K kernel (no workspace): each within the FP8 bars of the
+    reference's sequential sum, and each bit-identical from call to call (the
+    splits are added in a fixed order)."""
+    N, K = 14336, 4096
+    say("kn f8 split determinism", M, N, K)
+    A, B, sa, sb = f8_inputs(oracle, M, N, K, 9500 + M, "kn")
+    ref = oracle.f8_gemm(A, B, sa, sb, b_layout=oracle.B_KN, nthreads=NTH)
+    dA, dB = dev_t(A), dev_t(B)
+    need = _lib.lib().fke_qgemm_workspace_size(M, N, K, _lib.B_KN)
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    for wsp, nbytes in ((ws, need), (None, 0)):
+        runs = []
+        for _ in range(2):
+            C = torch.empty((M, N), dtype=torch.float32, device=dev)
+            st = _lib.lib().fke_qgemm_f8_ws(dA.data_ptr(), dB.data_ptr(), C.data_ptr(), M, N, K, sa, sb, None,
+                                            _lib.OUT_F32, _lib.B_KN, None if wsp is None else wsp.data_ptr(),
+                                            nbytes, torch.cuda.current_stream().cuda_stream)
+            _lib.check(st, "fke_qgemm_f8_ws")
+            torch.cuda.synchronize()
+            runs.append(host(C))
+        assert_same(runs[1], runs[0], f"fp8 kn ws={nbytes} run to run")
+        assert_fp8_close(runs[0], ref, "f32", f"kn ws={nbytes} M={M}")
+
+
 @pytest.mark.parametrize("M", [1, 7, 16])
 def test_fp8_dropin_launcher_decode(oracle, dev, M):
     """The drop-in fke_launch_fp8_gemm_scaled (B [K,N], fp32 out, alpha =
