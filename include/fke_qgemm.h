@@ -138,9 +138,10 @@ int fke_qgemm_f8_on_path(int path, const uint8_t* A, const uint8_t* B, void* C,
  * (device, stream) on first need (not while that stream is being captured
  * into a graph: a capture then runs the decode unsplit, or on the workspace
  * the stream already has).  fke_qgemm_i8_ws / fke_qgemm_f8_ws are the same
- * calls on the caller's workspace: NULL or fewer bytes run the decode with
- * fewer splits or unsplit (same results); calls that can overlap in time must
- * not share one.  Other kernel families ignore the workspace.
+ * calls on the caller's workspace (16-byte aligned): NULL, fewer bytes or an
+ * unaligned pointer run the decode with fewer splits or unsplit (same
+ * results); calls that can overlap in time must not share one.  Other kernel
+ * families ignore the workspace.
  */
 size_t fke_qgemm_workspace_size(int M, int N, int K, int b_layout);
 int fke_qgemm_i8_ws(const int8_t* A, const int8_t* B, void* C, int M, int N, int K,

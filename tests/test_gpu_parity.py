@@ -335,15 +335,17 @@ def test_gemv_kn_f8_tolerance(oracle, dev, M, N, K, nan_codes):
         assert_fp8_close(got, ref, out, f"kn {M, N, K} nan={nan_codes}")
 
 
-def kn_i8_ws(A, B, sa, sb, bias, out, ws, ws_bytes, stream=None):
-    """fke_qgemm_i8_ws (B [K,N]) on device inputs, with the caller's workspace."""
+def kn_i8_ws(A, B, sa, sb, bias, out, ws, ws_bytes, stream=None, ws_shift=0, c_shift=0):
+    """fke_qgemm_i8_ws (B [K,N]) on device inputs, with the caller's workspace
+    (ws_shift bytes past its start) and C c_shift elements into a buffer."""
     M, K = A.shape
     N = B.shape[1]
-    C = torch.empty((M, N), dtype=OUT_T[out], device=A.device)
+    Cbuf = torch.empty(M * N + c_shift, dtype=OUT_T[out], device=A.device)
+    C = Cbuf[c_shift:].view(M, N)
     st = _lib.lib().fke_qgemm_i8_ws(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, sa.data_ptr(),
                                     sb.data_ptr(), 1.0, 1.0, bias.data_ptr(),
                                     {"f32": _lib.OUT_F32, "bf16": _lib.OUT_BF16, "i32": _lib.OUT_I32}[out],
-                                    _lib.B_KN, None if ws is None else ws.data_ptr(), ws_bytes,
+                                    _lib.B_KN, None if ws is None else ws.data_ptr() + ws_shift, ws_bytes,
                                     stream if stream is not None else torch.cuda.current_stream().cuda_stream)
     _lib.check(st, "fke_qgemm_i8_ws")
     return C
@@ -369,6 +371,16 @@ def test_gemv_kn_split_full_and_fewer_splits(oracle, dev, M):
             torch.cuda.synchronize()
             assert_same(host(got), oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, out),
                         f"kn ws={nbytes} {out} M={M}")
+    # an output not aligned for the reduction's vector stores (element stores), and a
+    # workspace not 16-byte aligned (run unsplit)
+    ws = torch.empty(need + 16, dtype=torch.uint8, device=dev)
+    for out in ("f32", "bf16"):
+        got = kn_i8_ws(dA, dB, dsa, dsb, dbias, out, ws, need, c_shift=1)
+        torch.cuda.synchronize()
+        assert_same(host(got), oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, out), f"kn C+1 {out} M={M}")
+    got = kn_i8_ws(dA, dB, dsa, dsb, dbias, "i32", ws, need, ws_shift=4)
+    torch.cuda.synchronize()
+    assert_same(host(got), acc, f"kn ws+4 M={M}")
 
 
 def test_gemv_kn_graph_replays(oracle, dev):
