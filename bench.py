@@ -530,17 +530,26 @@ def shard_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
             "us": r["us_per_launch"], "GB/s": r["value"], "frac": r["roofline"]["frac"],
             "bytes": r["roofline"]["algorithmic_bytes_per_launch"], "kernel": r["kernel"]}
     sh = torch.cuda.current_stream(dev).cuda_stream
+    tiles = {_lib.PATH_MFMA_256x256: "256x256", _lib.PATH_MFMA_128x128: "128x128"}
     for name, (M, N, K, out, tdt) in {
             "tp8_prefill_colshard_4096x1376x4096_bf16": (4096, 1376, 4096, _lib.OUT_BF16, torch.bfloat16),
             "tp8_int8_colshard_8192x1024x8192_f32": (8192, 1024, 8192, _lib.OUT_F32, torch.float32),
-            "tp8_int8_kshard_8192x8192x1024_i32": (8192, 8192, 1024, _lib.OUT_I32, torch.int32)}.items():
+            "tp8_int8_kshard_8192x8192x1024_i32": (8192, 8192, 1024, _lib.OUT_I32, torch.int32),
+            "short_prefill_512x14336x4096_bf16": (512, 14336, 4096, _lib.OUT_BF16, torch.bfloat16)}.items():
         A, B, sa, sb = rand_i8(M, K), rand_i8(N, K), rand_u(M), rand_u(N)
         C = torch.empty((M, N), dtype=tdt, device=dev)
         ms = timed(lambda: L.fke_qgemm_i8(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, sa.data_ptr(),
                                           sb.data_ptr(), 1.0, 1.0, None, out, _lib.B_NK, sh),
                    args.steps, args.warmup)
         t = 2.0 * M * N * K / (ms * 1e-3) / 1e12
-        res[name] = {"ms": round(ms, 4), "TOPS": round(t, 1), "frac": round(t / PEAK_INT8_TOPS, 4)}
+        tile = L.fke_select_mfma_tile(M, N, K, _lib.B_NK, 0, 0)
+        res[name] = {"ms": round(ms, 4), "TOPS": round(t, 1), "frac": round(t / PEAK_INT8_TOPS, 4),
+                     "tile": tiles.get(tile, str(tile))}
+        if tile != _lib.PATH_MFMA_256x256:  # the 256x256 tile on the same shape, for comparison
+            ms2 = timed(lambda: L.fke_qgemm_i8_on_path(_lib.PATH_MFMA_256x256, A.data_ptr(), B.data_ptr(),
+                                                       C.data_ptr(), M, N, K, sa.data_ptr(), sb.data_ptr(), 1.0,
+                                                       1.0, None, out, _lib.B_NK, sh), args.steps, args.warmup)
+            res[name]["ms_256x256_tile"] = round(ms2, 4)
         del A, B, C
     return res
 

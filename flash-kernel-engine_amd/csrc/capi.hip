@@ -200,6 +200,24 @@ int pick_f8(const GemmArgs& p) {
     return FKE_PATH_GENERIC;
 }
 
+// FKE_PATH_MFMA_* -> the kernel's tile (B [K,N] runs 256x256 only); -1 for
+// any other path.
+int mfma_tile_of_path(int path, const GemmArgs& p) {
+    switch (path) {
+        case FKE_PATH_MFMA: return fke::MFMA_TILE_AUTO;
+        case FKE_PATH_MFMA_256x256: return fke::MFMA_TILE_256x256;
+        case FKE_PATH_MFMA_128x128: return p.b_layout == FKE_B_NK ? fke::MFMA_TILE_128x128 : -2;
+        default: return -1;
+    }
+}
+
+// The MFMA GEMM with the tile `path` names, after its shape check.
+int run_mfma(int path, const GemmArgs& p, int elem, hipStream_t s) {
+    const int tile = mfma_tile_of_path(path, p);
+    if (tile < 0 || !fke::mfma_supports(p, elem)) return hipErrorInvalidValue;
+    return fke::launch_mfma(p, elem, s, tile);
+}
+
 int run_i8(int path, const GemmArgs& p, void* stream, const KnWorkspace* ws) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (path == FKE_PATH_AUTO) path = pick_i8(p);
@@ -209,8 +227,8 @@ int run_i8(int path, const GemmArgs& p, void* stream, const KnWorkspace* ws) {
             if (!fke::gemv_i8_supports(p)) return hipErrorInvalidValue;
             return fke::launch_gemv_i8(p, s);
         case FKE_PATH_MFMA:
-            if (!fke::mfma_supports(p, fke::ELEM_I8)) return hipErrorInvalidValue;
-            return fke::launch_mfma(p, fke::ELEM_I8, s);
+        case FKE_PATH_MFMA_256x256:
+        case FKE_PATH_MFMA_128x128: return run_mfma(path, p, fke::ELEM_I8, s);
         case FKE_PATH_GENERIC: return fke::launch_generic(p, fke::ELEM_I8, s);
         case FKE_PATH_GEMV_DOT:
             if (!fke::gemv_dot_supports(p)) return hipErrorInvalidValue;
@@ -237,8 +255,8 @@ int run_half(int path, const GemmArgs& p, int elem, void* stream) {
     if (path == FKE_PATH_AUTO) path = pick_half(p, elem);
     switch (path) {
         case FKE_PATH_MFMA:
-            if (!fke::mfma_supports(p, elem)) return hipErrorInvalidValue;
-            return fke::launch_mfma(p, elem, s);
+        case FKE_PATH_MFMA_256x256:
+        case FKE_PATH_MFMA_128x128: return run_mfma(path, p, elem, s);
         case FKE_PATH_GENERIC: return fke::launch_generic(p, elem, s);
         default: return hipErrorInvalidValue;
     }
@@ -253,8 +271,8 @@ int run_f8(int path, const GemmArgs& p, void* stream, const KnWorkspace* ws = nu
             if (!fke::gemv_f8_supports(p)) return hipErrorInvalidValue;
             return fke::launch_gemv_f8(p, s);
         case FKE_PATH_MFMA:
-            if (!fke::mfma_supports(p, fke::ELEM_F8)) return hipErrorInvalidValue;
-            return fke::launch_mfma(p, fke::ELEM_F8, s);
+        case FKE_PATH_MFMA_256x256:
+        case FKE_PATH_MFMA_128x128: return run_mfma(path, p, fke::ELEM_F8, s);
         case FKE_PATH_GENERIC: return fke::launch_generic(p, fke::ELEM_F8, s);
         default: return hipErrorInvalidValue;
     }
@@ -421,6 +439,15 @@ int fke_select_path_half(const void* A, const void* B, const void* C, int M, int
     return pick_half(make_args(A, B, const_cast<void*>(C), M, N, K, nullptr, nullptr, 1.f, 1.f, nullptr, out_dtype,
                                b_layout),
                      half_elem(in_dtype));
+}
+
+int fke_select_mfma_tile(int M, int N, int K, int b_layout, int swiglu, int cus) {
+    if (M < 1 || N < 1 || K < 1 || (b_layout != FKE_B_NK && b_layout != FKE_B_KN) || (swiglu && N % 2)) return -1;
+    GemmArgs p = make_args(nullptr, nullptr, nullptr, M, N, K, nullptr, nullptr, 1.f, 1.f, nullptr, FKE_OUT_F32,
+                           b_layout);
+    p.swiglu = swiglu ? 1 : 0;
+    if (cus <= 0) cus = fke::device_cus();
+    return fke::mfma_pick_tile(p, cus) == fke::MFMA_TILE_128x128 ? FKE_PATH_MFMA_128x128 : FKE_PATH_MFMA_256x256;
 }
 
 // Reference src/tensor_core_attention.cu:13-86 (launch_wmma_gemm_fp16): A fp16

@@ -6,7 +6,11 @@
 // Workgroup tile 256x256, 4 waves (one per SIMD) in a 2x2 grid; each wave owns
 // 128x128 outputs as 4x4 MFMA blocks of 32x32 (256 accumulator AGPRs).  The
 // launch is persistent: one workgroup per CU (a multiple of the XCD count)
-// walks its tiles without a relaunch between them.
+// walks its tiles without a relaunch between them.  A 128x128 tile (each wave
+// 64x64 as 2x2 blocks, two workgroups per CU) serves shapes with fewer
+// 256x256 tiles than CUs (tensor-parallel shards, short prefills); every
+// output is still summed over K in the same order, so both tiles give
+// identical results.
 //   INT8: v_mfma_i32_32x32x32_i8   (exact int32 accumulation), 4 k steps/stage
 //   FP8 : v_mfma_f32_32x32x64_f8f6f4 with E4M3 operands (fp32), 2 k steps/stage
 // K advances 128 bytes per stage; two LDS stages of (256+256)x128 bytes
@@ -48,14 +52,25 @@ typedef int v8i __attribute__((ext_vector_type(8)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 256;
-constexpr int BN = 256;
-constexpr int BK = 128;                      // bytes of K per stage
+constexpr int BK = 128;  // bytes of K per stage
 constexpr int NWAVES = 4;
 constexpr int NTHREADS = NWAVES * 64;
-constexpr int STAGE_A = BM * BK;             // 32 KiB
-constexpr int STAGE = (BM + BN) * BK;        // 64 KiB
-constexpr int PW = BM * BK / 1024 / NWAVES;  // DMA loads per wave per panel (8)
+
+// Workgroup tile: each of the 4 waves (2x2) owns NI x NJ MFMA blocks of 32x32
+// (written for NI, NJ in {2, 4}; built as 4x4 and 2x2).
+template <int NI_, int NJ_>
+struct Tile {
+    static constexpr int NI = NI_, NJ = NJ_;
+    static constexpr int BM = 64 * NI, BN = 64 * NJ;  // tile rows, B columns (B rows of [N,K])
+    static constexpr int WM = 32 * NI, WN = 32 * NJ;  // one wave's rows, columns
+    static constexpr int STAGE_A = BM * BK;           // A part of one LDS stage
+    static constexpr int STAGE = (BM + BN) * BK;      // one LDS stage
+    static constexpr int PWA = BM / 32, PWB = BN / 32;  // 1-KiB DMA loads per wave per stage
+    static constexpr int NPIECE = NI * NJ;            // MFMAs per k step
+    static constexpr int OCC = NI * NJ <= 4 ? 2 : 1;  // workgroups per CU
+};
+using T256 = Tile<4, 4>;
+using T128 = Tile<2, 2>;
 
 __device__ __forceinline__ int swz(int r) { return ((r & 31) ^ ((r & 31) >> 3)) & 7; }
 
@@ -80,27 +95,30 @@ __device__ __forceinline__ void tile_of(int bid, int gm, int gn, int& tm, int& t
     tn = in_group / gsize;
 }
 
-// Weight row held by column c (0..255) of a SwiGLU tile whose 128 outputs
-// start at column o0; B is [gate; up] with I = rows / 2.  Each wave's 128 B
-// columns are 64 gate columns then the 64 up columns of the same outputs, so
-// MFMA block j (gate) and block j + 2 (up) of a wave hold the two operands of
-// one output in the same lane.
+// Weight row held by column c (0..BN-1) of a SwiGLU tile whose BN/2 outputs
+// start at column o0; B is [gate; up] with I = rows / 2.  Each wave's WN B
+// columns are WN/2 gate columns then the WN/2 up columns of the same outputs,
+// so MFMA block j (gate) and block j + NJ/2 (up) of a wave hold the two
+// operands of one output in the same lane.
+template <int NJ>
 __device__ __forceinline__ int swiglu_b_row(int c, int o0, int I) {
-    const int jj = (c >> 5) & 3;
-    const int o = o0 + (c >> 7) * 64 + (jj & 1) * 32 + (c & 31);
-    return jj >= 2 ? I + o : o;
+    constexpr int WN = 32 * NJ, H = NJ / 2;
+    const int jj = (c >> 5) % NJ;
+    const int o = o0 + (c / WN) * (WN / 2) + (jj % H) * 32 + (c & 31);
+    return jj >= H ? I + o : o;
 }
 
-// Direct-to-LDS copy plan of one 256-row x 128-byte K-contiguous panel (A, or
-// B in [N,K] order).  Each wave issues PW loads of 1 KiB (8 rows x 128 B);
+// Direct-to-LDS copy plan of one (32*PW)-row x 128-byte K-contiguous panel (A,
+// or B in [N,K] order).  Each wave issues PW loads of 1 KiB (8 rows x 128 B);
 // lane l lands at byte 16*l of its KiB, so it fetches the logical chunk that
 // the swizzle assigns to that physical slot.  Rows past `rows` re-read the
 // last valid row (their outputs are never stored).  SWI: panel row r holds
-// weight row swiglu_b_row(r, row0, rows / 2).
+// weight row swiglu_b_row<NJ>(r, row0, rows / 2).
+template <int PW>
 struct Panel {
     __amdgpu_buffer_rsrc_t rsrc;  // the whole operand, rows x ld bytes
     uint32_t off[PW];             // byte offset of this lane's 16-byte source at k = 0
-    template <bool SWI = false>
+    template <bool SWI = false, int NJ = 4>
     __device__ void init(const int8_t* base, int ld, int row0, int rows, int wave, int lane) {
         rsrc = make_rsrc(base, rows * ld);
 #pragma unroll
@@ -108,7 +126,7 @@ struct Panel {
             const int seg = wave * PW + i;
             const int r = seg * 8 + (lane >> 3);
             const int lc = (lane & 7) ^ swz(r);
-            const int src = SWI ? swiglu_b_row(r, row0, rows >> 1) : row0 + r;
+            const int src = SWI ? swiglu_b_row<NJ>(r, row0, rows >> 1) : row0 + r;
             off[i] = static_cast<uint32_t>(min(src, rows - 1) * ld + lc * 16);
         }
     }
@@ -118,7 +136,7 @@ struct Panel {
     }
 };
 
-// B stored [K,N]: a stage is 128 k rows of 256 n bytes, copied as they lie
+// B stored [K,N] (256-column tiles only): a stage is 128 k rows of 256 n bytes, copied as they lie
 // in memory, four rows per 1-KiB load; 16-byte chunk c of row k is stored at
 // chunk c ^ (k & 15).  The MFMA fragments (one column n per lane, k bytes
 // consecutive) are then read with ds_read_b64_tr_b8, which transposes 8x8
@@ -126,6 +144,7 @@ struct Panel {
 // memory (those outputs are never stored); reads past the end of B fall out
 // of the buffer's range and return 0.
 struct KNPanel {
+    static constexpr int PW = 8;  // 1-KiB loads per wave per stage
     __amdgpu_buffer_rsrc_t rsrc;  // all of B, K x N bytes
     uint32_t off[PW];             // byte offset of this lane's 16-byte source at stage 0
     int stage_bytes;              // BK rows of B
@@ -203,50 +222,52 @@ struct Mma<ELEM_F16> : Mma16<ELEM_F16> {};
 template <>
 struct Mma<ELEM_BF16> : Mma16<ELEM_BF16> {};
 
-template <int ELEM>
+template <int ELEM, class TL>
 struct Frags {
-    typename Mma<ELEM>::Frag a[4], b[4];
+    typename Mma<ELEM>::Frag a[TL::NI], b[TL::NJ];
 };
 
 // LDS reads of the wave's fragments of k step ks; read_piece issues read r
 // (one instruction, nothing waits for the data).
-//   A, and B in [N,K] order: ds_read_b128 of 16 k bytes.  INT8: r = 0..3 A
-//   block r, 4..7 B block r-4.  FP8: r = 2f + h, f = 0..3 A, 4..7 B, h =
-//   which 16 of the lane's 32 codes.  Rows wm*128 + 32*i + lr (A) and
-//   wn*128 + 32*j + lr (B^T) share swz(lr): one address plus immediates.
-//   B in [K,N] order: ds_read_b64_tr_b8 of 8 k bytes.  INT8: r = 4 + 2j + rr;
-//   FP8: r = 8 + 4j + rr, rr = which 8 of the lane's k bytes.
-template <int ELEM, int BL>
+//   A, and B in [N,K] order: ds_read_b128 of 16 k bytes.  INT8: r = 0..NI-1
+//   A block r, NI..NI+NJ-1 B block r-NI.  FP8: r = 2f + h, f < NI A, f >= NI
+//   B, h = which 16 of the lane's 32 codes.  Rows wm*WM + 32*i + lr (A) and
+//   wn*WN + 32*j + lr (B^T) share swz(lr): one address plus immediates.
+//   B in [K,N] order: ds_read_b64_tr_b8 of 8 k bytes.  INT8: r = NI + 2j + rr;
+//   FP8: r = 2NI + 4j + rr, rr = which 8 of the lane's k bytes.
+template <int ELEM, int BL, class TL>
 struct Reads {
-    static constexpr int A = Mma<ELEM>::FB == 16 ? 4 : 8;
-    static constexpr int N = BL == FKE_B_NK ? 2 * A : 3 * A;
+    static constexpr int PB = Mma<ELEM>::FB == 16 ? 1 : 2;  // reads per block and k step, [N,K]
+    static constexpr int A = PB * TL::NI;
+    static constexpr int N = A + (BL == FKE_B_NK ? PB : 2 * PB) * TL::NJ;
 };
 
-template <int ELEM, int BL>
+template <int ELEM, int BL, class TL>
 __device__ __forceinline__ void read_piece(const uint8_t* buf, int ks, int wm, int wn, int lane,
-                                           const uint32_t (&kn_off)[4][2], Frags<ELEM>& f, int r) {
+                                           const uint32_t (&kn_off)[TL::NJ][2], Frags<ELEM, TL>& f, int r) {
+    constexpr int NI = TL::NI;
     const int lr = lane & 31, lh = lane >> 5, sw = swz(lr);
-    const uint8_t* Ab = buf + (wm * 128 + lr) * BK;
-    const uint8_t* Bb = buf + STAGE_A + (wn * 128 + lr) * BK;
-    constexpr int RA = Reads<ELEM, BL>::A;
+    const uint8_t* Ab = buf + (wm * TL::WM + lr) * BK;
+    const uint8_t* Bb = buf + TL::STAGE_A + (wn * TL::WN + lr) * BK;
+    constexpr int RA = Reads<ELEM, BL, TL>::A;
     if constexpr (BL == FKE_B_KN) if (r >= RA) {
         constexpr int KSTEP = ELEM == ELEM_I8 ? 32 : 64;  // k rows per step
         const int p = r - RA;
         const int j = ELEM == ELEM_I8 ? p >> 1 : p >> 2, rr = ELEM == ELEM_I8 ? p & 1 : p & 3;
-        const v2i x = ds_read_tr8(buf + STAGE_A + kn_off[j][rr & 1] + (ks * KSTEP + (rr >> 1) * 16) * 256);
+        const v2i x = ds_read_tr8(buf + TL::STAGE_A + kn_off[j][rr & 1] + (ks * KSTEP + (rr >> 1) * 16) * 256);
         f.b[j][2 * rr] = x[0];
         f.b[j][2 * rr + 1] = x[1];
         return;
     }
     if constexpr (Mma<ELEM>::FB == 16) {
         const int co = ((ks * 2 + lh) ^ sw) << 4;  // this lane's 16-byte chunk of the 32-byte step
-        if (r < 4) f.a[r] = *reinterpret_cast<const v4i*>(Ab + r * 32 * BK + co);
-        else f.b[r - 4] = *reinterpret_cast<const v4i*>(Bb + (r - 4) * 32 * BK + co);
+        if (r < NI) f.a[r] = *reinterpret_cast<const v4i*>(Ab + r * 32 * BK + co);
+        else f.b[r - NI] = *reinterpret_cast<const v4i*>(Bb + (r - NI) * 32 * BK + co);
     } else {
         const int fi = r >> 1, h = r & 1;
         const int co = ((ks * 4 + lh * 2 + h) ^ sw) << 4;
-        v8i& d = fi < 4 ? f.a[fi] : f.b[fi - 4];
-        const v4i x = *reinterpret_cast<const v4i*>((fi < 4 ? Ab + fi * 32 * BK : Bb + (fi - 4) * 32 * BK) + co);
+        v8i& d = fi < NI ? f.a[fi] : f.b[fi - NI];
+        const v4i x = *reinterpret_cast<const v4i*>((fi < NI ? Ab + fi * 32 * BK : Bb + (fi - NI) * 32 * BK) + co);
         if (h == 0) {
             d[0] = x[0]; d[1] = x[1]; d[2] = x[2]; d[3] = x[3];
         } else {
@@ -264,20 +285,20 @@ __device__ __forceinline__ v8i sanitize8(v8i x) {
 }
 
 // FP8: clear the 0x7F/0xFF codes of a fragment set.
-template <int ELEM>
-__device__ __forceinline__ void sanitize_frags(Frags<ELEM>& f) {
+template <int ELEM, class TL>
+__device__ __forceinline__ void sanitize_frags(Frags<ELEM, TL>& f) {
     if constexpr (ELEM == ELEM_F8) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            f.a[i] = sanitize8(f.a[i]);
-            f.b[i] = sanitize8(f.b[i]);
-        }
+        for (int i = 0; i < TL::NI; ++i) f.a[i] = sanitize8(f.a[i]);
+#pragma unroll
+        for (int j = 0; j < TL::NJ; ++j) f.b[j] = sanitize8(f.b[j]);
     }
 }
 
-// MFMA (i, j) of one k step of the wave's 128x128 block.
-template <int ELEM>
-__device__ __forceinline__ void mfma_one(const Frags<ELEM>& f, typename Mma<ELEM>::AccT (&acc)[4][4], int i, int j) {
+// MFMA (i, j) of one k step of the wave's WM x WN block.
+template <int ELEM, class TL>
+__device__ __forceinline__ void mfma_one(const Frags<ELEM, TL>& f, typename Mma<ELEM>::AccT (&acc)[TL::NI][TL::NJ],
+                                         int i, int j) {
     typedef _Float16 v8h __attribute__((ext_vector_type(8)));
     typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
     if constexpr (ELEM == ELEM_I8)
@@ -292,28 +313,30 @@ __device__ __forceinline__ void mfma_one(const Frags<ELEM>& f, typename Mma<ELEM
                                                             __builtin_bit_cast(v8bf, f.b[j]), acc[i][j], 0, 0, 0);
 }
 
-// Output columns of one workgroup tile: 256, or 128 SwiGLU outputs (256 B rows).
-template <bool SWI>
-constexpr int tile_cols() { return SWI ? BN / 2 : BN; }
+// Output columns of one workgroup tile: BN, or BN/2 SwiGLU outputs (BN B rows).
+template <bool SWI, class TL>
+constexpr int tile_cols() { return SWI ? TL::BN / 2 : TL::BN; }
 
-template <int ELEM, int BL, int OUT, bool SWI>
-__global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
+template <int ELEM, int BL, int OUT, bool SWI, class TL>
+__global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p) {
     static_assert(!SWI || (ELEM == ELEM_I8 && BL == FKE_B_NK && OUT != FKE_OUT_I32), "SwiGLU: INT8, B [N,K], float out");
+    static_assert(BL == FKE_B_NK || TL::NJ == 4, "B [K,N]: 256-column tiles");
     constexpr int NKS = Mma<ELEM>::KSTEPS;
-    __shared__ __attribute__((aligned(1024))) uint8_t lds0[STAGE];
-    __shared__ __attribute__((aligned(1024))) uint8_t lds1[STAGE];
-    __shared__ __attribute__((aligned(16))) float epi_sa[BM];    // scale of each tile row
-    __shared__ __attribute__((aligned(16))) float epi_sb[BN];    // scale of each tile column
-    __shared__ __attribute__((aligned(16))) float epi_bias[BN];  // bias of each tile column
-    __shared__ int redo;                                          // FP8: rerun with NaN codes cleared
+    constexpr int NI = TL::NI, NJ = TL::NJ, BM = TL::BM, NPIECE = TL::NPIECE;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds0[TL::STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds1[TL::STAGE];
+    __shared__ __attribute__((aligned(16))) float epi_sa[BM];        // scale of each tile row
+    __shared__ __attribute__((aligned(16))) float epi_sb[TL::BN];    // scale of each tile column
+    __shared__ __attribute__((aligned(16))) float epi_bias[TL::BN];  // bias of each tile column
+    __shared__ int redo;                                              // FP8: rerun with NaN codes cleared
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar LDS/M0 math
-    const int wm = wave >> 1, wn = wave & 1;                     // wave's 128x128 block
+    const int wm = wave >> 1, wn = wave & 1;                     // wave's WM x WN block
 
     const int M = p.M, N = p.N, K = p.K;
-    constexpr int TC = tile_cols<SWI>();
+    constexpr int TC = tile_cols<SWI, TL>();
     const int NO = SWI ? N >> 1 : N;  // output columns
     const int gm = (M + BM - 1) / BM, gn = (NO + TC - 1) / TC;
     // Persistent: workgroup b takes tiles b, b + G, b + 2G, ... (G = grid size,
@@ -331,77 +354,79 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
     const int8_t* B = static_cast<const int8_t*>(p.B);
 
     // epilogue operands -> LDS (visible after the prologue barrier)
-    {
-        const int m = min(m0 + tid, M - 1);
-        const int n = min(SWI ? swiglu_b_row(tid, n0, NO) : n0 + tid, N - 1);  // B row of tile column tid
-        epi_sa[tid] = p.scale_a ? p.scale_a[m] : p.sa;
+    if (tid < BM) epi_sa[tid] = p.scale_a ? p.scale_a[min(m0 + tid, M - 1)] : p.sa;
+    if (tid < TL::BN) {
+        const int n = min(SWI ? swiglu_b_row<NJ>(tid, n0, NO) : n0 + tid, N - 1);  // B row of tile column tid
         epi_sb[tid] = p.scale_b ? p.scale_b[n] : p.sb;
         epi_bias[tid] = p.bias ? p.bias[n] : -0.0f;
-        if (tid == 0) redo = 0;
     }
+    if (tid == 0) redo = 0;
 
-    typename Mma<ELEM>::AccT acc[4][4];
+    typename Mma<ELEM>::AccT acc[NI][NJ];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NI; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < NJ; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
 
     const int KT = K / BK;
-    Panel pa;
+    Panel<TL::PWA> pa;
     pa.init(A, K, m0, M, wave, lane);
-    using BPanel = typename std::conditional<BL == FKE_B_NK, Panel, KNPanel>::type;
+    using BPanel = typename std::conditional<BL == FKE_B_NK, Panel<TL::PWB>, KNPanel>::type;
     BPanel pb;
-    uint32_t kn_off[4][2] = {};
+    uint32_t kn_off[NJ][2] = {};
     if constexpr (BL == FKE_B_NK) {
-        pb.template init<SWI>(B, K, n0, N, wave, lane);
+        pb.template init<SWI, NJ>(B, K, n0, N, wave, lane);
     } else {
         pb.init(B, N, K, n0, wave, lane);
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < NJ; ++j)
 #pragma unroll
             for (int rr = 0; rr < 2; ++rr) kn_off[j][rr] = kn_read_off<ELEM>(lane, wn, j, rr);
     }
 
-    // Copy of stage kt into buffer b, slot q of NSLOT: slots 0..PW-1 copy
-    // A, PW..2PW-1 copy B, all buffer -> LDS.
-    constexpr int NSLOT = 2 * PW;
+    // Copy of stage kt into buffer b, slot q of NSLOT: slots 0..PWA-1 copy
+    // A, the rest copy B, all buffer -> LDS.
+    constexpr int PWA = TL::PWA;
+    constexpr int NSLOT = PWA + (BL == FKE_B_NK ? TL::PWB : KNPanel::PW);
     auto copy = [&](int q, int kt, uint8_t* b) __attribute__((always_inline)) {
-        if (q < PW) pa.issue(q, kt * BK, b, wave);
-        else if constexpr (BL == FKE_B_NK) pb.issue(q - PW, kt * BK, b + STAGE_A, wave);
-        else pb.issue(q - PW, kt, b + STAGE_A, wave);
+        if (q < PWA) pa.issue(q, kt * BK, b, wave);
+        else if constexpr (BL == FKE_B_NK) pb.issue(q - PWA, kt * BK, b + TL::STAGE_A, wave);
+        else pb.issue(q - PWA, kt, b + TL::STAGE_A, wave);
     };
-    // A stage is NKS groups of 16 MFMAs.  Group g runs the MFMAs of one
-    // fragment set (g = 0: the previous stage's last step, carried across
-    // the barrier; g > 0: step g-1) while the LDS reads of step g fill the
-    // other set, and carries copy slots of the next stage (INT8, fp16, bf16:
-    // 6 / 6 / 4 / 0 over the four groups; FP8: all in the first of its
-    // two).  Within a group every memory instruction is
-    // paired with an MFMA, so it issues in the MFMA's shadow instead of
-    // stalling the matrix pipe.
+    // A stage is NKS groups of NPIECE MFMAs (16 for the 256x256 tile).
+    // Group g runs the MFMAs of one fragment set (g = 0: the previous stage's
+    // last step, carried across the barrier; g > 0: step g-1) while the LDS
+    // reads of step g fill the other set, and carries copy slots of the next
+    // stage (INT8, fp16, bf16, 256x256: 6 / 6 / 4 / 0 over the four groups;
+    // FP8: as many as the first of its two groups has MFMAs, the rest in the
+    // second).  Within a group every memory instruction is paired with an
+    // MFMA, so it issues in the MFMA's shadow instead of stalling the matrix
+    // pipe.
     constexpr int PER_GROUP = (NSLOT + NKS - 2) / (NKS - 1);
-    Frags<ELEM> f0, f1;
-    constexpr int NREAD = Reads<ELEM, BL>::N;  // LDS reads per step
-    auto group = [&](auto sanc, auto q0c, auto q1c, Frags<ELEM>& use, Frags<ELEM>& fill, const uint8_t* cur,
-                     int rks, uint8_t* nxt, int kc) __attribute__((always_inline)) {
+    Frags<ELEM, TL> f0, f1;
+    constexpr int NREAD = Reads<ELEM, BL, TL>::N;  // LDS reads per step
+    auto group = [&](auto sanc, auto q0c, auto q1c, Frags<ELEM, TL>& use, Frags<ELEM, TL>& fill,
+                     const uint8_t* cur, int rks, uint8_t* nxt, int kc) __attribute__((always_inline)) {
         constexpr bool SAN = decltype(sanc)::value;
         constexpr int Q0 = decltype(q0c)::value, Q1 = decltype(q1c)::value;
         constexpr int NQ = Q1 - Q0;
-        static_assert(NQ <= 16, "at most one copy slot per MFMA");
+        static_assert(NQ <= NPIECE, "at most one copy slot per MFMA");
         fence();
-        if constexpr (SAN) sanitize_frags<ELEM>(use);
-        // Piece t: MFMA (t/4, t%4), then the reads r = t (mod 16) of the
-        // next step, then copy slot Q0 + t for the first NQ pieces (early in
-        // the group, so each copy has the rest of the stage to land: 1.8 %
+        if constexpr (SAN) sanitize_frags<ELEM, TL>(use);
+        // Piece t: MFMA (t/NJ, t%NJ), then the reads r = t (mod NPIECE) of
+        // the next step, then copy slot Q0 + t for the first NQ pieces (early
+        // in the group, so each copy has the rest of the stage to land: 1.8 %
         // faster at 8192^3 INT8 than placing them in the group's last pieces).
         // Each piece is fenced, so this is the issue order.
 #pragma unroll
-        for (int t = 0; t < 16; ++t) {
+        for (int t = 0; t < NPIECE; ++t) {
             fence();
-            mfma_one<ELEM>(use, acc, t >> 2, t & 3);
+            mfma_one<ELEM, TL>(use, acc, t / NJ, t % NJ);
 #pragma unroll
-            for (int r = t; r < NREAD; r += 16) read_piece<ELEM, BL>(cur, rks, wm, wn, lane, kn_off, fill, r);
+            for (int r = t; r < NREAD; r += NPIECE)
+                read_piece<ELEM, BL, TL>(cur, rks, wm, wn, lane, kn_off, fill, r);
             if (t < NQ) copy(Q0 + t, kc, nxt);
         }
         fence();
@@ -413,6 +438,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
         using S = decltype(sanc);
         if constexpr (NKS == 4) {
             constexpr int P = PER_GROUP, P2 = 2 * P < NSLOT ? 2 * P : NSLOT;
+            static_assert(P <= NPIECE, "copies of a stage fit its first three groups");
             group(S{}, I0{}, std::integral_constant<int, P>{}, f1, f0, cur, 0, nxt, kc);
             group(S{}, std::integral_constant<int, P>{}, std::integral_constant<int, P2>{}, f0, f1, cur, 1, nxt, kc);
             group(S{}, std::integral_constant<int, P2>{}, std::integral_constant<int, NSLOT>{}, f1, f0, cur, 2, nxt, kc);
@@ -426,8 +452,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
             // vmcnt(0).  Splitting them 8 / 8 left the last copies one MFMA
             // before that wait and measured 5 % slower (438-444 us against
             // 416-422 us at 8192^3, both B layouts).
-            group(S{}, I0{}, std::integral_constant<int, NSLOT>{}, f1, f0, cur, 0, nxt, kc);
-            group(S{}, std::integral_constant<int, NSLOT>{}, std::integral_constant<int, NSLOT>{}, f0, f1, cur, 1, nxt,
+            constexpr int P = NSLOT < NPIECE ? NSLOT : NPIECE;
+            group(S{}, I0{}, std::integral_constant<int, P>{}, f1, f0, cur, 0, nxt, kc);
+            group(S{}, std::integral_constant<int, P>{}, std::integral_constant<int, NSLOT>{}, f0, f1, cur, 1, nxt,
                   kc);
         }
         wait_lgkm0();  // last step's fragments in registers (f1): cur may be overwritten after the barrier
@@ -448,10 +475,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
         wait_vm0();
         barrier();
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            f1.a[i] = typename Mma<ELEM>::Frag{};
-            f1.b[i] = typename Mma<ELEM>::Frag{};
-        }
+        for (int i = 0; i < NI; ++i) f1.a[i] = typename Mma<ELEM>::Frag{};
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) f1.b[j] = typename Mma<ELEM>::Frag{};
         int kt = 0;
         for (; kt + 2 <= KT; kt += 2) {
             stage(S{}, lds0, lds1, kt);
@@ -459,9 +485,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
         }
         if (kt < KT) stage(S{}, lds0, lds1, kt);  // odd stage count
         // the last stage's carried step
-        if constexpr (S::value) sanitize_frags<ELEM>(f1);
+        if constexpr (S::value) sanitize_frags<ELEM, TL>(f1);
 #pragma unroll
-        for (int t = 0; t < 16; ++t) mfma_one<ELEM>(f1, acc, t >> 2, t & 3);
+        for (int t = 0; t < NPIECE; ++t) mfma_one<ELEM, TL>(f1, acc, t / NJ, t % NJ);
     };
 
     if constexpr (ELEM != ELEM_F8) {
@@ -477,9 +503,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
         k_loop(F{});
         float t = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < NI; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < NJ; ++j)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) t += acc[i][j][v];
         if (__builtin_isnan(t)) redo = 1;  // benign race: every writer stores 1
@@ -487,9 +513,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
         barrier();
         if (redo) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < NI; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < NJ; ++j)
 #pragma unroll
                     for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
             k_loop(std::true_type{});
@@ -513,24 +539,25 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
     const __amdgpu_buffer_rsrc_t rc = make_rsrc(static_cast<char*>(p.C) + static_cast<size_t>(m0) * row_bytes,
                                                 min(M - m0, BM) * static_cast<int>(row_bytes));
     if constexpr (SWI) {
-        // SwiGLU: block j (gate) and j + 2 (up) of the wave hold output column
-        // n0 + 64*wn + 32*j + lane%32; h = swiglu_pair(g, u) of the two
-        // canonical epilogue values.
+        // SwiGLU: block j (gate) and j + NJ/2 (up) of the wave hold output
+        // column n0 + wn*WN/2 + 32*j + lane%32; h = swiglu_pair(g, u) of the
+        // two canonical epilogue values.
+        constexpr int WN = TL::WN;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int cg = wn * 128 + j * 32 + lr, cu = cg + 64;  // tile columns of the gate / up rows
+        for (int j = 0; j < NJ / 2; ++j) {
+            const int cg = wn * WN + j * 32 + lr, cu = cg + WN / 2;  // tile columns of the gate / up rows
             const float sbg = epi_sb[cg], sbu = epi_sb[cu];
             const float bg = epi_bias[cg], bu = epi_bias[cu];
-            const int o = n0 + wn * 64 + j * 32 + lr;
+            const int o = n0 + wn * (WN / 2) + j * 32 + lr;
             const uint32_t lane_off = o < NO
-                ? static_cast<uint32_t>(wm * 128 + 4 * lh) * row_bytes + static_cast<uint32_t>(o) * OB
+                ? static_cast<uint32_t>(wm * TL::WM + 4 * lh) * row_bytes + static_cast<uint32_t>(o) * OB
                 : 0x80000000u;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < NI; ++i) {
                 fence();
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
-                    const int rm = wm * 128 + i * 32 + 8 * g + 4 * lh;
+                    const int rm = wm * TL::WM + i * 32 + 8 * g + 4 * lh;
                     const float4 sa4 = *reinterpret_cast<const float4*>(&epi_sa[rm]);
                     const float sav[4] = {sa4.x, sa4.y, sa4.z, sa4.w};
 #pragma unroll
@@ -539,7 +566,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
                         const int voff =
                             static_cast<int>(lane_off + static_cast<uint32_t>(i * 32 + 8 * g + e) * row_bytes);
                         const float yg = __builtin_fmaf(static_cast<float>(acc[i][j][v]), sav[e] * sbg, bg);
-                        const float yu = __builtin_fmaf(static_cast<float>(acc[i][j + 2][v]), sav[e] * sbu, bu);
+                        const float yu = __builtin_fmaf(static_cast<float>(acc[i][j + NJ / 2][v]), sav[e] * sbu, bu);
                         const float h = swiglu_pair(yg, yu);
                         if constexpr (OUT == FKE_OUT_F32)
                             __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(h), rc, voff, 0, 2);
@@ -552,19 +579,19 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
         continue;
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int cn = wn * 128 + j * 32 + lr;  // column within the tile
+    for (int j = 0; j < NJ; ++j) {
+        const int cn = wn * TL::WN + j * 32 + lr;  // column within the tile
         const float sbn = epi_sb[cn];
         const float bn = epi_bias[cn];
         const uint32_t lane_off = n0 + cn < N
-            ? static_cast<uint32_t>(wm * 128 + 4 * lh) * row_bytes + static_cast<uint32_t>(n0 + cn) * OB
+            ? static_cast<uint32_t>(wm * TL::WM + 4 * lh) * row_bytes + static_cast<uint32_t>(n0 + cn) * OB
             : 0x80000000u;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < NI; ++i) {
             fence();
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const int rm = wm * 128 + i * 32 + 8 * g + 4 * lh;  // first of 4 consecutive tile rows
+                const int rm = wm * TL::WM + i * 32 + 8 * g + 4 * lh;  // first of 4 consecutive tile rows
                 const float4 sa4 = *reinterpret_cast<const float4*>(&epi_sa[rm]);
                 const float sav[4] = {sa4.x, sa4.y, sa4.z, sa4.w};
 #pragma unroll
@@ -594,33 +621,47 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_mfma_kernel(GemmArgs p) {
     }
 }
 
-template <int ELEM, int BL, int OUT, bool SWI = false>
-hipError_t launch_t(const GemmArgs& p, hipStream_t stream) {
-    constexpr int TC = tile_cols<SWI>();
-    const int gm = (p.M + BM - 1) / BM, gn = ((SWI ? p.N / 2 : p.N) + TC - 1) / TC;
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < NXCD)
-        cus = 256;
-    const int grid = min(gm * gn, cus / NXCD * NXCD);
+template <int ELEM, int BL, int OUT, bool SWI, class TL>
+hipError_t launch_t(const GemmArgs& p, hipStream_t stream, int cus) {
+    constexpr int TC = tile_cols<SWI, TL>();
+    const int gm = (p.M + TL::BM - 1) / TL::BM, gn = ((SWI ? p.N / 2 : p.N) + TC - 1) / TC;
+    const int grid = min(gm * gn, cus / NXCD * NXCD * TL::OCC);
     GemmArgs a = p;
     void* args[] = {&a};
-    return hipLaunchKernel(reinterpret_cast<const void*>(&gemm_mfma_kernel<ELEM, BL, OUT, SWI>),
+    return hipLaunchKernel(reinterpret_cast<const void*>(&gemm_mfma_kernel<ELEM, BL, OUT, SWI, TL>),
                            dim3(grid), dim3(NTHREADS), args, 0, stream);
 }
 
+template <int ELEM, int BL, int OUT, bool SWI = false>
+hipError_t launch_tile(const GemmArgs& p, hipStream_t s, int tile, int cus) {
+    if constexpr (BL == FKE_B_KN) {
+        return launch_t<ELEM, BL, OUT, SWI, T256>(p, s, cus);
+    } else {
+        return tile == MFMA_TILE_128x128 ? launch_t<ELEM, BL, OUT, SWI, T128>(p, s, cus)
+                                         : launch_t<ELEM, BL, OUT, SWI, T256>(p, s, cus);
+    }
+}
+
 template <int ELEM, int BL>
-hipError_t launch_out(const GemmArgs& p, hipStream_t s) {
+hipError_t launch_out(const GemmArgs& p, hipStream_t s, int tile, int cus) {
     switch (p.out_dtype) {
-        case FKE_OUT_F32: return launch_t<ELEM, BL, FKE_OUT_F32>(p, s);
-        case FKE_OUT_BF16: return launch_t<ELEM, BL, FKE_OUT_BF16>(p, s);
+        case FKE_OUT_F32: return launch_tile<ELEM, BL, FKE_OUT_F32>(p, s, tile, cus);
+        case FKE_OUT_BF16: return launch_tile<ELEM, BL, FKE_OUT_BF16>(p, s, tile, cus);
         default:
-            if constexpr (ELEM == ELEM_I8) return launch_t<ELEM, BL, FKE_OUT_I32>(p, s);
+            if constexpr (ELEM == ELEM_I8) return launch_tile<ELEM, BL, FKE_OUT_I32>(p, s, tile, cus);
             return hipErrorInvalidValue;
     }
 }
 
 }  // namespace
+
+int device_cus() {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < NXCD)
+        cus = 256;
+    return cus;
+}
 
 bool mfma_supports(const GemmArgs& p, int elem) {
     const uintptr_t a = reinterpret_cast<uintptr_t>(p.A), b = reinterpret_cast<uintptr_t>(p.B);
@@ -639,20 +680,42 @@ bool mfma_supports(const GemmArgs& p, int elem) {
     return true;
 }
 
-hipError_t launch_mfma(const GemmArgs& p, int elem, hipStream_t s) {
+// Tile for a shape on `cus` CUs.  The 256x256 tile reads the fewest operand
+// bytes per MFMA and wins whenever its tiles fill the CUs.  Below that, the
+// 128x128 tile wins if its tiles fit one round of two workgroups per CU
+// (4096x1376x4096: 30.0 against 49.2 us; 512x4096x4096: 22.4 against 45.7);
+// a second, partial round of them loses to one 256x256 round (3072x4096x4096:
+// 59.2 against 57.1 us), and so does the 128x128 tile on shapes that fill the
+// CUs (8192^3: 502 against 442 us).  A 256x128 tile (one workgroup per CU)
+// measured slower than 128x128 on every such shape, INT8, FP8 and bf16.
+int mfma_pick_tile(const GemmArgs& p, int cus) {
+    if (p.b_layout == FKE_B_KN) return MFMA_TILE_256x256;
+    const int64_t NO = p.swiglu ? p.N / 2 : p.N;
+    auto tiles = [&](int64_t bm, int64_t bn) {
+        const int64_t tc = p.swiglu ? bn / 2 : bn;
+        return (p.M + bm - 1) / bm * ((NO + tc - 1) / tc);
+    };
+    if (tiles(256, 256) < cus && tiles(128, 128) <= 2 * static_cast<int64_t>(cus)) return MFMA_TILE_128x128;
+    return MFMA_TILE_256x256;
+}
+
+hipError_t launch_mfma(const GemmArgs& p, int elem, hipStream_t s, int tile) {
+    const int cus = device_cus();
+    if (tile == MFMA_TILE_AUTO) tile = mfma_pick_tile(p, cus);
     if (elem == ELEM_F16 || elem == ELEM_BF16) {
         GemmArgs q = p;
         q.K = 2 * p.K;  // the kernel walks K bytes
-        return elem == ELEM_F16 ? launch_out<ELEM_F16, FKE_B_NK>(q, s) : launch_out<ELEM_BF16, FKE_B_NK>(q, s);
+        return elem == ELEM_F16 ? launch_out<ELEM_F16, FKE_B_NK>(q, s, tile, cus)
+                                : launch_out<ELEM_BF16, FKE_B_NK>(q, s, tile, cus);
     }
     if (p.swiglu)
-        return p.out_dtype == FKE_OUT_F32 ? launch_t<ELEM_I8, FKE_B_NK, FKE_OUT_F32, true>(p, s)
-                                          : launch_t<ELEM_I8, FKE_B_NK, FKE_OUT_BF16, true>(p, s);
+        return p.out_dtype == FKE_OUT_F32 ? launch_tile<ELEM_I8, FKE_B_NK, FKE_OUT_F32, true>(p, s, tile, cus)
+                                          : launch_tile<ELEM_I8, FKE_B_NK, FKE_OUT_BF16, true>(p, s, tile, cus);
     if (elem == ELEM_I8)
-        return p.b_layout == FKE_B_NK ? launch_out<ELEM_I8, FKE_B_NK>(p, s)
-                                      : launch_out<ELEM_I8, FKE_B_KN>(p, s);
-    return p.b_layout == FKE_B_NK ? launch_out<ELEM_F8, FKE_B_NK>(p, s)
-                                  : launch_out<ELEM_F8, FKE_B_KN>(p, s);
+        return p.b_layout == FKE_B_NK ? launch_out<ELEM_I8, FKE_B_NK>(p, s, tile, cus)
+                                      : launch_out<ELEM_I8, FKE_B_KN>(p, s, tile, cus);
+    return p.b_layout == FKE_B_NK ? launch_out<ELEM_F8, FKE_B_NK>(p, s, tile, cus)
+                                  : launch_out<ELEM_F8, FKE_B_KN>(p, s, tile, cus);
 }
 
 }  // namespace fke

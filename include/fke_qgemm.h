@@ -59,8 +59,14 @@ enum fke_path {
     FKE_PATH_GEMV = 1,    /* decode family, M<=512 (INT8, NK): weight streamed  */
     FKE_PATH_MFMA = 2,    /* LDS-staged MFMA GEMM (INT8 i32 / FP8 f32 acc)      */
     FKE_PATH_GENERIC = 3, /* any-shape tiled fallback (exact reference order)   */
-    FKE_PATH_GEMV_DOT = 4 /* decode, VALU dot products only (no MFMA): INT8,    */
-                          /* B [N,K], M <= 16, K % 64 == 0 (fke_qgemm_i8*_on_path) */
+    FKE_PATH_GEMV_DOT = 4, /* decode, VALU dot products only (no MFMA): INT8,   */
+                           /* B [N,K], M <= 16, K % 64 == 0 (fke_qgemm_i8*_on_path) */
+    /* The MFMA GEMM with its workgroup tile pinned (FKE_PATH_MFMA picks the
+     * tile by tile count: 128x128 where 256x256 tiles would leave CUs idle,
+     * see fke_select_mfma_tile).  Same results bit for bit; 128x128 takes
+     * B [N,K] only (B [K,N]: hipErrorInvalidValue). */
+    FKE_PATH_MFMA_256x256 = 5,
+    FKE_PATH_MFMA_128x128 = 6
 };
 
 /*
@@ -290,6 +296,11 @@ int fke_select_path_i8_swiglu(const void* A, const void* W, const void* H, int M
                               int out_dtype);
 int fke_select_path_half(const void* A, const void* B, const void* C, int M, int N, int K,
                          int in_dtype, int out_dtype, int b_layout);
+/* The workgroup tile FKE_PATH_MFMA runs for this shape on a GPU of `cus`
+ * CUs (<= 0: the current device's, 256 without a device), as the
+ * FKE_PATH_MFMA_* value that pins it; swiglu != 0 for the fused SwiGLU GEMM
+ * with N = 2I.  Host logic only; launches nothing. */
+int fke_select_mfma_tile(int M, int N, int K, int b_layout, int swiglu, int cus);
 
 /* Replaces flash_engine::print_device_info (reference include/flash_engine.h:29,
  * src/flash_engine_api.cu:7-27): prints the device's properties to stdout. */

@@ -90,16 +90,17 @@ MFMA_SHAPES = [(256, 256, 64), (300, 200, 512), (513, 333, 384), (1, 100, 128), 
 
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
 @pytest.mark.parametrize("shape", MFMA_SHAPES)
-def test_mfma_integer_operands_bit_exact(oracle, dev, dt, shape):
+@pytest.mark.parametrize("tile", ["mfma_256x256", "mfma_128x128"])
+def test_mfma_integer_operands_bit_exact(oracle, dev, dt, shape, tile):
     M, N, K = shape
-    say("half gemm mfma integers", dt, shape)
+    say("half gemm mfma integers", dt, shape, tile)
     a, b = int_operands(M, N, K, 100 + M + N + K)
     A, B = enc(a, dt), enc(b, dt)
     sa, sb, bias = epi_vectors(M, N, 7)
-    got = run(A, B, dt, path="mfma", sa=sa, sb=sb, bias=bias)
+    got = run(A, B, dt, path=tile, sa=sa, sb=sb, bias=bias)
     ref = oracle.gemm_half(A, B, code(dt, oracle), sa, sb, bias=bias, nthreads=NTH)
     same_bits(got, ref, f"{dt} {shape}")
-    gotb = run(A, B, dt, path="mfma", sa=sa, sb=sb, bias=bias, out="bf16")
+    gotb = run(A, B, dt, path=tile, sa=sa, sb=sb, bias=bias, out="bf16")
     same_bits(gotb, enc(ref, "bf16"), f"{dt} {shape} bf16 out")
 
 
@@ -134,6 +135,8 @@ def test_mfma_random_within_bound(oracle, dev, dt, shape):
     assert np.all(err <= bound), f"max err/bound {np.max(err / np.maximum(bound, 1e-30)):.3f}"
     gotb = run(A, B, dt, path="mfma", out="bf16")
     same_bits(gotb, enc(got, "bf16"), "bf16 out = bf16(fp32 out)")
+    for tile in ("mfma_256x256", "mfma_128x128"):  # same K order in both tiles
+        same_bits(run(A, B, dt, path=tile), got, f"{tile} vs auto")
 
 
 @pytest.mark.parametrize("dt", ["f16", "bf16"])

@@ -122,12 +122,19 @@ def test_c1_golden(oracle, dev, path):
 
 # ------------------------------------------------------- kernel families x options
 
-@pytest.mark.parametrize("path", ["mfma", "generic"])
+# Every MFMA tile, pinned (the dispatcher would pick a small one for shapes
+# this size), and the generic kernel.  B [K,N] runs the 256x256 tile only.
+I8_FAMILIES = ["mfma_256x256", "mfma_128x128", "generic"]
+
+
+@pytest.mark.parametrize("path", I8_FAMILIES)
 @pytest.mark.parametrize("layout", ["nk", "kn"])
 @pytest.mark.parametrize("out", ["f32", "bf16", "i32"])
 @pytest.mark.parametrize("opts", ["vec_bias", "scalar"])
 def test_i8_families_ragged(oracle, dev, path, layout, out, opts):
-    M, N, K = 300, 528, 384  # ragged in M and N against the 256x256 tile
+    if layout == "kn" and path == "mfma_128x128":
+        pytest.skip("B [K,N] runs the 256x256 tile only (rejection tested in test_mfma_small_tile_rejects_b_kn)")
+    M, N, K = 300, 528, 384  # ragged in M and N against every tile
     say("i8", path, layout, out, opts, (M, N, K))
     A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 100, layout)
     acc = oracle.w8a8_acc(A, B, oracle.B_NK if layout == "nk" else oracle.B_KN)
@@ -619,6 +626,51 @@ def test_c4_square_full(oracle, dev):
     assert_same(f32, oracle_out(oracle, acc_ref, sa, sb, 1.0, 1.0, None, "f32"), "c4 f32")
 
 
+@pytest.mark.parametrize("tile", ["mfma_128x128", "mfma_256x256"])
+@pytest.mark.parametrize("shape", [(1, 1, 128), (129, 65, 256), (256, 128, 128), (257, 129, 640),
+                                   (513, 1000, 1152), (64, 4000, 256)])
+def test_mfma_tiles_ragged_shapes(oracle, dev, tile, shape):
+    """Both tiles against the oracle, bit-exact, on shapes ragged in M and N
+    against each tile (and exactly one 128x128 tile), every output type,
+    per-row / per-column scales with bias."""
+    M, N, K = shape
+    say("i8 small tile", tile, shape)
+    A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 900 + M + N, "nk", act="normal")
+    acc = oracle.w8a8_acc(A, B)
+    for out in ("i32", "f32", "bf16"):
+        got = gpu_i8(A, B, "nk", out, tile, sa, sb, bias=bias)
+        assert_same(got, oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, out), f"{tile} {shape} {out}")
+
+
+def test_mfma_small_tile_rejects_b_kn(oracle, dev):
+    A, B, sa, sb, _ = inputs_i8(oracle, 64, 64, 128, 950, "kn")
+    with pytest.raises(_lib.FkeError):
+        gpu_i8(A, B, "kn", "f32", "mfma_128x128", sa, sb)
+
+
+@pytest.mark.parametrize("M,N,K,out,want", [
+    (4096, 1376, 4096, "bf16", _lib.PATH_MFMA_128x128),   # 8-way column shard of 11008
+    (8192, 1024, 8192, "f32", _lib.PATH_MFMA_128x128),    # 8-way column shard of 8192
+    (512, 4096, 4096, "bf16", _lib.PATH_MFMA_128x128),    # a short prefill
+])
+def test_mfma_few_tile_shapes_full(oracle, dev, M, N, K, out, want):
+    """Shapes with fewer 256x256 tiles than CUs: the tile the dispatcher picks
+    on this GPU, every output against the oracle, and equal to the other
+    tiles' outputs bit for bit."""
+    L = _lib.lib()
+    pick = L.fke_select_mfma_tile(M, N, K, 0, 0, 0)
+    say("few-tile shape", M, N, K, out, "tile path", pick)
+    if L.fke_select_mfma_tile(M, N, K, 0, 0, 256) == want:
+        assert torch.cuda.get_device_properties(0).multi_processor_count != 256 or pick == want
+    A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 4000 + N)
+    acc = oracle.w8a8_acc(A, B, nthreads=NTH)
+    ref = oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, out)
+    got = gpu_i8(A, B, "nk", out, "auto", sa, sb, bias=bias)
+    assert_same(got, ref, f"auto {M}x{N}x{K}")
+    for tile in ("mfma_256x256", "mfma_128x128"):
+        assert_same(gpu_i8(A, B, "nk", out, tile, sa, sb, bias=bias), ref, f"{tile} {M}x{N}x{K}")
+
+
 # ---------------------------------------------------------------------- FP8
 
 def f8_inputs(oracle, M, N, K, seed, layout="kn", with_nan_codes=False):
@@ -688,16 +740,20 @@ def test_fp8_generic_bit_exact(oracle, dev, layout, shape):
 @pytest.mark.parametrize("out", ["f32", "bf16"])
 @pytest.mark.parametrize("nan_codes", [False, True])
 def test_fp8_mfma_tolerance(oracle, dev, layout, out, nan_codes):
+    """Every tile (B [N,K]; B [K,N] has the 256x256 one) within the FP8 bounds,
+    and the smaller tiles equal to the 256x256 tile bit for bit: each output
+    is summed over K in the same order whatever the tile."""
     M, N, K = 300, 528, 1024
     say("fp8 mfma", layout, out, nan_codes)
     A, B, sa, sb = f8_inputs(oracle, M, N, K, 700, layout, with_nan_codes=nan_codes)
     bias = oracle.gen_f32_normal((N,), 701, 0.0, 0.02)
     code = oracle.B_KN if layout == "kn" else oracle.B_NK
     ref = oracle.f8_gemm(A, B, sa, sb, bias=bias, b_layout=code)
-    got = gpu_f8(A, B, sa, sb, layout, out, "mfma", bias=bias)
-    if out == "bf16":
-        got = oracle.bf16_to_f32(got)
-    assert_fp8_close(got, ref, out, f"mfma {layout} nan={nan_codes}")
+    big = gpu_f8(A, B, sa, sb, layout, out, "mfma_256x256", bias=bias)
+    got = oracle.bf16_to_f32(big) if out == "bf16" else big
+    assert_fp8_close(got, ref, out, f"mfma 256x256 {layout} nan={nan_codes}")
+    if layout == "nk":
+        assert_same(gpu_f8(A, B, sa, sb, layout, out, "mfma_128x128", bias=bias), big, "fp8 128x128 vs 256x256")
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 300, 4096), (3, 1000, 2048), (16, 777, 5056), (16, 4096, 14336),
