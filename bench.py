@@ -84,6 +84,9 @@ def parse():
                          "VALU dot-product kernels (FKE_PATH_GEMV_DOT), for the choice between them")
     ap.add_argument("--shards", action="store_true",
                     help="also time the per-GPU shards of 8-way tensor parallelism (part of --extra)")
+    ap.add_argument("--tile-sweep", action="store_true",
+                    help="also time both MFMA GEMM tiles (256x256, 128x128) on shapes around the dispatcher's "
+                         "tile rule, INT8, FP8 and bf16 (B [N,K]), beside the tile it picks")
     ap.add_argument("--data-sweep", action="store_true",
                     help="also time the headline GEMM on zero, constant and narrow-range operands (clock vs data)")
     ap.add_argument("--vendor", action="store_true",
@@ -232,6 +235,8 @@ def main():
         line["vendor_context"] = vendor_configs(torch, dev, gen, timed, args)
     if args.data_sweep:
         line["data_sweep"] = data_sweep(torch, L, _lib, dev, gen, timed, args)
+    if args.tile_sweep:
+        line["tile_sweep"] = tile_sweep(torch, L, _lib, dev, gen, timed, args)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(line), flush=True)
@@ -542,7 +547,7 @@ def shard_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
                                           sb.data_ptr(), 1.0, 1.0, None, out, _lib.B_NK, sh),
                    args.steps, args.warmup)
         t = 2.0 * M * N * K / (ms * 1e-3) / 1e12
-        tile = L.fke_select_mfma_tile(M, N, K, _lib.B_NK, 0, 0)
+        tile = L.fke_select_mfma_tile(M, N, K, 1, _lib.B_NK, 0, 0)
         res[name] = {"ms": round(ms, 4), "TOPS": round(t, 1), "frac": round(t / PEAK_INT8_TOPS, 4),
                      "tile": tiles.get(tile, str(tile))}
         if tile != _lib.PATH_MFMA_256x256:  # the 256x256 tile on the same shape, for comparison
@@ -551,6 +556,59 @@ def shard_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
                                                        1.0, None, out, _lib.B_NK, sh), args.steps, args.warmup)
             res[name]["ms_256x256_tile"] = round(ms2, 4)
         del A, B, C
+    return res
+
+
+# Shapes around the MFMA tile rule (B [N,K]): 256x256 tiles / 128x128 tiles.
+TILE_SWEEP_SHAPES = [
+    (256, 4096, 4096), (512, 4096, 4096), (1024, 4096, 4096), (2048, 4096, 4096),  # 16..128 / 64..512
+    (3072, 4096, 4096), (4096, 4096, 4096),                                          # 192 / 768, 256 / 1024
+    (4096, 512, 4096), (2048, 1376, 4096), (4096, 1376, 4096), (4096, 2048, 4096),   # 32..128 / 128..512
+    (4096, 3584, 4096), (512, 14336, 4096), (1024, 14336, 4096),                     # 224 / 896, 112 / 448, 224
+    (8192, 1024, 8192), (8192, 8192, 1024), (4096, 11008, 4096),                     # 128 / 512, 1024, 688
+    (8192, 8192, 512), (8192, 8192, 2048), (4096, 4096, 1024), (4096, 4096, 2048),   # short K, many tiles
+    (4096, 11008, 1024), (4096, 11008, 2048), (16384, 8192, 1024)]
+
+
+def tile_sweep(torch, L, _lib, dev, gen, timed, args):
+    """Both MFMA tiles pinned (FKE_PATH_MFMA_256x256 / _128x128) on each shape, INT8 and FP8 with bf16 out and
+    bf16 operands with bf16 out, against the tile fke_select_mfma_tile picks."""
+    sh = torch.cuda.current_stream(dev).cuda_stream
+    names = {_lib.PATH_MFMA_256x256: "256x256", _lib.PATH_MFMA_128x128: "128x128"}
+    res = {}
+    for (M, N, K) in TILE_SWEEP_SHAPES:
+        C = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        sa = torch.rand(M, device=dev, generator=gen)
+        sb = torch.rand(N, device=dev, generator=gen)
+        for elem in ("i8", "f8", "bf16"):
+            if elem == "bf16":
+                A = torch.randn((M, K), device=dev, generator=gen).to(torch.bfloat16)
+                B = torch.randn((N, K), device=dev, generator=gen).to(torch.bfloat16)
+            else:
+                A = torch.randint(-127, 128, (M, K), dtype=torch.int8, device=dev, generator=gen)
+                B = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=gen)
+                if elem == "f8":  # no NaN codes (those rerun a tile)
+                    A[(A & 0x7F) == 0x7F] = 0
+                    B[(B & 0x7F) == 0x7F] = 0
+            row = {"pick": names[L.fke_select_mfma_tile(M, N, K, 2 if elem == "bf16" else 1, _lib.B_NK, 0, 0)]}
+            for path, name in names.items():
+                if elem == "i8":
+                    fn = lambda: L.fke_qgemm_i8_on_path(path, A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K,
+                                                        sa.data_ptr(), sb.data_ptr(), 1.0, 1.0, None, _lib.OUT_BF16,
+                                                        _lib.B_NK, sh)
+                elif elem == "f8":
+                    fn = lambda: L.fke_qgemm_f8_on_path(path, A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K,
+                                                        0.01, 0.01, None, _lib.OUT_BF16, _lib.B_NK, sh)
+                else:
+                    fn = lambda: L.fke_gemm_half_on_path(path, A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K,
+                                                         _lib.IN_BF16, sa.data_ptr(), sb.data_ptr(), 1.0, 1.0, None,
+                                                         _lib.OUT_BF16, _lib.B_NK, sh)
+                if fn() != 0:
+                    raise RuntimeError(f"tile sweep: {elem} {name} {M}x{N}x{K} rejected")
+                row[f"us_{name}"] = round(timed(fn, 20, 5) * 1e3, 2)
+            res[f"{elem}_{M}x{N}x{K}_bf16"] = row
+            del A, B
+        del C
     return res
 
 

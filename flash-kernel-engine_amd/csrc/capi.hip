@@ -441,13 +441,17 @@ int fke_select_path_half(const void* A, const void* B, const void* C, int M, int
                      half_elem(in_dtype));
 }
 
-int fke_select_mfma_tile(int M, int N, int K, int b_layout, int swiglu, int cus) {
-    if (M < 1 || N < 1 || K < 1 || (b_layout != FKE_B_NK && b_layout != FKE_B_KN) || (swiglu && N % 2)) return -1;
+int fke_select_mfma_tile(int M, int N, int K, int operand_bytes, int b_layout, int swiglu, int cus) {
+    if (M < 1 || N < 1 || K < 1 || (operand_bytes != 1 && operand_bytes != 2) ||
+        (b_layout != FKE_B_NK && b_layout != FKE_B_KN) || (swiglu && N % 2))
+        return -1;
     GemmArgs p = make_args(nullptr, nullptr, nullptr, M, N, K, nullptr, nullptr, 1.f, 1.f, nullptr, FKE_OUT_F32,
                            b_layout);
     p.swiglu = swiglu ? 1 : 0;
     if (cus <= 0) cus = fke::device_cus();
-    return fke::mfma_pick_tile(p, cus) == fke::MFMA_TILE_128x128 ? FKE_PATH_MFMA_128x128 : FKE_PATH_MFMA_256x256;
+    const int elem = operand_bytes == 1 ? fke::ELEM_I8 : fke::ELEM_BF16;  // the rule depends on the width only
+    return fke::mfma_pick_tile(p, elem, cus) == fke::MFMA_TILE_128x128 ? FKE_PATH_MFMA_128x128
+                                                                       : FKE_PATH_MFMA_256x256;
 }
 
 // Reference src/tensor_core_attention.cu:13-86 (launch_wmma_gemm_fp16): A fp16

@@ -39,7 +39,7 @@ hipError_t launch_gemv_i8(const GemmArgs& p, hipStream_t stream);
 // [K,N] always runs 256x256.
 enum MfmaTile { MFMA_TILE_AUTO = 0, MFMA_TILE_256x256 = 1, MFMA_TILE_128x128 = 2 };
 hipError_t launch_mfma(const GemmArgs& p, int elem, hipStream_t stream, int tile = MFMA_TILE_AUTO);
-int mfma_pick_tile(const GemmArgs& p, int cus);
+int mfma_pick_tile(const GemmArgs& p, int elem, int cus);
 // CUs of the current device (256 without one).
 int device_cus();
 hipError_t launch_quant_rows(const void* X, int in_dtype, int M, int K, int8_t* Q, float* S,

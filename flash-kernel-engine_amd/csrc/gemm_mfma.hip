@@ -680,16 +680,27 @@ bool mfma_supports(const GemmArgs& p, int elem) {
     return true;
 }
 
-// Tile for a shape on `cus` CUs.  The 256x256 tile reads the fewest operand
-// bytes per MFMA and wins whenever its tiles fill the CUs.  Below that, the
-// 128x128 tile wins if its tiles fit one round of two workgroups per CU
-// (4096x1376x4096: 30.0 against 49.2 us; 512x4096x4096: 22.4 against 45.7);
-// a second, partial round of them loses to one 256x256 round (3072x4096x4096:
-// 59.2 against 57.1 us), and so does the 128x128 tile on shapes that fill the
-// CUs (8192^3: 502 against 442 us).  A 256x128 tile (one workgroup per CU)
-// measured slower than 128x128 on every such shape, INT8, FP8 and bf16.
-int mfma_pick_tile(const GemmArgs& p, int cus) {
+// Tile for a shape on `cus` CUs (measured on 16 INT8 / FP8 / bf16 shapes per
+// rule, B [N,K]).
+// - The 256x256 tile reads the fewest operand bytes per MFMA and wins on long
+//   K whenever its tiles fill the CUs (8192^3: 442 against 502 us; C3
+//   4096x11008x4096: 171 against 180).
+// - Short K: a tile's prologue (first stage in flight) and epilogue (its
+//   stores) are a large share of its time, and two 128x128 workgroups per CU
+//   overlap one's with the other's K loop: 128x128 wins at K <= 2048 bytes
+//   with 8-bit operands (4096x4096x1024 INT8: 24.8 against 32.7 us;
+//   8192x8192x2048: 140 against 146) and at K <= 1024 bytes with 16-bit ones
+//   (at 2048 bytes bf16 varies by shape, -7 to +4 %).
+// - Few tiles: 128x128 wins when 256x256 tiles would leave CUs idle and its
+//   own fit one round of two workgroups per CU (4096x1376x4096: 28 against
+//   46 us); a second, partial round of them loses (3072x4096x4096: 57.4
+//   against 55.0 us).
+// A 256x128 tile (one workgroup per CU) measured slower than 128x128 on every
+// few-tile shape, INT8, FP8 and bf16.
+int mfma_pick_tile(const GemmArgs& p, int elem, int cus) {
     if (p.b_layout == FKE_B_KN) return MFMA_TILE_256x256;
+    const int64_t kb = static_cast<int64_t>(p.K) * elem_bytes(elem);
+    if (kb <= (elem_bytes(elem) == 1 ? 2048 : 1024)) return MFMA_TILE_128x128;
     const int64_t NO = p.swiglu ? p.N / 2 : p.N;
     auto tiles = [&](int64_t bm, int64_t bn) {
         const int64_t tc = p.swiglu ? bn / 2 : bn;
@@ -701,7 +712,7 @@ int mfma_pick_tile(const GemmArgs& p, int cus) {
 
 hipError_t launch_mfma(const GemmArgs& p, int elem, hipStream_t s, int tile) {
     const int cus = device_cus();
-    if (tile == MFMA_TILE_AUTO) tile = mfma_pick_tile(p, cus);
+    if (tile == MFMA_TILE_AUTO) tile = mfma_pick_tile(p, elem, cus);
     if (elem == ELEM_F16 || elem == ELEM_BF16) {
         GemmArgs q = p;
         q.K = 2 * p.K;  // the kernel walks K bytes

@@ -90,9 +90,9 @@ int main(void) {
                     CHECK(ws == 0 || (lay == FKE_B_KN && M <= 16 && ws % row == 0 && ws / row >= 2 && ws / row <= 8));
                     ++n_ws;
                     /* MFMA tile: 128x128 for B [N,K] only; -1 only for an odd SwiGLU N */
-                    for (int sw = 0; sw < 2; ++sw) {
-                        const int t = fke_select_mfma_tile(M, N, K, lay, sw, 256);
-                        CHECK(t == -1 ? (sw && N % 2)
+                    for (int sw = 0; sw < 4; ++sw) {
+                        const int t = fke_select_mfma_tile(M, N, K, 1 + (sw >> 1), lay, sw & 1, 256);
+                        CHECK(t == -1 ? ((sw & 1) && N % 2)
                                       : (t == FKE_PATH_MFMA_256x256 || (t == FKE_PATH_MFMA_128x128 && lay == FKE_B_NK)));
                         if (t >= 0) ++n_tiles[t == FKE_PATH_MFMA_128x128];
                     }

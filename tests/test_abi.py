@@ -343,28 +343,35 @@ def test_torch_extension_rejects_host_tensors():
         m.quantized_gemm_int8_swiglu_forward(a, a)
 
 
-@pytest.mark.parametrize("M,N,K,layout,swiglu,cus,want", [
-    (8192, 8192, 8192, 0, 0, 256, _lib.PATH_MFMA_256x256),   # 1024 tiles
-    (4096, 11008, 4096, 0, 0, 256, _lib.PATH_MFMA_256x256),  # 688 tiles
-    (4096, 1376, 4096, 0, 0, 256, _lib.PATH_MFMA_128x128),   # 96 tiles of 256x256, 352 of 128x128
-    (8192, 1024, 8192, 0, 0, 256, _lib.PATH_MFMA_128x128),   # 128 / 512: one round of two per CU
-    (512, 4096, 4096, 0, 0, 256, _lib.PATH_MFMA_128x128),    # 32 / 128
-    (3072, 4096, 4096, 0, 0, 256, _lib.PATH_MFMA_256x256),   # 192 / 768: a second, partial round
-    (1024, 14336, 4096, 0, 0, 256, _lib.PATH_MFMA_256x256),  # 224 / 896
-    (4096, 1376, 4096, 1, 0, 256, _lib.PATH_MFMA_256x256),   # B [K,N]: 256x256 only
-    (4096, 1376, 4096, 0, 1, 256, _lib.PATH_MFMA_128x128),   # SwiGLU, 688 outputs: 96 tiles / 352
-    (4096, 2752, 4096, 0, 1, 256, _lib.PATH_MFMA_256x256),   # SwiGLU, 1376 outputs: 176 / 704
-    (4096, 1376, 4096, 0, 0, 80, _lib.PATH_MFMA_256x256),    # fills 80 CUs
+@pytest.mark.parametrize("M,N,K,nbytes,layout,swiglu,cus,want", [
+    (8192, 8192, 8192, 1, 0, 0, 256, _lib.PATH_MFMA_256x256),   # 1024 tiles
+    (4096, 11008, 4096, 1, 0, 0, 256, _lib.PATH_MFMA_256x256),  # 688 tiles
+    (4096, 1376, 4096, 1, 0, 0, 256, _lib.PATH_MFMA_128x128),   # 96 tiles of 256x256, 352 of 128x128
+    (8192, 1024, 8192, 1, 0, 0, 256, _lib.PATH_MFMA_128x128),   # 128 / 512: one round of two per CU
+    (512, 4096, 4096, 1, 0, 0, 256, _lib.PATH_MFMA_128x128),    # 32 / 128
+    (3072, 4096, 4096, 1, 0, 0, 256, _lib.PATH_MFMA_256x256),   # 192 / 768: a second, partial round
+    (1024, 14336, 4096, 1, 0, 0, 256, _lib.PATH_MFMA_256x256),  # 224 / 896
+    (8192, 8192, 2048, 1, 0, 0, 256, _lib.PATH_MFMA_128x128),   # short K, 8-bit: <= 2048 bytes
+    (8192, 8192, 2049, 1, 0, 0, 256, _lib.PATH_MFMA_256x256),
+    (8192, 8192, 512, 2, 0, 0, 256, _lib.PATH_MFMA_128x128),    # short K, 16-bit: <= 1024 bytes
+    (8192, 8192, 1024, 2, 0, 0, 256, _lib.PATH_MFMA_256x256),
+    (4096, 1376, 4096, 2, 0, 0, 256, _lib.PATH_MFMA_128x128),   # few tiles, bf16
+    (4096, 1376, 4096, 1, 1, 0, 256, _lib.PATH_MFMA_256x256),   # B [K,N]: 256x256 only
+    (4096, 4096, 1024, 1, 1, 0, 256, _lib.PATH_MFMA_256x256),
+    (4096, 1376, 4096, 1, 0, 1, 256, _lib.PATH_MFMA_128x128),   # SwiGLU, 688 outputs: 96 tiles / 352
+    (4096, 2752, 4096, 1, 0, 1, 256, _lib.PATH_MFMA_256x256),   # SwiGLU, 1376 outputs: 176 / 704
+    (4096, 1376, 4096, 1, 0, 0, 80, _lib.PATH_MFMA_256x256),    # fills 80 CUs
 ])
-def test_mfma_tile_choice(M, N, K, layout, swiglu, cus, want):
-    assert _lib.lib().fke_select_mfma_tile(M, N, K, layout, swiglu, cus) == want
+def test_mfma_tile_choice(M, N, K, nbytes, layout, swiglu, cus, want):
+    assert _lib.lib().fke_select_mfma_tile(M, N, K, nbytes, layout, swiglu, cus) == want
 
 
 def test_mfma_tile_choice_rejects_bad_arguments():
     L = _lib.lib()
-    assert L.fke_select_mfma_tile(0, 64, 64, 0, 0, 256) == -1
-    assert L.fke_select_mfma_tile(64, 64, 64, 2, 0, 256) == -1
-    assert L.fke_select_mfma_tile(64, 63, 64, 0, 1, 256) == -1
+    assert L.fke_select_mfma_tile(0, 64, 64, 1, 0, 0, 256) == -1
+    assert L.fke_select_mfma_tile(64, 64, 64, 1, 2, 0, 256) == -1
+    assert L.fke_select_mfma_tile(64, 63, 64, 1, 0, 1, 256) == -1
+    assert L.fke_select_mfma_tile(64, 64, 64, 4, 0, 0, 256) == -1
 
 
 def test_pinned_small_tile_rejects_b_kn_before_any_launch():

@@ -652,16 +652,18 @@ def test_mfma_small_tile_rejects_b_kn(oracle, dev):
     (4096, 1376, 4096, "bf16", _lib.PATH_MFMA_128x128),   # 8-way column shard of 11008
     (8192, 1024, 8192, "f32", _lib.PATH_MFMA_128x128),    # 8-way column shard of 8192
     (512, 4096, 4096, "bf16", _lib.PATH_MFMA_128x128),    # a short prefill
+    (4096, 4096, 1024, "f32", _lib.PATH_MFMA_128x128),    # short K: 1024 tiles
+    (8192, 8192, 1024, "i32", _lib.PATH_MFMA_128x128),    # 8-way K shard of 8192^3 (int32 partials)
 ])
 def test_mfma_few_tile_shapes_full(oracle, dev, M, N, K, out, want):
-    """Shapes with fewer 256x256 tiles than CUs: the tile the dispatcher picks
-    on this GPU, every output against the oracle, and equal to the other
-    tiles' outputs bit for bit."""
+    """Shapes the dispatcher gives the 128x128 tile (fewer 256x256 tiles than
+    CUs, or short K): the tile it picks on this GPU, every output against the
+    oracle, and the same outputs from both pinned tiles."""
     L = _lib.lib()
-    pick = L.fke_select_mfma_tile(M, N, K, 0, 0, 0)
+    pick = L.fke_select_mfma_tile(M, N, K, 1, 0, 0, 0)
     say("few-tile shape", M, N, K, out, "tile path", pick)
-    if L.fke_select_mfma_tile(M, N, K, 0, 0, 256) == want:
-        assert torch.cuda.get_device_properties(0).multi_processor_count != 256 or pick == want
+    assert L.fke_select_mfma_tile(M, N, K, 1, 0, 0, 256) == want
+    assert torch.cuda.get_device_properties(0).multi_processor_count != 256 or pick == want
     A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 4000 + N)
     acc = oracle.w8a8_acc(A, B, nthreads=NTH)
     ref = oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, out)
