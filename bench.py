@@ -44,8 +44,15 @@ PEAK_HBM_GBS = 8000.0     # MI355X HBM3E, published (8 TB/s)
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic.json")
 
 
-def gemv_kernel(M):
-    """Decode kernel the dispatcher picks for M rows (K % 4096 == 0, B [N,K])."""
+TILE_LABELS = {5: "256x256", 6: "128x128", 7: "128x128_ring4"}
+
+
+def gemv_kernel(L, _lib, M, N=14336, K=4096):
+    """Kernel the dispatcher picks for an M-row INT8 batch on B [N,K] (K % 4096 == 0): the decode
+    family's, or the MFMA GEMM's with its tile."""
+    path = L.fke_select_path_i8(4096, 4096, 4096, M, N, K, _lib.OUT_BF16, _lib.B_NK)
+    if path == _lib.PATH_MFMA:
+        return f"gemm_mfma_kernel<i8,NK,bf16,{TILE_LABELS[L.fke_select_mfma_tile(M, N, K, 1, _lib.B_NK, 0, 0)]}>"
     return "gemv_rows_kernel" if M <= 2 else "gemv_lds_kernel"
 
 
@@ -85,7 +92,7 @@ def parse():
     ap.add_argument("--shards", action="store_true",
                     help="also time the per-GPU shards of 8-way tensor parallelism (part of --extra)")
     ap.add_argument("--tile-sweep", action="store_true",
-                    help="also time both MFMA GEMM tiles (256x256, 128x128) on shapes around the dispatcher's "
+                    help="also time every MFMA GEMM tile (256x256, 128x128, 128x128 four-stage ring) on shapes around the dispatcher's "
                          "tile rule, INT8, FP8 and bf16 (B [N,K]), beside the tile it picks")
     ap.add_argument("--data-sweep", action="store_true",
                     help="also time the headline GEMM on zero, constant and narrow-range operands (clock vs data)")
@@ -510,7 +517,7 @@ def gemv_bench(torch, L, _lib, dev, gen, M, nbuf, launches, N=14336, K=4096, lay
     eager = eager_us(torch, dev, launch, launches)
     nbytes = gemv_bytes(M, N, K)
     gbs = nbytes / (us * 1e-6) / 1e9
-    kernel = gemv_kernel(M) if layout == "nk" else "gemv_kn_split_kernel<i8>+kn_reduce_kernel<i8,bf16>"
+    kernel = gemv_kernel(L, _lib, M, N, K) if layout == "nk" else "gemv_kn_split_kernel<i8>+kn_reduce_kernel<i8,bf16>"
     return {"metric": f"HBM GB/s, decode GEMV M={M} N={N} K={K}, B {'[N,K]' if layout == 'nk' else '[K,N]'} "
                       f"(bf16 out, fused bias)",
             "value": round(gbs, 1), "unit": "GB/s", "us_per_launch": round(us, 3),
@@ -571,10 +578,12 @@ TILE_SWEEP_SHAPES = [
 
 
 def tile_sweep(torch, L, _lib, dev, gen, timed, args):
-    """Both MFMA tiles pinned (FKE_PATH_MFMA_256x256 / _128x128) on each shape, INT8 and FP8 with bf16 out and
-    bf16 operands with bf16 out, against the tile fke_select_mfma_tile picks."""
+    """Every MFMA tile pinned (FKE_PATH_MFMA_256x256 / _128x128 / _128x128_RING4) on each shape, INT8 and FP8
+    with bf16 out and bf16 operands with bf16 out, against the tile fke_select_mfma_tile picks.  The operands
+    stay the same from launch to launch (cache-warm)."""
     sh = torch.cuda.current_stream(dev).cuda_stream
-    names = {_lib.PATH_MFMA_256x256: "256x256", _lib.PATH_MFMA_128x128: "128x128"}
+    names = {_lib.PATH_MFMA_256x256: "256x256", _lib.PATH_MFMA_128x128: "128x128",
+             _lib.PATH_MFMA_128x128_RING4: "128x128_ring4"}
     res = {}
     for (M, N, K) in TILE_SWEEP_SHAPES:
         C = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
@@ -613,11 +622,11 @@ def tile_sweep(torch, L, _lib, dev, gen, timed, args):
 
 
 def batch_configs(torch, L, _lib, dev, gen, args):
-    """Batched decode on the decode weights (N = 14336, K = 4096): 32, 64 and 128 rows, which
-    the dispatcher gives to the LDS-streamed kernel with 2 / 4 activation blocks (128 rows as
-    two 64-row workgroup rows)."""
+    """Batched decode on the decode weights (N = 14336, K = 4096): 32, 64, 128 and 256 rows. The
+    dispatcher gives 32 and 64 to the LDS-streamed kernel (2 / 4 activation blocks) and 128 and 256
+    to the MFMA GEMM's 4-stage 128x128 ring (one tile per CU); each line names its kernel."""
     return {f"gemv_M{m}": gemv_bench(torch, L, _lib, dev, gen, m, args.gemv_buffers, args.gemv_launches)
-            for m in (32, 64, 128)}
+            for m in (32, 64, 128, 256)}
 
 
 def extra_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):

@@ -207,6 +207,7 @@ int mfma_tile_of_path(int path, const GemmArgs& p) {
         case FKE_PATH_MFMA: return fke::MFMA_TILE_AUTO;
         case FKE_PATH_MFMA_256x256: return fke::MFMA_TILE_256x256;
         case FKE_PATH_MFMA_128x128: return p.b_layout == FKE_B_NK ? fke::MFMA_TILE_128x128 : -2;
+        case FKE_PATH_MFMA_128x128_RING4: return p.b_layout == FKE_B_NK ? fke::MFMA_TILE_128x128_RING4 : -2;
         default: return -1;
     }
 }
@@ -228,7 +229,8 @@ int run_i8(int path, const GemmArgs& p, void* stream, const KnWorkspace* ws) {
             return fke::launch_gemv_i8(p, s);
         case FKE_PATH_MFMA:
         case FKE_PATH_MFMA_256x256:
-        case FKE_PATH_MFMA_128x128: return run_mfma(path, p, fke::ELEM_I8, s);
+        case FKE_PATH_MFMA_128x128:
+        case FKE_PATH_MFMA_128x128_RING4: return run_mfma(path, p, fke::ELEM_I8, s);
         case FKE_PATH_GENERIC: return fke::launch_generic(p, fke::ELEM_I8, s);
         case FKE_PATH_GEMV_DOT:
             if (!fke::gemv_dot_supports(p)) return hipErrorInvalidValue;
@@ -256,7 +258,8 @@ int run_half(int path, const GemmArgs& p, int elem, void* stream) {
     switch (path) {
         case FKE_PATH_MFMA:
         case FKE_PATH_MFMA_256x256:
-        case FKE_PATH_MFMA_128x128: return run_mfma(path, p, elem, s);
+        case FKE_PATH_MFMA_128x128:
+        case FKE_PATH_MFMA_128x128_RING4: return run_mfma(path, p, elem, s);
         case FKE_PATH_GENERIC: return fke::launch_generic(p, elem, s);
         default: return hipErrorInvalidValue;
     }
@@ -272,7 +275,8 @@ int run_f8(int path, const GemmArgs& p, void* stream, const KnWorkspace* ws = nu
             return fke::launch_gemv_f8(p, s);
         case FKE_PATH_MFMA:
         case FKE_PATH_MFMA_256x256:
-        case FKE_PATH_MFMA_128x128: return run_mfma(path, p, fke::ELEM_F8, s);
+        case FKE_PATH_MFMA_128x128:
+        case FKE_PATH_MFMA_128x128_RING4: return run_mfma(path, p, fke::ELEM_F8, s);
         case FKE_PATH_GENERIC: return fke::launch_generic(p, fke::ELEM_F8, s);
         default: return hipErrorInvalidValue;
     }
@@ -450,8 +454,11 @@ int fke_select_mfma_tile(int M, int N, int K, int operand_bytes, int b_layout, i
     p.swiglu = swiglu ? 1 : 0;
     if (cus <= 0) cus = fke::device_cus();
     const int elem = operand_bytes == 1 ? fke::ELEM_I8 : fke::ELEM_BF16;  // the rule depends on the width only
-    return fke::mfma_pick_tile(p, elem, cus) == fke::MFMA_TILE_128x128 ? FKE_PATH_MFMA_128x128
-                                                                       : FKE_PATH_MFMA_256x256;
+    switch (fke::mfma_pick_tile(p, elem, cus)) {
+        case fke::MFMA_TILE_128x128: return FKE_PATH_MFMA_128x128;
+        case fke::MFMA_TILE_128x128_RING4: return FKE_PATH_MFMA_128x128_RING4;
+        default: return FKE_PATH_MFMA_256x256;
+    }
 }
 
 // Reference src/tensor_core_attention.cu:13-86 (launch_wmma_gemm_fp16): A fp16

@@ -42,6 +42,7 @@
 // bias) are staged once in LDS beside the two stages.
 #include "fke_internal.h"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace fke {
@@ -57,20 +58,24 @@ constexpr int NWAVES = 4;
 constexpr int NTHREADS = NWAVES * 64;
 
 // Workgroup tile: each of the 4 waves (2x2) owns NI x NJ MFMA blocks of 32x32
-// (written for NI, NJ in {2, 4}; built as 4x4 and 2x2).
-template <int NI_, int NJ_>
+// (written for NI, NJ in {2, 4}; built as 4x4 and 2x2), with a ring of NS LDS
+// stages (2 or 4: the copy of stage k + NS - 1 is issued while stage k runs).
+template <int NI_, int NJ_, int NS_ = 2>
 struct Tile {
-    static constexpr int NI = NI_, NJ = NJ_;
+    static constexpr int NI = NI_, NJ = NJ_, NS = NS_;
+    static_assert(NS == 2 || NS == 4, "ring of 2 or 4 stages");
     static constexpr int BM = 64 * NI, BN = 64 * NJ;  // tile rows, B columns (B rows of [N,K])
     static constexpr int WM = 32 * NI, WN = 32 * NJ;  // one wave's rows, columns
     static constexpr int STAGE_A = BM * BK;           // A part of one LDS stage
     static constexpr int STAGE = (BM + BN) * BK;      // one LDS stage
     static constexpr int PWA = BM / 32, PWB = BN / 32;  // 1-KiB DMA loads per wave per stage
     static constexpr int NPIECE = NI * NJ;            // MFMAs per k step
-    static constexpr int OCC = NI * NJ <= 4 ? 2 : 1;  // workgroups per CU
+    static constexpr int OCC = NS == 2 && NI * NJ <= 4 ? 2 : 1;  // workgroups per CU
+    static_assert(NS * STAGE <= 128 * 1024, "the stages fit the CU's LDS beside the epilogue operands");
 };
 using T256 = Tile<4, 4>;
 using T128 = Tile<2, 2>;
+using T128R4 = Tile<2, 2, 4>;  // one workgroup per CU, three stages in flight
 
 __device__ __forceinline__ int swz(int r) { return ((r & 31) ^ ((r & 31) >> 3)) & 7; }
 
@@ -325,6 +330,8 @@ __global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p
     constexpr int NI = TL::NI, NJ = TL::NJ, BM = TL::BM, NPIECE = TL::NPIECE;
     __shared__ __attribute__((aligned(1024))) uint8_t lds0[TL::STAGE];
     __shared__ __attribute__((aligned(1024))) uint8_t lds1[TL::STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds2[TL::NS > 2 ? TL::STAGE : 16];  // NS = 4 only
+    __shared__ __attribute__((aligned(1024))) uint8_t lds3[TL::NS > 2 ? TL::STAGE : 16];
     __shared__ __attribute__((aligned(16))) float epi_sa[BM];        // scale of each tile row
     __shared__ __attribute__((aligned(16))) float epi_sb[TL::BN];    // scale of each tile column
     __shared__ __attribute__((aligned(16))) float epi_bias[TL::BN];  // bias of each tile column
@@ -433,8 +440,12 @@ __global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p
     };
     using I0 = std::integral_constant<int, 0>;
     using F = std::false_type;
+    // Stage kt: MFMAs on `cur` while stage kt + NS - 1 is copied into `nxt`.
+    // Past the end the last stage is copied again (into a buffer whose stage
+    // is done), so the body has no data-dependent branch.
+    constexpr int NS = TL::NS;
     auto stage = [&](auto sanc, const uint8_t* cur, uint8_t* nxt, int kt) __attribute__((always_inline)) {
-        const int kc = min(kt + 1, KT - 1);  // the last stage re-copies itself
+        const int kc = min(kt + NS - 1, KT - 1);
         using S = decltype(sanc);
         if constexpr (NKS == 4) {
             constexpr int P = PER_GROUP, P2 = 2 * P < NSLOT ? 2 * P : NSLOT;
@@ -457,33 +468,52 @@ __global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p
             group(S{}, std::integral_constant<int, P>{}, std::integral_constant<int, NSLOT>{}, f0, f1, cur, 1, nxt,
                   kc);
         }
-        wait_lgkm0();  // last step's fragments in registers (f1): cur may be overwritten after the barrier
-        wait_vm0();    // this wave's share of stage kt+1 has landed
+        wait_lgkm0();                  // last step's fragments in registers (f1): cur may be overwritten after the barrier
+        wait_vm<(NS - 2) * NSLOT>();   // this wave's share of stage kt+1 has landed (later stages may be in flight)
         barrier();
     };
 
-    // The whole K loop.  Buffer roles are static (lds0 / lds1 are distinct
-    // objects, so the compiler sees that a stage's DMA never aliases the
-    // other stage's reads), hence two stages per iteration; the body has no
+    // The whole K loop.  Buffer roles are static (lds0..lds3 are distinct
+    // objects, so the compiler sees that a stage's DMA never aliases another
+    // stage's reads), hence NS stages per iteration; the body has no
     // data-dependent branches, so the accumulators stay in AGPRs.
     auto k_loop = [&](auto sanc) __attribute__((always_inline)) {
         using S = decltype(sanc);
-        // Prologue: stage 0 -> lds0; f1 (the carried set) starts at zero.
+        // Prologue: stages 0..NS-2 -> lds0..; f1 (the carried set) starts at zero.
 #pragma unroll
         for (int q = 0; q < NSLOT; ++q) copy(q, 0, lds0);
+        if constexpr (NS == 4) {
+#pragma unroll
+            for (int q = 0; q < NSLOT; ++q) copy(q, min(1, KT - 1), lds1);
+#pragma unroll
+            for (int q = 0; q < NSLOT; ++q) copy(q, min(2, KT - 1), lds2);
+        }
         wait_lgkm0();
-        wait_vm0();
+        wait_vm<(NS - 2) * NSLOT>();  // stage 0 has landed
         barrier();
 #pragma unroll
         for (int i = 0; i < NI; ++i) f1.a[i] = typename Mma<ELEM>::Frag{};
 #pragma unroll
         for (int j = 0; j < NJ; ++j) f1.b[j] = typename Mma<ELEM>::Frag{};
         int kt = 0;
-        for (; kt + 2 <= KT; kt += 2) {
-            stage(S{}, lds0, lds1, kt);
-            stage(S{}, lds1, lds0, kt + 1);
+        if constexpr (NS == 2) {
+            for (; kt + 2 <= KT; kt += 2) {
+                stage(S{}, lds0, lds1, kt);
+                stage(S{}, lds1, lds0, kt + 1);
+            }
+            if (kt < KT) stage(S{}, lds0, lds1, kt);  // odd stage count
+        } else {
+            for (; kt + 4 <= KT; kt += 4) {
+                stage(S{}, lds0, lds3, kt);
+                stage(S{}, lds1, lds0, kt + 1);
+                stage(S{}, lds2, lds1, kt + 2);
+                stage(S{}, lds3, lds2, kt + 3);
+            }
+            if (kt < KT) stage(S{}, lds0, lds3, kt);  // stage counts not a multiple of 4
+            if (kt + 1 < KT) stage(S{}, lds1, lds0, kt + 1);
+            if (kt + 2 < KT) stage(S{}, lds2, lds1, kt + 2);
+            wait_vm0();  // the re-copies of the last stage have landed before the tile moves on
         }
-        if (kt < KT) stage(S{}, lds0, lds1, kt);  // odd stage count
         // the last stage's carried step
         if constexpr (S::value) sanitize_frags<ELEM, TL>(f1);
 #pragma unroll
@@ -637,8 +667,11 @@ hipError_t launch_tile(const GemmArgs& p, hipStream_t s, int tile, int cus) {
     if constexpr (BL == FKE_B_KN) {
         return launch_t<ELEM, BL, OUT, SWI, T256>(p, s, cus);
     } else {
-        return tile == MFMA_TILE_128x128 ? launch_t<ELEM, BL, OUT, SWI, T128>(p, s, cus)
-                                         : launch_t<ELEM, BL, OUT, SWI, T256>(p, s, cus);
+        switch (tile) {
+            case MFMA_TILE_128x128: return launch_t<ELEM, BL, OUT, SWI, T128>(p, s, cus);
+            case MFMA_TILE_128x128_RING4: return launch_t<ELEM, BL, OUT, SWI, T128R4>(p, s, cus);
+            default: return launch_t<ELEM, BL, OUT, SWI, T256>(p, s, cus);
+        }
     }
 }
 
@@ -680,34 +713,67 @@ bool mfma_supports(const GemmArgs& p, int elem) {
     return true;
 }
 
-// Tile for a shape on `cus` CUs (measured on 16 INT8 / FP8 / bf16 shapes per
-// rule, B [N,K]).
+// Tile for a shape on `cus` CUs (measured on 23 INT8 / FP8 / bf16 shapes,
+// operands cache-warm and weights cold, B [N,K]).
+// - At most one 128x128 tile per CU: the 4-stage ring.  A lone tile waits on
+//   every stage's copy (about 1 us from HBM), which three stages in flight
+//   hide: 512x4096x4096 INT8 22 against 31 us with cold weights,
+//   1024x4096x4096 21.3 against 25.9 warm, bf16 256x4096x4096 26 against 41.
 // - The 256x256 tile reads the fewest operand bytes per MFMA and wins on long
-//   K whenever its tiles fill the CUs (8192^3: 442 against 502 us; C3
-//   4096x11008x4096: 171 against 180).
+//   K whenever its tiles fill the CUs (8192^3: 432 against 528 us cold; C3
+//   4096x11008x4096: 178 against 230).
 // - Short K: a tile's prologue (first stage in flight) and epilogue (its
 //   stores) are a large share of its time, and two 128x128 workgroups per CU
 //   overlap one's with the other's K loop: 128x128 wins at K <= 2048 bytes
-//   with 8-bit operands (4096x4096x1024 INT8: 24.8 against 32.7 us;
-//   8192x8192x2048: 140 against 146) and at K <= 1024 bytes with 16-bit ones
+//   with 8-bit operands (4096x4096x1024 INT8: 25.0 against 31.0 us warm;
+//   8192x8192x2048: 146 against 150) and at K <= 1024 bytes with 16-bit ones
 //   (at 2048 bytes bf16 varies by shape, -7 to +4 %).
-// - Few tiles: 128x128 wins when 256x256 tiles would leave CUs idle and its
-//   own fit one round of two workgroups per CU (4096x1376x4096: 28 against
-//   46 us); a second, partial round of them loses (3072x4096x4096: 57.4
-//   against 55.0 us).
+// - Few tiles: 128x128 (two per CU) when 256x256 tiles would leave CUs idle
+//   and its own fit one round of two per CU (4096x1376x4096: 28 against 47 us
+//   warm, 37 against 51 cold); a second, partial round of them loses
+//   (3072x4096x4096: 57.9 against 56.7 us), and so does the ring once CUs hold
+//   two tiles (4096x1376x4096: 34.4).
 // A 256x128 tile (one workgroup per CU) measured slower than 128x128 on every
 // few-tile shape, INT8, FP8 and bf16.
 int mfma_pick_tile(const GemmArgs& p, int elem, int cus) {
     if (p.b_layout == FKE_B_KN) return MFMA_TILE_256x256;
-    const int64_t kb = static_cast<int64_t>(p.K) * elem_bytes(elem);
-    if (kb <= (elem_bytes(elem) == 1 ? 2048 : 1024)) return MFMA_TILE_128x128;
     const int64_t NO = p.swiglu ? p.N / 2 : p.N;
     auto tiles = [&](int64_t bm, int64_t bn) {
         const int64_t tc = p.swiglu ? bn / 2 : bn;
         return (p.M + bm - 1) / bm * ((NO + tc - 1) / tc);
     };
-    if (tiles(256, 256) < cus && tiles(128, 128) <= 2 * static_cast<int64_t>(cus)) return MFMA_TILE_128x128;
+    const int64_t t128 = tiles(128, 128);
+    if (t128 <= cus) return MFMA_TILE_128x128_RING4;
+    const int64_t kb = static_cast<int64_t>(p.K) * elem_bytes(elem);
+    if (kb <= (elem_bytes(elem) == 1 ? 2048 : 1024)) return MFMA_TILE_128x128;
+    if (tiles(256, 256) < cus && t128 <= 2 * static_cast<int64_t>(cus)) return MFMA_TILE_128x128;
     return MFMA_TILE_256x256;
+}
+
+// Time (us) of the MFMA GEMM on an 8-bit B [N,K] shape, for the choice
+// between it and the streamed decode kernel (cold weights, bf16 out; fitted on
+// N = 1792..14336, K = 4096, M = 64..512).  Ring: the larger of the per-stage
+// latency floor (0.67 us per 128-byte stage) and the weight stream at the
+// 2.1 TB/s its one-tile-per-CU grid reaches.  128x128: a stage of about 1 us
+// per round of two tiles per CU.  256x256: 1.35 us per stage and 11 us per
+// round of tiles.
+double mfma_time_estimate_us(const GemmArgs& p, int cus) {
+    const double kt = p.K / 128.0;
+    const int64_t NO = p.swiglu ? p.N / 2 : p.N;
+    switch (mfma_pick_tile(p, ELEM_I8, cus)) {
+        case MFMA_TILE_128x128_RING4:
+            return std::max(0.67 * kt, static_cast<double>(p.N) * p.K / 2.1e6) + 1.0;
+        case MFMA_TILE_128x128: {
+            const int64_t tc = p.swiglu ? 64 : 128;
+            const double t = static_cast<double>((p.M + 127) / 128 * ((NO + tc - 1) / tc));
+            return 1.05 * kt + 6.0 * t / cus;
+        }
+        default: {
+            const int64_t tc = p.swiglu ? 128 : 256;
+            const int64_t t = (p.M + 255) / 256 * ((NO + tc - 1) / tc);
+            return static_cast<double>((t + cus - 1) / cus) * (1.35 * kt + 11.0);
+        }
+    }
 }
 
 hipError_t launch_mfma(const GemmArgs& p, int elem, hipStream_t s, int tile) {

@@ -946,11 +946,15 @@ hipError_t launch_rows_m(const GemmArgs& p, hipStream_t s) {
 //    with (c0, cw, ca) = (4.0, 0.046, 0.004) for two 16-row blocks and
 //    (5.2, 0.056, 0.0078) for four (each fit within 1 % of its three shapes;
 //    chunks after the first measured up to 8 % faster): the weight stream
-//    slows as more MFMAs and activation items sit between its items;
-//  * MFMA GEMM: per round of 256x256 tiles over the CUs, 1.35 us per 128-byte
-//    K stage + 11 us.
-// Past 16 rows the MFMA GEMM has fewer tiles than CUs up to the hundreds of
-// rows (one 256-row tile row), so it takes a whole tile's time for any M.
+//    slows as more MFMAs and activation items sit between its items; the
+//    workgroup rows of the chunks share the CUs, so small N runs several
+//    chunks at once (N = 1792, M = 128: one chunk's 9.1 us);
+//  * MFMA GEMM: mfma_time_estimate_us, by the tile it would run.  Up to a
+//    few hundred rows it runs the 4-stage 128x128 ring, one tile per CU,
+//    whose time hardly depends on M (28 us at N = 14336, K = 4096), while
+//    the streamed kernel adds a chunk per 64 rows: the streamed kernel keeps
+//    M <= 64 there (19.6 against 22.7 us) and the MFMA GEMM takes M >= 65
+//    (26.5 against 36.6 us at M = 128).
 bool gemv_i8_batch_pays(const GemmArgs& p) {
     if (p.M <= 16 || p.M > FKE_GEMV_MAX_M) return p.M <= 16;
     const double kib = p.K / 1024.0;
@@ -958,11 +962,10 @@ bool gemv_i8_batch_pays(const GemmArgs& p) {
     const double share = static_cast<double>((no + g - 1) / g) * (p.swiglu ? 2 : 1) * kib;
     const bool four = p.M > 32;
     const double chunk = (four ? 5.2 : 4.0) + (four ? 0.056 : 0.046) * share + (four ? 0.0078 : 0.004) * min(p.M, 64) * kib;
-    const double t_lds = ((p.M + 63) / 64) * chunk;
-    const int64_t tiles = ((static_cast<int64_t>(p.M) + 255) / 256) * ((static_cast<int64_t>(p.N) + 255) / 256);
-    const int64_t rounds = (tiles + cu_count() - 1) / cu_count();
-    const double t_mfma = rounds * (p.K / 128.0 * 1.35 + 11.0);
-    return t_lds < t_mfma;
+    // one row of g workgroups per 64 rows; rows share the CUs (one workgroup each)
+    const int64_t waves = ((p.M + 63) / 64 * g + cu_count() - 1) / cu_count();
+    const double t_lds = waves * chunk;
+    return t_lds < mfma_time_estimate_us(p, cu_count());
 }
 
 bool gemv_i8_supports(const GemmArgs& p) {

@@ -16,7 +16,7 @@ LIB_PATH = os.path.join(_PKG, "lib", "libfke_qgemm.so")
 OUT_F32, OUT_BF16, OUT_I32 = 0, 1, 2
 B_NK, B_KN = 0, 1
 PATH_AUTO, PATH_GEMV, PATH_MFMA, PATH_GENERIC, PATH_GEMV_DOT = 0, 1, 2, 3, 4
-PATH_MFMA_256x256, PATH_MFMA_128x128 = 5, 6
+PATH_MFMA_256x256, PATH_MFMA_128x128, PATH_MFMA_128x128_RING4 = 5, 6, 7
 IN_F32, IN_BF16, IN_F16 = 0, 1, 2
 HIP_SUCCESS, HIP_ERROR_INVALID_VALUE = 0, 1
 W8A8_NOALLOC_SCRATCH_BYTES = 32 << 20  # FKE_W8A8_NOALLOC_SCRATCH_BYTES

@@ -66,7 +66,8 @@ enum fke_path {
      * fke_select_mfma_tile).  Same results bit for bit; 128x128 takes B [N,K]
      * only (B [K,N]: hipErrorInvalidValue). */
     FKE_PATH_MFMA_256x256 = 5,
-    FKE_PATH_MFMA_128x128 = 6
+    FKE_PATH_MFMA_128x128 = 6,
+    FKE_PATH_MFMA_128x128_RING4 = 7 /* 128x128, one workgroup per CU, four LDS stages */
 };
 
 /*

@@ -259,11 +259,16 @@ def test_path_unavailable_for_shape_is_rejected():
     (4, 14336, 4096, 0, _lib.PATH_GEMV),
     (16, 14336, 4096, 0, _lib.PATH_GEMV),
     (17, 14336, 4096, 0, _lib.PATH_GEMV),    # batches: LDS-streamed kernel against the MFMA GEMM's cost
-    (128, 14336, 4096, 0, _lib.PATH_GEMV),
+    (64, 14336, 4096, 0, _lib.PATH_GEMV),
+    (65, 14336, 4096, 0, _lib.PATH_MFMA),    # past one 64-row chunk: the MFMA GEMM's 128x128 ring
+    (128, 14336, 4096, 0, _lib.PATH_MFMA),
     (192, 14336, 4096, 0, _lib.PATH_MFMA),
-    (192, 4096, 4096, 0, _lib.PATH_GEMV),
+    (128, 4096, 4096, 0, _lib.PATH_GEMV),
+    (192, 4096, 4096, 0, _lib.PATH_MFMA),
     (384, 4096, 4096, 0, _lib.PATH_MFMA),
-    (384, 4096, 14336, 0, _lib.PATH_GEMV),
+    (256, 1792, 4096, 0, _lib.PATH_GEMV),    # small N: the streamed kernel's chunks run side by side
+    (512, 1792, 4096, 0, _lib.PATH_MFMA),
+    (384, 4096, 14336, 0, _lib.PATH_MFMA),
     (512, 4096, 14336, 0, _lib.PATH_MFMA),
     (17, 14336, 1024, 0, _lib.PATH_MFMA),    # K < 2048: no streamed batch kernel
     (100, 4096, 2112, 0, _lib.PATH_GEMV),    # K % 128 != 0: no MFMA GEMM, the streamed kernel takes it
@@ -348,7 +353,10 @@ def test_torch_extension_rejects_host_tensors():
     (4096, 11008, 4096, 1, 0, 0, 256, _lib.PATH_MFMA_256x256),  # 688 tiles
     (4096, 1376, 4096, 1, 0, 0, 256, _lib.PATH_MFMA_128x128),   # 96 tiles of 256x256, 352 of 128x128
     (8192, 1024, 8192, 1, 0, 0, 256, _lib.PATH_MFMA_128x128),   # 128 / 512: one round of two per CU
-    (512, 4096, 4096, 1, 0, 0, 256, _lib.PATH_MFMA_128x128),    # 32 / 128
+    (512, 4096, 4096, 1, 0, 0, 256, _lib.PATH_MFMA_128x128_RING4),  # 128 tiles: one per CU at most
+    (128, 14336, 4096, 1, 0, 0, 256, _lib.PATH_MFMA_128x128_RING4),  # 112
+    (1024, 4096, 4096, 2, 0, 0, 256, _lib.PATH_MFMA_128x128_RING4),  # 256
+    (256, 4096, 1024, 1, 0, 0, 256, _lib.PATH_MFMA_128x128_RING4),   # 64, short K
     (3072, 4096, 4096, 1, 0, 0, 256, _lib.PATH_MFMA_256x256),   # 192 / 768: a second, partial round
     (1024, 14336, 4096, 1, 0, 0, 256, _lib.PATH_MFMA_256x256),  # 224 / 896
     (8192, 8192, 2048, 1, 0, 0, 256, _lib.PATH_MFMA_128x128),   # short K, 8-bit: <= 2048 bytes
@@ -376,8 +384,8 @@ def test_mfma_tile_choice_rejects_bad_arguments():
 
 def test_pinned_small_tile_rejects_b_kn_before_any_launch():
     L = _lib.lib()
-    path = _lib.PATH_MFMA_128x128
-    assert L.fke_qgemm_i8_on_path(path, P, P, P, 256, 256, 256, None, None, 1.0, 1.0, None,
-                                  _lib.OUT_F32, _lib.B_KN, None) == _lib.HIP_ERROR_INVALID_VALUE
-    assert L.fke_qgemm_f8_on_path(path, P, P, P, 256, 256, 256, 1.0, 1.0, None,
-                                  _lib.OUT_F32, _lib.B_KN, None) == _lib.HIP_ERROR_INVALID_VALUE
+    for path in (_lib.PATH_MFMA_128x128, _lib.PATH_MFMA_128x128_RING4):
+        assert L.fke_qgemm_i8_on_path(path, P, P, P, 256, 256, 256, None, None, 1.0, 1.0, None,
+                                      _lib.OUT_F32, _lib.B_KN, None) == _lib.HIP_ERROR_INVALID_VALUE
+        assert L.fke_qgemm_f8_on_path(path, P, P, P, 256, 256, 256, 1.0, 1.0, None,
+                                      _lib.OUT_F32, _lib.B_KN, None) == _lib.HIP_ERROR_INVALID_VALUE

@@ -179,6 +179,7 @@ CASES = [
     (17, 130, 256, "mfma"), (300, 200, 512, "mfma"), (256, 128, 128, "mfma"), (513, 333, 384, "mfma"),
     (300, 200, 512, "mfma_256x256"), (513, 333, 384, "mfma_256x256"),
     (17, 130, 256, "mfma_128x128"), (256, 128, 128, "mfma_128x128"), (513, 333, 384, "mfma_128x128"),
+    (17, 130, 256, "mfma_128x128_ring4"), (300, 200, 640, "mfma_128x128_ring4"), (513, 333, 384, "mfma_128x128_ring4"),
     (33, 40, 100, "generic"), (7, 9, 77, "generic"), (1, 5, 3, "generic"), (70, 100, 256, "generic"),
 ]
 
