@@ -44,7 +44,8 @@ PEAK_HBM_GBS = 8000.0     # MI355X HBM3E, published (8 TB/s)
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic.json")
 
 
-TILE_LABELS = {5: "256x256", 6: "128x128", 7: "128x128_ring4"}
+# FKE_PATH_MFMA_* (include/fke_qgemm.h) -> tile name
+TILE_LABELS = {5: "256x256", 6: "128x128", 7: "128x128_ring4", 8: "128x64_ring4", 9: "64x64_ring4"}
 
 
 def gemv_kernel(L, _lib, M, N=14336, K=4096):
@@ -52,7 +53,7 @@ def gemv_kernel(L, _lib, M, N=14336, K=4096):
     family's, or the MFMA GEMM's with its tile."""
     path = L.fke_select_path_i8(4096, 4096, 4096, M, N, K, _lib.OUT_BF16, _lib.B_NK)
     if path == _lib.PATH_MFMA:
-        return f"gemm_mfma_kernel<i8,NK,bf16,{TILE_LABELS[L.fke_select_mfma_tile(M, N, K, 1, _lib.B_NK, 0, 0)]}>"
+        return f"gemm_mfma_kernel<i8,NK,bf16,{TILE_LABELS[L.fke_select_mfma_tile(M, N, K, _lib.B_NK, 0, 0)]}>"
     return "gemv_rows_kernel" if M <= 2 else "gemv_lds_kernel"
 
 
@@ -92,7 +93,7 @@ def parse():
     ap.add_argument("--shards", action="store_true",
                     help="also time the per-GPU shards of 8-way tensor parallelism (part of --extra)")
     ap.add_argument("--tile-sweep", action="store_true",
-                    help="also time every MFMA GEMM tile (256x256, 128x128, 128x128 four-stage ring) on shapes around the dispatcher's "
+                    help="also time every MFMA GEMM tile (256x256, 128x128, and the 4-stage rings) on shapes around the dispatcher's "
                          "tile rule, INT8, FP8 and bf16 (B [N,K]), beside the tile it picks")
     ap.add_argument("--data-sweep", action="store_true",
                     help="also time the headline GEMM on zero, constant and narrow-range operands (clock vs data)")
@@ -542,7 +543,7 @@ def shard_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
             "us": r["us_per_launch"], "GB/s": r["value"], "frac": r["roofline"]["frac"],
             "bytes": r["roofline"]["algorithmic_bytes_per_launch"], "kernel": r["kernel"]}
     sh = torch.cuda.current_stream(dev).cuda_stream
-    tiles = {_lib.PATH_MFMA_256x256: "256x256", _lib.PATH_MFMA_128x128: "128x128"}
+    tiles = TILE_LABELS
     for name, (M, N, K, out, tdt) in {
             "tp8_prefill_colshard_4096x1376x4096_bf16": (4096, 1376, 4096, _lib.OUT_BF16, torch.bfloat16),
             "tp8_int8_colshard_8192x1024x8192_f32": (8192, 1024, 8192, _lib.OUT_F32, torch.float32),
@@ -554,7 +555,7 @@ def shard_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
                                           sb.data_ptr(), 1.0, 1.0, None, out, _lib.B_NK, sh),
                    args.steps, args.warmup)
         t = 2.0 * M * N * K / (ms * 1e-3) / 1e12
-        tile = L.fke_select_mfma_tile(M, N, K, 1, _lib.B_NK, 0, 0)
+        tile = L.fke_select_mfma_tile(M, N, K, _lib.B_NK, 0, 0)
         res[name] = {"ms": round(ms, 4), "TOPS": round(t, 1), "frac": round(t / PEAK_INT8_TOPS, 4),
                      "tile": tiles.get(tile, str(tile))}
         if tile != _lib.PATH_MFMA_256x256:  # the 256x256 tile on the same shape, for comparison
@@ -578,45 +579,53 @@ TILE_SWEEP_SHAPES = [
 
 
 def tile_sweep(torch, L, _lib, dev, gen, timed, args):
-    """Every MFMA tile pinned (FKE_PATH_MFMA_256x256 / _128x128 / _128x128_RING4) on each shape, INT8 and FP8
-    with bf16 out and bf16 operands with bf16 out, against the tile fke_select_mfma_tile picks.  The operands
-    stay the same from launch to launch (cache-warm)."""
+    """Every MFMA tile pinned (the FKE_PATH_MFMA_* paths of TILE_LABELS) on each shape, INT8 and FP8
+    with bf16 out and bf16 operands with bf16 out, beside the tile fke_select_mfma_tile picks: "warm" reuses
+    one weight buffer (it stays in the caches), "cold" cycles the weights over at least 512 MiB of buffers
+    (as a model's forward pass meets them).  Each variant runs 30 ms back to back before its timed launches."""
     sh = torch.cuda.current_stream(dev).cuda_stream
-    names = {_lib.PATH_MFMA_256x256: "256x256", _lib.PATH_MFMA_128x128: "128x128",
-             _lib.PATH_MFMA_128x128_RING4: "128x128_ring4"}
+    names = TILE_LABELS
     res = {}
     for (M, N, K) in TILE_SWEEP_SHAPES:
         C = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
         sa = torch.rand(M, device=dev, generator=gen)
         sb = torch.rand(N, device=dev, generator=gen)
         for elem in ("i8", "f8", "bf16"):
+            eb = 2 if elem == "bf16" else 1
+            nb = max(2, min(64, (512 << 20) // (N * K * eb) + 1))
             if elem == "bf16":
                 A = torch.randn((M, K), device=dev, generator=gen).to(torch.bfloat16)
-                B = torch.randn((N, K), device=dev, generator=gen).to(torch.bfloat16)
+                Bs = [torch.randn((N, K), device=dev, generator=gen).to(torch.bfloat16) for _ in range(nb)]
             else:
                 A = torch.randint(-127, 128, (M, K), dtype=torch.int8, device=dev, generator=gen)
-                B = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=gen)
+                Bs = [torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=gen) for _ in range(nb)]
                 if elem == "f8":  # no NaN codes (those rerun a tile)
                     A[(A & 0x7F) == 0x7F] = 0
-                    B[(B & 0x7F) == 0x7F] = 0
-            row = {"pick": names[L.fke_select_mfma_tile(M, N, K, 2 if elem == "bf16" else 1, _lib.B_NK, 0, 0)]}
+                    for B in Bs:
+                        B[(B & 0x7F) == 0x7F] = 0
+            row = {"pick": names[L.fke_select_mfma_tile(M, N, K, _lib.B_NK, 0, 0)], "cold_buffers": nb}
             for path, name in names.items():
-                if elem == "i8":
-                    fn = lambda: L.fke_qgemm_i8_on_path(path, A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K,
-                                                        sa.data_ptr(), sb.data_ptr(), 1.0, 1.0, None, _lib.OUT_BF16,
-                                                        _lib.B_NK, sh)
-                elif elem == "f8":
-                    fn = lambda: L.fke_qgemm_f8_on_path(path, A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K,
-                                                        0.01, 0.01, None, _lib.OUT_BF16, _lib.B_NK, sh)
-                else:
-                    fn = lambda: L.fke_gemm_half_on_path(path, A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K,
-                                                         _lib.IN_BF16, sa.data_ptr(), sb.data_ptr(), 1.0, 1.0, None,
-                                                         _lib.OUT_BF16, _lib.B_NK, sh)
-                if fn() != 0:
-                    raise RuntimeError(f"tile sweep: {elem} {name} {M}x{N}x{K} rejected")
-                row[f"us_{name}"] = round(timed(fn, 20, 5) * 1e3, 2)
+                for mode in ("warm", "cold"):
+                    it = [0]
+
+                    def fn():
+                        B = Bs[0] if mode == "warm" else Bs[it[0] % nb]
+                        it[0] += 1
+                        if elem == "i8":
+                            return L.fke_qgemm_i8_on_path(path, A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K,
+                                                          sa.data_ptr(), sb.data_ptr(), 1.0, 1.0, None, _lib.OUT_BF16,
+                                                          _lib.B_NK, sh)
+                        if elem == "f8":
+                            return L.fke_qgemm_f8_on_path(path, A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K,
+                                                          0.01, 0.01, None, _lib.OUT_BF16, _lib.B_NK, sh)
+                        return L.fke_gemm_half_on_path(path, A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K,
+                                                       _lib.IN_BF16, sa.data_ptr(), sb.data_ptr(), 1.0, 1.0, None,
+                                                       _lib.OUT_BF16, _lib.B_NK, sh)
+                    if fn() != 0:
+                        raise RuntimeError(f"tile sweep: {elem} {name} {M}x{N}x{K} rejected")
+                    row[f"us_{name}_{mode}"] = round(timed(fn, 20, 5, preheat_ms=30.0) * 1e3, 2)
             res[f"{elem}_{M}x{N}x{K}_bf16"] = row
-            del A, B
+            del A, Bs
         del C
     return res
 

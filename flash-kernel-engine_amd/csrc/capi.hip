@@ -208,6 +208,8 @@ int mfma_tile_of_path(int path, const GemmArgs& p) {
         case FKE_PATH_MFMA_256x256: return fke::MFMA_TILE_256x256;
         case FKE_PATH_MFMA_128x128: return p.b_layout == FKE_B_NK ? fke::MFMA_TILE_128x128 : -2;
         case FKE_PATH_MFMA_128x128_RING4: return p.b_layout == FKE_B_NK ? fke::MFMA_TILE_128x128_RING4 : -2;
+        case FKE_PATH_MFMA_128x64_RING4: return p.b_layout == FKE_B_NK && !p.swiglu ? fke::MFMA_TILE_128x64_RING4 : -2;
+        case FKE_PATH_MFMA_64x64_RING4: return p.b_layout == FKE_B_NK && !p.swiglu ? fke::MFMA_TILE_64x64_RING4 : -2;
         default: return -1;
     }
 }
@@ -230,7 +232,9 @@ int run_i8(int path, const GemmArgs& p, void* stream, const KnWorkspace* ws) {
         case FKE_PATH_MFMA:
         case FKE_PATH_MFMA_256x256:
         case FKE_PATH_MFMA_128x128:
-        case FKE_PATH_MFMA_128x128_RING4: return run_mfma(path, p, fke::ELEM_I8, s);
+        case FKE_PATH_MFMA_128x128_RING4:
+        case FKE_PATH_MFMA_128x64_RING4:
+        case FKE_PATH_MFMA_64x64_RING4: return run_mfma(path, p, fke::ELEM_I8, s);
         case FKE_PATH_GENERIC: return fke::launch_generic(p, fke::ELEM_I8, s);
         case FKE_PATH_GEMV_DOT:
             if (!fke::gemv_dot_supports(p)) return hipErrorInvalidValue;
@@ -259,7 +263,9 @@ int run_half(int path, const GemmArgs& p, int elem, void* stream) {
         case FKE_PATH_MFMA:
         case FKE_PATH_MFMA_256x256:
         case FKE_PATH_MFMA_128x128:
-        case FKE_PATH_MFMA_128x128_RING4: return run_mfma(path, p, elem, s);
+        case FKE_PATH_MFMA_128x128_RING4:
+        case FKE_PATH_MFMA_128x64_RING4:
+        case FKE_PATH_MFMA_64x64_RING4: return run_mfma(path, p, elem, s);
         case FKE_PATH_GENERIC: return fke::launch_generic(p, elem, s);
         default: return hipErrorInvalidValue;
     }
@@ -276,7 +282,9 @@ int run_f8(int path, const GemmArgs& p, void* stream, const KnWorkspace* ws = nu
         case FKE_PATH_MFMA:
         case FKE_PATH_MFMA_256x256:
         case FKE_PATH_MFMA_128x128:
-        case FKE_PATH_MFMA_128x128_RING4: return run_mfma(path, p, fke::ELEM_F8, s);
+        case FKE_PATH_MFMA_128x128_RING4:
+        case FKE_PATH_MFMA_128x64_RING4:
+        case FKE_PATH_MFMA_64x64_RING4: return run_mfma(path, p, fke::ELEM_F8, s);
         case FKE_PATH_GENERIC: return fke::launch_generic(p, fke::ELEM_F8, s);
         default: return hipErrorInvalidValue;
     }
@@ -445,18 +453,17 @@ int fke_select_path_half(const void* A, const void* B, const void* C, int M, int
                      half_elem(in_dtype));
 }
 
-int fke_select_mfma_tile(int M, int N, int K, int operand_bytes, int b_layout, int swiglu, int cus) {
-    if (M < 1 || N < 1 || K < 1 || (operand_bytes != 1 && operand_bytes != 2) ||
-        (b_layout != FKE_B_NK && b_layout != FKE_B_KN) || (swiglu && N % 2))
-        return -1;
+int fke_select_mfma_tile(int M, int N, int K, int b_layout, int swiglu, int cus) {
+    if (M < 1 || N < 1 || K < 1 || (b_layout != FKE_B_NK && b_layout != FKE_B_KN) || (swiglu && N % 2)) return -1;
     GemmArgs p = make_args(nullptr, nullptr, nullptr, M, N, K, nullptr, nullptr, 1.f, 1.f, nullptr, FKE_OUT_F32,
                            b_layout);
     p.swiglu = swiglu ? 1 : 0;
     if (cus <= 0) cus = fke::device_cus();
-    const int elem = operand_bytes == 1 ? fke::ELEM_I8 : fke::ELEM_BF16;  // the rule depends on the width only
-    switch (fke::mfma_pick_tile(p, elem, cus)) {
+    switch (fke::mfma_pick_tile(p, cus)) {
         case fke::MFMA_TILE_128x128: return FKE_PATH_MFMA_128x128;
         case fke::MFMA_TILE_128x128_RING4: return FKE_PATH_MFMA_128x128_RING4;
+        case fke::MFMA_TILE_128x64_RING4: return FKE_PATH_MFMA_128x64_RING4;
+        case fke::MFMA_TILE_64x64_RING4: return FKE_PATH_MFMA_64x64_RING4;
         default: return FKE_PATH_MFMA_256x256;
     }
 }

@@ -37,9 +37,16 @@ hipError_t launch_generic(const GemmArgs& p, int elem, hipStream_t stream);
 hipError_t launch_gemv_i8(const GemmArgs& p, hipStream_t stream);
 // MFMA GEMM workgroup tile: AUTO = chosen by tile count (mfma_pick_tile); B
 // [K,N] always runs 256x256.
-enum MfmaTile { MFMA_TILE_AUTO = 0, MFMA_TILE_256x256 = 1, MFMA_TILE_128x128 = 2, MFMA_TILE_128x128_RING4 = 3 };
+enum MfmaTile {
+    MFMA_TILE_AUTO = 0,
+    MFMA_TILE_256x256 = 1,
+    MFMA_TILE_128x128 = 2,
+    MFMA_TILE_128x128_RING4 = 3,
+    MFMA_TILE_128x64_RING4 = 4,  // not for SwiGLU
+    MFMA_TILE_64x64_RING4 = 5    // not for SwiGLU
+};
 hipError_t launch_mfma(const GemmArgs& p, int elem, hipStream_t stream, int tile = MFMA_TILE_AUTO);
-int mfma_pick_tile(const GemmArgs& p, int elem, int cus);
+int mfma_pick_tile(const GemmArgs& p, int cus);
 // Estimated time (us) of the MFMA GEMM on an 8-bit B [N,K] shape.
 double mfma_time_estimate_us(const GemmArgs& p, int cus);
 // CUs of the current device (256 without one).

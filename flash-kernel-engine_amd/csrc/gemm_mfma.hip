@@ -58,8 +58,8 @@ constexpr int NWAVES = 4;
 constexpr int NTHREADS = NWAVES * 64;
 
 // Workgroup tile: each of the 4 waves (2x2) owns NI x NJ MFMA blocks of 32x32
-// (written for NI, NJ in {2, 4}; built as 4x4 and 2x2), with a ring of NS LDS
-// stages (2 or 4: the copy of stage k + NS - 1 is issued while stage k runs).
+// (NI, NJ in {1, 2, 4}), with a ring of NS LDS stages (2 or 4: the copy of
+// stage k + NS - 1 is issued while stage k runs).
 template <int NI_, int NJ_, int NS_ = 2>
 struct Tile {
     static constexpr int NI = NI_, NJ = NJ_, NS = NS_;
@@ -76,6 +76,8 @@ struct Tile {
 using T256 = Tile<4, 4>;
 using T128 = Tile<2, 2>;
 using T128R4 = Tile<2, 2, 4>;  // one workgroup per CU, three stages in flight
+using T128x64R4 = Tile<2, 1, 4>;
+using T64R4 = Tile<1, 1, 4>;
 
 __device__ __forceinline__ int swz(int r) { return ((r & 31) ^ ((r & 31) >> 3)) & 7; }
 
@@ -326,6 +328,7 @@ template <int ELEM, int BL, int OUT, bool SWI, class TL>
 __global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p) {
     static_assert(!SWI || (ELEM == ELEM_I8 && BL == FKE_B_NK && OUT != FKE_OUT_I32), "SwiGLU: INT8, B [N,K], float out");
     static_assert(BL == FKE_B_NK || TL::NJ == 4, "B [K,N]: 256-column tiles");
+    static_assert(!SWI || TL::NJ >= 2, "SwiGLU: each wave pairs gate and up blocks");
     constexpr int NKS = Mma<ELEM>::KSTEPS;
     constexpr int NI = TL::NI, NJ = TL::NJ, BM = TL::BM, NPIECE = TL::NPIECE;
     __shared__ __attribute__((aligned(1024))) uint8_t lds0[TL::STAGE];
@@ -419,13 +422,13 @@ __global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p
         constexpr bool SAN = decltype(sanc)::value;
         constexpr int Q0 = decltype(q0c)::value, Q1 = decltype(q1c)::value;
         constexpr int NQ = Q1 - Q0;
-        static_assert(NQ <= NPIECE, "at most one copy slot per MFMA");
         fence();
         if constexpr (SAN) sanitize_frags<ELEM, TL>(use);
         // Piece t: MFMA (t/NJ, t%NJ), then the reads r = t (mod NPIECE) of
-        // the next step, then copy slot Q0 + t for the first NQ pieces (early
-        // in the group, so each copy has the rest of the stage to land: 1.8 %
-        // faster at 8192^3 INT8 than placing them in the group's last pieces).
+        // the next step, then copy slots Q0 + c, c = t (mod NPIECE) (one per
+        // piece in its first pieces unless the group has more copies than
+        // MFMAs; early in the group, so each copy has the rest of the stage to
+        // land: 1.8 % faster at 8192^3 INT8 than the group's last pieces).
         // Each piece is fenced, so this is the issue order.
 #pragma unroll
         for (int t = 0; t < NPIECE; ++t) {
@@ -434,7 +437,8 @@ __global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p
 #pragma unroll
             for (int r = t; r < NREAD; r += NPIECE)
                 read_piece<ELEM, BL, TL>(cur, rks, wm, wn, lane, kn_off, fill, r);
-            if (t < NQ) copy(Q0 + t, kc, nxt);
+#pragma unroll
+            for (int c = t; c < NQ; c += NPIECE) copy(Q0 + c, kc, nxt);
         }
         fence();
     };
@@ -449,7 +453,6 @@ __global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p
         using S = decltype(sanc);
         if constexpr (NKS == 4) {
             constexpr int P = PER_GROUP, P2 = 2 * P < NSLOT ? 2 * P : NSLOT;
-            static_assert(P <= NPIECE, "copies of a stage fit its first three groups");
             group(S{}, I0{}, std::integral_constant<int, P>{}, f1, f0, cur, 0, nxt, kc);
             group(S{}, std::integral_constant<int, P>{}, std::integral_constant<int, P2>{}, f0, f1, cur, 1, nxt, kc);
             group(S{}, std::integral_constant<int, P2>{}, std::integral_constant<int, NSLOT>{}, f1, f0, cur, 2, nxt, kc);
@@ -457,13 +460,14 @@ __global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p
                   kc);
         } else {
             static_assert(NKS == 2, "k steps per stage");
-            // FP8 steps are twice as long (64-cycle MFMAs): all copies ride
-            // in the first group, one per MFMA, and the whole second group
-            // (16 x 64 cycles) is left for them to land before the stage's
-            // vmcnt(0).  Splitting them 8 / 8 left the last copies one MFMA
-            // before that wait and measured 5 % slower (438-444 us against
-            // 416-422 us at 8192^3, both B layouts).
-            constexpr int P = NSLOT < NPIECE ? NSLOT : NPIECE;
+            // FP8 steps are twice as long (64-cycle MFMAs): on the 256x256
+            // tile all copies ride in the first group, one per MFMA, and the
+            // whole second group (16 x 64 cycles) is left for them to land
+            // before the stage's vmcnt(0).  Splitting them 8 / 8 left the
+            // last copies one MFMA before that wait and measured 5 % slower
+            // (438-444 us against 416-422 us at 8192^3, both B layouts).
+            // Smaller tiles have more copies than MFMAs per group: half each.
+            constexpr int P = NSLOT <= NPIECE ? NSLOT : (NSLOT + 1) / 2;
             group(S{}, I0{}, std::integral_constant<int, P>{}, f1, f0, cur, 0, nxt, kc);
             group(S{}, std::integral_constant<int, P>{}, std::integral_constant<int, NSLOT>{}, f0, f1, cur, 1, nxt,
                   kc);
@@ -670,6 +674,12 @@ hipError_t launch_tile(const GemmArgs& p, hipStream_t s, int tile, int cus) {
         switch (tile) {
             case MFMA_TILE_128x128: return launch_t<ELEM, BL, OUT, SWI, T128>(p, s, cus);
             case MFMA_TILE_128x128_RING4: return launch_t<ELEM, BL, OUT, SWI, T128R4>(p, s, cus);
+            case MFMA_TILE_128x64_RING4:
+                if constexpr (!SWI) return launch_t<ELEM, BL, OUT, SWI, T128x64R4>(p, s, cus);
+                return hipErrorInvalidValue;
+            case MFMA_TILE_64x64_RING4:
+                if constexpr (!SWI) return launch_t<ELEM, BL, OUT, SWI, T64R4>(p, s, cus);
+                return hipErrorInvalidValue;
             default: return launch_t<ELEM, BL, OUT, SWI, T256>(p, s, cus);
         }
     }
@@ -713,56 +723,60 @@ bool mfma_supports(const GemmArgs& p, int elem) {
     return true;
 }
 
-// Tile for a shape on `cus` CUs (measured on 23 INT8 / FP8 / bf16 shapes,
-// operands cache-warm and weights cold, B [N,K]).
-// - At most one 128x128 tile per CU: the 4-stage ring.  A lone tile waits on
-//   every stage's copy (about 1 us from HBM), which three stages in flight
-//   hide: 512x4096x4096 INT8 22 against 31 us with cold weights,
-//   1024x4096x4096 21.3 against 25.9 warm, bf16 256x4096x4096 26 against 41.
-// - The 256x256 tile reads the fewest operand bytes per MFMA and wins on long
-//   K whenever its tiles fill the CUs (8192^3: 432 against 528 us cold; C3
-//   4096x11008x4096: 178 against 230).
-// - Short K: a tile's prologue (first stage in flight) and epilogue (its
-//   stores) are a large share of its time, and two 128x128 workgroups per CU
-//   overlap one's with the other's K loop: 128x128 wins at K <= 2048 bytes
-//   with 8-bit operands (4096x4096x1024 INT8: 25.0 against 31.0 us warm;
-//   8192x8192x2048: 146 against 150) and at K <= 1024 bytes with 16-bit ones
-//   (at 2048 bytes bf16 varies by shape, -7 to +4 %).
-// - Few tiles: 128x128 (two per CU) when 256x256 tiles would leave CUs idle
-//   and its own fit one round of two per CU (4096x1376x4096: 28 against 47 us
-//   warm, 37 against 51 cold); a second, partial round of them loses
-//   (3072x4096x4096: 57.9 against 56.7 us), and so does the ring once CUs hold
-//   two tiles (4096x1376x4096: 34.4).
+// Tile for a shape on `cus` CUs (`bench.py --tile-sweep`: 23 shapes, INT8,
+// FP8 and bf16, weights cache-warm and cold, B [N,K]; times below are INT8,
+// cold weights, bf16 out).
+// - The tiles fit the CUs one each: a 4-stage ring, the smallest tile whose
+//   count fits (64x64, else 128x64, else 128x128; SwiGLU pairs need 128
+//   columns).  A lone tile is bound by the bytes its CU loads, (BM + BN) * K,
+//   at about 45 GB/s per CU, and waits on every stage's copy unless several
+//   are in flight: 512x1792x4096 runs 12.0 us on 64x64, 14.6 on 128x64, 19.8
+//   on 128x128, 30.2 on 128x128 with two stages; 128x14336x4096 (64x64 would
+//   be 448 tiles) 20.3 on 128x64 against 26.5 on 128x128.
+// - Fewer 256x256 tiles than CUs, and 128x128 tiles that fit one round of
+//   two per CU: 128x128 with two stages, two workgroups per CU
+//   (4096x1376x4096: 37.9 us against 41.2 on the 128x64 ring, 42.5 on the
+//   128x128 ring and 51.3 on 256x256).
+// - Everything else: 256x256, which reads the fewest operand bytes per MFMA
+//   (3072x4096x4096: 55.8 against 60.3 us; 4096x11008x4096: 181 against
+//   243).  That includes short K: two 128x128 workgroups per CU hide a short
+//   tile's prologue and epilogue, but fetch each weight panel twice as often,
+//   which loses once the weights come from HBM (8192x8192x1024: 105 against
+//   120 us cold, though 99 against 103 warm).
 // A 256x128 tile (one workgroup per CU) measured slower than 128x128 on every
 // few-tile shape, INT8, FP8 and bf16.
-int mfma_pick_tile(const GemmArgs& p, int elem, int cus) {
+int mfma_pick_tile(const GemmArgs& p, int cus) {
     if (p.b_layout == FKE_B_KN) return MFMA_TILE_256x256;
     const int64_t NO = p.swiglu ? p.N / 2 : p.N;
     auto tiles = [&](int64_t bm, int64_t bn) {
         const int64_t tc = p.swiglu ? bn / 2 : bn;
         return (p.M + bm - 1) / bm * ((NO + tc - 1) / tc);
     };
+    if (!p.swiglu && tiles(64, 64) <= cus) return MFMA_TILE_64x64_RING4;
+    if (!p.swiglu && tiles(128, 64) <= cus) return MFMA_TILE_128x64_RING4;
     const int64_t t128 = tiles(128, 128);
     if (t128 <= cus) return MFMA_TILE_128x128_RING4;
-    const int64_t kb = static_cast<int64_t>(p.K) * elem_bytes(elem);
-    if (kb <= (elem_bytes(elem) == 1 ? 2048 : 1024)) return MFMA_TILE_128x128;
     if (tiles(256, 256) < cus && t128 <= 2 * static_cast<int64_t>(cus)) return MFMA_TILE_128x128;
     return MFMA_TILE_256x256;
 }
 
 // Time (us) of the MFMA GEMM on an 8-bit B [N,K] shape, for the choice
 // between it and the streamed decode kernel (cold weights, bf16 out; fitted on
-// N = 1792..14336, K = 4096, M = 64..512).  Ring: the larger of the per-stage
-// latency floor (0.67 us per 128-byte stage) and the weight stream at the
-// 2.1 TB/s its one-tile-per-CU grid reaches.  128x128: a stage of about 1 us
-// per round of two tiles per CU.  256x256: 1.35 us per stage and 11 us per
-// round of tiles.
+// N = 1792..14336, K = 4096 and 14336, M = 16..512, within about 20 %).
+// Ring tiles: the larger of the bytes one CU loads, (BM + BN) * K, at 44 GB/s
+// and the weights at 4.2 TB/s, plus 1 us.  128x128 with two stages: about
+// 1 us per stage per round of two tiles per CU.  256x256: 1.35 us per stage
+// and 11 us per round of tiles.
 double mfma_time_estimate_us(const GemmArgs& p, int cus) {
     const double kt = p.K / 128.0;
     const int64_t NO = p.swiglu ? p.N / 2 : p.N;
-    switch (mfma_pick_tile(p, ELEM_I8, cus)) {
-        case MFMA_TILE_128x128_RING4:
-            return std::max(0.67 * kt, static_cast<double>(p.N) * p.K / 2.1e6) + 1.0;
+    auto ring = [&](double bm, double bn) {
+        return std::max((bm + bn) * p.K / 44.0e3, static_cast<double>(p.N) * p.K / 4.2e6) + 1.0;
+    };
+    switch (mfma_pick_tile(p, cus)) {
+        case MFMA_TILE_64x64_RING4: return ring(64, 64);
+        case MFMA_TILE_128x64_RING4: return ring(128, 64);
+        case MFMA_TILE_128x128_RING4: return ring(128, 128);
         case MFMA_TILE_128x128: {
             const int64_t tc = p.swiglu ? 64 : 128;
             const double t = static_cast<double>((p.M + 127) / 128 * ((NO + tc - 1) / tc));
@@ -778,7 +792,7 @@ double mfma_time_estimate_us(const GemmArgs& p, int cus) {
 
 hipError_t launch_mfma(const GemmArgs& p, int elem, hipStream_t s, int tile) {
     const int cus = device_cus();
-    if (tile == MFMA_TILE_AUTO) tile = mfma_pick_tile(p, elem, cus);
+    if (tile == MFMA_TILE_AUTO) tile = mfma_pick_tile(p, cus);
     if (elem == ELEM_F16 || elem == ELEM_BF16) {
         GemmArgs q = p;
         q.K = 2 * p.K;  // the kernel walks K bytes

@@ -950,11 +950,11 @@ hipError_t launch_rows_m(const GemmArgs& p, hipStream_t s) {
 //    workgroup rows of the chunks share the CUs, so small N runs several
 //    chunks at once (N = 1792, M = 128: one chunk's 9.1 us);
 //  * MFMA GEMM: mfma_time_estimate_us, by the tile it would run.  Up to a
-//    few hundred rows it runs the 4-stage 128x128 ring, one tile per CU,
-//    whose time hardly depends on M (28 us at N = 14336, K = 4096), while
-//    the streamed kernel adds a chunk per 64 rows: the streamed kernel keeps
-//    M <= 64 there (19.6 against 22.7 us) and the MFMA GEMM takes M >= 65
-//    (26.5 against 36.6 us at M = 128).
+//    few hundred rows it runs a 4-stage ring tile, one per CU, whose time
+//    hardly depends on M, while the streamed kernel adds a chunk per 64 rows:
+//    at N = 14336, K = 4096 the streamed kernel keeps M <= 32 (14.6 against
+//    16.2 us on the 64x64 ring) and the MFMA GEMM takes M = 48..64 (16.2
+//    against 19.3) and M = 65..128 on the 128x64 ring (20.3 against 36.7).
 bool gemv_i8_batch_pays(const GemmArgs& p) {
     if (p.M <= 16 || p.M > FKE_GEMV_MAX_M) return p.M <= 16;
     const double kib = p.K / 1024.0;

@@ -17,6 +17,7 @@ OUT_F32, OUT_BF16, OUT_I32 = 0, 1, 2
 B_NK, B_KN = 0, 1
 PATH_AUTO, PATH_GEMV, PATH_MFMA, PATH_GENERIC, PATH_GEMV_DOT = 0, 1, 2, 3, 4
 PATH_MFMA_256x256, PATH_MFMA_128x128, PATH_MFMA_128x128_RING4 = 5, 6, 7
+PATH_MFMA_128x64_RING4, PATH_MFMA_64x64_RING4 = 8, 9
 IN_F32, IN_BF16, IN_F16 = 0, 1, 2
 HIP_SUCCESS, HIP_ERROR_INVALID_VALUE = 0, 1
 W8A8_NOALLOC_SCRATCH_BYTES = 32 << 20  # FKE_W8A8_NOALLOC_SCRATCH_BYTES
@@ -42,7 +43,7 @@ SIGNATURES = {
     "fke_gemm_half_on_path": ([_i, _p, _p, _p, _i, _i, _i, _i, _p, _p, _f, _f, _p, _i, _i, _p], _i),
     "fke_launch_wmma_gemm_fp16": ([_p, _p, _p, _i, _i, _i, _f, _f, _p], _i),
     "fke_select_path_half": ([_p, _p, _p, _i, _i, _i, _i, _i, _i], _i),
-    "fke_select_mfma_tile": ([_i, _i, _i, _i, _i, _i, _i], _i),
+    "fke_select_mfma_tile": ([_i, _i, _i, _i, _i, _i], _i),
     "fke_w8a8_linear_workspace_size": ([_i, _i], ct.c_size_t),
     "fke_w8a8_linear": ([_p, _i, _p, _p, _i, _i, _i, _p, _f, _p, _i, _p, ct.c_size_t, _p], _i),
     "fke_w8a8_linear_noalloc": ([_p, _i, _p, _p, _i, _i, _i, _p, _f, _p, _i, _p], _i),

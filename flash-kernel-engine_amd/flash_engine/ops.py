@@ -18,14 +18,15 @@ import torch
 
 from . import _ext, _lib
 from ._lib import (B_KN, B_NK, OUT_BF16, OUT_F32, OUT_I32, PATH_AUTO, PATH_GEMV, PATH_GEMV_DOT, PATH_GENERIC,
-                   PATH_MFMA, PATH_MFMA_128x128, PATH_MFMA_128x128_RING4,
-                   PATH_MFMA_256x256)
+                   PATH_MFMA, PATH_MFMA_64x64_RING4, PATH_MFMA_128x64_RING4, PATH_MFMA_128x128,
+                   PATH_MFMA_128x128_RING4, PATH_MFMA_256x256)
 
 _OUT_CODES = {torch.float32: OUT_F32, torch.bfloat16: OUT_BF16, torch.int32: OUT_I32}
 _LAYOUTS = {"nk": B_NK, "kn": B_KN}
 _PATHS = {"auto": PATH_AUTO, "gemv": PATH_GEMV, "mfma": PATH_MFMA, "generic": PATH_GENERIC,
           "gemv_dot": PATH_GEMV_DOT, "mfma_256x256": PATH_MFMA_256x256, "mfma_128x128": PATH_MFMA_128x128,
-          "mfma_128x128_ring4": PATH_MFMA_128x128_RING4}
+          "mfma_128x128_ring4": PATH_MFMA_128x128_RING4, "mfma_128x64_ring4": PATH_MFMA_128x64_RING4,
+          "mfma_64x64_ring4": PATH_MFMA_64x64_RING4}
 
 
 def _stream(t: torch.Tensor) -> int:

@@ -61,13 +61,15 @@ enum fke_path {
     FKE_PATH_GENERIC = 3, /* any-shape tiled fallback (exact reference order)   */
     FKE_PATH_GEMV_DOT = 4, /* decode, VALU dot products only (no MFMA): INT8,   */
                            /* B [N,K], M <= 16, K % 64 == 0 (fke_qgemm_i8*_on_path) */
-    /* The MFMA GEMM with its workgroup tile pinned (FKE_PATH_MFMA picks
-     * 128x128 for short K and where 256x256 tiles would leave CUs idle, see
-     * fke_select_mfma_tile).  Same results bit for bit; 128x128 takes B [N,K]
-     * only (B [K,N]: hipErrorInvalidValue). */
+    /* The MFMA GEMM with its workgroup tile pinned (FKE_PATH_MFMA picks a
+     * 128x128 tile where 256x256 tiles would leave CUs idle, see
+     * fke_select_mfma_tile).  Same results bit for bit; the 128x128 tiles
+     * take B [N,K] only (B [K,N]: hipErrorInvalidValue). */
     FKE_PATH_MFMA_256x256 = 5,
     FKE_PATH_MFMA_128x128 = 6,
-    FKE_PATH_MFMA_128x128_RING4 = 7 /* 128x128, one workgroup per CU, four LDS stages */
+    FKE_PATH_MFMA_128x128_RING4 = 7, /* 128x128, one workgroup per CU, four LDS stages */
+    FKE_PATH_MFMA_128x64_RING4 = 8,  /* 128x64 (rows x columns), the same; not SwiGLU  */
+    FKE_PATH_MFMA_64x64_RING4 = 9    /* 64x64, the same; not SwiGLU                    */
 };
 
 /*
@@ -297,12 +299,12 @@ int fke_select_path_i8_swiglu(const void* A, const void* W, const void* H, int M
                               int out_dtype);
 int fke_select_path_half(const void* A, const void* B, const void* C, int M, int N, int K,
                          int in_dtype, int out_dtype, int b_layout);
-/* The workgroup tile FKE_PATH_MFMA runs for this shape on a GPU of `cus`
- * CUs (<= 0: the current device's, 256 without a device), as the
- * FKE_PATH_MFMA_* value that pins it, or -1 for bad arguments.
- * operand_bytes: 1 (INT8, FP8) or 2 (fp16, bf16); swiglu != 0 for the fused
- * SwiGLU GEMM with N = 2I.  Host logic only; launches nothing. */
-int fke_select_mfma_tile(int M, int N, int K, int operand_bytes, int b_layout, int swiglu, int cus);
+/* The workgroup tile FKE_PATH_MFMA runs for this shape (any operand type) on
+ * a GPU of `cus` CUs (<= 0: the current device's, 256 without a device), as
+ * the FKE_PATH_MFMA_* value that pins it, or -1 for bad arguments; swiglu !=
+ * 0 for the fused SwiGLU GEMM with N = 2I.  Host logic only; launches
+ * nothing. */
+int fke_select_mfma_tile(int M, int N, int K, int b_layout, int swiglu, int cus);
 
 /* Replaces flash_engine::print_device_info (reference include/flash_engine.h:29,
  * src/flash_engine_api.cu:7-27): prints the device's properties to stdout. */

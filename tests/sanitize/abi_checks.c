@@ -65,7 +65,7 @@ int main(void) {
     const int dims[] = {1, 2, 3, 15, 16, 17, 63, 64, 65, 127, 128, 129, 512, 513, 2047, 2048, 4095, 4096,
                         4104, 8192, 14336, 65536, 1 << 20, (1 << 20) + 16, 1 << 24, INT_MAX / 2, INT_MAX};
     const int nd = (int)(sizeof dims / sizeof *dims);
-    long n_paths[5] = {0}, n_ws = 0, n_tiles[3] = {0};
+    long n_paths[5] = {0}, n_ws = 0, n_tiles[5] = {0};
     for (int a = 0; a < nd; ++a)
         for (int b = 0; b < nd; ++b)
             for (int c = 0; c < nd; ++c)
@@ -89,18 +89,20 @@ int main(void) {
                     const size_t row = (size_t)((N + 127LL) / 128) * 128 * 4 * (size_t)M;
                     CHECK(ws == 0 || (lay == FKE_B_KN && M <= 16 && ws % row == 0 && ws / row >= 2 && ws / row <= 8));
                     ++n_ws;
-                    /* MFMA tile: the 128x128 ones for B [N,K] only; -1 only for an odd SwiGLU N */
-                    for (int sw = 0; sw < 4; ++sw) {
-                        const int t = fke_select_mfma_tile(M, N, K, 1 + (sw >> 1), lay, sw & 1, 256);
-                        CHECK(t == -1 ? ((sw & 1) && N % 2)
+                    /* MFMA tile: the small ones for B [N,K] only, the narrow rings not for SwiGLU;
+                       -1 only for an odd SwiGLU N */
+                    for (int sw = 0; sw < 2; ++sw) {
+                        const int t = fke_select_mfma_tile(M, N, K, lay, sw, 256);
+                        CHECK(t == -1 ? (sw && N % 2)
                                       : (t == FKE_PATH_MFMA_256x256 ||
-                                         ((t == FKE_PATH_MFMA_128x128 || t == FKE_PATH_MFMA_128x128_RING4) &&
-                                          lay == FKE_B_NK)));
+                                         (t >= FKE_PATH_MFMA_128x128 && t <= FKE_PATH_MFMA_64x64_RING4 &&
+                                          lay == FKE_B_NK &&
+                                          !(sw && t >= FKE_PATH_MFMA_128x64_RING4))));
                         if (t >= 0) ++n_tiles[t - FKE_PATH_MFMA_256x256];
                     }
                 }
     CHECK(n_paths[FKE_PATH_GEMV + 1] > 0 && n_paths[FKE_PATH_MFMA + 1] > 0 && n_paths[FKE_PATH_GENERIC + 1] > 0);
-    CHECK(n_tiles[0] > 0 && n_tiles[1] > 0 && n_tiles[2] > 0);
+    for (int t = 0; t < 5; ++t) CHECK(n_tiles[t] > 0);
     CHECK(fke_select_path_i8(NULL, P, P, 8, 8, 8, 0, 0) == -1);
     CHECK(fke_select_path_f8(P, P, P, 8, 8, 8, FKE_OUT_I32, 0) == -1);
     CHECK(fke_status_string(1) != NULL && fke_version() != NULL);

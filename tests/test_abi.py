@@ -135,7 +135,8 @@ def test_swiglu_rejects_bad_arguments():
     (3, 14336, 4096, _lib.PATH_GEMV),
     (16, 14336, 4096, _lib.PATH_GEMV),
     (17, 14336, 4096, _lib.PATH_GEMV),     # batches: the LDS-streamed kernel while its cost model wins
-    (64, 14336, 4096, _lib.PATH_GEMV),
+    (32, 14336, 4096, _lib.PATH_GEMV),
+    (64, 14336, 4096, _lib.PATH_MFMA),     # the 128x128 ring (SwiGLU pairs need 128 columns)
     (128, 14336, 4096, _lib.PATH_MFMA),
     (4096, 14336, 4096, _lib.PATH_MFMA),
     (64, 64, 100, _lib.PATH_GENERIC),
@@ -259,14 +260,15 @@ def test_path_unavailable_for_shape_is_rejected():
     (4, 14336, 4096, 0, _lib.PATH_GEMV),
     (16, 14336, 4096, 0, _lib.PATH_GEMV),
     (17, 14336, 4096, 0, _lib.PATH_GEMV),    # batches: LDS-streamed kernel against the MFMA GEMM's cost
-    (64, 14336, 4096, 0, _lib.PATH_GEMV),
-    (65, 14336, 4096, 0, _lib.PATH_MFMA),    # past one 64-row chunk: the MFMA GEMM's 128x128 ring
-    (128, 14336, 4096, 0, _lib.PATH_MFMA),
+    (32, 14336, 4096, 0, _lib.PATH_GEMV),
+    (48, 14336, 4096, 0, _lib.PATH_MFMA),    # four activation blocks: the MFMA GEMM's 64x64 ring is faster
+    (64, 14336, 4096, 0, _lib.PATH_MFMA),
+    (128, 14336, 4096, 0, _lib.PATH_MFMA),   # 128x64 ring
     (192, 14336, 4096, 0, _lib.PATH_MFMA),
-    (128, 4096, 4096, 0, _lib.PATH_GEMV),
-    (192, 4096, 4096, 0, _lib.PATH_MFMA),
+    (64, 4096, 4096, 0, _lib.PATH_GEMV),
+    (128, 4096, 4096, 0, _lib.PATH_MFMA),
     (384, 4096, 4096, 0, _lib.PATH_MFMA),
-    (256, 1792, 4096, 0, _lib.PATH_GEMV),    # small N: the streamed kernel's chunks run side by side
+    (128, 1792, 4096, 0, _lib.PATH_GEMV),    # small N: the streamed kernel's chunks run side by side
     (512, 1792, 4096, 0, _lib.PATH_MFMA),
     (384, 4096, 14336, 0, _lib.PATH_MFMA),
     (512, 4096, 14336, 0, _lib.PATH_MFMA),
@@ -301,7 +303,8 @@ def test_dispatch_unaligned_pointer_falls_back():
 @pytest.mark.parametrize("M,N,K,layout,expect", [
     (1, 14336, 4096, 0, _lib.PATH_GEMV),      # FP8 decode: the LDS-streamed kernel
     (16, 14336, 4096, 0, _lib.PATH_GEMV),
-    (64, 14336, 4096, 0, _lib.PATH_GEMV),
+    (32, 14336, 4096, 0, _lib.PATH_GEMV),
+    (64, 14336, 4096, 0, _lib.PATH_MFMA),     # batches past 32 rows: the MFMA GEMM's 64x64 ring
     (1, 14336, 4096, 1, _lib.PATH_GEMV),      # B [K,N] (the reference layout): transposing decode kernel
     (16, 14336, 4096, 1, _lib.PATH_GEMV),
     (17, 14336, 4096, 1, _lib.PATH_MFMA),
@@ -348,43 +351,51 @@ def test_torch_extension_rejects_host_tensors():
         m.quantized_gemm_int8_swiglu_forward(a, a)
 
 
-@pytest.mark.parametrize("M,N,K,nbytes,layout,swiglu,cus,want", [
-    (8192, 8192, 8192, 1, 0, 0, 256, _lib.PATH_MFMA_256x256),   # 1024 tiles
-    (4096, 11008, 4096, 1, 0, 0, 256, _lib.PATH_MFMA_256x256),  # 688 tiles
-    (4096, 1376, 4096, 1, 0, 0, 256, _lib.PATH_MFMA_128x128),   # 96 tiles of 256x256, 352 of 128x128
-    (8192, 1024, 8192, 1, 0, 0, 256, _lib.PATH_MFMA_128x128),   # 128 / 512: one round of two per CU
-    (512, 4096, 4096, 1, 0, 0, 256, _lib.PATH_MFMA_128x128_RING4),  # 128 tiles: one per CU at most
-    (128, 14336, 4096, 1, 0, 0, 256, _lib.PATH_MFMA_128x128_RING4),  # 112
-    (1024, 4096, 4096, 2, 0, 0, 256, _lib.PATH_MFMA_128x128_RING4),  # 256
-    (256, 4096, 1024, 1, 0, 0, 256, _lib.PATH_MFMA_128x128_RING4),   # 64, short K
-    (3072, 4096, 4096, 1, 0, 0, 256, _lib.PATH_MFMA_256x256),   # 192 / 768: a second, partial round
-    (1024, 14336, 4096, 1, 0, 0, 256, _lib.PATH_MFMA_256x256),  # 224 / 896
-    (8192, 8192, 2048, 1, 0, 0, 256, _lib.PATH_MFMA_128x128),   # short K, 8-bit: <= 2048 bytes
-    (8192, 8192, 2049, 1, 0, 0, 256, _lib.PATH_MFMA_256x256),
-    (8192, 8192, 512, 2, 0, 0, 256, _lib.PATH_MFMA_128x128),    # short K, 16-bit: <= 1024 bytes
-    (8192, 8192, 1024, 2, 0, 0, 256, _lib.PATH_MFMA_256x256),
-    (4096, 1376, 4096, 2, 0, 0, 256, _lib.PATH_MFMA_128x128),   # few tiles, bf16
-    (4096, 1376, 4096, 1, 1, 0, 256, _lib.PATH_MFMA_256x256),   # B [K,N]: 256x256 only
-    (4096, 4096, 1024, 1, 1, 0, 256, _lib.PATH_MFMA_256x256),
-    (4096, 1376, 4096, 1, 0, 1, 256, _lib.PATH_MFMA_128x128),   # SwiGLU, 688 outputs: 96 tiles / 352
-    (4096, 2752, 4096, 1, 0, 1, 256, _lib.PATH_MFMA_256x256),   # SwiGLU, 1376 outputs: 176 / 704
-    (4096, 1376, 4096, 1, 0, 0, 80, _lib.PATH_MFMA_256x256),    # fills 80 CUs
+@pytest.mark.parametrize("M,N,K,layout,swiglu,cus,want", [
+    (8192, 8192, 8192, 0, 0, 256, _lib.PATH_MFMA_256x256),       # 1024 tiles of 256x256
+    (4096, 11008, 4096, 0, 0, 256, _lib.PATH_MFMA_256x256),      # 688
+    (3072, 4096, 4096, 0, 0, 256, _lib.PATH_MFMA_256x256),       # 192 / 768 of 128x128: a partial second round
+    (1024, 14336, 4096, 0, 0, 256, _lib.PATH_MFMA_256x256),      # 224 / 896
+    (8192, 8192, 1024, 0, 0, 256, _lib.PATH_MFMA_256x256),       # short K, many tiles
+    (4096, 1376, 4096, 0, 0, 256, _lib.PATH_MFMA_128x128),       # 96 / 352: one round of two per CU
+    (8192, 1024, 8192, 0, 0, 256, _lib.PATH_MFMA_128x128),       # 128 / 512
+    (512, 14336, 4096, 0, 0, 256, _lib.PATH_MFMA_128x128),       # 112 / 448
+    (64, 14336, 4096, 0, 0, 256, _lib.PATH_MFMA_64x64_RING4),    # 224 tiles of 64x64: one per CU at most
+    (256, 4096, 1024, 0, 0, 256, _lib.PATH_MFMA_64x64_RING4),    # 256
+    (512, 1792, 4096, 0, 0, 256, _lib.PATH_MFMA_64x64_RING4),    # 224
+    (128, 14336, 4096, 0, 0, 256, _lib.PATH_MFMA_128x64_RING4),  # 448 of 64x64, 224 of 128x64
+    (512, 4096, 4096, 0, 0, 256, _lib.PATH_MFMA_128x64_RING4),   # 512 / 256
+    (1024, 4096, 4096, 0, 0, 256, _lib.PATH_MFMA_128x128_RING4), # 1024 / 512 / 256 of 128x128
+    (256, 14336, 4096, 0, 0, 256, _lib.PATH_MFMA_128x128_RING4), # 224 of 128x128
+    (4096, 1376, 4096, 1, 0, 256, _lib.PATH_MFMA_256x256),       # B [K,N]: 256x256 only
+    (128, 4096, 1024, 1, 0, 256, _lib.PATH_MFMA_256x256),
+    (4096, 1376, 4096, 0, 1, 256, _lib.PATH_MFMA_128x128),       # SwiGLU, 688 outputs: 96 / 352
+    (128, 28672, 4096, 0, 1, 256, _lib.PATH_MFMA_128x128_RING4), # SwiGLU, 14336 outputs: 224 tiles of 64
+    (4096, 2752, 4096, 0, 1, 256, _lib.PATH_MFMA_256x256),       # SwiGLU, 1376 outputs: 176 / 704
+    (4096, 1376, 4096, 0, 0, 80, _lib.PATH_MFMA_256x256),        # fills 80 CUs
 ])
-def test_mfma_tile_choice(M, N, K, nbytes, layout, swiglu, cus, want):
-    assert _lib.lib().fke_select_mfma_tile(M, N, K, nbytes, layout, swiglu, cus) == want
+def test_mfma_tile_choice(M, N, K, layout, swiglu, cus, want):
+    assert _lib.lib().fke_select_mfma_tile(M, N, K, layout, swiglu, cus) == want
 
 
 def test_mfma_tile_choice_rejects_bad_arguments():
     L = _lib.lib()
-    assert L.fke_select_mfma_tile(0, 64, 64, 1, 0, 0, 256) == -1
-    assert L.fke_select_mfma_tile(64, 64, 64, 1, 2, 0, 256) == -1
-    assert L.fke_select_mfma_tile(64, 63, 64, 1, 0, 1, 256) == -1
-    assert L.fke_select_mfma_tile(64, 64, 64, 4, 0, 0, 256) == -1
+    assert L.fke_select_mfma_tile(0, 64, 64, 0, 0, 256) == -1
+    assert L.fke_select_mfma_tile(64, 64, 64, 2, 0, 256) == -1
+    assert L.fke_select_mfma_tile(64, 63, 64, 0, 1, 256) == -1
+
+
+def test_narrow_ring_tiles_reject_swiglu_before_any_launch():
+    L = _lib.lib()
+    for path in (_lib.PATH_MFMA_128x64_RING4, _lib.PATH_MFMA_64x64_RING4):
+        assert L.fke_qgemm_i8_swiglu_on_path(path, P, P, P, 64, 64, 256, None, None, 1.0, 1.0, None,
+                                             _lib.OUT_BF16, None) == _lib.HIP_ERROR_INVALID_VALUE
 
 
 def test_pinned_small_tile_rejects_b_kn_before_any_launch():
     L = _lib.lib()
-    for path in (_lib.PATH_MFMA_128x128, _lib.PATH_MFMA_128x128_RING4):
+    for path in (_lib.PATH_MFMA_128x128, _lib.PATH_MFMA_128x128_RING4, _lib.PATH_MFMA_128x64_RING4,
+                 _lib.PATH_MFMA_64x64_RING4):
         assert L.fke_qgemm_i8_on_path(path, P, P, P, 256, 256, 256, None, None, 1.0, 1.0, None,
                                       _lib.OUT_F32, _lib.B_KN, None) == _lib.HIP_ERROR_INVALID_VALUE
         assert L.fke_qgemm_f8_on_path(path, P, P, P, 256, 256, 256, 1.0, 1.0, None,

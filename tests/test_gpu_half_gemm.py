@@ -90,7 +90,8 @@ MFMA_SHAPES = [(256, 256, 64), (300, 200, 512), (513, 333, 384), (1, 100, 128), 
 
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
 @pytest.mark.parametrize("shape", MFMA_SHAPES)
-@pytest.mark.parametrize("tile", ["mfma_256x256", "mfma_128x128", "mfma_128x128_ring4"])
+@pytest.mark.parametrize("tile", ["mfma_256x256", "mfma_128x128", "mfma_128x128_ring4", "mfma_128x64_ring4",
+                                  "mfma_64x64_ring4"])
 def test_mfma_integer_operands_bit_exact(oracle, dev, dt, shape, tile):
     M, N, K = shape
     say("half gemm mfma integers", dt, shape, tile)
@@ -135,7 +136,7 @@ def test_mfma_random_within_bound(oracle, dev, dt, shape):
     assert np.all(err <= bound), f"max err/bound {np.max(err / np.maximum(bound, 1e-30)):.3f}"
     gotb = run(A, B, dt, path="mfma", out="bf16")
     same_bits(gotb, enc(got, "bf16"), "bf16 out = bf16(fp32 out)")
-    for tile in ("mfma_256x256", "mfma_128x128", "mfma_128x128_ring4"):  # same K order in every tile
+    for tile in ("mfma_256x256", "mfma_128x128", "mfma_128x128_ring4", "mfma_128x64_ring4", "mfma_64x64_ring4"):
         same_bits(run(A, B, dt, path=tile), got, f"{tile} vs auto")
 
 

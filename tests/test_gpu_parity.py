@@ -124,7 +124,8 @@ def test_c1_golden(oracle, dev, path):
 
 # Every MFMA tile, pinned (the dispatcher would pick a small one for shapes
 # this size), and the generic kernel.  B [K,N] runs the 256x256 tile only.
-I8_FAMILIES = ["mfma_256x256", "mfma_128x128", "mfma_128x128_ring4", "generic"]
+SMALL_TILES = ["mfma_128x128", "mfma_128x128_ring4", "mfma_128x64_ring4", "mfma_64x64_ring4"]
+I8_FAMILIES = ["mfma_256x256"] + SMALL_TILES + ["generic"]
 
 
 @pytest.mark.parametrize("path", I8_FAMILIES)
@@ -132,7 +133,7 @@ I8_FAMILIES = ["mfma_256x256", "mfma_128x128", "mfma_128x128_ring4", "generic"]
 @pytest.mark.parametrize("out", ["f32", "bf16", "i32"])
 @pytest.mark.parametrize("opts", ["vec_bias", "scalar"])
 def test_i8_families_ragged(oracle, dev, path, layout, out, opts):
-    if layout == "kn" and path in ("mfma_128x128", "mfma_128x128_ring4"):
+    if layout == "kn" and path in SMALL_TILES:
         pytest.skip("B [K,N] runs the 256x256 tile only (rejection tested in test_mfma_small_tile_rejects_b_kn)")
     M, N, K = 300, 528, 384  # ragged in M and N against every tile
     say("i8", path, layout, out, opts, (M, N, K))
@@ -626,7 +627,7 @@ def test_c4_square_full(oracle, dev):
     assert_same(f32, oracle_out(oracle, acc_ref, sa, sb, 1.0, 1.0, None, "f32"), "c4 f32")
 
 
-@pytest.mark.parametrize("tile", ["mfma_128x128", "mfma_128x128_ring4", "mfma_256x256"])
+@pytest.mark.parametrize("tile", SMALL_TILES + ["mfma_256x256"])
 @pytest.mark.parametrize("shape", [(1, 1, 128), (129, 65, 256), (256, 128, 128), (257, 129, 640),
                                    (513, 1000, 1152), (64, 4000, 256), (100, 300, 384), (130, 200, 512),
                                    (300, 2000, 1664)])
@@ -646,7 +647,7 @@ def test_mfma_tiles_ragged_shapes(oracle, dev, tile, shape):
 
 def test_mfma_small_tile_rejects_b_kn(oracle, dev):
     A, B, sa, sb, _ = inputs_i8(oracle, 64, 64, 128, 950, "kn")
-    for tile in ("mfma_128x128", "mfma_128x128_ring4"):
+    for tile in SMALL_TILES:
         with pytest.raises(_lib.FkeError):
             gpu_i8(A, B, "kn", "f32", tile, sa, sb)
 
@@ -654,26 +655,28 @@ def test_mfma_small_tile_rejects_b_kn(oracle, dev):
 @pytest.mark.parametrize("M,N,K,out,want", [
     (4096, 1376, 4096, "bf16", _lib.PATH_MFMA_128x128),   # 8-way column shard of 11008
     (8192, 1024, 8192, "f32", _lib.PATH_MFMA_128x128),    # 8-way column shard of 8192
-    (512, 4096, 4096, "bf16", _lib.PATH_MFMA_128x128_RING4),  # a short prefill: one tile per CU at most
-    (128, 14336, 4096, "bf16", _lib.PATH_MFMA_128x128_RING4),  # a decode batch of 128 rows
-    (4096, 4096, 1024, "f32", _lib.PATH_MFMA_128x128),    # short K: 1024 tiles
-    (8192, 8192, 1024, "i32", _lib.PATH_MFMA_128x128),    # 8-way K shard of 8192^3 (int32 partials)
+    (512, 4096, 4096, "bf16", _lib.PATH_MFMA_128x64_RING4),   # a short prefill: one tile per CU at most
+    (128, 14336, 4096, "bf16", _lib.PATH_MFMA_128x64_RING4),  # a decode batch of 128 rows
+    (64, 14336, 4096, "bf16", _lib.PATH_MFMA_64x64_RING4),    # a decode batch of 64 rows
+    (500, 1792, 4096, "f32", _lib.PATH_MFMA_64x64_RING4),     # ragged rows, 224 tiles
+    (2048, 1376, 4096, "f32", _lib.PATH_MFMA_128x128_RING4),  # 176 tiles
 ])
 def test_mfma_few_tile_shapes_full(oracle, dev, M, N, K, out, want):
-    """Shapes the dispatcher gives the 128x128 tile (fewer 256x256 tiles than
-    CUs, or short K): the tile it picks on this GPU, every output against the
-    oracle, and the same outputs from both pinned tiles."""
+    """Shapes the dispatcher gives a 128x128 tile (fewer 256x256 tiles than
+    CUs): the tile it picks on this GPU, every output against the oracle, and
+    the same outputs from every pinned tile (and the streamed decode kernel
+    where it takes the shape)."""
     L = _lib.lib()
-    pick = L.fke_select_mfma_tile(M, N, K, 1, 0, 0, 0)
+    pick = L.fke_select_mfma_tile(M, N, K, 0, 0, 0)
     say("few-tile shape", M, N, K, out, "tile path", pick)
-    assert L.fke_select_mfma_tile(M, N, K, 1, 0, 0, 256) == want
+    assert L.fke_select_mfma_tile(M, N, K, 0, 0, 256) == want
     assert torch.cuda.get_device_properties(0).multi_processor_count != 256 or pick == want
     A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 4000 + N)
     acc = oracle.w8a8_acc(A, B, nthreads=NTH)
     ref = oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, out)
     got = gpu_i8(A, B, "nk", out, "auto", sa, sb, bias=bias)
     assert_same(got, ref, f"auto {M}x{N}x{K}")
-    for tile in ("mfma_256x256", "mfma_128x128", "mfma_128x128_ring4"):
+    for tile in ["mfma_256x256"] + SMALL_TILES:
         assert_same(gpu_i8(A, B, "nk", out, tile, sa, sb, bias=bias), ref, f"{tile} {M}x{N}x{K}")
     if M <= 512:  # the streamed decode kernel gives the same bits
         assert_same(gpu_i8(A, B, "nk", out, "gemv", sa, sb, bias=bias), ref, f"gemv {M}x{N}x{K}")
@@ -761,7 +764,7 @@ def test_fp8_mfma_tolerance(oracle, dev, layout, out, nan_codes):
     got = oracle.bf16_to_f32(big) if out == "bf16" else big
     assert_fp8_close(got, ref, out, f"mfma 256x256 {layout} nan={nan_codes}")
     if layout == "nk":
-        for tile in ("mfma_128x128", "mfma_128x128_ring4"):
+        for tile in SMALL_TILES:
             assert_same(gpu_f8(A, B, sa, sb, layout, out, tile, bias=bias), big, f"fp8 {tile} vs 256x256")
 
 
