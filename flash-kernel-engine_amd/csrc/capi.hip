@@ -200,16 +200,16 @@ int pick_f8(const GemmArgs& p) {
     return FKE_PATH_GENERIC;
 }
 
-// FKE_PATH_MFMA_* -> the kernel's tile (B [K,N] runs 256x256 only); -1 for
-// any other path.
+// FKE_PATH_MFMA_* -> the kernel's tile (the 64-column rings: not SwiGLU);
+// -1 for any other path, -2 for a tile the call cannot take.
 int mfma_tile_of_path(int path, const GemmArgs& p) {
     switch (path) {
         case FKE_PATH_MFMA: return fke::MFMA_TILE_AUTO;
         case FKE_PATH_MFMA_256x256: return fke::MFMA_TILE_256x256;
-        case FKE_PATH_MFMA_128x128: return p.b_layout == FKE_B_NK ? fke::MFMA_TILE_128x128 : -2;
-        case FKE_PATH_MFMA_128x128_RING4: return p.b_layout == FKE_B_NK ? fke::MFMA_TILE_128x128_RING4 : -2;
-        case FKE_PATH_MFMA_128x64_RING4: return p.b_layout == FKE_B_NK && !p.swiglu ? fke::MFMA_TILE_128x64_RING4 : -2;
-        case FKE_PATH_MFMA_64x64_RING4: return p.b_layout == FKE_B_NK && !p.swiglu ? fke::MFMA_TILE_64x64_RING4 : -2;
+        case FKE_PATH_MFMA_128x128: return fke::MFMA_TILE_128x128;
+        case FKE_PATH_MFMA_128x128_RING4: return fke::MFMA_TILE_128x128_RING4;
+        case FKE_PATH_MFMA_128x64_RING4: return p.swiglu ? -2 : fke::MFMA_TILE_128x64_RING4;
+        case FKE_PATH_MFMA_64x64_RING4: return p.swiglu ? -2 : fke::MFMA_TILE_64x64_RING4;
         default: return -1;
     }
 }

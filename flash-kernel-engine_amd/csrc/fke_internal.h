@@ -35,8 +35,7 @@ constexpr int elem_bytes(int elem) { return elem >= ELEM_F16 ? 2 : 1; }
 // Launchers (return this launch's status; arguments already validated).
 hipError_t launch_generic(const GemmArgs& p, int elem, hipStream_t stream);
 hipError_t launch_gemv_i8(const GemmArgs& p, hipStream_t stream);
-// MFMA GEMM workgroup tile: AUTO = chosen by tile count (mfma_pick_tile); B
-// [K,N] always runs 256x256.
+// MFMA GEMM workgroup tile: AUTO = chosen by tile count (mfma_pick_tile).
 enum MfmaTile {
     MFMA_TILE_AUTO = 0,
     MFMA_TILE_256x256 = 1,

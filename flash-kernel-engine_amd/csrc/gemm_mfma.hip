@@ -14,11 +14,11 @@
 //   INT8: v_mfma_i32_32x32x32_i8   (exact int32 accumulation), 4 k steps/stage
 //   FP8 : v_mfma_f32_32x32x64_f8f6f4 with E4M3 operands (fp32), 2 k steps/stage
 // K advances 128 bytes per stage; two LDS stages of (256+256)x128 bytes
-// (128 KiB of the CU's 160 KiB).  A (and B when stored [N,K]) is copied
-// global->LDS with 128-bit direct-to-LDS loads (buffer_load_dwordx4 ... lds),
-// eight lanes per 128-byte row segment, from per-lane 32-bit offsets computed
-// once.  B stored [K,N] goes through registers and is byte-transposed with
-// v_perm_b32 into LDS.
+// (128 KiB of the CU's 160 KiB).  Both operands are copied global->LDS with
+// 128-bit direct-to-LDS loads (buffer_load_dwordx4 ... lds) from per-lane
+// 32-bit offsets computed once: A, and B stored [N,K], eight lanes per
+// 128-byte row segment; B stored [K,N] row by row as it lies in memory, its
+// fragments then read with the transposing ds_read_b64_tr_b8.
 //
 // Schedule of one stage, per wave (steps 0..n-1 of the stage are in LDS): n
 // groups of 16 MFMAs.  Group 0 runs the previous stage's last step, carried
@@ -143,25 +143,38 @@ struct Panel {
     }
 };
 
-// B stored [K,N] (256-column tiles only): a stage is 128 k rows of 256 n bytes, copied as they lie
-// in memory, four rows per 1-KiB load; 16-byte chunk c of row k is stored at
-// chunk c ^ (k & 15).  The MFMA fragments (one column n per lane, k bytes
-// consecutive) are then read with ds_read_b64_tr_b8, which transposes 8x8
-// byte blocks across lanes.  Columns past N read whatever follows them in
-// memory (those outputs are never stored); reads past the end of B fall out
-// of the buffer's range and return 0.
+// Chunk swizzle of a B [K,N] stage whose k rows hold BN bytes: logical
+// 16-byte chunk c of row r sits at chunk c ^ kn_swz<BN>(r).  With it the
+// transposed reads below touch every LDS bank once per 16-lane group (and,
+// for 128- and 64-byte rows, once per 32-lane half), and it repeats every 8
+// rows (16 for 256-byte rows), so other k steps are immediate offsets away.
+template <int BN>
+__device__ __forceinline__ int kn_swz(int r) {
+    if constexpr (BN == 256) return r & 15;
+    else if constexpr (BN == 128) return r & 7;
+    else return (r >> 1) & 3;
+}
+
+// B stored [K,N]: a stage is 128 k rows of BN n bytes, copied as they lie in
+// memory, 1024/BN rows per 1-KiB load, chunks swizzled by kn_swz.  The MFMA
+// fragments (one column n per lane, k bytes consecutive) are then read with
+// ds_read_b64_tr_b8, which transposes 8x8 byte blocks across lanes.  Columns
+// past N read whatever follows them in memory (those outputs are never
+// stored); reads past the end of B fall out of the buffer's range and return 0.
+template <int BN>
 struct KNPanel {
-    static constexpr int PW = 8;  // 1-KiB loads per wave per stage
-    __amdgpu_buffer_rsrc_t rsrc;  // all of B, K x N bytes
-    uint32_t off[PW];             // byte offset of this lane's 16-byte source at stage 0
-    int stage_bytes;              // BK rows of B
+    static constexpr int PW = BN / 32;  // 1-KiB loads per wave per stage
+    static constexpr int CH = BN / 16;  // 16-byte chunks per k row
+    __amdgpu_buffer_rsrc_t rsrc;        // all of B, K x N bytes
+    uint32_t off[PW];                   // byte offset of this lane's 16-byte source at stage 0
+    int stage_bytes;                    // BK rows of B
     __device__ void init(const int8_t* B, int N, int K, int n0, int wave, int lane) {
         rsrc = make_rsrc(B, K * N);
         stage_bytes = BK * N;
 #pragma unroll
         for (int i = 0; i < PW; ++i) {
-            const int r = (wave * PW + i) * 4 + (lane >> 4);  // k row within the stage
-            const int c = (lane & 15) ^ (r & 15);             // logical chunk landing at physical lane & 15
+            const int r = (wave * PW + i) * (1024 / BN) + lane / CH;  // k row within the stage
+            const int c = (lane % CH) ^ kn_swz<BN>(r);                // logical chunk landing at physical lane % CH
             off[i] = static_cast<uint32_t>(r * N + n0 + c * 16);
         }
     }
@@ -183,17 +196,17 @@ __device__ __forceinline__ v2i ds_read_tr8(const uint8_t* p) {
 // Per-lane offsets (within a stage's B region) of the transposed reads of
 // B block j, k rows 8*rr..8*rr+7 of the lane's half of the first step.
 // Lane l = 16G + s reads row HS*(G>>1) + 8*rr + s/2 at column block
-// wn*128 + 32j + 16*(G&1) + 8*(s&1), so that after the transpose lane l
-// holds column wn*128 + 32j + l%32 with its k bytes in order.  Rows a
-// multiple of 16 apart share the chunk swizzle, so other steps (and, for
-// FP8, k rows 16..31 of the half) are immediate offsets away.
-template <int ELEM>
+// wn*WN + 32j + 16*(G&1) + 8*(s&1), so that after the transpose lane l
+// holds column wn*WN + 32j + l%32 with its k bytes in order.  The swizzle
+// repeats every 8 rows, so other steps (and, for FP8, k rows 16..31 of the
+// half) are immediate offsets away.
+template <int ELEM, class TL>
 __device__ __forceinline__ uint32_t kn_read_off(int lane, int wn, int j, int rr) {
     constexpr int HS = ELEM == ELEM_I8 ? 16 : 32;  // k bytes of one lane-half per step
     const int G = lane >> 4, sl = lane & 15, b = sl >> 1;
     const int row = HS * (G >> 1) + 8 * rr + b;
-    const int chunk = (wn * 8 + 2 * j + (G & 1)) ^ (row & 15);
-    return static_cast<uint32_t>(row * 256 + chunk * 16 + 8 * (sl & 1));
+    const int chunk = (wn * (TL::WN / 16) + 2 * j + (G & 1)) ^ kn_swz<TL::BN>(row);
+    return static_cast<uint32_t>(row * TL::BN + chunk * 16 + 8 * (sl & 1));
 }
 
 // Per element type: fragment and accumulator types, k steps per stage, and
@@ -261,7 +274,7 @@ __device__ __forceinline__ void read_piece(const uint8_t* buf, int ks, int wm, i
         constexpr int KSTEP = ELEM == ELEM_I8 ? 32 : 64;  // k rows per step
         const int p = r - RA;
         const int j = ELEM == ELEM_I8 ? p >> 1 : p >> 2, rr = ELEM == ELEM_I8 ? p & 1 : p & 3;
-        const v2i x = ds_read_tr8(buf + TL::STAGE_A + kn_off[j][rr & 1] + (ks * KSTEP + (rr >> 1) * 16) * 256);
+        const v2i x = ds_read_tr8(buf + TL::STAGE_A + kn_off[j][rr & 1] + (ks * KSTEP + (rr >> 1) * 16) * TL::BN);
         f.b[j][2 * rr] = x[0];
         f.b[j][2 * rr + 1] = x[1];
         return;
@@ -327,7 +340,6 @@ constexpr int tile_cols() { return SWI ? TL::BN / 2 : TL::BN; }
 template <int ELEM, int BL, int OUT, bool SWI, class TL>
 __global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p) {
     static_assert(!SWI || (ELEM == ELEM_I8 && BL == FKE_B_NK && OUT != FKE_OUT_I32), "SwiGLU: INT8, B [N,K], float out");
-    static_assert(BL == FKE_B_NK || TL::NJ == 4, "B [K,N]: 256-column tiles");
     static_assert(!SWI || TL::NJ >= 2, "SwiGLU: each wave pairs gate and up blocks");
     constexpr int NKS = Mma<ELEM>::KSTEPS;
     constexpr int NI = TL::NI, NJ = TL::NJ, BM = TL::BM, NPIECE = TL::NPIECE;
@@ -383,7 +395,7 @@ __global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p
     const int KT = K / BK;
     Panel<TL::PWA> pa;
     pa.init(A, K, m0, M, wave, lane);
-    using BPanel = typename std::conditional<BL == FKE_B_NK, Panel<TL::PWB>, KNPanel>::type;
+    using BPanel = typename std::conditional<BL == FKE_B_NK, Panel<TL::PWB>, KNPanel<TL::BN>>::type;
     BPanel pb;
     uint32_t kn_off[NJ][2] = {};
     if constexpr (BL == FKE_B_NK) {
@@ -393,13 +405,13 @@ __global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p
 #pragma unroll
         for (int j = 0; j < NJ; ++j)
 #pragma unroll
-            for (int rr = 0; rr < 2; ++rr) kn_off[j][rr] = kn_read_off<ELEM>(lane, wn, j, rr);
+            for (int rr = 0; rr < 2; ++rr) kn_off[j][rr] = kn_read_off<ELEM, TL>(lane, wn, j, rr);
     }
 
     // Copy of stage kt into buffer b, slot q of NSLOT: slots 0..PWA-1 copy
     // A, the rest copy B, all buffer -> LDS.
     constexpr int PWA = TL::PWA;
-    constexpr int NSLOT = PWA + (BL == FKE_B_NK ? TL::PWB : KNPanel::PW);
+    constexpr int NSLOT = PWA + TL::PWB;  // B [K,N] panels take BN/32 loads per wave too
     auto copy = [&](int q, int kt, uint8_t* b) __attribute__((always_inline)) {
         if (q < PWA) pa.issue(q, kt * BK, b, wave);
         else if constexpr (BL == FKE_B_NK) pb.issue(q - PWA, kt * BK, b + TL::STAGE_A, wave);
@@ -668,20 +680,16 @@ hipError_t launch_t(const GemmArgs& p, hipStream_t stream, int cus) {
 
 template <int ELEM, int BL, int OUT, bool SWI = false>
 hipError_t launch_tile(const GemmArgs& p, hipStream_t s, int tile, int cus) {
-    if constexpr (BL == FKE_B_KN) {
-        return launch_t<ELEM, BL, OUT, SWI, T256>(p, s, cus);
-    } else {
-        switch (tile) {
-            case MFMA_TILE_128x128: return launch_t<ELEM, BL, OUT, SWI, T128>(p, s, cus);
-            case MFMA_TILE_128x128_RING4: return launch_t<ELEM, BL, OUT, SWI, T128R4>(p, s, cus);
-            case MFMA_TILE_128x64_RING4:
-                if constexpr (!SWI) return launch_t<ELEM, BL, OUT, SWI, T128x64R4>(p, s, cus);
-                return hipErrorInvalidValue;
-            case MFMA_TILE_64x64_RING4:
-                if constexpr (!SWI) return launch_t<ELEM, BL, OUT, SWI, T64R4>(p, s, cus);
-                return hipErrorInvalidValue;
-            default: return launch_t<ELEM, BL, OUT, SWI, T256>(p, s, cus);
-        }
+    switch (tile) {
+        case MFMA_TILE_128x128: return launch_t<ELEM, BL, OUT, SWI, T128>(p, s, cus);
+        case MFMA_TILE_128x128_RING4: return launch_t<ELEM, BL, OUT, SWI, T128R4>(p, s, cus);
+        case MFMA_TILE_128x64_RING4:
+            if constexpr (!SWI) return launch_t<ELEM, BL, OUT, SWI, T128x64R4>(p, s, cus);
+            return hipErrorInvalidValue;
+        case MFMA_TILE_64x64_RING4:
+            if constexpr (!SWI) return launch_t<ELEM, BL, OUT, SWI, T64R4>(p, s, cus);
+            return hipErrorInvalidValue;
+        default: return launch_t<ELEM, BL, OUT, SWI, T256>(p, s, cus);
     }
 }
 
@@ -744,9 +752,8 @@ bool mfma_supports(const GemmArgs& p, int elem) {
 //   which loses once the weights come from HBM (8192x8192x1024: 105 against
 //   120 us cold, though 99 against 103 warm).
 // A 256x128 tile (one workgroup per CU) measured slower than 128x128 on every
-// few-tile shape, INT8, FP8 and bf16.
+// few-tile shape, INT8, FP8 and bf16.  B [K,N] uses the same rule.
 int mfma_pick_tile(const GemmArgs& p, int cus) {
-    if (p.b_layout == FKE_B_KN) return MFMA_TILE_256x256;
     const int64_t NO = p.swiglu ? p.N / 2 : p.N;
     auto tiles = [&](int64_t bm, int64_t bn) {
         const int64_t tc = p.swiglu ? bn / 2 : bn;

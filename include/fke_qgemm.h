@@ -62,9 +62,9 @@ enum fke_path {
     FKE_PATH_GEMV_DOT = 4, /* decode, VALU dot products only (no MFMA): INT8,   */
                            /* B [N,K], M <= 16, K % 64 == 0 (fke_qgemm_i8*_on_path) */
     /* The MFMA GEMM with its workgroup tile pinned (FKE_PATH_MFMA picks a
-     * 128x128 tile where 256x256 tiles would leave CUs idle, see
-     * fke_select_mfma_tile).  Same results bit for bit; the 128x128 tiles
-     * take B [N,K] only (B [K,N]: hipErrorInvalidValue). */
+     * smaller tile where 256x256 tiles would leave CUs idle, see
+     * fke_select_mfma_tile).  Same results bit for bit, both B layouts; the
+     * 64-column tiles reject the SwiGLU GEMM (hipErrorInvalidValue). */
     FKE_PATH_MFMA_256x256 = 5,
     FKE_PATH_MFMA_128x128 = 6,
     FKE_PATH_MFMA_128x128_RING4 = 7, /* 128x128, one workgroup per CU, four LDS stages */

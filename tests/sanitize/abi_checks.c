@@ -89,14 +89,12 @@ int main(void) {
                     const size_t row = (size_t)((N + 127LL) / 128) * 128 * 4 * (size_t)M;
                     CHECK(ws == 0 || (lay == FKE_B_KN && M <= 16 && ws % row == 0 && ws / row >= 2 && ws / row <= 8));
                     ++n_ws;
-                    /* MFMA tile: the small ones for B [N,K] only, the narrow rings not for SwiGLU;
-                       -1 only for an odd SwiGLU N */
+                    /* MFMA tile: the narrow rings not for SwiGLU; -1 only for an odd SwiGLU N */
                     for (int sw = 0; sw < 2; ++sw) {
                         const int t = fke_select_mfma_tile(M, N, K, lay, sw, 256);
                         CHECK(t == -1 ? (sw && N % 2)
                                       : (t == FKE_PATH_MFMA_256x256 ||
                                          (t >= FKE_PATH_MFMA_128x128 && t <= FKE_PATH_MFMA_64x64_RING4 &&
-                                          lay == FKE_B_NK &&
                                           !(sw && t >= FKE_PATH_MFMA_128x64_RING4))));
                         if (t >= 0) ++n_tiles[t - FKE_PATH_MFMA_256x256];
                     }

@@ -367,8 +367,8 @@ def test_torch_extension_rejects_host_tensors():
     (512, 4096, 4096, 0, 0, 256, _lib.PATH_MFMA_128x64_RING4),   # 512 / 256
     (1024, 4096, 4096, 0, 0, 256, _lib.PATH_MFMA_128x128_RING4), # 1024 / 512 / 256 of 128x128
     (256, 14336, 4096, 0, 0, 256, _lib.PATH_MFMA_128x128_RING4), # 224 of 128x128
-    (4096, 1376, 4096, 1, 0, 256, _lib.PATH_MFMA_256x256),       # B [K,N]: 256x256 only
-    (128, 4096, 1024, 1, 0, 256, _lib.PATH_MFMA_256x256),
+    (4096, 1376, 4096, 1, 0, 256, _lib.PATH_MFMA_128x128),       # B [K,N]: the same rule
+    (128, 4096, 1024, 1, 0, 256, _lib.PATH_MFMA_64x64_RING4),
     (4096, 1376, 4096, 0, 1, 256, _lib.PATH_MFMA_128x128),       # SwiGLU, 688 outputs: 96 / 352
     (128, 28672, 4096, 0, 1, 256, _lib.PATH_MFMA_128x128_RING4), # SwiGLU, 14336 outputs: 224 tiles of 64
     (4096, 2752, 4096, 0, 1, 256, _lib.PATH_MFMA_256x256),       # SwiGLU, 1376 outputs: 176 / 704
@@ -390,13 +390,3 @@ def test_narrow_ring_tiles_reject_swiglu_before_any_launch():
     for path in (_lib.PATH_MFMA_128x64_RING4, _lib.PATH_MFMA_64x64_RING4):
         assert L.fke_qgemm_i8_swiglu_on_path(path, P, P, P, 64, 64, 256, None, None, 1.0, 1.0, None,
                                              _lib.OUT_BF16, None) == _lib.HIP_ERROR_INVALID_VALUE
-
-
-def test_pinned_small_tile_rejects_b_kn_before_any_launch():
-    L = _lib.lib()
-    for path in (_lib.PATH_MFMA_128x128, _lib.PATH_MFMA_128x128_RING4, _lib.PATH_MFMA_128x64_RING4,
-                 _lib.PATH_MFMA_64x64_RING4):
-        assert L.fke_qgemm_i8_on_path(path, P, P, P, 256, 256, 256, None, None, 1.0, 1.0, None,
-                                      _lib.OUT_F32, _lib.B_KN, None) == _lib.HIP_ERROR_INVALID_VALUE
-        assert L.fke_qgemm_f8_on_path(path, P, P, P, 256, 256, 256, 1.0, 1.0, None,
-                                      _lib.OUT_F32, _lib.B_KN, None) == _lib.HIP_ERROR_INVALID_VALUE

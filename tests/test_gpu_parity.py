@@ -123,7 +123,7 @@ def test_c1_golden(oracle, dev, path):
 # ------------------------------------------------------- kernel families x options
 
 # Every MFMA tile, pinned (the dispatcher would pick a small one for shapes
-# this size), and the generic kernel.  B [K,N] runs the 256x256 tile only.
+# this size), and the generic kernel, both B layouts.
 SMALL_TILES = ["mfma_128x128", "mfma_128x128_ring4", "mfma_128x64_ring4", "mfma_64x64_ring4"]
 I8_FAMILIES = ["mfma_256x256"] + SMALL_TILES + ["generic"]
 
@@ -133,8 +133,6 @@ I8_FAMILIES = ["mfma_256x256"] + SMALL_TILES + ["generic"]
 @pytest.mark.parametrize("out", ["f32", "bf16", "i32"])
 @pytest.mark.parametrize("opts", ["vec_bias", "scalar"])
 def test_i8_families_ragged(oracle, dev, path, layout, out, opts):
-    if layout == "kn" and path in SMALL_TILES:
-        pytest.skip("B [K,N] runs the 256x256 tile only (rejection tested in test_mfma_small_tile_rejects_b_kn)")
     M, N, K = 300, 528, 384  # ragged in M and N against every tile
     say("i8", path, layout, out, opts, (M, N, K))
     A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 100, layout)
@@ -628,28 +626,24 @@ def test_c4_square_full(oracle, dev):
 
 
 @pytest.mark.parametrize("tile", SMALL_TILES + ["mfma_256x256"])
+@pytest.mark.parametrize("layout", ["nk", "kn"])
 @pytest.mark.parametrize("shape", [(1, 1, 128), (129, 65, 256), (256, 128, 128), (257, 129, 640),
                                    (513, 1000, 1152), (64, 4000, 256), (100, 300, 384), (130, 200, 512),
                                    (300, 2000, 1664)])
-def test_mfma_tiles_ragged_shapes(oracle, dev, tile, shape):
+def test_mfma_tiles_ragged_shapes(oracle, dev, tile, layout, shape):
     """Every tile against the oracle, bit-exact, on shapes ragged in M and N
     against each tile (and exactly one 128x128 tile), K of 1 to 13 stages
-    (every remainder of the 4-stage ring's unrolling), every output type,
-    per-row / per-column scales with bias."""
+    (every remainder of the 4-stage ring's unrolling), both B layouts, every
+    output type, per-row / per-column scales with bias."""
     M, N, K = shape
-    say("i8 small tile", tile, shape)
-    A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 900 + M + N, "nk", act="normal")
-    acc = oracle.w8a8_acc(A, B)
+    if layout == "kn":  # the MFMA kernel takes B [K,N] with N % 16 == 0
+        N = max(16, (N + 15) // 16 * 16)
+    say("i8 small tile", tile, layout, (M, N, K))
+    A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 900 + M + N, layout, act="normal")
+    acc = oracle.w8a8_acc(A, B, oracle.B_NK if layout == "nk" else oracle.B_KN)
     for out in ("i32", "f32", "bf16"):
-        got = gpu_i8(A, B, "nk", out, tile, sa, sb, bias=bias)
-        assert_same(got, oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, out), f"{tile} {shape} {out}")
-
-
-def test_mfma_small_tile_rejects_b_kn(oracle, dev):
-    A, B, sa, sb, _ = inputs_i8(oracle, 64, 64, 128, 950, "kn")
-    for tile in SMALL_TILES:
-        with pytest.raises(_lib.FkeError):
-            gpu_i8(A, B, "kn", "f32", tile, sa, sb)
+        got = gpu_i8(A, B, layout, out, tile, sa, sb, bias=bias)
+        assert_same(got, oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, out), f"{tile} {layout} {(M, N, K)} {out}")
 
 
 @pytest.mark.parametrize("M,N,K,out,want", [
@@ -662,10 +656,10 @@ def test_mfma_small_tile_rejects_b_kn(oracle, dev):
     (2048, 1376, 4096, "f32", _lib.PATH_MFMA_128x128_RING4),  # 176 tiles
 ])
 def test_mfma_few_tile_shapes_full(oracle, dev, M, N, K, out, want):
-    """Shapes the dispatcher gives a 128x128 tile (fewer 256x256 tiles than
+    """Shapes the dispatcher gives a smaller tile (fewer 256x256 tiles than
     CUs): the tile it picks on this GPU, every output against the oracle, and
-    the same outputs from every pinned tile (and the streamed decode kernel
-    where it takes the shape)."""
+    the same outputs from every pinned tile with B in either layout (and from
+    the streamed decode kernel where it takes the shape)."""
     L = _lib.lib()
     pick = L.fke_select_mfma_tile(M, N, K, 0, 0, 0)
     say("few-tile shape", M, N, K, out, "tile path", pick)
@@ -678,6 +672,10 @@ def test_mfma_few_tile_shapes_full(oracle, dev, M, N, K, out, want):
     assert_same(got, ref, f"auto {M}x{N}x{K}")
     for tile in ["mfma_256x256"] + SMALL_TILES:
         assert_same(gpu_i8(A, B, "nk", out, tile, sa, sb, bias=bias), ref, f"{tile} {M}x{N}x{K}")
+    Bkn = np.ascontiguousarray(B.T)
+    assert L.fke_select_mfma_tile(M, N, K, 1, 0, 256) == want  # the same rule for B [K,N]
+    for tile in ["auto", "mfma_256x256"] + SMALL_TILES:
+        assert_same(gpu_i8(A, Bkn, "kn", out, tile, sa, sb, bias=bias), ref, f"B [K,N] {tile} {M}x{N}x{K}")
     if M <= 512:  # the streamed decode kernel gives the same bits
         assert_same(gpu_i8(A, B, "nk", out, "gemv", sa, sb, bias=bias), ref, f"gemv {M}x{N}x{K}")
 
@@ -751,9 +749,9 @@ def test_fp8_generic_bit_exact(oracle, dev, layout, shape):
 @pytest.mark.parametrize("out", ["f32", "bf16"])
 @pytest.mark.parametrize("nan_codes", [False, True])
 def test_fp8_mfma_tolerance(oracle, dev, layout, out, nan_codes):
-    """Every tile (B [N,K]; B [K,N] has the 256x256 one) within the FP8 bounds,
-    and the smaller tiles equal to the 256x256 tile bit for bit: each output
-    is summed over K in the same order whatever the tile."""
+    """The 256x256 tile within the FP8 bounds, and every smaller tile equal to
+    it bit for bit, both B layouts: each output is summed over K in the same
+    order whatever the tile."""
     M, N, K = 300, 528, 1024
     say("fp8 mfma", layout, out, nan_codes)
     A, B, sa, sb = f8_inputs(oracle, M, N, K, 700, layout, with_nan_codes=nan_codes)
@@ -763,9 +761,8 @@ def test_fp8_mfma_tolerance(oracle, dev, layout, out, nan_codes):
     big = gpu_f8(A, B, sa, sb, layout, out, "mfma_256x256", bias=bias)
     got = oracle.bf16_to_f32(big) if out == "bf16" else big
     assert_fp8_close(got, ref, out, f"mfma 256x256 {layout} nan={nan_codes}")
-    if layout == "nk":
-        for tile in SMALL_TILES:
-            assert_same(gpu_f8(A, B, sa, sb, layout, out, tile, bias=bias), big, f"fp8 {tile} vs 256x256")
+    for tile in SMALL_TILES:
+        assert_same(gpu_f8(A, B, sa, sb, layout, out, tile, bias=bias), big, f"fp8 {tile} {layout} vs 256x256")
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 300, 4096), (3, 1000, 2048), (16, 777, 5056), (16, 4096, 14336),
