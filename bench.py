@@ -48,12 +48,16 @@ TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic.json")
 TILE_LABELS = {5: "256x256", 6: "128x128", 7: "128x128_ring4", 8: "128x64_ring4", 9: "64x64_ring4"}
 
 
-def gemv_kernel(L, _lib, M, N=14336, K=4096):
-    """Kernel the dispatcher picks for an M-row INT8 batch on B [N,K] (K % 4096 == 0): the decode
-    family's, or the MFMA GEMM's with its tile."""
-    path = L.fke_select_path_i8(4096, 4096, 4096, M, N, K, _lib.OUT_BF16, _lib.B_NK)
+def gemv_kernel(L, _lib, M, N=14336, K=4096, layout="nk"):
+    """Kernel the dispatcher picks for an M-row INT8 batch (K % 4096 == 0, B [N,K] or [K,N]): the
+    decode family's, or the MFMA GEMM's with its tile."""
+    code = _lib.B_NK if layout == "nk" else _lib.B_KN
+    path = L.fke_select_path_i8(4096, 4096, 4096, M, N, K, _lib.OUT_BF16, code)
     if path == _lib.PATH_MFMA:
-        return f"gemm_mfma_kernel<i8,NK,bf16,{TILE_LABELS[L.fke_select_mfma_tile(M, N, K, _lib.B_NK, 0, 0)]}>"
+        tile = TILE_LABELS[L.fke_select_mfma_tile(M, N, K, code, 0, 0)]
+        return f"gemm_mfma_kernel<i8,{layout.upper()},bf16,{tile}>"
+    if layout == "kn":
+        return "gemv_kn_split_kernel<i8>+kn_reduce_kernel<i8,bf16>"
     return "gemv_rows_kernel" if M <= 2 else "gemv_lds_kernel"
 
 
@@ -518,7 +522,7 @@ def gemv_bench(torch, L, _lib, dev, gen, M, nbuf, launches, N=14336, K=4096, lay
     eager = eager_us(torch, dev, launch, launches)
     nbytes = gemv_bytes(M, N, K)
     gbs = nbytes / (us * 1e-6) / 1e9
-    kernel = gemv_kernel(L, _lib, M, N, K) if layout == "nk" else "gemv_kn_split_kernel<i8>+kn_reduce_kernel<i8,bf16>"
+    kernel = gemv_kernel(L, _lib, M, N, K, layout)
     return {"metric": f"HBM GB/s, decode GEMV M={M} N={N} K={K}, B {'[N,K]' if layout == 'nk' else '[K,N]'} "
                       f"(bf16 out, fused bias)",
             "value": round(gbs, 1), "unit": "GB/s", "us_per_launch": round(us, 3),
@@ -631,11 +635,16 @@ def tile_sweep(torch, L, _lib, dev, gen, timed, args):
 
 
 def batch_configs(torch, L, _lib, dev, gen, args):
-    """Batched decode on the decode weights (N = 14336, K = 4096): 32, 64, 128 and 256 rows. The
-    dispatcher gives 32 and 64 to the LDS-streamed kernel (2 / 4 activation blocks) and 128 and 256
-    to the MFMA GEMM's 4-stage 128x128 ring (one tile per CU); each line names its kernel."""
-    return {f"gemv_M{m}": gemv_bench(torch, L, _lib, dev, gen, m, args.gemv_buffers, args.gemv_launches)
-            for m in (32, 64, 128, 256)}
+    """Batched decode on the decode weights (N = 14336, K = 4096): 32, 64, 128 and 256 rows with B [N,K],
+    64 and 128 rows with B [K,N] (the reference's layout). The dispatcher gives 32 rows to the LDS-streamed
+    kernel and the larger batches to the MFMA GEMM's ring tiles (one tile per CU); each line names its
+    kernel."""
+    res = {f"gemv_M{m}": gemv_bench(torch, L, _lib, dev, gen, m, args.gemv_buffers, args.gemv_launches)
+           for m in (32, 64, 128, 256)}
+    for m in (64, 128):
+        res[f"gemv_M{m}_b_kn"] = gemv_bench(torch, L, _lib, dev, gen, m, args.gemv_buffers, args.gemv_launches,
+                                            layout="kn")
+    return res
 
 
 def extra_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):

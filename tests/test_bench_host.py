@@ -23,8 +23,11 @@ def test_tile_labels_cover_every_pinned_tile_path():
 
 
 @pytest.mark.parametrize("N,K", [(14336, 4096), (4096, 4096), (1792, 4096), (14336, 14336)])
-def test_batch_kernel_label_for_every_m(N, K):
+@pytest.mark.parametrize("layout", ["nk", "kn"])
+def test_batch_kernel_label_for_every_m(N, K, layout):
     L = _lib.lib()
     for M in range(1, 513):
-        label = bench.gemv_kernel(L, _lib, M, N, K)
-        assert label.startswith(("gemv_rows_kernel", "gemv_lds_kernel", "gemm_mfma_kernel<i8,NK,bf16,"))
+        label = bench.gemv_kernel(L, _lib, M, N, K, layout)
+        assert label.startswith(("gemv_rows_kernel", "gemv_lds_kernel", "gemv_kn_split_kernel",
+                                 f"gemm_mfma_kernel<i8,{layout.upper()},bf16,"))
+        assert (label.startswith("gemv_kn") or label.startswith("gemm_mfma")) if layout == "kn" else True
