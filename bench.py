@@ -498,10 +498,11 @@ def decode_family_configs(torch, L, _lib, dev, gen, args, N=14336, K=4096):
     return res
 
 
-def gemv_bench(torch, L, _lib, dev, gen, M, nbuf, launches, N=14336, K=4096, layout="nk"):
+def gemv_bench(torch, L, _lib, dev, gen, M, nbuf, launches, N=14336, K=4096, layout="nk", path=None):
     """Launch-averaged duration of the decode GEMV from a HIP graph of `launches`
     calls cycling over `nbuf` distinct weight buffers (>= 448 MiB in total);
-    B stored [N,K] ("nk") or [K,N] ("kn", the reference's Python-op layout)."""
+    B stored [N,K] ("nk") or [K,N] ("kn", the reference's Python-op layout);
+    `path` pins a kernel family (FKE_PATH_*) instead of the dispatcher's choice."""
     A = torch.clamp(torch.round(torch.randn((M, K), device=dev, generator=gen) * 30), -127, 127).to(torch.int8)
     shape = (N, K) if layout == "nk" else (K, N)
     code = _lib.B_NK if layout == "nk" else _lib.B_KN
@@ -512,9 +513,14 @@ def gemv_bench(torch, L, _lib, dev, gen, M, nbuf, launches, N=14336, K=4096, lay
     out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
 
     def launch(i, sh):
-        st = L.fke_qgemm_i8(A.data_ptr(), Bs[i % nbuf].data_ptr(), out.data_ptr(), M, N, K,
-                            sa.data_ptr(), sb.data_ptr(), 1.0, 1.0, bias.data_ptr(), _lib.OUT_BF16,
-                            code, sh)
+        if path is None:
+            st = L.fke_qgemm_i8(A.data_ptr(), Bs[i % nbuf].data_ptr(), out.data_ptr(), M, N, K,
+                                sa.data_ptr(), sb.data_ptr(), 1.0, 1.0, bias.data_ptr(), _lib.OUT_BF16,
+                                code, sh)
+        else:
+            st = L.fke_qgemm_i8_on_path(path, A.data_ptr(), Bs[i % nbuf].data_ptr(), out.data_ptr(), M, N, K,
+                                        sa.data_ptr(), sb.data_ptr(), 1.0, 1.0, bias.data_ptr(), _lib.OUT_BF16,
+                                        code, sh)
         if st:
             raise RuntimeError(f"gemv failed: {_lib.status_string(st)}")
 
@@ -523,6 +529,8 @@ def gemv_bench(torch, L, _lib, dev, gen, M, nbuf, launches, N=14336, K=4096, lay
     nbytes = gemv_bytes(M, N, K)
     gbs = nbytes / (us * 1e-6) / 1e9
     kernel = gemv_kernel(L, _lib, M, N, K, layout)
+    if path == _lib.PATH_GEMV and layout == "nk":
+        kernel = "gemv_rows_kernel" if M <= 2 else "gemv_lds_kernel"
     return {"metric": f"HBM GB/s, decode GEMV M={M} N={N} K={K}, B {'[N,K]' if layout == 'nk' else '[K,N]'} "
                       f"(bf16 out, fused bias)",
             "value": round(gbs, 1), "unit": "GB/s", "us_per_launch": round(us, 3),
@@ -636,14 +644,17 @@ def tile_sweep(torch, L, _lib, dev, gen, timed, args):
 
 def batch_configs(torch, L, _lib, dev, gen, args):
     """Batched decode on the decode weights (N = 14336, K = 4096): 32, 64, 128 and 256 rows with B [N,K],
-    64 and 128 rows with B [K,N] (the reference's layout). The dispatcher gives 32 rows to the LDS-streamed
-    kernel and the larger batches to the MFMA GEMM's ring tiles (one tile per CU); each line names its
-    kernel."""
+    64 and 128 rows with B [K,N] (the reference's layout), and 64 and 128 rows on the LDS-streamed kernel
+    pinned. The dispatcher gives 32 rows to the streamed kernel and the larger batches to the MFMA GEMM's
+    ring tiles (one tile per CU); each line names its kernel."""
     res = {f"gemv_M{m}": gemv_bench(torch, L, _lib, dev, gen, m, args.gemv_buffers, args.gemv_launches)
            for m in (32, 64, 128, 256)}
     for m in (64, 128):
         res[f"gemv_M{m}_b_kn"] = gemv_bench(torch, L, _lib, dev, gen, m, args.gemv_buffers, args.gemv_launches,
                                             layout="kn")
+    for m in (64, 128):  # the streamed decode kernel pinned, for the choice between it and the ring tiles
+        res[f"gemv_M{m}_streamed"] = gemv_bench(torch, L, _lib, dev, gen, m, args.gemv_buffers, args.gemv_launches,
+                                                path=_lib.PATH_GEMV)
     return res
 
 
