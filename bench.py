@@ -565,7 +565,7 @@ def shard_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
         C = torch.empty((M, N), dtype=tdt, device=dev)
         ms = timed(lambda: L.fke_qgemm_i8(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, sa.data_ptr(),
                                           sb.data_ptr(), 1.0, 1.0, None, out, _lib.B_NK, sh),
-                   args.steps, args.warmup)
+                   args.steps, args.warmup, args.preheat_ms)
         t = 2.0 * M * N * K / (ms * 1e-3) / 1e12
         tile = L.fke_select_mfma_tile(M, N, K, _lib.B_NK, 0, 0)
         res[name] = {"ms": round(ms, 4), "TOPS": round(t, 1), "frac": round(t / PEAK_INT8_TOPS, 4),
@@ -573,7 +573,7 @@ def shard_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
         if tile != _lib.PATH_MFMA_256x256:  # the 256x256 tile on the same shape, for comparison
             ms2 = timed(lambda: L.fke_qgemm_i8_on_path(_lib.PATH_MFMA_256x256, A.data_ptr(), B.data_ptr(),
                                                        C.data_ptr(), M, N, K, sa.data_ptr(), sb.data_ptr(), 1.0,
-                                                       1.0, None, out, _lib.B_NK, sh), args.steps, args.warmup)
+                                                       1.0, None, out, _lib.B_NK, sh), args.steps, args.warmup, args.preheat_ms)
             res[name]["ms_256x256_tile"] = round(ms2, 4)
         del A, B, C
     return res
@@ -667,7 +667,7 @@ def extra_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
     sh = torch.cuda.current_stream(dev).cuda_stream
     ms = timed(lambda: L.fke_qgemm_i8(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, sa.data_ptr(),
                                       sb.data_ptr(), 1.0, 1.0, None, _lib.OUT_BF16, _lib.B_NK, sh),
-               args.steps, args.warmup)
+               args.steps, args.warmup, args.preheat_ms)
     t = 2.0 * M * N * K / (ms * 1e-3) / 1e12
     res["prefill_4096x11008x4096_bf16"] = {"ms": round(ms, 4), "TOPS": round(t, 1),
                                            "frac": round(t / PEAK_INT8_TOPS, 4)}
@@ -678,7 +678,7 @@ def extra_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
     C = torch.empty((M, N), dtype=torch.float32, device=dev)
     ms = timed(lambda: L.fke_qgemm_i8(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, sa.data_ptr(),
                                       sb.data_ptr(), 1.0, 1.0, None, _lib.OUT_F32, _lib.B_KN, sh),
-               args.steps, args.warmup)
+               args.steps, args.warmup, args.preheat_ms)
     t = 2.0 * M * N * K / (ms * 1e-3) / 1e12
     res["int8_8192cubed_f32_Bkn"] = {"ms": round(ms, 4), "TOPS": round(t, 1), "frac": round(t / PEAK_INT8_TOPS, 4)}
     del A, B, C
@@ -692,7 +692,7 @@ def extra_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
     A8.view(-1)[::97] = 0x7F
     C = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
     ms = timed(lambda: L.fke_qgemm_f8(A8.data_ptr(), B8.data_ptr(), C.data_ptr(), M, N, K, 0.01, 0.01,
-                                      None, _lib.OUT_BF16, _lib.B_NK, sh), args.steps, args.warmup)
+                                      None, _lib.OUT_BF16, _lib.B_NK, sh), args.steps, args.warmup, args.preheat_ms)
     t = 2.0 * M * N * K / (ms * 1e-3) / 1e12
     res["fp8_8192cubed_bf16_Bnk_nan_codes"] = {"ms": round(ms, 4), "TFLOPS": round(t, 1),
                                                "frac": round(t / PEAK_FP8_TFLOPS, 4)}
@@ -743,7 +743,7 @@ def data_sweep(torch, L, _lib, dev, gen, timed, args):
             A = torch.randint(-r, r + 1, (M, K), dtype=torch.int8, device=dev, generator=gen)
             B = torch.randint(-r, r + 1, (N, K), dtype=torch.int8, device=dev, generator=gen)
         ms = timed(lambda: L.fke_qgemm_i8(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, None, None, 1.0, 1.0,
-                                          None, _lib.OUT_F32, _lib.B_NK, sh), args.steps, args.warmup)
+                                          None, _lib.OUT_F32, _lib.B_NK, sh), args.steps, args.warmup, args.preheat_ms)
         res[name] = {"ms": round(ms, 4), "TOPS": round(2.0 * M * N * K / ms / 1e9, 1)}
         del A, B
     return res
@@ -761,7 +761,7 @@ def fp8_configs(torch, L, _lib, dev, gen, timed, args):
     C = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
     for name, lay in (("kn", _lib.B_KN), ("nk", _lib.B_NK)):
         ms = timed(lambda: L.fke_qgemm_f8(A8.data_ptr(), B8.data_ptr(), C.data_ptr(), M, N, K, 0.01, 0.01,
-                                          None, _lib.OUT_BF16, lay, sh), args.steps, args.warmup)
+                                          None, _lib.OUT_BF16, lay, sh), args.steps, args.warmup, args.preheat_ms)
         t = 2.0 * M * N * K / (ms * 1e-3) / 1e12
         res[f"fp8_8192cubed_bf16_B{name}"] = {"ms": round(ms, 4), "TFLOPS": round(t, 1),
                                               "frac": round(t / PEAK_FP8_TFLOPS, 4)}
@@ -806,7 +806,7 @@ def vendor_configs(torch, dev, gen, timed, args):
     M = N = K = 8192
     A = torch.randint(-127, 128, (M, K), dtype=torch.int8, device=dev, generator=gen)
     B = torch.randint(-127, 128, (N, K), dtype=torch.int8, device=dev, generator=gen)
-    ms = timed(lambda: torch._int_mm(A, B.t()), args.steps, args.warmup)
+    ms = timed(lambda: torch._int_mm(A, B.t()), args.steps, args.warmup, args.preheat_ms)
     res["int8_8192cubed_i32out_torch_int_mm"] = {"ms": round(ms, 4), "TOPS": round(2.0 * M * N * K / ms / 1e9, 1)}
     del A, B
     try:
@@ -814,7 +814,7 @@ def vendor_configs(torch, dev, gen, timed, args):
         b8 = torch.randn((N, K), device=dev, generator=gen).to(torch.float8_e4m3fn)
         one = torch.tensor(1.0, device=dev)
         ms = timed(lambda: torch._scaled_mm(a8, b8.t(), scale_a=one, scale_b=one, out_dtype=torch.bfloat16),
-                   args.steps, args.warmup)
+                   args.steps, args.warmup, args.preheat_ms)
         res["fp8_8192cubed_bf16out_torch_scaled_mm"] = {"ms": round(ms, 4),
                                                        "TFLOPS": round(2.0 * M * N * K / ms / 1e9, 1)}
         del a8, b8
@@ -823,7 +823,7 @@ def vendor_configs(torch, dev, gen, timed, args):
     for name, dt in (("bf16", torch.bfloat16), ("f16", torch.float16)):
         Ah = torch.randn((M, K), device=dev, generator=gen).to(dt)
         Bh = torch.randn((N, K), device=dev, generator=gen).to(dt)
-        ms = timed(lambda: Ah @ Bh.t(), args.steps, args.warmup)
+        ms = timed(lambda: Ah @ Bh.t(), args.steps, args.warmup, args.preheat_ms)
         res[f"{name}_8192cubed_torch_matmul"] = {"ms": round(ms, 4), "TFLOPS": round(2.0 * M * N * K / ms / 1e9, 1)}
         del Ah, Bh
     return res
@@ -839,7 +839,7 @@ def half_configs(torch, L, _lib, dev, gen, timed, args):
         Bh = torch.randn((N, K), device=dev, generator=gen).to(dt)
         C = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
         ms = timed(lambda: L.fke_gemm_half(Ah.data_ptr(), Bh.data_ptr(), C.data_ptr(), M, N, K, code, None, None,
-                                           1.0, 1.0, None, _lib.OUT_BF16, _lib.B_NK, sh), args.steps, args.warmup)
+                                           1.0, 1.0, None, _lib.OUT_BF16, _lib.B_NK, sh), args.steps, args.warmup, args.preheat_ms)
         t = 2.0 * M * N * K / (ms * 1e-3) / 1e12
         res[f"{name}_gemm_8192cubed_bf16out"] = {"ms": round(ms, 4), "TFLOPS": round(t, 1),
                                                  "frac": round(t / PEAK_BF16_TFLOPS, 4),
@@ -862,7 +862,7 @@ def swiglu_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
     U = torch.empty((M, I), dtype=torch.bfloat16, device=dev)
     ms = timed(lambda: L.fke_qgemm_i8_swiglu(A.data_ptr(), W.data_ptr(), H.data_ptr(), M, I, K, sa.data_ptr(),
                                              sb.data_ptr(), 1.0, 1.0, None, _lib.OUT_BF16, sh),
-               args.steps, args.warmup)
+               args.steps, args.warmup, args.preheat_ms)
     Wu = W[I:]
     sbu = sb[I:]
 
@@ -873,7 +873,7 @@ def swiglu_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
                        1.0, None, _lib.OUT_BF16, _lib.B_NK, sh)
         L.fke_swiglu(G.data_ptr(), U.data_ptr(), H.data_ptr(), M * I, _lib.IN_BF16, sh)
 
-    ms_u = timed(unfused, args.steps, args.warmup)
+    ms_u = timed(unfused, args.steps, args.warmup, args.preheat_ms)
     t = 2.0 * M * 2 * I * K / (ms * 1e-3) / 1e12
     res["swiglu_gate_up_4096x14336x4096_bf16"] = {
         "ms": round(ms, 4), "TOPS": round(t, 1), "frac": round(t / PEAK_INT8_TOPS, 4),

@@ -11,8 +11,9 @@
 // the panel into LDS as it lies and let the LDS transpose it:
 // ds_read_b64_tr_b8 gives each lane 8 consecutive k bytes of one column.
 // INT8 runs v_mfma_i32_16x16x64_i8 (two k steps per 128-row item); FP8
-// v_mfma_scale_f32_16x16x128_f8f6f4 (one step), its fragments cleared of the
-// 0x7F / 0xFF codes on the VALU (the MFMA reads them as NaN).
+// v_mfma_scale_f32_16x16x128_f8f6f4 (one step) on the raw codes, and a wave
+// whose sums came out NaN (a 0x7F / 0xFF code, NaN to the MFMA, 0.0 to the
+// reference) streams its pieces again with those codes cleared on the VALU.
 //
 // A CU streams strided row segments at a rate that grows with the segment
 // width, and the chip needs most CUs streaming, so the panel is cut along K
@@ -211,55 +212,85 @@ __global__ __launch_bounds__(256) void gemv_kn_split_kernel(GemmArgs p, KnSplit 
     }
 
     AccV acc[KS_CB];
+    // The stream on raw codes (SAN false), or with FP8's 0x7F / 0xFF codes
+    // cleared on the VALU (SAN true, FP8's replay).
+    auto stream = [&](auto sanc) __attribute__((always_inline)) {
+        constexpr bool SAN = decltype(sanc)::value;
+        (void)SAN;
 #pragma unroll
-    for (int cb = 0; cb < KS_CB; ++cb) acc[cb] = AccV{0, 0, 0, 0};
+        for (int cb = 0; cb < KS_CB; ++cb) acc[cb] = AccV{0, 0, 0, 0};
 
-    int issued = 0;
+        int issued = 0;
 #pragma unroll
-    for (int q = 0; q < KS_NS; ++q)
-        if (issued < np) {
-            issue(issued, lring + q * SLOT);
-            ++issued;
-        }
-    for (int c = 0; c < np; ++c) {
-        lds_u8* const slot = lring + (c % KS_NS) * SLOT;
-        ks_wait_items(issued - c - 1);
-        // Fragments to registers, then the slot is refilled before the MFMAs.
-        v4i af[2];
-        v2i tr[32];
-        af[0] = ks_rd128(slot + aadr[0]);
-        af[1] = ks_rd128(slot + aadr[1]);
-        ks_read_w<F8, 0>(slot, wadr, tr);
-        ks_lgkm_wait_all(af, tr);
-        v4i wf[16];  // INT8: [2 steps][8 blocks] of 16 k bytes; FP8: [8 blocks][2 halves] of 16 k bytes
+        for (int q = 0; q < KS_NS; ++q)
+            if (issued < np) {
+                issue(issued, lring + q * SLOT);
+                ++issued;
+            }
+        for (int c = 0; c < np; ++c) {
+            lds_u8* const slot = lring + (c % KS_NS) * SLOT;
+            ks_wait_items(issued - c - 1);
+            // Fragments to registers, then the slot is refilled before the MFMAs.
+            v4i af[2];
+            v2i tr[32];
+            af[0] = ks_rd128(slot + aadr[0]);
+            af[1] = ks_rd128(slot + aadr[1]);
+            ks_read_w<F8, 0>(slot, wadr, tr);
+            ks_lgkm_wait_all(af, tr);
+            v4i wf[16];  // INT8: [2 steps][8 blocks] of 16 k bytes; FP8: [8 blocks][2 halves] of 16 k bytes
 #pragma unroll
-        for (int x = 0; x < 16; ++x) wf[x] = v4i{tr[2 * x][0], tr[2 * x][1], tr[2 * x + 1][0], tr[2 * x + 1][1]};
-        if (issued < np) {
-            issue(issued, slot);
-            ++issued;
-        }
-        if constexpr (F8) {
+            for (int x = 0; x < 16; ++x) wf[x] = v4i{tr[2 * x][0], tr[2 * x][1], tr[2 * x + 1][0], tr[2 * x + 1][1]};
+            if (issued < np) {
+                issue(issued, slot);
+                ++issued;
+            }
+            if constexpr (F8) {
+                if constexpr (SAN) {
 #pragma unroll
-            for (int h = 0; h < 2; ++h)
+                    for (int h = 0; h < 2; ++h)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) af[h][e] = static_cast<int>(e4m3_sanitize(static_cast<uint32_t>(af[h][e])));
+                        for (int e = 0; e < 4; ++e)
+                            af[h][e] = static_cast<int>(e4m3_sanitize(static_cast<uint32_t>(af[h][e])));
 #pragma unroll
-            for (int x = 0; x < 16; ++x)
+                    for (int x = 0; x < 16; ++x)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) wf[x][e] = static_cast<int>(e4m3_sanitize(static_cast<uint32_t>(wf[x][e])));
-            const v8i a8 = __builtin_shufflevector(af[0], af[1], 0, 1, 2, 3, 4, 5, 6, 7);
-#pragma unroll
-            for (int cb = 0; cb < KS_CB; ++cb)
-                acc[cb] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                    a8, __builtin_shufflevector(wf[2 * cb], wf[2 * cb + 1], 0, 1, 2, 3, 4, 5, 6, 7), acc[cb], 0, 0,
-                    0, 0, 0, 0);
-        } else {
-#pragma unroll
-            for (int s = 0; s < 2; ++s)
+                        for (int e = 0; e < 4; ++e)
+                            wf[x][e] = static_cast<int>(e4m3_sanitize(static_cast<uint32_t>(wf[x][e])));
+                }
+                const v8i a8 = __builtin_shufflevector(af[0], af[1], 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
                 for (int cb = 0; cb < KS_CB; ++cb)
-                    acc[cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[s], wf[8 * s + cb], acc[cb], 0, 0, 0);
+                    acc[cb] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                        a8, __builtin_shufflevector(wf[2 * cb], wf[2 * cb + 1], 0, 1, 2, 3, 4, 5, 6, 7), acc[cb], 0, 0,
+                        0, 0, 0, 0);
+            } else {
+#pragma unroll
+                for (int s = 0; s < 2; ++s)
+#pragma unroll
+                    for (int cb = 0; cb < KS_CB; ++cb)
+                        acc[cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[s], wf[8 * s + cb], acc[cb], 0, 0, 0);
+            }
         }
+    };
+    if constexpr (!F8) {
+        stream(std::false_type{});
+    } else {
+        // E4M3 0x7F / 0xFF are NaN to the MFMA but 0.0 to the reference.
+        // Real quantizers never emit them (they saturate at 448), and
+        // clearing every fragment costs VALU work the stream cannot hide, so
+        // the wave streams the raw codes first: every product of finite codes
+        // is finite and no sum of them overflows, so a NaN sum proves a NaN
+        // code in this wave's rows or columns, and only then does the wave
+        // stream its pieces again with the codes cleared.  Its ring slots are
+        // free (the stream ends with every copy landed) and the other waves
+        // are not waited for, so the replay is the wave's own.
+        stream(std::false_type{});
+        bool bad = false;
+#pragma unroll
+        for (int cb = 0; cb < KS_CB; ++cb)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) bad |= __builtin_isnan(acc[cb][v]);
+        if (__builtin_amdgcn_ballot_w64(bad) != 0) stream(std::true_type{});
     }
 
     // Lane l of block cb holds column 16cb + l%16, rows 4(l/16) + v.
@@ -531,68 +562,98 @@ __global__ __launch_bounds__(256) void gemv_kn_full_kernel(GemmArgs p) {
     }
 
     AccV acc[4];
+    // The stream on raw codes (SAN false), or with FP8's 0x7F / 0xFF codes
+    // cleared on the VALU (SAN true, FP8's replay).
+    auto stream = [&](auto sanc) __attribute__((always_inline)) {
+        constexpr bool SAN = decltype(sanc)::value;
+        (void)SAN;
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb) acc[cb] = AccV{0, 0, 0, 0};
+        for (int cb = 0; cb < 4; ++cb) acc[cb] = AccV{0, 0, 0, 0};
 
-    int issued = 0;
+        int issued = 0;
 #pragma unroll
-    for (int q = 0; q < KF_NS; ++q)
-        if (issued < np) {
-            issue(issued, lring + q * SLOT);
-            ++issued;
-        }
-    for (int c = 0; c < np; ++c) {
-        lds_u8* const slot = lring + (c % KF_NS) * SLOT;
-        kf_wait_items(issued - c - 1);
-        // Fragments to registers, then the slot is refilled before the MFMAs.
-        // 18 reads: at most 12 in flight (lgkmcnt's field is 4 bits).
-        v4i af[2];
-        v2i tr[16];  // INT8: [2 steps][4 blocks][2 eighths]; FP8: [4 blocks][4 eighths]
-        af[0] = kf_rd128(slot + aadr[0]);
-        af[1] = kf_rd128(slot + aadr[1]);
-#pragma unroll
-        for (int x = 0; x < 16; ++x) {
-            uint32_t a;
-            if constexpr (F8) {
-                const int cb = x >> 2, t = x & 3;  // eighth t of block cb: rows 32G + 8t ..
-                a = (t >= 2 ? wadr[cb ^ 3] : wadr[cb]) + (8 * t) * KF_W;
-            } else {
-                const int s = x >> 3, cb = (x >> 1) & 3, t = x & 1;  // rows 64s + 16G + 8t ..
-                a = wadr[cb] + (64 * s + 8 * t) * KF_W;
+        for (int q = 0; q < KF_NS; ++q)
+            if (issued < np) {
+                issue(issued, lring + q * SLOT);
+                ++issued;
             }
-            if (x + 2 >= 12) asm volatile("s_waitcnt lgkmcnt(11)" ::: "memory");
-            tr[x] = kf_rdtr(slot + a);
-        }
-        kf_lgkm_wait_all(af, tr);
-        v4i wf[8];  // INT8: [2 steps][4 blocks] of 16 k bytes; FP8: [4 blocks][2 halves] of 16 k bytes
+        for (int c = 0; c < np; ++c) {
+            lds_u8* const slot = lring + (c % KF_NS) * SLOT;
+            kf_wait_items(issued - c - 1);
+            // Fragments to registers, then the slot is refilled before the MFMAs.
+            // 18 reads: at most 12 in flight (lgkmcnt's field is 4 bits).
+            v4i af[2];
+            v2i tr[16];  // INT8: [2 steps][4 blocks][2 eighths]; FP8: [4 blocks][4 eighths]
+            af[0] = kf_rd128(slot + aadr[0]);
+            af[1] = kf_rd128(slot + aadr[1]);
 #pragma unroll
-        for (int x = 0; x < 8; ++x) wf[x] = v4i{tr[2 * x][0], tr[2 * x][1], tr[2 * x + 1][0], tr[2 * x + 1][1]};
-        if (issued < np) {
-            issue(issued, slot);
-            ++issued;
-        }
-        if constexpr (F8) {
+            for (int x = 0; x < 16; ++x) {
+                uint32_t a;
+                if constexpr (F8) {
+                    const int cb = x >> 2, t = x & 3;  // eighth t of block cb: rows 32G + 8t ..
+                    a = (t >= 2 ? wadr[cb ^ 3] : wadr[cb]) + (8 * t) * KF_W;
+                } else {
+                    const int s = x >> 3, cb = (x >> 1) & 3, t = x & 1;  // rows 64s + 16G + 8t ..
+                    a = wadr[cb] + (64 * s + 8 * t) * KF_W;
+                }
+                if (x + 2 >= 12) asm volatile("s_waitcnt lgkmcnt(11)" ::: "memory");
+                tr[x] = kf_rdtr(slot + a);
+            }
+            kf_lgkm_wait_all(af, tr);
+            v4i wf[8];  // INT8: [2 steps][4 blocks] of 16 k bytes; FP8: [4 blocks][2 halves] of 16 k bytes
 #pragma unroll
-            for (int h = 0; h < 2; ++h)
+            for (int x = 0; x < 8; ++x) wf[x] = v4i{tr[2 * x][0], tr[2 * x][1], tr[2 * x + 1][0], tr[2 * x + 1][1]};
+            if (issued < np) {
+                issue(issued, slot);
+                ++issued;
+            }
+            if constexpr (F8) {
+                if constexpr (SAN) {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) af[h][e] = static_cast<int>(e4m3_sanitize(static_cast<uint32_t>(af[h][e])));
+                    for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int x = 0; x < 8; ++x)
+                        for (int e = 0; e < 4; ++e)
+                            af[h][e] = static_cast<int>(e4m3_sanitize(static_cast<uint32_t>(af[h][e])));
 #pragma unroll
-                for (int e = 0; e < 4; ++e) wf[x][e] = static_cast<int>(e4m3_sanitize(static_cast<uint32_t>(wf[x][e])));
-            const v8i a8 = __builtin_shufflevector(af[0], af[1], 0, 1, 2, 3, 4, 5, 6, 7);
+                    for (int x = 0; x < 8; ++x)
 #pragma unroll
-            for (int cb = 0; cb < 4; ++cb)
-                acc[cb] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                    a8, __builtin_shufflevector(wf[2 * cb], wf[2 * cb + 1], 0, 1, 2, 3, 4, 5, 6, 7), acc[cb], 0, 0,
-                    0, 0, 0, 0);
-        } else {
-#pragma unroll
-            for (int s = 0; s < 2; ++s)
+                        for (int e = 0; e < 4; ++e)
+                            wf[x][e] = static_cast<int>(e4m3_sanitize(static_cast<uint32_t>(wf[x][e])));
+                }
+                const v8i a8 = __builtin_shufflevector(af[0], af[1], 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
                 for (int cb = 0; cb < 4; ++cb)
-                    acc[cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[s], wf[4 * s + cb], acc[cb], 0, 0, 0);
+                    acc[cb] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                        a8, __builtin_shufflevector(wf[2 * cb], wf[2 * cb + 1], 0, 1, 2, 3, 4, 5, 6, 7), acc[cb], 0, 0,
+                        0, 0, 0, 0);
+            } else {
+#pragma unroll
+                for (int s = 0; s < 2; ++s)
+#pragma unroll
+                    for (int cb = 0; cb < 4; ++cb)
+                        acc[cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[s], wf[4 * s + cb], acc[cb], 0, 0, 0);
+            }
         }
+    };
+    if constexpr (!F8) {
+        stream(std::false_type{});
+    } else {
+        // E4M3 0x7F / 0xFF are NaN to the MFMA but 0.0 to the reference.
+        // Real quantizers never emit them (they saturate at 448), and
+        // clearing every fragment costs VALU work the stream cannot hide, so
+        // the wave streams the raw codes first: every product of finite codes
+        // is finite and no sum of them overflows, so a NaN sum proves a NaN
+        // code in this wave's rows or columns, and only then does the wave
+        // stream its pieces again with the codes cleared.  Its ring slots are
+        // free (the stream ends with every copy landed) and the other waves
+        // are not waited for, so the replay is the wave's own.
+        stream(std::false_type{});
+        bool bad = false;
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) bad |= __builtin_isnan(acc[cb][v]);
+        if (__builtin_amdgcn_ballot_w64(bad) != 0) stream(std::true_type{});
     }
 
     // Cross-wave reduction through LDS (the ring is free: every wave has
