@@ -243,16 +243,4 @@ __device__ __forceinline__ void store_out(void* C, size_t idx, float y, int32_t 
     }
 }
 
-// store_out with non-temporal (streaming) stores.
-template <int OUT>
-__device__ __forceinline__ void store_out_nt(void* C, size_t idx, float y, int32_t acc) {
-    if constexpr (OUT == FKE_OUT_F32) {
-        __builtin_nontemporal_store(y, static_cast<float*>(C) + idx);
-    } else if constexpr (OUT == FKE_OUT_BF16) {
-        __builtin_nontemporal_store(f32_to_bf16_rne(y), static_cast<uint16_t*>(C) + idx);
-    } else {
-        __builtin_nontemporal_store(acc, static_cast<int32_t*>(C) + idx);
-    }
-}
-
 }  // namespace fke

@@ -133,7 +133,8 @@ struct Panel {
             const int seg = wave * PW + i;
             const int r = seg * 8 + (lane >> 3);
             const int lc = (lane & 7) ^ swz(r);
-            const int src = SWI ? swiglu_b_row<NJ>(r, row0, rows >> 1) : row0 + r;
+            int src = row0 + r;
+            if constexpr (SWI) src = swiglu_b_row<NJ>(r, row0, rows >> 1);  // (SwiGLU tiles have NJ >= 2)
             off[i] = static_cast<uint32_t>(min(src, rows - 1) * ld + lc * 16);
         }
     }
@@ -378,7 +379,9 @@ __global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p
     // epilogue operands -> LDS (visible after the prologue barrier)
     if (tid < BM) epi_sa[tid] = p.scale_a ? p.scale_a[min(m0 + tid, M - 1)] : p.sa;
     if (tid < TL::BN) {
-        const int n = min(SWI ? swiglu_b_row<NJ>(tid, n0, NO) : n0 + tid, N - 1);  // B row of tile column tid
+        int n = n0 + tid;  // B row of tile column tid
+        if constexpr (SWI) n = swiglu_b_row<NJ>(tid, n0, NO);
+        n = min(n, N - 1);
         epi_sb[tid] = p.scale_b ? p.scale_b[n] : p.sb;
         epi_bias[tid] = p.bias ? p.bias[n] : -0.0f;
     }
