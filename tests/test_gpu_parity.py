@@ -445,6 +445,70 @@ def test_gemv_kn_two_streams(oracle, dev):
             assert_same(host(o), refs[i], f"stream {i}")
 
 
+def test_host_threads_each_on_own_stream(oracle, dev):
+    """Four host threads call the library at once, each on a stream of its own
+    (the C ABI is stateless apart from the per-(device, stream) [K,N] decode
+    workspaces, created on a stream's first such call under a mutex, and
+    ctypes releases the GIL around each call): per thread, the [K,N] INT8
+    decode, the [N,K] MFMA GEMM and the [K,N] FP8 decode, twelve times over.
+    INT8 results bit-exact against the oracle; FP8 results bit-identical to
+    the same call made alone before the threads start (and that one within
+    the FP8 bar)."""
+    import threading
+
+    T, ITERS = 4, 12
+    cases = []
+    for t in range(T):
+        M, N, K = 1 + 5 * t, 4096, 2048  # M = 1, 6, 11, 16
+        A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 9700 + 10 * t, layout="kn", act="normal")
+        ref_kn = oracle_out(oracle, oracle.w8a8_acc(A, B, oracle.B_KN, nthreads=NTH), sa, sb, 1.0, 1.0, bias, "bf16")
+        M2, N2, K2 = 256 + 64 * t, 1024, 1024
+        A2, B2, sa2, sb2, bias2 = inputs_i8(oracle, M2, N2, K2, 9800 + 10 * t)
+        ref_nk = oracle_out(oracle, oracle.w8a8_acc(A2, B2, nthreads=NTH), sa2, sb2, 1.0, 1.0, bias2, "f32")
+        A3, B3, s3a, s3b = f8_inputs(oracle, M, N, K, 9900 + 10 * t, "kn")
+        ref_f8 = oracle.f8_gemm(A3, B3, s3a, s3b, b_layout=oracle.B_KN, nthreads=NTH)
+        cases.append(dict(kn=[dev_t(x) for x in (A, B, sa, sb, bias)], ref_kn=ref_kn,
+                          nk=[dev_t(x) for x in (A2, B2, sa2, sb2, bias2)], ref_nk=ref_nk,
+                          f8=(dev_t(A3), dev_t(B3), float(s3a), float(s3b)), ref_f8=ref_f8))
+    say("host threads", T, "x", ITERS, "iterations")
+    solo = []
+    for c in cases:  # FP8 references: the same calls, one at a time
+        A3, B3, s3a, s3b = c["f8"]
+        r = ops.fp8_gemm_scaled(A3, B3, s3a, s3b, out_dtype=torch.float32, b_layout="kn")
+        torch.cuda.synchronize()
+        assert_fp8_close(host(r), c["ref_f8"], "f32", "threads: solo fp8 kn")
+        solo.append(host(r))
+
+    errors = []
+    start = threading.Barrier(T)
+
+    def work(t):
+        try:
+            c = cases[t]
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                start.wait(timeout=60)
+                for i in range(ITERS):
+                    y1 = ops.w8a8_gemm(*c["kn"], out_dtype=torch.bfloat16, b_layout="kn")
+                    y2 = ops.w8a8_gemm(*c["nk"], out_dtype=torch.float32, b_layout="nk")
+                    A3, B3, s3a, s3b = c["f8"]
+                    y3 = ops.fp8_gemm_scaled(A3, B3, s3a, s3b, out_dtype=torch.float32, b_layout="kn")
+                    s.synchronize()
+                    assert_same(host(y1), c["ref_kn"], f"thread {t} iteration {i}: i8 kn")
+                    assert_same(host(y2), c["ref_nk"], f"thread {t} iteration {i}: i8 nk")
+                    assert_same(host(y3), solo[t], f"thread {t} iteration {i}: f8 kn against the solo call")
+        except BaseException as e:  # reported below, from the test's own thread
+            errors.append((t, repr(e)))
+
+    threads = [threading.Thread(target=work, args=(t,)) for t in range(T)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=120)
+    assert not any(th.is_alive() for th in threads), "a host thread did not finish"
+    assert not errors, errors
+
+
 @pytest.mark.parametrize("M", [1, 16])
 def test_gemv_kn_f8_split_deterministic(oracle, dev, M):
     """FP8 decode with B [K,N] at the C2 shape on the K-split kernels and on
