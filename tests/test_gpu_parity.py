@@ -863,6 +863,57 @@ def test_fp8_streamed_isolated_nan_codes(oracle, dev, M):
     assert_fp8_close(got, ref, "f32", f"streamed isolated NaN codes M={M}")
 
 
+# Extreme operands on every family, both layouts.  INT8: -128 (the generators
+# never emit it), +-127, at K = 8192, where |acc| reaches 8192 * 128^2 =
+# 1.34e8; compared as int32.  FP8: codes 0x7E / 0xFE only (+-448, the largest
+# finite E4M3): every product is +-49 * 2^12 and every partial sum over
+# K = 8192 an integer multiple of 2^12 below 2^24 * 2^12, so each is exact in
+# fp32 in any order and the MFMA and streamed families must match the
+# reference's sequential sum bit for bit.
+EXTREME_CASES = (
+    [(1, 4096, 8192, "nk", "gemv"), (2, 4096, 8192, "nk", "gemv"), (16, 4096, 8192, "nk", "gemv"),
+     (16, 4096, 8192, "nk", "gemv_dot"), (40, 4096, 8192, "nk", "gemv"), (100, 4096, 8192, "nk", "gemv"),
+     (1, 4096, 8192, "kn", "gemv"), (16, 4096, 8192, "kn", "gemv"),
+     (37, 50, 8192, "nk", "generic"), (37, 48, 8192, "kn", "generic")]
+    + [(300, 528, 8192, lay, "mfma_" + t) for lay in ("nk", "kn")
+       for t in ("256x256", "128x128", "128x128_ring4", "128x64_ring4", "64x64_ring4")])
+
+
+def extreme_i8(M, N, K, layout, seed):
+    r = np.random.default_rng(seed)
+    A = np.where(r.random((M, K)) < 0.5, -128, 127).astype(np.int8)
+    A[0] = -128  # one row of -128 only
+    Bnk = np.where(r.random((N, K)) < 0.5, -128, -127).astype(np.int8)
+    Bnk[1] = 127
+    return A, (Bnk if layout == "nk" else np.ascontiguousarray(Bnk.T))
+
+
+@pytest.mark.parametrize("M,N,K,layout,path", EXTREME_CASES)
+def test_extreme_int8_operands(oracle, dev, M, N, K, layout, path):
+    say("extreme int8", M, N, K, layout, path)
+    A, B = extreme_i8(M, N, K, layout, 11000 + M + N)
+    code = oracle.B_KN if layout == "kn" else oracle.B_NK
+    acc = oracle.w8a8_acc(A, B, code, nthreads=NTH)
+    assert np.abs(acc.astype(np.int64)).max() >= 8192 * 127 * 127  # the case reaches the large sums
+    assert_same(gpu_i8(A, B, layout, "i32", path=path), acc, f"extreme int8 {path} {layout}")
+
+
+@pytest.mark.parametrize("M,N,K,layout,path",
+                         [c for c in EXTREME_CASES if c[4] != "gemv_dot" and not (c[4] == "gemv" and c[0] > 16 and c[3] == "kn")])
+def test_extreme_fp8_codes_exact(oracle, dev, M, N, K, layout, path):
+    say("extreme fp8", M, N, K, layout, path)
+    r = np.random.default_rng(12000 + M + N)
+    A = np.where(r.random((M, K)) < 0.5, 0x7E, 0xFE).astype(np.uint8)
+    Bkn = np.where(r.random((K, N)) < 0.5, 0x7E, 0xFE).astype(np.uint8)
+    Bkn[:, 0] = 0x7E  # a column of +448 only: with row 0 below, the sum K * 448^2
+    A[0] = 0x7E
+    B = Bkn if layout == "kn" else np.ascontiguousarray(Bkn.T)
+    sa, sb = 0.5, 0.25
+    ref = oracle.f8_gemm(A, B, sa, sb, b_layout=oracle.B_KN if layout == "kn" else oracle.B_NK, nthreads=NTH)
+    assert ref[0, 0] == np.float32(K * 448.0 * 448.0 * sa * sb)
+    assert_same(gpu_f8(A, B, sa, sb, layout, "f32", path=path), ref, f"extreme fp8 {path} {layout}")
+
+
 def test_c5_fp8_full(oracle, dev):
     """FP8 square: 8192^3 e4m3 (per-tensor amax/448 scales, B [K,N]), bf16 out,
     against the reference's sequential fp32 sum on 1024 rows spread over M
