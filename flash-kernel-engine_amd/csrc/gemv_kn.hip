@@ -134,7 +134,11 @@ __device__ __forceinline__ void ks_read_w(const lds_u8* slot, const uint32_t (&w
 // Wave w of workgroup b streams column block 4*(b/S) + w (128 columns) over
 // the 128-row pieces [s*PS, min(P, (s+1)*PS)) of split s = b % S and writes
 // its sums to part[block][s][m][column] for m < M.
-template <int EL>
+// NT: the weight copies are non-temporal.  At N = 14336, K = 4096 that is
+// 13.0 against 14.9 us at M = 1 and still ahead at M = 12 (16.8 / 17.0), but
+// behind from M = 14 (M = 16: 17.9 against 17.4 with the default policy).
+constexpr int KS_NT_MAX_M = 12;
+template <int EL, bool NT>
 __global__ __launch_bounds__(256) void gemv_kn_split_kernel(GemmArgs p, KnSplit sp) {
     constexpr bool F8 = EL == ELEM_F8;
     using AccV = typename std::conditional<F8, v4f, v4i>::type;
@@ -182,7 +186,7 @@ __global__ __launch_bounds__(256) void gemv_kn_split_kernel(GemmArgs p, KnSplit 
         for (int d = 0; d < KS_DB; ++d) {
             const uint32_t base = (((d >> 1) ^ (d >> 2)) & 1) ? bbase1 : bbase0;
             const uint32_t off = k0 + 8 * d < K ? base + static_cast<uint32_t>((k0 + 8 * d) * N) : 0x80000000u;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, dst + d * 1024, 16, static_cast<int>(off), 0, 0, 2);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, dst + d * 1024, 16, static_cast<int>(off), 0, 0, NT ? 2 : 0);
         }
 #pragma unroll
         for (int d = 0; d < KS_DA; ++d) {
@@ -374,8 +378,9 @@ hipError_t launch_kn_split_out(const GemmArgs& p, const KnSplit& sp, hipStream_t
     KnSplit s = sp;
     void* args[] = {&a, &s};
     const int nblk = (p.N + 4 * KS_W - 1) / (4 * KS_W);
-    hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(&gemv_kn_split_kernel<EL>), dim3(nblk * sp.S),
-                                   dim3(256), args, 0, stream);
+    const void* split = p.M <= KS_NT_MAX_M ? reinterpret_cast<const void*>(&gemv_kn_split_kernel<EL, true>)
+                                           : reinterpret_cast<const void*>(&gemv_kn_split_kernel<EL, false>);
+    hipError_t e = hipLaunchKernel(split, dim3(nblk * sp.S), dim3(256), args, 0, stream);
     if (e != hipSuccess) return e;
     const int64_t outs = static_cast<int64_t>(p.M) * p.N;  // N % 16 == 0
     const void* f;
