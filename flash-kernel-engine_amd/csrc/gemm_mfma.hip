@@ -138,9 +138,10 @@ struct Panel {
             off[i] = static_cast<uint32_t>(min(src, rows - 1) * ld + lc * 16);
         }
     }
-    // Load i of this wave for the stage at K byte k0 (uniform).
+    // Load i of this wave for the stage at K byte k0 (uniform); AUX: cache policy.
+    template <int AUX = 0>
     __device__ __forceinline__ void issue(int i, int k0, uint8_t* lds, int wave) const {
-        dma16(rsrc, off[i], k0, lds + (wave * PW + i) * 1024);
+        dma16<AUX>(rsrc, off[i], k0, lds + (wave * PW + i) * 1024);
     }
 };
 
@@ -179,8 +180,9 @@ struct KNPanel {
             off[i] = static_cast<uint32_t>(r * N + n0 + c * 16);
         }
     }
+    template <int AUX = 0>
     __device__ __forceinline__ void issue(int i, int kt, uint8_t* lds, int wave) const {
-        dma16(rsrc, off[i], kt * stage_bytes, lds + (wave * PW + i) * 1024);
+        dma16<AUX>(rsrc, off[i], kt * stage_bytes, lds + (wave * PW + i) * 1024);
     }
 };
 
@@ -338,7 +340,9 @@ __device__ __forceinline__ void mfma_one(const Frags<ELEM, TL>& f, typename Mma<
 template <bool SWI, class TL>
 constexpr int tile_cols() { return SWI ? TL::BN / 2 : TL::BN; }
 
-template <int ELEM, int BL, int OUT, bool SWI, class TL>
+// BNT: the B panel is read exactly once (one row of tiles), so its copies are
+// non-temporal (launch_t decides; A is re-read by every tile of the row).
+template <int ELEM, int BL, int OUT, bool SWI, class TL, bool BNT = false>
 __global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p) {
     static_assert(!SWI || (ELEM == ELEM_I8 && BL == FKE_B_NK && OUT != FKE_OUT_I32), "SwiGLU: INT8, B [N,K], float out");
     static_assert(!SWI || TL::NJ >= 2, "SwiGLU: each wave pairs gate and up blocks");
@@ -417,8 +421,8 @@ __global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p
     constexpr int NSLOT = PWA + TL::PWB;  // B [K,N] panels take BN/32 loads per wave too
     auto copy = [&](int q, int kt, uint8_t* b) __attribute__((always_inline)) {
         if (q < PWA) pa.issue(q, kt * BK, b, wave);
-        else if constexpr (BL == FKE_B_NK) pb.issue(q - PWA, kt * BK, b + TL::STAGE_A, wave);
-        else pb.issue(q - PWA, kt, b + TL::STAGE_A, wave);
+        else if constexpr (BL == FKE_B_NK) pb.template issue<BNT ? 2 : 0>(q - PWA, kt * BK, b + TL::STAGE_A, wave);
+        else pb.template issue<BNT ? 2 : 0>(q - PWA, kt, b + TL::STAGE_A, wave);
     };
     // A stage is NKS groups of NPIECE MFMAs (16 for the 256x256 tile).
     // Group g runs the MFMAs of one fragment set (g = 0: the previous stage's
@@ -677,8 +681,16 @@ hipError_t launch_t(const GemmArgs& p, hipStream_t stream, int cus) {
     const int grid = min(gm * gn, cus / NXCD * NXCD * TL::OCC);
     GemmArgs a = p;
     void* args[] = {&a};
-    return hipLaunchKernel(reinterpret_cast<const void*>(&gemm_mfma_kernel<ELEM, BL, OUT, SWI, TL>),
-                           dim3(grid), dim3(NTHREADS), args, 0, stream);
+    // One row of tiles reads each B byte once: non-temporal B copies (8-bit
+    // operands on the ring tiles, the batched-decode shapes).  Measured at
+    // N = 14336, K = 4096, cold weights: M = 64 on the 64x64 ring 16.6 -> 15.4
+    // us, M = 128 on the 128x64 ring 19.7 -> 19.2; with more tile rows the
+    // panel is re-read from L2 and non-temporal copies lose (4096x1376x4096:
+    // 27.6 against 46.6 us).
+    const void* f = reinterpret_cast<const void*>(&gemm_mfma_kernel<ELEM, BL, OUT, SWI, TL>);
+    if constexpr (TL::NS == 4 && elem_bytes(ELEM) == 1)
+        if (gm == 1) f = reinterpret_cast<const void*>(&gemm_mfma_kernel<ELEM, BL, OUT, SWI, TL, true>);
+    return hipLaunchKernel(f, dim3(grid), dim3(NTHREADS), args, 0, stream);
 }
 
 template <int ELEM, int BL, int OUT, bool SWI = false>
