@@ -766,6 +766,15 @@ bool mfma_supports(const GemmArgs& p, int elem) {
 //   tile's prologue and epilogue, but fetch each weight panel twice as often,
 //   which loses once the weights come from HBM (8192x8192x1024: 105 against
 //   120 us cold, though 99 against 103 warm).
+// - One row of tiles with more tiles than CUs (decode batches against a large
+//   N, e.g. an LM head): the smallest tile height that holds M, over several
+//   rounds, rather than 256x256 rows of mostly padding.  M <= 64: the 64x64
+//   ring (64x65536x4096: 59.9 us against 89.6 on 256x256; 64x128256: 116.7
+//   against 152.3), unless one round of the 128x128 ring leaves an eighth of
+//   the CUs or more idle (64x16896: 23.5 against 27.5 on 64x64, but
+//   64x32768: 35.0 against 31.8).  M <= 128: 128x128 tiles at two per CU
+//   (128x49152: 58.1 against 70.3; 128x65536: 72.0 against 82.3).  Past 128
+//   rows 256x256 stays ahead (256x65536: 86.6 against 104.5 on 128x128).
 // A 256x128 tile (one workgroup per CU) measured slower than 128x128 on every
 // few-tile shape, INT8, FP8 and bf16.  B [K,N] uses the same rule.
 int mfma_pick_tile(const GemmArgs& p, int cus) {
@@ -775,9 +784,12 @@ int mfma_pick_tile(const GemmArgs& p, int cus) {
         return (p.M + bm - 1) / bm * ((NO + tc - 1) / tc);
     };
     if (!p.swiglu && tiles(64, 64) <= cus) return MFMA_TILE_64x64_RING4;
-    if (!p.swiglu && tiles(128, 64) <= cus) return MFMA_TILE_128x64_RING4;
     const int64_t t128 = tiles(128, 128);
+    if (!p.swiglu && p.M <= 64)
+        return t128 * 8 <= static_cast<int64_t>(cus) * 7 ? MFMA_TILE_128x128_RING4 : MFMA_TILE_64x64_RING4;
+    if (!p.swiglu && tiles(128, 64) <= cus) return MFMA_TILE_128x64_RING4;
     if (t128 <= cus) return MFMA_TILE_128x128_RING4;
+    if (!p.swiglu && p.M <= 128) return MFMA_TILE_128x128;
     if (tiles(256, 256) < cus && t128 <= 2 * static_cast<int64_t>(cus)) return MFMA_TILE_128x128;
     return MFMA_TILE_256x256;
 }
@@ -785,15 +797,19 @@ int mfma_pick_tile(const GemmArgs& p, int cus) {
 // Time (us) of the MFMA GEMM on an 8-bit B [N,K] shape, for the choice
 // between it and the streamed decode kernel (cold weights, bf16 out; fitted on
 // N = 1792..14336, K = 4096 and 14336, M = 16..512, within about 20 %).
-// Ring tiles: the larger of the bytes one CU loads, (BM + BN) * K, at 44 GB/s
-// and the weights at 4.2 TB/s, plus 1 us.  128x128 with two stages: about
+// Ring tiles: the larger of the bytes one CU loads, (BM + BN) * K per round of
+// tiles, at 44 GB/s and the weights at 4.2 TB/s (4.5 TB/s past two rounds:
+// 64x65536x4096 ran 59.9 us, 64x128256x4096 116.7), plus 1 us.  128x128 with two stages: about
 // 1 us per stage per round of two tiles per CU.  256x256: 1.35 us per stage
 // and 11 us per round of tiles.
 double mfma_time_estimate_us(const GemmArgs& p, int cus) {
     const double kt = p.K / 128.0;
     const int64_t NO = p.swiglu ? p.N / 2 : p.N;
-    auto ring = [&](double bm, double bn) {
-        return std::max((bm + bn) * p.K / 44.0e3, static_cast<double>(p.N) * p.K / 4.2e6) + 1.0;
+    auto ring = [&](int64_t bm, int64_t bn) {
+        const int64_t tc = p.swiglu ? bn / 2 : bn;
+        const double rounds = static_cast<double>(((p.M + bm - 1) / bm * ((NO + tc - 1) / tc) + cus - 1) / cus);
+        return std::max(static_cast<double>(bm + bn) * p.K * rounds / 44.0e3,
+                        static_cast<double>(p.N) * p.K / (rounds > 2 ? 4.5e6 : 4.2e6)) + 1.0;
     };
     switch (mfma_pick_tile(p, cus)) {
         case MFMA_TILE_64x64_RING4: return ring(64, 64);

@@ -262,6 +262,8 @@ def test_path_unavailable_for_shape_is_rejected():
     (17, 14336, 4096, 0, _lib.PATH_GEMV),    # batches: LDS-streamed kernel against the MFMA GEMM's cost
     (32, 14336, 4096, 0, _lib.PATH_GEMV),
     (48, 14336, 4096, 0, _lib.PATH_MFMA),    # four activation blocks: the MFMA GEMM's 64x64 ring is faster
+    (32, 65536, 4096, 0, _lib.PATH_GEMV),    # large N: streamed 51.6 against 57.2 us on four 64x64 rounds
+    (48, 65536, 4096, 0, _lib.PATH_MFMA),    # 59.3 on four 64x64 rounds against 70.5 streamed
     (64, 14336, 4096, 0, _lib.PATH_MFMA),
     (128, 14336, 4096, 0, _lib.PATH_MFMA),   # 128x64 ring
     (192, 14336, 4096, 0, _lib.PATH_MFMA),
@@ -373,6 +375,17 @@ def test_torch_extension_rejects_host_tensors():
     (128, 28672, 4096, 0, 1, 256, _lib.PATH_MFMA_128x128_RING4), # SwiGLU, 14336 outputs: 224 tiles of 64
     (4096, 2752, 4096, 0, 1, 256, _lib.PATH_MFMA_256x256),       # SwiGLU, 1376 outputs: 176 / 704
     (4096, 1376, 4096, 0, 0, 80, _lib.PATH_MFMA_256x256),        # fills 80 CUs
+    # one row of tiles, more tiles than CUs (decode batches against a large N)
+    (64, 65536, 4096, 0, 0, 256, _lib.PATH_MFMA_64x64_RING4),    # 1024 tiles of 64x64: four rounds
+    (64, 128256, 4096, 1, 0, 256, _lib.PATH_MFMA_64x64_RING4),   # B [K,N]: the same rule
+    (48, 32768, 4096, 0, 0, 256, _lib.PATH_MFMA_64x64_RING4),    # 256 of 128x128 would leave no CU idle
+    (64, 16896, 4096, 0, 0, 256, _lib.PATH_MFMA_128x128_RING4),  # 132 of 128x128: one round, half the CUs
+    (64, 28672, 4096, 0, 0, 256, _lib.PATH_MFMA_128x128_RING4),  # 224 = 7/8 of the CUs
+    (64, 28800, 4096, 0, 0, 256, _lib.PATH_MFMA_64x64_RING4),    # 225
+    (128, 65536, 4096, 0, 0, 256, _lib.PATH_MFMA_128x128),       # 512 of 128x128: two per CU
+    (96, 131072, 4096, 0, 0, 256, _lib.PATH_MFMA_128x128),       # 1024 of 128x128: four rounds
+    (256, 65536, 4096, 0, 0, 256, _lib.PATH_MFMA_256x256),       # past 128 rows: 256x256
+    (128, 65536, 4096, 0, 1, 256, _lib.PATH_MFMA_256x256),       # SwiGLU keeps the previous rule
 ])
 def test_mfma_tile_choice(M, N, K, layout, swiglu, cus, want):
     assert _lib.lib().fke_select_mfma_tile(M, N, K, layout, swiglu, cus) == want
