@@ -710,6 +710,25 @@ def test_mfma_tiles_ragged_shapes(oracle, dev, tile, layout, shape):
         assert_same(got, oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, out), f"{tile} {layout} {(M, N, K)} {out}")
 
 
+@pytest.mark.parametrize("M,N,K,layout,want", [
+    (48, 33024, 1024, "nk", _lib.PATH_MFMA_64x64_RING4),    # 516 tiles of 64x64: three rounds, one tile row
+    (64, 65536, 512, "kn", _lib.PATH_MFMA_64x64_RING4),     # 1024 tiles, B [K,N]
+    (100, 70000, 512, "nk", _lib.PATH_MFMA_128x128),        # 547 of 128x128, ragged rows and columns
+])
+def test_single_tile_row_many_rounds(oracle, dev, M, N, K, layout, want):
+    """One row of tiles with more tiles than CUs (decode batches against a large
+    N): the dispatcher's tile (several rounds per workgroup, B copied
+    non-temporally), int32 and bf16 outputs bit-exact against the oracle."""
+    say("single tile row", M, N, K, layout)
+    code = _lib.B_KN if layout == "kn" else _lib.B_NK
+    assert _lib.lib().fke_select_mfma_tile(M, N, K, code, 0, 0) == want
+    A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 13000 + M, layout=layout)
+    acc = oracle.w8a8_acc(A, B, oracle.B_KN if layout == "kn" else oracle.B_NK, nthreads=NTH)
+    assert_same(gpu_i8(A, B, layout, "i32", path="mfma"), acc, f"single row {(M, N, K)} i32")
+    got = gpu_i8(A, B, layout, "bf16", path="mfma", sa_vec=sa, sb_vec=sb, bias=bias)
+    assert_same(got, oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, "bf16"), f"single row {(M, N, K)} bf16")
+
+
 @pytest.mark.parametrize("M,N,K,out,want", [
     (4096, 1376, 4096, "bf16", _lib.PATH_MFMA_128x128),   # 8-way column shard of 11008
     (8192, 1024, 8192, "f32", _lib.PATH_MFMA_128x128),    # 8-way column shard of 8192
