@@ -973,7 +973,13 @@ bool gemv_i8_batch_pays(const GemmArgs& p) {
     const int64_t g = lds_grid(p), no = p.swiglu ? p.N / 2 : p.N;
     const double share = static_cast<double>((no + g - 1) / g) * (p.swiglu ? 2 : 1) * kib;
     const bool four = p.M > 32;
-    const double chunk = (four ? 5.2 : 4.0) + (four ? 0.056 : 0.046) * share + (four ? 0.0078 : 0.004) * min(p.M, 64) * kib;
+    double chunk = (four ? 5.2 : 4.0) + (four ? 0.056 : 0.046) * share + (four ? 0.0078 : 0.004) * min(p.M, 64) * kib;
+    // Shares past LK_TMAX 16-row tiles take several tile chunks, and with four
+    // blocks each further chunk streams the 64 activation rows again at a CU's
+    // ~44 KiB/us (64x16896x4096: 28.0 us, 22 without this term; two blocks
+    // showed no such cost: 32x20480x4096, 19.7 us against 19.2).
+    const int64_t th = ((no + g - 1) / g + 15) / 16 * (p.swiglu ? 2 : 1);
+    if (four) chunk += static_cast<double>((th + LK_TMAX - 1) / LK_TMAX - 1) * 64.0 * kib / 44.0;
     // one row of g workgroups per 64 rows; rows share the CUs (one workgroup each)
     const int64_t waves = ((p.M + 63) / 64 * g + cu_count() - 1) / cu_count();
     const double t_lds = waves * chunk;

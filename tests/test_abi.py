@@ -264,6 +264,8 @@ def test_path_unavailable_for_shape_is_rejected():
     (48, 14336, 4096, 0, _lib.PATH_MFMA),    # four activation blocks: the MFMA GEMM's 64x64 ring is faster
     (32, 65536, 4096, 0, _lib.PATH_GEMV),    # large N: streamed 51.6 against 57.2 us on four 64x64 rounds
     (48, 65536, 4096, 0, _lib.PATH_MFMA),    # 59.3 on four 64x64 rounds against 70.5 streamed
+    (64, 16896, 4096, 0, _lib.PATH_MFMA),    # two tile chunks streamed (28.0 us) against the 128x128 ring (23.4)
+    (32, 20480, 4096, 0, _lib.PATH_GEMV),    # two chunks with two blocks: streamed 19.7 against 24.6
     (64, 14336, 4096, 0, _lib.PATH_MFMA),
     (128, 14336, 4096, 0, _lib.PATH_MFMA),   # 128x64 ring
     (192, 14336, 4096, 0, _lib.PATH_MFMA),
