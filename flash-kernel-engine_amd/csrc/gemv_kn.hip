@@ -732,11 +732,25 @@ static size_t kn_ws_bytes(int M, int N, int S) {
 // K splits: as many as fill the CUs with one 512-column workgroup each
 // (kCUs; S <= 8, at least one 128-row piece per split, and no more than a
 // workspace of ws_bytes holds), with no empty split.  S = 1: the full kernel.
+// Past kCUs / 2 blocks (N > 65536) the workgroups take several rounds, and
+// S in 2..4 is the one with the fewest rounds per split (ties: the smaller):
+// at N = 81920 / 98304 / 128256, K = 4096, M = 1, S = 3 / 4 / 2 ran 54 / 64 /
+// 79 us against 88 / 107 / 108 us for the full kernel.
 static void kn_splits(const GemmArgs& p, size_t ws_bytes, int* S_out, int* PS_out) {
     constexpr int kCUs = 256;
     const int P = (p.K + KS_ROWS - 1) / KS_ROWS;
     const int nblk = (p.N + 4 * KS_W - 1) / (4 * KS_W);
     int S = kCUs / nblk;
+    if (S < 2) {
+        double best = 0.0;
+        for (int s = 2; s <= 4; ++s) {
+            const double per = static_cast<double>((static_cast<int64_t>(nblk) * s + kCUs - 1) / kCUs) / s;
+            if (s == 2 || per < best - 1e-9) {
+                best = per;
+                S = s;
+            }
+        }
+    }
     if (S > KS_SMAX) S = KS_SMAX;
     if (S > P) S = P;
     while (S > 1 && kn_ws_bytes(p.M, p.N, S) > ws_bytes) --S;

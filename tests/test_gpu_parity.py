@@ -301,9 +301,11 @@ def test_c2_decode_full_b_kn(oracle, dev, M):
 
 # (M, N, K): one 64-column block and a ragged last block (N % 64 != 0), a K
 # that ends in half an item (K % 128 == 64), K below one item per wave (waves
-# without items), K = 14336 (28 items per wave), more blocks than CUs
+# without items), K = 14336 (28 items per wave), more blocks than CUs, and N
+# past 65536 (K splits over several rounds of workgroups: S = 3 with splits of
+# 3 / 3 / 2 items, S = 2)
 KN_SHAPES = [(1, 16, 4096), (3, 304, 1024), (16, 1040, 192), (5, 4096, 64), (2, 4096, 14336),
-             (16, 20016, 2048), (8, 1008, 4160)]
+             (16, 20016, 2048), (8, 1008, 4160), (1, 82000, 1024), (9, 100000, 512)]
 
 
 @pytest.mark.parametrize("M,N,K", KN_SHAPES)
