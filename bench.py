@@ -94,6 +94,9 @@ def parse():
     ap.add_argument("--decode-families", action="store_true",
                     help="also time decode M=1,2,4,8,16 on the MFMA kernels the dispatcher picks and on the "
                          "VALU dot-product kernels (FKE_PATH_GEMV_DOT), for the choice between them")
+    ap.add_argument("--ksplit", action="store_true",
+                    help="also time the MFMA GEMM's K split on few-tile shapes with a long K beside the unsplit tile "
+                         "(part of --extra)")
     ap.add_argument("--shards", action="store_true",
                     help="also time the per-GPU shards of 8-way tensor parallelism (part of --extra)")
     ap.add_argument("--tile-sweep", action="store_true",
@@ -229,8 +232,10 @@ def main():
         del src, dst
     if args.extra:
         line["extra"] = extra_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args)
-    elif args.swiglu or args.half or args.fp8 or args.shards or args.batch or args.decode_families:
+    elif args.swiglu or args.half or args.fp8 or args.shards or args.batch or args.decode_families or args.ksplit:
         line["extra"] = {}
+        if args.ksplit:
+            line["extra"].update(ksplit_configs(torch, L, _lib, dev, gen, args))
         if args.decode_families:
             line["extra"].update(decode_family_configs(torch, L, _lib, dev, gen, args))
         if args.batch:
@@ -658,6 +663,36 @@ def batch_configs(torch, L, _lib, dev, gen, args):
     return res
 
 
+KSPLIT_SHAPES = [(64, 4096, 14336, "nk"), (128, 8192, 28672, "nk"), (100, 1000, 14720, "nk"),
+                 (128, 1024, 8192, "nk"), (300, 528, 8192, "nk"), (200, 2000, 8192, "kn")]
+
+
+def ksplit_configs(torch, L, _lib, dev, gen, args):
+    """The MFMA GEMM's K split (few output tiles, a long K): the dispatcher's call, which splits K, beside
+    the unsplit tile the tile rule picks, pinned; cold weights cycled from a HIP graph like the decode
+    lines (the byte counts are the operands' and the output's, not the partial sums')."""
+    import ctypes
+    res = {}
+    names = {_lib.PATH_MFMA_64x64_RING4: "64x64_ring4", _lib.PATH_MFMA_128x64_RING4: "128x64_ring4",
+             _lib.PATH_MFMA_128x128_RING4: "128x128_ring4", _lib.PATH_MFMA_128x128: "128x128",
+             _lib.PATH_MFMA_256x256: "256x256"}
+    for M, N, K, lay in KSPLIT_SHAPES:
+        code = _lib.B_KN if lay == "kn" else _lib.B_NK
+        t = ctypes.c_int(0)
+        S = L.fke_select_mfma_split(M, N, K, code, 0, ctypes.byref(t))
+        unsplit = L.fke_select_mfma_tile(M, N, K, code, 0, 0)
+        nbuf = min(128, max(args.gemv_buffers, -(-(448 << 20) // (N * K))))  # >= 448 MiB of weights: past the MALL
+        key = f"ksplit_{M}x{N}x{K}_{lay}"
+        r = gemv_bench(torch, L, _lib, dev, gen, M, nbuf, args.gemv_launches, N=N, K=K, layout=lay)
+        r["kernel"] = (f"gemm_mfma_kernel {names[t.value]}, {S} K splits + splitk_reduce_kernel" if S > 1
+                       else f"{r['kernel']} (unsplit)")
+        res[key] = r
+        u = gemv_bench(torch, L, _lib, dev, gen, M, nbuf, args.gemv_launches, N=N, K=K, layout=lay, path=unsplit)
+        u["kernel"] = f"gemm_mfma_kernel {names[unsplit]} (unsplit, pinned)"
+        res[key + "_unsplit"] = u
+    return res
+
+
 def extra_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
     res = {}
     # prefill 4096 x 11008 x 4096, bf16 out
@@ -701,6 +736,7 @@ def extra_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
     res.update(shard_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args))
     res["gemv_M4"] = gemv_bench(torch, L, _lib, dev, gen, 4, args.gemv_buffers, args.gemv_launches)
     res.update(batch_configs(torch, L, _lib, dev, gen, args))
+    res.update(ksplit_configs(torch, L, _lib, dev, gen, args))
     # per-token INT8 quantiser in front of the W8A8 GEMM: bf16 activations of C3 (4096 x 4096),
     # 12 rotating inputs (384 MiB, more than the MALL), timed from a HIP graph like the GEMV
     M, K, nx = 4096, 4096, 12

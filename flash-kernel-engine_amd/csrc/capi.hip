@@ -153,8 +153,12 @@ size_t w8a8_ws_bytes(int M, int K) { return w8a8_ws_scale_offset(M, K) + 4 * sta
 
 // Shared body of fke_w8a8_linear / fke_w8a8_swiglu_linear.  p describes the
 // GEMM on the int8 codes with A = X: the quantiser writes X's codes and row
-// scales into the workspace, then the GEMM reads them there.
-int run_w8a8_from_float(GemmArgs p, int in_dtype, void* workspace, size_t workspace_bytes, void* stream) {
+// scales into the workspace, then the GEMM reads them there.  The workspace
+// past the row scales (from the next 256-byte boundary) holds a K split's
+// partial sums when it is large enough; with `may_alloc` an empty remainder
+// lets the split use the stream's own workspace instead.
+int run_w8a8_from_float(GemmArgs p, int in_dtype, void* workspace, size_t workspace_bytes, void* stream,
+                        bool may_alloc = true) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (!workspace || workspace_bytes < w8a8_ws_bytes(p.M, p.K)) return hipErrorInvalidValue;
     int8_t* Q = static_cast<int8_t*>(workspace);
@@ -163,7 +167,13 @@ int run_w8a8_from_float(GemmArgs p, int in_dtype, void* workspace, size_t worksp
     if (st != hipSuccess) return st;
     p.A = Q;
     p.scale_a = S;
-    return run_i8(FKE_PATH_AUTO, p, stream);
+    const size_t used = (w8a8_ws_bytes(p.M, p.K) + 255) & ~static_cast<size_t>(255);
+    KnWorkspace rest;
+    if (workspace_bytes > used) {
+        rest.ptr = static_cast<char*>(workspace) + used;
+        rest.bytes = workspace_bytes - used;
+    }
+    return run_i8(FKE_PATH_AUTO, p, stream, rest.ptr || !may_alloc ? &rest : nullptr);
 }
 
 // SwiGLU GEMM: B is the merged [2I, K] weight; the kernels see N = 2I.
@@ -214,10 +224,22 @@ int mfma_tile_of_path(int path, const GemmArgs& p) {
     }
 }
 
-// The MFMA GEMM with the tile `path` names, after its shape check.
-int run_mfma(int path, const GemmArgs& p, int elem, hipStream_t s) {
+// The MFMA GEMM with the tile `path` names, after its shape check.  The
+// automatic tile also takes the K split the plan gives (8-bit shapes with few
+// tiles and a long K), on the caller's workspace (`given`) or else on the
+// stream's own; unsplit, on the tile rule's tile, when that is too small.
+int run_mfma(int path, const GemmArgs& p, int elem, hipStream_t s, const KnWorkspace* given = nullptr) {
     const int tile = mfma_tile_of_path(path, p);
     if (tile < 0 || !fke::mfma_supports(p, elem)) return hipErrorInvalidValue;
+    if (tile == fke::MFMA_TILE_AUTO) {
+        const fke::MfmaPlan pl = fke::mfma_plan(p, elem, fke::device_cus());
+        if (pl.S > 1) {
+            const size_t need = fke::mfma_split_bytes(p, pl.S);
+            const KnWorkspace ws = given ? *given : kn_workspace(s, need);
+            if (ws.ptr && ws.bytes >= need && (reinterpret_cast<uintptr_t>(ws.ptr) & 15) == 0)
+                return fke::launch_mfma(p, elem, s, pl.tile, fke::SplitK{pl.S, pl.KS, ws.ptr});
+        }
+    }
     return fke::launch_mfma(p, elem, s, tile);
 }
 
@@ -234,7 +256,7 @@ int run_i8(int path, const GemmArgs& p, void* stream, const KnWorkspace* ws) {
         case FKE_PATH_MFMA_128x128:
         case FKE_PATH_MFMA_128x128_RING4:
         case FKE_PATH_MFMA_128x64_RING4:
-        case FKE_PATH_MFMA_64x64_RING4: return run_mfma(path, p, fke::ELEM_I8, s);
+        case FKE_PATH_MFMA_64x64_RING4: return run_mfma(path, p, fke::ELEM_I8, s, ws);
         case FKE_PATH_GENERIC: return fke::launch_generic(p, fke::ELEM_I8, s);
         case FKE_PATH_GEMV_DOT:
             if (!fke::gemv_dot_supports(p)) return hipErrorInvalidValue;
@@ -284,7 +306,7 @@ int run_f8(int path, const GemmArgs& p, void* stream, const KnWorkspace* ws = nu
         case FKE_PATH_MFMA_128x128:
         case FKE_PATH_MFMA_128x128_RING4:
         case FKE_PATH_MFMA_128x64_RING4:
-        case FKE_PATH_MFMA_64x64_RING4: return run_mfma(path, p, fke::ELEM_F8, s);
+        case FKE_PATH_MFMA_64x64_RING4: return run_mfma(path, p, fke::ELEM_F8, s, ws);
         case FKE_PATH_GENERIC: return fke::launch_generic(p, fke::ELEM_F8, s);
         default: return hipErrorInvalidValue;
     }
@@ -329,7 +351,10 @@ size_t fke_qgemm_workspace_size(int M, int N, int K, int b_layout) {
     const void* a = reinterpret_cast<const void*>(uintptr_t{4096});
     const GemmArgs p = make_args(a, a, const_cast<void*>(a), M, N, K, nullptr, nullptr, 1.f, 1.f, nullptr, FKE_OUT_F32,
                                  b_layout);
-    return fke::gemv_kn_supports(p, fke::ELEM_I8) ? fke::gemv_kn_workspace_bytes(p) : 0;
+    const size_t kn = fke::gemv_kn_supports(p, fke::ELEM_I8) ? fke::gemv_kn_workspace_bytes(p) : 0;
+    const fke::MfmaPlan pl = fke::mfma_plan(p, fke::ELEM_I8, fke::device_cus());
+    const size_t split = pl.S > 1 && fke::mfma_supports(p, fke::ELEM_I8) ? fke::mfma_split_bytes(p, pl.S) : 0;
+    return kn > split ? kn : split;
 }
 
 int fke_qgemm_i8_ws(const int8_t* A, const int8_t* B, void* C, int M, int N, int K, const float* scale_a,
@@ -411,7 +436,7 @@ int fke_w8a8_linear_noalloc(const void* X, int in_dtype, const int8_t* W, void* 
     st = scratch_of_device(dev, &ptr);
     if (st != hipSuccess) return st;
     return run_w8a8_from_float(make_args(X, W, Y, M, N, K, nullptr, w_scale, 1.0f, sb, bias, out_dtype, FKE_B_NK),
-                               in_dtype, ptr, FKE_W8A8_NOALLOC_SCRATCH_BYTES, stream);
+                               in_dtype, ptr, FKE_W8A8_NOALLOC_SCRATCH_BYTES, stream, false);
 }
 
 int fke_w8a8_swiglu_linear(const void* X, int in_dtype, const int8_t* W, void* H, int M, int I, int K,
@@ -466,6 +491,24 @@ int fke_select_mfma_tile(int M, int N, int K, int b_layout, int swiglu, int cus)
         case fke::MFMA_TILE_64x64_RING4: return FKE_PATH_MFMA_64x64_RING4;
         default: return FKE_PATH_MFMA_256x256;
     }
+}
+
+int fke_select_mfma_split(int M, int N, int K, int b_layout, int cus, int* tile_path) {
+    if (M < 1 || N < 1 || K < 1 || (b_layout != FKE_B_NK && b_layout != FKE_B_KN)) return -1;
+    const GemmArgs p = make_args(nullptr, nullptr, nullptr, M, N, K, nullptr, nullptr, 1.f, 1.f, nullptr,
+                                 FKE_OUT_BF16, b_layout);
+    if (cus <= 0) cus = fke::device_cus();
+    const fke::MfmaPlan pl = fke::mfma_plan(p, fke::ELEM_I8, cus);
+    if (tile_path) {
+        switch (pl.tile) {
+            case fke::MFMA_TILE_128x128: *tile_path = FKE_PATH_MFMA_128x128; break;
+            case fke::MFMA_TILE_128x128_RING4: *tile_path = FKE_PATH_MFMA_128x128_RING4; break;
+            case fke::MFMA_TILE_128x64_RING4: *tile_path = FKE_PATH_MFMA_128x64_RING4; break;
+            case fke::MFMA_TILE_64x64_RING4: *tile_path = FKE_PATH_MFMA_64x64_RING4; break;
+            default: *tile_path = FKE_PATH_MFMA_256x256;
+        }
+    }
+    return pl.S;
 }
 
 // Reference src/tensor_core_attention.cu:13-86 (launch_wmma_gemm_fp16): A fp16

@@ -44,7 +44,26 @@ enum MfmaTile {
     MFMA_TILE_128x64_RING4 = 4,  // not for SwiGLU
     MFMA_TILE_64x64_RING4 = 5    // not for SwiGLU
 };
-hipError_t launch_mfma(const GemmArgs& p, int elem, hipStream_t stream, int tile = MFMA_TILE_AUTO);
+// K split of the MFMA GEMM: S ranges of KS stages (128 K bytes each); split s
+// writes its raw sums (int32 for INT8, fp32 for FP8) to part[s][M][N], and a
+// second kernel adds the S sums of each output in the order s = 0..S-1 and
+// applies the epilogue.  S = 1: no split, the fused epilogue.
+struct SplitK {
+    int S = 1;
+    int KS = 0;
+    void* part = nullptr;
+};
+// Tile and K split the MFMA GEMM runs with on `cus` CUs (S = 1: none).
+struct MfmaPlan {
+    int tile;
+    int S;
+    int KS;
+};
+MfmaPlan mfma_plan(const GemmArgs& p, int elem, int cus);
+// Bytes of the partial sums of an S-way split (S * M * N * 4).
+size_t mfma_split_bytes(const GemmArgs& p, int S);
+hipError_t launch_mfma(const GemmArgs& p, int elem, hipStream_t stream, int tile = MFMA_TILE_AUTO,
+                       const SplitK& sk = SplitK{});
 int mfma_pick_tile(const GemmArgs& p, int cus);
 // Estimated time (us) of the MFMA GEMM on an 8-bit B [N,K] shape.
 double mfma_time_estimate_us(const GemmArgs& p, int cus);

@@ -343,7 +343,7 @@ constexpr int tile_cols() { return SWI ? TL::BN / 2 : TL::BN; }
 // BNT: the B panel is read exactly once (one row of tiles), so its copies are
 // non-temporal (launch_t decides; A is re-read by every tile of the row).
 template <int ELEM, int BL, int OUT, bool SWI, class TL, bool BNT = false>
-__global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p) {
+__global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p, SplitK sk) {
     static_assert(!SWI || (ELEM == ELEM_I8 && BL == FKE_B_NK && OUT != FKE_OUT_I32), "SwiGLU: INT8, B [N,K], float out");
     static_assert(!SWI || TL::NJ >= 2, "SwiGLU: each wave pairs gate and up blocks");
     constexpr int NKS = Mma<ELEM>::KSTEPS;
@@ -371,10 +371,15 @@ __global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p
     // XCD and each XCD walks its tile range in the same order as a one-tile-
     // per-workgroup launch would), so a CU moves to its next tile without a
     // workgroup relaunch.
-    for (int slot = blockIdx.x; slot < gm * gn; slot += gridDim.x) {
+    // K split (S > 1): the S splits of a tile are walked as S rows of tiles,
+    // item (split, tm, tn) summing K stages [split * KS, split * KS + KS).
+    const int S = sk.S;
+    for (int slot = blockIdx.x; slot < gm * gn * S; slot += gridDim.x) {
     if (slot != static_cast<int>(blockIdx.x)) barrier();  // the last tile's epilogue read epi_* from LDS
     int tm, tn;
-    tile_of(slot, gm, gn, tm, tn);
+    tile_of(slot, gm * S, gn, tm, tn);
+    const int split = tm / gm;
+    tm -= split * gm;
     const int m0 = tm * BM, n0 = tn * TC;  // n0: first output column
 
     const int8_t* A = static_cast<const int8_t*>(p.A);
@@ -399,7 +404,8 @@ __global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
 
-    const int KT = K / BK;
+    const int kt0 = split * sk.KS;  // first K stage of this item
+    const int KT = S > 1 ? min(K / BK - kt0, sk.KS) : K / BK;
     Panel<TL::PWA> pa;
     pa.init(A, K, m0, M, wave, lane);
     using BPanel = typename std::conditional<BL == FKE_B_NK, Panel<TL::PWB>, KNPanel<TL::BN>>::type;
@@ -413,6 +419,17 @@ __global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p
         for (int j = 0; j < NJ; ++j)
 #pragma unroll
             for (int rr = 0; rr < 2; ++rr) kn_off[j][rr] = kn_read_off<ELEM, TL>(lane, wn, j, rr);
+    }
+    if (kt0 > 0) {  // the copies start at stage kt0 (K-contiguous rows; B [K,N]: kt0 stages of k rows)
+#pragma unroll
+        for (int i = 0; i < TL::PWA; ++i) pa.off[i] += static_cast<uint32_t>(kt0 * BK);
+        if constexpr (BL == FKE_B_NK) {
+#pragma unroll
+            for (int i = 0; i < TL::PWB; ++i) pb.off[i] += static_cast<uint32_t>(kt0 * BK);
+        } else {
+#pragma unroll
+            for (int i = 0; i < KNPanel<TL::BN>::PW; ++i) pb.off[i] += static_cast<uint32_t>(kt0) * pb.stage_bytes;
+        }
     }
 
     // Copy of stage kt into buffer b, slot q of NSLOT: slots 0..PWA-1 copy
@@ -586,8 +603,42 @@ __global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p
     // edge tiles.  Stores are non-temporal: the output is written once and
     // should not evict the operand panels other workgroups still stream
     // through L2.
-    constexpr int OB = OUT == FKE_OUT_BF16 ? 2 : 4;  // output bytes per element
     const int lr = lane & 31, lh = lane >> 5;
+    if constexpr (!SWI) {
+        if (S > 1) {
+            // K split: the item's raw sums to part[split][m][n] (int32 / fp32),
+            // through a buffer resource based at row m0 of the split whose
+            // range ends at the last valid row, as the fused epilogue below.
+            const uint32_t prow = static_cast<uint32_t>(N) * 4;
+            const __amdgpu_buffer_rsrc_t rp =
+                make_rsrc(static_cast<char*>(sk.part) + (static_cast<size_t>(split) * M + m0) * prow,
+                          min(M - m0, BM) * static_cast<int>(prow));
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                const int cn = wn * TL::WN + j * 32 + lr;
+                const uint32_t lane_off =
+                    n0 + cn < N ? static_cast<uint32_t>(wm * TL::WM + 4 * lh) * prow + static_cast<uint32_t>(n0 + cn) * 4
+                                : 0x80000000u;
+#pragma unroll
+                for (int i = 0; i < NI; ++i) {
+                    fence();
+#pragma unroll
+                    for (int g = 0; g < 4; ++g)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int voff = static_cast<int>(lane_off + static_cast<uint32_t>(i * 32 + 8 * g + e) * prow);
+                            const int v = 4 * g + e;
+                            uint32_t bits;
+                            if constexpr (ELEM == ELEM_I8) bits = static_cast<uint32_t>(acc[i][j][v]);
+                            else bits = __float_as_uint(acc[i][j][v]);
+                            __builtin_amdgcn_raw_buffer_store_b32(bits, rp, voff, 0, 0);
+                        }
+                }
+            }
+            continue;
+        }
+    }
+    constexpr int OB = OUT == FKE_OUT_BF16 ? 2 : 4;  // output bytes per element
     const uint32_t row_bytes = static_cast<uint32_t>(NO) * OB;
     const __amdgpu_buffer_rsrc_t rc = make_rsrc(static_cast<char*>(p.C) + static_cast<size_t>(m0) * row_bytes,
                                                 min(M - m0, BM) * static_cast<int>(row_bytes));
@@ -674,13 +725,48 @@ __global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p
     }
 }
 
+// The second kernel of a K split: thread idx adds the S partial sums of output
+// idx = m * N + n in the order s = 0..S-1 (INT8: exact int32; FP8: fp32 in
+// that fixed order) and applies the fused epilogue's arithmetic:
+// y = fmaf(sum, sa_m * sb_n, bias_n) (FP8: fmaf(sum, sa * sb, bias_n)), bias_n
+// = -0.0 without a bias, as the fused epilogue does.
+template <int ELEM, int OUT>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs p, SplitK sk) {
+    using AccE = typename std::conditional<ELEM == ELEM_I8, int32_t, float>::type;
+    const int64_t mn = static_cast<int64_t>(p.M) * p.N;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (idx >= mn) return;
+    const int m = static_cast<int>(idx / p.N), n = static_cast<int>(idx % p.N);
+    const AccE* part = static_cast<const AccE*>(sk.part);
+    AccE v[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) v[t] = t < sk.S ? part[t * mn + idx] : AccE(0);
+    AccE sum = v[0];
+#pragma unroll
+    for (int t = 1; t < 8; ++t)
+        if (t < sk.S) sum += v[t];
+    const float bn = p.bias ? p.bias[n] : -0.0f;
+    float y;
+    int32_t a = 0;
+    if constexpr (ELEM == ELEM_I8) {
+        a = sum;
+        const float sam = p.scale_a ? p.scale_a[m] : p.sa, sbn = p.scale_b ? p.scale_b[n] : p.sb;
+        y = __builtin_fmaf(static_cast<float>(a), sam * sbn, bn);
+    } else {
+        y = __builtin_fmaf(sum, p.sa * p.sb, bn);
+    }
+    store_out<OUT>(p.C, static_cast<size_t>(idx), y, a);
+}
+
 template <int ELEM, int BL, int OUT, bool SWI, class TL>
-hipError_t launch_t(const GemmArgs& p, hipStream_t stream, int cus) {
+hipError_t launch_t(const GemmArgs& p, hipStream_t stream, int cus, const SplitK& sk) {
     constexpr int TC = tile_cols<SWI, TL>();
     const int gm = (p.M + TL::BM - 1) / TL::BM, gn = ((SWI ? p.N / 2 : p.N) + TC - 1) / TC;
-    const int grid = min(gm * gn, cus / NXCD * NXCD * TL::OCC);
+    const int grid = min(gm * gn * sk.S, cus / NXCD * NXCD * TL::OCC);
+    if (sk.S > 1 && (SWI || elem_bytes(ELEM) != 1 || sk.part == nullptr)) return hipErrorInvalidValue;
     GemmArgs a = p;
-    void* args[] = {&a};
+    SplitK k = sk;
+    void* args[] = {&a, &k};
     // One row of tiles reads each B byte once: non-temporal B copies (8-bit
     // operands on the ring tiles, the batched-decode shapes).  Measured at
     // N = 14336, K = 4096, cold weights: M = 64 on the 64x64 ring 16.6 -> 15.4
@@ -690,31 +776,38 @@ hipError_t launch_t(const GemmArgs& p, hipStream_t stream, int cus) {
     const void* f = reinterpret_cast<const void*>(&gemm_mfma_kernel<ELEM, BL, OUT, SWI, TL>);
     if constexpr (TL::NS == 4 && elem_bytes(ELEM) == 1)
         if (gm == 1) f = reinterpret_cast<const void*>(&gemm_mfma_kernel<ELEM, BL, OUT, SWI, TL, true>);
-    return hipLaunchKernel(f, dim3(grid), dim3(NTHREADS), args, 0, stream);
+    const hipError_t e = hipLaunchKernel(f, dim3(grid), dim3(NTHREADS), args, 0, stream);
+    if (e != hipSuccess || sk.S == 1) return e;
+    if constexpr (!SWI && elem_bytes(ELEM) == 1) {
+        const int64_t mn = static_cast<int64_t>(p.M) * p.N;
+        return hipLaunchKernel(reinterpret_cast<const void*>(&splitk_reduce_kernel<ELEM, OUT>),
+                               dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), args, 0, stream);
+    }
+    return hipErrorInvalidValue;  // not reached: checked before the launch
 }
 
 template <int ELEM, int BL, int OUT, bool SWI = false>
-hipError_t launch_tile(const GemmArgs& p, hipStream_t s, int tile, int cus) {
+hipError_t launch_tile(const GemmArgs& p, hipStream_t s, int tile, int cus, const SplitK& sk) {
     switch (tile) {
-        case MFMA_TILE_128x128: return launch_t<ELEM, BL, OUT, SWI, T128>(p, s, cus);
-        case MFMA_TILE_128x128_RING4: return launch_t<ELEM, BL, OUT, SWI, T128R4>(p, s, cus);
+        case MFMA_TILE_128x128: return launch_t<ELEM, BL, OUT, SWI, T128>(p, s, cus, sk);
+        case MFMA_TILE_128x128_RING4: return launch_t<ELEM, BL, OUT, SWI, T128R4>(p, s, cus, sk);
         case MFMA_TILE_128x64_RING4:
-            if constexpr (!SWI) return launch_t<ELEM, BL, OUT, SWI, T128x64R4>(p, s, cus);
+            if constexpr (!SWI) return launch_t<ELEM, BL, OUT, SWI, T128x64R4>(p, s, cus, sk);
             return hipErrorInvalidValue;
         case MFMA_TILE_64x64_RING4:
-            if constexpr (!SWI) return launch_t<ELEM, BL, OUT, SWI, T64R4>(p, s, cus);
+            if constexpr (!SWI) return launch_t<ELEM, BL, OUT, SWI, T64R4>(p, s, cus, sk);
             return hipErrorInvalidValue;
-        default: return launch_t<ELEM, BL, OUT, SWI, T256>(p, s, cus);
+        default: return launch_t<ELEM, BL, OUT, SWI, T256>(p, s, cus, sk);
     }
 }
 
 template <int ELEM, int BL>
-hipError_t launch_out(const GemmArgs& p, hipStream_t s, int tile, int cus) {
+hipError_t launch_out(const GemmArgs& p, hipStream_t s, int tile, int cus, const SplitK& sk) {
     switch (p.out_dtype) {
-        case FKE_OUT_F32: return launch_tile<ELEM, BL, FKE_OUT_F32>(p, s, tile, cus);
-        case FKE_OUT_BF16: return launch_tile<ELEM, BL, FKE_OUT_BF16>(p, s, tile, cus);
+        case FKE_OUT_F32: return launch_tile<ELEM, BL, FKE_OUT_F32>(p, s, tile, cus, sk);
+        case FKE_OUT_BF16: return launch_tile<ELEM, BL, FKE_OUT_BF16>(p, s, tile, cus, sk);
         default:
-            if constexpr (ELEM == ELEM_I8) return launch_tile<ELEM, BL, FKE_OUT_I32>(p, s, tile, cus);
+            if constexpr (ELEM == ELEM_I8) return launch_tile<ELEM, BL, FKE_OUT_I32>(p, s, tile, cus, sk);
             return hipErrorInvalidValue;
     }
 }
@@ -802,7 +895,9 @@ int mfma_pick_tile(const GemmArgs& p, int cus) {
 // 64x65536x4096 ran 59.9 us, 64x128256x4096 116.7), plus 1 us.  128x128 with two stages: about
 // 1 us per stage per round of two tiles per CU.  256x256: 1.35 us per stage
 // and 11 us per round of tiles.
-double mfma_time_estimate_us(const GemmArgs& p, int cus) {
+namespace {
+
+double mfma_unsplit_estimate_us(const GemmArgs& p, int cus) {
     const double kt = p.K / 128.0;
     const int64_t NO = p.swiglu ? p.N / 2 : p.N;
     auto ring = [&](int64_t bm, int64_t bn) {
@@ -817,34 +912,122 @@ double mfma_time_estimate_us(const GemmArgs& p, int cus) {
         case MFMA_TILE_128x128_RING4: return ring(128, 128);
         case MFMA_TILE_128x128: {
             const int64_t tc = p.swiglu ? 64 : 128;
-            const double t = static_cast<double>((p.M + 127) / 128 * ((NO + tc - 1) / tc));
+            const double t = static_cast<double>((int64_t{p.M} + 127) / 128 * ((NO + tc - 1) / tc));
             return 1.05 * kt + 6.0 * t / cus;
         }
         default: {
             const int64_t tc = p.swiglu ? 128 : 256;
-            const int64_t t = (p.M + 255) / 256 * ((NO + tc - 1) / tc);
+            const int64_t t = (int64_t{p.M} + 255) / 256 * ((NO + tc - 1) / tc);
             return static_cast<double>((t + cus - 1) / cus) * (1.35 * kt + 11.0);
         }
     }
 }
 
-hipError_t launch_mfma(const GemmArgs& p, int elem, hipStream_t s, int tile) {
+constexpr int kSplitMax = 8;                            // splits of one tile's K range
+constexpr int kSplitMinStages = 4;                      // BK stages per split, at least
+constexpr size_t kSplitMaxBytes = size_t{32} << 20;     // partial sums of all splits
+
+// One round of bm x bn ring tiles (count <= CUs), each summing ks_bytes of
+// K, measured on one-round shapes (cold weights, bf16 out): the bytes one CU
+// loads, (bm + bn) * ks_bytes, at 80 GB/s when two or more tile rows share
+// each B panel in L2 and 52 GB/s for one tile row (B [K,N]: 48 GB/s); a K
+// split's items at 55 and 42 GB/s (shorter K ranges, more of them in flight);
+// the weights at 4.2 TB/s, half as much again with two or more tile rows (the
+// rows' workgroups do not share every panel in L2); plus 1 us.  Unsplit
+// 64x64: 64x4096x14336 36.5 us, 128x4096x14336 24.6, 128x8192x28672 80.8;
+// split: 64x4096x14336 20.3 (64x64, 3 splits), 128x8192x28672 65.6 (128x128,
+// 3 splits), 100x1000x14720 10.9 (64x64, 8 splits).
+double ring_round_us(const GemmArgs& p, int bm, int bn, int64_t ks_bytes, bool split) {
+    const int64_t gm = (int64_t{p.M} + bm - 1) / bm;
+    const double rate = split ? (gm >= 2 ? 55.0e3 : 42.0e3)
+                              : (p.b_layout == FKE_B_KN ? 48.0e3 : (gm >= 2 ? 80.0e3 : 52.0e3));
+    const double weights = static_cast<double>(p.N) * p.K * (gm >= 2 ? 1.5 : 1.0) / 4.2e6;
+    return std::max(static_cast<double>(bm + bn) * ks_bytes / rate, weights) + 1.0;
+}
+
+// Time (us) of a K split on ring tiles bm x bn: the first kernel's round, then
+// the partial sums written and read back once at about 4 TB/s, the output
+// written, and 3 us for the second launch.
+double split_estimate_us(const GemmArgs& p, int bm, int bn, int S, int KS) {
+    const double mn = static_cast<double>(p.M) * p.N;
+    return ring_round_us(p, bm, bn, static_cast<int64_t>(KS) * BK, true) + 3.0 +
+           (2.0 * S * mn * 4.0 + mn * (p.out_dtype == FKE_OUT_BF16 ? 2 : 4)) / 4.0e6;
+}
+
+int ring_bm(int tile) { return tile == MFMA_TILE_64x64_RING4 ? 64 : 128; }
+int ring_bn(int tile) { return tile == MFMA_TILE_128x128_RING4 ? 128 : 64; }
+
+}  // namespace
+
+size_t mfma_split_bytes(const GemmArgs& p, int S) {
+    return static_cast<size_t>(S) * static_cast<size_t>(p.M) * static_cast<size_t>(p.N) * 4;
+}
+
+// K split of an 8-bit GEMM with few tiles and a long K: a ring tile whose
+// count, times S, still fits one round of the CUs, each item summing KS of
+// the K stages.  Every ring tile and S = 2..8 (at least four stages a split,
+// at most 32 MiB of partial sums) is priced by split_estimate_us; the best is
+// taken when it is under 0.85 of the unsplit time (ring_round_us for one
+// round of ring tiles).
+MfmaPlan mfma_plan(const GemmArgs& p, int elem, int cus) {
+    MfmaPlan pl{mfma_pick_tile(p, cus), 1, 0};
+    if (p.swiglu || elem_bytes(elem) != 1) return pl;
+    const int KT = p.K / BK;
+    double base = mfma_unsplit_estimate_us(p, cus);
+    if (pl.tile == MFMA_TILE_64x64_RING4 || pl.tile == MFMA_TILE_128x64_RING4 || pl.tile == MFMA_TILE_128x128_RING4) {
+        const int bm = ring_bm(pl.tile), bn = ring_bn(pl.tile);
+        if ((int64_t{p.M} + bm - 1) / bm * ((int64_t{p.N} + bn - 1) / bn) <= cus)
+            base = ring_round_us(p, bm, bn, p.K, false);
+    }
+    double best = 0.85 * base;
+    const struct { int tile, bm, bn; } rings[] = {{MFMA_TILE_64x64_RING4, 64, 64},
+                                                  {MFMA_TILE_128x64_RING4, 128, 64},
+                                                  {MFMA_TILE_128x128_RING4, 128, 128}};
+    for (const auto& r : rings) {
+        const int64_t t = (int64_t{p.M} + r.bm - 1) / r.bm * ((int64_t{p.N} + r.bn - 1) / r.bn);
+        for (int S = 2; S <= kSplitMax && t * S <= cus; ++S) {
+            const int KS = (KT + S - 1) / S;
+            if (KS < kSplitMinStages) break;
+            const int s = (KT + KS - 1) / KS;  // splits that have stages
+            if (mfma_split_bytes(p, s) > kSplitMaxBytes) break;
+            const double e = split_estimate_us(p, r.bm, r.bn, s, KS);
+            if (e < best) {
+                best = e;
+                pl = MfmaPlan{r.tile, s, KS};
+            }
+        }
+    }
+    return pl;
+}
+
+double mfma_time_estimate_us(const GemmArgs& p, int cus) {
+    const MfmaPlan pl = mfma_plan(p, ELEM_I8, cus);
+    if (pl.S == 1) return mfma_unsplit_estimate_us(p, cus);
+    return split_estimate_us(p, ring_bm(pl.tile), ring_bn(pl.tile), pl.S, pl.KS);
+}
+
+hipError_t launch_mfma(const GemmArgs& p, int elem, hipStream_t s, int tile, const SplitK& sk) {
     const int cus = device_cus();
     if (tile == MFMA_TILE_AUTO) tile = mfma_pick_tile(p, cus);
+    if (sk.S < 1 || sk.S > kSplitMax) return hipErrorInvalidValue;
+    if (sk.S > 1) {  // every split has stages: the last starts before K ends
+        if (p.swiglu || elem_bytes(elem) != 1 || sk.part == nullptr || sk.KS < 1) return hipErrorInvalidValue;
+        if (static_cast<int64_t>(sk.S - 1) * sk.KS >= p.K / BK) return hipErrorInvalidValue;
+    }
     if (elem == ELEM_F16 || elem == ELEM_BF16) {
         GemmArgs q = p;
         q.K = 2 * p.K;  // the kernel walks K bytes
-        return elem == ELEM_F16 ? launch_out<ELEM_F16, FKE_B_NK>(q, s, tile, cus)
-                                : launch_out<ELEM_BF16, FKE_B_NK>(q, s, tile, cus);
+        return elem == ELEM_F16 ? launch_out<ELEM_F16, FKE_B_NK>(q, s, tile, cus, sk)
+                                : launch_out<ELEM_BF16, FKE_B_NK>(q, s, tile, cus, sk);
     }
     if (p.swiglu)
-        return p.out_dtype == FKE_OUT_F32 ? launch_tile<ELEM_I8, FKE_B_NK, FKE_OUT_F32, true>(p, s, tile, cus)
-                                          : launch_tile<ELEM_I8, FKE_B_NK, FKE_OUT_BF16, true>(p, s, tile, cus);
+        return p.out_dtype == FKE_OUT_F32 ? launch_tile<ELEM_I8, FKE_B_NK, FKE_OUT_F32, true>(p, s, tile, cus, sk)
+                                          : launch_tile<ELEM_I8, FKE_B_NK, FKE_OUT_BF16, true>(p, s, tile, cus, sk);
     if (elem == ELEM_I8)
-        return p.b_layout == FKE_B_NK ? launch_out<ELEM_I8, FKE_B_NK>(p, s, tile, cus)
-                                      : launch_out<ELEM_I8, FKE_B_KN>(p, s, tile, cus);
-    return p.b_layout == FKE_B_NK ? launch_out<ELEM_F8, FKE_B_NK>(p, s, tile, cus)
-                                  : launch_out<ELEM_F8, FKE_B_KN>(p, s, tile, cus);
+        return p.b_layout == FKE_B_NK ? launch_out<ELEM_I8, FKE_B_NK>(p, s, tile, cus, sk)
+                                      : launch_out<ELEM_I8, FKE_B_KN>(p, s, tile, cus, sk);
+    return p.b_layout == FKE_B_NK ? launch_out<ELEM_F8, FKE_B_NK>(p, s, tile, cus, sk)
+                                  : launch_out<ELEM_F8, FKE_B_KN>(p, s, tile, cus, sk);
 }
 
 }  // namespace fke

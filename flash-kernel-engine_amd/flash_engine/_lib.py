@@ -44,6 +44,7 @@ SIGNATURES = {
     "fke_launch_wmma_gemm_fp16": ([_p, _p, _p, _i, _i, _i, _f, _f, _p], _i),
     "fke_select_path_half": ([_p, _p, _p, _i, _i, _i, _i, _i, _i], _i),
     "fke_select_mfma_tile": ([_i, _i, _i, _i, _i, _i], _i),
+    "fke_select_mfma_split": ([_i, _i, _i, _i, _i, ct.POINTER(ct.c_int)], _i),
     "fke_w8a8_linear_workspace_size": ([_i, _i], ct.c_size_t),
     "fke_w8a8_linear": ([_p, _i, _p, _p, _i, _i, _i, _p, _f, _p, _i, _p, ct.c_size_t, _p], _i),
     "fke_w8a8_linear_noalloc": ([_p, _i, _p, _p, _i, _i, _i, _p, _f, _p, _i, _p], _i),

@@ -10,9 +10,9 @@
  *   - A, B, C, scale and bias pointers are caller-owned DEVICE buffers.  C is
  *     fully overwritten.  The library allocates nothing for them; the one
  *     device memory it allocates itself is the workspace of the B [K,N] decode
- *     (M <= 16) on each stream that runs it (see fke_qgemm_workspace_size),
- *     held until the process ends, and the fke_qgemm_*_ws entry points take
- *     the caller's instead.
+ *     (M <= 16) and of the MFMA GEMM's K split on each stream that runs them
+ *     (see fke_qgemm_workspace_size), held until the process ends, and the
+ *     fke_qgemm_*_ws entry points take the caller's instead.
  *   - All matrices are row-major.  A is [M,K].  B is [N,K] (FKE_B_NK,
  *     K-contiguous per output column) or [K,N] (FKE_B_KN).  C is [M,N].
  *   - The call is asynchronous on `stream` (a hipStream_t; NULL = the null
@@ -140,9 +140,11 @@ int fke_qgemm_f8_on_path(int path, const uint8_t* A, const uint8_t* B, void* C,
  * counterpart: the reference kernels sum all of K in one thread,
  * src/quantized_gemm.cu:29-37, :106-116).  The decode splits K over up to 8
  * workgroups per 512-column block and adds the splits' partial sums in a
- * second kernel, in split order (exact for INT8, deterministic for FP8); the
+ * second kernel, in split order (exact for INT8, deterministic for FP8).  The
+ * MFMA GEMM's K split (fke_select_mfma_split) uses the same workspace.  The
  * partial sums need fke_qgemm_workspace_size(M, N, K, b_layout) bytes of
- * device memory (0 for shapes the decode does not run or does not split).
+ * device memory (0 for shapes that neither the decode nor the MFMA GEMM
+ * splits; the larger of the two needs otherwise).
  * fke_qgemm_i8 / fke_qgemm_f8 use a workspace the library allocates per
  * (device, stream) on first need (not while that stream is being captured
  * into a graph: a capture then runs the decode unsplit, or on the workspace
@@ -305,6 +307,19 @@ int fke_select_path_half(const void* A, const void* B, const void* C, int M, int
  * 0 for the fused SwiGLU GEMM with N = 2I.  Host logic only; launches
  * nothing. */
 int fke_select_mfma_tile(int M, int N, int K, int b_layout, int swiglu, int cus);
+/* The K split FKE_PATH_MFMA takes for an 8-bit GEMM of this shape (INT8 and
+ * FP8, not SwiGLU) on `cus` CUs (<= 0: the current device's): the number of
+ * splits S (1 = unsplit, on fke_select_mfma_tile's tile; -1 for bad
+ * arguments) and, in *tile_path when not NULL, the FKE_PATH_MFMA_* tile it
+ * runs on.  No reference counterpart (the reference has one GEMM launch per
+ * call, src/quantized_gemm.cu:143-164): with few output tiles and a long K,
+ * S ring-tile workgroups per output tile each sum a contiguous 1/S of K, and
+ * a second kernel adds the S partial sums in split order (exact for INT8,
+ * deterministic for FP8) and applies the epilogue.  The partial sums,
+ * S * M * N * 4 bytes, live in the workspace described at
+ * fke_qgemm_workspace_size; without room the GEMM runs unsplit.  Host logic
+ * only; launches nothing. */
+int fke_select_mfma_split(int M, int N, int K, int b_layout, int cus, int* tile_path);
 
 /* Replaces flash_engine::print_device_info (reference include/flash_engine.h:29,
  * src/flash_engine_api.cu:7-27): prints the device's properties to stdout. */

@@ -65,7 +65,7 @@ int main(void) {
     const int dims[] = {1, 2, 3, 15, 16, 17, 63, 64, 65, 127, 128, 129, 512, 513, 2047, 2048, 4095, 4096,
                         4104, 8192, 14336, 65536, 1 << 20, (1 << 20) + 16, 1 << 24, INT_MAX / 2, INT_MAX};
     const int nd = (int)(sizeof dims / sizeof *dims);
-    long n_paths[5] = {0}, n_ws = 0, n_tiles[5] = {0};
+    long n_paths[5] = {0}, n_ws = 0, n_tiles[5] = {0}, n_split = 0;
     for (int a = 0; a < nd; ++a)
         for (int b = 0; b < nd; ++b)
             for (int c = 0; c < nd; ++c)
@@ -87,7 +87,16 @@ int main(void) {
                     /* B [K,N] decode workspace: M*N*4 bytes per split (N rounded to 128), at most 8 splits */
                     const size_t ws = fke_qgemm_workspace_size(M, N, K, lay);
                     const size_t row = (size_t)((N + 127LL) / 128) * 128 * 4 * (size_t)M;
-                    CHECK(ws == 0 || (lay == FKE_B_KN && M <= 16 && ws % row == 0 && ws / row >= 2 && ws / row <= 8));
+                    /* or the MFMA GEMM's K split: S * M * N * 4 bytes, 2 <= S <= 8 */
+                    int tp = -1;
+                    const int S = fke_select_mfma_split(M, N, K, lay, 256, &tp);
+                    CHECK(S >= 1 && S <= 8 && (tp == FKE_PATH_MFMA_256x256 ||
+                                               (tp >= FKE_PATH_MFMA_128x128 && tp <= FKE_PATH_MFMA_64x64_RING4)));
+                    CHECK(S == 1 || tp >= FKE_PATH_MFMA_128x128_RING4);
+                    const size_t split = S > 1 ? (size_t)S * (size_t)M * (size_t)N * 4 : 0;
+                    CHECK(ws == 0 || ws == split ||
+                          (lay == FKE_B_KN && M <= 16 && ws % row == 0 && ws / row >= 2 && ws / row <= 8));
+                    n_split += S > 1;
                     ++n_ws;
                     /* MFMA tile: the narrow rings not for SwiGLU; -1 only for an odd SwiGLU N */
                     for (int sw = 0; sw < 2; ++sw) {
@@ -101,6 +110,8 @@ int main(void) {
                 }
     CHECK(n_paths[FKE_PATH_GEMV + 1] > 0 && n_paths[FKE_PATH_MFMA + 1] > 0 && n_paths[FKE_PATH_GENERIC + 1] > 0);
     for (int t = 0; t < 5; ++t) CHECK(n_tiles[t] > 0);
+    CHECK(n_split > 0);
+    CHECK(fke_select_mfma_split(0, 64, 64, 0, 256, NULL) == -1 && fke_select_mfma_split(64, 64, 64, 2, 256, NULL) == -1);
     CHECK(fke_select_path_i8(NULL, P, P, 8, 8, 8, 0, 0) == -1);
     CHECK(fke_select_path_f8(P, P, P, 8, 8, 8, FKE_OUT_I32, 0) == -1);
     CHECK(fke_status_string(1) != NULL && fke_version() != NULL);

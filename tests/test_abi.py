@@ -2,6 +2,7 @@
 symbol include/fke_qgemm.h declares, rejects bad arguments with
 hipErrorInvalidValue before any HIP call, and dispatches shapes to the
 expected kernel family.  No GPU compute is issued here."""
+import ctypes as ct
 import os
 import re
 import subprocess
@@ -391,6 +392,37 @@ def test_torch_extension_rejects_host_tensors():
 ])
 def test_mfma_tile_choice(M, N, K, layout, swiglu, cus, want):
     assert _lib.lib().fke_select_mfma_tile(M, N, K, layout, swiglu, cus) == want
+
+
+@pytest.mark.parametrize("M,N,K,layout,want_s,want_tile", [
+    (64, 4096, 14336, 0, 4, _lib.PATH_MFMA_64x64_RING4),     # one tile row: 64 tiles, 28 stages a split
+    (100, 1000, 14720, 0, 7, _lib.PATH_MFMA_64x64_RING4),    # 115 stages: 6 splits of 17 and one of 13
+    (200, 2000, 8192, 1, 4, _lib.PATH_MFMA_128x64_RING4),    # B [K,N] (slower unsplit)
+    (128, 8192, 28672, 0, 4, _lib.PATH_MFMA_128x128_RING4),  # 64 tiles of 128x128: one tile row
+    (120, 2000, 28672, 0, 8, _lib.PATH_MFMA_128x64_RING4),
+    (128, 4096, 14336, 0, 1, _lib.PATH_MFMA_64x64_RING4),    # two tile rows share B: unsplit is as fast
+    (200, 2000, 8192, 0, 1, _lib.PATH_MFMA_64x64_RING4),     # the same with B [N,K]
+    (128, 14336, 4096, 0, 1, _lib.PATH_MFMA_128x64_RING4),   # 224 tiles: no room to split
+    (512, 4096, 14336, 0, 1, _lib.PATH_MFMA_128x64_RING4),   # 256 tiles
+    (128, 4096, 384, 0, 1, _lib.PATH_MFMA_64x64_RING4),      # three stages: too short to split
+    (4096, 4096, 4096, 0, 1, _lib.PATH_MFMA_256x256),
+])
+def test_mfma_split_choice(M, N, K, layout, want_s, want_tile):
+    t = ct.c_int(-1)
+    L = _lib.lib()
+    assert L.fke_select_mfma_split(M, N, K, layout, 256, ct.byref(t)) == want_s
+    assert t.value == want_tile
+    assert L.fke_select_mfma_split(M, N, K, layout, 256, None) == want_s
+    if want_s == 1:
+        assert want_tile == L.fke_select_mfma_tile(M, N, K, layout, 0, 256)
+    if not (layout == _lib.B_KN and M <= 16):
+        assert L.fke_qgemm_workspace_size(M, N, K, layout) == (want_s * M * N * 4 if want_s > 1 else 0)
+
+
+def test_mfma_split_rejects_bad_arguments():
+    L = _lib.lib()
+    assert L.fke_select_mfma_split(0, 64, 64, 0, 256, None) == -1
+    assert L.fke_select_mfma_split(64, 64, 64, 2, 256, None) == -1
 
 
 def test_mfma_tile_choice_rejects_bad_arguments():

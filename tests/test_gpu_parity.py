@@ -8,6 +8,7 @@ MFMA family within 2e-2 max-norm relative error of the reference's sequential
 fp32 sum (and bit-exact on the GENERIC family, which keeps that order).
 Every test prints the case it is about to run before touching the GPU.
 """
+import ctypes
 import os
 import subprocess
 
@@ -765,6 +766,89 @@ def test_mfma_few_tile_shapes_full(oracle, dev, M, N, K, out, want):
         assert_same(gpu_i8(A, B, "nk", out, "gemv", sa, sb, bias=bias), ref, f"gemv {M}x{N}x{K}")
 
 
+def mfma_split_of(M, N, K, layout):
+    t = ctypes.c_int(0)
+    S = _lib.lib().fke_select_mfma_split(M, N, K, _lib.B_KN if layout == "kn" else _lib.B_NK, 256,
+                                         ctypes.byref(t))
+    return S, t.value
+
+
+# The automatic MFMA path splits K on these (checked on 256 CUs): a few output
+# tiles with a long K, a split count that does not divide the stages, ragged
+# rows and columns, and both B layouts.
+SPLIT_CASES = [
+    (64, 4096, 14336, "nk"),    # 64 tiles of 64x64, 4 splits of 28 stages
+    (100, 1000, 14720, "nk"),   # 32 tiles of 64x64, 7 splits: 6 of 17 stages and one of 13
+    (200, 2000, 8192, "kn"),    # B [K,N], 64 tiles of 128x64, 4 splits
+    (120, 2000, 28672, "nk"),   # ragged rows and columns, 32 tiles of 128x64, 8 splits
+    (256, 2048, 28672, "nk"),   # 32 tiles of 128x128 over two tile rows, 7 splits
+]
+
+
+@pytest.mark.parametrize("M,N,K,layout", SPLIT_CASES)
+def test_mfma_k_split_int8_exact(oracle, dev, M, N, K, layout):
+    """The K split of the MFMA GEMM (the split items' int32 partial sums added
+    in split order, then the epilogue): int32, bf16 and f32 outputs bit-exact
+    against the oracle, and equal to the unsplit kernel on the same tile."""
+    S, tile = mfma_split_of(M, N, K, layout)
+    say("mfma k split", M, N, K, layout, "splits", S, "tile path", tile)
+    assert S > 1
+    A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 14000 + M, layout=layout)
+    acc = oracle.w8a8_acc(A, B, oracle.B_KN if layout == "kn" else oracle.B_NK, nthreads=NTH)
+    assert_same(gpu_i8(A, B, layout, "i32", path="mfma"), acc, f"split {(M, N, K)} i32")
+    for out in ("bf16", "f32"):
+        ref = oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, out)
+        assert_same(gpu_i8(A, B, layout, out, path="mfma", sa_vec=sa, sb_vec=sb, bias=bias), ref,
+                    f"split {(M, N, K)} {out}")
+    name = {_lib.PATH_MFMA_64x64_RING4: "mfma_64x64_ring4", _lib.PATH_MFMA_128x64_RING4: "mfma_128x64_ring4",
+            _lib.PATH_MFMA_128x128_RING4: "mfma_128x128_ring4"}[tile]
+    ref = oracle_out(oracle, acc, None, None, 0.5, 0.25, None, "f32")
+    assert_same(gpu_i8(A, B, layout, "f32", path=name, sa=0.5, sb=0.25), ref, f"unsplit {name} {(M, N, K)}")
+    assert_same(gpu_i8(A, B, layout, "f32", path="mfma", sa=0.5, sb=0.25), ref, f"split scalar scales {(M, N, K)}")
+
+
+def test_mfma_k_split_workspace(oracle, dev):
+    """fke_qgemm_i8_ws on a split shape: the caller's workspace when it holds the
+    partial sums (fke_qgemm_workspace_size bytes), unsplit when it is too small,
+    NULL or unaligned; every result bit-exact."""
+    M, N, K = 64, 4096, 14336
+    S, _ = mfma_split_of(M, N, K, "nk")
+    need = _lib.lib().fke_qgemm_workspace_size(M, N, K, _lib.B_NK)
+    say("mfma k split workspace", S, need)
+    assert S > 1 and need == S * M * N * 4
+    A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 15000)
+    acc = oracle.w8a8_acc(A, B, nthreads=NTH)
+    ref = oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, "bf16")
+    Ad, Bd, sad, sbd, biasd = dev_t(A), dev_t(B), dev_t(sa), dev_t(sb), dev_t(bias)
+    ws = torch.empty(need + 64, dtype=torch.uint8, device=dev)
+    for ptr, nbytes in ((ws.data_ptr(), need), (ws.data_ptr(), need - 4), (None, 0), (ws.data_ptr() + 4, need)):
+        C = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        st = _lib.lib().fke_qgemm_i8_ws(Ad.data_ptr(), Bd.data_ptr(), C.data_ptr(), M, N, K, sad.data_ptr(),
+                                        sbd.data_ptr(), 1.0, 1.0, biasd.data_ptr(), _lib.OUT_BF16, _lib.B_NK,
+                                        ptr, nbytes, torch.cuda.current_stream().cuda_stream)
+        _lib.check(st, "fke_qgemm_i8_ws")
+        torch.cuda.synchronize()
+        assert_same(host(C), ref, f"workspace {nbytes} bytes at offset {0 if ptr is None else ptr - ws.data_ptr()}")
+
+
+@pytest.mark.parametrize("layout", ["nk", "kn"])
+def test_mfma_k_split_fp8(oracle, dev, layout):
+    """FP8 on a split shape: within the FP8 bounds of the reference's sequential
+    sum, and the same bits on every call (the partial sums are added in split
+    order)."""
+    M, N, K = 64, 4096, 14336
+    S, _ = mfma_split_of(M, N, K, layout)
+    say("mfma k split fp8", layout, S)
+    assert S > 1
+    A, B, sa, sb = f8_inputs(oracle, M, N, K, 16000, layout)
+    bias = oracle.gen_f32_normal((N,), 16001, 0.0, 0.02)
+    ref = oracle.f8_gemm(A, B, sa, sb, bias=bias, b_layout=oracle.B_KN if layout == "kn" else oracle.B_NK,
+                         nthreads=NTH)
+    got = gpu_f8(A, B, sa, sb, layout, "f32", "mfma", bias=bias)
+    assert_fp8_close(got, ref, "f32", f"split {layout}")
+    assert_same(gpu_f8(A, B, sa, sb, layout, "f32", "mfma", bias=bias), got, "split fp8 repeat")
+
+
 # ---------------------------------------------------------------------- FP8
 
 def f8_inputs(oracle, M, N, K, seed, layout="kn", with_nan_codes=False):
@@ -897,7 +981,8 @@ EXTREME_CASES = (
      (1, 4096, 8192, "kn", "gemv"), (16, 4096, 8192, "kn", "gemv"),
      (37, 50, 8192, "nk", "generic"), (37, 48, 8192, "kn", "generic")]
     + [(300, 528, 8192, lay, "mfma_" + t) for lay in ("nk", "kn")
-       for t in ("256x256", "128x128", "128x128_ring4", "128x64_ring4", "64x64_ring4")])
+       for t in ("256x256", "128x128", "128x128_ring4", "128x64_ring4", "64x64_ring4")]
+    + [(300, 528, 8192, lay, "mfma") for lay in ("nk", "kn")])  # the automatic tile: a K split
 
 
 def extreme_i8(M, N, K, layout, seed):
