@@ -204,6 +204,12 @@ __global__ __launch_bounds__(ROWS_WAVES * 64) void gemv_rows_kernel(GemmArgs p) 
         sbn[q] = p.scale_b ? p.scale_b[row_of(q)] : p.sb;
         biasn[q] = p.bias ? p.bias[row_of(q)] : 0.0f;
     }
+    // Activation scales too, before the stream: loaded after it, their
+    // latency would sit between each wave's last sum and its store.  Rows
+    // m >= M of the MT-row template read row 0 (never stored).
+    float sam[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) sam[m] = p.scale_a ? p.scale_a[m < M ? m : 0] : p.sa;
     int32_t acc[NB][MT];
 #pragma unroll
     for (int q = 0; q < NB; ++q)
@@ -250,11 +256,10 @@ __global__ __launch_bounds__(ROWS_WAVES * 64) void gemv_rows_kernel(GemmArgs p) 
     // lane m*NB + q stores output (m, NB*n + q).
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
-        const float sam = p.scale_a ? p.scale_a[m] : p.sa;
         float y[NB];
 #pragma unroll
         for (int q = 0; q < NB; ++q) {
-            const float sc = sam * sbn[q];
+            const float sc = sam[m] * sbn[q];
             y[q] = p.bias ? __builtin_fmaf(static_cast<float>(tot[q][m]), sc, biasn[q])
                           : static_cast<float>(tot[q][m]) * sc;
         }
