@@ -6,13 +6,12 @@
 // tested) without a GPU.  Otherwise the return value is the status of this
 // call's hipLaunchKernel (the reference returned cudaGetLastError() after its
 // launch, src/quantized_gemm.cu:74,138, which could also surface an earlier
-// sticky error).  No state is kept between calls, apart from the device
-// scratch of fke_w8a8_linear_noalloc (and its per-device address, set once)
-// and the per-stream workspaces of the [K,N] decode's K splits (below).
+// sticky error).  No call path allocates device memory.  State kept between
+// calls: the per-device addresses of the two static device arrays below (set
+// once), the stream-to-slot table of the K splits' pool, and the event and
+// last stream that order fke_w8a8_linear_noalloc calls across streams.
 #include <cstdio>
 #include <mutex>
-#include <utility>
-#include <vector>
 
 #include "fke_internal.h"
 
@@ -23,85 +22,144 @@
 // address on the current device comes from hipGetSymbolAddress (below).
 static __device__ __align__(256) uint8_t scratch[FKE_W8A8_NOALLOC_SCRATCH_BYTES];
 
+// Partial sums of the K splits (the [K,N] decode's and the MFMA GEMM's),
+// FKE_SPLIT_SLOTS slots of FKE_SPLIT_SLOT_BYTES per GPU, reserved with the
+// code object: no call path allocates device memory.  A stream gets a slot
+// the first time one of its calls splits K and keeps it for the life of the
+// process: calls on one stream run in order and share it, calls on different
+// streams never do.  No split plan needs more than one slot.
+static __device__ __align__(256) uint8_t split_pool[size_t{FKE_SPLIT_SLOTS} * FKE_SPLIT_SLOT_BYTES];
+
 namespace {
-
-// Per-device address of `scratch`, looked up once per device with that device
-// current (the first allocation-free call on it) and immutable afterwards.
-constexpr int kMaxDevices = 64;
-std::once_flag g_scratch_once[kMaxDevices];
-void* g_scratch_ptr[kMaxDevices];
-hipError_t g_scratch_status[kMaxDevices];
-
-hipError_t scratch_of_device(int dev, void** out) {
-    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
-    std::call_once(g_scratch_once[dev], [dev] {
-        void* ptr = nullptr;
-        g_scratch_status[dev] = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-        g_scratch_ptr[dev] = ptr;
-    });
-    if (g_scratch_status[dev] != hipSuccess) return g_scratch_status[dev];
-    *out = g_scratch_ptr[dev];
-    return hipSuccess;
-}
 
 using fke::GemmArgs;
 
-// Workspaces of the [K,N] decode's K splits (the partial sums its second
-// kernel adds), one per (device, stream): calls on one stream run in order,
-// so they can share one; calls on different streams never do.  Allocated the
-// first time a stream needs one and then held until the process ends.  A
-// stream that is being captured into a graph gets no new allocation: it uses
-// what it already has, and the decode runs with fewer splits (or unsplit)
-// when that is too small or absent.  A workspace outgrown by a larger shape
-// is replaced, and the old one kept (a launch queued on it may not have run
-// yet).
-struct KnWorkspace {
+constexpr int kMaxDevices = 64;
+
+// Per-device set-up, done once per device with that device current (the
+// first call on it that needs it) and immutable afterwards: the addresses of
+// `scratch` and `split_pool` on that device, and the event that orders
+// fke_w8a8_linear_noalloc calls across streams.
+struct DeviceSetup {
+    std::once_flag once;
+    hipError_t status = hipSuccess;
+    uint8_t* scratch = nullptr;
+    uint8_t* pool = nullptr;
+    hipEvent_t noalloc_done = nullptr;
+};
+DeviceSetup g_dev[kMaxDevices];
+
+hipError_t device_setup(int dev, DeviceSetup** out) {
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    DeviceSetup& d = g_dev[dev];
+    std::call_once(d.once, [&d] {
+        void* a = nullptr;
+        void* b = nullptr;
+        d.status = hipGetSymbolAddress(&a, HIP_SYMBOL(scratch));
+        if (d.status == hipSuccess) d.status = hipGetSymbolAddress(&b, HIP_SYMBOL(split_pool));
+        if (d.status == hipSuccess) d.status = hipEventCreateWithFlags(&d.noalloc_done, hipEventDisableTiming);
+        d.scratch = static_cast<uint8_t*>(a);
+        d.pool = static_cast<uint8_t*>(b);
+    });
+    if (d.status != hipSuccess) return d.status;
+    *out = &d;
+    return hipSuccess;
+}
+
+// The current device, and a check that stream `s` belongs to it (device
+// memory looked up here must be the copy on the stream's device).
+hipError_t current_device_of(hipStream_t s, int* dev) {
+    hipError_t st = hipGetDevice(dev);
+    if (st != hipSuccess) return st;
+    if (s && s != hipStreamPerThread) {
+        hipDevice_t sdev = 0;
+        st = hipStreamGetDevice(s, &sdev);
+        if (st != hipSuccess) return st;
+        if (sdev != *dev) return hipErrorInvalidValue;
+    }
+    return hipSuccess;
+}
+
+// Device memory for a K split's partial sums.
+struct Workspace {
     void* ptr = nullptr;
     size_t bytes = 0;
 };
-constexpr size_t kKnWsMinBytes = size_t{8} << 20;  // covers M = 16 at N = 14336 (7.3 MiB)
-constexpr size_t kKnWsMaxStreams = 64;              // beyond this many streams: unsplit
-std::mutex g_kn_mu;
-std::vector<std::pair<std::pair<int, hipStream_t>, KnWorkspace>> g_kn_ws;
-std::vector<void*> g_kn_retired;
 
-KnWorkspace kn_workspace(hipStream_t s, size_t need) {
-    if (need == 0) return {};
+// Slot table of split_pool: slot i of device d belongs to g_slot_stream[d][i].
+std::mutex g_slot_mu;
+hipStream_t g_slot_stream[kMaxDevices][FKE_SPLIT_SLOTS];
+int g_slot_count[kMaxDevices];
+
+// The pool slot of stream `s` on the current device, assigned on first use.
+// Empty (the call then runs unsplit) when every slot belongs to another
+// stream, for hipStreamPerThread (one handle for many streams) and for a
+// stream of another device.  Under graph capture the capturing stream's slot
+// is used like any other: the graph's kernels keep its address.
+Workspace stream_slot(hipStream_t s) {
+    if (s == hipStreamPerThread) return {};
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return {};
-    if (s) {  // the workspace must live on the stream's device, which must be current
-        hipDevice_t sdev = 0;
-        if (hipStreamGetDevice(s, &sdev) != hipSuccess || sdev != dev) return {};
+    DeviceSetup* d = nullptr;
+    if (current_device_of(s, &dev) != hipSuccess || device_setup(dev, &d) != hipSuccess) return {};
+    std::lock_guard<std::mutex> lock(g_slot_mu);
+    int i = 0;
+    while (i < g_slot_count[dev] && g_slot_stream[dev][i] != s) ++i;
+    if (i == g_slot_count[dev]) {
+        if (i == FKE_SPLIT_SLOTS) return {};
+        g_slot_stream[dev][i] = s;
+        g_slot_count[dev] = i + 1;
     }
-    std::lock_guard<std::mutex> lock(g_kn_mu);
-    KnWorkspace* have = nullptr;
-    for (auto& e : g_kn_ws)
-        if (e.first.first == dev && e.first.second == s) have = &e.second;
-    if (have && have->bytes >= need) return *have;
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
-        return have ? *have : KnWorkspace{};
-    if (!have && g_kn_ws.size() >= kKnWsMaxStreams) return {};
-    KnWorkspace ws;
-    ws.bytes = need > kKnWsMinBytes ? need : kKnWsMinBytes;
-    if (hipMalloc(&ws.ptr, ws.bytes) != hipSuccess) return have ? *have : KnWorkspace{};
-    if (have) {
-        g_kn_retired.push_back(have->ptr);
-        *have = ws;
-    } else {
-        g_kn_ws.push_back({{dev, s}, ws});
-    }
-    return ws;
+    Workspace w;
+    w.ptr = d->pool + static_cast<size_t>(i) * FKE_SPLIT_SLOT_BYTES;
+    w.bytes = FKE_SPLIT_SLOT_BYTES;
+    return w;
 }
 
-// The [K,N] decode on the caller's workspace (`given`), or else on the
-// stream's own.
-hipError_t run_kn(const GemmArgs& p, int elem, hipStream_t s, const KnWorkspace* given) {
-    const KnWorkspace ws = given ? *given : kn_workspace(s, fke::gemv_kn_workspace_bytes(p));
+// Where a call's K-split partial sums go.  POOL: the stream's slot (the
+// plain entry points).  CALLER: the caller's workspace exactly as given (a
+// NULL, short or unaligned one gives fewer splits or none: the _ws entry
+// points, and the allocation-free linear's scratch).  CALLER_OR_POOL: the
+// caller's when it holds the whole plan, else the stream's slot
+// (fke_w8a8_linear's workspace past its codes and scales).
+enum WsMode { WS_POOL, WS_CALLER, WS_CALLER_OR_POOL };
+struct WsChoice {
+    WsMode mode = WS_POOL;
+    Workspace caller;
+};
+
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
+
+Workspace split_workspace(hipStream_t s, size_t need, const WsChoice& wc) {
+    if (need == 0) return {};
+    if (wc.mode == WS_CALLER) return wc.caller;
+    if (wc.mode == WS_CALLER_OR_POOL && wc.caller.ptr && wc.caller.bytes >= need && aligned16(wc.caller.ptr))
+        return wc.caller;
+    return stream_slot(s);
+}
+
+// The caller's workspace of a _ws entry point, taken as given.
+WsChoice caller_ws(void* workspace, size_t workspace_bytes) {
+    WsChoice wc;
+    wc.mode = WS_CALLER;
+    wc.caller.ptr = workspace;
+    wc.caller.bytes = workspace ? workspace_bytes : 0;
+    return wc;
+}
+
+// Cross-stream order of fke_w8a8_linear_noalloc calls on each device: the
+// stream of the last call made outside graph capture, and whether it
+// recorded DeviceSetup::noalloc_done.
+std::mutex g_noalloc_mu[kMaxDevices];
+hipStream_t g_noalloc_last[kMaxDevices];
+bool g_noalloc_recorded[kMaxDevices];
+
+// The [K,N] decode, split over the workspace `wc` gives.
+hipError_t run_kn(const GemmArgs& p, int elem, hipStream_t s, const WsChoice& wc) {
+    const Workspace ws = split_workspace(s, fke::gemv_kn_workspace_bytes(p), wc);
     return fke::launch_gemv_kn(p, elem, fke::gemv_kn_plan(p, ws.ptr, ws.bytes), s);
 }
 
-int run_i8(int path, const GemmArgs& p, void* stream, const KnWorkspace* ws = nullptr);
+int run_i8(int path, const GemmArgs& p, void* stream, const WsChoice& wc = WsChoice{});
 
 bool common_args_ok(const void* A, const void* B, const void* C, int M, int N, int K,
                     int b_layout) {
@@ -155,10 +213,10 @@ size_t w8a8_ws_bytes(int M, int K) { return w8a8_ws_scale_offset(M, K) + 4 * sta
 // GEMM on the int8 codes with A = X: the quantiser writes X's codes and row
 // scales into the workspace, then the GEMM reads them there.  The workspace
 // past the row scales (from the next 256-byte boundary) holds a K split's
-// partial sums when it is large enough; with `may_alloc` an empty remainder
-// lets the split use the stream's own workspace instead.
+// partial sums: as a whole plan's, or else the stream's pool slot takes them
+// (`mode` WS_CALLER_OR_POOL), or as many splits as it holds (WS_CALLER).
 int run_w8a8_from_float(GemmArgs p, int in_dtype, void* workspace, size_t workspace_bytes, void* stream,
-                        bool may_alloc = true) {
+                        WsMode mode) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (!workspace || workspace_bytes < w8a8_ws_bytes(p.M, p.K)) return hipErrorInvalidValue;
     int8_t* Q = static_cast<int8_t*>(workspace);
@@ -168,12 +226,13 @@ int run_w8a8_from_float(GemmArgs p, int in_dtype, void* workspace, size_t worksp
     p.A = Q;
     p.scale_a = S;
     const size_t used = (w8a8_ws_bytes(p.M, p.K) + 255) & ~static_cast<size_t>(255);
-    KnWorkspace rest;
+    WsChoice wc;
+    wc.mode = mode;
     if (workspace_bytes > used) {
-        rest.ptr = static_cast<char*>(workspace) + used;
-        rest.bytes = workspace_bytes - used;
+        wc.caller.ptr = static_cast<char*>(workspace) + used;
+        wc.caller.bytes = workspace_bytes - used;
     }
-    return run_i8(FKE_PATH_AUTO, p, stream, rest.ptr || !may_alloc ? &rest : nullptr);
+    return run_i8(FKE_PATH_AUTO, p, stream, wc);
 }
 
 // SwiGLU GEMM: B is the merged [2I, K] weight; the kernels see N = 2I.
@@ -226,29 +285,29 @@ int mfma_tile_of_path(int path, const GemmArgs& p) {
 
 // The MFMA GEMM with the tile `path` names, after its shape check.  The
 // automatic tile also takes the K split the plan gives (8-bit shapes with few
-// tiles and a long K), on the caller's workspace (`given`) or else on the
-// stream's own; unsplit, on the tile rule's tile, when that is too small.
-int run_mfma(int path, const GemmArgs& p, int elem, hipStream_t s, const KnWorkspace* given = nullptr) {
+// tiles and a long K), on the workspace `wc` gives; unsplit, on the tile
+// rule's tile, when that does not hold the partial sums.
+int run_mfma(int path, const GemmArgs& p, int elem, hipStream_t s, const WsChoice& wc = WsChoice{}) {
     const int tile = mfma_tile_of_path(path, p);
     if (tile < 0 || !fke::mfma_supports(p, elem)) return hipErrorInvalidValue;
     if (tile == fke::MFMA_TILE_AUTO) {
         const fke::MfmaPlan pl = fke::mfma_plan(p, elem, fke::device_cus());
         if (pl.S > 1) {
             const size_t need = fke::mfma_split_bytes(p, pl.S);
-            const KnWorkspace ws = given ? *given : kn_workspace(s, need);
-            if (ws.ptr && ws.bytes >= need && (reinterpret_cast<uintptr_t>(ws.ptr) & 15) == 0)
+            const Workspace ws = split_workspace(s, need, wc);
+            if (ws.ptr && ws.bytes >= need && aligned16(ws.ptr))
                 return fke::launch_mfma(p, elem, s, pl.tile, fke::SplitK{pl.S, pl.KS, ws.ptr});
         }
     }
     return fke::launch_mfma(p, elem, s, tile);
 }
 
-int run_i8(int path, const GemmArgs& p, void* stream, const KnWorkspace* ws) {
+int run_i8(int path, const GemmArgs& p, void* stream, const WsChoice& wc) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (path == FKE_PATH_AUTO) path = pick_i8(p);
     switch (path) {
         case FKE_PATH_GEMV:
-            if (fke::gemv_kn_supports(p, fke::ELEM_I8)) return run_kn(p, fke::ELEM_I8, s, ws);
+            if (fke::gemv_kn_supports(p, fke::ELEM_I8)) return run_kn(p, fke::ELEM_I8, s, wc);
             if (!fke::gemv_i8_supports(p)) return hipErrorInvalidValue;
             return fke::launch_gemv_i8(p, s);
         case FKE_PATH_MFMA:
@@ -256,7 +315,7 @@ int run_i8(int path, const GemmArgs& p, void* stream, const KnWorkspace* ws) {
         case FKE_PATH_MFMA_128x128:
         case FKE_PATH_MFMA_128x128_RING4:
         case FKE_PATH_MFMA_128x64_RING4:
-        case FKE_PATH_MFMA_64x64_RING4: return run_mfma(path, p, fke::ELEM_I8, s, ws);
+        case FKE_PATH_MFMA_64x64_RING4: return run_mfma(path, p, fke::ELEM_I8, s, wc);
         case FKE_PATH_GENERIC: return fke::launch_generic(p, fke::ELEM_I8, s);
         case FKE_PATH_GEMV_DOT:
             if (!fke::gemv_dot_supports(p)) return hipErrorInvalidValue;
@@ -293,12 +352,12 @@ int run_half(int path, const GemmArgs& p, int elem, void* stream) {
     }
 }
 
-int run_f8(int path, const GemmArgs& p, void* stream, const KnWorkspace* ws = nullptr) {
+int run_f8(int path, const GemmArgs& p, void* stream, const WsChoice& wc = WsChoice{}) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (path == FKE_PATH_AUTO) path = pick_f8(p);
     switch (path) {
         case FKE_PATH_GEMV:
-            if (fke::gemv_kn_supports(p, fke::ELEM_F8)) return run_kn(p, fke::ELEM_F8, s, ws);
+            if (fke::gemv_kn_supports(p, fke::ELEM_F8)) return run_kn(p, fke::ELEM_F8, s, wc);
             if (!fke::gemv_f8_supports(p)) return hipErrorInvalidValue;
             return fke::launch_gemv_f8(p, s);
         case FKE_PATH_MFMA:
@@ -306,7 +365,7 @@ int run_f8(int path, const GemmArgs& p, void* stream, const KnWorkspace* ws = nu
         case FKE_PATH_MFMA_128x128:
         case FKE_PATH_MFMA_128x128_RING4:
         case FKE_PATH_MFMA_128x64_RING4:
-        case FKE_PATH_MFMA_64x64_RING4: return run_mfma(path, p, fke::ELEM_F8, s, ws);
+        case FKE_PATH_MFMA_64x64_RING4: return run_mfma(path, p, fke::ELEM_F8, s, wc);
         case FKE_PATH_GENERIC: return fke::launch_generic(p, fke::ELEM_F8, s);
         default: return hipErrorInvalidValue;
     }
@@ -357,26 +416,27 @@ size_t fke_qgemm_workspace_size(int M, int N, int K, int b_layout) {
     return kn > split ? kn : split;
 }
 
+int fke_split_slots_in_use(void) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return -1;
+    std::lock_guard<std::mutex> lock(g_slot_mu);
+    return g_slot_count[dev];
+}
+
 int fke_qgemm_i8_ws(const int8_t* A, const int8_t* B, void* C, int M, int N, int K, const float* scale_a,
                     const float* scale_b, float sa, float sb, const float* bias, int out_dtype, int b_layout,
                     void* workspace, size_t workspace_bytes, void* stream) {
     if (!i8_args_ok(A, B, C, M, N, K, out_dtype, b_layout)) return hipErrorInvalidValue;
-    KnWorkspace ws;
-    ws.ptr = workspace;
-    ws.bytes = workspace ? workspace_bytes : 0;
     return run_i8(FKE_PATH_AUTO, make_args(A, B, C, M, N, K, scale_a, scale_b, sa, sb, bias, out_dtype, b_layout),
-                  stream, &ws);
+                  stream, caller_ws(workspace, workspace_bytes));
 }
 
 int fke_qgemm_f8_ws(const uint8_t* A, const uint8_t* B, void* C, int M, int N, int K, float sa, float sb,
                     const float* bias, int out_dtype, int b_layout, void* workspace, size_t workspace_bytes,
                     void* stream) {
     if (!f8_args_ok(A, B, C, M, N, K, out_dtype, b_layout)) return hipErrorInvalidValue;
-    KnWorkspace ws;
-    ws.ptr = workspace;
-    ws.bytes = workspace ? workspace_bytes : 0;
     return run_f8(FKE_PATH_AUTO, make_args(A, B, C, M, N, K, nullptr, nullptr, sa, sb, bias, out_dtype, b_layout),
-                  stream, &ws);
+                  stream, caller_ws(workspace, workspace_bytes));
 }
 
 int fke_qgemm_i8_swiglu_on_path(int path, const int8_t* A, const int8_t* W, void* H, int M, int I, int K,
@@ -412,7 +472,7 @@ int fke_w8a8_linear(const void* X, int in_dtype, const int8_t* W, void* Y, int M
     if (in_dtype != FKE_IN_F32 && in_dtype != FKE_IN_BF16) return hipErrorInvalidValue;
     if (out_dtype != FKE_OUT_F32 && out_dtype != FKE_OUT_BF16) return hipErrorInvalidValue;
     return run_w8a8_from_float(make_args(X, W, Y, M, N, K, nullptr, w_scale, 1.0f, sb, bias, out_dtype, FKE_B_NK),
-                               in_dtype, workspace, workspace_bytes, stream);
+                               in_dtype, workspace, workspace_bytes, stream, WS_CALLER_OR_POOL);
 }
 
 int fke_w8a8_linear_noalloc(const void* X, int in_dtype, const int8_t* W, void* Y, int M, int N, int K,
@@ -423,20 +483,36 @@ int fke_w8a8_linear_noalloc(const void* X, int in_dtype, const int8_t* W, void* 
     if (w8a8_ws_bytes(M, K) > FKE_W8A8_NOALLOC_SCRATCH_BYTES) return hipErrorInvalidValue;
     // The scratch must be the copy on the stream's device, looked up with
     // that device current: a stream of another device is refused.
+    hipStream_t s = static_cast<hipStream_t>(stream);
     int dev = 0;
-    hipError_t st = hipGetDevice(&dev);
+    hipError_t st = current_device_of(s, &dev);
     if (st != hipSuccess) return st;
-    if (stream) {
-        hipDevice_t sdev = 0;
-        st = hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev);
+    DeviceSetup* d = nullptr;
+    st = device_setup(dev, &d);
+    if (st != hipSuccess) return st;
+    // Calls made outside graph capture are ordered on the device's event: a
+    // call on another stream than the last one's (or on hipStreamPerThread,
+    // whose one handle names a stream per host thread) first waits for the
+    // work queued before that event was recorded, and every such call
+    // records it after its own launches.  Under capture neither happens.
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    st = hipStreamIsCapturing(s, &cs);
+    if (st != hipSuccess) return st;
+    const bool eager = cs == hipStreamCaptureStatusNone;
+    std::lock_guard<std::mutex> lock(g_noalloc_mu[dev]);
+    if (eager && g_noalloc_recorded[dev] && (g_noalloc_last[dev] != s || s == hipStreamPerThread)) {
+        st = hipStreamWaitEvent(s, d->noalloc_done, 0);
         if (st != hipSuccess) return st;
-        if (sdev != dev) return hipErrorInvalidValue;
     }
-    void* ptr = nullptr;
-    st = scratch_of_device(dev, &ptr);
+    st = static_cast<hipError_t>(
+        run_w8a8_from_float(make_args(X, W, Y, M, N, K, nullptr, w_scale, 1.0f, sb, bias, out_dtype, FKE_B_NK),
+                            in_dtype, d->scratch, FKE_W8A8_NOALLOC_SCRATCH_BYTES, stream, WS_CALLER));
+    if (st != hipSuccess || !eager) return st;
+    st = hipEventRecord(d->noalloc_done, s);
     if (st != hipSuccess) return st;
-    return run_w8a8_from_float(make_args(X, W, Y, M, N, K, nullptr, w_scale, 1.0f, sb, bias, out_dtype, FKE_B_NK),
-                               in_dtype, ptr, FKE_W8A8_NOALLOC_SCRATCH_BYTES, stream, false);
+    g_noalloc_last[dev] = s;
+    g_noalloc_recorded[dev] = true;
+    return hipSuccess;
 }
 
 int fke_w8a8_swiglu_linear(const void* X, int in_dtype, const int8_t* W, void* H, int M, int I, int K,
@@ -445,7 +521,7 @@ int fke_w8a8_swiglu_linear(const void* X, int in_dtype, const int8_t* W, void* H
     if (!swiglu_args_ok(X, W, H, M, I, K, out_dtype)) return hipErrorInvalidValue;
     if (in_dtype != FKE_IN_F32 && in_dtype != FKE_IN_BF16) return hipErrorInvalidValue;
     return run_w8a8_from_float(make_swiglu_args(X, W, H, M, I, K, nullptr, w_scale, 1.0f, sb, bias, out_dtype),
-                               in_dtype, workspace, workspace_bytes, stream);
+                               in_dtype, workspace, workspace_bytes, stream, WS_CALLER_OR_POOL);
 }
 
 int fke_swiglu(const void* gate, const void* up, void* out, int64_t n, int dtype, void* stream) {

@@ -43,6 +43,7 @@
 #include "fke_internal.h"
 
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 namespace fke {
@@ -814,11 +815,15 @@ hipError_t launch_out(const GemmArgs& p, hipStream_t s, int tile, int cus, const
 
 }  // namespace
 
+// Read once per device and kept (0: not read yet).
 int device_cus() {
+    static std::atomic<int> known[64];
     int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < NXCD)
-        cus = 256;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    if (dev >= 0 && dev < 64 && (cus = known[dev].load(std::memory_order_relaxed)) > 0) return cus;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < NXCD)
+        return 256;
+    if (dev >= 0 && dev < 64) known[dev].store(cus, std::memory_order_relaxed);
     return cus;
 }
 
@@ -925,7 +930,7 @@ double mfma_unsplit_estimate_us(const GemmArgs& p, int cus) {
 
 constexpr int kSplitMax = 8;                            // splits of one tile's K range
 constexpr int kSplitMinStages = 4;                      // BK stages per split, at least
-constexpr size_t kSplitMaxBytes = size_t{32} << 20;     // partial sums of all splits
+constexpr size_t kSplitMaxBytes = FKE_SPLIT_SLOT_BYTES; // partial sums of all splits: one split-pool slot
 
 // One round of bm x bn ring tiles (count <= CUs), each summing ks_bytes of
 // K, measured on one-round shapes (cold weights, bf16 out): the bytes one CU

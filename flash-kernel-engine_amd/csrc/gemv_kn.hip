@@ -729,15 +729,17 @@ static size_t kn_ws_bytes(int M, int N, int S) {
     return static_cast<size_t>((N + KS_W - 1) / KS_W) * static_cast<size_t>(S) * static_cast<size_t>(M) * KS_W * 4;
 }
 
-// K splits: as many as fill the CUs with one 512-column workgroup each
-// (kCUs; S <= 8, at least one 128-row piece per split, and no more than a
-// workspace of ws_bytes holds), with no empty split.  S = 1: the full kernel.
-// Past kCUs / 2 blocks (N > 65536) the workgroups take several rounds, and
+// K splits: as many as fill the device's CUs with one 512-column workgroup
+// each (S <= 8, at least one 128-row piece per split, and no more than a
+// workspace of ws_bytes, or a split-pool slot, holds), with no empty split.
+// S = 1: the full kernel.
+// Past CUs / 2 blocks (N > 65536 on 256 CUs) the workgroups take several rounds, and
 // S in 2..4 is the one with the fewest rounds per split (ties: the smaller):
 // at N = 81920 / 98304 / 128256, K = 4096, M = 1, S = 3 / 4 / 2 ran 54 / 64 /
 // 79 us against 88 / 107 / 108 us for the full kernel.
 static void kn_splits(const GemmArgs& p, size_t ws_bytes, int* S_out, int* PS_out) {
-    constexpr int kCUs = 256;
+    const int kCUs = device_cus();
+    if (ws_bytes > FKE_SPLIT_SLOT_BYTES) ws_bytes = FKE_SPLIT_SLOT_BYTES;
     const int P = (p.K + KS_ROWS - 1) / KS_ROWS;
     const int nblk = (p.N + 4 * KS_W - 1) / (4 * KS_W);
     int S = kCUs / nblk;

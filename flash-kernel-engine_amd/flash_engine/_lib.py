@@ -21,6 +21,7 @@ PATH_MFMA_128x64_RING4, PATH_MFMA_64x64_RING4 = 8, 9
 IN_F32, IN_BF16, IN_F16 = 0, 1, 2
 HIP_SUCCESS, HIP_ERROR_INVALID_VALUE = 0, 1
 W8A8_NOALLOC_SCRATCH_BYTES = 32 << 20  # FKE_W8A8_NOALLOC_SCRATCH_BYTES
+SPLIT_SLOTS, SPLIT_SLOT_BYTES = 16, 16 << 20  # FKE_SPLIT_SLOTS, FKE_SPLIT_SLOT_BYTES
 
 # Every exported symbol with its (argtypes, restype).
 _p, _i, _f = ct.c_void_p, ct.c_int, ct.c_float
@@ -32,6 +33,7 @@ SIGNATURES = {
     "fke_qgemm_f8": ([_p, _p, _p, _i, _i, _i, _f, _f, _p, _i, _i, _p], _i),
     "fke_qgemm_f8_on_path": ([_i, _p, _p, _p, _i, _i, _i, _f, _f, _p, _i, _i, _p], _i),
     "fke_qgemm_workspace_size": ([_i, _i, _i, _i], ct.c_size_t),
+    "fke_split_slots_in_use": ([], _i),
     "fke_qgemm_i8_ws": ([_p, _p, _p, _i, _i, _i, _p, _p, _f, _f, _p, _i, _i, _p, ct.c_size_t, _p], _i),
     "fke_qgemm_f8_ws": ([_p, _p, _p, _i, _i, _i, _f, _f, _p, _i, _i, _p, ct.c_size_t, _p], _i),
     "fke_quantize_rows_i8": ([_p, _i, _i, _i, _p, _p, _p], _i),

@@ -8,20 +8,21 @@
  * Conventions shared by all GEMM entry points (reference:
  * flash-kernel-engine include/quantized_gemm.cuh:6-41, src/quantized_gemm.cu):
  *   - A, B, C, scale and bias pointers are caller-owned DEVICE buffers.  C is
- *     fully overwritten.  The library allocates nothing for them; the one
- *     device memory it allocates itself is the workspace of the B [K,N] decode
- *     (M <= 16) and of the MFMA GEMM's K split on each stream that runs them
- *     (see fke_qgemm_workspace_size), held until the process ends, and the
- *     fke_qgemm_*_ws entry points take the caller's instead.
+ *     fully overwritten.  No entry point allocates or frees device memory
+ *     (as the reference launchers, src/quantized_gemm.cu:56-75, :120-139).
+ *     The K splits' partial sums go to the caller's workspace (the _ws entry
+ *     points, fke_w8a8_linear) or to device memory the library reserves
+ *     with its code object (FKE_SPLIT_SLOTS slots of FKE_SPLIT_SLOT_BYTES per
+ *     GPU, one per stream; see fke_qgemm_workspace_size).
  *   - All matrices are row-major.  A is [M,K].  B is [N,K] (FKE_B_NK,
  *     K-contiguous per output column) or [K,N] (FKE_B_KN).  C is [M,N].
  *   - The call is asynchronous on `stream` (a hipStream_t; NULL = the null
  *     stream) and never synchronises.  Calls are re-entrant from any host
- *     thread.  Global state: the device scratch of fke_w8a8_linear_noalloc,
- *     shared by its calls on one GPU, and the per-(device, stream) [K,N]
- *     decode workspaces (calls on one stream run in order; different streams
- *     never share one).
- */
+ *     thread.  Global state: the stream-to-slot table of the split pool
+ *     (calls on one stream share its slot; different streams never do), and
+ *     the device scratch of fke_w8a8_linear_noalloc with the event that
+ *     orders its calls.
+  */
 #ifndef FKE_QGEMM_H
 #define FKE_QGEMM_H
 
@@ -144,17 +145,32 @@ int fke_qgemm_f8_on_path(int path, const uint8_t* A, const uint8_t* B, void* C,
  * MFMA GEMM's K split (fke_select_mfma_split) uses the same workspace.  The
  * partial sums need fke_qgemm_workspace_size(M, N, K, b_layout) bytes of
  * device memory (0 for shapes that neither the decode nor the MFMA GEMM
- * splits; the larger of the two needs otherwise).
- * fke_qgemm_i8 / fke_qgemm_f8 use a workspace the library allocates per
- * (device, stream) on first need (not while that stream is being captured
- * into a graph: a capture then runs the decode unsplit, or on the workspace
- * the stream already has).  fke_qgemm_i8_ws / fke_qgemm_f8_ws are the same
- * calls on the caller's workspace (16-byte aligned): NULL, fewer bytes or an
- * unaligned pointer run the decode with fewer splits or unsplit (same
- * results); calls that can overlap in time must not share one.  Other kernel
- * families ignore the workspace.
+ * splits; the larger of the two needs otherwise; never more than
+ * FKE_SPLIT_SLOT_BYTES: the split plans are capped to one slot).
+ * fke_qgemm_i8 / fke_qgemm_f8 and the drop-in launchers put them in the
+ * stream's slot of the library's split pool: a stream is given one of the
+ * FKE_SPLIT_SLOTS slots of its GPU on its first split call (also while it
+ * is being captured into a graph, whose kernels then keep that slot's
+ * address) and keeps it; past FKE_SPLIT_SLOTS streams on one GPU, and on
+ * hipStreamPerThread, calls run unsplit.  A graph captured on a stream must
+ * not be replayed while other work that uses the capture stream's slot (calls
+ * on that stream, other graphs captured on it) can run at the same time.
+ * fke_qgemm_i8_ws / fke_qgemm_f8_ws are the same calls on the caller's
+ * workspace (16-byte aligned), taken as given: NULL, fewer bytes or an
+ * unaligned pointer run with fewer splits or unsplit.  INT8 results are the
+ * same bits whatever the workspace.  FP8 sums each split in fp32 and adds the
+ * splits in order, so the bits depend on the number of splits: a workspace of
+ * at least fke_qgemm_workspace_size bytes gives the bits of fke_qgemm_f8
+ * (eager or captured), a smaller one other bits (within the same FP8 error
+ * bounds, and the same from call to call).  Calls that can overlap in time
+ * must not share a workspace.  Other kernel families ignore it.
  */
+#define FKE_SPLIT_SLOTS 16
+#define FKE_SPLIT_SLOT_BYTES (16u << 20)
 size_t fke_qgemm_workspace_size(int M, int N, int K, int b_layout);
+/* Slots of the current GPU's split pool that streams hold (0..FKE_SPLIT_SLOTS),
+ * or -1 without a device.  Host logic only; launches nothing. */
+int fke_split_slots_in_use(void);
 int fke_qgemm_i8_ws(const int8_t* A, const int8_t* B, void* C, int M, int N, int K,
                     const float* scale_a, const float* scale_b, float sa, float sb,
                     const float* bias, int out_dtype, int b_layout,
@@ -257,7 +273,10 @@ int fke_launch_wmma_gemm_fp16(const void* d_A, const void* d_B, float* d_C, int 
  * `stream`: the quantiser writes the codes and scales into the caller's
  * device `workspace` (at least fke_w8a8_linear_workspace_size(M, K) bytes,
  * else hipErrorInvalidValue), the GEMM reads them there; calls that share a
- * workspace must be ordered (same stream).
+ * workspace must be ordered (same stream).  A K split's partial sums go to
+ * the workspace past the row scales (from the next 256-byte boundary) when it
+ * holds fke_qgemm_workspace_size(M, N, K, FKE_B_NK) bytes there, else to the
+ * stream's slot of the split pool.
  */
 size_t fke_w8a8_linear_workspace_size(int M, int K);
 int fke_w8a8_linear(const void* X, int in_dtype, const int8_t* W, void* Y, int M, int N, int K,
@@ -271,12 +290,18 @@ int fke_w8a8_linear(const void* X, int in_dtype, const int8_t* W, void* Y, int M
  * arguments and result as fke_w8a8_linear, bit for bit; the quantised
  * activations and row scales go to a library-owned device array of
  * FKE_W8A8_NOALLOC_SCRATCH_BYTES bytes per GPU (held until the process ends;
- * its address is looked up once per device).  The call allocates nothing.
+ * its address is looked up once per device); a K split's partial sums go
+ * to the same array, past the codes and scales, with as many splits as fit.
+ * The call allocates nothing.
  * Rejects, with hipErrorInvalidValue, shapes whose workspace
  * (fke_w8a8_linear_workspace_size(M, K)) exceeds the array, and a stream of a
  * device other than the current one.  Every call on one GPU shares that GPU's
- * array: calls that overlap on one GPU (other streams, other host threads
- * without ordering) race; calls ordered on one stream are safe.  Nothing in
+ * array.  Calls made outside graph capture are ordered: a call on a stream
+ * other than the previous call's first makes its stream wait (on the
+ * device's event, recorded after every such call) for the work queued
+ * before the previous call ended, so calls from several streams or host
+ * threads never overlap.  Work captured into a graph is not ordered: a
+ * replay that can overlap another call on the same GPU races.  Nothing in
  * the array needs to start at zero (each call writes what it reads).
  */
 #define FKE_W8A8_NOALLOC_SCRATCH_BYTES (32u << 20)
@@ -312,12 +337,12 @@ int fke_select_mfma_tile(int M, int N, int K, int b_layout, int swiglu, int cus)
  * splits S (1 = unsplit, on fke_select_mfma_tile's tile; -1 for bad
  * arguments) and, in *tile_path when not NULL, the FKE_PATH_MFMA_* tile it
  * runs on.  No reference counterpart (the reference has one GEMM launch per
- * call, src/quantized_gemm.cu:143-164): with few output tiles and a long K,
+ * call, src/quantized_gemm.cu:70-72, :134-136): with few output tiles and a long K,
  * S ring-tile workgroups per output tile each sum a contiguous 1/S of K, and
  * a second kernel adds the S partial sums in split order (exact for INT8,
  * deterministic for FP8) and applies the epilogue.  The partial sums,
- * S * M * N * 4 bytes, live in the workspace described at
- * fke_qgemm_workspace_size; without room the GEMM runs unsplit.  Host logic
+ * S * M * N * 4 bytes (at most FKE_SPLIT_SLOT_BYTES), live in the workspace
+ * described at fke_qgemm_workspace_size; without room the GEMM runs unsplit.  Host logic
  * only; launches nothing. */
 int fke_select_mfma_split(int M, int N, int K, int b_layout, int cus, int* tile_path);
 

@@ -437,3 +437,43 @@ def test_narrow_ring_tiles_reject_swiglu_before_any_launch():
     for path in (_lib.PATH_MFMA_128x64_RING4, _lib.PATH_MFMA_64x64_RING4):
         assert L.fke_qgemm_i8_swiglu_on_path(path, P, P, P, 64, 64, 256, None, None, 1.0, 1.0, None,
                                              _lib.OUT_BF16, None) == _lib.HIP_ERROR_INVALID_VALUE
+
+
+def test_library_imports_no_device_allocator():
+    """No entry point can allocate or free device memory: the library does not
+    even import an allocation routine (the K splits' partial sums go to the
+    caller's workspace or to the static split pool)."""
+    out = subprocess.run(["nm", "-D", "--undefined-only", _lib.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    imported = set(re.findall(r"\bU (hip\w+)", out))
+    assert "hipLaunchKernel" in imported
+    alloc = {s for s in imported if re.match(r"hip(Ext)?(Malloc|Free|MemPool|HostAlloc|HostMalloc|MemAlloc)", s)}
+    assert not alloc, f"allocation routines imported: {sorted(alloc)}"
+
+
+def test_split_pool_constants_match_header():
+    text = open(HEADER).read()
+    slots = int(re.search(r"#define FKE_SPLIT_SLOTS (\d+)", text).group(1))
+    slot = re.search(r"#define FKE_SPLIT_SLOT_BYTES \((\d+)u << (\d+)\)", text)
+    scratch = re.search(r"#define FKE_W8A8_NOALLOC_SCRATCH_BYTES \((\d+)u << (\d+)\)", text)
+    assert slots == _lib.SPLIT_SLOTS
+    assert int(slot.group(1)) << int(slot.group(2)) == _lib.SPLIT_SLOT_BYTES
+    assert int(scratch.group(1)) << int(scratch.group(2)) == _lib.W8A8_NOALLOC_SCRATCH_BYTES
+    assert _lib.lib().fke_split_slots_in_use() == -1  # no device here
+
+
+@pytest.mark.parametrize("layout", [0, 1])
+def test_split_plans_fit_one_pool_slot(layout):
+    """Every split plan, decode and MFMA, fits one slot of the split pool,
+    including shapes whose uncapped plan would not (M = 16 against an LM head
+    of 262144 columns, a long-K batch against 16384 columns)."""
+    L = _lib.lib()
+    cap = _lib.SPLIT_SLOT_BYTES
+    seen_cap = False
+    for M in (1, 4, 16, 64, 128, 200, 256):
+        for N in (1024, 8192, 14336, 16384, 65536, 128256, 262144):
+            for K in (1024, 4096, 14336, 28672):
+                ws = L.fke_qgemm_workspace_size(M, N, K, layout)
+                assert ws <= cap, (M, N, K, layout, ws)
+                seen_cap |= ws > cap // 2
+    assert seen_cap

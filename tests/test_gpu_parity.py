@@ -393,9 +393,9 @@ def test_gemv_kn_split_full_and_fewer_splits(oracle, dev, M):
 
 
 def test_gemv_kn_graph_replays(oracle, dev):
-    """The split [K,N] decode captured into a HIP graph (on the stream's own
-    workspace, and on a caller's workspace): three replays with other [K,N]
-    decodes run eagerly between them, each replay bit-exact."""
+    """The split [K,N] decode captured into a HIP graph (on the stream's slot
+    of the split pool, and on a caller's workspace): three replays with other
+    [K,N] decodes run eagerly between them, each replay bit-exact."""
     M, N, K = 4, 14336, 4096
     say("kn graph replays", M, N, K)
     A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 9200, layout="kn", act="normal")
@@ -405,7 +405,7 @@ def test_gemv_kn_graph_replays(oracle, dev):
     d2 = [dev_t(x) for x in (A2, B2, sa2, sb2, bias2)]
     s = torch.cuda.Stream()
     ws = torch.empty(_lib.lib().fke_qgemm_workspace_size(M, N, K, _lib.B_KN), dtype=torch.uint8, device=dev)
-    with torch.cuda.stream(s):  # the stream's own workspace exists before the capture
+    with torch.cuda.stream(s):  # an eager call on the stream first: the capture reuses its slot
         ops.w8a8_gemm(dA, dB, dsa, dsb, dbias, out_dtype=torch.bfloat16, b_layout="kn")
     s.synchronize()
     g = torch.cuda.CUDAGraph()
@@ -428,7 +428,7 @@ def test_gemv_kn_graph_replays(oracle, dev):
 
 def test_gemv_kn_two_streams(oracle, dev):
     """[K,N] decodes of different inputs on two streams at once, each on its
-    stream's own workspace: both bit-exact."""
+    stream's slot of the split pool: both bit-exact."""
     M, N, K = 8, 14336, 4096
     say("kn two streams", M, N, K)
     ins = [inputs_i8(oracle, M, N, K, 9400 + 10 * i, layout="kn", act="normal") for i in range(2)]
@@ -450,9 +450,9 @@ def test_gemv_kn_two_streams(oracle, dev):
 
 def test_host_threads_each_on_own_stream(oracle, dev):
     """Four host threads call the library at once, each on a stream of its own
-    (the C ABI is stateless apart from the per-(device, stream) [K,N] decode
-    workspaces, created on a stream's first such call under a mutex, and
-    ctypes releases the GIL around each call): per thread, the [K,N] INT8
+    (the C ABI is stateless apart from the stream-to-slot table of the split
+    pool, filled on a stream's first split call under a mutex, and ctypes
+    releases the GIL around each call): per thread, the [K,N] INT8
     decode, the [N,K] MFMA GEMM and the [K,N] FP8 decode, twelve times over.
     INT8 results bit-exact against the oracle; FP8 results bit-identical to
     the same call made alone before the threads start (and that one within
@@ -831,16 +831,19 @@ def test_mfma_k_split_workspace(oracle, dev):
         assert_same(host(C), ref, f"workspace {nbytes} bytes at offset {0 if ptr is None else ptr - ws.data_ptr()}")
 
 
+@pytest.mark.parametrize("nan_codes", [False, True])
 @pytest.mark.parametrize("layout", ["nk", "kn"])
-def test_mfma_k_split_fp8(oracle, dev, layout):
+def test_mfma_k_split_fp8(oracle, dev, layout, nan_codes):
     """FP8 on a split shape: within the FP8 bounds of the reference's sequential
     sum, and the same bits on every call (the partial sums are added in split
-    order)."""
+    order).  With 0x7F / 0xFF codes in both operands every split item's sums
+    come out NaN on the MFMA and are replayed with those codes cleared (the
+    reference reads them as 0.0)."""
     M, N, K = 64, 4096, 14336
     S, _ = mfma_split_of(M, N, K, layout)
-    say("mfma k split fp8", layout, S)
+    say("mfma k split fp8", layout, S, "nan codes" if nan_codes else "")
     assert S > 1
-    A, B, sa, sb = f8_inputs(oracle, M, N, K, 16000, layout)
+    A, B, sa, sb = f8_inputs(oracle, M, N, K, 16000, layout, with_nan_codes=nan_codes)
     bias = oracle.gen_f32_normal((N,), 16001, 0.0, 0.02)
     ref = oracle.f8_gemm(A, B, sa, sb, bias=bias, b_layout=oracle.B_KN if layout == "kn" else oracle.B_NK,
                          nthreads=NTH)
@@ -1050,6 +1053,27 @@ def test_python_op_matches_reference_numpy_op(oracle, dev):
             assert_same(got_np, ref, "python op (numpy in)")
             got_t = ops.quantized_gemm_int8(dev_t(A), dev_t(B), sa, sb)
             assert_same(host(got_t), ref, "python op (torch in)")
+
+
+def test_python_op_host_operands_with_a_gpu(oracle, dev):
+    """numpy operands where a GPU is visible run the HIP kernels: held in a
+    wider integer type with every value in [-128, 127] they give the
+    reference op's result (its astype(np.int32) widening changes nothing
+    there, python/flash_engine/ops.py:184); values past int8 raise ValueError
+    and float arrays TypeError, where the reference op would widen them (the
+    int8 kernels cannot take them), before anything is launched."""
+    say("python op, host operands of other types")
+    r = np.random.default_rng(6)
+    A = r.integers(-128, 128, (20, 96)).astype(np.int16)
+    B = r.integers(-128, 128, (96, 48)).astype(np.int64)
+    ref = oracle.ref_py_gemm_i8(A.astype(np.int8), B.astype(np.int8), 0.01, 0.02)
+    expr = (A.astype(np.int32) @ B.astype(np.int32)).astype(np.float32) * (0.01 * 0.02)  # the reference's line
+    assert_same(ref, expr, "oracle against the reference expression")
+    assert_same(ops.quantized_gemm_int8(A, B, 0.01, 0.02), ref, "int16 / int64 operands")
+    with pytest.raises(ValueError, match="int8 range"):
+        ops.quantized_gemm_int8(A * 2, B, 0.01, 0.02)
+    with pytest.raises(TypeError, match="integers"):
+        ops.quantized_gemm_int8(A.astype(np.float32), B, 0.01, 0.02)
 
 
 # ------------------------------------------------- per-token INT8 quantiser

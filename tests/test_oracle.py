@@ -274,6 +274,56 @@ def test_f8_reference_sequential_order(oracle):
     assert np.allclose(ref, exact, rtol=1e-5, atol=1e-6 * np.abs(exact).max())
 
 
+def _round_to_bits(q, bits):
+    """Nearest-even binary float with `bits` significand bits of the exact
+    rational q (normal range), as a Python float."""
+    from fractions import Fraction
+    if q == 0:
+        return 0.0
+    a = abs(q)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** e > a:
+        e -= 1
+    scaled = a * Fraction(2) ** (bits - 1 - e)   # in [2^(bits-1), 2^bits)
+    n = round(scaled)                             # Fraction rounds half to even
+    return float((1 if q > 0 else -1) * n * Fraction(2) ** (e - bits + 1))
+
+
+def test_f8_bias_and_bf16_epilogue(oracle):
+    """fko_f8_gemm's bias and bf16 arm on its own: y = fmaf(s, fp32(sa*sb),
+    bias[n]) with s the sequential fp32 sum, rounded once (checked with exact
+    rationals), then bf16 = nearest-even of that fp32 y to 8 significand bits.
+    Bias magnitudes span the sums' so that a separate multiply-then-add (two
+    roundings) would differ somewhere."""
+    from fractions import Fraction
+    r = rng(53)
+    M, K, N = 6, 90, 7
+    A = r.integers(0, 256, (M, K), dtype=np.uint8)
+    B = r.integers(0, 256, (K, N), dtype=np.uint8)
+    table = oracle.e4m3_decode_table()
+    sa, sb = 0.3, 0.7
+    alpha = np.float32(np.float32(sa) * np.float32(sb))
+    bias = (r.standard_normal(N) * np.array([1e-3, 1e-1, 1, 10, 100, 1e3, 1e4])).astype(np.float32)
+    y32 = oracle.f8_gemm(A, B, sa, sb, bias=bias, b_layout=oracle.B_KN)
+    y16 = oracle.f8_gemm(A, B, sa, sb, bias=bias, out_dtype=oracle.OUT_BF16, b_layout=oracle.B_KN)
+    y16_nk = oracle.f8_gemm(A, np.ascontiguousarray(B.T), sa, sb, bias=bias, out_dtype=oracle.OUT_BF16,
+                            b_layout=oracle.B_NK)
+    two_roundings = 0
+    for m in range(M):
+        for n in range(N):
+            s = np.float32(0.0)
+            for k in range(K):
+                s = np.float32(s + table[A[m, k]] * table[B[k, n]])
+            exact = Fraction(float(s)) * Fraction(float(alpha)) + Fraction(float(bias[n]))
+            want = np.float32(_round_to_bits(exact, 24))
+            assert y32[m, n].view(np.uint32) == want.view(np.uint32), (m, n, y32[m, n], want)
+            want16 = np.float32(_round_to_bits(Fraction(float(want)), 8))
+            assert y16[m, n] == (want16.view(np.uint32) >> 16), (m, n)
+            two_roundings += np.float32(np.float32(s * alpha) + bias[n]) != want
+    assert np.array_equal(y16_nk, y16)
+    assert two_roundings > 0, "no case separates the fused multiply-add from two roundings"
+
+
 def test_f8_order_matters_case(oracle):
     """A case where the sequential order is observable: 448*448 = 200704 has an
     fp32 ulp of 2^-6, so each following 1.0 * 2^-9 product is rounded away one

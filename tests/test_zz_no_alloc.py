@@ -1,8 +1,10 @@
 """The allocation-free W8A8 linear (fke_w8a8_linear_noalloc), through the C
 ABI: bit-identical to fke_w8a8_linear with a caller workspace, on two calls in
 a row (the second smaller, so it reads only what it wrote over the first
-call's leftovers in the shared device scratch), and on a shape whose
-workspace fills most of the scratch."""
+call's leftovers in the shared device scratch), on a shape whose workspace
+fills most of the scratch, on a shape whose GEMM splits K (partial sums in
+the scratch past the codes and scales), and on two streams whose calls the
+library orders."""
 import numpy as np
 import pytest
 
@@ -89,3 +91,31 @@ def test_noalloc_near_the_scratch_limit():
     st = L.fke_w8a8_linear_noalloc(x.data_ptr(), _lib.IN_BF16, W.data_ptr(), y.data_ptr(), 4096, 256, 8192,
                                    ws.data_ptr(), 1.0, bias.data_ptr(), _lib.OUT_BF16, sh)
     assert st == _lib.HIP_ERROR_INVALID_VALUE   # past the scratch: refused before any launch
+
+
+def test_noalloc_k_split_and_two_streams():
+    """64x4096x14336 splits K four ways on the MFMA ring tiles: the partial sums
+    go to the scratch past the codes and scales.  Then calls alternate between
+    two streams with no host synchronisation, on inputs of different shapes
+    (the split shape and a decode shape): the library orders them, and every
+    output equals its workspace-entry reference."""
+    dev = torch.device("cuda:0")
+    L = _lib.lib()
+    sh = torch.cuda.current_stream(dev).cuda_stream
+    M, N, K = 64, 4096, 14336
+    assert L.fke_select_mfma_split(M, N, K, _lib.B_NK, 0, None) == 4
+    say("noalloc linear k split", M, N, K)
+    cases = [_inputs(M, N, K, 31, dev), _inputs(2, 2048, 14336, 32, dev)]
+    refs = [_with_workspace(L, *c, _lib.OUT_BF16, torch.bfloat16, sh) for c in cases]
+    got = _noalloc(L, *cases[0], _lib.OUT_BF16, torch.bfloat16, sh)
+    torch.cuda.synchronize()
+    assert _same(got, refs[0]), "noalloc differs on the split shape"
+    streams = [torch.cuda.Stream(dev), torch.cuda.Stream(dev)]
+    say("noalloc linear two streams, 8 calls each")
+    outs = []
+    for i in range(16):
+        c = i % 2
+        outs.append((c, _noalloc(L, *cases[c], _lib.OUT_BF16, torch.bfloat16, streams[c].cuda_stream)))
+    torch.cuda.synchronize()
+    for i, (c, y) in enumerate(outs):
+        assert _same(y, refs[c]), f"call {i} on stream {c} differs"
