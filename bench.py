@@ -104,6 +104,10 @@ def parse():
                          "tile rule, INT8, FP8 and bf16 (B [N,K]), beside the tile it picks")
     ap.add_argument("--data-sweep", action="store_true",
                     help="also time the headline GEMM on zero, constant and narrow-range operands (clock vs data)")
+    ap.add_argument("--mfma-ceiling", action="store_true",
+                    help="the INT8 matrix-core ceiling: a register-only v_mfma_i32_32x32x32_i8 stream "
+                         "(libfke_probe.so) on the headline's operand distribution and on constant operands, "
+                         "with the shader clock and socket power while it runs")
     ap.add_argument("--vendor", action="store_true",
                     help="also time the vendor library (hipBLASLt through torch) on the 8192^3 GEMMs, for context")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -252,6 +256,8 @@ def main():
         line["vendor_context"] = vendor_configs(torch, dev, gen, timed, args)
     if args.data_sweep:
         line["data_sweep"] = data_sweep(torch, L, _lib, dev, gen, timed, args)
+    if args.mfma_ceiling:
+        line["mfma_ceiling"] = mfma_ceiling(torch, dev, gen, timed, args)
     if args.tile_sweep:
         line["tile_sweep"] = tile_sweep(torch, L, _lib, dev, gen, timed, args)
     if not args.no_cpu:
@@ -782,6 +788,51 @@ def data_sweep(torch, L, _lib, dev, gen, timed, args):
                                           None, _lib.OUT_F32, _lib.B_NK, sh), args.steps, args.warmup, args.preheat_ms)
         res[name] = {"ms": round(ms, 4), "TOPS": round(2.0 * M * N * K / ms / 1e9, 1)}
         del A, B
+    return res
+
+
+def mfma_ceiling(torch, dev, gen, timed, args):
+    """What the matrix cores sustain on their own, at the board's power limit:
+    one workgroup of 4 waves per CU streams v_mfma_i32_32x32x32_i8 in the
+    GEMM's 4x4-block order on operands held in registers (no LDS, no memory
+    traffic in the loop; csrc/probe_mfma.hip), for operands drawn as the
+    headline's (uniform int8 [-127,127]) and for constant ones.  Each runs
+    back to back for the pre-heat time, then `steps` timed launches, then
+    1.1 s more while amdsmi reads the clock and socket power."""
+    import ctypes as ct
+    P = ct.CDLL(os.path.join(PKG, "lib", "libfke_probe.so"))
+    P.fke_probe_mfma_src_bytes.argtypes = [ct.c_int]
+    P.fke_probe_mfma_src_bytes.restype = ct.c_size_t
+    P.fke_probe_mfma_out_elems.argtypes = [ct.c_int]
+    P.fke_probe_mfma_out_elems.restype = ct.c_size_t
+    P.fke_probe_mfma_i8.argtypes = [ct.c_void_p, ct.c_void_p, ct.c_int, ct.c_int, ct.c_void_p]
+    P.fke_probe_mfma_i8.restype = ct.c_int
+    sh = torch.cuda.current_stream(dev).cuda_stream
+    grid = torch.cuda.get_device_properties(dev).multi_processor_count
+    iters = 2048
+    out = torch.empty(P.fke_probe_mfma_out_elems(grid), dtype=torch.int32, device=dev)
+    nbytes = P.fke_probe_mfma_src_bytes(grid)
+    ops = float(grid) * 4 * iters * 32 * 2 * 32 * 32 * 32
+    res = {"grid": grid, "iters": iters, "ops_per_launch": ops}
+    for name, src in (("uniform_-127_127", torch.randint(-127, 128, (nbytes,), dtype=torch.int8, device=dev,
+                                                           generator=gen)),
+                      ("ones", torch.ones(nbytes, dtype=torch.int8, device=dev))):
+        def fn():
+            st = P.fke_probe_mfma_i8(src.data_ptr(), out.data_ptr(), grid, iters, sh)
+            if st:
+                raise RuntimeError(f"fke_probe_mfma_i8 failed: status {st}")
+        torch.cuda.synchronize()
+        clock = ClockSampler() if args.clock_ms > 0 else None
+        if clock:
+            clock.start()
+        ms = timed(fn, max(args.steps, 20), 5, args.preheat_ms)
+        if clock:
+            preheat(torch, fn, args.clock_ms)
+        sclk = clock.stop() if clock else None
+        pops = ops / (ms * 1e-3) / 1e15
+        res[name] = {"ms": round(ms, 4), "POPs": round(pops, 3), "frac_of_peak": round(pops * 1e3 / PEAK_INT8_TOPS, 4),
+                     "sclk_mhz": sclk}
+        del src
     return res
 
 

@@ -200,6 +200,13 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, i
         r, reinterpret_cast<__attribute__((address_space(3))) void*>(reinterpret_cast<uintptr_t>(l)), 16,
         static_cast<int>(voff), soff, 0, AUX);
 }
+// 4 bytes per lane, buffer -> LDS (buffer_load_dword ... lds): lane l's word
+// lands at lds + 4*l.
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, uint32_t voff, int soff, void* l) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        r, reinterpret_cast<__attribute__((address_space(3))) void*>(reinterpret_cast<uintptr_t>(l)), 4,
+        static_cast<int>(voff), soff, 0, 0);
+}
 
 // ---- per-token INT8 quantisation (quant_i8.hip) ----
 

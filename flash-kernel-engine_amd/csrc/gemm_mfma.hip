@@ -119,23 +119,37 @@ __device__ __forceinline__ int swiglu_b_row(int c, int o0, int I) {
 // Direct-to-LDS copy plan of one (32*PW)-row x 128-byte K-contiguous panel (A,
 // or B in [N,K] order).  Each wave issues PW loads of 1 KiB (8 rows x 128 B);
 // lane l lands at byte 16*l of its KiB, so it fetches the logical chunk that
-// the swizzle assigns to that physical slot.  Rows past `rows` re-read the
-// last valid row (their outputs are never stored).  SWI: panel row r holds
-// weight row swiglu_b_row<NJ>(r, row0, rows / 2).
+// the swizzle assigns to that physical slot.
+//  * at_tile: the per-lane offsets are relative to the tile's first row and
+//    the same for every tile (set once by init_lanes); the buffer resource
+//    starts at that row and ends with the operand, so rows past the end read
+//    zero (their outputs are never stored).  Moving to another tile is scalar
+//    work only.
+//  * init (SwiGLU B): panel row r holds weight row swiglu_b_row<NJ>(r, row0,
+//    rows / 2), a per-tile lane offset over all of B; rows past `rows` re-read
+//    the last valid row.
 template <int PW>
 struct Panel {
-    __amdgpu_buffer_rsrc_t rsrc;  // the whole operand, rows x ld bytes
+    __amdgpu_buffer_rsrc_t rsrc;  // from the tile's first row (init: the whole operand)
     uint32_t off[PW];             // byte offset of this lane's 16-byte source at k = 0
-    template <bool SWI = false, int NJ = 4>
-    __device__ void init(const int8_t* base, int ld, int row0, int rows, int wave, int lane) {
+    __device__ void init_lanes(int ld, int wave, int lane) {
+#pragma unroll
+        for (int i = 0; i < PW; ++i) {
+            const int r = (wave * PW + i) * 8 + (lane >> 3);
+            off[i] = static_cast<uint32_t>(r * ld + ((lane & 7) ^ swz(r)) * 16);
+        }
+    }
+    __device__ __forceinline__ void at_tile(const int8_t* base, int ld, int row0, int rows) {
+        rsrc = make_rsrc(base + static_cast<size_t>(row0) * ld, (rows - row0) * ld);
+    }
+    template <int NJ>
+    __device__ void init_swiglu(const int8_t* base, int ld, int row0, int rows, int wave, int lane) {
         rsrc = make_rsrc(base, rows * ld);
 #pragma unroll
         for (int i = 0; i < PW; ++i) {
-            const int seg = wave * PW + i;
-            const int r = seg * 8 + (lane >> 3);
+            const int r = (wave * PW + i) * 8 + (lane >> 3);
             const int lc = (lane & 7) ^ swz(r);
-            int src = row0 + r;
-            if constexpr (SWI) src = swiglu_b_row<NJ>(r, row0, rows >> 1);  // (SwiGLU tiles have NJ >= 2)
+            const int src = swiglu_b_row<NJ>(r, row0, rows >> 1);  // (SwiGLU tiles have NJ >= 2)
             off[i] = static_cast<uint32_t>(min(src, rows - 1) * ld + lc * 16);
         }
     }
@@ -168,18 +182,20 @@ template <int BN>
 struct KNPanel {
     static constexpr int PW = BN / 32;  // 1-KiB loads per wave per stage
     static constexpr int CH = BN / 16;  // 16-byte chunks per k row
-    __amdgpu_buffer_rsrc_t rsrc;        // all of B, K x N bytes
-    uint32_t off[PW];                   // byte offset of this lane's 16-byte source at stage 0
+    __amdgpu_buffer_rsrc_t rsrc;        // B from the tile's first column to its end
+    uint32_t off[PW];                   // byte offset of this lane's 16-byte source at stage 0 (any tile)
     int stage_bytes;                    // BK rows of B
-    __device__ void init(const int8_t* B, int N, int K, int n0, int wave, int lane) {
-        rsrc = make_rsrc(B, K * N);
+    __device__ void init_lanes(int N, int wave, int lane) {
         stage_bytes = BK * N;
 #pragma unroll
         for (int i = 0; i < PW; ++i) {
             const int r = (wave * PW + i) * (1024 / BN) + lane / CH;  // k row within the stage
             const int c = (lane % CH) ^ kn_swz<BN>(r);                // logical chunk landing at physical lane % CH
-            off[i] = static_cast<uint32_t>(r * N + n0 + c * 16);
+            off[i] = static_cast<uint32_t>(r * N + c * 16);
         }
+    }
+    __device__ __forceinline__ void at_tile(const int8_t* B, int N, int K, int n0) {
+        rsrc = make_rsrc(B + n0, K * N - n0);
     }
     template <int AUX = 0>
     __device__ __forceinline__ void issue(int i, int kt, uint8_t* lds, int wave) const {
@@ -319,6 +335,18 @@ __device__ __forceinline__ void sanitize_frags(Frags<ELEM, TL>& f) {
     }
 }
 
+// Element v of an accumulator block, as its 32 bits, read straight out of
+// the AGPR that holds it (v_accvgpr_read_b32): the accumulators stay in AGPRs
+// until the epilogue reads them one at a time, instead of being copied to
+// VGPRs all at once when the K loop ends, which would take every VGPR and
+// spill the rest of the epilogue's state to scratch.
+template <class AccT>
+__device__ __forceinline__ uint32_t acc_bits(const AccT& a, int v) {
+    uint32_t x;
+    asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(x) : "a"(a[v]));
+    return x;
+}
+
 // MFMA (i, j) of one k step of the wave's WM x WN block.
 template <int ELEM, class TL>
 __device__ __forceinline__ void mfma_one(const Frags<ELEM, TL>& f, typename Mma<ELEM>::AccT (&acc)[TL::NI][TL::NJ],
@@ -337,6 +365,45 @@ __device__ __forceinline__ void mfma_one(const Frags<ELEM, TL>& f, typename Mma<
                                                             __builtin_bit_cast(v8bf, f.b[j]), acc[i][j], 0, 0, 0);
 }
 
+// One lane's epilogue operands, read out of LDS with inline ds_reads and one
+// wait: the compiler would order its own LDS reads after every LDS-DMA copy
+// in flight (it cannot always tell the epilogue's arrays from the stages the
+// next tile's copies fill), which would make the epilogue wait for those
+// copies.  sa[i][g]: scale_a of tile rows WM*wm + 32i + 8g + 4*(lane/32) +
+// 0..3; sb[j], bias[j]: scale_b and bias of tile column WN*wn + 32j + lane%32.
+template <int NI, int NJ>
+struct EpiOps {
+    typedef float v4f __attribute__((ext_vector_type(4)));
+    v4f sa[NI][4];
+    float sb[NJ], bias[NJ];
+    template <int WM, int WN>
+    __device__ __forceinline__ void read(const float* esa, const float* esb, const float* ebias, int wm, int wn,
+                                         int lane) {
+        typedef __attribute__((address_space(3))) const float* lds_f;
+        const int lr = lane & 31, lh = lane >> 5;
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                asm volatile("ds_read_b128 %0, %1"
+                             : "=v"(sa[i][g])
+                             : "v"((lds_f)(esa + wm * WM + i * 32 + 8 * g + 4 * lh)));
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            asm volatile("ds_read_b32 %0, %1" : "=v"(sb[j]) : "v"((lds_f)(esb + wn * WN + j * 32 + lr)));
+            asm volatile("ds_read_b32 %0, %1" : "=v"(bias[j]) : "v"((lds_f)(ebias + wn * WN + j * 32 + lr)));
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        // the registers are tied to the wait: nothing reads them before it
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) asm volatile("" : "+v"(sa[i][g]));
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) asm volatile("" : "+v"(sb[j]), "+v"(bias[j]));
+    }
+};
+
 // Output columns of one workgroup tile: BN, or BN/2 SwiGLU outputs (BN B rows).
 template <bool SWI, class TL>
 constexpr int tile_cols() { return SWI ? TL::BN / 2 : TL::BN; }
@@ -353,10 +420,12 @@ __global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p
     __shared__ __attribute__((aligned(1024))) uint8_t lds1[TL::STAGE];
     __shared__ __attribute__((aligned(1024))) uint8_t lds2[TL::NS > 2 ? TL::STAGE : 16];  // NS = 4 only
     __shared__ __attribute__((aligned(1024))) uint8_t lds3[TL::NS > 2 ? TL::STAGE : 16];
-    __shared__ __attribute__((aligned(16))) float epi_sa[BM];        // scale of each tile row
-    __shared__ __attribute__((aligned(16))) float epi_sb[TL::BN];    // scale of each tile column
-    __shared__ __attribute__((aligned(16))) float epi_bias[TL::BN];  // bias of each tile column
-    __shared__ int redo;                                              // FP8: rerun with NaN codes cleared
+    // Epilogue operands of two items (the one in its epilogue, the next one):
+    // scale of each tile row, scale and bias of each tile column.
+    __shared__ __attribute__((aligned(16))) float epi_sa[2][BM];
+    __shared__ __attribute__((aligned(16))) float epi_sb[2][TL::BN];
+    __shared__ __attribute__((aligned(16))) float epi_bias[2][TL::BN];
+    __shared__ int redo;  // FP8: rerun with NaN codes cleared
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -367,80 +436,95 @@ __global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p
     constexpr int TC = tile_cols<SWI, TL>();
     const int NO = SWI ? N >> 1 : N;  // output columns
     const int gm = (M + BM - 1) / BM, gn = (NO + TC - 1) / TC;
-    // Persistent: workgroup b takes tiles b, b + G, b + 2G, ... (G = grid size,
-    // a multiple of the XCD count, so every tile of a workgroup stays on its
-    // XCD and each XCD walks its tile range in the same order as a one-tile-
-    // per-workgroup launch would), so a CU moves to its next tile without a
-    // workgroup relaunch.
-    // K split (S > 1): the S splits of a tile are walked as S rows of tiles,
-    // item (split, tm, tn) summing K stages [split * KS, split * KS + KS).
     const int S = sk.S;
-    for (int slot = blockIdx.x; slot < gm * gn * S; slot += gridDim.x) {
-    if (slot != static_cast<int>(blockIdx.x)) barrier();  // the last tile's epilogue read epi_* from LDS
-    int tm, tn;
-    tile_of(slot, gm * S, gn, tm, tn);
-    const int split = tm / gm;
-    tm -= split * gm;
-    const int m0 = tm * BM, n0 = tn * TC;  // n0: first output column
-
+    const int items = gm * gn * S;
     const int8_t* A = static_cast<const int8_t*>(p.A);
     const int8_t* B = static_cast<const int8_t*>(p.B);
 
-    // epilogue operands -> LDS (visible after the prologue barrier)
-    if (tid < BM) epi_sa[tid] = p.scale_a ? p.scale_a[min(m0 + tid, M - 1)] : p.sa;
-    if (tid < TL::BN) {
-        int n = n0 + tid;  // B row of tile column tid
-        if constexpr (SWI) n = swiglu_b_row<NJ>(tid, n0, NO);
-        n = min(n, N - 1);
-        epi_sb[tid] = p.scale_b ? p.scale_b[n] : p.sb;
-        epi_bias[tid] = p.bias ? p.bias[n] : -0.0f;
-    }
-    if (tid == 0) redo = 0;
+    // One output tile, or under a K split (S > 1) one K range of a tile: the S
+    // splits of a tile are walked as S rows of tiles, item (split, tm, tn)
+    // summing K stages [split * KS, split * KS + KT).
+    struct Item {
+        int m0, n0, split, kt0, KT;  // n0: first output column
+    };
+    auto item_of = [&](int slot) __attribute__((always_inline)) {
+        int tm, tn;
+        tile_of(slot, gm * S, gn, tm, tn);
+        Item it;
+        it.split = tm / gm;
+        it.m0 = (tm - it.split * gm) * BM;
+        it.n0 = tn * TC;
+        it.kt0 = it.split * sk.KS;
+        it.KT = S > 1 ? min(K / BK - it.kt0, sk.KS) : K / BK;
+        return it;
+    };
 
-    typename Mma<ELEM>::AccT acc[NI][NJ];
-#pragma unroll
-    for (int i = 0; i < NI; ++i)
-#pragma unroll
-        for (int j = 0; j < NJ; ++j)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
-
-    const int kt0 = split * sk.KS;  // first K stage of this item
-    const int KT = S > 1 ? min(K / BK - kt0, sk.KS) : K / BK;
+    // Copy plans.  The per-lane offsets are the same for every tile (SwiGLU's
+    // B: set per tile); a tile's first row or column is scalar state.
     Panel<TL::PWA> pa;
-    pa.init(A, K, m0, M, wave, lane);
+    pa.init_lanes(K, wave, lane);
     using BPanel = typename std::conditional<BL == FKE_B_NK, Panel<TL::PWB>, KNPanel<TL::BN>>::type;
     BPanel pb;
     uint32_t kn_off[NJ][2] = {};
     if constexpr (BL == FKE_B_NK) {
-        pb.template init<SWI, NJ>(B, K, n0, N, wave, lane);
+        if constexpr (!SWI) pb.init_lanes(K, wave, lane);
     } else {
-        pb.init(B, N, K, n0, wave, lane);
+        pb.init_lanes(N, wave, lane);
 #pragma unroll
         for (int j = 0; j < NJ; ++j)
 #pragma unroll
             for (int rr = 0; rr < 2; ++rr) kn_off[j][rr] = kn_read_off<ELEM, TL>(lane, wn, j, rr);
     }
-    if (kt0 > 0) {  // the copies start at stage kt0 (K-contiguous rows; B [K,N]: kt0 stages of k rows)
-#pragma unroll
-        for (int i = 0; i < TL::PWA; ++i) pa.off[i] += static_cast<uint32_t>(kt0 * BK);
+    int ckt0 = 0;  // first K stage of the item the copies are issued for
+    auto at_item = [&](const Item& it) __attribute__((always_inline)) {
+        pa.at_tile(A, K, it.m0, M);
         if constexpr (BL == FKE_B_NK) {
-#pragma unroll
-            for (int i = 0; i < TL::PWB; ++i) pb.off[i] += static_cast<uint32_t>(kt0 * BK);
+            if constexpr (SWI) pb.template init_swiglu<NJ>(B, K, it.n0, N, wave, lane);
+            else pb.at_tile(B, K, it.n0, N);
         } else {
-#pragma unroll
-            for (int i = 0; i < KNPanel<TL::BN>::PW; ++i) pb.off[i] += static_cast<uint32_t>(kt0) * pb.stage_bytes;
+            pb.at_tile(B, N, K, it.n0);
         }
-    }
+        ckt0 = it.kt0;
+    };
+
+    // Epilogue operands of an item into LDS set `set`, by dword LDS-DMA (no
+    // registers wait for them; issued before the item's stage copies, they
+    // have landed once stage 0 has): wave w fills entries 64w..64w+63 of each
+    // array it covers, entries past M or N reading zero.  A missing scale or
+    // bias is written as its constant.
+    auto load_epi = [&](const Item& it, int set) __attribute__((always_inline)) {
+        const int e = wave * 64 + lane;  // entry of this lane
+        if (wave * 64 < BM) {
+            if (p.scale_a) dma4(make_rsrc(p.scale_a, M * 4), static_cast<uint32_t>(it.m0 + e) * 4, 0, &epi_sa[set][wave * 64]);
+            else epi_sa[set][e] = p.sa;
+        }
+        if (wave * 64 < TL::BN) {
+            int n = it.n0 + e;  // B row of tile column e
+            if constexpr (SWI) n = min(swiglu_b_row<NJ>(e, it.n0, NO), N - 1);
+            const uint32_t off = static_cast<uint32_t>(n) * 4;
+            if (p.scale_b) dma4(make_rsrc(p.scale_b, N * 4), off, 0, &epi_sb[set][wave * 64]);
+            else epi_sb[set][e] = p.sb;
+            if (p.bias) dma4(make_rsrc(p.bias, N * 4), off, 0, &epi_bias[set][wave * 64]);
+            else epi_bias[set][e] = -0.0f;
+        }
+    };
+
+    typename Mma<ELEM>::AccT acc[NI][NJ];
+    int slot = blockIdx.x;
+    if (slot >= items) return;  // (the grid never has more workgroups than items)
+    Item cur = item_of(slot);
+    int par = 0;  // epi_* set of item cur
 
     // Copy of stage kt into buffer b, slot q of NSLOT: slots 0..PWA-1 copy
     // A, the rest copy B, all buffer -> LDS.
     constexpr int PWA = TL::PWA;
     constexpr int NSLOT = PWA + TL::PWB;  // B [K,N] panels take BN/32 loads per wave too
+    // kt counts from the first stage of the item at_item set last (ckt0).
     auto copy = [&](int q, int kt, uint8_t* b) __attribute__((always_inline)) {
-        if (q < PWA) pa.issue(q, kt * BK, b, wave);
-        else if constexpr (BL == FKE_B_NK) pb.template issue<BNT ? 2 : 0>(q - PWA, kt * BK, b + TL::STAGE_A, wave);
-        else pb.template issue<BNT ? 2 : 0>(q - PWA, kt, b + TL::STAGE_A, wave);
+        const int ka = ckt0 + kt;
+        if (q < PWA) pa.issue(q, ka * BK, b, wave);
+        else if constexpr (BL == FKE_B_NK) pb.template issue<BNT ? 2 : 0>(q - PWA, ka * BK, b + TL::STAGE_A, wave);
+        else pb.template issue<BNT ? 2 : 0>(q - PWA, ka, b + TL::STAGE_A, wave);
     };
     // A stage is NKS groups of NPIECE MFMAs (16 for the 256x256 tile).
     // Group g runs the MFMAs of one fragment set (g = 0: the previous stage's
@@ -485,15 +569,15 @@ __global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p
     // Past the end the last stage is copied again (into a buffer whose stage
     // is done), so the body has no data-dependent branch.
     constexpr int NS = TL::NS;
-    auto stage = [&](auto sanc, const uint8_t* cur, uint8_t* nxt, int kt) __attribute__((always_inline)) {
-        const int kc = min(kt + NS - 1, KT - 1);
+    auto stage = [&](auto sanc, const uint8_t* cbuf, uint8_t* nxt, int kt) __attribute__((always_inline)) {
+        const int kc = min(kt + NS - 1, cur.KT - 1);
         using S = decltype(sanc);
         if constexpr (NKS == 4) {
             constexpr int P = PER_GROUP, P2 = 2 * P < NSLOT ? 2 * P : NSLOT;
-            group(S{}, I0{}, std::integral_constant<int, P>{}, f1, f0, cur, 0, nxt, kc);
-            group(S{}, std::integral_constant<int, P>{}, std::integral_constant<int, P2>{}, f0, f1, cur, 1, nxt, kc);
-            group(S{}, std::integral_constant<int, P2>{}, std::integral_constant<int, NSLOT>{}, f1, f0, cur, 2, nxt, kc);
-            group(S{}, std::integral_constant<int, NSLOT>{}, std::integral_constant<int, NSLOT>{}, f0, f1, cur, 3, nxt,
+            group(S{}, I0{}, std::integral_constant<int, P>{}, f1, f0, cbuf, 0, nxt, kc);
+            group(S{}, std::integral_constant<int, P>{}, std::integral_constant<int, P2>{}, f0, f1, cbuf, 1, nxt, kc);
+            group(S{}, std::integral_constant<int, P2>{}, std::integral_constant<int, NSLOT>{}, f1, f0, cbuf, 2, nxt, kc);
+            group(S{}, std::integral_constant<int, NSLOT>{}, std::integral_constant<int, NSLOT>{}, f0, f1, cbuf, 3, nxt,
                   kc);
         } else {
             static_assert(NKS == 2, "k steps per stage");
@@ -505,22 +589,18 @@ __global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p
             // (438-444 us against 416-422 us at 8192^3, both B layouts).
             // Smaller tiles have more copies than MFMAs per group: half each.
             constexpr int P = NSLOT <= NPIECE ? NSLOT : (NSLOT + 1) / 2;
-            group(S{}, I0{}, std::integral_constant<int, P>{}, f1, f0, cur, 0, nxt, kc);
-            group(S{}, std::integral_constant<int, P>{}, std::integral_constant<int, NSLOT>{}, f0, f1, cur, 1, nxt,
+            group(S{}, I0{}, std::integral_constant<int, P>{}, f1, f0, cbuf, 0, nxt, kc);
+            group(S{}, std::integral_constant<int, P>{}, std::integral_constant<int, NSLOT>{}, f0, f1, cbuf, 1, nxt,
                   kc);
         }
-        wait_lgkm0();                  // last step's fragments in registers (f1): cur may be overwritten after the barrier
+        wait_lgkm0();                  // last step's fragments in registers (f1): cbuf may be overwritten after the barrier
         wait_vm<(NS - 2) * NSLOT>();   // this wave's share of stage kt+1 has landed (later stages may be in flight)
         barrier();
     };
 
-    // The whole K loop.  Buffer roles are static (lds0..lds3 are distinct
-    // objects, so the compiler sees that a stage's DMA never aliases another
-    // stage's reads), hence NS stages per iteration; the body has no
-    // data-dependent branches, so the accumulators stay in AGPRs.
-    auto k_loop = [&](auto sanc) __attribute__((always_inline)) {
-        using S = decltype(sanc);
-        // Prologue: stages 0..NS-2 -> lds0..; f1 (the carried set) starts at zero.
+    // Stages 0..NS-2 of the item at_item set last, into lds0.. (issued, not
+    // waited for).
+    auto prologue_copies = [&](int KT) __attribute__((always_inline)) {
 #pragma unroll
         for (int q = 0; q < NSLOT; ++q) copy(q, 0, lds0);
         if constexpr (NS == 4) {
@@ -529,13 +609,37 @@ __global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p
 #pragma unroll
             for (int q = 0; q < NSLOT; ++q) copy(q, min(2, KT - 1), lds2);
         }
+    };
+    // VMEM instructions a wave issues after its stage-0 copies and before the
+    // K loop waits for them: the copies of stages 1..NS-2, and, when the
+    // copies were issued ahead of the previous item's epilogue, that
+    // epilogue's stores (counted as a quarter of them, should the compiler
+    // pair stores).  vmcnt retires in issue order and counts to 63 at most,
+    // so waiting down to this many waits for stage 0 and not for the stores
+    // issued after it.
+    constexpr int NSTORE = (SWI ? NI * (NJ / 2) : NI * NJ) * 16;
+    constexpr int WAIT0 = (NS - 2) * NSLOT;
+    constexpr int WAIT0_AFTER_EPI = WAIT0 + NSTORE / 4 < 63 ? WAIT0 + NSTORE / 4 : 63;
+
+    // The whole K loop of item `cur`, whose first NS-1 stages have been
+    // issued (after_epi: ahead of the previous item's epilogue).  Buffer
+    // roles are static (lds0..lds3 are distinct objects, so the compiler sees
+    // that a stage's DMA never aliases another stage's reads), hence NS
+    // stages per iteration; the body has no data-dependent branches, so the
+    // accumulators stay in AGPRs.  On return no copy is in flight in any wave
+    // and no wave reads the stages any more: the next item's copies may start.
+    auto k_loop = [&](auto sanc, bool after_epi) __attribute__((always_inline)) {
+        using S = decltype(sanc);
         wait_lgkm0();
-        wait_vm<(NS - 2) * NSLOT>();  // stage 0 has landed
+        if (after_epi) wait_vm<WAIT0_AFTER_EPI>();  // stage 0 has landed
+        else wait_vm<WAIT0>();
         barrier();
+        // f1 (the carried set) starts at zero.
 #pragma unroll
         for (int i = 0; i < NI; ++i) f1.a[i] = typename Mma<ELEM>::Frag{};
 #pragma unroll
         for (int j = 0; j < NJ; ++j) f1.b[j] = typename Mma<ELEM>::Frag{};
+        const int KT = cur.KT;
         int kt = 0;
         if constexpr (NS == 2) {
             for (; kt + 2 <= KT; kt += 2) {
@@ -553,7 +657,8 @@ __global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p
             if (kt < KT) stage(S{}, lds0, lds3, kt);  // stage counts not a multiple of 4
             if (kt + 1 < KT) stage(S{}, lds1, lds0, kt + 1);
             if (kt + 2 < KT) stage(S{}, lds2, lds1, kt + 2);
-            wait_vm0();  // the re-copies of the last stage have landed before the tile moves on
+            wait_vm0();  // the re-copies of the last stage have landed, in every wave
+            barrier();
         }
         // the last stage's carried step
         if constexpr (S::value) sanitize_frags<ELEM, TL>(f1);
@@ -561,170 +666,219 @@ __global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p
         for (int t = 0; t < NPIECE; ++t) mfma_one<ELEM, TL>(f1, acc, t / NJ, t % NJ);
     };
 
-    if constexpr (ELEM != ELEM_F8) {
-        k_loop(F{});
-    } else {
-        // E4M3 0x7F/0xFF are NaN to the MFMA but 0.0 to the reference.
-        // Clearing them costs ~5 VALU per operand word, more than the MFMAs
-        // can hide, and real quantizers never emit them (they saturate at
-        // 448).  So run the K loop on the raw codes first: every product is
-        // finite and no sum can overflow, so a NaN accumulator proves a
-        // NaN code in the tile's rows or columns.  Only then does the
-        // workgroup run the loop again with the codes cleared.
-        k_loop(F{});
-        float t = 0.0f;
+    // Fused epilogue of item `cur` (its tile's scale_a, scale_b and bias in
+    // set `par` of epi_*).
+    auto epilogue = [&]() __attribute__((always_inline)) {
+        // 32x32 block layout of the accumulator: lane l holds
+        // column l%32 and rows 8*(v/4) + 4*(l/32) + v%4 for v = 0..15.
+        // y = fma(acc, sa_m*sb_n, bias_n) with bias_n = -0.0 when there is no
+        // bias, which is exactly acc*s (signed zeros included).
+        // The tile is written through a buffer resource based at row m0 whose
+        // range ends at the last valid row, so stores to rows >= M fall out of
+        // range and are dropped; a lane whose column is >= N adds 2^31 to its
+        // offsets and drops all of its stores.  One code path serves full and
+        // edge tiles.  Stores are non-temporal: the output is written once and
+        // should not evict the operand panels other workgroups still stream
+        // through L2.
+        const int lr = lane & 31, lh = lane >> 5;
+        if constexpr (!SWI) {
+            if (S > 1) {
+                // K split: the item's raw sums to part[split][m][n] (int32 / fp32),
+                // through a buffer resource based at row m0 of the split whose
+                // range ends at the last valid row, as the fused epilogue below.
+                const uint32_t prow = static_cast<uint32_t>(N) * 4;
+                const __amdgpu_buffer_rsrc_t rp =
+                    make_rsrc(static_cast<char*>(sk.part) + (static_cast<size_t>(cur.split) * M + cur.m0) * prow,
+                              min(M - cur.m0, BM) * static_cast<int>(prow));
 #pragma unroll
-        for (int i = 0; i < NI; ++i)
+                for (int j = 0; j < NJ; ++j) {
+                    const int cn = wn * TL::WN + j * 32 + lr;
+                    const uint32_t lane_off =
+                        cur.n0 + cn < N ? static_cast<uint32_t>(wm * TL::WM + 4 * lh) * prow + static_cast<uint32_t>(cur.n0 + cn) * 4
+                                    : 0x80000000u;
 #pragma unroll
-            for (int j = 0; j < NJ; ++j)
+                    for (int i = 0; i < NI; ++i) {
+                        fence();
 #pragma unroll
-                for (int v = 0; v < 16; ++v) t += acc[i][j][v];
-        if (__builtin_isnan(t)) redo = 1;  // benign race: every writer stores 1
-        wait_lgkm0();
-        barrier();
-        if (redo) {
+                        for (int g = 0; g < 4; ++g)
 #pragma unroll
-            for (int i = 0; i < NI; ++i)
-#pragma unroll
-                for (int j = 0; j < NJ; ++j)
-#pragma unroll
-                    for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
-            k_loop(std::true_type{});
+                            for (int e = 0; e < 4; ++e) {
+                                const int voff = static_cast<int>(lane_off + static_cast<uint32_t>(i * 32 + 8 * g + e) * prow);
+                                const int v = 4 * g + e;
+                                uint32_t bits;
+                                bits = acc_bits(acc[i][j], v);
+                                __builtin_amdgcn_raw_buffer_store_b32(bits, rp, voff, 0, 0);
+                            }
+                    }
+                }
+                return;
+            }
         }
-    }
-
-    // Fused epilogue.  32x32 block layout of the accumulator: lane l holds
-    // column l%32 and rows 8*(v/4) + 4*(l/32) + v%4 for v = 0..15.
-    // y = fma(acc, sa_m*sb_n, bias_n) with bias_n = -0.0 when there is no
-    // bias, which is exactly acc*s (signed zeros included).
-    // The tile is written through a buffer resource based at row m0 whose
-    // range ends at the last valid row, so stores to rows >= M fall out of
-    // range and are dropped; a lane whose column is >= N adds 2^31 to its
-    // offsets and drops all of its stores.  One code path serves full and
-    // edge tiles.  Stores are non-temporal: the output is written once and
-    // should not evict the operand panels other workgroups still stream
-    // through L2.
-    const int lr = lane & 31, lh = lane >> 5;
-    if constexpr (!SWI) {
-        if (S > 1) {
-            // K split: the item's raw sums to part[split][m][n] (int32 / fp32),
-            // through a buffer resource based at row m0 of the split whose
-            // range ends at the last valid row, as the fused epilogue below.
-            const uint32_t prow = static_cast<uint32_t>(N) * 4;
-            const __amdgpu_buffer_rsrc_t rp =
-                make_rsrc(static_cast<char*>(sk.part) + (static_cast<size_t>(split) * M + m0) * prow,
-                          min(M - m0, BM) * static_cast<int>(prow));
+        constexpr int OB = OUT == FKE_OUT_BF16 ? 2 : 4;  // output bytes per element
+        const uint32_t row_bytes = static_cast<uint32_t>(NO) * OB;
+        const __amdgpu_buffer_rsrc_t rc = make_rsrc(static_cast<char*>(p.C) + static_cast<size_t>(cur.m0) * row_bytes,
+                                                    min(M - cur.m0, BM) * static_cast<int>(row_bytes));
+        // This lane's epilogue operands, out of LDS into registers in one go:
+        // sa[i][g] = scale_a of tile rows wm*WM + 32i + 8g + 4*lh + 0..3, and
+        // scale_b / bias of tile column wn*WN + 32j + lane%32.
+        EpiOps<NI, NJ> eo;
+        eo.template read<TL::WM, TL::WN>(epi_sa[par], epi_sb[par], epi_bias[par], wm, wn, lane);
+        if constexpr (SWI) {
+            // SwiGLU: block j (gate) and j + NJ/2 (up) of the wave hold output
+            // column n0 + wn*WN/2 + 32*j + lane%32; h = swiglu_pair(g, u) of the
+            // two canonical epilogue values.
+            constexpr int WN = TL::WN;
 #pragma unroll
-            for (int j = 0; j < NJ; ++j) {
-                const int cn = wn * TL::WN + j * 32 + lr;
-                const uint32_t lane_off =
-                    n0 + cn < N ? static_cast<uint32_t>(wm * TL::WM + 4 * lh) * prow + static_cast<uint32_t>(n0 + cn) * 4
-                                : 0x80000000u;
+            for (int j = 0; j < NJ / 2; ++j) {
+                // tile columns wn*WN + 32j + lr (gate) and that + WN/2 (up)
+                const float sbg = eo.sb[j], sbu = eo.sb[j + NJ / 2];
+                const float bg = eo.bias[j], bu = eo.bias[j + NJ / 2];
+                const int o = cur.n0 + wn * (WN / 2) + j * 32 + lr;
+                const uint32_t lane_off = o < NO
+                    ? static_cast<uint32_t>(wm * TL::WM + 4 * lh) * row_bytes + static_cast<uint32_t>(o) * OB
+                    : 0x80000000u;
 #pragma unroll
                 for (int i = 0; i < NI; ++i) {
                     fence();
 #pragma unroll
-                    for (int g = 0; g < 4; ++g)
+                    for (int g = 0; g < 4; ++g) {
+                        const float sav[4] = {eo.sa[i][g][0], eo.sa[i][g][1], eo.sa[i][g][2], eo.sa[i][g][3]};
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
-                            const int voff = static_cast<int>(lane_off + static_cast<uint32_t>(i * 32 + 8 * g + e) * prow);
                             const int v = 4 * g + e;
-                            uint32_t bits;
-                            if constexpr (ELEM == ELEM_I8) bits = static_cast<uint32_t>(acc[i][j][v]);
-                            else bits = __float_as_uint(acc[i][j][v]);
-                            __builtin_amdgcn_raw_buffer_store_b32(bits, rp, voff, 0, 0);
+                            const int voff =
+                                static_cast<int>(lane_off + static_cast<uint32_t>(i * 32 + 8 * g + e) * row_bytes);
+                            const float yg = __builtin_fmaf(static_cast<float>(static_cast<int32_t>(acc_bits(acc[i][j], v))),
+                                                            sav[e] * sbg, bg);
+                            const float yu = __builtin_fmaf(
+                                static_cast<float>(static_cast<int32_t>(acc_bits(acc[i][j + NJ / 2], v))), sav[e] * sbu, bu);
+                            const float h = swiglu_pair(yg, yu);
+                            if constexpr (OUT == FKE_OUT_F32)
+                                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(h), rc, voff, 0, 2);
+                            else
+                                __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_rne(h), rc, voff, 0, 2);
                         }
+                    }
                 }
             }
-            continue;
+            return;
         }
-    }
-    constexpr int OB = OUT == FKE_OUT_BF16 ? 2 : 4;  // output bytes per element
-    const uint32_t row_bytes = static_cast<uint32_t>(NO) * OB;
-    const __amdgpu_buffer_rsrc_t rc = make_rsrc(static_cast<char*>(p.C) + static_cast<size_t>(m0) * row_bytes,
-                                                min(M - m0, BM) * static_cast<int>(row_bytes));
-    if constexpr (SWI) {
-        // SwiGLU: block j (gate) and j + NJ/2 (up) of the wave hold output
-        // column n0 + wn*WN/2 + 32*j + lane%32; h = swiglu_pair(g, u) of the
-        // two canonical epilogue values.
-        constexpr int WN = TL::WN;
 #pragma unroll
-        for (int j = 0; j < NJ / 2; ++j) {
-            const int cg = wn * WN + j * 32 + lr, cu = cg + WN / 2;  // tile columns of the gate / up rows
-            const float sbg = epi_sb[cg], sbu = epi_sb[cu];
-            const float bg = epi_bias[cg], bu = epi_bias[cu];
-            const int o = n0 + wn * (WN / 2) + j * 32 + lr;
-            const uint32_t lane_off = o < NO
-                ? static_cast<uint32_t>(wm * TL::WM + 4 * lh) * row_bytes + static_cast<uint32_t>(o) * OB
+        for (int j = 0; j < NJ; ++j) {
+            const int cn = wn * TL::WN + j * 32 + lr;  // column within the tile
+            const float sbn = eo.sb[j];
+            const float bn = eo.bias[j];
+            const uint32_t lane_off = cur.n0 + cn < N
+                ? static_cast<uint32_t>(wm * TL::WM + 4 * lh) * row_bytes + static_cast<uint32_t>(cur.n0 + cn) * OB
                 : 0x80000000u;
 #pragma unroll
             for (int i = 0; i < NI; ++i) {
                 fence();
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
-                    const int rm = wm * TL::WM + i * 32 + 8 * g + 4 * lh;
-                    const float4 sa4 = *reinterpret_cast<const float4*>(&epi_sa[rm]);
-                    const float sav[4] = {sa4.x, sa4.y, sa4.z, sa4.w};
+                    const float sav[4] = {eo.sa[i][g][0], eo.sa[i][g][1], eo.sa[i][g][2], eo.sa[i][g][3]};
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const int v = 4 * g + e;
-                        const int voff =
-                            static_cast<int>(lane_off + static_cast<uint32_t>(i * 32 + 8 * g + e) * row_bytes);
-                        const float yg = __builtin_fmaf(static_cast<float>(acc[i][j][v]), sav[e] * sbg, bg);
-                        const float yu = __builtin_fmaf(static_cast<float>(acc[i][j + NJ / 2][v]), sav[e] * sbu, bu);
-                        const float h = swiglu_pair(yg, yu);
+                        const int voff = static_cast<int>(lane_off + static_cast<uint32_t>(i * 32 + 8 * g + e) * row_bytes);
+                        float y;
+                        int32_t a = 0;
+                        if constexpr (ELEM == ELEM_I8) {
+                            a = static_cast<int32_t>(acc_bits(acc[i][j], v));
+                            y = __builtin_fmaf(static_cast<float>(a), sav[e] * sbn, bn);
+                        } else if constexpr (ELEM == ELEM_F8) {
+                            y = __builtin_fmaf(__uint_as_float(acc_bits(acc[i][j], v)), p.sa * p.sb, bn);
+                        } else {
+                            y = __builtin_fmaf(__uint_as_float(acc_bits(acc[i][j], v)), sav[e] * sbn, bn);
+                        }
                         if constexpr (OUT == FKE_OUT_F32)
-                            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(h), rc, voff, 0, 2);
+                            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(y), rc, voff, 0, 2);
+                        else if constexpr (OUT == FKE_OUT_BF16)
+                            __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_rne(y), rc, voff, 0, 2);
                         else
-                            __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_rne(h), rc, voff, 0, 2);
+                            __builtin_amdgcn_raw_buffer_store_b32(static_cast<uint32_t>(a), rc, voff, 0, 2);
                     }
                 }
             }
         }
-        continue;
-    }
+    };
+
+    // Persistent walk: workgroup b takes items b, b + G, b + 2G, ... (G = grid
+    // size, a multiple of the XCD count, so every tile of a workgroup stays on
+    // its XCD and each XCD walks its tile range in the same order as a
+    // one-tile-per-workgroup launch would).  The next item's first stages and
+    // epilogue operands are requested as soon as this item's K loop is done,
+    // ahead of its epilogue: they arrive while the epilogue runs, and the next
+    // K loop does not wait behind the epilogue's stores.
+    at_item(cur);
+    load_epi(cur, par);  // (issued before the stage copies: waited for with stage 0)
+    prologue_copies(cur.KT);
+    if (tid == 0) redo = 0;  // visible after the K loop's first barrier
+    bool after_epi = false;
+    for (;;) {
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-        const int cn = wn * TL::WN + j * 32 + lr;  // column within the tile
-        const float sbn = epi_sb[cn];
-        const float bn = epi_bias[cn];
-        const uint32_t lane_off = n0 + cn < N
-            ? static_cast<uint32_t>(wm * TL::WM + 4 * lh) * row_bytes + static_cast<uint32_t>(n0 + cn) * OB
-            : 0x80000000u;
+        for (int i = 0; i < NI; ++i)
 #pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            fence();
+            for (int j = 0; j < NJ; ++j)
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int rm = wm * TL::WM + i * 32 + 8 * g + 4 * lh;  // first of 4 consecutive tile rows
-                const float4 sa4 = *reinterpret_cast<const float4*>(&epi_sa[rm]);
-                const float sav[4] = {sa4.x, sa4.y, sa4.z, sa4.w};
+                for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
+
+        if constexpr (ELEM != ELEM_F8) {
+            k_loop(F{}, after_epi);
+        } else {
+            // E4M3 0x7F/0xFF are NaN to the MFMA but 0.0 to the reference.
+            // Clearing them costs ~5 VALU per operand word, more than the MFMAs
+            // can hide, and real quantizers never emit them (they saturate at
+            // 448).  So run the K loop on the raw codes first: every product is
+            // finite and no sum can overflow, so a NaN accumulator proves a
+            // NaN code in the tile's rows or columns.  Only then does the
+            // workgroup run the loop again with the codes cleared.
+            k_loop(F{}, after_epi);
+            float t = 0.0f;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int v = 4 * g + e;
-                    const int voff = static_cast<int>(lane_off + static_cast<uint32_t>(i * 32 + 8 * g + e) * row_bytes);
-                    float y;
-                    int32_t a = 0;
-                    if constexpr (ELEM == ELEM_I8) {
-                        a = acc[i][j][v];
-                        y = __builtin_fmaf(static_cast<float>(a), sav[e] * sbn, bn);
-                    } else if constexpr (ELEM == ELEM_F8) {
-                        y = __builtin_fmaf(acc[i][j][v], p.sa * p.sb, bn);
-                    } else {
-                        y = __builtin_fmaf(acc[i][j][v], sav[e] * sbn, bn);
-                    }
-                    if constexpr (OUT == FKE_OUT_F32)
-                        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(y), rc, voff, 0, 2);
-                    else if constexpr (OUT == FKE_OUT_BF16)
-                        __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_rne(y), rc, voff, 0, 2);
-                    else
-                        __builtin_amdgcn_raw_buffer_store_b32(static_cast<uint32_t>(a), rc, voff, 0, 2);
-                }
+            for (int i = 0; i < NI; ++i)
+#pragma unroll
+                for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) t += __uint_as_float(acc_bits(acc[i][j], v));
+            if (__builtin_isnan(t)) redo = 1;  // benign race: every writer stores 1
+            wait_lgkm0();
+            barrier();
+            if (redo) {
+#pragma unroll
+                for (int i = 0; i < NI; ++i)
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                        for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
+                prologue_copies(cur.KT);  // the copy plans still point at this item
+                k_loop(std::true_type{}, false);
             }
         }
-    }
+
+        const int next = slot + static_cast<int>(gridDim.x);
+        const bool more = next < items;
+        Item nx = cur;
+        if (more) {
+            nx = item_of(next);
+            at_item(nx);
+            load_epi(nx, par ^ 1);
+            prologue_copies(nx.KT);
+        }
+        epilogue();
+        if (!more) break;
+        barrier();  // every wave has read this item's redo flag
+        // redo = 0 for the next item, written by an inline ds_write: the compiler
+        // would hold its own LDS store until the copies in flight had landed
+        if (tid == 0) asm volatile("ds_write_b32 %0, %1" ::"v"((__attribute__((address_space(3))) int*)&redo), "v"(0)
+                                   : "memory");
+        cur = nx;
+        slot = next;
+        par ^= 1;
+        after_epi = true;
     }
 }
+
 
 // The second kernel of a K split: thread idx adds the S partial sums of output
 // idx = m * N + n in the order s = 0..S-1 (INT8: exact int32; FP8: fp32 in
