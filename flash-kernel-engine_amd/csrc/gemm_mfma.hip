@@ -438,6 +438,9 @@ __global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p
     const int gm = (M + BM - 1) / BM, gn = (NO + TC - 1) / TC;
     const int S = sk.S;
     const int items = gm * gn * S;
+    // K stages of BK bytes; the last holds KREM bytes when K % BK != 0 (K a
+    // multiple of 16): its chunks past K are cleared in LDS before it is read.
+    const int KTT = (K + BK - 1) / BK, KREM = K % BK;
     const int8_t* A = static_cast<const int8_t*>(p.A);
     const int8_t* B = static_cast<const int8_t*>(p.B);
 
@@ -455,7 +458,7 @@ __global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p
         it.m0 = (tm - it.split * gm) * BM;
         it.n0 = tn * TC;
         it.kt0 = it.split * sk.KS;
-        it.KT = S > 1 ? min(K / BK - it.kt0, sk.KS) : K / BK;
+        it.KT = S > 1 ? min(KTT - it.kt0, sk.KS) : KTT;
         return it;
     };
 
@@ -526,6 +529,32 @@ __global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p
         else if constexpr (BL == FKE_B_NK) pb.template issue<BNT ? 2 : 0>(q - PWA, ka * BK, b + TL::STAGE_A, wave);
         else pb.template issue<BNT ? 2 : 0>(q - PWA, ka, b + TL::STAGE_A, wave);
     };
+    // Stage kt of the current item, in `buf`, is the partial last stage of K:
+    // every lane clears the 16-byte chunks past K that its own copies put
+    // there (its copies have landed), then waits for its LDS writes, ahead of
+    // the barrier after which the stage is read.  A, and B in [N,K] order:
+    // the chunk's K offset is its logical chunk in the row; B in [K,N] order
+    // needs nothing (its rows past K fall outside B and read zero).
+    auto clear_tail = [&](uint8_t* buf, int kt) __attribute__((always_inline)) {
+        if (KREM == 0 || ckt0 + kt != KTT - 1) return;
+        const int rem = KREM >> 4;  // whole chunks of the stage inside K
+        const int4 z = {0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < PWA; ++i) {
+            const int r = (wave * PWA + i) * 8 + (lane >> 3);
+            if (((lane & 7) ^ swz(r)) >= rem) *reinterpret_cast<int4*>(buf + (wave * PWA + i) * 1024 + 16 * lane) = z;
+        }
+        if constexpr (BL == FKE_B_NK) {
+#pragma unroll
+            for (int i = 0; i < TL::PWB; ++i) {
+                const int r = (wave * TL::PWB + i) * 8 + (lane >> 3);
+                if (((lane & 7) ^ swz(r)) >= rem)
+                    *reinterpret_cast<int4*>(buf + TL::STAGE_A + (wave * TL::PWB + i) * 1024 + 16 * lane) = z;
+            }
+        }
+        wait_lgkm0();
+    };
+
     // A stage is NKS groups of NPIECE MFMAs (16 for the 256x256 tile).
     // Group g runs the MFMAs of one fragment set (g = 0: the previous stage's
     // last step, carried across the barrier; g > 0: step g-1) while the LDS
@@ -569,7 +598,10 @@ __global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p
     // Past the end the last stage is copied again (into a buffer whose stage
     // is done), so the body has no data-dependent branch.
     constexpr int NS = TL::NS;
-    auto stage = [&](auto sanc, const uint8_t* cbuf, uint8_t* nxt, int kt) __attribute__((always_inline)) {
+    // CLR: stage kt+1 may be the partial last stage (the last stages of the
+    // loop), whose tail is cleared before the barrier.
+    auto stage = [&](auto sanc, auto clrc, const uint8_t* cbuf, uint8_t* nxt, uint8_t* after, int kt)
+                     __attribute__((always_inline)) {
         const int kc = min(kt + NS - 1, cur.KT - 1);
         using S = decltype(sanc);
         if constexpr (NKS == 4) {
@@ -595,6 +627,7 @@ __global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p
         }
         wait_lgkm0();                  // last step's fragments in registers (f1): cbuf may be overwritten after the barrier
         wait_vm<(NS - 2) * NSLOT>();   // this wave's share of stage kt+1 has landed (later stages may be in flight)
+        if constexpr (decltype(clrc)::value) clear_tail(after, kt + 1);  // stage kt+1 is in `after`
         barrier();
     };
 
@@ -633,6 +666,7 @@ __global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p
         wait_lgkm0();
         if (after_epi) wait_vm<WAIT0_AFTER_EPI>();  // stage 0 has landed
         else wait_vm<WAIT0>();
+        clear_tail(lds0, 0);
         barrier();
         // f1 (the carried set) starts at zero.
 #pragma unroll
@@ -641,22 +675,29 @@ __global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p
         for (int j = 0; j < NJ; ++j) f1.b[j] = typename Mma<ELEM>::Frag{};
         const int KT = cur.KT;
         int kt = 0;
+        using T = std::true_type;
+        // The loop runs the stages whose next stage is not the item's last;
+        // the last few stages follow it, with the partial-stage check.
         if constexpr (NS == 2) {
-            for (; kt + 2 <= KT; kt += 2) {
-                stage(S{}, lds0, lds1, kt);
-                stage(S{}, lds1, lds0, kt + 1);
+            for (; kt + 4 <= KT; kt += 2) {
+                stage(S{}, F{}, lds0, lds1, lds1, kt);
+                stage(S{}, F{}, lds1, lds0, lds0, kt + 1);
             }
-            if (kt < KT) stage(S{}, lds0, lds1, kt);  // odd stage count
+            if (kt < KT) stage(S{}, T{}, lds0, lds1, lds1, kt);
+            if (kt + 1 < KT) stage(S{}, T{}, lds1, lds0, lds0, kt + 1);
+            if (kt + 2 < KT) stage(S{}, T{}, lds0, lds1, lds1, kt + 2);
         } else {
-            for (; kt + 4 <= KT; kt += 4) {
-                stage(S{}, lds0, lds3, kt);
-                stage(S{}, lds1, lds0, kt + 1);
-                stage(S{}, lds2, lds1, kt + 2);
-                stage(S{}, lds3, lds2, kt + 3);
+            for (; kt + 6 <= KT; kt += 4) {
+                stage(S{}, F{}, lds0, lds3, lds1, kt);
+                stage(S{}, F{}, lds1, lds0, lds2, kt + 1);
+                stage(S{}, F{}, lds2, lds1, lds3, kt + 2);
+                stage(S{}, F{}, lds3, lds2, lds0, kt + 3);
             }
-            if (kt < KT) stage(S{}, lds0, lds3, kt);  // stage counts not a multiple of 4
-            if (kt + 1 < KT) stage(S{}, lds1, lds0, kt + 1);
-            if (kt + 2 < KT) stage(S{}, lds2, lds1, kt + 2);
+            if (kt < KT) stage(S{}, T{}, lds0, lds3, lds1, kt);
+            if (kt + 1 < KT) stage(S{}, T{}, lds1, lds0, lds2, kt + 1);
+            if (kt + 2 < KT) stage(S{}, T{}, lds2, lds1, lds3, kt + 2);
+            if (kt + 3 < KT) stage(S{}, T{}, lds3, lds2, lds0, kt + 3);
+            if (kt + 4 < KT) stage(S{}, T{}, lds0, lds3, lds1, kt + 4);
             wait_vm0();  // the re-copies of the last stage have landed, in every wave
             barrier();
         }
@@ -984,7 +1025,8 @@ int device_cus() {
 bool mfma_supports(const GemmArgs& p, int elem) {
     const uintptr_t a = reinterpret_cast<uintptr_t>(p.A), b = reinterpret_cast<uintptr_t>(p.B);
     const int64_t kb = static_cast<int64_t>(p.K) * elem_bytes(elem);  // K bytes per row
-    if (p.M < 1 || p.N < 1 || kb < BK || kb % BK != 0) return false;
+    // rows start 16-byte aligned; a last stage shorter than BK is cleared past K
+    if (p.M < 1 || p.N < 1 || kb < 16 || kb % 16 != 0) return false;
     if ((a | b) & 15) return false;
     // per-lane DMA offsets are 32-bit: (rows - 1) * K + K must fit
     if (p.M * kb > INT32_MAX) return false;
@@ -1131,7 +1173,7 @@ size_t mfma_split_bytes(const GemmArgs& p, int S) {
 MfmaPlan mfma_plan(const GemmArgs& p, int elem, int cus) {
     MfmaPlan pl{mfma_pick_tile(p, cus), 1, 0};
     if (p.swiglu || elem_bytes(elem) != 1) return pl;
-    const int KT = p.K / BK;
+    const int KT = static_cast<int>((static_cast<int64_t>(p.K) * elem_bytes(elem) + BK - 1) / BK);
     double base = mfma_unsplit_estimate_us(p, cus);
     if (pl.tile == MFMA_TILE_64x64_RING4 || pl.tile == MFMA_TILE_128x64_RING4 || pl.tile == MFMA_TILE_128x128_RING4) {
         const int bm = ring_bm(pl.tile), bn = ring_bn(pl.tile);
@@ -1171,7 +1213,7 @@ hipError_t launch_mfma(const GemmArgs& p, int elem, hipStream_t s, int tile, con
     if (sk.S < 1 || sk.S > kSplitMax) return hipErrorInvalidValue;
     if (sk.S > 1) {  // every split has stages: the last starts before K ends
         if (p.swiglu || elem_bytes(elem) != 1 || sk.part == nullptr || sk.KS < 1) return hipErrorInvalidValue;
-        if (static_cast<int64_t>(sk.S - 1) * sk.KS >= p.K / BK) return hipErrorInvalidValue;
+        if (static_cast<int64_t>(sk.S - 1) * sk.KS >= (p.K + BK - 1) / BK) return hipErrorInvalidValue;
     }
     if (elem == ELEM_F16 || elem == ELEM_BF16) {
         GemmArgs q = p;

@@ -163,10 +163,11 @@ def test_half_gemm_rejects_bad_arguments_and_dispatch():
     sel = L.fke_select_path_half
     assert sel(P, P, P, 8192, 8192, 8192, BF16, 0, 0) == _lib.PATH_MFMA
     assert sel(P, P, P, 1, 4096, 4096, F16, 1, 0) == _lib.PATH_MFMA
-    assert sel(P, P, P, 256, 256, 96, F16, 0, 0) == _lib.PATH_GENERIC      # K % 64
+    assert sel(P, P, P, 256, 256, 96, F16, 0, 0) == _lib.PATH_MFMA         # 192 K bytes: a partial last stage
+    assert sel(P, P, P, 256, 256, 100, F16, 0, 0) == _lib.PATH_GENERIC     # 200 K bytes: K % 8 != 0
     assert sel(P, P, P, 256, 256, 256, F16, 0, 1) == _lib.PATH_GENERIC     # B [K,N]
     assert sel(P + 2, P, P, 256, 256, 256, F16, 0, 0) == _lib.PATH_GENERIC
-    assert L.fke_gemm_half_on_path(_lib.PATH_MFMA, P, P, P, 64, 64, 96, F16, None, None, 1.0, 1.0, None, 0, 0,
+    assert L.fke_gemm_half_on_path(_lib.PATH_MFMA, P, P, P, 64, 64, 100, F16, None, None, 1.0, 1.0, None, 0, 0,
                                    None) == INVALID
     assert L.fke_gemm_half_on_path(_lib.PATH_GEMV, P, P, P, 1, 64, 64, F16, None, None, 1.0, 1.0, None, 0, 0,
                                    None) == INVALID
@@ -278,7 +279,7 @@ def test_path_unavailable_for_shape_is_rejected():
     (384, 4096, 14336, 0, _lib.PATH_MFMA),
     (512, 4096, 14336, 0, _lib.PATH_MFMA),
     (17, 14336, 1024, 0, _lib.PATH_MFMA),    # K < 2048: no streamed batch kernel
-    (100, 4096, 2112, 0, _lib.PATH_GEMV),    # K % 128 != 0: no MFMA GEMM, the streamed kernel takes it
+    (100, 4096, 2112, 0, _lib.PATH_MFMA),    # K % 128 != 0: the MFMA GEMM, its last K stage cleared past K
     (17, 14336, 4096, 1, _lib.PATH_MFMA),
     (4096, 11008, 4096, 0, _lib.PATH_MFMA),
     (8192, 8192, 8192, 0, _lib.PATH_MFMA),
@@ -290,7 +291,10 @@ def test_path_unavailable_for_shape_is_rejected():
     (17, 4096, 4096, 1, _lib.PATH_MFMA),
     (64, 64, 100, 0, _lib.PATH_GENERIC),
     (64, 64, 4, 0, _lib.PATH_GENERIC),
-    (8, 64, 96, 0, _lib.PATH_GENERIC),
+    (8, 64, 96, 0, _lib.PATH_MFMA),          # K of 6 16-byte chunks: one partial stage
+    (8, 64, 104, 0, _lib.PATH_GENERIC),      # K % 16 != 0: rows not 16-byte aligned
+    (300, 520, 4104, 0, _lib.PATH_GENERIC),
+    (300, 520, 4112, 0, _lib.PATH_MFMA),
 ])
 def test_dispatch_i8(M, N, K, layout, expect):
     assert _lib.lib().fke_select_path_i8(P, P, P, M, N, K, 0, layout) == expect
@@ -313,7 +317,8 @@ def test_dispatch_unaligned_pointer_falls_back():
     (1, 14336, 4096, 1, _lib.PATH_GEMV),      # B [K,N] (the reference layout): transposing decode kernel
     (16, 14336, 4096, 1, _lib.PATH_GEMV),
     (17, 14336, 4096, 1, _lib.PATH_MFMA),
-    (4, 14336, 4000, 1, _lib.PATH_GENERIC),   # K % 64 != 0
+    (4, 14336, 4000, 1, _lib.PATH_MFMA),      # K % 64 != 0: not the decode kernel; the MFMA GEMM (K % 16 == 0)
+    (4, 14336, 4004, 1, _lib.PATH_GENERIC),   # K % 16 != 0
     (8192, 8192, 8192, 0, _lib.PATH_MFMA),
     (4, 14336, 1024, 0, _lib.PATH_MFMA),      # K < 2048
     (4, 300, 2112, 0, _lib.PATH_GEMV),        # K % 128 != 0: no MFMA GEMM

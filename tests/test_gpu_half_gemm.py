@@ -85,7 +85,9 @@ def epi_vectors(M, N, seed):
             r.standard_normal(N).astype(np.float32))
 
 
-MFMA_SHAPES = [(256, 256, 64), (300, 200, 512), (513, 333, 384), (1, 100, 128), (40, 1000, 64)]
+MFMA_SHAPES = [(256, 256, 64), (300, 200, 512), (513, 333, 384), (1, 100, 128), (40, 1000, 64),
+               # K % 64 != 0 (K % 8 == 0): a partial last stage, cleared past K
+               (129, 70, 8), (256, 256, 72), (300, 200, 1000)]
 
 
 @pytest.mark.parametrize("dt", ["f16", "bf16"])

@@ -766,6 +766,70 @@ def test_mfma_few_tile_shapes_full(oracle, dev, M, N, K, out, want):
         assert_same(gpu_i8(A, B, "nk", out, "gemv", sa, sb, bias=bias), ref, f"gemv {M}x{N}x{K}")
 
 
+# K % 128 != 0 on the MFMA GEMM (K a multiple of 16): the last stage is
+# partial and its chunks past K are cleared in LDS.  One and several stages,
+# ragged M and N, both layouts.
+PARTIAL_K_SHAPES = [(129, 65, 16), (257, 129, 144), (64, 4000, 2880), (300, 520, 4160), (513, 1040, 1040)]
+
+
+@pytest.mark.parametrize("tile", SMALL_TILES + ["mfma_256x256", "mfma"])
+@pytest.mark.parametrize("layout", ["nk", "kn"])
+@pytest.mark.parametrize("shape", PARTIAL_K_SHAPES)
+def test_mfma_partial_last_stage_i8(oracle, dev, tile, layout, shape):
+    """INT8 with K % 128 != 0 on every MFMA tile: int32, fp32 and bf16
+    outputs bit-exact against the oracle."""
+    M, N, K = shape
+    if layout == "kn":
+        N = (N + 15) // 16 * 16
+    say("i8 partial last stage", tile, layout, (M, N, K))
+    A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 17000 + K, layout, act="normal")
+    acc = oracle.w8a8_acc(A, B, oracle.B_NK if layout == "nk" else oracle.B_KN, nthreads=NTH)
+    for out in ("i32", "f32", "bf16"):
+        got = gpu_i8(A, B, layout, out, tile, sa, sb, bias=bias)
+        assert_same(got, oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, out), f"{tile} {layout} {(M, N, K)} {out}")
+
+
+@pytest.mark.parametrize("layout", ["nk", "kn"])
+@pytest.mark.parametrize("shape", PARTIAL_K_SHAPES)
+def test_mfma_partial_last_stage_fp8(oracle, dev, layout, shape):
+    """FP8 with K % 128 != 0 (0x7F / 0xFF codes included): every pinned tile
+    gives the same bits (they sum K in the same stages and steps), within the
+    FP8 bars of the reference's sequential sum, as is the dispatcher's choice
+    (which may split K, and so add in another order)."""
+    M, N, K = shape
+    if layout == "kn":
+        N = (N + 15) // 16 * 16
+    say("f8 partial last stage", layout, (M, N, K))
+    A, B, sa, sb = f8_inputs(oracle, M, N, K, 17500 + K, layout, with_nan_codes=True)
+    ref = oracle.f8_gemm(A, B, sa, sb, b_layout=oracle.B_KN if layout == "kn" else oracle.B_NK, nthreads=NTH)
+    first = gpu_f8(A, B, sa, sb, layout, "f32", "mfma_256x256")
+    assert_fp8_close(first, ref, "f32", f"partial stage {layout} {(M, N, K)}")
+    for tile in SMALL_TILES:
+        assert_same(gpu_f8(A, B, sa, sb, layout, "f32", tile), first, f"{tile} {layout} {(M, N, K)}")
+    assert_fp8_close(gpu_f8(A, B, sa, sb, layout, "f32", "mfma"), ref, "f32", f"auto {layout} {(M, N, K)}")
+
+
+@pytest.mark.parametrize("M,N,K,layout", [(64, 4096, 14352, "nk"), (100, 1000, 14736, "nk"),
+                                          (200, 2000, 8208, "kn")])
+def test_mfma_k_split_partial_last_stage(oracle, dev, M, N, K, layout):
+    """A K split whose last split ends in the partial stage: int32 and bf16
+    bit-exact against the oracle; FP8 within its bars and the same bits on
+    every call."""
+    S, tile = mfma_split_of(M, N, K, layout)
+    say("mfma k split, partial last stage", M, N, K, layout, "splits", S)
+    assert S > 1
+    A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 17800 + M, layout=layout)
+    acc = oracle.w8a8_acc(A, B, oracle.B_KN if layout == "kn" else oracle.B_NK, nthreads=NTH)
+    assert_same(gpu_i8(A, B, layout, "i32", path="mfma"), acc, f"split {(M, N, K)} i32")
+    ref = oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, "bf16")
+    assert_same(gpu_i8(A, B, layout, "bf16", "mfma", sa, sb, bias=bias), ref, f"split {(M, N, K)} bf16")
+    A8, B8, s8a, s8b = f8_inputs(oracle, M, N, K, 17900 + M, layout, with_nan_codes=True)
+    ref8 = oracle.f8_gemm(A8, B8, s8a, s8b, b_layout=oracle.B_KN if layout == "kn" else oracle.B_NK, nthreads=NTH)
+    got8 = gpu_f8(A8, B8, s8a, s8b, layout, "f32", "mfma")
+    assert_fp8_close(got8, ref8, "f32", f"split fp8 {(M, N, K)}")
+    assert_same(gpu_f8(A8, B8, s8a, s8b, layout, "f32", "mfma"), got8, "split fp8 repeat")
+
+
 def mfma_split_of(M, N, K, layout):
     t = ctypes.c_int(0)
     S = _lib.lib().fke_select_mfma_split(M, N, K, _lib.B_KN if layout == "kn" else _lib.B_NK, 256,
