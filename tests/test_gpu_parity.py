@@ -830,6 +830,38 @@ def test_mfma_k_split_partial_last_stage(oracle, dev, M, N, K, layout):
     assert_same(gpu_f8(A8, B8, s8a, s8b, layout, "f32", "mfma"), got8, "split fp8 repeat")
 
 
+@pytest.mark.parametrize("path", ["mfma", "gemv", "generic"])
+def test_bf16_rounding_of_epilogue_values(oracle, dev, path):
+    """The bf16 output's rounding on chosen fp32 values: with A all zero the
+    epilogue value is fmaf(0, s, bias[n]) = bias[n] exactly, so the bias
+    carries the patterns (halfway cases of both parities, values just off
+    them, fp32 denormals and the largest finite values, both signs, and 4096
+    random finite patterns); every output equals the oracle's round to
+    nearest even, bit for bit, on each kernel family."""
+    r = np.random.default_rng(21)
+    pats = []
+    for hi in (0x3F80, 0x3F81, 0x4B7F, 0x0001, 0x007F, 0x7F7F, 0x0080):
+        for lo in (0x8000, 0x7FFF, 0x8001, 0x0000, 0xFFFF):
+            pats.append((hi << 16) | lo)
+    pats += [1, 2, 0x7FFFFF, 0x7F7FFFFF, 0x00800000]
+    pats = np.array(pats, dtype=np.uint32)
+    pats = np.concatenate([pats, pats | 0x80000000])
+    rnd = r.integers(0, 2**32, 4096, dtype=np.uint64).astype(np.uint32)
+    rnd = rnd[(rnd & 0x7F800000) != 0x7F800000]  # finite
+    bias = np.concatenate([pats, rnd]).view(np.float32)
+    M, K = (4, 4096) if path == "gemv" else (40, 512)
+    N = (bias.size + 15) // 16 * 16
+    bias = np.concatenate([bias, np.zeros(N - bias.size, np.float32)])
+    say("bf16 rounding", path, M, N, K)
+    A = np.zeros((M, K), np.int8)
+    B = oracle.gen_i8_uniform((N, K), 22)
+    sa = oracle.gen_f32_uniform((M,), 23, 0.001, 0.02)
+    sb = oracle.gen_f32_uniform((N,), 24, 0.001, 0.02)
+    acc = np.zeros((M, N), np.int32)
+    ref = oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, "bf16")
+    assert_same(gpu_i8(A, B, "nk", "bf16", path, sa, sb, bias=bias), ref, f"bf16 rounding {path}")
+
+
 def mfma_split_of(M, N, K, layout):
     t = ctypes.c_int(0)
     S = _lib.lib().fke_select_mfma_split(M, N, K, _lib.B_KN if layout == "kn" else _lib.B_NK, 256,
