@@ -7,7 +7,10 @@ throughput in TOPS.  The decode GEMV (bf16 out + fused bias, weights rotated
 over 8 distinct 56 MiB buffers so the 256 MiB MALL cannot hold them) is timed in
 the same run and reported under "decode_gemv", and the M=16 decode (the other
 end of the decode configs) under "decode_gemv_m16", and a 64-row batch on the
-same weights (the batched decode kernel) under "decode_batch_m64".  The other
+same weights (the batched decode kernel) under "decode_batch_m64".  Beside
+them, "hbm_read_floor" is the fastest plain read of the same 56 MiB on the same
+box (a kernel that only loads, several grid shapes), and each decode line's
+"of_read_floor" is that time over its own.  The other
 two GEMM configurations of the benchmark set sit in the same line with their
 own rooflines: "c3" (prefill 4096x11008x4096, bf16 out) and "c5" (FP8 e4m3
 8192^3, B [K,N] as the reference's launcher reads it, operands drawn as fp32
@@ -196,6 +199,11 @@ def main():
     # the same decode with B stored [K,N], the layout of the reference's Python op
     gemv_kn1 = gemv_bench(torch, L, _lib, dev, gen, 1, args.gemv_buffers, args.gemv_launches, layout="kn")
     gemv_kn16 = gemv_bench(torch, L, _lib, dev, gen, 16, args.gemv_buffers, args.gemv_launches, layout="kn")
+    # the fastest plain read of the same weight bytes on this box, and each decode line against it
+    floor = read_floor(torch, dev, gen, 14336 * 4096, args.gemv_buffers, args.gemv_launches)
+    for d in (gemv, gemv16, gemv_kn1, gemv_kn16):
+        d["read_floor_us"] = floor["us"]
+        d["of_read_floor"] = round(floor["us"] / d["us_per_launch"], 4)
 
     line = {
         "metric": "INT8 TOPS at 8192^3 + HBM GB/s at M=1 decode GEMV (N=14336,K=4096)",
@@ -227,6 +235,7 @@ def main():
         "decode_batch_m64": batch64,
         "decode_gemv_b_kn": gemv_kn1,
         "decode_gemv_m16_b_kn": gemv_kn16,
+        "hbm_read_floor": floor,
         "timed_wall_s": round(wall, 3),
     }
     line["hbm_copy_GBps"] = copy_bandwidth(torch, dev, gen)
@@ -436,6 +445,46 @@ def copy_bandwidth(torch, dev, gen):
     gbs = 2.0 * (1 << 30) * 10 / (e0.elapsed_time(e1) * 1e-3) / 1e9
     del src, dst
     return round(gbs, 1)
+
+
+def read_floor(torch, dev, gen, nbytes, nbuf, launches):
+    """The fastest plain read of `nbytes` this box sustains: a kernel that only
+    loads (csrc/probe_read.hip: 1 KiB per load instruction, non-temporal, one
+    folded value per lane kept live, nothing stored), on `nbuf` rotating random
+    buffers from a HIP graph of `launches` launches like the decode lines, over a
+    few grid shapes - the decode row kernel's (one 4 KiB block per wave, two
+    waves per workgroup), one 8 KiB block per wave, and persistent grids of one
+    or two workgroups per CU.  The decode GEMV reads its weights once, so this
+    is the attainable floor beside the 8.0 TB/s specification."""
+    import ctypes as ct
+    P = ct.CDLL(os.path.join(PKG, "lib", "libfke_probe.so"))
+    P.fke_probe_read_out_elems.argtypes = [ct.c_int, ct.c_int]
+    P.fke_probe_read_out_elems.restype = ct.c_size_t
+    P.fke_probe_read.argtypes = [ct.c_void_p, ct.c_int64, ct.c_void_p, ct.c_int, ct.c_int, ct.c_int, ct.c_int32,
+                                 ct.c_void_p]
+    P.fke_probe_read.restype = ct.c_int
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    bufs = [torch.randint(-127, 128, (nbytes,), dtype=torch.int8, device=dev, generator=gen) for _ in range(nbuf)]
+    kib = nbytes // 1024
+    shapes = {"4KiB_per_wave_2_waves": (4, 2, kib // 8), "8KiB_per_wave_4_waves": (8, 4, kib // 32),
+              "persistent_2_per_cu_4_waves": (8, 4, 2 * cus), "persistent_1_per_cu_8_waves": (8, 8, cus)}
+    res = {"bytes": nbytes, "buffers": nbuf}
+    best = None
+    for name, (unit, waves, grid) in shapes.items():
+        out = torch.empty(P.fke_probe_read_out_elems(grid, waves), dtype=torch.int32, device=dev)
+
+        def launch(i, st, unit=unit, waves=waves, grid=grid, out=out):
+            r = P.fke_probe_read(bufs[i % nbuf].data_ptr(), nbytes, out.data_ptr(), grid, waves, unit, 0x7F7F7F7F, st)
+            if r:
+                raise RuntimeError(f"fke_probe_read failed: status {r}")
+        us = graph_us(torch, dev, launch, launches, 2 * nbuf)
+        res[name] = round(us, 3)
+        best = us if best is None else min(best, us)
+    res["us"] = round(best, 3)
+    res["GB/s"] = round(nbytes / best / 1e3, 1)
+    res["frac_of_spec"] = round(nbytes / best / 1e3 / PEAK_HBM_GBS, 4)
+    del bufs
+    return res
 
 
 def gemv_bytes(M, N, K, out_bytes=2, bias=True):

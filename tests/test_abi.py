@@ -482,3 +482,24 @@ def test_split_plans_fit_one_pool_slot(layout):
                 assert ws <= cap, (M, N, K, layout, ws)
                 seen_cap |= ws > cap // 2
     assert seen_cap
+
+
+def test_probe_library_exports_and_argument_checks():
+    """The measurement probes bench.py loads (libfke_probe.so, not part of the
+    C ABI) export their entry points, and the read probe turns bad arguments
+    into hipErrorInvalidValue before any launch."""
+    path = os.path.join(os.path.dirname(_lib.LIB_PATH), "libfke_probe.so")
+    probe = ct.CDLL(path)
+    for name in ("fke_probe_mfma_i8", "fke_probe_mfma_src_bytes", "fke_probe_mfma_out_elems", "fke_probe_read",
+                 "fke_probe_read_out_elems"):
+        assert hasattr(probe, name), name
+    probe.fke_probe_read.argtypes = [ct.c_void_p, ct.c_int64, ct.c_void_p, ct.c_int, ct.c_int, ct.c_int, ct.c_int32,
+                                 ct.c_void_p]
+    probe.fke_probe_read.restype = ct.c_int
+    probe.fke_probe_read_out_elems.argtypes = [ct.c_int, ct.c_int]
+    probe.fke_probe_read_out_elems.restype = ct.c_size_t
+    assert probe.fke_probe_read_out_elems(256, 4) == 1024
+    bad = [(None, 4096, P, 1, 1, 4), (P, 4096, None, 1, 1, 4), (P, 4096, P, 0, 1, 4), (P, 4096, P, 1, 9, 4),
+           (P, 4096, P, 1, 1, 2), (P, 4096 + 16, P, 1, 1, 4), (P, 1 << 31, P, 1, 1, 8), (P, 0, P, 1, 1, 4)]
+    for src, n, out, grid, waves, unit in bad:
+        assert probe.fke_probe_read(src, n, out, grid, waves, unit, 0, None) == _lib.HIP_ERROR_INVALID_VALUE
