@@ -426,6 +426,63 @@ def test_gemv_kn_graph_replays(oracle, dev):
         assert torch.equal(other, other2)
 
 
+def test_graph_replays_every_nk_family(oracle, dev):
+    """One HIP graph holding, with B [N,K], the row kernel (M = 1), the
+    LDS-streamed decode (M = 16), the MFMA GEMM, its K split (first kernel and
+    the kernel that adds the splits, on the stream's pool slot) and the FP8
+    decode: three replays with eager calls on other inputs between them, every
+    replay checked against the oracle (INT8 bit-exact; FP8 within the FP8 bar
+    and bit-identical from replay to replay)."""
+    L = _lib.lib()
+    tile = ctypes.c_int(0)
+    assert L.fke_select_mfma_split(100, 1000, 14720, _lib.B_NK, 0, ctypes.byref(tile)) > 1  # the K split shape
+    cases = [(1, 4096, 4096, "bf16"), (16, 4096, 4096, "bf16"), (300, 512, 1024, "f32"), (100, 1000, 14720, "bf16")]
+    data, refs, others = [], [], []
+    for i, (M, N, K, out) in enumerate(cases):
+        say("graph replays", M, N, K, out)
+        A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 9400 + 10 * i, act="normal")
+        refs.append(oracle_out(oracle, oracle.w8a8_acc(A, B, oracle.B_NK, nthreads=NTH), sa, sb, 1.0, 1.0, bias, out))
+        data.append([dev_t(x) for x in (A, B, sa, sb, bias)])
+        A2, B2, sa2, sb2, bias2 = inputs_i8(oracle, M, N, K, 9405 + 10 * i, act="normal")
+        others.append([dev_t(x) for x in (A2, B2, sa2, sb2, bias2)])
+    qa, qb, fsa, fsb = f8_inputs(oracle, 8, 2048, 4096, 9480, layout="nk")
+    f8_ref = oracle.f8_gemm(qa, qb, fsa, fsb, None, oracle.OUT_F32, oracle.B_NK, nthreads=NTH)
+    dqa, dqb = dev_t(qa), dev_t(qb)
+
+    def run_all(ins):
+        outs = [ops.w8a8_gemm(*d[:2], d[2], d[3], d[4], out_dtype=OUT_T[c[3]]) for d, c in zip(ins, cases)]
+        outs.append(ops.fp8_gemm_scaled(dqa, dqb, fsa, fsb, None, out_dtype=torch.float32, b_layout="nk"))
+        return outs
+
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):  # eager first: the stream takes its pool slot, the capture reuses it
+        run_all(data)
+    s.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        outs = run_all(data)
+    f8_first = None
+    for r in range(3):
+        for o in outs:
+            o.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for o, ref, c in zip(outs, refs, cases):
+            assert_same(host(o), ref, f"replay {r} {c}")
+        f8 = host(outs[-1])
+        assert_fp8_close(f8, f8_ref, "f32", f"replay {r} fp8 decode")
+        if f8_first is None:
+            f8_first = f8
+        assert np.array_equal(f8.view(np.uint32), f8_first.view(np.uint32)), f"replay {r}: fp8 bits changed"
+        eager = run_all(others)  # other inputs, eagerly, on the current stream
+        torch.cuda.synchronize()
+        again = run_all(others)
+        torch.cuda.synchronize()
+        for a, b in zip(eager[:-1], again[:-1]):
+            assert torch.equal(a, b)
+
+
 def test_gemv_kn_two_streams(oracle, dev):
     """[K,N] decodes of different inputs on two streams at once, each on its
     stream's slot of the split pool: both bit-exact."""
