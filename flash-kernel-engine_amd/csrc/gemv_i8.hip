@@ -17,7 +17,8 @@
 //    activation chunks in registers for the NB rows, and reduces its partial
 //    sums with DPP row rotations, one ds_swizzle and two readlanes - no LDS
 //    and no barrier, so a wave retires as soon as its rows are done and the
-//    load queue never drains.
+//    load queue never drains.  Also the FP8 decode at M = 1 (E4M3 codes
+//    converted to fp32 in registers, fp32 FMAs).
 //  * gemv_i8_kernel (5 <= M <= 16 when neither MFMA kernel's 32-bit offsets
 //    reach), described below; it amortises the activation chunks over R
 //    rows per wave.
@@ -152,6 +153,39 @@ __device__ __forceinline__ int32_t wave_sum(int32_t v) {
     return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 32);
 }
 
+// The same sum in fp32, in the same fixed order (FP8 row kernel).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float wave_sum_f32(float v) {
+    v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f32<0x124>(v);  // row_ror:4
+    v += dpp_f32<0x128>(v);  // row_ror:8
+    v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));  // bit mode, xor 16
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)) +
+           __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+}
+
+typedef float v2f __attribute__((ext_vector_type(2)));
+
+// E4M3 codes -> fp32 with gfx950's v_cvt_pk_f32_fp8 (two codes per
+// instruction; checked against the reference's decode, src/quantized_gemm.cu:
+// 81-97, on all 256 codes: identical, except 0x7F / 0xFF, which it turns into
+// NaN where the reference reads 0.0 - see e4m3_sanitize).  16 codes of one
+// 16-byte chunk, in byte order.
+__device__ __forceinline__ void e4m3_chunk_to_f32(v4i c, float (&f)[16]) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const v2f lo = __builtin_amdgcn_cvt_pk_f32_fp8(c[e], false), hi = __builtin_amdgcn_cvt_pk_f32_fp8(c[e], true);
+        f[4 * e] = lo.x;
+        f[4 * e + 1] = lo.y;
+        f[4 * e + 2] = hi.x;
+        f[4 * e + 3] = hi.y;
+    }
+}
+
 constexpr int ROWS_WAVES = 2;  // waves per workgroup of gemv_rows_kernel
 // Weight rows per wave of the plain kernel.  One: at N = 14336, K = 4096 the
 // launch is bounded by its ramp and drain, and 2 / 4 / 8 rows per wave
@@ -163,10 +197,21 @@ constexpr int ROWS_NB = 1;
 // wave stores swiglu_pair of the two epilogue values).
 // FULLK: K is a multiple of 4096, so every 256-chunk block is whole: the
 // activation chunks come with plain loads and no offset needs the 2^31 guard.
-template <int MT, int OUT, bool FULLK, int NB, bool SWI = false>
+// EL = ELEM_F8 (E4M3 codes, M = 1; plain GEMM, fp32 / bf16 out): each lane
+// turns its codes into fp32 with v_cvt_pk_f32_fp8 and sums the exact products
+// with fp32 FMAs in a fixed order (its chunks in order, then the wave sum), so
+// the result is the same on every call.  Codes 0x7F / 0xFF are NaN to the
+// conversion but 0.0 to the reference: the stream runs on the raw codes (no
+// sum of finite E4M3 products overflows fp32, so a NaN total proves such a
+// code in the row or in the activations) and a wave whose total comes out NaN
+// streams its row again with those codes cleared.
+template <int MT, int OUT, bool FULLK, int NB, bool SWI = false, int EL = ELEM_I8>
 __global__ __launch_bounds__(ROWS_WAVES * 64) void gemv_rows_kernel(GemmArgs p) {
+    constexpr bool F8 = EL == ELEM_F8;
     static_assert(!SWI || NB == 2, "SwiGLU streams one gate and one up row");
     static_assert(MT * NB <= 64, "one storing lane per output");
+    static_assert(!F8 || (MT == 1 && NB == 1 && !SWI && OUT != FKE_OUT_I32), "FP8: M = 1, fp32 or bf16 out");
+    using Acc = typename std::conditional<F8, float, int32_t>::type;
     const int lane = threadIdx.x & 63;
     const int NO = SWI ? p.N >> 1 : p.N;           // output columns
     const int NU = SWI ? NO : (p.N + NB - 1) / NB;  // waves with work
@@ -210,11 +255,13 @@ __global__ __launch_bounds__(ROWS_WAVES * 64) void gemv_rows_kernel(GemmArgs p) 
     float sam[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) sam[m] = p.scale_a ? p.scale_a[m < M ? m : 0] : p.sa;
-    int32_t acc[NB][MT];
+    Acc acc[NB][MT];
+    auto stream = [&](auto clear_c) __attribute__((always_inline)) {
+    constexpr bool clear = decltype(clear_c)::value;
 #pragma unroll
     for (int q = 0; q < NB; ++q)
 #pragma unroll
-        for (int m = 0; m < MT; ++m) acc[q][m] = 0;
+        for (int m = 0; m < MT; ++m) acc[q][m] = Acc(0);
     int blk = 0;
     do {
         int off[4];
@@ -240,18 +287,51 @@ __global__ __launch_bounds__(ROWS_WAVES * 64) void gemv_rows_kernel(GemmArgs p) 
                     a[m][u] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(ra[m], off[u], 0, 0));
                 }
             }
+        if constexpr (F8) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                v4i ac = a[0][u], bc = b[0][u];
+                if constexpr (clear) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        ac[e] = static_cast<int>(e4m3_sanitize(static_cast<uint32_t>(ac[e])));
+                        bc[e] = static_cast<int>(e4m3_sanitize(static_cast<uint32_t>(bc[e])));
+                    }
+                }
+                float af[16], bf[16];
+                e4m3_chunk_to_f32(ac, af);
+                e4m3_chunk_to_f32(bc, bf);
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[0][0] = __builtin_fmaf(af[i], bf[i], acc[0][0]);
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < NB; ++q)
+#pragma unroll
+                for (int m = 0; m < MT; ++m)
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) acc[q][m] = dot16(a[m][u], b[q][u], acc[q][m]);
+        }
+    } while (++blk < nblk);
+    };
+    Acc tot[NB][MT];
+    auto totals = [&]() __attribute__((always_inline)) {
 #pragma unroll
         for (int q = 0; q < NB; ++q)
 #pragma unroll
-            for (int m = 0; m < MT; ++m)
-#pragma unroll
-                for (int u = 0; u < 4; ++u) acc[q][m] = dot16(a[m][u], b[q][u], acc[q][m]);
-    } while (++blk < nblk);
-    int32_t tot[NB][MT];
-#pragma unroll
-    for (int q = 0; q < NB; ++q)
-#pragma unroll
-        for (int m = 0; m < MT; ++m) tot[q][m] = wave_sum(acc[q][m]);
+            for (int m = 0; m < MT; ++m) {
+                if constexpr (F8) tot[q][m] = wave_sum_f32(acc[q][m]);
+                else tot[q][m] = wave_sum(acc[q][m]);
+            }
+    };
+    stream(std::false_type{});
+    totals();
+    if constexpr (F8) {
+        if (tot[0][0] != tot[0][0]) {  // uniform over the wave: replay with the codes cleared
+            stream(std::true_type{});
+            totals();
+        }
+    }
     // All lanes hold every total.  SWI: lane m stores output (m, n); plain:
     // lane m*NB + q stores output (m, NB*n + q).
 #pragma unroll
@@ -263,6 +343,9 @@ __global__ __launch_bounds__(ROWS_WAVES * 64) void gemv_rows_kernel(GemmArgs p) 
             y[q] = p.bias ? __builtin_fmaf(static_cast<float>(tot[q][m]), sc, biasn[q])
                           : static_cast<float>(tot[q][m]) * sc;
         }
+        int32_t ti[NB];
+#pragma unroll
+        for (int q = 0; q < NB; ++q) ti[q] = F8 ? 0 : static_cast<int32_t>(tot[q][m]);
         if constexpr (SWI) {
             if (lane == m && m < M && nw < NO)
                 store_out<OUT>(p.C, static_cast<size_t>(m) * NO + n, swiglu_pair(y[0], y[1]), 0);
@@ -270,7 +353,7 @@ __global__ __launch_bounds__(ROWS_WAVES * 64) void gemv_rows_kernel(GemmArgs p) 
 #pragma unroll
             for (int q = 0; q < NB; ++q)
                 if (lane == m * NB + q && m < M && nw < NU && n * NB + q < p.N)
-                    store_out<OUT>(p.C, static_cast<size_t>(m) * p.N + n * NB + q, y[q], tot[q][m]);
+                    store_out<OUT>(p.C, static_cast<size_t>(m) * p.N + n * NB + q, y[q], ti[q]);
         }
     }
 }
@@ -923,6 +1006,18 @@ hipError_t launch_rows(const GemmArgs& p, hipStream_t stream) {
     return hipLaunchKernel(f, grid, dim3(ROWS_WAVES * 64), args, 0, stream);
 }
 
+// FP8 at M = 1: the row kernel on E4M3 codes (one weight row per wave).
+template <bool FULLK>
+hipError_t launch_rows_f8(const GemmArgs& p, hipStream_t stream) {
+    GemmArgs a = p;
+    void* args[] = {&a};
+    const dim3 grid((p.N + ROWS_WAVES - 1) / ROWS_WAVES);
+    const void* f = p.out_dtype == FKE_OUT_F32
+        ? reinterpret_cast<const void*>(&gemv_rows_kernel<1, FKE_OUT_F32, FULLK, 1, false, ELEM_F8>)
+        : reinterpret_cast<const void*>(&gemv_rows_kernel<1, FKE_OUT_BF16, FULLK, 1, false, ELEM_F8>);
+    return hipLaunchKernel(f, grid, dim3(ROWS_WAVES * 64), args, 0, stream);
+}
+
 template <int MT, int R>
 hipError_t launch_t(const GemmArgs& p, hipStream_t stream) {
     GemmArgs a = p;
@@ -1049,15 +1144,18 @@ hipError_t launch_gemv_i8(const GemmArgs& p, hipStream_t s) {
     return launch_t<16, 4>(p, s);
 }
 
-// FP8 decode and batches: the LDS-streamed kernel on E4M3 codes (B [N,K]).
+// FP8 decode and batches (B [N,K]): the row kernel at M = 1 (N = 14336,
+// K = 4096: 10.3-10.5 us against 11.7 us on the LDS-streamed kernel; 4096 x
+// 14336: 10.8 against 12.7), the LDS-streamed kernel on E4M3 codes above.
 bool gemv_f8_supports(const GemmArgs& p) {
     const uintptr_t a = reinterpret_cast<uintptr_t>(p.A), b = reinterpret_cast<uintptr_t>(p.B);
     return p.M >= 1 && p.M <= FKE_GEMV_MAX_M && p.N >= 1 && p.K % 64 == 0 && p.b_layout == FKE_B_NK &&
            !p.swiglu && (p.out_dtype == FKE_OUT_F32 || p.out_dtype == FKE_OUT_BF16) && ((a | b) & 15) == 0 &&
-           lds_fits<512>(p);
+           (p.M == 1 || lds_fits<512>(p));
 }
 
 hipError_t launch_gemv_f8(const GemmArgs& p, hipStream_t s) {
+    if (p.M == 1) return p.K % 4096 == 0 ? launch_rows_f8<true>(p, s) : launch_rows_f8<false>(p, s);
     const bool big = lds_fits<1024>(p) && (pieces_even(p.K, 1024) || !pieces_even(p.K, 512));
     if (p.M > 32) return launch_lds_f8<512, 4, 4>(p, s);
     if (p.M > 16) return big ? launch_lds_f8<1024, 2, 2>(p, s) : launch_lds_f8<512, 4, 2>(p, s);

@@ -310,7 +310,8 @@ def test_dispatch_unaligned_pointer_falls_back():
 
 
 @pytest.mark.parametrize("M,N,K,layout,expect", [
-    (1, 14336, 4096, 0, _lib.PATH_GEMV),      # FP8 decode: the LDS-streamed kernel
+    (1, 14336, 4096, 0, _lib.PATH_GEMV),      # FP8 decode: the row kernel at M = 1, the LDS-streamed kernel above
+    (1, 14336, 1024, 0, _lib.PATH_GEMV),      # the row kernel takes any K % 64 == 0
     (16, 14336, 4096, 0, _lib.PATH_GEMV),
     (32, 14336, 4096, 0, _lib.PATH_GEMV),
     (64, 14336, 4096, 0, _lib.PATH_MFMA),     # batches past 32 rows: the MFMA GEMM's 64x64 ring

@@ -1090,13 +1090,15 @@ def test_fp8_mfma_tolerance(oracle, dev, layout, out, nan_codes):
         assert_same(gpu_f8(A, B, sa, sb, layout, out, tile, bias=bias), big, f"fp8 {tile} {layout} vs 256x256")
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 300, 4096), (3, 1000, 2048), (16, 777, 5056), (16, 4096, 14336),
-                                   (17, 129, 4096), (40, 500, 2048), (64, 1000, 14336), (130, 300, 8192)])
+@pytest.mark.parametrize("M,N,K", [(1, 300, 4096), (1, 777, 4160), (1, 1001, 1984), (3, 1000, 2048), (16, 777, 5056),
+                                   (16, 4096, 14336), (17, 129, 4096), (40, 500, 2048), (64, 1000, 14336),
+                                   (130, 300, 8192)])
 @pytest.mark.parametrize("nan_codes", [False, True])
 def test_fp8_streamed_tolerance(oracle, dev, M, N, K, nan_codes):
-    """FP8 decode and batches (B [N,K]) on the LDS-streamed kernel: fp32 sums in
-    another order than the reference's sequential loop, so the FP8 bar (2e-2
-    relative); codes 0x7F / 0xFF count as 0.0 like the reference."""
+    """FP8 decode and batches (B [N,K]) on the row kernel (M = 1, K a multiple
+    of 4096 or not) and the LDS-streamed kernel: fp32 sums in another order than
+    the reference's sequential loop, so the FP8 bar (2e-2 relative); codes 0x7F
+    / 0xFF count as 0.0 like the reference."""
     say("fp8 streamed", M, N, K, nan_codes)
     A, B, sa, sb = f8_inputs(oracle, M, N, K, 800 + M + K, "nk", with_nan_codes=nan_codes)
     bias = oracle.gen_f32_normal((N,), 801 + N, 0.0, 0.02)
