@@ -942,7 +942,8 @@ def fp8_configs(torch, L, _lib, dev, gen, timed, args):
                                               "frac": round(t / PEAK_FP8_TFLOPS, 4)}
     del A8, B8, C
     # FP8 decode on the decode weights (N = 14336, K = 4096, B [N,K], bf16 out + bias): the
-    # LDS-streamed kernel, 8 rotating weights, HIP-graph timed like the INT8 decode lines
+    # row kernel at M = 1 and the LDS-streamed kernel at M = 16, 8 rotating weights, HIP-graph
+    # timed like the INT8 decode lines
     N, K, nbuf = 14336, 4096, args.gemv_buffers
     Bs = []
     for _ in range(nbuf):
@@ -951,8 +952,9 @@ def fp8_configs(torch, L, _lib, dev, gen, timed, args):
         Bs.append(b)
     bias = torch.randn(N, device=dev, generator=gen) * 0.02
     # the same bytes read as B [K,N] (the reference launcher's layout) run the transposing decode kernel
-    for lname, lay, kname in (("", _lib.B_NK, "gemv_lds_kernel (FP8)"), ("_Bkn", _lib.B_KN, "gemv_kn_split_kernel<f8>+kn_reduce_kernel<f8>")):
+    for lname, lay, kname in (("", _lib.B_NK, None), ("_Bkn", _lib.B_KN, "gemv_kn_split_kernel<f8>+kn_reduce_kernel<f8>")):
         for M in (1, 16):
+            kern = kname or ("gemv_rows_kernel (FP8)" if M == 1 else "gemv_lds_kernel (FP8)")
             A8 = torch.randint(0, 256, (M, K), dtype=torch.uint8, device=dev, generator=gen)
             A8[(A8 & 0x7F) == 0x7F] = 0
             out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
@@ -968,7 +970,7 @@ def fp8_configs(torch, L, _lib, dev, gen, timed, args):
             gbs = nbytes / (us * 1e-6) / 1e9
             res[f"fp8_decode_M{M}_14336x4096_bf16{lname}"] = {"us": round(us, 3), "GB/s": round(gbs, 1),
                                                               "frac": round(gbs / PEAK_HBM_GBS, 4),
-                                                              "bytes": nbytes, "kernel": kname}
+                                                              "bytes": nbytes, "kernel": kern}
     del Bs
     return res
 
