@@ -307,69 +307,40 @@ __global__ __launch_bounds__(256) void gemv_kn_split_kernel(GemmArgs p, KnSplit 
             if (mb + v < M) part[(mb + v) * KS_W + 16 * cb + j] = acc[cb][v];
 }
 
-// One thread per V consecutive outputs (m, n..n+V-1), n % V == 0 (V = 1 or
-// 4): the S partials of each in split order (4V-byte loads), then the
-// epilogue.  VEC (V = 4): C is aligned for one 16-byte (fp32 / int32) or
-// 8-byte (bf16) store of the four.  64 threads per workgroup; four outputs
-// per thread when that still gives every CU a workgroup, else one: the
-// kernel is latency-bound, and at N = 14336, K = 4096 (bf16, one box) the
-// call took 12.7 us at M = 1 with one output per thread (224 workgroups)
-// against 13.7 with four (56), and 15.6 us at M = 16 with four (896) against
-// 17.1 with one (3584) or 17.9 with four per thread in 256-thread groups.
-constexpr int KR_T = 64;  // threads per workgroup of the second kernel
-
-template <int EL, int OUT, int V, bool VEC>
-__global__ __launch_bounds__(KR_T) void kn_reduce_kernel(GemmArgs p, KnSplit sp) {
+// One thread per output (m, n): the S partials in split order, then the
+// epilogue.  The kernel is latency-bound (every load is in flight at once):
+// workgroups of 256 threads, or of 64 while that would leave CUs without one
+// (M = 1: 224 workgroups).  Same box, N = 14336, K = 4096, bf16: M = 16
+// 16.7 us for the call against 17.5 with four outputs per thread (16-byte
+// loads, one 8-byte store) in 64-thread groups and 17.6 in 256-thread groups;
+// M = 1 12.9 us with 64-thread groups, 13.0 with 256.
+template <int EL, int OUT, int T>
+__global__ __launch_bounds__(T) void kn_reduce_kernel(GemmArgs p, KnSplit sp) {
     constexpr bool F8 = EL == ELEM_F8;
-    static_assert(V == 1 || V == 4, "one or four outputs per thread");
-    static_assert(!VEC || V == 4, "vector stores of four outputs");
     using AccE = typename std::conditional<F8, float, int32_t>::type;
-    typedef AccE AccV __attribute__((ext_vector_type(V)));
-    const int N = p.N, S = sp.S, NV = N / V;
-    const int64_t idx = static_cast<int64_t>(blockIdx.x) * KR_T + threadIdx.x;
-    if (idx >= static_cast<int64_t>(p.M) * NV) return;
-    const int m = static_cast<int>(idx / NV), n = static_cast<int>(idx % NV) * V;
+    const int N = p.N, S = sp.S;
+    const int m = blockIdx.y, n = blockIdx.x * T + threadIdx.x;  // grid: column blocks x M
+    if (n >= N) return;
     const AccE* part = static_cast<const AccE*>(sp.part) + static_cast<size_t>(n / KS_W) * S * p.M * KS_W +
                        static_cast<size_t>(m) * KS_W + (n % KS_W);
-    AccV v[KS_SMAX];
+    AccE v[KS_SMAX];
 #pragma unroll
-    for (int t = 0; t < KS_SMAX; ++t)
-        v[t] = t < S ? *reinterpret_cast<const AccV*>(part + static_cast<size_t>(t) * p.M * KS_W) : AccV(0);
-    AccV s = v[0];
+    for (int t = 0; t < KS_SMAX; ++t) v[t] = t < S ? part[static_cast<size_t>(t) * p.M * KS_W] : AccE(0);
+    AccE s = v[0];
 #pragma unroll
     for (int t = 1; t < KS_SMAX; ++t)
         if (t < S) s += v[t];
-    float y[V];
-    int32_t si[V];
-    const float sam = p.scale_a ? p.scale_a[m] : p.sa;
-#pragma unroll
-    for (int e = 0; e < V; ++e) {
-        const AccE se = s[e];
-        si[e] = 0;
-        if constexpr (F8) {
-            const float sab = p.sa * p.sb;
-            y[e] = p.bias ? __builtin_fmaf(se, sab, p.bias[n + e]) : se * sab;
-        } else {
-            si[e] = se;
-            const float sc = sam * (p.scale_b ? p.scale_b[n + e] : p.sb);
-            y[e] = p.bias ? __builtin_fmaf(static_cast<float>(se), sc, p.bias[n + e]) : static_cast<float>(se) * sc;
-        }
-    }
-    const size_t o = static_cast<size_t>(m) * N + n;
-    if constexpr (VEC) {
-        if constexpr (OUT == FKE_OUT_F32) {
-            *reinterpret_cast<float4*>(static_cast<float*>(p.C) + o) = float4{y[0], y[1], y[2], y[3]};
-        } else if constexpr (OUT == FKE_OUT_BF16) {
-            const uint32_t lo = f32_to_bf16_rne(y[0]) | (static_cast<uint32_t>(f32_to_bf16_rne(y[1])) << 16);
-            const uint32_t hi = f32_to_bf16_rne(y[2]) | (static_cast<uint32_t>(f32_to_bf16_rne(y[3])) << 16);
-            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.C) + o) = uint2{lo, hi};
-        } else {
-            *reinterpret_cast<int4*>(static_cast<int32_t*>(p.C) + o) = int4{si[0], si[1], si[2], si[3]};
-        }
+    float y;
+    int32_t si = 0;
+    if constexpr (F8) {
+        const float sab = p.sa * p.sb;
+        y = p.bias ? __builtin_fmaf(s, sab, p.bias[n]) : s * sab;
     } else {
-#pragma unroll
-        for (int e = 0; e < V; ++e) store_out<OUT>(p.C, o + e, y[e], si[e]);
+        si = s;
+        const float sc = (p.scale_a ? p.scale_a[m] : p.sa) * (p.scale_b ? p.scale_b[n] : p.sb);
+        y = p.bias ? __builtin_fmaf(static_cast<float>(s), sc, p.bias[n]) : static_cast<float>(s) * sc;
     }
+    store_out<OUT>(p.C, static_cast<size_t>(m) * N + n, y, si);
 }
 
 template <int EL, int OUT>
@@ -382,18 +353,11 @@ hipError_t launch_kn_split_out(const GemmArgs& p, const KnSplit& sp, hipStream_t
                                            : reinterpret_cast<const void*>(&gemv_kn_split_kernel<EL, false>);
     hipError_t e = hipLaunchKernel(split, dim3(nblk * sp.S), dim3(256), args, 0, stream);
     if (e != hipSuccess) return e;
-    const int64_t outs = static_cast<int64_t>(p.M) * p.N;  // N % 16 == 0
-    const void* f;
-    int64_t threads = outs;
-    if ((outs / 4 + KR_T - 1) / KR_T >= 256) {
-        threads = outs / 4;
-        f = (reinterpret_cast<uintptr_t>(p.C) & (OUT == FKE_OUT_BF16 ? 7 : 15)) == 0
-                ? reinterpret_cast<const void*>(&kn_reduce_kernel<EL, OUT, 4, true>)
-                : reinterpret_cast<const void*>(&kn_reduce_kernel<EL, OUT, 4, false>);
-    } else {
-        f = reinterpret_cast<const void*>(&kn_reduce_kernel<EL, OUT, 1, false>);
-    }
-    return hipLaunchKernel(f, dim3(static_cast<unsigned>((threads + KR_T - 1) / KR_T)), dim3(KR_T), args, 0, stream);
+    if (static_cast<int64_t>(p.M) * p.N >= 256 * 256)
+        return hipLaunchKernel(reinterpret_cast<const void*>(&kn_reduce_kernel<EL, OUT, 256>),
+                               dim3((p.N + 255) / 256, p.M), dim3(256), args, 0, stream);
+    return hipLaunchKernel(reinterpret_cast<const void*>(&kn_reduce_kernel<EL, OUT, 64>), dim3((p.N + 63) / 64, p.M),
+                           dim3(64), args, 0, stream);
 }
 
 template <int EL>
