@@ -921,18 +921,19 @@ __global__ __launch_bounds__(NTHREADS, TL::OCC) void gemm_mfma_kernel(GemmArgs p
 }
 
 
-// The second kernel of a K split: thread idx adds the S partial sums of output
-// idx = m * N + n in the order s = 0..S-1 (INT8: exact int32; FP8: fp32 in
-// that fixed order) and applies the fused epilogue's arithmetic:
+// The second kernel of a K split: the thread of output (m, n) (grid: column
+// blocks x M) adds the S partial sums of idx = m * N + n in the order
+// s = 0..S-1 (INT8: exact int32; FP8: fp32 in that fixed order) and applies
+// the fused epilogue's arithmetic:
 // y = fmaf(sum, sa_m * sb_n, bias_n) (FP8: fmaf(sum, sa * sb, bias_n)), bias_n
 // = -0.0 without a bias, as the fused epilogue does.
 template <int ELEM, int OUT>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs p, SplitK sk) {
     using AccE = typename std::conditional<ELEM == ELEM_I8, int32_t, float>::type;
     const int64_t mn = static_cast<int64_t>(p.M) * p.N;
-    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (idx >= mn) return;
-    const int m = static_cast<int>(idx / p.N), n = static_cast<int>(idx % p.N);
+    const int m = blockIdx.y, n = blockIdx.x * 256 + threadIdx.x;  // grid: column blocks x M
+    if (n >= p.N) return;
+    const int64_t idx = static_cast<int64_t>(m) * p.N + n;
     const AccE* part = static_cast<const AccE*>(sk.part);
     AccE v[8];
 #pragma unroll
@@ -975,9 +976,9 @@ hipError_t launch_t(const GemmArgs& p, hipStream_t stream, int cus, const SplitK
     const hipError_t e = hipLaunchKernel(f, dim3(grid), dim3(NTHREADS), args, 0, stream);
     if (e != hipSuccess || sk.S == 1) return e;
     if constexpr (!SWI && elem_bytes(ELEM) == 1) {
-        const int64_t mn = static_cast<int64_t>(p.M) * p.N;
+        // (a split plan has at most one ring tile per CU and split: M is far below grid.y's 65536)
         return hipLaunchKernel(reinterpret_cast<const void*>(&splitk_reduce_kernel<ELEM, OUT>),
-                               dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), args, 0, stream);
+                               dim3((p.N + 255) / 256, p.M), dim3(256), args, 0, stream);
     }
     return hipErrorInvalidValue;  // not reached: checked before the launch
 }
