@@ -1090,7 +1090,8 @@ def test_fp8_mfma_tolerance(oracle, dev, layout, out, nan_codes):
         assert_same(gpu_f8(A, B, sa, sb, layout, out, tile, bias=bias), big, f"fp8 {tile} {layout} vs 256x256")
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 300, 4096), (1, 777, 4160), (1, 1001, 1984), (3, 1000, 2048), (16, 777, 5056),
+@pytest.mark.parametrize("M,N,K", [(1, 300, 4096), (1, 14336, 4096), (1, 777, 4160), (1, 1001, 1984), (3, 1000, 2048),
+                                   (16, 777, 5056),
                                    (16, 4096, 14336), (17, 129, 4096), (40, 500, 2048), (64, 1000, 14336),
                                    (130, 300, 8192)])
 @pytest.mark.parametrize("nan_codes", [False, True])
