@@ -88,13 +88,14 @@ bool mfma_supports(const GemmArgs& p, int elem);
 bool gemv_dot_supports(const GemmArgs& p);
 hipError_t launch_gemv_dot(const GemmArgs& p, hipStream_t stream);
 // Decode (M <= 16) with B stored [K,N], INT8 or FP8 (gemv_kn.hip): with a
-// workspace for partial sums, S K splits of 512-column workgroups and a
-// second kernel that adds the splits; without one (S = 1), one workgroup per
-// 64-column block over all of K.
+// workspace for partial sums, S K splits of 512-column workgroups (M = 1:
+// 1024-column workgroups of the row kernel) and a second kernel that adds the
+// splits; without one (S = 1), one workgroup per 64-column block over all of K.
 struct KnSplit {
     int S;       // K splits (1: no workspace)
     int PS;      // 128-row pieces per split
     void* part;  // [ceil(N/128)][S][M][128] partial sums (int32 / fp32)
+    int rowk;    // 1: the M = 1 row kernel writes them (1024-column workgroups), 0: the split kernel
 };
 bool gemv_kn_supports(const GemmArgs& p, int elem);
 size_t gemv_kn_workspace_bytes(const GemmArgs& p);  // 0: runs unsplit
@@ -142,6 +143,25 @@ __device__ __forceinline__ uint32_t e4m3_sanitize(uint32_t w) {
     const uint32_t hi = (w & 0x7F7F7F7Fu) + 0x01010101u;
     const uint32_t sel = ((hi >> 5) & 0x04040404u) | 0x03020100u;
     return __builtin_amdgcn_perm(0u, w, sel);
+}
+
+typedef float v2f __attribute__((ext_vector_type(2)));
+
+// E4M3 codes -> fp32 with gfx950's v_cvt_pk_f32_fp8 (two codes per
+// instruction; checked against the reference's decode, src/quantized_gemm.cu:
+// 81-97, on all 256 codes: identical, except 0x7F / 0xFF, which it turns into
+// NaN where the reference reads 0.0 - see e4m3_sanitize).  16 codes of one
+// 16-byte chunk (a vector of four 32-bit words), in byte order.
+template <typename V4>
+__device__ __forceinline__ void e4m3_chunk_to_f32(V4 c, float (&f)[16]) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const v2f lo = __builtin_amdgcn_cvt_pk_f32_fp8(c[e], false), hi = __builtin_amdgcn_cvt_pk_f32_fp8(c[e], true);
+        f[4 * e] = lo.x;
+        f[4 * e + 1] = lo.y;
+        f[4 * e + 2] = hi.x;
+        f[4 * e + 3] = hi.y;
+    }
 }
 
 // Canonical fused epilogue: s = fp32(sa_m*sb_n); y = bias ? fma(v,s,bias) : v*s.

@@ -168,24 +168,6 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
            __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
 }
 
-typedef float v2f __attribute__((ext_vector_type(2)));
-
-// E4M3 codes -> fp32 with gfx950's v_cvt_pk_f32_fp8 (two codes per
-// instruction; checked against the reference's decode, src/quantized_gemm.cu:
-// 81-97, on all 256 codes: identical, except 0x7F / 0xFF, which it turns into
-// NaN where the reference reads 0.0 - see e4m3_sanitize).  16 codes of one
-// 16-byte chunk, in byte order.
-__device__ __forceinline__ void e4m3_chunk_to_f32(v4i c, float (&f)[16]) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const v2f lo = __builtin_amdgcn_cvt_pk_f32_fp8(c[e], false), hi = __builtin_amdgcn_cvt_pk_f32_fp8(c[e], true);
-        f[4 * e] = lo.x;
-        f[4 * e + 1] = lo.y;
-        f[4 * e + 2] = hi.x;
-        f[4 * e + 3] = hi.y;
-    }
-}
-
 constexpr int ROWS_WAVES = 2;  // waves per workgroup of gemv_rows_kernel
 // Weight rows per wave of the plain kernel.  One: at N = 14336, K = 4096 the
 // launch is bounded by its ramp and drain, and 2 / 4 / 8 rows per wave

@@ -31,6 +31,10 @@
 //    ~8 us more at that shape: its store / count / load round trips queue
 //    behind the other workgroups' streams, where the second kernel's run
 //    after them (13.2 against 19 us for M = 1).
+//  * Row kernel (gemv_kn_row_kernel + kn_reduce_kernel), M = 1: workgroup =
+//    1024 consecutive columns x one of S <= 64 K ranges, loaded straight into
+//    registers and summed on the VALU (no MFMA, no LDS staging); its partial
+//    sums take the split kernel's layout and second kernel.
 //  * Full kernel (gemv_kn_full_kernel), when there is no workspace or K is
 //    too short to split: one workgroup per 64-column block over all of K,
 //    blocks 2j and 2j+1 (the two halves of each 128-byte line) on one XCD.
@@ -314,7 +318,7 @@ __global__ __launch_bounds__(256) void gemv_kn_split_kernel(GemmArgs p, KnSplit 
 // 16.7 us for the call against 17.5 with four outputs per thread (16-byte
 // loads, one 8-byte store) in 64-thread groups and 17.6 in 256-thread groups;
 // M = 1 12.9 us with 64-thread groups, 13.0 with 256.
-template <int EL, int OUT, int T>
+template <int EL, int OUT, int T, int SM>
 __global__ __launch_bounds__(T) void kn_reduce_kernel(GemmArgs p, KnSplit sp) {
     constexpr bool F8 = EL == ELEM_F8;
     using AccE = typename std::conditional<F8, float, int32_t>::type;
@@ -323,12 +327,12 @@ __global__ __launch_bounds__(T) void kn_reduce_kernel(GemmArgs p, KnSplit sp) {
     if (n >= N) return;
     const AccE* part = static_cast<const AccE*>(sp.part) + static_cast<size_t>(n / KS_W) * S * p.M * KS_W +
                        static_cast<size_t>(m) * KS_W + (n % KS_W);
-    AccE v[KS_SMAX];
+    AccE v[SM];
 #pragma unroll
-    for (int t = 0; t < KS_SMAX; ++t) v[t] = t < S ? part[static_cast<size_t>(t) * p.M * KS_W] : AccE(0);
+    for (int t = 0; t < SM; ++t) v[t] = t < S ? part[static_cast<size_t>(t) * p.M * KS_W] : AccE(0);
     AccE s = v[0];
 #pragma unroll
-    for (int t = 1; t < KS_SMAX; ++t)
+    for (int t = 1; t < SM; ++t)
         if (t < S) s += v[t];
     float y;
     int32_t si = 0;
@@ -343,21 +347,249 @@ __global__ __launch_bounds__(T) void kn_reduce_kernel(GemmArgs p, KnSplit sp) {
     store_out<OUT>(p.C, static_cast<size_t>(m) * N + n, y, si);
 }
 
+// ===========================================================================
+// Row kernel (M = 1): 1024 columns per workgroup, loaded from HBM straight
+// into registers; no LDS staging and no MFMA.
+// ===========================================================================
+// One activation row leaves an MFMA nothing to share between its 16 rows, and
+// the transposing LDS reads serve only to turn k rows into columns.  Here lane
+// l loads bytes 16l..16l+15 (16 columns) of a 1 KiB row segment, one load
+// instruction per k row; the workgroup's waves read the 128 consecutive rows
+// of a piece over the same 1024 columns, a few rows per wave at a time (a
+// batch).  A lane turns each 4 rows x 4 columns of a batch into four words of
+// 4 k bytes (a byte transpose in eight v_perm_b32) and sums them with
+// v_dot4_i32_i8 against the activation word of those 4 rows (INT8), or
+// converts the codes with v_cvt_pk_f32_fp8 and adds the exact products with
+// fma in k order (FP8).  The waves' sums meet in LDS in the order w = 0, 1,
+// ... and go to the workspace in the split kernel's layout ([block of 128
+// columns][split][128]); kn_reduce_kernel finishes them.
+// Why: 1024-column blocks take up to 64 K splits, where the split kernel's
+// 512-column blocks take 8, so shapes with few column blocks still fill the
+// CUs (N = 4096, K = 14336: 224 workgroups and 13.5 against 23.2 us); at
+// N = 14336, K = 4096 both take 224 workgroups and the same time (12.9 us),
+// although a plain read of this kernel's pattern is 1 us faster than of the
+// split kernel's (10.3 against 11.3 us, back-to-back launches).
+// Layout (N = 14336 / 4096 x K = 4096 / 14336, INT8 and FP8, one box, same
+// A/B): 16 waves x 4-row batches x 2 in flight; 8 waves x 4 or 8 rows x 2,
+// and 4 waves x 8 rows x 2, within 0.1 us of it; 16-row batches 0.8 us
+// slower, three or four in flight 0.1-1.1 us slower: every load of a wave is
+// issued early, so the arithmetic of its last batch runs after the stream,
+// and short batches keep that tail short.
+constexpr int KR_W = 1024;   // columns per workgroup
+constexpr int KR_SMAX = 64;  // K splits at most
+constexpr int KR_WAVES = 16; // waves per workgroup
+constexpr int KR_ROWS = 4;   // rows per wave per batch
+constexpr int KR_D = 2;      // batches in flight per wave
+static_assert(KS_ROWS % (KR_WAVES * KR_ROWS) == 0, "a 128-row piece is whole batches of every wave");
+static_assert(KR_ROWS == 4 || KR_ROWS == 8 || KR_ROWS == 16, "4, 8 or 16 activation bytes per batch");
+static_assert(KR_D >= 2 && KR_D <= 4, "two to four batches in flight");
+static_assert(KR_W % KS_W == 0, "workgroups cover whole 128-column blocks of the partial-sum layout");
+
+// 4 x 4 byte transpose: byte j of r[i] is (row i, column j); byte i of c[j] becomes it.
+__device__ __forceinline__ void kr_transpose4(uint32_t r0, uint32_t r1, uint32_t r2, uint32_t r3, uint32_t (&c)[4]) {
+    const uint32_t lo01 = __builtin_amdgcn_perm(r1, r0, 0x05010400u);  // r0.0 r1.0 r0.1 r1.1
+    const uint32_t hi01 = __builtin_amdgcn_perm(r1, r0, 0x07030602u);  // r0.2 r1.2 r0.3 r1.3
+    const uint32_t lo23 = __builtin_amdgcn_perm(r3, r2, 0x05010400u);
+    const uint32_t hi23 = __builtin_amdgcn_perm(r3, r2, 0x07030602u);
+    c[0] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);  // r0.0 r1.0 r2.0 r3.0
+    c[1] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);
+    c[2] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
+    c[3] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
+}
+
+template <int EL>
+__global__ __launch_bounds__(KR_WAVES * 64) void gemv_kn_row_kernel(GemmArgs p, KnSplit sp) {
+    constexpr bool F8 = EL == ELEM_F8;
+    constexpr int BP = KS_ROWS / (KR_WAVES * KR_ROWS);  // batches per wave per 128-row piece
+    constexpr int AW = KR_ROWS / 4;                     // activation words per batch
+    using AccE = typename std::conditional<F8, float, int32_t>::type;
+    __shared__ __attribute__((aligned(16))) AccE red[KR_WAVES][KR_W];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int N = p.N, K = p.K, S = sp.S;
+    const int cbg = blockIdx.x / S, split = blockIdx.x % S;
+    const int c0 = cbg * KR_W;
+    const int P = (K + KS_ROWS - 1) / KS_ROWS;
+    const int i0 = split * sp.PS, i1 = min(P, i0 + sp.PS);  // this split's pieces
+    const int nb = (i1 - i0) * BP;                          // batches of each wave
+    // N % 16 == 0: a lane's 16 columns are all in or all out
+    const uint32_t lane_off = c0 + 16 * lane < N ? static_cast<uint32_t>(c0 + 16 * lane) : 0x80000000u;
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.B, K * N);
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, K);
+
+    // Batch j of the wave: sub-step h = j % BP of piece i0 + j / BP, rows
+    // k0 .. k0 + KR_ROWS - 1 with k0 = 128 i + KR_ROWS (h * waves + w), so each
+    // sub-step of the workgroup reads consecutive rows.  The activation bytes
+    // of those rows come first (one load, the same address in every lane, so
+    // that it counts with the batch), then those rows of the lane's columns.
+    // Batches past the split and columns past N read as zero; K % 64 == 0, so
+    // a batch is all in K or all out.
+    auto load = [&](int j, v4i (&b)[KR_ROWS], int (&a)[AW]) __attribute__((always_inline)) {
+        const int k0 = (i0 + j / BP) * KS_ROWS + KR_ROWS * ((j % BP) * KR_WAVES + wave);
+        const bool on = j < nb && k0 < K;
+        // Bit 31 set: outside every range.  Outside batches take row 0, so that
+        // no offset (with the row's r * N added) passes 2^32: at most
+        // 2^31 + K * N for an invalid column, 2^31 + 16 * N for a batch outside.
+        const int kk = on ? k0 : 0;
+        const uint32_t off = on ? 0u : 0x80000000u;
+        if constexpr (AW == 4) {
+            const v4i av = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(ra, static_cast<int>(off | kk), 0, 0));
+#pragma unroll
+            for (int q = 0; q < 4; ++q) a[q] = av[q];
+        } else if constexpr (AW == 2) {
+            const v2i av = __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(ra, static_cast<int>(off | kk), 0, 0));
+            a[0] = av[0];
+            a[1] = av[1];
+        } else {
+            a[0] = __builtin_bit_cast(int, __builtin_amdgcn_raw_buffer_load_b32(ra, static_cast<int>(off | kk), 0, 0));
+        }
+        const uint32_t base = off | (lane_off + static_cast<uint32_t>(kk * N));
+#pragma unroll
+        for (int r = 0; r < KR_ROWS; ++r)
+            b[r] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rb, static_cast<int>(base), r * N, 2));
+    };
+
+    AccE acc[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[j] = AccE(0);
+
+    auto consume = [&](const v4i (&b)[KR_ROWS], const int (&a)[AW], auto san) __attribute__((always_inline)) {
+        if constexpr (F8) {
+            constexpr bool SAN = decltype(san)::value;
+            float af[KR_ROWS];
+#pragma unroll
+            for (int q = 0; q < AW; ++q) {
+                const uint32_t w = SAN ? e4m3_sanitize(static_cast<uint32_t>(a[q])) : static_cast<uint32_t>(a[q]);
+                const v2f lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), false);
+                const v2f hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), true);
+                af[4 * q] = lo.x;
+                af[4 * q + 1] = lo.y;
+                af[4 * q + 2] = hi.x;
+                af[4 * q + 3] = hi.y;
+            }
+#pragma unroll
+            for (int r = 0; r < KR_ROWS; ++r) {
+                v4i w = b[r];
+                if constexpr (SAN) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) w[e] = static_cast<int>(e4m3_sanitize(static_cast<uint32_t>(w[e])));
+                }
+                float bf[16];
+                e4m3_chunk_to_f32(w, bf);
+#pragma unroll
+                for (int j = 0; j < 16; ++j) acc[j] = __builtin_fmaf(af[r], bf[j], acc[j]);
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < AW; ++q)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    uint32_t c[4];
+                    kr_transpose4(static_cast<uint32_t>(b[4 * q][e]), static_cast<uint32_t>(b[4 * q + 1][e]),
+                                  static_cast<uint32_t>(b[4 * q + 2][e]), static_cast<uint32_t>(b[4 * q + 3][e]), c);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        acc[4 * e + j] = __builtin_amdgcn_sdot4(static_cast<int>(c[j]), a[q], acc[4 * e + j], false);
+                }
+        }
+    };
+    // KR_D batches in flight in KR_D buffers, KR_D batches per iteration.  The
+    // loads are issued unconditionally (a batch past the split reads nothing),
+    // so the compiler's wait before each batch's use counts only the later
+    // batches' loads; only the arithmetic of batches past the split is
+    // skipped.  The scheduling barriers keep each batch's loads ahead of the
+    // previous batch's arithmetic.
+    auto stream = [&](auto san) __attribute__((always_inline)) {
+        v4i b[KR_D][KR_ROWS];
+        int a[KR_D][AW];
+#pragma unroll
+        for (int d = 0; d < KR_D - 1; ++d) load(d, b[d], a[d]);
+        for (int j = 0; j < nb; j += KR_D) {
+#pragma unroll
+            for (int d = 0; d < KR_D; ++d) {
+                fence();
+                load(j + d + KR_D - 1, b[(d + KR_D - 1) % KR_D], a[(d + KR_D - 1) % KR_D]);
+                fence();
+                if (j + d < nb) consume(b[d], a[d], san);
+            }
+        }
+        fence();
+    };
+    if constexpr (!F8) {
+        stream(std::false_type{});
+    } else {
+        // E4M3 0x7F / 0xFF: NaN to v_cvt_pk_f32_fp8, 0.0 to the reference.  The
+        // stream runs on the raw codes; every product of finite codes is finite
+        // and no sum of them overflows fp32, so a NaN sum proves a NaN code in
+        // the wave's rows, and only then does the wave stream them again with
+        // the codes cleared.
+        stream(std::false_type{});
+        bool bad = false;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) bad |= __builtin_isnan(acc[j]);
+        if (__builtin_amdgcn_ballot_w64(bad) != 0) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
+            stream(std::true_type{});
+        }
+    }
+
+    // The waves' sums in the order w = 0, 1, ...: lane l of wave w holds
+    // columns 16l..16l+15 of the workgroup's block; thread t finishes columns
+    // CT t .. CT t + CT - 1.
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        AccE* d = &red[wave][16 * lane + 4 * e];
+        d[0] = acc[4 * e];
+        d[1] = acc[4 * e + 1];
+        d[2] = acc[4 * e + 2];
+        d[3] = acc[4 * e + 3];
+    }
+    __syncthreads();
+    constexpr int CT = KR_W / (KR_WAVES * 64);
+    AccE* const part = static_cast<AccE*>(sp.part);
+#pragma unroll
+    for (int h = 0; h < CT; ++h) {
+        const int col = CT * tid + h, n = c0 + col;
+        AccE s = red[0][col];
+#pragma unroll
+        for (int w = 1; w < KR_WAVES; ++w) s += red[w][col];
+        if (n < N) part[(static_cast<size_t>(n / KS_W) * S + split) * KS_W + n % KS_W] = s;
+    }
+}
+
 template <int EL, int OUT>
 hipError_t launch_kn_split_out(const GemmArgs& p, const KnSplit& sp, hipStream_t stream) {
     GemmArgs a = p;
     KnSplit s = sp;
     void* args[] = {&a, &s};
-    const int nblk = (p.N + 4 * KS_W - 1) / (4 * KS_W);
-    const void* split = p.M <= KS_NT_MAX_M ? reinterpret_cast<const void*>(&gemv_kn_split_kernel<EL, true>)
-                                           : reinterpret_cast<const void*>(&gemv_kn_split_kernel<EL, false>);
-    hipError_t e = hipLaunchKernel(split, dim3(nblk * sp.S), dim3(256), args, 0, stream);
+    hipError_t e;
+    if (sp.rowk) {
+        const int nblk = (p.N + KR_W - 1) / KR_W;
+        e = hipLaunchKernel(reinterpret_cast<const void*>(&gemv_kn_row_kernel<EL>), dim3(nblk * sp.S),
+                            dim3(KR_WAVES * 64), args, 0, stream);
+    } else {
+        const int nblk = (p.N + 4 * KS_W - 1) / (4 * KS_W);
+        const void* split = p.M <= KS_NT_MAX_M ? reinterpret_cast<const void*>(&gemv_kn_split_kernel<EL, true>)
+                                               : reinterpret_cast<const void*>(&gemv_kn_split_kernel<EL, false>);
+        e = hipLaunchKernel(split, dim3(nblk * sp.S), dim3(256), args, 0, stream);
+    }
     if (e != hipSuccess) return e;
-    if (static_cast<int64_t>(p.M) * p.N >= 256 * 256)
-        return hipLaunchKernel(reinterpret_cast<const void*>(&kn_reduce_kernel<EL, OUT, 256>),
-                               dim3((p.N + 255) / 256, p.M), dim3(256), args, 0, stream);
-    return hipLaunchKernel(reinterpret_cast<const void*>(&kn_reduce_kernel<EL, OUT, 64>), dim3((p.N + 63) / 64, p.M),
-                           dim3(64), args, 0, stream);
+    // the split count bounds the partial sums each thread loads at once
+    const void* red;
+    if (static_cast<int64_t>(p.M) * p.N >= 256 * 256) {
+        red = sp.S <= 8    ? reinterpret_cast<const void*>(&kn_reduce_kernel<EL, OUT, 256, 8>)
+              : sp.S <= 16 ? reinterpret_cast<const void*>(&kn_reduce_kernel<EL, OUT, 256, 16>)
+              : sp.S <= 32 ? reinterpret_cast<const void*>(&kn_reduce_kernel<EL, OUT, 256, 32>)
+                           : reinterpret_cast<const void*>(&kn_reduce_kernel<EL, OUT, 256, KR_SMAX>);
+        return hipLaunchKernel(red, dim3((p.N + 255) / 256, p.M), dim3(256), args, 0, stream);
+    }
+    red = sp.S <= 8    ? reinterpret_cast<const void*>(&kn_reduce_kernel<EL, OUT, 64, 8>)
+          : sp.S <= 16 ? reinterpret_cast<const void*>(&kn_reduce_kernel<EL, OUT, 64, 16>)
+          : sp.S <= 32 ? reinterpret_cast<const void*>(&kn_reduce_kernel<EL, OUT, 64, 32>)
+                       : reinterpret_cast<const void*>(&kn_reduce_kernel<EL, OUT, 64, KR_SMAX>);
+    return hipLaunchKernel(red, dim3((p.N + 63) / 64, p.M), dim3(64), args, 0, stream);
 }
 
 template <int EL>
@@ -701,10 +933,27 @@ static size_t kn_ws_bytes(int M, int N, int S) {
 // S in 2..4 is the one with the fewest rounds per split (ties: the smaller):
 // at N = 81920 / 98304 / 128256, K = 4096, M = 1, S = 3 / 4 / 2 ran 54 / 64 /
 // 79 us against 88 / 107 / 108 us for the full kernel.
-static void kn_splits(const GemmArgs& p, size_t ws_bytes, int* S_out, int* PS_out) {
+// M = 1 takes the row kernel instead whenever two or more splits of its
+// 1024-column workgroups fit: S = CUs / blocks (at most 64, whole 128-row
+// pieces, none empty; 16 at N = 14336, K = 4096: 224 workgroups).
+static void kn_splits(const GemmArgs& p, size_t ws_bytes, int* S_out, int* PS_out, int* rowk_out) {
     const int kCUs = device_cus();
     if (ws_bytes > FKE_SPLIT_SLOT_BYTES) ws_bytes = FKE_SPLIT_SLOT_BYTES;
     const int P = (p.K + KS_ROWS - 1) / KS_ROWS;
+    *rowk_out = 0;
+    if (p.M == 1) {
+        int S = kCUs / ((p.N + KR_W - 1) / KR_W);
+        if (S > KR_SMAX) S = KR_SMAX;
+        if (S > P) S = P;
+        while (S > 1 && kn_ws_bytes(1, p.N, S) > ws_bytes) --S;
+        if (S >= 2) {
+            const int PS = (P + S - 1) / S;
+            *S_out = (P + PS - 1) / PS;
+            *PS_out = PS;
+            *rowk_out = 1;
+            return;
+        }
+    }
     const int nblk = (p.N + 4 * KS_W - 1) / (4 * KS_W);
     int S = kCUs / nblk;
     if (S < 2) {
@@ -731,8 +980,8 @@ static void kn_splits(const GemmArgs& p, size_t ws_bytes, int* S_out, int* PS_ou
 }
 
 size_t gemv_kn_workspace_bytes(const GemmArgs& p) {
-    int S, PS;
-    kn_splits(p, SIZE_MAX, &S, &PS);
+    int S, PS, rowk;
+    kn_splits(p, SIZE_MAX, &S, &PS, &rowk);
     return S > 1 ? kn_ws_bytes(p.M, p.N, S) : 0;
 }
 
@@ -741,7 +990,7 @@ size_t gemv_kn_workspace_bytes(const GemmArgs& p) {
 KnSplit gemv_kn_plan(const GemmArgs& p, void* ws, size_t ws_bytes) {
     KnSplit sp;
     const bool usable = ws && (reinterpret_cast<uintptr_t>(ws) & 15) == 0;
-    kn_splits(p, usable ? ws_bytes : 0, &sp.S, &sp.PS);
+    kn_splits(p, usable ? ws_bytes : 0, &sp.S, &sp.PS, &sp.rowk);
     sp.part = sp.S > 1 ? ws : nullptr;
     return sp;
 }

@@ -77,9 +77,14 @@ def test_workspace_entry_points_reject_bad_arguments():
 
 
 @pytest.mark.parametrize("M,N,K,layout,expect", [
-    # C2 with B [K,N]: 28 workgroups of 512 columns x 8 K splits, [M][N] int32 partials each
-    (1, 14336, 4096, 1, 8 * 1 * 14336 * 4),
+    # C2 with B [K,N]: 28 workgroups of 512 columns x 8 K splits, [M][N] int32 partials each;
+    # M = 1 on the row kernel: 14 workgroups of 1024 columns x 16 splits
+    (1, 14336, 4096, 1, 16 * 1 * 14336 * 4),
     (16, 14336, 4096, 1, 8 * 16 * 14336 * 4),
+    # row kernel: 4 blocks -> 64 splits at most, 112 pieces in 56 splits of 2;
+    # 126 blocks -> 2 splits
+    (1, 4096, 14336, 1, 56 * 1 * 4096 * 4),
+    (1, 128256, 4096, 1, 2 * 1 * 128256 * 4),
     # splits capped by the 128-row pieces of K: K = 512 -> 4 splits
     (4, 14336, 512, 1, 4 * 4 * 14336 * 4),
     # N = 2^16: 128 blocks of 512 columns -> 2 splits

@@ -304,9 +304,12 @@ def test_c2_decode_full_b_kn(oracle, dev, M):
 # that ends in half an item (K % 128 == 64), K below one item per wave (waves
 # without items), K = 14336 (28 items per wave), more blocks than CUs, and N
 # past 65536 (K splits over several rounds of workgroups: S = 3 with splits of
-# 3 / 3 / 2 items, S = 2)
+# 3 / 3 / 2 items, S = 2).  M = 1 runs the row kernel: 1024-column blocks, one
+# block with 16 valid columns (32 splits), 56 splits of K = 14336, 17 splits
+# of which the last has one 128-row piece (K = 4160), and 81 blocks x 3.
 KN_SHAPES = [(1, 16, 4096), (3, 304, 1024), (16, 1040, 192), (5, 4096, 64), (2, 4096, 14336),
-             (16, 20016, 2048), (8, 1008, 4160), (1, 82000, 1024), (9, 100000, 512)]
+             (16, 20016, 2048), (8, 1008, 4160), (1, 82000, 1024), (9, 100000, 512),
+             (1, 4096, 14336), (1, 14352, 4160)]
 
 
 @pytest.mark.parametrize("M,N,K", KN_SHAPES)
@@ -327,7 +330,7 @@ def test_gemv_kn_i8_bit_exact(oracle, dev, M, N, K, out, opts):
         assert_same(got, oracle_out(oracle, acc, None, None, 0.013, 0.021, None, out), f"kn scalar {M, N, K}")
 
 
-@pytest.mark.parametrize("M,N,K", KN_SHAPES + [(16, 14336, 4096)])
+@pytest.mark.parametrize("M,N,K", KN_SHAPES + [(16, 14336, 4096), (1, 14336, 4096)])
 @pytest.mark.parametrize("nan_codes", [False, True])
 def test_gemv_kn_f8_tolerance(oracle, dev, M, N, K, nan_codes):
     """FP8 decode with B [K,N] (the reference launcher's layout) on the
@@ -371,7 +374,8 @@ def test_gemv_kn_split_full_and_fewer_splits(oracle, dev, M):
     A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 9100 + M, layout="kn", act="normal")
     acc = oracle.w8a8_acc(A, B, oracle.B_KN, nthreads=NTH)
     need = _lib.lib().fke_qgemm_workspace_size(M, N, K, _lib.B_KN)
-    assert need == 4 * 8 * M * N  # 8 splits of [M][N] int32 partial sums
+    # [M][N] int32 partial sums per split: 8 splits, 16 on the M = 1 row kernel
+    assert need == 4 * (16 if M == 1 else 8) * M * N
     dA, dB, dsa, dsb, dbias = dev_t(A), dev_t(B), dev_t(sa), dev_t(sb), dev_t(bias)
     for nbytes in (need, need // 3, 0):
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev) if nbytes else None
