@@ -60,7 +60,8 @@ def gemv_kernel(L, _lib, M, N=14336, K=4096, layout="nk"):
         tile = TILE_LABELS[L.fke_select_mfma_tile(M, N, K, code, 0, 0)]
         return f"gemm_mfma_kernel<i8,{layout.upper()},bf16,{tile}>"
     if layout == "kn":
-        return "gemv_kn_split_kernel<i8>+kn_reduce_kernel<i8,bf16>"
+        first = "gemv_kn_row_kernel<i8>" if M == 1 else "gemv_kn_split_kernel<i8>"
+        return first + "+kn_reduce_kernel<i8,bf16>"
     return "gemv_rows_kernel" if M <= 2 else "gemv_lds_kernel"
 
 
@@ -952,9 +953,12 @@ def fp8_configs(torch, L, _lib, dev, gen, timed, args):
         Bs.append(b)
     bias = torch.randn(N, device=dev, generator=gen) * 0.02
     # the same bytes read as B [K,N] (the reference launcher's layout) run the transposing decode kernel
-    for lname, lay, kname in (("", _lib.B_NK, None), ("_Bkn", _lib.B_KN, "gemv_kn_split_kernel<f8>+kn_reduce_kernel<f8>")):
+    for lname, lay in (("", _lib.B_NK), ("_Bkn", _lib.B_KN)):
         for M in (1, 16):
-            kern = kname or ("gemv_rows_kernel (FP8)" if M == 1 else "gemv_lds_kernel (FP8)")
+            if lay == _lib.B_KN:
+                kern = ("gemv_kn_row_kernel<f8>" if M == 1 else "gemv_kn_split_kernel<f8>") + "+kn_reduce_kernel<f8>"
+            else:
+                kern = "gemv_rows_kernel (FP8)" if M == 1 else "gemv_lds_kernel (FP8)"
             A8 = torch.randint(0, 256, (M, K), dtype=torch.uint8, device=dev, generator=gen)
             A8[(A8 & 0x7F) == 0x7F] = 0
             out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
