@@ -28,6 +28,7 @@ def test_batch_kernel_label_for_every_m(N, K, layout):
     L = _lib.lib()
     for M in range(1, 513):
         label = bench.gemv_kernel(L, _lib, M, N, K, layout)
-        assert label.startswith(("gemv_rows_kernel", "gemv_lds_kernel", "gemv_kn_split_kernel",
+        assert label.startswith(("gemv_rows_kernel", "gemv_lds_kernel", "gemv_kn_split_kernel", "gemv_kn_row_kernel",
                                  f"gemm_mfma_kernel<i8,{layout.upper()},bf16,"))
+        assert label.startswith("gemv_kn_row_kernel") == (layout == "kn" and M == 1)
         assert (label.startswith("gemv_kn") or label.startswith("gemm_mfma")) if layout == "kn" else True
