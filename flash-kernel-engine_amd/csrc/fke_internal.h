@@ -88,14 +88,16 @@ bool mfma_supports(const GemmArgs& p, int elem);
 bool gemv_dot_supports(const GemmArgs& p);
 hipError_t launch_gemv_dot(const GemmArgs& p, hipStream_t stream);
 // Decode (M <= 16) with B stored [K,N], INT8 or FP8 (gemv_kn.hip): with a
-// workspace for partial sums, S K splits of 512-column workgroups (M = 1:
-// 1024-column workgroups of the row kernel) and a second kernel that adds the
-// splits; without one (S = 1), one workgroup per 64-column block over all of K.
+// workspace for partial sums, S K splits of 128- to 512-column workgroups
+// (M = 1: 1024-column workgroups of the row kernel) and a second kernel that
+// adds the splits; without one (S = 1), one workgroup per 64-column block over
+// all of K.
 struct KnSplit {
     int S;       // K splits (1: no workspace)
     int PS;      // 128-row pieces per split
     void* part;  // [ceil(N/128)][S][M][128] partial sums (int32 / fp32)
     int rowk;    // 1: the M = 1 row kernel writes them (1024-column workgroups), 0: the split kernel
+    int kw;      // the split kernel's waves per workgroup (1, 2 or 4 blocks of 128 columns)
 };
 bool gemv_kn_supports(const GemmArgs& p, int elem);
 size_t gemv_kn_workspace_bytes(const GemmArgs& p);  // 0: runs unsplit

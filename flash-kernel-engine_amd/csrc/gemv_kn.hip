@@ -20,9 +20,10 @@
 // as well as N when a workspace holds the partial sums:
 //
 //  * Split kernel (gemv_kn_split_kernel + kn_reduce_kernel).  Workgroup =
-//    512 consecutive columns x one of S K ranges (grid ceil(N/512) x S, S <=
-//    8: 224 workgroups at N = 14336, K = 4096); wave w streams the 128-column
-//    block 4*blockIdx/S + w over the range, so the workgroup reads 512
+//    KW = 1, 2 or 4 waves of 128 consecutive columns each x one of S K ranges
+//    (grid ceil(N/(128 KW)) x S, S <= 8; at N = 14336, K = 4096 two waves and
+//    S = 4: 224 workgroups); wave w streams the 128-column block
+//    KW*blockIdx/S + w over the range, so the workgroup reads 128 KW
 //    contiguous bytes of every row it touches.  Each wave writes its block's
 //    partial sums ([M][128], int32 / fp32) to the workspace; a second kernel
 //    adds the S partials of each output in the fixed order s = 0..S-1 (exact
@@ -135,26 +136,26 @@ __device__ __forceinline__ void ks_read_w(const lds_u8* slot, const uint32_t (&w
     }
 }
 
-// Wave w of workgroup b streams column block 4*(b/S) + w (128 columns) over
+// Wave w of workgroup b streams column block KW*(b/S) + w (128 columns) over
 // the 128-row pieces [s*PS, min(P, (s+1)*PS)) of split s = b % S and writes
 // its sums to part[block][s][m][column] for m < M.
 // NT: the weight copies are non-temporal.  At N = 14336, K = 4096 that is
 // 13.0 against 14.9 us at M = 1 and still ahead at M = 12 (16.8 / 17.0), but
 // behind from M = 14 (M = 16: 17.9 against 17.4 with the default policy).
 constexpr int KS_NT_MAX_M = 12;
-template <int EL, bool NT>
-__global__ __launch_bounds__(256) void gemv_kn_split_kernel(GemmArgs p, KnSplit sp) {
+template <int EL, bool NT, int KW>
+__global__ __launch_bounds__(KW * 64) void gemv_kn_split_kernel(GemmArgs p, KnSplit sp) {
     constexpr bool F8 = EL == ELEM_F8;
     using AccV = typename std::conditional<F8, v4f, v4i>::type;
     using AccE = typename std::conditional<F8, float, int32_t>::type;
-    __shared__ __attribute__((aligned(1024))) uint8_t ring[KS_NS][4][KS_ITEM];
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[KS_NS][KW][KS_ITEM];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int M = p.M, N = p.N, K = p.K;
     const int S = sp.S;
     const int split = static_cast<int>(blockIdx.x) % S;
-    const int cbg = 4 * (static_cast<int>(blockIdx.x) / S) + wave;  // this wave's column block
+    const int cbg = KW * (static_cast<int>(blockIdx.x) / S) + wave;  // this wave's column block
     const int n0 = cbg * KS_W;
     if (n0 >= N) return;  // no barrier below: the other waves go on alone
     const int P = (K + KS_ROWS - 1) / KS_ROWS;
@@ -163,7 +164,7 @@ __global__ __launch_bounds__(256) void gemv_kn_split_kernel(GemmArgs p, KnSplit 
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.B, K * N);
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, M * K);
     lds_u8* const lring = (lds_u8*)(&ring[0][wave][0]);  // slot q at + q * SLOT
-    constexpr int SLOT = 4 * KS_ITEM;
+    constexpr int SLOT = KW * KS_ITEM;
 
     // Copy geometry.  Weights, copy d: item row i = 8d + l/8 at physical
     // chunk l%8, holding logical chunk (l%8) ^ ks_swz(i); ks_swz(i) is
@@ -570,10 +571,25 @@ hipError_t launch_kn_split_out(const GemmArgs& p, const KnSplit& sp, hipStream_t
         e = hipLaunchKernel(reinterpret_cast<const void*>(&gemv_kn_row_kernel<EL>), dim3(nblk * sp.S),
                             dim3(KR_WAVES * 64), args, 0, stream);
     } else {
-        const int nblk = (p.N + 4 * KS_W - 1) / (4 * KS_W);
-        const void* split = p.M <= KS_NT_MAX_M ? reinterpret_cast<const void*>(&gemv_kn_split_kernel<EL, true>)
-                                               : reinterpret_cast<const void*>(&gemv_kn_split_kernel<EL, false>);
-        e = hipLaunchKernel(split, dim3(nblk * sp.S), dim3(256), args, 0, stream);
+        const int nblk = (p.N + sp.kw * KS_W - 1) / (sp.kw * KS_W);
+        const bool nt = p.M <= KS_NT_MAX_M;
+        const void* split;
+        switch (sp.kw) {
+            case 1:
+                split = nt ? reinterpret_cast<const void*>(&gemv_kn_split_kernel<EL, true, 1>)
+                           : reinterpret_cast<const void*>(&gemv_kn_split_kernel<EL, false, 1>);
+                break;
+            case 2:
+                split = nt ? reinterpret_cast<const void*>(&gemv_kn_split_kernel<EL, true, 2>)
+                           : reinterpret_cast<const void*>(&gemv_kn_split_kernel<EL, false, 2>);
+                break;
+            case 4:
+                split = nt ? reinterpret_cast<const void*>(&gemv_kn_split_kernel<EL, true, 4>)
+                           : reinterpret_cast<const void*>(&gemv_kn_split_kernel<EL, false, 4>);
+                break;
+            default: return hipErrorInvalidValue;
+        }
+        e = hipLaunchKernel(split, dim3(nblk * sp.S), dim3(sp.kw * 64), args, 0, stream);
     }
     if (e != hipSuccess) return e;
     // the split count bounds the partial sums each thread loads at once
@@ -925,36 +941,20 @@ static size_t kn_ws_bytes(int M, int N, int S) {
     return static_cast<size_t>((N + KS_W - 1) / KS_W) * static_cast<size_t>(S) * static_cast<size_t>(M) * KS_W * 4;
 }
 
-// K splits: as many as fill the device's CUs with one 512-column workgroup
-// each (S <= 8, at least one 128-row piece per split, and no more than a
-// workspace of ws_bytes, or a split-pool slot, holds), with no empty split.
-// S = 1: the full kernel.
-// Past CUs / 2 blocks (N > 65536 on 256 CUs) the workgroups take several rounds, and
-// S in 2..4 is the one with the fewest rounds per split (ties: the smaller):
-// at N = 81920 / 98304 / 128256, K = 4096, M = 1, S = 3 / 4 / 2 ran 54 / 64 /
-// 79 us against 88 / 107 / 108 us for the full kernel.
-// M = 1 takes the row kernel instead whenever two or more splits of its
-// 1024-column workgroups fit: S = CUs / blocks (at most 64, whole 128-row
-// pieces, none empty; 16 at N = 14336, K = 4096: 224 workgroups).
-static void kn_splits(const GemmArgs& p, size_t ws_bytes, int* S_out, int* PS_out, int* rowk_out) {
-    const int kCUs = device_cus();
-    if (ws_bytes > FKE_SPLIT_SLOT_BYTES) ws_bytes = FKE_SPLIT_SLOT_BYTES;
+// K splits of the split kernel for workgroups of kw waves (128 columns each):
+// as many as fill the device's CUs with one workgroup each (S <= 8, at least
+// one 128-row piece per split, and no more than a workspace of ws_bytes, or a
+// split-pool slot, holds), with no empty split; grid 0 and S = 1: the full kernel.
+// Past CUs / 2 blocks the workgroups take several rounds, and S in 2..4 is the
+// one with the fewest rounds per split (ties: the smaller): at N = 81920 /
+// 98304 / 128256, K = 4096, M = 1, four-wave workgroups with S = 3 / 4 / 2 ran
+// 54 / 64 / 79 us against 88 / 107 / 108 us for the full kernel.
+struct KsPlan {
+    int S, PS, grid;
+};
+static KsPlan ks_plan(const GemmArgs& p, int kw, int kCUs, size_t ws_bytes) {
     const int P = (p.K + KS_ROWS - 1) / KS_ROWS;
-    *rowk_out = 0;
-    if (p.M == 1) {
-        int S = kCUs / ((p.N + KR_W - 1) / KR_W);
-        if (S > KR_SMAX) S = KR_SMAX;
-        if (S > P) S = P;
-        while (S > 1 && kn_ws_bytes(1, p.N, S) > ws_bytes) --S;
-        if (S >= 2) {
-            const int PS = (P + S - 1) / S;
-            *S_out = (P + PS - 1) / PS;
-            *PS_out = PS;
-            *rowk_out = 1;
-            return;
-        }
-    }
-    const int nblk = (p.N + 4 * KS_W - 1) / (4 * KS_W);
+    const int nblk = (p.N + kw * KS_W - 1) / (kw * KS_W);
     int S = kCUs / nblk;
     if (S < 2) {
         double best = 0.0;
@@ -969,20 +969,69 @@ static void kn_splits(const GemmArgs& p, size_t ws_bytes, int* S_out, int* PS_ou
     if (S > KS_SMAX) S = KS_SMAX;
     if (S > P) S = P;
     while (S > 1 && kn_ws_bytes(p.M, p.N, S) > ws_bytes) --S;
-    if (S < 2) {
-        *S_out = 1;
-        *PS_out = P;
-        return;
-    }
+    if (S < 2) return KsPlan{1, P, 0};
     const int PS = (P + S - 1) / S;
-    *S_out = (P + PS - 1) / PS;
-    *PS_out = PS;
+    S = (P + PS - 1) / PS;
+    return KsPlan{S, PS, nblk * S};
+}
+
+// The plan: M = 1 takes the row kernel whenever two or more splits of its
+// 1024-column workgroups fit: S = CUs / blocks (at most 64, whole 128-row
+// pieces, none empty; 16 at N = 14336, K = 4096: 224 workgroups).  Otherwise
+// the split kernel, on workgroups of two waves (256 columns; four splits at
+// N = 14336), of four when two-wave blocks outnumber half the CUs (N > 32768
+// on 256 CUs: fewer, wider workgroups over several rounds), and of one when
+// two-wave workgroups, their splits capped, fill less than 7/8 of the CUs and
+// one-wave ones fill more (few column blocks, long K), or past 13 rows when
+// one-wave ones fill 7/8 with fewer splits (fewer partial sums).  Same-box A/B
+// (HIP graphs, K = 4096 unless noted, INT8 bf16 out, us): N = 14336, M = 4 /
+// 8 / 10 / 12 / 14 / 16: two waves 13.8 / 14.2 / 14.5 / 14.5 / 15.9 / 16.2,
+// one 14.8 / 15.0 / 15.1 / 15.2 / 15.9 / 16.0, four 14.1 / 15.1 / 15.5 /
+// 16.0 / 16.5 / 16.8; N = 4096, K = 14336, M = 4 / 16: one 13.5 / 15.0, two
+// 17.2 / 18.5, four 24.0 / 25.8; N = 128256, M = 16: four 98.4, two 100.7,
+// one 103.1.
+static void kn_splits(const GemmArgs& p, size_t ws_bytes, KnSplit* sp) {
+    const int kCUs = device_cus();
+    if (ws_bytes > FKE_SPLIT_SLOT_BYTES) ws_bytes = FKE_SPLIT_SLOT_BYTES;
+    const int P = (p.K + KS_ROWS - 1) / KS_ROWS;
+    sp->rowk = 0;
+    if (p.M == 1) {
+        int S = kCUs / ((p.N + KR_W - 1) / KR_W);
+        if (S > KR_SMAX) S = KR_SMAX;
+        if (S > P) S = P;
+        while (S > 1 && kn_ws_bytes(1, p.N, S) > ws_bytes) --S;
+        if (S >= 2) {
+            const int PS = (P + S - 1) / S;
+            sp->S = (P + PS - 1) / PS;
+            sp->PS = PS;
+            sp->rowk = 1;
+            sp->kw = 0;
+            return;
+        }
+    }
+    const int fill = kCUs - kCUs / 8;
+    int kw = 2;
+    KsPlan pl;
+    if ((p.N + 2 * KS_W - 1) / (2 * KS_W) > kCUs / 2) {
+        kw = 4;
+        pl = ks_plan(p, 4, kCUs, ws_bytes);
+    } else {
+        pl = ks_plan(p, 2, kCUs, ws_bytes);
+        const KsPlan p1 = ks_plan(p, 1, kCUs, ws_bytes);
+        if (p1.S > 1 && ((pl.grid < fill && p1.grid > pl.grid) || (p.M > 13 && p1.S < pl.S && p1.grid >= fill))) {
+            kw = 1;
+            pl = p1;
+        }
+    }
+    sp->S = pl.S;
+    sp->PS = pl.PS;
+    sp->kw = kw;
 }
 
 size_t gemv_kn_workspace_bytes(const GemmArgs& p) {
-    int S, PS, rowk;
-    kn_splits(p, SIZE_MAX, &S, &PS, &rowk);
-    return S > 1 ? kn_ws_bytes(p.M, p.N, S) : 0;
+    KnSplit sp;
+    kn_splits(p, SIZE_MAX, &sp);
+    return sp.S > 1 ? kn_ws_bytes(p.M, p.N, sp.S) : 0;
 }
 
 // No split (S = 1) without a workspace, or with one not 16-byte aligned (the
@@ -990,7 +1039,7 @@ size_t gemv_kn_workspace_bytes(const GemmArgs& p) {
 KnSplit gemv_kn_plan(const GemmArgs& p, void* ws, size_t ws_bytes) {
     KnSplit sp;
     const bool usable = ws && (reinterpret_cast<uintptr_t>(ws) & 15) == 0;
-    kn_splits(p, usable ? ws_bytes : 0, &sp.S, &sp.PS, &sp.rowk);
+    kn_splits(p, usable ? ws_bytes : 0, &sp);
     sp.part = sp.S > 1 ? ws : nullptr;
     return sp;
 }

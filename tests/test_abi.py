@@ -77,20 +77,24 @@ def test_workspace_entry_points_reject_bad_arguments():
 
 
 @pytest.mark.parametrize("M,N,K,layout,expect", [
-    # C2 with B [K,N]: 28 workgroups of 512 columns x 8 K splits, [M][N] int32 partials each;
-    # M = 1 on the row kernel: 14 workgroups of 1024 columns x 16 splits
+    # C2 with B [K,N], [M][N] int32 partials per split: M = 1 on the row kernel, 14 workgroups
+    # of 1024 columns x 16 splits; M = 16 on one-wave workgroups, 112 of 128 columns x 2
+    # splits; M = 4 on two-wave workgroups, 56 of 256 columns x 4 splits
     (1, 14336, 4096, 1, 16 * 1 * 14336 * 4),
-    (16, 14336, 4096, 1, 8 * 16 * 14336 * 4),
+    (16, 14336, 4096, 1, 2 * 16 * 14336 * 4),
+    (4, 14336, 4096, 1, 4 * 4 * 14336 * 4),
     # row kernel: 4 blocks -> 64 splits at most, 112 pieces in 56 splits of 2;
     # 126 blocks -> 2 splits
     (1, 4096, 14336, 1, 56 * 1 * 4096 * 4),
     (1, 128256, 4096, 1, 2 * 1 * 128256 * 4),
     # splits capped by the 128-row pieces of K: K = 512 -> 4 splits
     (4, 14336, 512, 1, 4 * 4 * 14336 * 4),
-    # N = 2^16: 128 blocks of 512 columns -> 2 splits
+    # N = 2^16: four-wave workgroups, 128 blocks of 512 columns -> 2 splits
     (2, 65536, 4096, 1, 2 * 2 * 65536 * 4),
-    # N rounded up to 128-column blocks
+    # N rounded up to 128-column blocks (one-wave workgroups: 9 blocks x 8 splits)
     (3, 1040, 4096, 1, 8 * 3 * 1152 * 4),
+    # M = 16, N = 20016, K = 2048: two-wave workgroups x 3 splits (one-wave ones split as often)
+    (16, 20016, 2048, 1, 3 * 16 * 20096 * 4),
     # unsplit: K of one piece, the decode not taken (M > 16, B [N,K], N % 16 != 0, K % 64 != 0)
     (1, 14336, 128, 1, 0), (17, 14336, 4096, 1, 0), (1, 14336, 4096, 0, 0), (1, 1000, 4096, 1, 0),
     (1, 14336, 4000, 1, 0), (0, 14336, 4096, 1, 0), (1, 14336, 4096, 2, 0),

@@ -374,8 +374,9 @@ def test_gemv_kn_split_full_and_fewer_splits(oracle, dev, M):
     A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 9100 + M, layout="kn", act="normal")
     acc = oracle.w8a8_acc(A, B, oracle.B_KN, nthreads=NTH)
     need = _lib.lib().fke_qgemm_workspace_size(M, N, K, _lib.B_KN)
-    # [M][N] int32 partial sums per split: 8 splits, 16 on the M = 1 row kernel
-    assert need == 4 * (16 if M == 1 else 8) * M * N
+    # [M][N] int32 partial sums per split: 16 on the M = 1 row kernel, 2 on the one-wave split
+    # workgroups at M = 16
+    assert need == 4 * {1: 16, 16: 2}[M] * M * N
     dA, dB, dsa, dsb, dbias = dev_t(A), dev_t(B), dev_t(sa), dev_t(sb), dev_t(bias)
     for nbytes in (need, need // 3, 0):
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev) if nbytes else None
