@@ -153,10 +153,16 @@ std::mutex g_noalloc_mu[kMaxDevices];
 hipStream_t g_noalloc_last[kMaxDevices];
 bool g_noalloc_recorded[kMaxDevices];
 
-// The [K,N] decode, split over the workspace `wc` gives.
+int run_mfma(int path, const GemmArgs& p, int elem, hipStream_t s, const WsChoice& wc = WsChoice{});
+
+// The [K,N] decode, split over the workspace `wc` gives.  Past 16 rows it
+// needs its split (the one-kernel decode takes 16 rows); a workspace without
+// room for one gets the MFMA GEMM.
 hipError_t run_kn(const GemmArgs& p, int elem, hipStream_t s, const WsChoice& wc) {
     const Workspace ws = split_workspace(s, fke::gemv_kn_workspace_bytes(p), wc);
-    return fke::launch_gemv_kn(p, elem, fke::gemv_kn_plan(p, ws.ptr, ws.bytes), s);
+    const fke::KnSplit sp = fke::gemv_kn_plan(p, ws.ptr, ws.bytes);
+    if (sp.S < 2 && p.M > 16) return static_cast<hipError_t>(run_mfma(FKE_PATH_MFMA, p, elem, s, wc));
+    return fke::launch_gemv_kn(p, elem, sp, s);
 }
 
 int run_i8(int path, const GemmArgs& p, void* stream, const WsChoice& wc = WsChoice{});
@@ -287,7 +293,7 @@ int mfma_tile_of_path(int path, const GemmArgs& p) {
 // automatic tile also takes the K split the plan gives (8-bit shapes with few
 // tiles and a long K), on the workspace `wc` gives; unsplit, on the tile
 // rule's tile, when that does not hold the partial sums.
-int run_mfma(int path, const GemmArgs& p, int elem, hipStream_t s, const WsChoice& wc = WsChoice{}) {
+int run_mfma(int path, const GemmArgs& p, int elem, hipStream_t s, const WsChoice& wc) {
     const int tile = mfma_tile_of_path(path, p);
     if (tile < 0 || !fke::mfma_supports(p, elem)) return hipErrorInvalidValue;
     if (tile == fke::MFMA_TILE_AUTO) {

@@ -67,13 +67,13 @@ constexpr int KS_W = 128;                // columns (bytes of a B row) per wave
 constexpr int KS_CB = KS_W / 16;         // 16-column MFMA blocks per wave
 constexpr int KS_ROWS = 128;             // k rows per item
 constexpr int KS_BI = KS_ROWS * KS_W;    // weight bytes per item (16 KiB)
-constexpr int KS_AI = 16 * KS_ROWS;      // activation bytes per item (2 KiB)
-constexpr int KS_ITEM = KS_BI + KS_AI;   // 18 KiB
+constexpr int KS_AI = 16 * KS_ROWS;      // activation bytes per item and 16-row block (2 KiB)
+constexpr int KS_ITEM = KS_BI + KS_AI;   // 18 KiB (one activation block)
 constexpr int KS_DB = KS_BI / 1024;      // weight copies per item
-constexpr int KS_DA = KS_AI / 1024;      // activation copies per item
-constexpr int KS_DI = KS_DB + KS_DA;     // copies per item
+constexpr int KS_DA = KS_AI / 1024;      // activation copies per item and block
 constexpr int KS_NS = 2;                 // ring slots per wave (144 KiB of LDS per workgroup)
 constexpr int KS_SMAX = 8;               // K splits at most
+constexpr int KN_MAX_M = 32;             // rows at most (two 16-row activation blocks)
 
 // LDS layouts (16-byte chunks, swizzled so that every 16-lane group of a read
 // touches 32 distinct banks and every 32-lane half 64, whether the LDS serves
@@ -101,17 +101,21 @@ __device__ __forceinline__ v2i ks_rdtr(const lds_u8* a) {
 }
 // Every LDS read has landed; the registers they wrote are tied to the wait,
 // so nothing reads (or copies) them before it.
-__device__ __forceinline__ void ks_lgkm_wait_all(v4i (&a)[2], v2i (&t)[32]) {
+template <int MB>
+__device__ __forceinline__ void ks_lgkm_wait_all(v4i (&a)[MB][2], v2i (&t)[32]) {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    asm volatile("" : "+v"(a[0]), "+v"(a[1]));
+#pragma unroll
+    for (int b = 0; b < MB; ++b) asm volatile("" : "+v"(a[b][0]), "+v"(a[b][1]));
 #pragma unroll
     for (int i = 0; i < 32; ++i) asm volatile("" : "+v"(t[i]));
 }
-// s_waitcnt vmcnt(KS_DI * n): every copy but those of the n latest items has landed.
+// s_waitcnt vmcnt(DI * n) for DI copies per item: every copy but those of
+// the n latest items has landed.
+template <int DI>
 __device__ __forceinline__ void ks_wait_items(int n) {
-    static_assert(KS_DI == 18 && KS_NS == 2, "vmcnt steps below: 18 copies, at most one later item");
+    static_assert(KS_NS == 2, "at most one later item");
     if (n == 0) wait_vm<0>();
-    else wait_vm<18>();
+    else wait_vm<DI>();
 }
 
 // Weight read of item fragment X (compile-time), at an immediate offset from
@@ -120,11 +124,12 @@ __device__ __forceinline__ void ks_wait_items(int n) {
 //  FP8:  X = 4cb + t       -> rows 32G + 8t + b of block cb (the swizzle
 //        flips bit 0 of the chunk for t >= 2, i.e. block cb ^ 1's address).
 // At most 14 LDS reads are in flight when one is issued (lgkmcnt is 4 bits;
-// the two activation reads come first).
-template <bool F8, int X>
+// the NA activation reads come first).
+template <bool F8, int NA, int X>
 __device__ __forceinline__ void ks_read_w(const lds_u8* slot, const uint32_t (&wadr)[KS_CB], v2i (&tr)[32]) {
+    static_assert(NA <= 13, "the activation reads leave room for the weight reads");
     if constexpr (X < 32) {
-        if constexpr (X + 2 >= 14) asm volatile("s_waitcnt lgkmcnt(13)" ::: "memory");
+        if constexpr (X + NA >= 14) asm volatile("s_waitcnt lgkmcnt(13)" ::: "memory");
         if constexpr (F8) {
             constexpr int cb = X >> 2, t = X & 3;
             tr[X] = ks_rdtr<8 * t * KS_W>(slot + wadr[t >= 2 ? (cb ^ 1) : cb]);
@@ -132,7 +137,7 @@ __device__ __forceinline__ void ks_read_w(const lds_u8* slot, const uint32_t (&w
             constexpr int s = X >> 4, cb = (X >> 1) & 7, t = X & 1;
             tr[X] = ks_rdtr<(64 * s + 8 * t) * KS_W>(slot + wadr[cb]);
         }
-        ks_read_w<F8, X + 1>(slot, wadr, tr);
+        ks_read_w<F8, NA, X + 1>(slot, wadr, tr);
     }
 }
 
@@ -143,12 +148,16 @@ __device__ __forceinline__ void ks_read_w(const lds_u8* slot, const uint32_t (&w
 // 13.0 against 14.9 us at M = 1 and still ahead at M = 12 (16.8 / 17.0), but
 // behind from M = 14 (M = 16: 17.9 against 17.4 with the default policy).
 constexpr int KS_NT_MAX_M = 12;
-template <int EL, bool NT, int KW>
+template <int EL, bool NT, int KW, int MB>
 __global__ __launch_bounds__(KW * 64) void gemv_kn_split_kernel(GemmArgs p, KnSplit sp) {
     constexpr bool F8 = EL == ELEM_F8;
+    constexpr int ITEM = KS_BI + MB * KS_AI;  // bytes per item: weights, then MB activation blocks
+    constexpr int DA = MB * KS_DA;            // activation copies per item
+    constexpr int DI = KS_DB + DA;            // copies per item
+    static_assert(KS_NS * KW * ITEM <= 160 * 1024, "the ring fits the LDS");
     using AccV = typename std::conditional<F8, v4f, v4i>::type;
     using AccE = typename std::conditional<F8, float, int32_t>::type;
-    __shared__ __attribute__((aligned(1024))) uint8_t ring[KS_NS][KW][KS_ITEM];
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[KS_NS][KW][ITEM];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -164,7 +173,7 @@ __global__ __launch_bounds__(KW * 64) void gemv_kn_split_kernel(GemmArgs p, KnSp
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.B, K * N);
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, M * K);
     lds_u8* const lring = (lds_u8*)(&ring[0][wave][0]);  // slot q at + q * SLOT
-    constexpr int SLOT = KW * KS_ITEM;
+    constexpr int SLOT = KW * ITEM;
 
     // Copy geometry.  Weights, copy d: item row i = 8d + l/8 at physical
     // chunk l%8, holding logical chunk (l%8) ^ ks_swz(i); ks_swz(i) is
@@ -174,11 +183,11 @@ __global__ __launch_bounds__(KW * 64) void gemv_kn_split_kernel(GemmArgs p, KnSp
     const int lr = lane >> 3, lc = lane & 7;
     const uint32_t bbase0 = static_cast<uint32_t>(lr * N + n0 + 16 * (lc ^ lr));
     const uint32_t bbase1 = static_cast<uint32_t>(lr * N + n0 + 16 * (lc ^ lr ^ 1));
-    uint32_t aoff[KS_DA];
-    int akb[KS_DA];
-    bool arow[KS_DA];
+    uint32_t aoff[DA];
+    int akb[DA];
+    bool arow[DA];
 #pragma unroll
-    for (int d = 0; d < KS_DA; ++d) {
+    for (int d = 0; d < DA; ++d) {
         const int m = 8 * d + lr;
         const int c = lc ^ ks_aswz(m);
         arow[d] = m < M;
@@ -194,7 +203,7 @@ __global__ __launch_bounds__(KW * 64) void gemv_kn_split_kernel(GemmArgs p, KnSp
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, dst + d * 1024, 16, static_cast<int>(off), 0, 0, NT ? 2 : 0);
         }
 #pragma unroll
-        for (int d = 0; d < KS_DA; ++d) {
+        for (int d = 0; d < DA; ++d) {
             const uint32_t off = arow[d] && k0 + akb[d] < K ? aoff[d] + static_cast<uint32_t>(k0) : 0x80000000u;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, dst + KS_BI + d * 1024, 16, static_cast<int>(off), 0, 0, 0);
         }
@@ -220,14 +229,16 @@ __global__ __launch_bounds__(KW * 64) void gemv_kn_split_kernel(GemmArgs p, KnSp
         aadr[e] = static_cast<uint32_t>(KS_BI + am * KS_ROWS + 16 * (c ^ ks_aswz(am)));
     }
 
-    AccV acc[KS_CB];
+    AccV acc[MB][KS_CB];
     // The stream on raw codes (SAN false), or with FP8's 0x7F / 0xFF codes
     // cleared on the VALU (SAN true, FP8's replay).
     auto stream = [&](auto sanc) __attribute__((always_inline)) {
         constexpr bool SAN = decltype(sanc)::value;
         (void)SAN;
 #pragma unroll
-        for (int cb = 0; cb < KS_CB; ++cb) acc[cb] = AccV{0, 0, 0, 0};
+        for (int b = 0; b < MB; ++b)
+#pragma unroll
+            for (int cb = 0; cb < KS_CB; ++cb) acc[b][cb] = AccV{0, 0, 0, 0};
 
         int issued = 0;
 #pragma unroll
@@ -238,14 +249,17 @@ __global__ __launch_bounds__(KW * 64) void gemv_kn_split_kernel(GemmArgs p, KnSp
             }
         for (int c = 0; c < np; ++c) {
             lds_u8* const slot = lring + (c % KS_NS) * SLOT;
-            ks_wait_items(issued - c - 1);
+            ks_wait_items<DI>(issued - c - 1);
             // Fragments to registers, then the slot is refilled before the MFMAs.
-            v4i af[2];
+            v4i af[MB][2];
             v2i tr[32];
-            af[0] = ks_rd128(slot + aadr[0]);
-            af[1] = ks_rd128(slot + aadr[1]);
-            ks_read_w<F8, 0>(slot, wadr, tr);
-            ks_lgkm_wait_all(af, tr);
+#pragma unroll
+            for (int b = 0; b < MB; ++b) {
+                af[b][0] = ks_rd128(slot + aadr[0] + b * KS_AI);
+                af[b][1] = ks_rd128(slot + aadr[1] + b * KS_AI);
+            }
+            ks_read_w<F8, 2 * MB, 0>(slot, wadr, tr);
+            ks_lgkm_wait_all<MB>(af, tr);
             v4i wf[16];  // INT8: [2 steps][8 blocks] of 16 k bytes; FP8: [8 blocks][2 halves] of 16 k bytes
 #pragma unroll
             for (int x = 0; x < 16; ++x) wf[x] = v4i{tr[2 * x][0], tr[2 * x][1], tr[2 * x + 1][0], tr[2 * x + 1][1]};
@@ -256,28 +270,36 @@ __global__ __launch_bounds__(KW * 64) void gemv_kn_split_kernel(GemmArgs p, KnSp
             if constexpr (F8) {
                 if constexpr (SAN) {
 #pragma unroll
-                    for (int h = 0; h < 2; ++h)
+                    for (int b = 0; b < MB; ++b)
 #pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            af[h][e] = static_cast<int>(e4m3_sanitize(static_cast<uint32_t>(af[h][e])));
+                        for (int h = 0; h < 2; ++h)
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                af[b][h][e] = static_cast<int>(e4m3_sanitize(static_cast<uint32_t>(af[b][h][e])));
 #pragma unroll
                     for (int x = 0; x < 16; ++x)
 #pragma unroll
                         for (int e = 0; e < 4; ++e)
                             wf[x][e] = static_cast<int>(e4m3_sanitize(static_cast<uint32_t>(wf[x][e])));
                 }
-                const v8i a8 = __builtin_shufflevector(af[0], af[1], 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
-                for (int cb = 0; cb < KS_CB; ++cb)
-                    acc[cb] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                        a8, __builtin_shufflevector(wf[2 * cb], wf[2 * cb + 1], 0, 1, 2, 3, 4, 5, 6, 7), acc[cb], 0, 0,
-                        0, 0, 0, 0);
+                for (int b = 0; b < MB; ++b) {
+                    const v8i a8 = __builtin_shufflevector(af[b][0], af[b][1], 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+                    for (int cb = 0; cb < KS_CB; ++cb)
+                        acc[b][cb] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                            a8, __builtin_shufflevector(wf[2 * cb], wf[2 * cb + 1], 0, 1, 2, 3, 4, 5, 6, 7), acc[b][cb],
+                            0, 0, 0, 0, 0, 0);
+                }
             } else {
 #pragma unroll
                 for (int s = 0; s < 2; ++s)
 #pragma unroll
-                    for (int cb = 0; cb < KS_CB; ++cb)
-                        acc[cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[s], wf[8 * s + cb], acc[cb], 0, 0, 0);
+                    for (int b = 0; b < MB; ++b)
+#pragma unroll
+                        for (int cb = 0; cb < KS_CB; ++cb)
+                            acc[b][cb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[b][s], wf[8 * s + cb], acc[b][cb], 0,
+                                                                               0, 0);
             }
         }
     };
@@ -296,20 +318,27 @@ __global__ __launch_bounds__(KW * 64) void gemv_kn_split_kernel(GemmArgs p, KnSp
         stream(std::false_type{});
         bool bad = false;
 #pragma unroll
-        for (int cb = 0; cb < KS_CB; ++cb)
+        for (int b = 0; b < MB; ++b)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) bad |= __builtin_isnan(acc[cb][v]);
+            for (int cb = 0; cb < KS_CB; ++cb)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) bad |= __builtin_isnan(acc[b][cb][v]);
         if (__builtin_amdgcn_ballot_w64(bad) != 0) stream(std::true_type{});
     }
 
-    // Lane l of block cb holds column 16cb + l%16, rows 4(l/16) + v.
+    // Lane l of activation block b and column block cb holds column
+    // 16cb + l%16, rows 16b + 4(l/16) + v.
     AccE* const part = static_cast<AccE*>(sp.part) + (static_cast<size_t>(cbg) * S + split) * M * KS_W;
-    const int j = lane & 15, mb = 4 * G;
+    const int j = lane & 15;
 #pragma unroll
-    for (int cb = 0; cb < KS_CB; ++cb)
+    for (int b = 0; b < MB; ++b) {
+        const int mb = 16 * b + 4 * G;
 #pragma unroll
-        for (int v = 0; v < 4; ++v)
-            if (mb + v < M) part[(mb + v) * KS_W + 16 * cb + j] = acc[cb][v];
+        for (int cb = 0; cb < KS_CB; ++cb)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                if (mb + v < M) part[(mb + v) * KS_W + 16 * cb + j] = acc[b][cb][v];
+    }
 }
 
 // One thread per output (m, n): the S partials in split order, then the
@@ -560,6 +589,31 @@ __global__ __launch_bounds__(KR_WAVES * 64) void gemv_kn_row_kernel(GemmArgs p, 
     }
 }
 
+// The split kernel for M rows on kw-wave workgroups: 16-row activation blocks
+// MB = 1 or 2 (M <= 16 / 32), non-temporal weight copies up to KS_NT_MAX_M
+// rows; four waves only with one block.  (Four blocks, M <= 64, measured
+// slower than the MFMA GEMM's 64x64 ring past 32 rows: N = 14336, K = 4096,
+// M = 48 / 64 21.8 / 23.2 us on two-wave workgroups and 25.5 / 26.4 on one-wave
+// ones against 21.4 / 21.8.)
+template <int EL>
+const void* ks_kernel(int M, int kw) {
+    if (M <= 16) {
+        const bool nt = M <= KS_NT_MAX_M;
+        switch (kw) {
+            case 1: return nt ? reinterpret_cast<const void*>(&gemv_kn_split_kernel<EL, true, 1, 1>)
+                              : reinterpret_cast<const void*>(&gemv_kn_split_kernel<EL, false, 1, 1>);
+            case 2: return nt ? reinterpret_cast<const void*>(&gemv_kn_split_kernel<EL, true, 2, 1>)
+                              : reinterpret_cast<const void*>(&gemv_kn_split_kernel<EL, false, 2, 1>);
+            case 4: return nt ? reinterpret_cast<const void*>(&gemv_kn_split_kernel<EL, true, 4, 1>)
+                              : reinterpret_cast<const void*>(&gemv_kn_split_kernel<EL, false, 4, 1>);
+            default: return nullptr;
+        }
+    }
+    if ((kw != 1 && kw != 2) || M > KN_MAX_M) return nullptr;
+    return kw == 1 ? reinterpret_cast<const void*>(&gemv_kn_split_kernel<EL, false, 1, 2>)
+                   : reinterpret_cast<const void*>(&gemv_kn_split_kernel<EL, false, 2, 2>);
+}
+
 template <int EL, int OUT>
 hipError_t launch_kn_split_out(const GemmArgs& p, const KnSplit& sp, hipStream_t stream) {
     GemmArgs a = p;
@@ -572,23 +626,8 @@ hipError_t launch_kn_split_out(const GemmArgs& p, const KnSplit& sp, hipStream_t
                             dim3(KR_WAVES * 64), args, 0, stream);
     } else {
         const int nblk = (p.N + sp.kw * KS_W - 1) / (sp.kw * KS_W);
-        const bool nt = p.M <= KS_NT_MAX_M;
-        const void* split;
-        switch (sp.kw) {
-            case 1:
-                split = nt ? reinterpret_cast<const void*>(&gemv_kn_split_kernel<EL, true, 1>)
-                           : reinterpret_cast<const void*>(&gemv_kn_split_kernel<EL, false, 1>);
-                break;
-            case 2:
-                split = nt ? reinterpret_cast<const void*>(&gemv_kn_split_kernel<EL, true, 2>)
-                           : reinterpret_cast<const void*>(&gemv_kn_split_kernel<EL, false, 2>);
-                break;
-            case 4:
-                split = nt ? reinterpret_cast<const void*>(&gemv_kn_split_kernel<EL, true, 4>)
-                           : reinterpret_cast<const void*>(&gemv_kn_split_kernel<EL, false, 4>);
-                break;
-            default: return hipErrorInvalidValue;
-        }
+        const void* split = ks_kernel<EL>(p.M, sp.kw);
+        if (!split) return hipErrorInvalidValue;
         e = hipLaunchKernel(split, dim3(nblk * sp.S), dim3(sp.kw * 64), args, 0, stream);
     }
     if (e != hipSuccess) return e;
@@ -925,9 +964,10 @@ hipError_t launch_kn_full(const GemmArgs& p, hipStream_t stream) {
 
 }  // namespace
 
-bool gemv_kn_supports(const GemmArgs& p, int elem) {
+// The shapes the [K,N] kernels take (gemv_kn_supports adds the plan's rule past 16 rows).
+static bool kn_shape_ok(const GemmArgs& p, int elem) {
     const uintptr_t a = reinterpret_cast<uintptr_t>(p.A), b = reinterpret_cast<uintptr_t>(p.B);
-    if (p.b_layout != FKE_B_KN || p.swiglu || p.M < 1 || p.M > 16 || p.N < 1 || p.K < 64) return false;
+    if (p.b_layout != FKE_B_KN || p.swiglu || p.M < 1 || p.M > KN_MAX_M || p.N < 1 || p.K < 64) return false;
     if (elem != ELEM_I8 && elem != ELEM_F8) return false;
     if (elem == ELEM_F8 && p.out_dtype == FKE_OUT_I32) return false;
     // 16-byte copies: row starts (B: k*N + n, A: m*K + k) must stay 16-byte aligned
@@ -1028,6 +1068,20 @@ static void kn_splits(const GemmArgs& p, size_t ws_bytes, KnSplit* sp) {
     sp->kw = kw;
 }
 
+// 17..32 rows (two activation blocks per item) only where the split
+// plan, at a pool slot's size, fills 7/8 of the CUs or more in one round on
+// one- or two-wave workgroups; other batches go to the MFMA GEMM's tiles.
+bool gemv_kn_supports(const GemmArgs& p, int elem) {
+    if (!kn_shape_ok(p, elem)) return false;
+    if (p.M <= 16) return true;
+    KnSplit sp;
+    kn_splits(p, SIZE_MAX, &sp);
+    if (sp.S < 2 || sp.rowk || sp.kw == 4) return false;
+    const int kCUs = device_cus();
+    const int grid = (p.N + sp.kw * KS_W - 1) / (sp.kw * KS_W) * sp.S;
+    return grid <= kCUs && grid >= kCUs - kCUs / 8;
+}
+
 size_t gemv_kn_workspace_bytes(const GemmArgs& p) {
     KnSplit sp;
     kn_splits(p, SIZE_MAX, &sp);
@@ -1045,6 +1099,7 @@ KnSplit gemv_kn_plan(const GemmArgs& p, void* ws, size_t ws_bytes) {
 }
 
 hipError_t launch_gemv_kn(const GemmArgs& p, int elem, const KnSplit& sp, hipStream_t stream) {
+    if (sp.S < 2 && p.M > 16) return hipErrorInvalidValue;  // the full kernel takes 16 rows
     if (sp.S > 1) {
         if (!sp.part) return hipErrorInvalidValue;
         return elem == ELEM_F8 ? launch_kn_split<ELEM_F8>(p, sp, stream) : launch_kn_split<ELEM_I8>(p, sp, stream);

@@ -95,8 +95,10 @@ def test_workspace_entry_points_reject_bad_arguments():
     (3, 1040, 4096, 1, 8 * 3 * 1152 * 4),
     # M = 16, N = 20016, K = 2048: two-wave workgroups x 3 splits (one-wave ones split as often)
     (16, 20016, 2048, 1, 3 * 16 * 20096 * 4),
+    # 17..32 rows on the split decode: one-wave workgroups x 2 splits at N = 14336
+    (17, 14336, 4096, 1, 2 * 17 * 14336 * 4), (32, 14336, 4096, 1, 2 * 32 * 14336 * 4),
     # unsplit: K of one piece, the decode not taken (M > 16, B [N,K], N % 16 != 0, K % 64 != 0)
-    (1, 14336, 128, 1, 0), (17, 14336, 4096, 1, 0), (1, 14336, 4096, 0, 0), (1, 1000, 4096, 1, 0),
+    (1, 14336, 128, 1, 0), (33, 14336, 4096, 1, 0), (1, 14336, 4096, 0, 0), (1, 1000, 4096, 1, 0),
     (1, 14336, 4000, 1, 0), (0, 14336, 4096, 1, 0), (1, 14336, 4096, 2, 0),
 ])
 def test_workspace_size(M, N, K, layout, expect):
@@ -289,7 +291,10 @@ def test_path_unavailable_for_shape_is_rejected():
     (512, 4096, 14336, 0, _lib.PATH_MFMA),
     (17, 14336, 1024, 0, _lib.PATH_MFMA),    # K < 2048: no streamed batch kernel
     (100, 4096, 2112, 0, _lib.PATH_MFMA),    # K % 128 != 0: the MFMA GEMM, its last K stage cleared past K
-    (17, 14336, 4096, 1, _lib.PATH_MFMA),
+    (17, 14336, 4096, 1, _lib.PATH_GEMV),    # B [K,N] to 32 rows: the split decode while its plan fills the CUs
+    (32, 14336, 4096, 1, _lib.PATH_GEMV),
+    (33, 14336, 4096, 1, _lib.PATH_MFMA),
+    (32, 131072, 4096, 1, _lib.PATH_MFMA),   # four-wave workgroups over several rounds: the MFMA GEMM
     (4096, 11008, 4096, 0, _lib.PATH_MFMA),
     (8192, 8192, 8192, 0, _lib.PATH_MFMA),
     (8192, 8192, 8192, 1, _lib.PATH_MFMA),
@@ -297,7 +302,7 @@ def test_path_unavailable_for_shape_is_rejected():
     (16, 14336, 4096, 1, _lib.PATH_GEMV),
     (4, 4096, 64, 1, _lib.PATH_GEMV),
     (4, 4104, 4096, 1, _lib.PATH_GENERIC),   # B [K,N] with N % 16 != 0: neither fast kernel
-    (17, 4096, 4096, 1, _lib.PATH_MFMA),
+    (17, 4096, 4096, 1, _lib.PATH_GEMV),
     (64, 64, 100, 0, _lib.PATH_GENERIC),
     (64, 64, 4, 0, _lib.PATH_GENERIC),
     (8, 64, 96, 0, _lib.PATH_MFMA),          # K of 6 16-byte chunks: one partial stage
@@ -326,7 +331,8 @@ def test_dispatch_unaligned_pointer_falls_back():
     (64, 14336, 4096, 0, _lib.PATH_MFMA),     # batches past 32 rows: the MFMA GEMM's 64x64 ring
     (1, 14336, 4096, 1, _lib.PATH_GEMV),      # B [K,N] (the reference layout): transposing decode kernel
     (16, 14336, 4096, 1, _lib.PATH_GEMV),
-    (17, 14336, 4096, 1, _lib.PATH_MFMA),
+    (17, 14336, 4096, 1, _lib.PATH_GEMV),
+    (33, 14336, 4096, 1, _lib.PATH_MFMA),
     (4, 14336, 4000, 1, _lib.PATH_MFMA),      # K % 64 != 0: not the decode kernel; the MFMA GEMM (K % 16 == 0)
     (4, 14336, 4004, 1, _lib.PATH_GENERIC),   # K % 16 != 0
     (8192, 8192, 8192, 0, _lib.PATH_MFMA),

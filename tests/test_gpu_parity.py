@@ -307,9 +307,11 @@ def test_c2_decode_full_b_kn(oracle, dev, M):
 # 3 / 3 / 2 items, S = 2).  M = 1 runs the row kernel: 1024-column blocks, one
 # block with 16 valid columns (32 splits), 56 splits of K = 14336, 17 splits
 # of which the last has one 128-row piece (K = 4160), and 81 blocks x 3.
+# 17..32 rows: two activation blocks on one-wave workgroups (rows 29..31 of
+# the second empty in one) and on two-wave workgroups.
 KN_SHAPES = [(1, 16, 4096), (3, 304, 1024), (16, 1040, 192), (5, 4096, 64), (2, 4096, 14336),
              (16, 20016, 2048), (8, 1008, 4160), (1, 82000, 1024), (9, 100000, 512),
-             (1, 4096, 14336), (1, 14352, 4160)]
+             (1, 4096, 14336), (1, 14352, 4160), (17, 14336, 4096), (32, 20016, 2048), (29, 4096, 4096)]
 
 
 @pytest.mark.parametrize("M,N,K", KN_SHAPES)
@@ -363,20 +365,21 @@ def kn_i8_ws(A, B, sa, sb, bias, out, ws, ws_bytes, stream=None, ws_shift=0, c_s
     return C
 
 
-@pytest.mark.parametrize("M", [1, 16])
+@pytest.mark.parametrize("M", [1, 16, 24])
 def test_gemv_kn_split_full_and_fewer_splits(oracle, dev, M):
     """C2 with B [K,N] through fke_qgemm_i8_ws: the K-split kernels on a
     workspace of fke_qgemm_workspace_size bytes, on a third of it (fewer
-    splits) and on none (the one-kernel full-K decode), every output dtype
-    bit-exact against the oracle."""
+    splits) and on none (the one-kernel full-K decode; past 16 rows the MFMA
+    GEMM), every output dtype bit-exact against the oracle."""
     N, K = 14336, 4096
     say("c2 kn split/full", M, N, K)
     A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 9100 + M, layout="kn", act="normal")
     acc = oracle.w8a8_acc(A, B, oracle.B_KN, nthreads=NTH)
     need = _lib.lib().fke_qgemm_workspace_size(M, N, K, _lib.B_KN)
     # [M][N] int32 partial sums per split: 16 on the M = 1 row kernel, 2 on the one-wave split
-    # workgroups at M = 16
-    assert need == 4 * {1: 16, 16: 2}[M] * M * N
+    # workgroups at M = 16 and 24 (past 16 rows a workspace without room for the split, or one
+    # not 16-byte aligned, gives the MFMA GEMM)
+    assert need == 4 * {1: 16, 16: 2, 24: 2}[M] * M * N
     dA, dB, dsa, dsb, dbias = dev_t(A), dev_t(B), dev_t(sa), dev_t(sb), dev_t(bias)
     for nbytes in (need, need // 3, 0):
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev) if nbytes else None
