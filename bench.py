@@ -492,9 +492,13 @@ def gemv_bytes(M, N, K, out_bytes=2, bias=True):
     return M * K + N * K + 4 * M + 4 * N + (4 * N if bias else 0) + out_bytes * M * N
 
 
-def graph_us(torch, dev, launch, launches, warm, reps=3):
+def graph_us(torch, dev, launch, launches, warm, reps=3, windows=3, detail=None):
     """Per-launch microseconds of `launch(i, stream)` captured `launches` times in
-    one HIP graph, replayed `reps` times; events on the graph's stream."""
+    one HIP graph: `windows` timed windows of `reps` replays each (events on the
+    graph's stream), their median returned and every window's figure appended to
+    `detail` when given.  (The boxes now and then run a few milliseconds of HBM
+    traffic about 30 % slower, every kernel alike; the median keeps one such
+    window from setting the figure.)"""
     s = torch.cuda.Stream(device=dev)
     s.wait_stream(torch.cuda.current_stream(dev))
     with torch.cuda.stream(s):  # warm up outside the graph
@@ -509,14 +513,19 @@ def graph_us(torch, dev, launch, launches, warm, reps=3):
     with torch.cuda.stream(s):
         g.replay()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    with torch.cuda.stream(s):  # replay on s, where the events are recorded
-        e0.record(s)
-        for _ in range(reps):
-            g.replay()
-        e1.record(s)
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) * 1e3 / (reps * launches)
+    per = []
+    for _ in range(windows):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(s):  # replay on s, where the events are recorded
+            e0.record(s)
+            for _ in range(reps):
+                g.replay()
+            e1.record(s)
+        torch.cuda.synchronize()
+        per.append(e0.elapsed_time(e1) * 1e3 / (reps * launches))
+    if detail is not None:
+        detail.extend(round(x, 3) for x in per)
+    return sorted(per)[len(per) // 2]
 
 
 def eager_us(torch, dev, launch, launches):
@@ -591,7 +600,8 @@ def gemv_bench(torch, L, _lib, dev, gen, M, nbuf, launches, N=14336, K=4096, lay
         if st:
             raise RuntimeError(f"gemv failed: {_lib.status_string(st)}")
 
-    us = graph_us(torch, dev, launch, launches, 2 * nbuf)
+    windows = []
+    us = graph_us(torch, dev, launch, launches, 2 * nbuf, detail=windows)
     eager = eager_us(torch, dev, launch, launches)
     nbytes = gemv_bytes(M, N, K)
     gbs = nbytes / (us * 1e-6) / 1e9
@@ -601,9 +611,10 @@ def gemv_bench(torch, L, _lib, dev, gen, M, nbuf, launches, N=14336, K=4096, lay
     return {"metric": f"HBM GB/s, decode GEMV M={M} N={N} K={K}, B {'[N,K]' if layout == 'nk' else '[K,N]'} "
                       f"(bf16 out, fused bias)",
             "value": round(gbs, 1), "unit": "GB/s", "us_per_launch": round(us, 3),
-            "us_per_call_eager": round(eager, 3),
+            "us_per_launch_windows": windows, "us_per_call_eager": round(eager, 3),
             "weight_buffers": nbuf, "weight_bytes_cycled": nbuf * N * K,
-            "timing": f"HIP graph of {launches} launches x 3 replays, events on the graph's stream",
+            "timing": f"HIP graph of {launches} launches, median of 3 windows of 3 replays, events on the "
+                      f"graph's stream",
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
                          "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
                          "traffic": traffic(f"{kernel} M={M} N={N} K={K} bf16+bias"),
