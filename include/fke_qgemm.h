@@ -137,11 +137,13 @@ int fke_qgemm_f8_on_path(int path, const uint8_t* A, const uint8_t* B, void* C,
                          int out_dtype, int b_layout, void* stream);
 
 /*
- * Workspace of the B [K,N] decode (M <= 16, INT8 and FP8; no reference
- * counterpart: the reference kernels sum all of K in one thread,
- * src/quantized_gemm.cu:29-37, :106-116).  The decode splits K over up to 8
- * workgroups per 512-column block and adds the splits' partial sums in a
- * second kernel, in split order (exact for INT8, deterministic for FP8).  The
+ * Workspace of the B [K,N] decode (M <= 16, and 17..32 where its split fills
+ * the CUs; INT8 and FP8; no reference counterpart: the reference kernels sum
+ * all of K in one thread, src/quantized_gemm.cu:29-37, :106-116).  The decode
+ * splits K over workgroups of 128 to 1024 columns (up to 8 splits; M = 1 up to
+ * 64) and adds the splits' partial sums in a second kernel, in split order
+ * (exact for INT8, deterministic for FP8).  Past 16 rows the decode needs its
+ * split: a workspace without room for it runs the MFMA GEMM instead.  The
  * MFMA GEMM's K split (fke_select_mfma_split) uses the same workspace.  The
  * partial sums need fke_qgemm_workspace_size(M, N, K, b_layout) bytes of
  * device memory (0 for shapes that neither the decode nor the MFMA GEMM
