@@ -1145,7 +1145,7 @@ def test_fp8_streamed_isolated_nan_codes(oracle, dev, M):
 EXTREME_CASES = (
     [(1, 4096, 8192, "nk", "gemv"), (2, 4096, 8192, "nk", "gemv"), (16, 4096, 8192, "nk", "gemv"),
      (16, 4096, 8192, "nk", "gemv_dot"), (40, 4096, 8192, "nk", "gemv"), (100, 4096, 8192, "nk", "gemv"),
-     (1, 4096, 8192, "kn", "gemv"), (16, 4096, 8192, "kn", "gemv"),
+     (1, 4096, 8192, "kn", "gemv"), (16, 4096, 8192, "kn", "gemv"), (24, 4096, 8192, "kn", "gemv"),
      (37, 50, 8192, "nk", "generic"), (37, 48, 8192, "kn", "generic")]
     + [(300, 528, 8192, lay, "mfma_" + t) for lay in ("nk", "kn")
        for t in ("256x256", "128x128", "128x128_ring4", "128x64_ring4", "64x64_ring4")]
@@ -1172,7 +1172,7 @@ def test_extreme_int8_operands(oracle, dev, M, N, K, layout, path):
 
 
 @pytest.mark.parametrize("M,N,K,layout,path",
-                         [c for c in EXTREME_CASES if c[4] != "gemv_dot" and not (c[4] == "gemv" and c[0] > 16 and c[3] == "kn")])
+                         [c for c in EXTREME_CASES if c[4] != "gemv_dot" and not (c[4] == "gemv" and c[0] > 32 and c[3] == "kn")])
 def test_extreme_fp8_codes_exact(oracle, dev, M, N, K, layout, path):
     say("extreme fp8", M, N, K, layout, path)
     r = np.random.default_rng(12000 + M + N)
