@@ -722,12 +722,12 @@ def tile_sweep(torch, L, _lib, dev, gen, timed, args):
 
 def batch_configs(torch, L, _lib, dev, gen, args):
     """Batched decode on the decode weights (N = 14336, K = 4096): 32, 64, 128 and 256 rows with B [N,K],
-    64 and 128 rows with B [K,N] (the reference's layout), and 64 and 128 rows on the LDS-streamed kernel
-    pinned. The dispatcher gives 32 rows to the streamed kernel and the larger batches to the MFMA GEMM's
-    ring tiles (one tile per CU); each line names its kernel."""
+    32, 64 and 128 rows with B [K,N] (the reference's layout), and 64 and 128 rows on the LDS-streamed kernel
+    pinned. The dispatcher gives 32 rows to the streamed kernel ([K,N]: the split decode) and the larger
+    batches to the MFMA GEMM's ring tiles (one tile per CU); each line names its kernel."""
     res = {f"gemv_M{m}": gemv_bench(torch, L, _lib, dev, gen, m, args.gemv_buffers, args.gemv_launches)
            for m in (32, 64, 128, 256)}
-    for m in (64, 128):
+    for m in (32, 64, 128):
         res[f"gemv_M{m}_b_kn"] = gemv_bench(torch, L, _lib, dev, gen, m, args.gemv_buffers, args.gemv_launches,
                                             layout="kn")
     for m in (64, 128):  # the streamed decode kernel pinned, for the choice between it and the ring tiles
