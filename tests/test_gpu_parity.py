@@ -621,6 +621,24 @@ def test_fp8_dropin_launcher_decode(oracle, dev, M):
     assert_fp8_close(C.cpu().numpy(), ref, "f32", f"drop-in M={M}")
 
 
+def test_fp8_dropin_launcher_batch_on_the_split_decode(oracle, dev):
+    """The drop-in fke_launch_fp8_gemm_scaled (B [K,N]) with a 24-row batch at
+    the decode weights' shape, which the dispatcher gives to the [K,N] split
+    decode (two activation blocks per item), against the reference's
+    sequential sum (the threaded restatement), 0x7F / 0xFF codes included."""
+    M, N, K = 24, 14336, 4096
+    say("fp8 drop-in batch", M, N, K)
+    L = _lib.lib()
+    assert L.fke_select_path_f8(4096, 4096, 4096, M, N, K, _lib.OUT_F32, _lib.B_KN) == _lib.PATH_GEMV
+    A, B, sa, sb = f8_inputs(oracle, M, N, K, 7700, "kn", with_nan_codes=True)
+    ref = oracle.f8_gemm(A, B, sa, sb, b_layout=oracle.B_KN, nthreads=NTH)  # the sequential sum, threaded
+    C = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    _lib.check(L.fke_launch_fp8_gemm_scaled(dev_t(A).data_ptr(), dev_t(B).data_ptr(), C.data_ptr(), sa, sb, M, N, K,
+                                            None), "fke_launch_fp8_gemm_scaled")
+    torch.cuda.synchronize()
+    assert_fp8_close(C.cpu().numpy(), ref, "f32", f"drop-in batch M={M}")
+
+
 @pytest.mark.parametrize("M", list(range(1, 17)))
 def test_gemv_dot_family_bit_exact(oracle, dev, M):
     """The VALU dot-product decode kernels (row kernel for M <= 4, split-K sdot
