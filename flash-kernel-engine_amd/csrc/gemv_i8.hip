@@ -896,13 +896,8 @@ hipError_t launch_mfma_skinny(const GemmArgs& p, hipStream_t stream) {
 
 bool pieces_even(int K, int piece) { return ((K + piece - 1) / piece) % 4 == 0; }
 
-int cu_count() {
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
-        cus = 256;
-    return cus;
-}
+// The device's CU count, cached per device (device_cus).
+int cu_count() { return device_cus(); }
 
 // Workgroups of gemv_lds_kernel: one per CU, fewer when the rows run out
 // (at least 16 rows each), more when a share would exceed LK_RMAX rows.
