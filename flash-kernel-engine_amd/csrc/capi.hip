@@ -156,12 +156,16 @@ bool g_noalloc_recorded[kMaxDevices];
 int run_mfma(int path, const GemmArgs& p, int elem, hipStream_t s, const WsChoice& wc = WsChoice{});
 
 // The [K,N] decode, split over the workspace `wc` gives.  Past 16 rows it
-// needs its split (the one-kernel decode takes 16 rows); a workspace without
-// room for one gets the MFMA GEMM.
+// needs its split (the one-kernel decode takes 16 rows), and with operands
+// only 4-byte aligned (N or K not a multiple of 16 / 64) a workspace of one
+// split at least; without it the MFMA GEMM runs, or the generic kernel.
 hipError_t run_kn(const GemmArgs& p, int elem, hipStream_t s, const WsChoice& wc) {
     const Workspace ws = split_workspace(s, fke::gemv_kn_workspace_bytes(p), wc);
     const fke::KnSplit sp = fke::gemv_kn_plan(p, ws.ptr, ws.bytes);
-    if (sp.S < 2 && p.M > 16) return static_cast<hipError_t>(run_mfma(FKE_PATH_MFMA, p, elem, s, wc));
+    if (!fke::gemv_kn_plan_runs(p, sp)) {
+        if (fke::mfma_supports(p, elem)) return static_cast<hipError_t>(run_mfma(FKE_PATH_MFMA, p, elem, s, wc));
+        return fke::launch_generic(p, elem, s);
+    }
     return fke::launch_gemv_kn(p, elem, sp, s);
 }
 

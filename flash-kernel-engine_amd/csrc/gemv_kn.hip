@@ -427,7 +427,13 @@ __device__ __forceinline__ void kr_transpose4(uint32_t r0, uint32_t r1, uint32_t
     c[3] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
 }
 
-template <int EL>
+// DW: 4-byte loads (N % 4 == 0, K % 4 == 0, 4-byte-aligned operands: the
+// shapes the 16-byte loads cannot take), four per lane and row, each word of
+// 4 columns all in N or all out.  Load e of a row covers bytes 256e ..
+// 256e + 255 of the block's segment (lane l's word at 256e + 4l), so each
+// instruction reads whole cache lines; lane l then holds columns 256e + 4l +
+// j (j < 4) where the 16-byte form holds 16l + 4e + j.
+template <int EL, bool DW>
 __global__ __launch_bounds__(KR_WAVES * 64) void gemv_kn_row_kernel(GemmArgs p, KnSplit sp) {
     constexpr bool F8 = EL == ELEM_F8;
     constexpr int BP = KS_ROWS / (KR_WAVES * KR_ROWS);  // batches per wave per 128-row piece
@@ -443,8 +449,17 @@ __global__ __launch_bounds__(KR_WAVES * 64) void gemv_kn_row_kernel(GemmArgs p, 
     const int P = (K + KS_ROWS - 1) / KS_ROWS;
     const int i0 = split * sp.PS, i1 = min(P, i0 + sp.PS);  // this split's pieces
     const int nb = (i1 - i0) * BP;                          // batches of each wave
-    // N % 16 == 0: a lane's 16 columns are all in or all out
-    const uint32_t lane_off = c0 + 16 * lane < N ? static_cast<uint32_t>(c0 + 16 * lane) : 0x80000000u;
+    // 16-byte loads (N % 16 == 0): a lane's 16 columns are all in or all out;
+    // DW: each of its four words is
+    constexpr int LW = DW ? 4 : 1;
+    // the block's column of word e of lane l (DW), or of its 16 bytes
+    auto colw = [&](int e) __attribute__((always_inline)) { return DW ? 256 * e + 4 * lane : 16 * lane + 4 * e; };
+    uint32_t lane_off[LW];
+#pragma unroll
+    for (int e = 0; e < LW; ++e) {
+        const int col = c0 + colw(e);
+        lane_off[e] = col < N ? static_cast<uint32_t>(col) : 0x80000000u;
+    }
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.B, K * N);
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, K);
 
@@ -453,8 +468,8 @@ __global__ __launch_bounds__(KR_WAVES * 64) void gemv_kn_row_kernel(GemmArgs p, 
     // sub-step of the workgroup reads consecutive rows.  The activation bytes
     // of those rows come first (one load, the same address in every lane, so
     // that it counts with the batch), then those rows of the lane's columns.
-    // Batches past the split and columns past N read as zero; K % 64 == 0, so
-    // a batch is all in K or all out.
+    // Batches past the split and columns past N read as zero; K % 4 == 0 (K %
+    // 64 == 0 with 16-byte loads), so a batch of 4 rows is all in K or all out.
     auto load = [&](int j, v4i (&b)[KR_ROWS], int (&a)[AW]) __attribute__((always_inline)) {
         const int k0 = (i0 + j / BP) * KS_ROWS + KR_ROWS * ((j % BP) * KR_WAVES + wave);
         const bool on = j < nb && k0 < K;
@@ -474,10 +489,21 @@ __global__ __launch_bounds__(KR_WAVES * 64) void gemv_kn_row_kernel(GemmArgs p, 
         } else {
             a[0] = __builtin_bit_cast(int, __builtin_amdgcn_raw_buffer_load_b32(ra, static_cast<int>(off | kk), 0, 0));
         }
-        const uint32_t base = off | (lane_off + static_cast<uint32_t>(kk * N));
+        if constexpr (DW) {
 #pragma unroll
-        for (int r = 0; r < KR_ROWS; ++r)
-            b[r] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rb, static_cast<int>(base), r * N, 2));
+            for (int r = 0; r < KR_ROWS; ++r)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    b[r][e] = __builtin_bit_cast(int, __builtin_amdgcn_raw_buffer_load_b32(
+                                                          rb, static_cast<int>(off | (lane_off[e] + static_cast<uint32_t>(kk * N))),
+                                                          r * N, 2));
+        } else {
+            const uint32_t base = off | (lane_off[0] + static_cast<uint32_t>(kk * N));
+#pragma unroll
+            for (int r = 0; r < KR_ROWS; ++r)
+                b[r] = __builtin_bit_cast(v4i,
+                                          __builtin_amdgcn_raw_buffer_load_b128(rb, static_cast<int>(base), r * N, 2));
+        }
     };
 
     AccE acc[16];
@@ -566,11 +592,11 @@ __global__ __launch_bounds__(KR_WAVES * 64) void gemv_kn_row_kernel(GemmArgs p, 
     }
 
     // The waves' sums in the order w = 0, 1, ...: lane l of wave w holds
-    // columns 16l..16l+15 of the workgroup's block; thread t finishes columns
-    // CT t .. CT t + CT - 1.
+    // columns colw(e) + j of the workgroup's block in acc[4e + j]; thread t
+    // finishes columns CT t .. CT t + CT - 1.
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        AccE* d = &red[wave][16 * lane + 4 * e];
+        AccE* d = &red[wave][colw(e)];
         d[0] = acc[4 * e];
         d[1] = acc[4 * e + 1];
         d[2] = acc[4 * e + 2];
@@ -622,8 +648,9 @@ hipError_t launch_kn_split_out(const GemmArgs& p, const KnSplit& sp, hipStream_t
     hipError_t e;
     if (sp.rowk) {
         const int nblk = (p.N + KR_W - 1) / KR_W;
-        e = hipLaunchKernel(reinterpret_cast<const void*>(&gemv_kn_row_kernel<EL>), dim3(nblk * sp.S),
-                            dim3(KR_WAVES * 64), args, 0, stream);
+        const void* row = sp.dw ? reinterpret_cast<const void*>(&gemv_kn_row_kernel<EL, true>)
+                                : reinterpret_cast<const void*>(&gemv_kn_row_kernel<EL, false>);
+        e = hipLaunchKernel(row, dim3(nblk * sp.S), dim3(KR_WAVES * 64), args, 0, stream);
     } else {
         const int nblk = (p.N + sp.kw * KS_W - 1) / (sp.kw * KS_W);
         const void* split = ks_kernel<EL>(p.M, sp.kw);
@@ -964,16 +991,26 @@ hipError_t launch_kn_full(const GemmArgs& p, hipStream_t stream) {
 
 }  // namespace
 
-// The shapes the [K,N] kernels take (gemv_kn_supports adds the plan's rule past 16 rows).
-static bool kn_shape_ok(const GemmArgs& p, int elem) {
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p.A), b = reinterpret_cast<uintptr_t>(p.B);
-    if (p.b_layout != FKE_B_KN || p.swiglu || p.M < 1 || p.M > KN_MAX_M || p.N < 1 || p.K < 64) return false;
+// Layout, operand types and 32-bit offsets common to every [K,N] kernel.
+static bool kn_common_ok(const GemmArgs& p, int elem) {
+    if (p.b_layout != FKE_B_KN || p.swiglu || p.M < 1 || p.M > KN_MAX_M || p.N < 1 || p.K < 4) return false;
     if (elem != ELEM_I8 && elem != ELEM_F8) return false;
     if (elem == ELEM_F8 && p.out_dtype == FKE_OUT_I32) return false;
-    // 16-byte copies: row starts (B: k*N + n, A: m*K + k) must stay 16-byte aligned
-    if (p.N % 16 != 0 || p.K % 64 != 0 || ((a | b) & 15) != 0) return false;
-    // 32-bit buffer offsets and ranges over all of B and A
     return static_cast<int64_t>(p.K) * p.N <= INT32_MAX && static_cast<int64_t>(p.M) * p.K <= INT32_MAX;
+}
+// 16-byte copies: row starts (B: k*N + n, A: m*K + k) stay 16-byte aligned (every kernel).
+static bool kn_aligned16(const GemmArgs& p) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p.A), b = reinterpret_cast<uintptr_t>(p.B);
+    return p.K >= 64 && p.N % 16 == 0 && p.K % 64 == 0 && ((a | b) & 15) == 0;
+}
+// 4-byte loads: the row kernel's dword form (M = 1), which a workspace of one
+// split's partial sums or more lets run.
+static bool kn_aligned4(const GemmArgs& p) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p.A), b = reinterpret_cast<uintptr_t>(p.B);
+    return p.M == 1 && p.N % 4 == 0 && p.K % 4 == 0 && ((a | b) & 3) == 0;
+}
+static bool kn_shape_ok(const GemmArgs& p, int elem) {
+    return kn_common_ok(p, elem) && (kn_aligned16(p) || kn_aligned4(p));
 }
 
 // Partial sums of the split kernel: [ceil(N/128)][S][M][128], 4 bytes each.
@@ -1035,12 +1072,15 @@ static void kn_splits(const GemmArgs& p, size_t ws_bytes, KnSplit* sp) {
     if (ws_bytes > FKE_SPLIT_SLOT_BYTES) ws_bytes = FKE_SPLIT_SLOT_BYTES;
     const int P = (p.K + KS_ROWS - 1) / KS_ROWS;
     sp->rowk = 0;
+    sp->dw = !kn_aligned16(p);
     if (p.M == 1) {
         int S = kCUs / ((p.N + KR_W - 1) / KR_W);
         if (S > KR_SMAX) S = KR_SMAX;
         if (S > P) S = P;
+        if (S < 1) S = 1;
         while (S > 1 && kn_ws_bytes(1, p.N, S) > ws_bytes) --S;
-        if (S >= 2) {
+        // the dword form has no other kernel: one split will do
+        if (S >= 2 || (sp->dw && kn_ws_bytes(1, p.N, 1) <= ws_bytes)) {
             const int PS = (P + S - 1) / S;
             sp->S = (P + PS - 1) / PS;
             sp->PS = PS;
@@ -1048,6 +1088,12 @@ static void kn_splits(const GemmArgs& p, size_t ws_bytes, KnSplit* sp) {
             sp->kw = 0;
             return;
         }
+    }
+    if (sp->dw) {  // no kernel without its workspace: gemv_kn_plan_runs says no
+        sp->S = 1;
+        sp->PS = P;
+        sp->kw = 0;
+        return;
     }
     const int fill = kCUs - kCUs / 8;
     int kw = 2;
@@ -1073,8 +1119,12 @@ static void kn_splits(const GemmArgs& p, size_t ws_bytes, KnSplit* sp) {
 // one- or two-wave workgroups; other batches go to the MFMA GEMM's tiles.
 bool gemv_kn_supports(const GemmArgs& p, int elem) {
     if (!kn_shape_ok(p, elem)) return false;
-    if (p.M <= 16) return true;
     KnSplit sp;
+    if (!kn_aligned16(p)) {  // the row kernel's dword form
+        kn_splits(p, SIZE_MAX, &sp);
+        return sp.rowk != 0;
+    }
+    if (p.M <= 16) return true;
     kn_splits(p, SIZE_MAX, &sp);
     if (sp.S < 2 || sp.rowk || sp.kw == 4) return false;
     const int kCUs = device_cus();
@@ -1085,7 +1135,11 @@ bool gemv_kn_supports(const GemmArgs& p, int elem) {
 size_t gemv_kn_workspace_bytes(const GemmArgs& p) {
     KnSplit sp;
     kn_splits(p, SIZE_MAX, &sp);
-    return sp.S > 1 ? kn_ws_bytes(p.M, p.N, sp.S) : 0;
+    return sp.S > 1 || sp.rowk ? kn_ws_bytes(p.M, p.N, sp.S) : 0;
+}
+
+bool gemv_kn_plan_runs(const GemmArgs& p, const KnSplit& sp) {
+    return sp.rowk || (!sp.dw && (sp.S > 1 || p.M <= 16));
 }
 
 // No split (S = 1) without a workspace, or with one not 16-byte aligned (the
@@ -1094,13 +1148,13 @@ KnSplit gemv_kn_plan(const GemmArgs& p, void* ws, size_t ws_bytes) {
     KnSplit sp;
     const bool usable = ws && (reinterpret_cast<uintptr_t>(ws) & 15) == 0;
     kn_splits(p, usable ? ws_bytes : 0, &sp);
-    sp.part = sp.S > 1 ? ws : nullptr;
+    sp.part = sp.S > 1 || sp.rowk ? ws : nullptr;
     return sp;
 }
 
 hipError_t launch_gemv_kn(const GemmArgs& p, int elem, const KnSplit& sp, hipStream_t stream) {
-    if (sp.S < 2 && p.M > 16) return hipErrorInvalidValue;  // the full kernel takes 16 rows
-    if (sp.S > 1) {
+    if (!gemv_kn_plan_runs(p, sp)) return hipErrorInvalidValue;  // the full kernel: 16 rows, 16-byte loads
+    if (sp.S > 1 || sp.rowk) {
         if (!sp.part) return hipErrorInvalidValue;
         return elem == ELEM_F8 ? launch_kn_split<ELEM_F8>(p, sp, stream) : launch_kn_split<ELEM_I8>(p, sp, stream);
     }

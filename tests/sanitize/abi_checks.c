@@ -96,7 +96,7 @@ int main(void) {
                     CHECK(S == 1 || tp >= FKE_PATH_MFMA_128x128_RING4);
                     const size_t split = S > 1 ? (size_t)S * (size_t)M * (size_t)N * 4 : 0;
                     CHECK(ws == 0 || ws == split ||
-                          (lay == FKE_B_KN && M <= 32 && ws % row == 0 && ws / row >= 2 &&
+                          (lay == FKE_B_KN && M <= 32 && ws % row == 0 && ws / row >= (M == 1 ? 1 : 2) &&
                            ws / row <= (M == 1 ? 64 : 8)));
                     n_split += S > 1;
                     ++n_ws;

@@ -98,8 +98,11 @@ def test_workspace_entry_points_reject_bad_arguments():
     # 17..32 rows on the split decode: one-wave workgroups x 2 splits at N = 14336
     (17, 14336, 4096, 1, 2 * 17 * 14336 * 4), (32, 14336, 4096, 1, 2 * 32 * 14336 * 4),
     # unsplit: K of one piece, the decode not taken (M > 16, B [N,K], N % 16 != 0, K % 64 != 0)
-    (1, 14336, 128, 1, 0), (33, 14336, 4096, 1, 0), (1, 14336, 4096, 0, 0), (1, 1000, 4096, 1, 0),
-    (1, 14336, 4000, 1, 0), (0, 14336, 4096, 1, 0), (1, 14336, 4096, 2, 0),
+    (1, 14336, 128, 1, 0), (33, 14336, 4096, 1, 0), (1, 14336, 4096, 0, 0), (1, 1002, 4096, 1, 0),
+    (1, 14336, 4002, 1, 0), (0, 14336, 4096, 1, 0), (1, 14336, 4096, 2, 0),
+    # M = 1 with N or K only a multiple of 4: the row kernel's 4-byte form (8 blocks of 128 x 32 splits;
+    # 112 blocks x 16 splits)
+    (1, 1000, 4096, 1, 32 * 1 * 1024 * 4), (1, 14336, 4000, 1, 16 * 1 * 14336 * 4),
 ])
 def test_workspace_size(M, N, K, layout, expect):
     assert _lib.lib().fke_qgemm_workspace_size(M, N, K, layout) == expect
@@ -301,7 +304,9 @@ def test_path_unavailable_for_shape_is_rejected():
     (1, 14336, 4096, 1, _lib.PATH_GEMV),     # B [K,N] decode: the transposing streamed kernel
     (16, 14336, 4096, 1, _lib.PATH_GEMV),
     (4, 4096, 64, 1, _lib.PATH_GEMV),
-    (4, 4104, 4096, 1, _lib.PATH_GENERIC),   # B [K,N] with N % 16 != 0: neither fast kernel
+    (4, 4104, 4096, 1, _lib.PATH_GENERIC),   # B [K,N] with N % 16 != 0: neither fast kernel past one row
+    (1, 4104, 4096, 1, _lib.PATH_GEMV),      # one row: the row kernel's 4-byte form
+    (1, 1002, 4096, 1, _lib.PATH_GENERIC),   # N % 4 != 0
     (17, 4096, 4096, 1, _lib.PATH_GEMV),
     (64, 64, 100, 0, _lib.PATH_GENERIC),
     (64, 64, 4, 0, _lib.PATH_GENERIC),

@@ -400,6 +400,53 @@ def test_gemv_kn_split_full_and_fewer_splits(oracle, dev, M):
     assert_same(host(got), acc, f"kn ws+4 M={M}")
 
 
+def dev_at(x, shift):
+    """A device copy of array x placed `shift` bytes into a uint8 buffer (an
+    operand only `shift`-aligned); returns (buffer, pointer)."""
+    raw = np.ascontiguousarray(x).view(np.uint8).reshape(-1)
+    buf = torch.zeros(raw.size + shift, dtype=torch.uint8, device="cuda")
+    buf[shift:].copy_(torch.from_numpy(raw))
+    return buf, buf.data_ptr() + shift
+
+
+# M = 1 with B [K,N] whose N or K is only a multiple of 4, or whose operands
+# are only 4-byte aligned: the row kernel's 4-byte form (one split when the
+# plan gives one, a ragged last 1024-column block, K not a multiple of 128).
+KN_DW_CASES = [(1000, 4096, 0), (14340, 4096, 0), (4100, 4100, 0), (2052, 100, 0), (14336, 4000, 0),
+               (14336, 4096, 4), (1024, 4, 4)]
+
+
+@pytest.mark.parametrize("N,K,shift", KN_DW_CASES)
+def test_gemv_kn_row_kernel_dword_form(oracle, dev, N, K, shift):
+    """INT8 bit-exact on every output type, and FP8 (0x7F / 0xFF codes
+    included) within the bounds of the sequential sum, through fke_qgemm_i8 /
+    fke_qgemm_f8 with A and B `shift` bytes past 16-byte alignment."""
+    M = 1
+    say("kn row kernel, 4-byte loads", M, N, K, shift)
+    L = _lib.lib()
+    assert L.fke_select_path_i8(4096 + shift, 4096 + shift, 4096, M, N, K, _lib.OUT_BF16, _lib.B_KN) == _lib.PATH_GEMV
+    A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 9700 + N + K, layout="kn", act="normal")
+    acc = oracle.w8a8_acc(A, B, oracle.B_KN, nthreads=NTH)
+    (ba, pa), (bb, pb) = dev_at(A, shift), dev_at(B, shift)
+    dsa, dsb, dbias = dev_t(sa), dev_t(sb), dev_t(bias)
+    for out in ("i32", "f32", "bf16"):
+        C = torch.empty((M, N), dtype=OUT_T[out], device=dev)
+        _lib.check(L.fke_qgemm_i8(pa, pb, C.data_ptr(), M, N, K, dsa.data_ptr(), dsb.data_ptr(), 1.0, 1.0,
+                                  dbias.data_ptr(), {"f32": _lib.OUT_F32, "bf16": _lib.OUT_BF16, "i32": _lib.OUT_I32}[out],
+                                  _lib.B_KN, torch.cuda.current_stream().cuda_stream), "fke_qgemm_i8")
+        torch.cuda.synchronize()
+        want = acc if out == "i32" else oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, out)
+        assert_same(host(C), want, f"kn dword {out} N={N} K={K} shift={shift}")
+    A8, B8, fa, fb = f8_inputs(oracle, M, N, K, 9800 + N + K, "kn", with_nan_codes=True)
+    ref = oracle.f8_gemm(A8, B8, fa, fb, b_layout=oracle.B_KN, nthreads=NTH)
+    (ba, pa), (bb, pb) = dev_at(A8, shift), dev_at(B8, shift)
+    C = torch.empty((M, N), dtype=torch.float32, device=dev)
+    _lib.check(L.fke_qgemm_f8(pa, pb, C.data_ptr(), M, N, K, fa, fb, None, _lib.OUT_F32, _lib.B_KN,
+                              torch.cuda.current_stream().cuda_stream), "fke_qgemm_f8")
+    torch.cuda.synchronize()
+    assert_fp8_close(host(C), ref, "f32", f"kn dword fp8 N={N} K={K} shift={shift}")
+
+
 def test_gemv_kn_graph_replays(oracle, dev):
     """The split [K,N] decode captured into a HIP graph (on the stream's slot
     of the split pool, and on a caller's workspace): three replays with other
