@@ -259,9 +259,14 @@ GemmArgs make_swiglu_args(const void* A, const void* W, void* H, int M, int I, i
     return p;
 }
 
+// Decode with B [K,N]: the transposing kernels, but the MFMA GEMM where the
+// row kernel's 4-byte form would stream the weights more than once.
+bool kn_decode_pays(const GemmArgs& p, int elem) {
+    return fke::gemv_kn_supports(p, elem) && !(fke::gemv_kn_yields_to_mfma(p) && fke::mfma_supports(p, elem));
+}
+
 int pick_i8(const GemmArgs& p) {
-    // decode with B [K,N]: the transposing LDS-streamed kernel
-    if (fke::gemv_kn_supports(p, fke::ELEM_I8)) return FKE_PATH_GEMV;
+    if (kn_decode_pays(p, fke::ELEM_I8)) return FKE_PATH_GEMV;
     // decode and batches up to FKE_GEMV_MAX_M rows: the decode family where
     // its cost model beats the MFMA GEMM's, or where that GEMM cannot run
     if (fke::gemv_i8_supports(p) && (fke::gemv_i8_batch_pays(p) || !fke::mfma_supports(p, fke::ELEM_I8)))
@@ -271,7 +276,7 @@ int pick_i8(const GemmArgs& p) {
 }
 
 int pick_f8(const GemmArgs& p) {
-    if (fke::gemv_kn_supports(p, fke::ELEM_F8)) return FKE_PATH_GEMV;  // decode with B [K,N]
+    if (kn_decode_pays(p, fke::ELEM_F8)) return FKE_PATH_GEMV;
     // decode and small batches (B [N,K]): the streamed kernel, by the same cost model as INT8
     if (fke::gemv_f8_supports(p) && (fke::gemv_i8_batch_pays(p) || !fke::mfma_supports(p, fke::ELEM_F8)))
         return FKE_PATH_GEMV;

@@ -96,11 +96,14 @@ struct KnSplit {
     int S;       // K splits (1: no workspace)
     int PS;      // 128-row pieces per split
     void* part;  // [ceil(N/128)][S][M][128] partial sums (int32 / fp32)
-    int rowk;    // 1: the M = 1 row kernel writes them (1024-column workgroups), 0: the split kernel
+    int rowk;    // 1: the row kernel writes them (1024-column workgroups), 0: the split kernel
     int kw;      // the split kernel's waves per workgroup (1, 2 or 4 blocks of 128 columns)
     int dw;      // 1: 4-byte loads (the row kernel's form for operands the 16-byte loads cannot take)
 };
 bool gemv_kn_supports(const GemmArgs& p, int elem);
+// Whether the MFMA GEMM should take the shape where it can: past 4 rows with
+// 4-byte operands (the row kernel streams the weights once per 4 rows).
+bool gemv_kn_yields_to_mfma(const GemmArgs& p);
 size_t gemv_kn_workspace_bytes(const GemmArgs& p);  // 0: runs unsplit
 KnSplit gemv_kn_plan(const GemmArgs& p, void* ws, size_t ws_bytes);
 // Whether the plan has a kernel (past 16 rows, or with 4-byte operands, the decode needs its workspace).

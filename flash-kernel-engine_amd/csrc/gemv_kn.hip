@@ -32,10 +32,12 @@
 //    ~8 us more at that shape: its store / count / load round trips queue
 //    behind the other workgroups' streams, where the second kernel's run
 //    after them (13.2 against 19 us for M = 1).
-//  * Row kernel (gemv_kn_row_kernel + kn_reduce_kernel), M = 1: workgroup =
-//    1024 consecutive columns x one of S <= 64 K ranges, loaded straight into
-//    registers and summed on the VALU (no MFMA, no LDS staging); its partial
-//    sums take the split kernel's layout and second kernel.
+//  * Row kernel (gemv_kn_row_kernel + kn_reduce_kernel), M = 1, and up to 32
+//    rows with operands the 16-byte loads cannot take: workgroup = 1024
+//    consecutive columns x one of S <= 64 K ranges x 1, 2 or 4 activation
+//    rows, loaded straight into registers and summed on the VALU (no MFMA, no
+//    LDS staging); its partial sums take the split kernel's layout and second
+//    kernel.
 //  * Full kernel (gemv_kn_full_kernel), when there is no workspace or K is
 //    too short to split: one workgroup per 64-column block over all of K,
 //    blocks 2j and 2j+1 (the two halves of each 128-byte line) on one XCD.
@@ -378,8 +380,9 @@ __global__ __launch_bounds__(T) void kn_reduce_kernel(GemmArgs p, KnSplit sp) {
 }
 
 // ===========================================================================
-// Row kernel (M = 1): 1024 columns per workgroup, loaded from HBM straight
-// into registers; no LDS staging and no MFMA.
+// Row kernel (M = 1; and 2..32 rows where the 16-byte loads cannot run):
+// 1024 columns per workgroup, loaded from HBM straight into registers; no LDS
+// staging and no MFMA.
 // ===========================================================================
 // One activation row leaves an MFMA nothing to share between its 16 rows, and
 // the transposing LDS reads serve only to turn k rows into columns.  Here lane
@@ -390,9 +393,11 @@ __global__ __launch_bounds__(T) void kn_reduce_kernel(GemmArgs p, KnSplit sp) {
 // 4 k bytes (a byte transpose in eight v_perm_b32) and sums them with
 // v_dot4_i32_i8 against the activation word of those 4 rows (INT8), or
 // converts the codes with v_cvt_pk_f32_fp8 and adds the exact products with
-// fma in k order (FP8).  The waves' sums meet in LDS in the order w = 0, 1,
-// ... and go to the workspace in the split kernel's layout ([block of 128
-// columns][split][128]); kn_reduce_kernel finishes them.
+// fma in k order (FP8), for each of the workgroup's activation rows.  The
+// waves' sums meet in LDS in the order w = 0, 1, ... and go to the workspace
+// in the split kernel's layout ([block of 128 columns][split][M][128]);
+// kn_reduce_kernel finishes them.  More than four activation rows take
+// workgroups of four rows each (grid y), each streaming the same weights.
 // Why: 1024-column blocks take up to 64 K splits, where the split kernel's
 // 512-column blocks take 8, so shapes with few column blocks still fill the
 // CUs (N = 4096, K = 14336: 224 workgroups and 13.5 against 23.2 us); at
@@ -407,10 +412,8 @@ __global__ __launch_bounds__(T) void kn_reduce_kernel(GemmArgs p, KnSplit sp) {
 // and short batches keep that tail short.
 constexpr int KR_W = 1024;   // columns per workgroup
 constexpr int KR_SMAX = 64;  // K splits at most
-constexpr int KR_WAVES = 16; // waves per workgroup
 constexpr int KR_ROWS = 4;   // rows per wave per batch
 constexpr int KR_D = 2;      // batches in flight per wave
-static_assert(KS_ROWS % (KR_WAVES * KR_ROWS) == 0, "a 128-row piece is whole batches of every wave");
 static_assert(KR_ROWS == 4 || KR_ROWS == 8 || KR_ROWS == 16, "4, 8 or 16 activation bytes per batch");
 static_assert(KR_D >= 2 && KR_D <= 4, "two to four batches in flight");
 static_assert(KR_W % KS_W == 0, "workgroups cover whole 128-column blocks of the partial-sum layout");
@@ -427,25 +430,35 @@ __device__ __forceinline__ void kr_transpose4(uint32_t r0, uint32_t r1, uint32_t
     c[3] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
 }
 
+// MR activation rows per workgroup (1, 2 or 4): rows MR * blockIdx.y .. + MR -
+// 1 of A, those past M read as zero and not stored.  Sixteen waves for one
+// row; eight for more, whose 16 MR accumulators per lane need the registers
+// of two waves per SIMD.
+constexpr int kr_waves(int mr) { return mr == 1 ? 16 : 8; }
+// The activation rows per workgroup for M rows.
+constexpr int kr_rows(int M) { return M == 1 ? 1 : M == 2 ? 2 : 4; }
+
 // DW: 4-byte loads (N % 4 == 0, K % 4 == 0, 4-byte-aligned operands: the
 // shapes the 16-byte loads cannot take), four per lane and row, each word of
 // 4 columns all in N or all out.  Load e of a row covers bytes 256e ..
 // 256e + 255 of the block's segment (lane l's word at 256e + 4l), so each
 // instruction reads whole cache lines; lane l then holds columns 256e + 4l +
 // j (j < 4) where the 16-byte form holds 16l + 4e + j.
-template <int EL, bool DW>
-__global__ __launch_bounds__(KR_WAVES * 64) void gemv_kn_row_kernel(GemmArgs p, KnSplit sp) {
+template <int EL, bool DW, int MR>
+__global__ __launch_bounds__(kr_waves(MR) * 64) void gemv_kn_row_kernel(GemmArgs p, KnSplit sp) {
     constexpr bool F8 = EL == ELEM_F8;
-    constexpr int BP = KS_ROWS / (KR_WAVES * KR_ROWS);  // batches per wave per 128-row piece
-    constexpr int AW = KR_ROWS / 4;                     // activation words per batch
+    constexpr int WV = kr_waves(MR);
+    constexpr int BP = KS_ROWS / (WV * KR_ROWS);  // batches per wave per 128-row piece
+    constexpr int AW = KR_ROWS / 4;               // activation words per row and batch
+    static_assert(KS_ROWS % (WV * KR_ROWS) == 0, "a 128-row piece is whole batches of every wave");
     using AccE = typename std::conditional<F8, float, int32_t>::type;
-    __shared__ __attribute__((aligned(16))) AccE red[KR_WAVES][KR_W];
+    __shared__ __attribute__((aligned(16))) AccE red[WV][KR_W];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int N = p.N, K = p.K, S = sp.S;
+    const int M = p.M, N = p.N, K = p.K, S = sp.S;
     const int cbg = blockIdx.x / S, split = blockIdx.x % S;
-    const int c0 = cbg * KR_W;
+    const int c0 = cbg * KR_W, m0 = blockIdx.y * MR;
     const int P = (K + KS_ROWS - 1) / KS_ROWS;
     const int i0 = split * sp.PS, i1 = min(P, i0 + sp.PS);  // this split's pieces
     const int nb = (i1 - i0) * BP;                          // batches of each wave
@@ -460,34 +473,44 @@ __global__ __launch_bounds__(KR_WAVES * 64) void gemv_kn_row_kernel(GemmArgs p, 
         const int col = c0 + colw(e);
         lane_off[e] = col < N ? static_cast<uint32_t>(col) : 0x80000000u;
     }
+    // activation rows: m K, rows past M at bit 31
+    uint32_t arow[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) arow[m] = m0 + m < M ? static_cast<uint32_t>((m0 + m) * K) : 0x80000000u;
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.B, K * N);
-    const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, K);
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, M * K);
 
     // Batch j of the wave: sub-step h = j % BP of piece i0 + j / BP, rows
     // k0 .. k0 + KR_ROWS - 1 with k0 = 128 i + KR_ROWS (h * waves + w), so each
     // sub-step of the workgroup reads consecutive rows.  The activation bytes
-    // of those rows come first (one load, the same address in every lane, so
-    // that it counts with the batch), then those rows of the lane's columns.
-    // Batches past the split and columns past N read as zero; K % 4 == 0 (K %
-    // 64 == 0 with 16-byte loads), so a batch of 4 rows is all in K or all out.
-    auto load = [&](int j, v4i (&b)[KR_ROWS], int (&a)[AW]) __attribute__((always_inline)) {
-        const int k0 = (i0 + j / BP) * KS_ROWS + KR_ROWS * ((j % BP) * KR_WAVES + wave);
+    // of those rows come first (one load per activation row, the same address
+    // in every lane, so that it counts with the batch), then those rows of the
+    // lane's columns.  Batches past the split, rows past M and columns past N
+    // read as zero; K % 4 == 0 (K % 64 == 0 with 16-byte loads), so a batch of
+    // 4 rows is all in K or all out.
+    auto load = [&](int j, v4i (&b)[KR_ROWS], int (&a)[MR][AW]) __attribute__((always_inline)) {
+        const int k0 = (i0 + j / BP) * KS_ROWS + KR_ROWS * ((j % BP) * WV + wave);
         const bool on = j < nb && k0 < K;
         // Bit 31 set: outside every range.  Outside batches take row 0, so that
         // no offset (with the row's r * N added) passes 2^32: at most
-        // 2^31 + K * N for an invalid column, 2^31 + 16 * N for a batch outside.
+        // 2^31 + K * N for an invalid column, 2^31 + 16 * N for a batch outside,
+        // 2^31 + M * K for an activation row or batch outside.
         const int kk = on ? k0 : 0;
         const uint32_t off = on ? 0u : 0x80000000u;
-        if constexpr (AW == 4) {
-            const v4i av = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(ra, static_cast<int>(off | kk), 0, 0));
 #pragma unroll
-            for (int q = 0; q < 4; ++q) a[q] = av[q];
-        } else if constexpr (AW == 2) {
-            const v2i av = __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(ra, static_cast<int>(off | kk), 0, 0));
-            a[0] = av[0];
-            a[1] = av[1];
-        } else {
-            a[0] = __builtin_bit_cast(int, __builtin_amdgcn_raw_buffer_load_b32(ra, static_cast<int>(off | kk), 0, 0));
+        for (int m = 0; m < MR; ++m) {
+            const int ao = static_cast<int>(off | (arow[m] + static_cast<uint32_t>(kk)));
+            if constexpr (AW == 4) {
+                const v4i av = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(ra, ao, 0, 0));
+#pragma unroll
+                for (int q = 0; q < 4; ++q) a[m][q] = av[q];
+            } else if constexpr (AW == 2) {
+                const v2i av = __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(ra, ao, 0, 0));
+                a[m][0] = av[0];
+                a[m][1] = av[1];
+            } else {
+                a[m][0] = __builtin_bit_cast(int, __builtin_amdgcn_raw_buffer_load_b32(ra, ao, 0, 0));
+            }
         }
         if constexpr (DW) {
 #pragma unroll
@@ -506,24 +529,29 @@ __global__ __launch_bounds__(KR_WAVES * 64) void gemv_kn_row_kernel(GemmArgs p, 
         }
     };
 
-    AccE acc[16];
+    AccE acc[MR][16];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) acc[j] = AccE(0);
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc[m][j] = AccE(0);
 
-    auto consume = [&](const v4i (&b)[KR_ROWS], const int (&a)[AW], auto san) __attribute__((always_inline)) {
+    auto consume = [&](const v4i (&b)[KR_ROWS], const int (&a)[MR][AW], auto san) __attribute__((always_inline)) {
         if constexpr (F8) {
             constexpr bool SAN = decltype(san)::value;
-            float af[KR_ROWS];
+            float af[MR][KR_ROWS];
 #pragma unroll
-            for (int q = 0; q < AW; ++q) {
-                const uint32_t w = SAN ? e4m3_sanitize(static_cast<uint32_t>(a[q])) : static_cast<uint32_t>(a[q]);
-                const v2f lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), false);
-                const v2f hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), true);
-                af[4 * q] = lo.x;
-                af[4 * q + 1] = lo.y;
-                af[4 * q + 2] = hi.x;
-                af[4 * q + 3] = hi.y;
-            }
+            for (int m = 0; m < MR; ++m)
+#pragma unroll
+                for (int q = 0; q < AW; ++q) {
+                    const uint32_t w =
+                        SAN ? e4m3_sanitize(static_cast<uint32_t>(a[m][q])) : static_cast<uint32_t>(a[m][q]);
+                    const v2f lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), false);
+                    const v2f hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), true);
+                    af[m][4 * q] = lo.x;
+                    af[m][4 * q + 1] = lo.y;
+                    af[m][4 * q + 2] = hi.x;
+                    af[m][4 * q + 3] = hi.y;
+                }
 #pragma unroll
             for (int r = 0; r < KR_ROWS; ++r) {
                 v4i w = b[r];
@@ -534,7 +562,9 @@ __global__ __launch_bounds__(KR_WAVES * 64) void gemv_kn_row_kernel(GemmArgs p, 
                 float bf[16];
                 e4m3_chunk_to_f32(w, bf);
 #pragma unroll
-                for (int j = 0; j < 16; ++j) acc[j] = __builtin_fmaf(af[r], bf[j], acc[j]);
+                for (int m = 0; m < MR; ++m)
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) acc[m][j] = __builtin_fmaf(af[m][r], bf[j], acc[m][j]);
             }
         } else {
 #pragma unroll
@@ -545,8 +575,11 @@ __global__ __launch_bounds__(KR_WAVES * 64) void gemv_kn_row_kernel(GemmArgs p, 
                     kr_transpose4(static_cast<uint32_t>(b[4 * q][e]), static_cast<uint32_t>(b[4 * q + 1][e]),
                                   static_cast<uint32_t>(b[4 * q + 2][e]), static_cast<uint32_t>(b[4 * q + 3][e]), c);
 #pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        acc[4 * e + j] = __builtin_amdgcn_sdot4(static_cast<int>(c[j]), a[q], acc[4 * e + j], false);
+                    for (int m = 0; m < MR; ++m)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            acc[m][4 * e + j] =
+                                __builtin_amdgcn_sdot4(static_cast<int>(c[j]), a[m][q], acc[m][4 * e + j], false);
                 }
         }
     };
@@ -558,7 +591,7 @@ __global__ __launch_bounds__(KR_WAVES * 64) void gemv_kn_row_kernel(GemmArgs p, 
     // previous batch's arithmetic.
     auto stream = [&](auto san) __attribute__((always_inline)) {
         v4i b[KR_D][KR_ROWS];
-        int a[KR_D][AW];
+        int a[KR_D][MR][AW];
 #pragma unroll
         for (int d = 0; d < KR_D - 1; ++d) load(d, b[d], a[d]);
         for (int j = 0; j < nb; j += KR_D) {
@@ -583,35 +616,44 @@ __global__ __launch_bounds__(KR_WAVES * 64) void gemv_kn_row_kernel(GemmArgs p, 
         stream(std::false_type{});
         bool bad = false;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) bad |= __builtin_isnan(acc[j]);
+        for (int m = 0; m < MR; ++m)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) bad |= __builtin_isnan(acc[m][j]);
         if (__builtin_amdgcn_ballot_w64(bad) != 0) {
 #pragma unroll
-            for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
+            for (int m = 0; m < MR; ++m)
+#pragma unroll
+                for (int j = 0; j < 16; ++j) acc[m][j] = 0.0f;
             stream(std::true_type{});
         }
     }
 
-    // The waves' sums in the order w = 0, 1, ...: lane l of wave w holds
-    // columns colw(e) + j of the workgroup's block in acc[4e + j]; thread t
-    // finishes columns CT t .. CT t + CT - 1.
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        AccE* d = &red[wave][colw(e)];
-        d[0] = acc[4 * e];
-        d[1] = acc[4 * e + 1];
-        d[2] = acc[4 * e + 2];
-        d[3] = acc[4 * e + 3];
-    }
-    __syncthreads();
-    constexpr int CT = KR_W / (KR_WAVES * 64);
+    // The waves' sums, one activation row at a time, in the order w = 0, 1,
+    // ...: lane l of wave w holds columns colw(e) + j of the workgroup's block
+    // in acc[m][4e + j]; thread t finishes columns CT t .. CT t + CT - 1.
+    constexpr int CT = KR_W / (WV * 64);
     AccE* const part = static_cast<AccE*>(sp.part);
 #pragma unroll
-    for (int h = 0; h < CT; ++h) {
-        const int col = CT * tid + h, n = c0 + col;
-        AccE s = red[0][col];
+    for (int m = 0; m < MR; ++m) {
+        if (m > 0) __syncthreads();  // every thread has read the previous row's sums
 #pragma unroll
-        for (int w = 1; w < KR_WAVES; ++w) s += red[w][col];
-        if (n < N) part[(static_cast<size_t>(n / KS_W) * S + split) * KS_W + n % KS_W] = s;
+        for (int e = 0; e < 4; ++e) {
+            AccE* d = &red[wave][colw(e)];
+            d[0] = acc[m][4 * e];
+            d[1] = acc[m][4 * e + 1];
+            d[2] = acc[m][4 * e + 2];
+            d[3] = acc[m][4 * e + 3];
+        }
+        __syncthreads();
+        if (m0 + m >= M) continue;  // the same for the whole workgroup
+#pragma unroll
+        for (int h = 0; h < CT; ++h) {
+            const int col = CT * tid + h, n = c0 + col;
+            AccE s = red[0][col];
+#pragma unroll
+            for (int w = 1; w < WV; ++w) s += red[w][col];
+            if (n < N) part[((static_cast<size_t>(n / KS_W) * S + split) * M + m0 + m) * KS_W + n % KS_W] = s;
+        }
     }
 }
 
@@ -640,6 +682,13 @@ const void* ks_kernel(int M, int kw) {
                    : reinterpret_cast<const void*>(&gemv_kn_split_kernel<EL, false, 2, 2>);
 }
 
+template <int EL, bool DW>
+const void* kr_kernel(int mr) {
+    return mr == 1   ? reinterpret_cast<const void*>(&gemv_kn_row_kernel<EL, DW, 1>)
+           : mr == 2 ? reinterpret_cast<const void*>(&gemv_kn_row_kernel<EL, DW, 2>)
+                     : reinterpret_cast<const void*>(&gemv_kn_row_kernel<EL, DW, 4>);
+}
+
 template <int EL, int OUT>
 hipError_t launch_kn_split_out(const GemmArgs& p, const KnSplit& sp, hipStream_t stream) {
     GemmArgs a = p;
@@ -647,10 +696,9 @@ hipError_t launch_kn_split_out(const GemmArgs& p, const KnSplit& sp, hipStream_t
     void* args[] = {&a, &s};
     hipError_t e;
     if (sp.rowk) {
-        const int nblk = (p.N + KR_W - 1) / KR_W;
-        const void* row = sp.dw ? reinterpret_cast<const void*>(&gemv_kn_row_kernel<EL, true>)
-                                : reinterpret_cast<const void*>(&gemv_kn_row_kernel<EL, false>);
-        e = hipLaunchKernel(row, dim3(nblk * sp.S), dim3(KR_WAVES * 64), args, 0, stream);
+        const int nblk = (p.N + KR_W - 1) / KR_W, mr = kr_rows(p.M);
+        const void* row = sp.dw ? kr_kernel<EL, true>(mr) : kr_kernel<EL, false>(mr);
+        e = hipLaunchKernel(row, dim3(nblk * sp.S, (p.M + mr - 1) / mr), dim3(kr_waves(mr) * 64), args, 0, stream);
     } else {
         const int nblk = (p.N + sp.kw * KS_W - 1) / (sp.kw * KS_W);
         const void* split = ks_kernel<EL>(p.M, sp.kw);
@@ -1003,11 +1051,11 @@ static bool kn_aligned16(const GemmArgs& p) {
     const uintptr_t a = reinterpret_cast<uintptr_t>(p.A), b = reinterpret_cast<uintptr_t>(p.B);
     return p.K >= 64 && p.N % 16 == 0 && p.K % 64 == 0 && ((a | b) & 15) == 0;
 }
-// 4-byte loads: the row kernel's dword form (M = 1), which a workspace of one
-// split's partial sums or more lets run.
+// 4-byte loads: the row kernel's dword form (any M to 32), which a workspace
+// of one split's partial sums or more lets run.
 static bool kn_aligned4(const GemmArgs& p) {
     const uintptr_t a = reinterpret_cast<uintptr_t>(p.A), b = reinterpret_cast<uintptr_t>(p.B);
-    return p.M == 1 && p.N % 4 == 0 && p.K % 4 == 0 && ((a | b) & 3) == 0;
+    return p.N % 4 == 0 && p.K % 4 == 0 && ((a | b) & 3) == 0;
 }
 static bool kn_shape_ok(const GemmArgs& p, int elem) {
     return kn_common_ok(p, elem) && (kn_aligned16(p) || kn_aligned4(p));
@@ -1054,7 +1102,9 @@ static KsPlan ks_plan(const GemmArgs& p, int kw, int kCUs, size_t ws_bytes) {
 
 // The plan: M = 1 takes the row kernel whenever two or more splits of its
 // 1024-column workgroups fit: S = CUs / blocks (at most 64, whole 128-row
-// pieces, none empty; 16 at N = 14336, K = 4096: 224 workgroups).  Otherwise
+// pieces, none empty; 16 at N = 14336, K = 4096: 224 workgroups).  So does
+// any M (to 32) that the 16-byte loads cannot take, with blocks counted once
+// per workgroup of activation rows and one split when no more fit.  Otherwise
 // the split kernel, on workgroups of two waves (256 columns; four splits at
 // N = 14336), of four when two-wave blocks outnumber half the CUs (N > 32768
 // on 256 CUs: fewer, wider workgroups over several rounds), and of one when
@@ -1073,14 +1123,15 @@ static void kn_splits(const GemmArgs& p, size_t ws_bytes, KnSplit* sp) {
     const int P = (p.K + KS_ROWS - 1) / KS_ROWS;
     sp->rowk = 0;
     sp->dw = !kn_aligned16(p);
-    if (p.M == 1) {
-        int S = kCUs / ((p.N + KR_W - 1) / KR_W);
+    if (p.M == 1 || sp->dw) {
+        const int mr = kr_rows(p.M);
+        int S = kCUs / ((p.N + KR_W - 1) / KR_W * ((p.M + mr - 1) / mr));
         if (S > KR_SMAX) S = KR_SMAX;
         if (S > P) S = P;
         if (S < 1) S = 1;
-        while (S > 1 && kn_ws_bytes(1, p.N, S) > ws_bytes) --S;
+        while (S > 1 && kn_ws_bytes(p.M, p.N, S) > ws_bytes) --S;
         // the dword form has no other kernel: one split will do
-        if (S >= 2 || (sp->dw && kn_ws_bytes(1, p.N, 1) <= ws_bytes)) {
+        if (S >= 2 || (sp->dw && kn_ws_bytes(p.M, p.N, 1) <= ws_bytes)) {
             const int PS = (P + S - 1) / S;
             sp->S = (P + PS - 1) / PS;
             sp->PS = PS;
@@ -1131,6 +1182,10 @@ bool gemv_kn_supports(const GemmArgs& p, int elem) {
     const int grid = (p.N + sp.kw * KS_W - 1) / (sp.kw * KS_W) * sp.S;
     return grid <= kCUs && grid >= kCUs - kCUs / 8;
 }
+
+// Same box, N = 14336, K = 4000, B [K,N], INT8 bf16 out: M = 4 16.2 us on
+// the row kernel against 19.4 on the MFMA GEMM; M = 16 27.8 against 20.3.
+bool gemv_kn_yields_to_mfma(const GemmArgs& p) { return p.M > 4 && !kn_aligned16(p); }
 
 size_t gemv_kn_workspace_bytes(const GemmArgs& p) {
     KnSplit sp;

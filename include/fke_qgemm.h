@@ -138,7 +138,7 @@ int fke_qgemm_f8_on_path(int path, const uint8_t* A, const uint8_t* B, void* C,
 
 /*
  * Workspace of the B [K,N] decode (M <= 16, and 17..32 where its split fills
- * the CUs; M = 1 also with N and K only multiples of 4 and 4-byte-aligned
+ * the CUs; M <= 32 also with N and K only multiples of 4 and 4-byte-aligned
  * operands, which need it; INT8 and FP8; no reference counterpart: the reference kernels sum
  * all of K in one thread, src/quantized_gemm.cu:29-37, :106-116).  The decode
  * splits K over workgroups of 128 to 1024 columns (up to 8 splits; M = 1 up to

@@ -85,9 +85,10 @@ int main(void) {
                     const int ps = fke_select_path_i8_swiglu(P, P, P, M, N, K, FKE_OUT_BF16);
                     CHECK(ps == -1 || (ps >= FKE_PATH_GEMV && ps <= FKE_PATH_GENERIC));
                     /* B [K,N] decode workspace (M <= 32): M*N*4 bytes per split (N rounded to 128),
-                       at most 8 splits (M = 1: 64, the row kernel) */
+                       2..8 splits (the row kernel, M = 1 or N, K not multiples of 16 / 64: 1..64) */
                     const size_t ws = fke_qgemm_workspace_size(M, N, K, lay);
                     const size_t row = (size_t)((N + 127LL) / 128) * 128 * 4 * (size_t)M;
+                    const int rowk = M == 1 || N % 16 != 0 || K % 64 != 0;
                     /* or the MFMA GEMM's K split: S * M * N * 4 bytes, 2 <= S <= 8 */
                     int tp = -1;
                     const int S = fke_select_mfma_split(M, N, K, lay, 256, &tp);
@@ -96,8 +97,8 @@ int main(void) {
                     CHECK(S == 1 || tp >= FKE_PATH_MFMA_128x128_RING4);
                     const size_t split = S > 1 ? (size_t)S * (size_t)M * (size_t)N * 4 : 0;
                     CHECK(ws == 0 || ws == split ||
-                          (lay == FKE_B_KN && M <= 32 && ws % row == 0 && ws / row >= (M == 1 ? 1 : 2) &&
-                           ws / row <= (M == 1 ? 64 : 8)));
+                          (lay == FKE_B_KN && M <= 32 && ws % row == 0 && ws / row >= (rowk ? 1 : 2) &&
+                           ws / row <= (rowk ? 64 : 8)));
                     n_split += S > 1;
                     ++n_ws;
                     /* MFMA tile: the narrow rings not for SwiGLU; -1 only for an odd SwiGLU N */

@@ -100,9 +100,12 @@ def test_workspace_entry_points_reject_bad_arguments():
     # unsplit: K of one piece, the decode not taken (M > 16, B [N,K], N % 16 != 0, K % 64 != 0)
     (1, 14336, 128, 1, 0), (33, 14336, 4096, 1, 0), (1, 14336, 4096, 0, 0), (1, 1002, 4096, 1, 0),
     (1, 14336, 4002, 1, 0), (0, 14336, 4096, 1, 0), (1, 14336, 4096, 2, 0),
-    # M = 1 with N or K only a multiple of 4: the row kernel's 4-byte form (8 blocks of 128 x 32 splits;
-    # 112 blocks x 16 splits)
+    # N or K only a multiple of 4: the row kernel's 4-byte form (8 blocks of 128 x 32 splits;
+    # 112 blocks x 16 splits); past one row, 1024-column blocks x row groups of 2 / 4 rows
+    # (M = 3: 15 blocks -> 16 splits of 2 pieces; M = 16: 60 -> 4 splits; M = 32: 120 -> 2)
     (1, 1000, 4096, 1, 32 * 1 * 1024 * 4), (1, 14336, 4000, 1, 16 * 1 * 14336 * 4),
+    (4, 1000, 4096, 1, 32 * 4 * 1024 * 4), (3, 14340, 4096, 1, 16 * 3 * 14464 * 4),
+    (16, 14340, 4096, 1, 4 * 16 * 14464 * 4), (32, 14340, 4096, 1, 2 * 32 * 14464 * 4),
 ])
 def test_workspace_size(M, N, K, layout, expect):
     assert _lib.lib().fke_qgemm_workspace_size(M, N, K, layout) == expect
@@ -251,19 +254,24 @@ def test_path_unavailable_for_shape_is_rejected():
                                   0, 0, None) == INVALID
     assert L.fke_qgemm_i8_swiglu_on_path(_lib.PATH_GEMV_DOT, P, P, P, 5, 64, 4096, None, None, 1.0, 1.0, None,
                                          1, None) == INVALID
-    # GEMV with B [K,N]: M <= 16, N % 16 == 0, K % 64 == 0
+    # GEMV with B [K,N]: M <= 16 (to 32 where the split fills the CUs) with N % 16 == 0 and
+    # K % 64 == 0, or M <= 32 with N % 4 == 0 and K % 4 == 0 (the row kernel's 4-byte form)
     assert L.fke_qgemm_i8_on_path(_lib.PATH_GEMV, P, P, P, 17, 64, 4096, None, None, 1.0, 1.0, None,
                                   0, 1, None) == INVALID
-    assert L.fke_qgemm_i8_on_path(_lib.PATH_GEMV, P, P, P, 4, 72, 4096, None, None, 1.0, 1.0, None,
+    assert L.fke_qgemm_i8_on_path(_lib.PATH_GEMV, P, P, P, 4, 70, 4096, None, None, 1.0, 1.0, None,
                                   0, 1, None) == INVALID
-    assert L.fke_qgemm_i8_on_path(_lib.PATH_GEMV, P, P, P, 4, 64, 4000, None, None, 1.0, 1.0, None,
+    assert L.fke_qgemm_i8_on_path(_lib.PATH_GEMV, P, P, P, 4, 64, 4002, None, None, 1.0, 1.0, None,
+                                  0, 1, None) == INVALID
+    assert L.fke_qgemm_i8_on_path(_lib.PATH_GEMV, P, P, P, 33, 72, 4096, None, None, 1.0, 1.0, None,
                                   0, 1, None) == INVALID
     assert L.fke_qgemm_i8_on_path(_lib.PATH_MFMA, P, P, P, 64, 64, 100, None, None, 1.0, 1.0, None,
                                   0, 0, None) == INVALID
-    # FP8 decode family: B [N,K] with K >= 2048, or B [K,N] with M <= 16; fp32 / bf16 out
+    # FP8 decode family: B [N,K] with K >= 2048, or B [K,N] as for INT8; fp32 / bf16 out
     assert L.fke_qgemm_f8_on_path(_lib.PATH_GEMV, P, P, P, 17, 64, 4096, 1.0, 1.0, None, 0, 1,
                                   None) == INVALID
-    assert L.fke_qgemm_f8_on_path(_lib.PATH_GEMV, P, P, P, 4, 72, 4096, 1.0, 1.0, None, 0, 1,
+    assert L.fke_qgemm_f8_on_path(_lib.PATH_GEMV, P, P, P, 4, 70, 4096, 1.0, 1.0, None, 0, 1,
+                                  None) == INVALID
+    assert L.fke_qgemm_f8_on_path(_lib.PATH_GEMV, P, P, P, 33, 72, 4096, 1.0, 1.0, None, 0, 1,
                                   None) == INVALID
     assert L.fke_qgemm_f8_on_path(_lib.PATH_GEMV, P, P, P, 4, 64, 1024, 1.0, 1.0, None, 0, 0,
                                   None) == INVALID
@@ -304,8 +312,12 @@ def test_path_unavailable_for_shape_is_rejected():
     (1, 14336, 4096, 1, _lib.PATH_GEMV),     # B [K,N] decode: the transposing streamed kernel
     (16, 14336, 4096, 1, _lib.PATH_GEMV),
     (4, 4096, 64, 1, _lib.PATH_GEMV),
-    (4, 4104, 4096, 1, _lib.PATH_GENERIC),   # B [K,N] with N % 16 != 0: neither fast kernel past one row
-    (1, 4104, 4096, 1, _lib.PATH_GEMV),      # one row: the row kernel's 4-byte form
+    (4, 4104, 4096, 1, _lib.PATH_GEMV),      # B [K,N] with N % 16 != 0: the row kernel's 4-byte form
+    (1, 4104, 4096, 1, _lib.PATH_GEMV),
+    (32, 4104, 4096, 1, _lib.PATH_GEMV),
+    (5, 14336, 4000, 1, _lib.PATH_MFMA),     # past 4 rows the MFMA GEMM where it can (K % 16 == 0, N % 16 == 0)
+    (4, 14336, 4000, 1, _lib.PATH_GEMV),     # one row group: the 4-byte form
+    (33, 4104, 4096, 1, _lib.PATH_GENERIC),  # past 32 rows: no [K,N] decode, and the MFMA GEMM needs N % 16
     (1, 1002, 4096, 1, _lib.PATH_GENERIC),   # N % 4 != 0
     (17, 4096, 4096, 1, _lib.PATH_GEMV),
     (64, 64, 100, 0, _lib.PATH_GENERIC),
@@ -338,8 +350,11 @@ def test_dispatch_unaligned_pointer_falls_back():
     (16, 14336, 4096, 1, _lib.PATH_GEMV),
     (17, 14336, 4096, 1, _lib.PATH_GEMV),
     (33, 14336, 4096, 1, _lib.PATH_MFMA),
-    (4, 14336, 4000, 1, _lib.PATH_MFMA),      # K % 64 != 0: not the decode kernel; the MFMA GEMM (K % 16 == 0)
-    (4, 14336, 4004, 1, _lib.PATH_GENERIC),   # K % 16 != 0
+    (4, 14336, 4000, 1, _lib.PATH_GEMV),      # K % 64 != 0: the row kernel's 4-byte form (K % 4 == 0)
+    (4, 14336, 4004, 1, _lib.PATH_GEMV),      # K % 16 != 0 (K % 4 == 0): the 4-byte form too
+    (16, 14336, 4000, 1, _lib.PATH_MFMA),     # past 4 rows the MFMA GEMM where it can
+    (16, 14336, 4004, 1, _lib.PATH_GEMV),     # and the 4-byte form where it cannot
+    (4, 14336, 4002, 1, _lib.PATH_GENERIC),   # K % 4 != 0
     (8192, 8192, 8192, 0, _lib.PATH_MFMA),
     (4, 14336, 1024, 0, _lib.PATH_MFMA),      # K < 2048
     (4, 300, 2112, 0, _lib.PATH_GEMV),        # K % 128 != 0: no MFMA GEMM

@@ -409,23 +409,25 @@ def dev_at(x, shift):
     return buf, buf.data_ptr() + shift
 
 
-# M = 1 with B [K,N] whose N or K is only a multiple of 4, or whose operands
-# are only 4-byte aligned: the row kernel's 4-byte form (one split when the
-# plan gives one, a ragged last 1024-column block, K not a multiple of 128).
-KN_DW_CASES = [(1000, 4096, 0), (14340, 4096, 0), (4100, 4100, 0), (2052, 100, 0), (14336, 4000, 0),
-               (14336, 4096, 4), (1024, 4, 4)]
+# B [K,N] whose N or K is only a multiple of 4, or whose operands are only
+# 4-byte aligned: the row kernel's 4-byte form (one split when the plan gives
+# one, a ragged last 1024-column block, K not a multiple of 128; past one row,
+# workgroups of 2 or 4 activation rows, the last group part empty).
+KN_DW_CASES = [(1, 1000, 4096, 0), (1, 14340, 4096, 0), (1, 4100, 4100, 0), (1, 2052, 100, 0), (1, 14336, 4000, 0),
+               (1, 14336, 4096, 4), (1, 1024, 4, 4), (2, 14340, 4096, 0), (3, 4100, 4100, 4), (4, 1000, 4096, 0),
+               (5, 2052, 100, 0), (8, 14336, 4096, 4), (16, 14340, 4096, 0), (17, 4100, 1028, 4),
+               (32, 14340, 4096, 0)]
 
 
-@pytest.mark.parametrize("N,K,shift", KN_DW_CASES)
-def test_gemv_kn_row_kernel_dword_form(oracle, dev, N, K, shift):
+@pytest.mark.parametrize("M,N,K,shift", KN_DW_CASES)
+def test_gemv_kn_row_kernel_dword_form(oracle, dev, M, N, K, shift):
     """INT8 bit-exact on every output type, and FP8 (0x7F / 0xFF codes
     included) within the bounds of the sequential sum, through fke_qgemm_i8 /
     fke_qgemm_f8 with A and B `shift` bytes past 16-byte alignment."""
-    M = 1
     say("kn row kernel, 4-byte loads", M, N, K, shift)
     L = _lib.lib()
     assert L.fke_select_path_i8(4096 + shift, 4096 + shift, 4096, M, N, K, _lib.OUT_BF16, _lib.B_KN) == _lib.PATH_GEMV
-    A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 9700 + N + K, layout="kn", act="normal")
+    A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 9700 + 31 * M + N + K, layout="kn", act="normal")
     acc = oracle.w8a8_acc(A, B, oracle.B_KN, nthreads=NTH)
     (ba, pa), (bb, pb) = dev_at(A, shift), dev_at(B, shift)
     dsa, dsb, dbias = dev_t(sa), dev_t(sb), dev_t(bias)
@@ -436,15 +438,15 @@ def test_gemv_kn_row_kernel_dword_form(oracle, dev, N, K, shift):
                                   _lib.B_KN, torch.cuda.current_stream().cuda_stream), "fke_qgemm_i8")
         torch.cuda.synchronize()
         want = acc if out == "i32" else oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, out)
-        assert_same(host(C), want, f"kn dword {out} N={N} K={K} shift={shift}")
-    A8, B8, fa, fb = f8_inputs(oracle, M, N, K, 9800 + N + K, "kn", with_nan_codes=True)
+        assert_same(host(C), want, f"kn dword {out} M={M} N={N} K={K} shift={shift}")
+    A8, B8, fa, fb = f8_inputs(oracle, M, N, K, 9800 + 31 * M + N + K, "kn", with_nan_codes=True)
     ref = oracle.f8_gemm(A8, B8, fa, fb, b_layout=oracle.B_KN, nthreads=NTH)
     (ba, pa), (bb, pb) = dev_at(A8, shift), dev_at(B8, shift)
     C = torch.empty((M, N), dtype=torch.float32, device=dev)
     _lib.check(L.fke_qgemm_f8(pa, pb, C.data_ptr(), M, N, K, fa, fb, None, _lib.OUT_F32, _lib.B_KN,
                               torch.cuda.current_stream().cuda_stream), "fke_qgemm_f8")
     torch.cuda.synchronize()
-    assert_fp8_close(host(C), ref, "f32", f"kn dword fp8 N={N} K={K} shift={shift}")
+    assert_fp8_close(host(C), ref, "f32", f"kn dword fp8 M={M} N={N} K={K} shift={shift}")
 
 
 def test_gemv_kn_graph_replays(oracle, dev):
