@@ -110,7 +110,8 @@ def parse():
                     help="also time the headline GEMM on zero, constant and narrow-range operands (clock vs data)")
     ap.add_argument("--odd-k", action="store_true",
                     help="prefill shapes with K %% 128 != 0 (4096x11008x4160, 4096x4096x2880) on the MFMA GEMM "
-                         "(partial last stage) and on the any-shape generic kernel (part of --extra)")
+                         "(partial last stage), 4096x11008x4100 on the INT8 word kernel, each also on the "
+                         "any-shape generic kernel (part of --extra)")
     ap.add_argument("--mfma-ceiling", action="store_true",
                     help="the INT8 matrix-core ceiling: a register-only v_mfma_i32_32x32x32_i8 stream "
                          "(libfke_probe.so) on the headline's operand distribution and on constant operands, "
@@ -837,14 +838,15 @@ def extra_configs(torch, L, _lib, dev, gen, timed, rand_i8, rand_u, args):
 def odd_k_configs(torch, L, _lib, dev, timed, rand_i8, rand_u, args):
     """Prefill W8A8 shapes whose K is not a multiple of the 128-byte stage (bf16
     out, per-token x per-channel scales): the dispatcher's MFMA GEMM (its last
-    stage cleared past K) and the any-shape generic kernel pinned on the same
-    call, each with its roofline."""
+    stage cleared past K; for K % 16 != 0 the word kernel) and the any-shape
+    generic kernel pinned on the same call, each with its roofline."""
     res = {}
     sh = torch.cuda.current_stream(dev).cuda_stream
-    for M, N, K in ((4096, 11008, 4160), (4096, 4096, 2880)):
+    for M, N, K in ((4096, 11008, 4160), (4096, 4096, 2880), (4096, 11008, 4100)):
         A, B, sa, sb = rand_i8(M, K), rand_i8(N, K), rand_u(M), rand_u(N)
         C = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
-        for name, path in (("mfma", _lib.PATH_AUTO), ("generic", _lib.PATH_GENERIC)):
+        fast = "words" if K % 16 else "mfma"
+        for name, path in ((fast, _lib.PATH_AUTO), ("generic", _lib.PATH_GENERIC)):
             if path == _lib.PATH_AUTO:
                 assert L.fke_select_path_i8(A.data_ptr(), B.data_ptr(), C.data_ptr(), M, N, K, _lib.OUT_BF16,
                                             _lib.B_NK) == _lib.PATH_MFMA
@@ -855,13 +857,14 @@ def odd_k_configs(torch, L, _lib, dev, timed, rand_i8, rand_u, args):
                 if st:
                     raise RuntimeError(f"fke_qgemm_i8_on_path failed: {_lib.status_string(st)}")
 
-            steps = args.steps if name == "mfma" else max(3, args.steps // 10)
-            ms = timed(run, steps, 2 if name == "generic" else args.warmup, args.preheat_ms if name == "mfma" else 0)
+            steps = args.steps if name != "generic" else max(3, args.steps // 10)
+            ms = timed(run, steps, 2 if name == "generic" else args.warmup, args.preheat_ms if name != "generic" else 0)
             t = 2.0 * M * N * K / (ms * 1e-3) / 1e12
             res[f"prefill_{M}x{N}x{K}_bf16_{name}"] = {
                 "ms": round(ms, 4), "TOPS": round(t, 1), "frac": round(t / PEAK_INT8_TOPS, 4),
-                "kernel": "gemm_mfma_kernel<i8,NK,bf16> (partial last stage)" if name == "mfma"
-                else "gemm_generic_kernel<i8>"}
+                "kernel": {"mfma": "gemm_mfma_kernel<i8,NK,bf16> (partial last stage)",
+                           "words": "gemm_i8_words_kernel<bf16> (4-byte loads, K % 4 == 0)",
+                           "generic": "gemm_generic_kernel<i8>"}[name]}
         del A, B, C
     return res
 

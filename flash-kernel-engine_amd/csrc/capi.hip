@@ -272,6 +272,7 @@ int pick_i8(const GemmArgs& p) {
     if (fke::gemv_i8_supports(p) && (fke::gemv_i8_batch_pays(p) || !fke::mfma_supports(p, fke::ELEM_I8)))
         return FKE_PATH_GEMV;
     if (fke::mfma_supports(p, fke::ELEM_I8)) return FKE_PATH_MFMA;
+    if (fke::words_supports(p)) return FKE_PATH_MFMA;  // K % 4 == 0: the word kernel's matrix cores
     return FKE_PATH_GENERIC;
 }
 
@@ -304,7 +305,13 @@ int mfma_tile_of_path(int path, const GemmArgs& p) {
 // rule's tile, when that does not hold the partial sums.
 int run_mfma(int path, const GemmArgs& p, int elem, hipStream_t s, const WsChoice& wc) {
     const int tile = mfma_tile_of_path(path, p);
-    if (tile < 0 || !fke::mfma_supports(p, elem)) return hipErrorInvalidValue;
+    if (tile < 0) return hipErrorInvalidValue;
+    if (!fke::mfma_supports(p, elem)) {
+        // INT8 with B [N,K], K % 4 == 0, 4-byte-aligned operands: the word kernel
+        if (tile == fke::MFMA_TILE_AUTO && elem == fke::ELEM_I8 && fke::words_supports(p))
+            return fke::launch_words(p, s);
+        return hipErrorInvalidValue;
+    }
     if (tile == fke::MFMA_TILE_AUTO) {
         const fke::MfmaPlan pl = fke::mfma_plan(p, elem, fke::device_cus());
         if (pl.S > 1) {

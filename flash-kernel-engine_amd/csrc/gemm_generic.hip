@@ -202,7 +202,168 @@ hipError_t launch_t(const GemmArgs& p, hipStream_t stream) {
                            dim3(256), args, 0, stream);
 }
 
+// ===========================================================================
+// INT8 word kernel: B [N,K] with K % 4 == 0 and A, B 4-byte aligned (the
+// reference's own INT8 domain: K / 4 packed words per row,
+// src/quantized_gemm.cu:28-37), for the shapes the MFMA GEMM's 16-byte copies
+// cannot take (K % 16 != 0, or pointers not 16-byte aligned).  128x128 output
+// tile per 256-thread workgroup, wave w the 64x64 block (w / 2, w % 2).  K
+// runs in stages of 64 bytes through a ring of WNS stages in LDS, copied with
+// 4-byte LDS-DMA loads (buffer_load_dword ... lds: lane l's word lands at
+// 4l of the instruction's 256 bytes), so no registers hold the stages in
+// flight; words past M, N or K read zero through the buffer range (K % 4 ==
+// 0: a word is all in K or all out).  A stage row (one M row of A, one N row
+// of B) is 64 bytes, logical 16-byte chunk c at physical chunk c ^ w_swz(r):
+// the 16 rows of a 16-lane fragment read then cover all 64 banks once.  The
+// waves multiply each stage with v_mfma_i32_16x16x64_i8, lane (g, r) of a
+// fragment taking bytes 16g .. 16g + 15 of row r.  Exact int32 sums, then the
+// same epilogue as the generic kernel.
+// ===========================================================================
+constexpr int WT = 128;                   // tile edge
+constexpr int WKC = 64;                   // K bytes per stage
+constexpr int WNS = 4;                    // ring stages (64 KiB of LDS)
+constexpr int WOP = WT * WKC;             // bytes of one operand's stage (8 KiB)
+constexpr int WCP = WOP / (4 * 256);      // 4-byte copies per wave, operand and stage (8)
+static_assert(WCP == 8 && WNS == 4, "copy and wait counts below");
+
+typedef int w4i __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) uint8_t w_lds;
+
+// Physical chunk of a stage row r is logical chunk ^ w_swz(r).
+__device__ __forceinline__ int w_swz(int r) { return (r >> 2) & 3; }
+__device__ __forceinline__ w4i w_rd128(const w_lds* a) {
+    w4i r;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(a));
+    return r;
+}
+
+template <int OUT>
+__global__ __launch_bounds__(256) void gemm_i8_words_kernel(GemmArgs p) {
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[WNS][2][WOP];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int M = p.M, N = p.N, K = p.K;
+    const int m0 = blockIdx.y * WT, n0 = blockIdx.x * WT;
+    const int nst = (K + WKC - 1) / WKC;
+
+    // Copy i of wave w (each operand): stage bytes 256 (8w + i) + 4l = tile
+    // row r = 4 (8w + i) + l / 16, physical chunk (l % 16) / 4, word l % 4,
+    // which holds logical chunk ((l % 16) / 4) ^ w_swz(r), w_swz(r) = i & 3.
+    // Offsets are 32-bit (M K and N K below 2^31); bit 31 set reads zero.
+    const int lr = lane >> 4, pc = (lane & 15) >> 2, dw = lane & 3;
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, M * K);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.B, N * K);
+    uint32_t arow[WCP], brow[WCP];
+#pragma unroll
+    for (int i = 0; i < WCP; ++i) {
+        const int r = 4 * (WCP * wave + i) + lr;
+        arow[i] = m0 + r < M ? static_cast<uint32_t>((m0 + r) * K) : 0x80000000u;
+        brow[i] = n0 + r < N ? static_cast<uint32_t>((n0 + r) * K) : 0x80000000u;
+    }
+    int kof[4];  // byte of the stage this lane copies, for copies with i % 4 == j
+#pragma unroll
+    for (int j = 0; j < 4; ++j) kof[j] = 16 * (pc ^ j) + 4 * dw;
+    auto issue = [&](int s) __attribute__((always_inline)) {
+        const int k0 = s * WKC, slot = s % WNS;
+#pragma unroll
+        for (int i = 0; i < WCP; ++i) {
+            const int kb = k0 + kof[i & 3];
+            const bool in = kb < K;
+            const int dst = (WCP * wave + i) * 256;
+            dma4(ra, in ? arow[i] + static_cast<uint32_t>(kb) : 0x80000000u, 0, &ring[slot][0][dst]);
+            dma4(rb, in ? brow[i] + static_cast<uint32_t>(kb) : 0x80000000u, 0, &ring[slot][1][dst]);
+        }
+    };
+
+    // Fragment reads: lane (g, r) = (lane / 16, lane % 16) reads logical
+    // chunk g of row 16 x + r of the wave's 64 rows.
+    const int g = lane >> 4, rr = lane & 15;
+    uint32_t fa[4], fb[4];
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+        const int ra_ = wm * 64 + 16 * x + rr, rb_ = wn * 64 + 16 * x + rr;
+        fa[x] = static_cast<uint32_t>(ra_ * WKC + 16 * (g ^ w_swz(ra_)));
+        fb[x] = static_cast<uint32_t>(WOP + rb_ * WKC + 16 * (g ^ w_swz(rb_)));
+    }
+    const w_lds* const lring = (const w_lds*)(&ring[0][0][0]);
+
+    w4i acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = w4i{0, 0, 0, 0};
+
+#pragma unroll
+    for (int s = 0; s < WNS - 1; ++s)
+        if (s < nst) issue(s);
+    for (int s = 0; s < nst; ++s) {
+        // Stage s has landed once at most the copies of the stages issued
+        // after it (s + 1 .. s + WNS - 2, those below nst) are in flight; the
+        // barrier then also says that every wave is done with stage s - 1,
+        // whose slot takes stage s + WNS - 1.
+        const int later = min(nst - 1 - s, WNS - 2);
+        if (later == 0) wait_vm<0>();
+        else if (later == 1) wait_vm<2 * WCP>();
+        else wait_vm<4 * WCP>();
+        barrier();
+        if (s + WNS - 1 < nst) issue(s + WNS - 1);
+        const w_lds* st = lring + (s % WNS) * 2 * WOP;
+        w4i af[4], bf[4];
+#pragma unroll
+        for (int x = 0; x < 4; ++x) af[x] = w_rd128(st + fa[x]);
+#pragma unroll
+        for (int x = 0; x < 4; ++x) bf[x] = w_rd128(st + fb[x]);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int x = 0; x < 4; ++x) asm volatile("" : "+v"(af[x]), "+v"(bf[x]));
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+
+    // Lane (g, c) of block (i, j) holds rows 16i + 4g + v, column 16j + c of the wave's block.
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int m = m0 + wm * 64 + 16 * i + 4 * g + v;
+            if (m >= M) continue;
+            const float sam = p.scale_a ? p.scale_a[m] : p.sa;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int n = n0 + wn * 64 + 16 * j + rr;
+                if (n >= N) continue;
+                const int32_t s32 = acc[i][j][v];
+                const float s = sam * (p.scale_b ? p.scale_b[n] : p.sb);
+                store_out<OUT>(p.C, static_cast<size_t>(m) * N + n, epilogue_value(static_cast<float>(s32), s, p.bias, n),
+                               s32);
+            }
+        }
+}
+
 }  // namespace
+
+bool words_supports(const GemmArgs& p) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p.A), b = reinterpret_cast<uintptr_t>(p.B);
+    if (p.M < 1 || p.N < 1 || p.K < 4 || p.K % 4 != 0 || p.swiglu || p.b_layout != FKE_B_NK) return false;
+    if ((a | b) & 3) return false;
+    if ((static_cast<int64_t>(p.M) + WT - 1) / WT > 65535) return false;  // grid y
+    // 32-bit buffer offsets
+    return static_cast<int64_t>(p.M) * p.K <= INT32_MAX && static_cast<int64_t>(p.N) * p.K <= INT32_MAX;
+}
+
+hipError_t launch_words(const GemmArgs& p, hipStream_t s) {
+    if (!words_supports(p)) return hipErrorInvalidValue;
+    GemmArgs a = p;
+    void* args[] = {&a};
+    const dim3 grid((p.N + WT - 1) / WT, (p.M + WT - 1) / WT);
+    const void* f = p.out_dtype == FKE_OUT_F32    ? reinterpret_cast<const void*>(&gemm_i8_words_kernel<FKE_OUT_F32>)
+                    : p.out_dtype == FKE_OUT_BF16 ? reinterpret_cast<const void*>(&gemm_i8_words_kernel<FKE_OUT_BF16>)
+                                                  : reinterpret_cast<const void*>(&gemm_i8_words_kernel<FKE_OUT_I32>);
+    return hipLaunchKernel(f, grid, dim3(256), args, 0, s);
+}
 
 hipError_t launch_generic(const GemmArgs& p, int elem, hipStream_t s) {
     if (p.swiglu) {

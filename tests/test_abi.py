@@ -240,7 +240,7 @@ def test_dropin_int8_rejects_k_not_multiple_of_4():
 
 def test_path_unavailable_for_shape_is_rejected():
     L = _lib.lib()
-    # GEMV needs M <= 512 (K >= 2048 past 16 rows), K % 64 == 0, B [N,K]; MFMA needs K % 128 == 0
+    # GEMV needs M <= 512 (K >= 2048 past 16 rows), K % 64 == 0, B [N,K]; MFMA needs K % 16 == 0 (INT8 with B [N,K]: K % 4 == 0, the word kernel)
     assert L.fke_qgemm_i8_on_path(_lib.PATH_GEMV, P, P, P, 17, 64, 1024, None, None, 1.0, 1.0, None,
                                   0, 0, None) == INVALID
     assert L.fke_qgemm_i8_on_path(_lib.PATH_GEMV, P, P, P, 513, 64, 4096, None, None, 1.0, 1.0, None,
@@ -264,7 +264,10 @@ def test_path_unavailable_for_shape_is_rejected():
                                   0, 1, None) == INVALID
     assert L.fke_qgemm_i8_on_path(_lib.PATH_GEMV, P, P, P, 33, 72, 4096, None, None, 1.0, 1.0, None,
                                   0, 1, None) == INVALID
-    assert L.fke_qgemm_i8_on_path(_lib.PATH_MFMA, P, P, P, 64, 64, 100, None, None, 1.0, 1.0, None,
+    assert L.fke_qgemm_i8_on_path(_lib.PATH_MFMA, P, P, P, 64, 64, 102, None, None, 1.0, 1.0, None,
+                                  0, 0, None) == INVALID
+    # the word kernel (K % 4 == 0) only on the automatic tile
+    assert L.fke_qgemm_i8_on_path(_lib.PATH_MFMA_128x128, P, P, P, 64, 64, 100, None, None, 1.0, 1.0, None,
                                   0, 0, None) == INVALID
     # FP8 decode family: B [N,K] with K >= 2048, or B [K,N] as for INT8; fp32 / bf16 out
     assert L.fke_qgemm_f8_on_path(_lib.PATH_GEMV, P, P, P, 17, 64, 4096, 1.0, 1.0, None, 0, 1,
@@ -320,11 +323,14 @@ def test_path_unavailable_for_shape_is_rejected():
     (33, 4104, 4096, 1, _lib.PATH_GENERIC),  # past 32 rows: no [K,N] decode, and the MFMA GEMM needs N % 16
     (1, 1002, 4096, 1, _lib.PATH_GENERIC),   # N % 4 != 0
     (17, 4096, 4096, 1, _lib.PATH_GEMV),
-    (64, 64, 100, 0, _lib.PATH_GENERIC),
-    (64, 64, 4, 0, _lib.PATH_GENERIC),
+    (64, 64, 100, 0, _lib.PATH_MFMA),        # K % 16 != 0, K % 4 == 0: the word kernel (B [N,K])
+    (64, 64, 4, 0, _lib.PATH_MFMA),
+    (64, 64, 102, 0, _lib.PATH_GENERIC),     # K % 4 != 0
     (8, 64, 96, 0, _lib.PATH_MFMA),          # K of 6 16-byte chunks: one partial stage
-    (8, 64, 104, 0, _lib.PATH_GENERIC),      # K % 16 != 0: rows not 16-byte aligned
-    (300, 520, 4104, 0, _lib.PATH_GENERIC),
+    (8, 64, 104, 0, _lib.PATH_MFMA),         # K % 16 != 0: rows not 16-byte aligned, the word kernel
+    (300, 520, 4104, 0, _lib.PATH_MFMA),
+    (300, 520, 4106, 0, _lib.PATH_GENERIC),
+    (300, 520, 4104, 1, _lib.PATH_GENERIC),  # B [K,N] past 32 rows: no word kernel
     (300, 520, 4112, 0, _lib.PATH_MFMA),
 ])
 def test_dispatch_i8(M, N, K, layout, expect):
@@ -334,7 +340,8 @@ def test_dispatch_i8(M, N, K, layout, expect):
 def test_dispatch_unaligned_pointer_falls_back():
     L = _lib.lib()
     assert L.fke_select_path_i8(P + 1, P, P, 1, 4096, 4096, 0, 0) == _lib.PATH_GENERIC
-    assert L.fke_select_path_i8(P, P + 4, P, 256, 4096, 4096, 0, 0) == _lib.PATH_GENERIC
+    assert L.fke_select_path_i8(P, P + 4, P, 256, 4096, 4096, 0, 0) == _lib.PATH_MFMA  # the word kernel
+    assert L.fke_select_path_i8(P, P + 2, P, 256, 4096, 4096, 0, 0) == _lib.PATH_GENERIC
     assert L.fke_select_path_f8(P + 2, P, P, 256, 256, 256, 0, 1) == _lib.PATH_GENERIC
     assert L.fke_select_path_f8(P, P, P, 8192, 8192, 8192, 1, 1) == _lib.PATH_MFMA
     assert L.fke_select_path_i8(None, P, P, 8, 8, 8, 0, 0) == -1

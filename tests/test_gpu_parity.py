@@ -1485,3 +1485,37 @@ def test_fp8_auto_dispatch_random_shapes(oracle, dev, M, N, K, layout, out):
     if out == "bf16":
         got = oracle.bf16_to_f32(got)
     assert_fp8_close(got, ref, out, f"auto {M, N, K, layout}")
+
+
+# INT8 with B [N,K] whose K is a multiple of 4 but not of 16, or whose
+# operands are only 4-byte aligned: the word kernel (128x128 tiles on the
+# matrix cores, 4-byte loads), through the automatic path.
+WORDS_CASES = [(1, 14336, 4100, 0), (3, 1000, 68, 0), (64, 64, 100, 0), (129, 257, 4, 0), (300, 520, 4104, 0),
+               (256, 4096, 4096, 4), (200, 1030, 1028, 4), (1024, 1024, 4100, 0)]
+
+
+@pytest.mark.parametrize("M,N,K,shift", WORDS_CASES)
+def test_words_kernel_bit_exact(oracle, dev, M, N, K, shift):
+    """Every output type bit-exact against the oracle, with A and B `shift`
+    bytes past 16-byte alignment; the call goes to FKE_PATH_MFMA."""
+    say("int8 word kernel", M, N, K, shift)
+    L = _lib.lib()
+    assert L.fke_select_path_i8(4096 + shift, 4096 + shift, 4096, M, N, K, _lib.OUT_BF16, _lib.B_NK) == _lib.PATH_MFMA
+    A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 9900 + 7 * M + N + K, layout="nk", act="normal")
+    acc = oracle.w8a8_acc(A, B, oracle.B_NK, nthreads=NTH)
+    (ba, pa), (bb, pb) = dev_at(A, shift), dev_at(B, shift)
+    dsa, dsb, dbias = dev_t(sa), dev_t(sb), dev_t(bias)
+    for out in ("i32", "f32", "bf16"):
+        C = torch.empty((M, N), dtype=OUT_T[out], device=dev)
+        _lib.check(L.fke_qgemm_i8(pa, pb, C.data_ptr(), M, N, K, dsa.data_ptr(), dsb.data_ptr(), 1.0, 1.0,
+                                  dbias.data_ptr(), {"f32": _lib.OUT_F32, "bf16": _lib.OUT_BF16, "i32": _lib.OUT_I32}[out],
+                                  _lib.B_NK, torch.cuda.current_stream().cuda_stream), "fke_qgemm_i8")
+        torch.cuda.synchronize()
+        want = acc if out == "i32" else oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, out)
+        assert_same(host(C), want, f"words {out} M={M} N={N} K={K} shift={shift}")
+    # scalar scales and no bias (the reference launcher's form)
+    C = torch.empty((M, N), dtype=torch.float32, device=dev)
+    _lib.check(L.fke_qgemm_i8(pa, pb, C.data_ptr(), M, N, K, None, None, 0.05, 0.02, None, _lib.OUT_F32, _lib.B_NK,
+                              torch.cuda.current_stream().cuda_stream), "fke_qgemm_i8")
+    torch.cuda.synchronize()
+    assert_same(host(C), oracle_out(oracle, acc, None, None, 0.05, 0.02, None, "f32"), f"words scalar M={M}")
