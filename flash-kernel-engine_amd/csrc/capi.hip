@@ -163,7 +163,8 @@ hipError_t run_kn(const GemmArgs& p, int elem, hipStream_t s, const WsChoice& wc
     const Workspace ws = split_workspace(s, fke::gemv_kn_workspace_bytes(p), wc);
     const fke::KnSplit sp = fke::gemv_kn_plan(p, ws.ptr, ws.bytes);
     if (!fke::gemv_kn_plan_runs(p, sp)) {
-        if (fke::mfma_supports(p, elem)) return static_cast<hipError_t>(run_mfma(FKE_PATH_MFMA, p, elem, s, wc));
+        if (fke::mfma_supports(p, elem) || fke::words_supports(p, elem))
+            return static_cast<hipError_t>(run_mfma(FKE_PATH_MFMA, p, elem, s, wc));
         return fke::launch_generic(p, elem, s);
     }
     return fke::launch_gemv_kn(p, elem, sp, s);
@@ -259,10 +260,15 @@ GemmArgs make_swiglu_args(const void* A, const void* W, void* H, int M, int I, i
     return p;
 }
 
-// Decode with B [K,N]: the transposing kernels, but the MFMA GEMM where the
-// row kernel's 4-byte form would stream the weights more than once.
+// Decode with B [K,N]: the transposing kernels, but where the row kernel's
+// 4-byte form would stream the weights more than once (past 4 rows) the MFMA
+// GEMM if it takes the shape, and past 20 rows the word kernel.  Same box,
+// N = 14340, K = 4096, bf16 out: row kernel / word kernel M = 16 40.0 / 48.4
+// us, M = 32 75.9 / 51.8 (FP8 43.8 / 57.8 and 80.5 / 61.1).
 bool kn_decode_pays(const GemmArgs& p, int elem) {
-    return fke::gemv_kn_supports(p, elem) && !(fke::gemv_kn_yields_to_mfma(p) && fke::mfma_supports(p, elem));
+    if (!fke::gemv_kn_supports(p, elem)) return false;
+    if (!fke::gemv_kn_yields_to_mfma(p)) return true;
+    return !(fke::mfma_supports(p, elem) || (p.M > 20 && fke::words_supports(p, elem)));
 }
 
 int pick_i8(const GemmArgs& p) {
@@ -272,7 +278,7 @@ int pick_i8(const GemmArgs& p) {
     if (fke::gemv_i8_supports(p) && (fke::gemv_i8_batch_pays(p) || !fke::mfma_supports(p, fke::ELEM_I8)))
         return FKE_PATH_GEMV;
     if (fke::mfma_supports(p, fke::ELEM_I8)) return FKE_PATH_MFMA;
-    if (fke::words_supports(p)) return FKE_PATH_MFMA;  // K % 4 == 0: the word kernel's matrix cores
+    if (fke::words_supports(p, fke::ELEM_I8)) return FKE_PATH_MFMA;  // the word kernel's matrix cores
     return FKE_PATH_GENERIC;
 }
 
@@ -282,6 +288,7 @@ int pick_f8(const GemmArgs& p) {
     if (fke::gemv_f8_supports(p) && (fke::gemv_i8_batch_pays(p) || !fke::mfma_supports(p, fke::ELEM_F8)))
         return FKE_PATH_GEMV;
     if (fke::mfma_supports(p, fke::ELEM_F8)) return FKE_PATH_MFMA;
+    if (fke::words_supports(p, fke::ELEM_F8)) return FKE_PATH_MFMA;  // the word kernel's matrix cores
     return FKE_PATH_GENERIC;
 }
 
@@ -307,9 +314,8 @@ int run_mfma(int path, const GemmArgs& p, int elem, hipStream_t s, const WsChoic
     const int tile = mfma_tile_of_path(path, p);
     if (tile < 0) return hipErrorInvalidValue;
     if (!fke::mfma_supports(p, elem)) {
-        // INT8 with B [N,K], K % 4 == 0, 4-byte-aligned operands: the word kernel
-        if (tile == fke::MFMA_TILE_AUTO && elem == fke::ELEM_I8 && fke::words_supports(p))
-            return fke::launch_words(p, s);
+        // K % 4 == 0 (and N % 4 == 0 with B [K,N]), 4-byte-aligned operands: the word kernel
+        if (tile == fke::MFMA_TILE_AUTO && fke::words_supports(p, elem)) return fke::launch_words(p, elem, s);
         return hipErrorInvalidValue;
     }
     if (tile == fke::MFMA_TILE_AUTO) {

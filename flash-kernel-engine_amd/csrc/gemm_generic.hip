@@ -20,6 +20,8 @@
 // the two operands of one output.
 #include "fke_internal.h"
 
+#include <type_traits>
+
 namespace fke {
 namespace {
 
@@ -203,65 +205,98 @@ hipError_t launch_t(const GemmArgs& p, hipStream_t stream) {
 }
 
 // ===========================================================================
-// INT8 word kernel: B [N,K] with K % 4 == 0 and A, B 4-byte aligned (the
-// reference's own INT8 domain: K / 4 packed words per row,
-// src/quantized_gemm.cu:28-37), for the shapes the MFMA GEMM's 16-byte copies
-// cannot take (K % 16 != 0, or pointers not 16-byte aligned).  128x128 output
-// tile per 256-thread workgroup, wave w the 64x64 block (w / 2, w % 2).  K
-// runs in stages of 64 bytes through a ring of WNS stages in LDS, copied with
-// 4-byte LDS-DMA loads (buffer_load_dword ... lds: lane l's word lands at
-// 4l of the instruction's 256 bytes), so no registers hold the stages in
-// flight; words past M, N or K read zero through the buffer range (K % 4 ==
-// 0: a word is all in K or all out).  A stage row (one M row of A, one N row
-// of B) is 64 bytes, logical 16-byte chunk c at physical chunk c ^ w_swz(r):
-// the 16 rows of a 16-lane fragment read then cover all 64 banks once.  The
-// waves multiply each stage with v_mfma_i32_16x16x64_i8, lane (g, r) of a
-// fragment taking bytes 16g .. 16g + 15 of row r.  Exact int32 sums, then the
-// same epilogue as the generic kernel.
+// Word kernel: INT8 and FP8 with K % 4 == 0, A and B 4-byte aligned (and
+// N % 4 == 0 for B [K,N]), for the shapes the MFMA GEMM's 16-byte copies
+// cannot take (K or, for B [K,N], N not a multiple of 16, or pointers not
+// 16-byte aligned).  The reference's INT8 kernel takes any K that is a
+// multiple of 4 (K / 4 packed words per row, src/quantized_gemm.cu:28-37);
+// its FP8 kernel any shape with B [K,N] (src/quantized_gemm.cu:99-118).
+// 128x128 output tile per 256-thread workgroup, wave w the 64x64 block
+// (w / 2, w % 2).  K runs in stages of 64 bytes through a ring of WNS stages
+// in LDS, copied with 4-byte LDS-DMA loads (buffer_load_dword ... lds: lane
+// l's word lands at 4l of the instruction's 256 bytes), so no registers hold
+// the stages in flight; words past M, N or K read zero through the buffer
+// range (a word is all in or all out).  Stage rows of A and of B [N,K] are 64
+// k bytes, logical 16-byte chunk c of row r at physical chunk c ^ ((r >> 2) &
+// 3); B [K,N] is 64 k rows of 128 column bytes, chunk c of k row r at c ^ (r
+// & 7), read with the transposing ds_read_b64_tr_b8.  Either way a 16-lane
+// fragment read covers the 64 banks once.  Lane (g, r) of a fragment holds k
+// bytes 16g .. 16g + 15 of row (column) r: INT8 multiplies them with
+// v_mfma_i32_16x16x64_i8 (exact int32 sums); FP8 with
+// v_mfma_scale_f32_16x16x128_f8f6f4, each lane's 32-byte operand being its
+// 16 bytes and 16 zero bytes in A and B alike (half the MFMA's k slots hold
+// zeros; the kernel is bound by its copies, not its MFMAs).  FP8 codes 0x7F
+// / 0xFF (NaN to the MFMA, 0.0 to the reference) make a sum NaN; the
+// workgroup then runs its K loop again with them cleared.  The epilogue is
+// the generic kernel's.
 // ===========================================================================
-constexpr int WT = 128;                   // tile edge
-constexpr int WKC = 64;                   // K bytes per stage
-constexpr int WNS = 4;                    // ring stages (64 KiB of LDS)
-constexpr int WOP = WT * WKC;             // bytes of one operand's stage (8 KiB)
-constexpr int WCP = WOP / (4 * 256);      // 4-byte copies per wave, operand and stage (8)
+constexpr int WT = 128;               // tile edge
+constexpr int WKC = 64;               // K bytes per stage
+constexpr int WNS = 4;                // ring stages (64 KiB of LDS)
+constexpr int WOP = WT * WKC;         // bytes of one operand's stage (8 KiB)
+constexpr int WCP = WOP / (4 * 256);  // 4-byte copies per wave, operand and stage (8)
 static_assert(WCP == 8 && WNS == 4, "copy and wait counts below");
 
+typedef int w2i __attribute__((ext_vector_type(2)));
 typedef int w4i __attribute__((ext_vector_type(4)));
+typedef int w8i __attribute__((ext_vector_type(8)));
+typedef float w4f __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) uint8_t w_lds;
 
-// Physical chunk of a stage row r is logical chunk ^ w_swz(r).
-__device__ __forceinline__ int w_swz(int r) { return (r >> 2) & 3; }
 __device__ __forceinline__ w4i w_rd128(const w_lds* a) {
     w4i r;
     asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(a));
     return r;
 }
+__device__ __forceinline__ w2i w_rdtr(const w_lds* a) {
+    w2i r;
+    asm volatile("ds_read_b64_tr_b8 %0, %1" : "=v"(r) : "v"(a));
+    return r;
+}
 
-template <int OUT>
-__global__ __launch_bounds__(256) void gemm_i8_words_kernel(GemmArgs p) {
+template <int EL, int BL, int OUT>
+__global__ __launch_bounds__(256) void gemm_words_kernel(GemmArgs p) {
+    constexpr bool F8 = EL == ELEM_F8, KN = BL == FKE_B_KN;
+    using Acc = typename std::conditional<F8, w4f, w4i>::type;
     __shared__ __attribute__((aligned(1024))) uint8_t ring[WNS][2][WOP];
+    __shared__ int nan_seen;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
     const int M = p.M, N = p.N, K = p.K;
     const int m0 = blockIdx.y * WT, n0 = blockIdx.x * WT;
     const int nst = (K + WKC - 1) / WKC;
+    if constexpr (F8) {
+        if (tid == 0) nan_seen = 0;
+        __syncthreads();  // before any wave can set it (no copy is in flight yet)
+    }
 
-    // Copy i of wave w (each operand): stage bytes 256 (8w + i) + 4l = tile
-    // row r = 4 (8w + i) + l / 16, physical chunk (l % 16) / 4, word l % 4,
-    // which holds logical chunk ((l % 16) / 4) ^ w_swz(r), w_swz(r) = i & 3.
-    // Offsets are 32-bit (M K and N K below 2^31); bit 31 set reads zero.
+    // Copy i of wave w, 64-byte rows (A; B [N,K]): stage bytes 256 (8w + i) +
+    // 4l = row r = 4 (8w + i) + l / 16, physical chunk (l % 16) / 4, word
+    // l % 4, holding logical chunk ((l % 16) / 4) ^ (i & 3).  B [K,N]: stage
+    // bytes 256 (8w + i) + 4l = k row kr = 2 (8w + i) + l / 32, physical chunk
+    // (l % 32) / 4, word l % 4, holding logical chunk ((l % 32) / 4) ^ (kr &
+    // 7).  Offsets are 32-bit (M K and N K below 2^31); bit 31 set reads zero.
     const int lr = lane >> 4, pc = (lane & 15) >> 2, dw = lane & 3;
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, M * K);
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.B, N * K);
     uint32_t arow[WCP], brow[WCP];
+    int bkr[WCP];
 #pragma unroll
     for (int i = 0; i < WCP; ++i) {
         const int r = 4 * (WCP * wave + i) + lr;
         arow[i] = m0 + r < M ? static_cast<uint32_t>((m0 + r) * K) : 0x80000000u;
-        brow[i] = n0 + r < N ? static_cast<uint32_t>((n0 + r) * K) : 0x80000000u;
+        if constexpr (KN) {
+            const int kr = 2 * (WCP * wave + i) + (lane >> 5);
+            const int col = n0 + 16 * (((lane & 31) >> 2) ^ (kr & 7)) + 4 * dw;
+            bkr[i] = kr;
+            brow[i] = col < N ? static_cast<uint32_t>(col) : 0x80000000u;
+        } else {
+            bkr[i] = 0;
+            brow[i] = n0 + r < N ? static_cast<uint32_t>((n0 + r) * K) : 0x80000000u;
+        }
     }
-    int kof[4];  // byte of the stage this lane copies, for copies with i % 4 == j
+    int kof[4];  // byte of the stage this lane copies (64-byte rows), for copies with i % 4 == j
 #pragma unroll
     for (int j = 0; j < 4; ++j) kof[j] = 16 * (pc ^ j) + 4 * dw;
     auto issue = [&](int s) __attribute__((always_inline)) {
@@ -269,58 +304,129 @@ __global__ __launch_bounds__(256) void gemm_i8_words_kernel(GemmArgs p) {
 #pragma unroll
         for (int i = 0; i < WCP; ++i) {
             const int kb = k0 + kof[i & 3];
-            const bool in = kb < K;
             const int dst = (WCP * wave + i) * 256;
-            dma4(ra, in ? arow[i] + static_cast<uint32_t>(kb) : 0x80000000u, 0, &ring[slot][0][dst]);
-            dma4(rb, in ? brow[i] + static_cast<uint32_t>(kb) : 0x80000000u, 0, &ring[slot][1][dst]);
+            dma4(ra, kb < K ? arow[i] + static_cast<uint32_t>(kb) : 0x80000000u, 0, &ring[slot][0][dst]);
+            if constexpr (KN) {
+                const int k = k0 + bkr[i];
+                dma4(rb, k < K ? brow[i] + static_cast<uint32_t>(k * N) : 0x80000000u, 0, &ring[slot][1][dst]);
+            } else {
+                dma4(rb, kb < K ? brow[i] + static_cast<uint32_t>(kb) : 0x80000000u, 0, &ring[slot][1][dst]);
+            }
         }
     };
 
-    // Fragment reads: lane (g, r) = (lane / 16, lane % 16) reads logical
-    // chunk g of row 16 x + r of the wave's 64 rows.
+    // Fragment reads: lane (g, rr) = (lane / 16, lane % 16); A and B [N,K]:
+    // logical chunk g of row 16 x + rr of the wave's 64 rows.  B [K,N]: two
+    // transposing reads, k rows 16g + 8t + b (b = rr / 2) at the 8-byte half
+    // rr % 2 of the wave's column block x.
     const int g = lane >> 4, rr = lane & 15;
-    uint32_t fa[4], fb[4];
+    uint32_t fa[4], fb[4][2];
 #pragma unroll
     for (int x = 0; x < 4; ++x) {
-        const int ra_ = wm * 64 + 16 * x + rr, rb_ = wn * 64 + 16 * x + rr;
-        fa[x] = static_cast<uint32_t>(ra_ * WKC + 16 * (g ^ w_swz(ra_)));
-        fb[x] = static_cast<uint32_t>(WOP + rb_ * WKC + 16 * (g ^ w_swz(rb_)));
+        const int ar = wm * 64 + 16 * x + rr;
+        fa[x] = static_cast<uint32_t>(ar * WKC + 16 * (g ^ ((ar >> 2) & 3)));
+        if constexpr (KN) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const int kr = 16 * g + 8 * t + (rr >> 1);
+                fb[x][t] = static_cast<uint32_t>(WOP + kr * WT + 16 * ((4 * wn + x) ^ (kr & 7)) + 8 * (rr & 1));
+            }
+        } else {
+            const int br = wn * 64 + 16 * x + rr;
+            fb[x][0] = fb[x][1] = static_cast<uint32_t>(WOP + br * WKC + 16 * (g ^ ((br >> 2) & 3)));
+        }
     }
     const w_lds* const lring = (const w_lds*)(&ring[0][0][0]);
 
-    w4i acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = w4i{0, 0, 0, 0};
-
-#pragma unroll
-    for (int s = 0; s < WNS - 1; ++s)
-        if (s < nst) issue(s);
-    for (int s = 0; s < nst; ++s) {
-        // Stage s has landed once at most the copies of the stages issued
-        // after it (s + 1 .. s + WNS - 2, those below nst) are in flight; the
-        // barrier then also says that every wave is done with stage s - 1,
-        // whose slot takes stage s + WNS - 1.
-        const int later = min(nst - 1 - s, WNS - 2);
-        if (later == 0) wait_vm<0>();
-        else if (later == 1) wait_vm<2 * WCP>();
-        else wait_vm<4 * WCP>();
-        barrier();
-        if (s + WNS - 1 < nst) issue(s + WNS - 1);
-        const w_lds* st = lring + (s % WNS) * 2 * WOP;
-        w4i af[4], bf[4];
-#pragma unroll
-        for (int x = 0; x < 4; ++x) af[x] = w_rd128(st + fa[x]);
-#pragma unroll
-        for (int x = 0; x < 4; ++x) bf[x] = w_rd128(st + fb[x]);
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-        for (int x = 0; x < 4; ++x) asm volatile("" : "+v"(af[x]), "+v"(bf[x]));
+    Acc acc[4][4];
+    auto k_loop = [&](auto sanc) __attribute__((always_inline)) {
+        constexpr bool SAN = decltype(sanc)::value;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+            for (int j = 0; j < 4; ++j) acc[i][j] = Acc{0, 0, 0, 0};
+#pragma unroll
+        for (int s = 0; s < WNS - 1; ++s)
+            if (s < nst) issue(s);
+        for (int s = 0; s < nst; ++s) {
+            // Stage s has landed once at most the copies of the stages issued
+            // after it (s + 1 .. s + WNS - 2, those below nst) are in flight;
+            // the barrier then also says that every wave is done with stage
+            // s - 1, whose slot takes stage s + WNS - 1.
+            const int later = min(nst - 1 - s, WNS - 2);
+            if (later == 0) wait_vm<0>();
+            else if (later == 1) wait_vm<2 * WCP>();
+            else wait_vm<4 * WCP>();
+            barrier();
+            if (s + WNS - 1 < nst) issue(s + WNS - 1);
+            const w_lds* st = lring + (s % WNS) * 2 * WOP;
+            w4i af[4], bf[4];
+#pragma unroll
+            for (int x = 0; x < 4; ++x) af[x] = w_rd128(st + fa[x]);
+            if constexpr (KN) {
+                w2i t0[4], t1[4];
+#pragma unroll
+                for (int x = 0; x < 4; ++x) {
+                    t0[x] = w_rdtr(st + fb[x][0]);
+                    t1[x] = w_rdtr(st + fb[x][1]);
+                }
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+                for (int x = 0; x < 4; ++x) {
+                    asm volatile("" : "+v"(af[x]), "+v"(t0[x]), "+v"(t1[x]));
+                    bf[x] = w4i{t0[x][0], t0[x][1], t1[x][0], t1[x][1]};
+                }
+            } else {
+#pragma unroll
+                for (int x = 0; x < 4; ++x) bf[x] = w_rd128(st + fb[x][0]);
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+                for (int x = 0; x < 4; ++x) asm volatile("" : "+v"(af[x]), "+v"(bf[x]));
+            }
+            if constexpr (F8) {
+                if constexpr (SAN) {
+#pragma unroll
+                    for (int x = 0; x < 4; ++x)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            af[x][e] = static_cast<int>(e4m3_sanitize(static_cast<uint32_t>(af[x][e])));
+                            bf[x][e] = static_cast<int>(e4m3_sanitize(static_cast<uint32_t>(bf[x][e])));
+                        }
+                }
+                const w4i z = {0, 0, 0, 0};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const w8i a8 = __builtin_shufflevector(af[i], z, 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                            a8, __builtin_shufflevector(bf[j], z, 0, 1, 2, 3, 4, 5, 6, 7), acc[i][j], 0, 0, 0, 0, 0, 0);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+            }
+        }
+    };
+    k_loop(std::false_type{});
+    if constexpr (F8) {
+        // Every product of finite codes is finite and no sum of them
+        // overflows fp32, so a NaN sum proves a NaN code; the workgroup
+        // decides together (the K loop has barriers), after every wave is
+        // done with the ring.
+        bool bad = false;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) bad |= __builtin_isnan(acc[i][j][v]);
+        if (__builtin_amdgcn_ballot_w64(bad) != 0 && lane == 0) nan_seen = 1;
+        __syncthreads();
+        if (nan_seen) k_loop(std::true_type{});
     }
 
     // Lane (g, c) of block (i, j) holds rows 16i + 4g + v, column 16j + c of the wave's block.
@@ -335,33 +441,53 @@ __global__ __launch_bounds__(256) void gemm_i8_words_kernel(GemmArgs p) {
             for (int j = 0; j < 4; ++j) {
                 const int n = n0 + wn * 64 + 16 * j + rr;
                 if (n >= N) continue;
-                const int32_t s32 = acc[i][j][v];
+                // (FP8 calls carry no scale vectors: s = fp32(sa * sb))
                 const float s = sam * (p.scale_b ? p.scale_b[n] : p.sb);
-                store_out<OUT>(p.C, static_cast<size_t>(m) * N + n, epilogue_value(static_cast<float>(s32), s, p.bias, n),
-                               s32);
+                if constexpr (F8) {
+                    store_out<OUT>(p.C, static_cast<size_t>(m) * N + n, epilogue_value(acc[i][j][v], s, p.bias, n), 0);
+                } else {
+                    const int32_t s32 = acc[i][j][v];
+                    store_out<OUT>(p.C, static_cast<size_t>(m) * N + n,
+                                   epilogue_value(static_cast<float>(s32), s, p.bias, n), s32);
+                }
             }
         }
 }
 
 }  // namespace
 
-bool words_supports(const GemmArgs& p) {
+bool words_supports(const GemmArgs& p, int elem) {
     const uintptr_t a = reinterpret_cast<uintptr_t>(p.A), b = reinterpret_cast<uintptr_t>(p.B);
-    if (p.M < 1 || p.N < 1 || p.K < 4 || p.K % 4 != 0 || p.swiglu || p.b_layout != FKE_B_NK) return false;
+    if (elem != ELEM_I8 && elem != ELEM_F8) return false;
+    if (elem == ELEM_F8 && p.out_dtype == FKE_OUT_I32) return false;
+    if (p.M < 1 || p.N < 1 || p.K < 4 || p.K % 4 != 0 || p.swiglu) return false;
+    if (p.b_layout != FKE_B_NK && (p.b_layout != FKE_B_KN || p.N % 4 != 0)) return false;
     if ((a | b) & 3) return false;
     if ((static_cast<int64_t>(p.M) + WT - 1) / WT > 65535) return false;  // grid y
     // 32-bit buffer offsets
     return static_cast<int64_t>(p.M) * p.K <= INT32_MAX && static_cast<int64_t>(p.N) * p.K <= INT32_MAX;
 }
 
-hipError_t launch_words(const GemmArgs& p, hipStream_t s) {
-    if (!words_supports(p)) return hipErrorInvalidValue;
+namespace {
+template <int EL, int BL>
+const void* words_kernel(int out) {
+    if constexpr (EL == ELEM_I8)
+        if (out == FKE_OUT_I32) return reinterpret_cast<const void*>(&gemm_words_kernel<EL, BL, FKE_OUT_I32>);
+    return out == FKE_OUT_F32 ? reinterpret_cast<const void*>(&gemm_words_kernel<EL, BL, FKE_OUT_F32>)
+                              : reinterpret_cast<const void*>(&gemm_words_kernel<EL, BL, FKE_OUT_BF16>);
+}
+}  // namespace
+
+hipError_t launch_words(const GemmArgs& p, int elem, hipStream_t s) {
+    if (!words_supports(p, elem)) return hipErrorInvalidValue;
     GemmArgs a = p;
     void* args[] = {&a};
     const dim3 grid((p.N + WT - 1) / WT, (p.M + WT - 1) / WT);
-    const void* f = p.out_dtype == FKE_OUT_F32    ? reinterpret_cast<const void*>(&gemm_i8_words_kernel<FKE_OUT_F32>)
-                    : p.out_dtype == FKE_OUT_BF16 ? reinterpret_cast<const void*>(&gemm_i8_words_kernel<FKE_OUT_BF16>)
-                                                  : reinterpret_cast<const void*>(&gemm_i8_words_kernel<FKE_OUT_I32>);
+    const bool kn = p.b_layout == FKE_B_KN;
+    const void* f = elem == ELEM_I8 ? (kn ? words_kernel<ELEM_I8, FKE_B_KN>(p.out_dtype)
+                                          : words_kernel<ELEM_I8, FKE_B_NK>(p.out_dtype))
+                                    : (kn ? words_kernel<ELEM_F8, FKE_B_KN>(p.out_dtype)
+                                          : words_kernel<ELEM_F8, FKE_B_NK>(p.out_dtype));
     return hipLaunchKernel(f, grid, dim3(256), args, 0, s);
 }
 

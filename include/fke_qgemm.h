@@ -59,8 +59,8 @@ enum fke_path {
     FKE_PATH_AUTO = 0,    /* dispatcher's choice                                */
     FKE_PATH_GEMV = 1,    /* decode family, M<=512 (INT8, NK): weight streamed  */
     FKE_PATH_MFMA = 2,    /* LDS-staged MFMA GEMM (INT8 i32 / FP8 f32 acc); for */
-                          /* INT8 B [N,K] with K % 4 == 0 and 4-byte-aligned A/B */
-                          /* (not 16) the word kernel, also on the MFMA units   */
+                          /* K % 4 == 0, 4-byte-aligned A/B (B [K,N]: N % 4 ==  */
+                          /* 0) but not 16, the word kernel, also on the MFMAs  */
     FKE_PATH_GENERIC = 3, /* any-shape tiled fallback (exact reference order)   */
     FKE_PATH_GEMV_DOT = 4, /* decode, VALU dot products only (no MFMA): INT8,   */
                            /* B [N,K], M <= 16, K % 64 == 0 (fke_qgemm_i8*_on_path) */

@@ -317,10 +317,12 @@ def test_path_unavailable_for_shape_is_rejected():
     (4, 4096, 64, 1, _lib.PATH_GEMV),
     (4, 4104, 4096, 1, _lib.PATH_GEMV),      # B [K,N] with N % 16 != 0: the row kernel's 4-byte form
     (1, 4104, 4096, 1, _lib.PATH_GEMV),
-    (32, 4104, 4096, 1, _lib.PATH_GEMV),
+    (20, 4104, 4096, 1, _lib.PATH_GEMV),
+    (21, 4104, 4096, 1, _lib.PATH_MFMA),     # past 20 rows the word kernel
     (5, 14336, 4000, 1, _lib.PATH_MFMA),     # past 4 rows the MFMA GEMM where it can (K % 16 == 0, N % 16 == 0)
     (4, 14336, 4000, 1, _lib.PATH_GEMV),     # one row group: the 4-byte form
-    (33, 4104, 4096, 1, _lib.PATH_GENERIC),  # past 32 rows: no [K,N] decode, and the MFMA GEMM needs N % 16
+    (33, 4104, 4096, 1, _lib.PATH_MFMA),     # past 32 rows: the word kernel (N % 4 == 0, K % 4 == 0)
+    (33, 4102, 4096, 1, _lib.PATH_GENERIC),  # N % 4 != 0
     (1, 1002, 4096, 1, _lib.PATH_GENERIC),   # N % 4 != 0
     (17, 4096, 4096, 1, _lib.PATH_GEMV),
     (64, 64, 100, 0, _lib.PATH_MFMA),        # K % 16 != 0, K % 4 == 0: the word kernel (B [N,K])
@@ -330,7 +332,8 @@ def test_path_unavailable_for_shape_is_rejected():
     (8, 64, 104, 0, _lib.PATH_MFMA),         # K % 16 != 0: rows not 16-byte aligned, the word kernel
     (300, 520, 4104, 0, _lib.PATH_MFMA),
     (300, 520, 4106, 0, _lib.PATH_GENERIC),
-    (300, 520, 4104, 1, _lib.PATH_GENERIC),  # B [K,N] past 32 rows: no word kernel
+    (300, 520, 4104, 1, _lib.PATH_MFMA),     # B [K,N] past 32 rows: the word kernel too
+    (300, 522, 4104, 1, _lib.PATH_GENERIC),
     (300, 520, 4112, 0, _lib.PATH_MFMA),
 ])
 def test_dispatch_i8(M, N, K, layout, expect):
@@ -362,6 +365,9 @@ def test_dispatch_unaligned_pointer_falls_back():
     (16, 14336, 4000, 1, _lib.PATH_MFMA),     # past 4 rows the MFMA GEMM where it can
     (16, 14336, 4004, 1, _lib.PATH_GEMV),     # and the 4-byte form where it cannot
     (4, 14336, 4002, 1, _lib.PATH_GENERIC),   # K % 4 != 0
+    (64, 14336, 4100, 1, _lib.PATH_MFMA),     # past 32 rows, K % 16 != 0: the word kernel (both layouts)
+    (64, 14336, 4100, 0, _lib.PATH_MFMA),
+    (64, 14338, 4100, 1, _lib.PATH_GENERIC),  # N % 4 != 0 with B [K,N]
     (8192, 8192, 8192, 0, _lib.PATH_MFMA),
     (4, 14336, 1024, 0, _lib.PATH_MFMA),      # K < 2048
     (4, 300, 2112, 0, _lib.PATH_GEMV),        # K % 128 != 0: no MFMA GEMM

@@ -412,11 +412,12 @@ def dev_at(x, shift):
 # B [K,N] whose N or K is only a multiple of 4, or whose operands are only
 # 4-byte aligned: the row kernel's 4-byte form (one split when the plan gives
 # one, a ragged last 1024-column block, K not a multiple of 128; past one row,
-# workgroups of 2 or 4 activation rows, the last group part empty).
+# workgroups of 2 or 4 activation rows, the last group part empty; past 20
+# rows the word kernel takes these shapes).
 KN_DW_CASES = [(1, 1000, 4096, 0), (1, 14340, 4096, 0), (1, 4100, 4100, 0), (1, 2052, 100, 0), (1, 14336, 4000, 0),
                (1, 14336, 4096, 4), (1, 1024, 4, 4), (2, 14340, 4096, 0), (3, 4100, 4100, 4), (4, 1000, 4096, 0),
                (5, 2052, 100, 0), (8, 14336, 4096, 4), (16, 14340, 4096, 0), (17, 4100, 1028, 4),
-               (32, 14340, 4096, 0)]
+               (20, 14340, 4096, 0)]
 
 
 @pytest.mark.parametrize("M,N,K,shift", KN_DW_CASES)
@@ -1487,35 +1488,69 @@ def test_fp8_auto_dispatch_random_shapes(oracle, dev, M, N, K, layout, out):
     assert_fp8_close(got, ref, out, f"auto {M, N, K, layout}")
 
 
-# INT8 with B [N,K] whose K is a multiple of 4 but not of 16, or whose
-# operands are only 4-byte aligned: the word kernel (128x128 tiles on the
-# matrix cores, 4-byte loads), through the automatic path.
-WORDS_CASES = [(1, 14336, 4100, 0), (3, 1000, 68, 0), (64, 64, 100, 0), (129, 257, 4, 0), (300, 520, 4104, 0),
-               (256, 4096, 4096, 4), (200, 1030, 1028, 4), (1024, 1024, 4100, 0)]
+# INT8 and FP8 whose K (and N, for B [K,N]) is a multiple of 4 but not of 16,
+# or whose operands are only 4-byte aligned: the word kernel (128x128 tiles
+# on the matrix cores, 4-byte copies), through the automatic path.  B [K,N]
+# from 33 rows (below, the [K,N] decode's 4-byte form takes such shapes).
+WORDS_CASES = [(1, 14336, 4100, 0, "nk"), (3, 1000, 68, 0, "nk"), (64, 64, 100, 0, "nk"), (129, 257, 4, 0, "nk"),
+               (300, 520, 4104, 0, "nk"), (256, 4096, 4096, 4, "nk"), (200, 1030, 1028, 4, "nk"),
+               (1024, 1024, 4100, 0, "nk"), (33, 4100, 4100, 0, "kn"), (64, 64, 100, 0, "kn"),
+               (129, 260, 4, 0, "kn"), (300, 520, 4104, 0, "kn"), (256, 4096, 4096, 4, "kn"),
+               (200, 1028, 1028, 4, "kn"), (1024, 1024, 4100, 0, "kn")]
 
 
-@pytest.mark.parametrize("M,N,K,shift", WORDS_CASES)
-def test_words_kernel_bit_exact(oracle, dev, M, N, K, shift):
-    """Every output type bit-exact against the oracle, with A and B `shift`
-    bytes past 16-byte alignment; the call goes to FKE_PATH_MFMA."""
-    say("int8 word kernel", M, N, K, shift)
+def _words_path(L, M, N, K, shift, layout, f8=False):
+    sel = L.fke_select_path_f8 if f8 else L.fke_select_path_i8
+    return sel(4096 + shift, 4096 + shift, 4096, M, N, K, _lib.OUT_BF16, _lib.B_KN if layout == "kn" else _lib.B_NK)
+
+
+@pytest.mark.parametrize("M,N,K,shift,layout", WORDS_CASES)
+def test_words_kernel_bit_exact(oracle, dev, M, N, K, shift, layout):
+    """INT8: every output type bit-exact against the oracle, with A and B
+    `shift` bytes past 16-byte alignment; the call goes to FKE_PATH_MFMA."""
+    say("int8 word kernel", M, N, K, shift, layout)
     L = _lib.lib()
-    assert L.fke_select_path_i8(4096 + shift, 4096 + shift, 4096, M, N, K, _lib.OUT_BF16, _lib.B_NK) == _lib.PATH_MFMA
-    A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 9900 + 7 * M + N + K, layout="nk", act="normal")
-    acc = oracle.w8a8_acc(A, B, oracle.B_NK, nthreads=NTH)
+    assert _words_path(L, M, N, K, shift, layout) == _lib.PATH_MFMA
+    bl, obl = (_lib.B_KN, oracle.B_KN) if layout == "kn" else (_lib.B_NK, oracle.B_NK)
+    A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 9900 + 7 * M + N + K, layout=layout, act="normal")
+    acc = oracle.w8a8_acc(A, B, obl, nthreads=NTH)
     (ba, pa), (bb, pb) = dev_at(A, shift), dev_at(B, shift)
     dsa, dsb, dbias = dev_t(sa), dev_t(sb), dev_t(bias)
     for out in ("i32", "f32", "bf16"):
         C = torch.empty((M, N), dtype=OUT_T[out], device=dev)
         _lib.check(L.fke_qgemm_i8(pa, pb, C.data_ptr(), M, N, K, dsa.data_ptr(), dsb.data_ptr(), 1.0, 1.0,
                                   dbias.data_ptr(), {"f32": _lib.OUT_F32, "bf16": _lib.OUT_BF16, "i32": _lib.OUT_I32}[out],
-                                  _lib.B_NK, torch.cuda.current_stream().cuda_stream), "fke_qgemm_i8")
+                                  bl, torch.cuda.current_stream().cuda_stream), "fke_qgemm_i8")
         torch.cuda.synchronize()
         want = acc if out == "i32" else oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, out)
-        assert_same(host(C), want, f"words {out} M={M} N={N} K={K} shift={shift}")
+        assert_same(host(C), want, f"words {out} M={M} N={N} K={K} shift={shift} {layout}")
     # scalar scales and no bias (the reference launcher's form)
     C = torch.empty((M, N), dtype=torch.float32, device=dev)
-    _lib.check(L.fke_qgemm_i8(pa, pb, C.data_ptr(), M, N, K, None, None, 0.05, 0.02, None, _lib.OUT_F32, _lib.B_NK,
+    _lib.check(L.fke_qgemm_i8(pa, pb, C.data_ptr(), M, N, K, None, None, 0.05, 0.02, None, _lib.OUT_F32, bl,
                               torch.cuda.current_stream().cuda_stream), "fke_qgemm_i8")
     torch.cuda.synchronize()
-    assert_same(host(C), oracle_out(oracle, acc, None, None, 0.05, 0.02, None, "f32"), f"words scalar M={M}")
+    assert_same(host(C), oracle_out(oracle, acc, None, None, 0.05, 0.02, None, "f32"), f"words scalar M={M} {layout}")
+
+
+@pytest.mark.parametrize("nan_codes", [False, True])
+@pytest.mark.parametrize("M,N,K,shift,layout", WORDS_CASES)
+def test_words_kernel_fp8(oracle, dev, M, N, K, shift, layout, nan_codes):
+    """FP8 within the bounds of the sequential fp32 sum (codes 0x7F / 0xFF
+    counted as 0.0: the workgroup's replay), bf16 and fp32 out with bias."""
+    say("fp8 word kernel", M, N, K, shift, layout, nan_codes)
+    L = _lib.lib()
+    assert _words_path(L, M, N, K, shift, layout, f8=True) == _lib.PATH_MFMA
+    bl, obl = (_lib.B_KN, oracle.B_KN) if layout == "kn" else (_lib.B_NK, oracle.B_NK)
+    A8, B8, fa, fb = f8_inputs(oracle, M, N, K, 9950 + 7 * M + N + K, layout, with_nan_codes=nan_codes)
+    bias = oracle.gen_f32_normal((N,), 9951 + M + N, 0.0, 0.02)
+    (ba, pa), (bb, pb) = dev_at(A8, shift), dev_at(B8, shift)
+    dbias = dev_t(bias)
+    ref = oracle.f8_gemm(A8, B8, fa, fb, bias=bias, b_layout=obl, nthreads=NTH)
+    for out in ("f32", "bf16"):
+        C = torch.empty((M, N), dtype=OUT_T[out], device=dev)
+        _lib.check(L.fke_qgemm_f8(pa, pb, C.data_ptr(), M, N, K, fa, fb, dbias.data_ptr(),
+                                  _lib.OUT_F32 if out == "f32" else _lib.OUT_BF16, bl,
+                                  torch.cuda.current_stream().cuda_stream), "fke_qgemm_f8")
+        torch.cuda.synchronize()
+        got = host(C) if out == "f32" else oracle.bf16_to_f32(host(C))
+        assert_fp8_close(got, ref, out, f"words fp8 M={M} N={N} K={K} shift={shift} {layout} nan={nan_codes}")
