@@ -187,9 +187,13 @@ constexpr int ROWS_NB = 1;
 // sum of finite E4M3 products overflows fp32, so a NaN total proves such a
 // code in the row or in the activations) and a wave whose total comes out NaN
 // streams its row again with those codes cleared.
-template <int MT, int OUT, bool FULLK, int NB, bool SWI = false, int EL = ELEM_I8>
+// DW: 4-byte loads (K % 4 == 0, 4-byte-aligned operands: the shapes the
+// 16-byte loads cannot take), 1024 words (4 KiB) of the row per block, 16 per
+// lane, lane l taking words l, l + 64, ...; each word is all in K or all out.
+template <int MT, int OUT, bool FULLK, int NB, bool SWI = false, int EL = ELEM_I8, bool DW = false>
 __global__ __launch_bounds__(ROWS_WAVES * 64) void gemv_rows_kernel(GemmArgs p) {
     constexpr bool F8 = EL == ELEM_F8;
+    static_assert(!DW || !FULLK, "4-byte loads: K is not a multiple of 4096 bytes of 16-byte chunks");
     static_assert(!SWI || NB == 2, "SwiGLU streams one gate and one up row");
     static_assert(MT * NB <= 64, "one storing lane per output");
     static_assert(!F8 || (MT == 1 && NB == 1 && !SWI && OUT != FKE_OUT_I32), "FP8: M = 1, fp32 or bf16 out");
@@ -204,7 +208,7 @@ __global__ __launch_bounds__(ROWS_WAVES * 64) void gemv_rows_kernel(GemmArgs p) 
     const int n = min(nw, NU - 1);
     auto row_of = [&](int q) __attribute__((always_inline)) { return SWI ? n + q * NO : min(n * NB + q, p.N - 1); };
     const int M = p.M, K = p.K;
-    const int ck = K >> 4;  // 16-byte chunks per row (K % 64 == 0)
+    const int ck = DW ? K >> 2 : K >> 4;  // 4-byte words / 16-byte chunks per row
     // B row n and the M activation rows through buffer resources: 32-bit
     // offsets, the weight stream non-temporal (read once, never re-used),
     // and chunks past the row end pointed at offset 2^31, which lies outside
@@ -222,7 +226,8 @@ __global__ __launch_bounds__(ROWS_WAVES * 64) void gemv_rows_kernel(GemmArgs p) 
         ra[m] = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<int8_t*>(static_cast<const int8_t*>(p.A) + static_cast<size_t>(m < M ? m : 0) * K), 0, K,
             0x00020000);
-    const int nblk = (ck + 255) >> 8;  // blocks of 256 chunks (4 KiB of the row), the last one partial; >= 1
+    // blocks of 4 KiB of the row (256 chunks, 1024 words), the last one partial; >= 1
+    const int nblk = DW ? (ck + 1023) >> 10 : (ck + 255) >> 8;
     // per-row epilogue operands: scalar loads (n is uniform) whose latency
     // hides behind the weight stream
     float sbn[NB], biasn[NB];
@@ -245,6 +250,52 @@ __global__ __launch_bounds__(ROWS_WAVES * 64) void gemv_rows_kernel(GemmArgs p) 
 #pragma unroll
         for (int m = 0; m < MT; ++m) acc[q][m] = Acc(0);
     int blk = 0;
+    if constexpr (DW) {
+    do {
+        int off[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int c = (blk << 10) + lane + 64 * u;
+            off[u] = c < ck ? c * 4 : static_cast<int>(0x80000000u);
+        }
+        int a[MT][16], b[NB][16];
+#pragma unroll
+        for (int q = 0; q < NB; ++q)
+#pragma unroll
+            for (int u = 0; u < 16; ++u)
+                b[q][u] = __builtin_bit_cast(int, __builtin_amdgcn_raw_buffer_load_b32(rb[q], off[u], 0, 2));
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int u = 0; u < 16; ++u)
+                a[m][u] = __builtin_bit_cast(int, __builtin_amdgcn_raw_buffer_load_b32(ra[m], off[u], 0, 0));
+        if constexpr (F8) {
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                uint32_t aw = static_cast<uint32_t>(a[0][u]), bw = static_cast<uint32_t>(b[0][u]);
+                if constexpr (clear) {
+                    aw = e4m3_sanitize(aw);
+                    bw = e4m3_sanitize(bw);
+                }
+                const v2f alo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(aw), false);
+                const v2f ahi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(aw), true);
+                const v2f blo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(bw), false);
+                const v2f bhi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(bw), true);
+                acc[0][0] = __builtin_fmaf(alo.x, blo.x, acc[0][0]);
+                acc[0][0] = __builtin_fmaf(alo.y, blo.y, acc[0][0]);
+                acc[0][0] = __builtin_fmaf(ahi.x, bhi.x, acc[0][0]);
+                acc[0][0] = __builtin_fmaf(ahi.y, bhi.y, acc[0][0]);
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < NB; ++q)
+#pragma unroll
+                for (int m = 0; m < MT; ++m)
+#pragma unroll
+                    for (int u = 0; u < 16; ++u) acc[q][m] = __builtin_amdgcn_sdot4(a[m][u], b[q][u], acc[q][m], false);
+        }
+    } while (++blk < nblk);
+    } else {
     do {
         int off[4];
 #pragma unroll
@@ -295,6 +346,7 @@ __global__ __launch_bounds__(ROWS_WAVES * 64) void gemv_rows_kernel(GemmArgs p) 
                     for (int u = 0; u < 4; ++u) acc[q][m] = dot16(a[m][u], b[q][u], acc[q][m]);
         }
     } while (++blk < nblk);
+    }
     };
     Acc tot[NB][MT];
     auto totals = [&]() __attribute__((always_inline)) {
@@ -961,7 +1013,7 @@ hipError_t launch_lds_f8(const GemmArgs& p, hipStream_t stream) {
     return hipLaunchKernel(f, dim3(lds_grid(p), rows), dim3(256), args, 0, stream);
 }
 
-template <int MT, bool FULLK, int NB = ROWS_NB>
+template <int MT, bool FULLK, int NB = ROWS_NB, bool DW = false>
 hipError_t launch_rows(const GemmArgs& p, hipStream_t stream) {
     GemmArgs a = p;
     void* args[] = {&a};
@@ -969,29 +1021,35 @@ hipError_t launch_rows(const GemmArgs& p, hipStream_t stream) {
     if (p.swiglu) {
         const dim3 grid((p.N / 2 + ROWS_WAVES - 1) / ROWS_WAVES);
         f = p.out_dtype == FKE_OUT_F32
-            ? reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_F32, FULLK, 2, true>)
-            : reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_BF16, FULLK, 2, true>);
+            ? reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_F32, FULLK, 2, true, ELEM_I8, DW>)
+            : reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_BF16, FULLK, 2, true, ELEM_I8, DW>);
         return hipLaunchKernel(f, grid, dim3(ROWS_WAVES * 64), args, 0, stream);
     }
     const int units = (p.N + NB - 1) / NB;
     const dim3 grid((units + ROWS_WAVES - 1) / ROWS_WAVES);
     switch (p.out_dtype) {
-        case FKE_OUT_F32: f = reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_F32, FULLK, NB>); break;
-        case FKE_OUT_BF16: f = reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_BF16, FULLK, NB>); break;
-        default: f = reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_I32, FULLK, NB>); break;
+        case FKE_OUT_F32:
+            f = reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_F32, FULLK, NB, false, ELEM_I8, DW>);
+            break;
+        case FKE_OUT_BF16:
+            f = reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_BF16, FULLK, NB, false, ELEM_I8, DW>);
+            break;
+        default:
+            f = reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_I32, FULLK, NB, false, ELEM_I8, DW>);
+            break;
     }
     return hipLaunchKernel(f, grid, dim3(ROWS_WAVES * 64), args, 0, stream);
 }
 
 // FP8 at M = 1: the row kernel on E4M3 codes (one weight row per wave).
-template <bool FULLK>
+template <bool FULLK, bool DW = false>
 hipError_t launch_rows_f8(const GemmArgs& p, hipStream_t stream) {
     GemmArgs a = p;
     void* args[] = {&a};
     const dim3 grid((p.N + ROWS_WAVES - 1) / ROWS_WAVES);
     const void* f = p.out_dtype == FKE_OUT_F32
-        ? reinterpret_cast<const void*>(&gemv_rows_kernel<1, FKE_OUT_F32, FULLK, 1, false, ELEM_F8>)
-        : reinterpret_cast<const void*>(&gemv_rows_kernel<1, FKE_OUT_BF16, FULLK, 1, false, ELEM_F8>);
+        ? reinterpret_cast<const void*>(&gemv_rows_kernel<1, FKE_OUT_F32, FULLK, 1, false, ELEM_F8, DW>)
+        : reinterpret_cast<const void*>(&gemv_rows_kernel<1, FKE_OUT_BF16, FULLK, 1, false, ELEM_F8, DW>);
     return hipLaunchKernel(f, grid, dim3(ROWS_WAVES * 64), args, 0, stream);
 }
 
@@ -1018,11 +1076,21 @@ bool skinny_offsets_fit(const GemmArgs& p) {
 // M = 2..4 (and SwiGLU up to 4): the row kernel with two weight rows per
 // wave, which reuses each activation chunk for both rows; measured 4-8 %
 // faster than the split-K kernel at N = 14336, K = 4096.
-template <bool FULLK>
+template <bool FULLK, bool DW = false>
 hipError_t launch_rows_m(const GemmArgs& p, hipStream_t s) {
-    if (p.M <= 1) return launch_rows<1, FULLK>(p, s);
-    if (p.M <= 2) return launch_rows<2, FULLK, 2>(p, s);
-    return launch_rows<4, FULLK, 2>(p, s);
+    if (p.M <= 1) return launch_rows<1, FULLK, ROWS_NB, DW>(p, s);
+    if (p.M <= 2) return launch_rows<2, FULLK, 2, DW>(p, s);
+    return launch_rows<4, FULLK, 2, DW>(p, s);
+}
+
+// The row kernel's 4-byte form: B [N,K], up to 4 rows, K % 4 == 0 and
+// 4-byte-aligned A / B where the 16-byte loads cannot run (K % 64 != 0 or
+// rows not 16-byte aligned).
+bool rows_dw_ok(const GemmArgs& p) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p.A), b = reinterpret_cast<uintptr_t>(p.B);
+    if (p.M < 1 || p.M > 4 || p.N < 1 || p.K < 4 || p.K % 4 != 0 || p.b_layout != FKE_B_NK) return false;
+    if ((a | b) & 3) return false;
+    return !(p.K % 64 == 0 && ((a | b) & 15) == 0);
 }
 
 }  // namespace
@@ -1045,6 +1113,10 @@ hipError_t launch_rows_m(const GemmArgs& p, hipStream_t s) {
 //    16.2 us on the 64x64 ring) and the MFMA GEMM takes M = 48..64 (16.2
 //    against 19.3) and M = 65..128 on the 128x64 ring (20.3 against 36.7).
 bool gemv_i8_batch_pays(const GemmArgs& p) {
+    // The row kernel's 4-byte form past one row loses to the MFMA GEMM where
+    // that GEMM can run (K % 16 == 0): 14336 x 4112, M = 4, 19.9 against
+    // 15.4 us (M = 1: 13.7 against 15.2).
+    if (p.M > 1 && rows_dw_ok(p)) return false;
     if (p.M <= 16 || p.M > FKE_GEMV_MAX_M) return p.M <= 16;
     const double kib = p.K / 1024.0;
     const int64_t g = lds_grid(p), no = p.swiglu ? p.N / 2 : p.N;
@@ -1064,6 +1136,7 @@ bool gemv_i8_batch_pays(const GemmArgs& p) {
 }
 
 bool gemv_i8_supports(const GemmArgs& p) {
+    if (rows_dw_ok(p)) return true;
     const uintptr_t a = reinterpret_cast<uintptr_t>(p.A), b = reinterpret_cast<uintptr_t>(p.B);
     if (!(p.M >= 1 && p.M <= FKE_GEMV_MAX_M && p.N >= 1 && p.K >= 64 && p.K % 64 == 0 &&
           p.b_layout == FKE_B_NK && ((a | b) & 15) == 0))
@@ -1096,6 +1169,7 @@ hipError_t launch_gemv_dot(const GemmArgs& p, hipStream_t s) {
 }
 
 hipError_t launch_gemv_i8(const GemmArgs& p, hipStream_t s) {
+    if (rows_dw_ok(p)) return launch_rows_m<false, true>(p, s);
     // M >= 3 with K >= 4 KiB: the LDS-streamed kernel (11.4-11.8 us at
     // N = 14336, K = 4096 for every M in 3..16, against 12.5-18.1 us for the
     // row and skinny kernels; SwiGLU 20.3-20.9 us against 21.5-34.3 us).  At
@@ -1126,12 +1200,14 @@ hipError_t launch_gemv_i8(const GemmArgs& p, hipStream_t s) {
 // 14336: 10.8 against 12.7), the LDS-streamed kernel on E4M3 codes above.
 bool gemv_f8_supports(const GemmArgs& p) {
     const uintptr_t a = reinterpret_cast<uintptr_t>(p.A), b = reinterpret_cast<uintptr_t>(p.B);
+    if (p.M == 1 && rows_dw_ok(p)) return !p.swiglu && (p.out_dtype == FKE_OUT_F32 || p.out_dtype == FKE_OUT_BF16);
     return p.M >= 1 && p.M <= FKE_GEMV_MAX_M && p.N >= 1 && p.K % 64 == 0 && p.b_layout == FKE_B_NK &&
            !p.swiglu && (p.out_dtype == FKE_OUT_F32 || p.out_dtype == FKE_OUT_BF16) && ((a | b) & 15) == 0 &&
            (p.M == 1 || lds_fits<512>(p));
 }
 
 hipError_t launch_gemv_f8(const GemmArgs& p, hipStream_t s) {
+    if (p.M == 1 && rows_dw_ok(p)) return launch_rows_f8<false, true>(p, s);
     if (p.M == 1) return p.K % 4096 == 0 ? launch_rows_f8<true>(p, s) : launch_rows_f8<false>(p, s);
     const bool big = lds_fits<1024>(p) && (pieces_even(p.K, 1024) || !pieces_even(p.K, 512));
     if (p.M > 32) return launch_lds_f8<512, 4, 4>(p, s);

@@ -70,7 +70,6 @@ constexpr int KS_CB = KS_W / 16;         // 16-column MFMA blocks per wave
 constexpr int KS_ROWS = 128;             // k rows per item
 constexpr int KS_BI = KS_ROWS * KS_W;    // weight bytes per item (16 KiB)
 constexpr int KS_AI = 16 * KS_ROWS;      // activation bytes per item and 16-row block (2 KiB)
-constexpr int KS_ITEM = KS_BI + KS_AI;   // 18 KiB (one activation block)
 constexpr int KS_DB = KS_BI / 1024;      // weight copies per item
 constexpr int KS_DA = KS_AI / 1024;      // activation copies per item and block
 constexpr int KS_NS = 2;                 // ring slots per wave (144 KiB of LDS per workgroup)

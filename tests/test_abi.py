@@ -328,6 +328,11 @@ def test_path_unavailable_for_shape_is_rejected():
     (64, 64, 100, 0, _lib.PATH_MFMA),        # K % 16 != 0, K % 4 == 0: the word kernel (B [N,K])
     (64, 64, 4, 0, _lib.PATH_MFMA),
     (64, 64, 102, 0, _lib.PATH_GENERIC),     # K % 4 != 0
+    (1, 14336, 4100, 0, _lib.PATH_GEMV),     # up to 4 rows: the [N,K] row kernel's 4-byte form
+    (1, 14336, 4112, 0, _lib.PATH_GEMV),     # (one row also where K % 16 == 0, K % 64 != 0)
+    (4, 14336, 4112, 0, _lib.PATH_MFMA),     # past one row the MFMA GEMM where it can run
+    (4, 14336, 4108, 0, _lib.PATH_GEMV),
+    (5, 14336, 4100, 0, _lib.PATH_MFMA),     # past 4 rows: the word kernel
     (8, 64, 96, 0, _lib.PATH_MFMA),          # K of 6 16-byte chunks: one partial stage
     (8, 64, 104, 0, _lib.PATH_MFMA),         # K % 16 != 0: rows not 16-byte aligned, the word kernel
     (300, 520, 4104, 0, _lib.PATH_MFMA),
@@ -366,6 +371,8 @@ def test_dispatch_unaligned_pointer_falls_back():
     (16, 14336, 4004, 1, _lib.PATH_GEMV),     # and the 4-byte form where it cannot
     (4, 14336, 4002, 1, _lib.PATH_GENERIC),   # K % 4 != 0
     (64, 14336, 4100, 1, _lib.PATH_MFMA),     # past 32 rows, K % 16 != 0: the word kernel (both layouts)
+    (1, 14336, 4100, 0, _lib.PATH_GEMV),      # one row, B [N,K]: the row kernel's 4-byte form
+    (2, 14336, 4100, 0, _lib.PATH_MFMA),
     (64, 14336, 4100, 0, _lib.PATH_MFMA),
     (64, 14338, 4100, 1, _lib.PATH_GENERIC),  # N % 4 != 0 with B [K,N]
     (8192, 8192, 8192, 0, _lib.PATH_MFMA),

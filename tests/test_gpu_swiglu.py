@@ -173,7 +173,7 @@ def swiglu_gemm_inputs(oracle, M, I, K, seed):
 CASES = [
     # (M, I, K, path)
     (1, 200, 4096, "gemv"), (1, 130, 192, "gemv"), (2, 77, 320, "gemv"), (3, 64, 4096, "gemv"),
-    (4, 33, 128, "gemv"), (5, 100, 256, "gemv"), (9, 300, 1024, "gemv"), (16, 47, 4096, "gemv"),
+    (4, 33, 128, "gemv"), (2, 77, 100, "gemv"), (4, 50, 68, "gemv"), (5, 100, 256, "gemv"), (9, 300, 1024, "gemv"), (16, 47, 4096, "gemv"),
     (17, 130, 2048, "gemv"), (40, 300, 4096, "gemv"), (64, 100, 2048, "gemv"), (100, 77, 4096, "gemv"),
     (200, 513, 2048, "gemv"),
     (17, 130, 256, "mfma"), (300, 200, 512, "mfma"), (256, 128, 128, "mfma"), (513, 333, 384, "mfma"),
