@@ -863,7 +863,7 @@ def odd_k_configs(torch, L, _lib, dev, timed, rand_i8, rand_u, args):
             res[f"prefill_{M}x{N}x{K}_bf16_{name}"] = {
                 "ms": round(ms, 4), "TOPS": round(t, 1), "frac": round(t / PEAK_INT8_TOPS, 4),
                 "kernel": {"mfma": "gemm_mfma_kernel<i8,NK,bf16> (partial last stage)",
-                           "words": "gemm_i8_words_kernel<bf16> (4-byte loads, K % 4 == 0)",
+                           "words": "gemm_words_kernel<i8,NK,bf16> (4-byte LDS-DMA copies, K % 4 == 0)",
                            "generic": "gemm_generic_kernel<i8>"}[name]}
         del A, B, C
     return res
