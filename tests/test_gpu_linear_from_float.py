@@ -65,7 +65,7 @@ def weights(oracle, N, K, seed):
 
 
 @pytest.mark.parametrize("M", [1, 2, 3, 4])
-@pytest.mark.parametrize("K", [4096, 8192, 4160, 64])
+@pytest.mark.parametrize("K", [4096, 8192, 4160, 64, 100, 4100])
 @pytest.mark.parametrize("xdt", ["f32", "bf16"])
 def test_decode_linear_from_float(oracle, dev, M, K, xdt):
     N = 333
@@ -83,6 +83,24 @@ def test_decode_linear_from_float(oracle, dev, M, K, xdt):
             torch.cuda.synchronize()
             same(host(y), ref, f"one call vs oracle M={M} K={K} {xdt}->{out} bias={b is not None}")
             same(host(y), host(y2), f"one call vs separate calls M={M} K={K} {xdt}->{out}")
+
+
+@pytest.mark.parametrize("M,K", [(40, 100), (300, 4100)])
+def test_linear_odd_k(oracle, dev, M, K):
+    """K a multiple of 4 only: the codes' rows are 4-byte aligned and the GEMM
+    is the word kernel; bit-exact against the oracle and the separate calls."""
+    N = 520
+    say("linear, odd K", M, K)
+    x = activations(M, K, 500 + M + K, "f32")
+    W, sb, bias = weights(oracle, N, K, 13 + K)
+    assert _lib.lib().fke_select_path_i8(4096, 4096, 4096, M, N, K, _lib.OUT_F32, _lib.B_NK) == _lib.PATH_MFMA
+    y = ops.w8a8_linear(x, dev_t(W), dev_t(sb), dev_t(bias), out_dtype=torch.float32)
+    q2, s2 = ops.quantize_per_token(x)
+    y2 = ops.w8a8_gemm(q2, dev_t(W), s2, dev_t(sb), dev_t(bias), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    q, s = oracle.quantize_rows_i8(host_bits(x), oracle.IN_F32)
+    same(host(y), oracle.w8a8_gemm(q, W, s, sb, bias=bias), f"odd K M={M} K={K} vs oracle")
+    same(host(y), host(y2), f"odd K M={M} K={K} vs separate calls")
 
 
 @pytest.mark.parametrize("M", [5, 17, 300])
