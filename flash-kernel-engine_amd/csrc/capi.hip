@@ -23,12 +23,19 @@
 static __device__ __align__(256) uint8_t scratch[FKE_W8A8_NOALLOC_SCRATCH_BYTES];
 
 // Partial sums of the K splits (the [K,N] decode's and the MFMA GEMM's),
-// FKE_SPLIT_SLOTS slots of FKE_SPLIT_SLOT_BYTES per GPU, reserved with the
-// code object: no call path allocates device memory.  A stream gets a slot
-// the first time one of its calls splits K and keeps it for the life of the
-// process: calls on one stream run in order and share it, calls on different
-// streams never do.  No split plan needs more than one slot.
+// FKE_SPLIT_SLOTS slots of FKE_SPLIT_SLOT_BYTES per GPU, then
+// FKE_SPLIT_SMALL_SLOTS of FKE_SPLIT_SMALL_SLOT_BYTES, reserved with the code
+// object: no call path allocates device memory.  A stream gets a slot the
+// first time one of its calls splits K (a large one while any is free) and
+// keeps it for the life of the process: calls on one stream run in order and
+// share it, calls on different streams never do.  No split plan needs more
+// than one large slot; plans adapt to a small one (the [K,N] decode with
+// fewer splits, the MFMA GEMM unsplit where its plan does not fit).  The
+// small slots keep the splits for the many streams a framework may cycle
+// through (torch's pool holds 32 per device and priority) at 2 MiB each: the
+// [K,N] decode at N = 14336, K = 4096 needs 0.9 / 1.75 MiB at M = 1 / 16.
 static __device__ __align__(256) uint8_t split_pool[size_t{FKE_SPLIT_SLOTS} * FKE_SPLIT_SLOT_BYTES];
+static __device__ __align__(256) uint8_t split_pool_small[size_t{FKE_SPLIT_SMALL_SLOTS} * FKE_SPLIT_SMALL_SLOT_BYTES];
 
 namespace {
 
@@ -45,6 +52,7 @@ struct DeviceSetup {
     hipError_t status = hipSuccess;
     uint8_t* scratch = nullptr;
     uint8_t* pool = nullptr;
+    uint8_t* pool_small = nullptr;
     hipEvent_t noalloc_done = nullptr;
 };
 DeviceSetup g_dev[kMaxDevices];
@@ -55,11 +63,14 @@ hipError_t device_setup(int dev, DeviceSetup** out) {
     std::call_once(d.once, [&d] {
         void* a = nullptr;
         void* b = nullptr;
+        void* c = nullptr;
         d.status = hipGetSymbolAddress(&a, HIP_SYMBOL(scratch));
         if (d.status == hipSuccess) d.status = hipGetSymbolAddress(&b, HIP_SYMBOL(split_pool));
+        if (d.status == hipSuccess) d.status = hipGetSymbolAddress(&c, HIP_SYMBOL(split_pool_small));
         if (d.status == hipSuccess) d.status = hipEventCreateWithFlags(&d.noalloc_done, hipEventDisableTiming);
         d.scratch = static_cast<uint8_t*>(a);
         d.pool = static_cast<uint8_t*>(b);
+        d.pool_small = static_cast<uint8_t*>(c);
     });
     if (d.status != hipSuccess) return d.status;
     *out = &d;
@@ -86,9 +97,11 @@ struct Workspace {
     size_t bytes = 0;
 };
 
-// Slot table of split_pool: slot i of device d belongs to g_slot_stream[d][i].
+// Slot table of the split pool: slot i of device d (split_pool for i <
+// FKE_SPLIT_SLOTS, split_pool_small after) belongs to g_slot_stream[d][i].
 std::mutex g_slot_mu;
-hipStream_t g_slot_stream[kMaxDevices][FKE_SPLIT_SLOTS];
+constexpr int kSlots = FKE_SPLIT_SLOTS + FKE_SPLIT_SMALL_SLOTS;
+hipStream_t g_slot_stream[kMaxDevices][kSlots];
 int g_slot_count[kMaxDevices];
 
 // The pool slot of stream `s` on the current device, assigned on first use.
@@ -105,13 +118,18 @@ Workspace stream_slot(hipStream_t s) {
     int i = 0;
     while (i < g_slot_count[dev] && g_slot_stream[dev][i] != s) ++i;
     if (i == g_slot_count[dev]) {
-        if (i == FKE_SPLIT_SLOTS) return {};
+        if (i == kSlots) return {};
         g_slot_stream[dev][i] = s;
         g_slot_count[dev] = i + 1;
     }
     Workspace w;
-    w.ptr = d->pool + static_cast<size_t>(i) * FKE_SPLIT_SLOT_BYTES;
-    w.bytes = FKE_SPLIT_SLOT_BYTES;
+    if (i < FKE_SPLIT_SLOTS) {
+        w.ptr = d->pool + static_cast<size_t>(i) * FKE_SPLIT_SLOT_BYTES;
+        w.bytes = FKE_SPLIT_SLOT_BYTES;
+    } else {
+        w.ptr = d->pool_small + static_cast<size_t>(i - FKE_SPLIT_SLOTS) * FKE_SPLIT_SMALL_SLOT_BYTES;
+        w.bytes = FKE_SPLIT_SMALL_SLOT_BYTES;
+    }
     return w;
 }
 

@@ -22,6 +22,7 @@ IN_F32, IN_BF16, IN_F16 = 0, 1, 2
 HIP_SUCCESS, HIP_ERROR_INVALID_VALUE = 0, 1
 W8A8_NOALLOC_SCRATCH_BYTES = 32 << 20  # FKE_W8A8_NOALLOC_SCRATCH_BYTES
 SPLIT_SLOTS, SPLIT_SLOT_BYTES = 16, 16 << 20  # FKE_SPLIT_SLOTS, FKE_SPLIT_SLOT_BYTES
+SPLIT_SMALL_SLOTS, SPLIT_SMALL_SLOT_BYTES = 48, 2 << 20  # FKE_SPLIT_SMALL_SLOTS, FKE_SPLIT_SMALL_SLOT_BYTES
 
 # Every exported symbol with its (argtypes, restype).
 _p, _i, _f = ct.c_void_p, ct.c_int, ct.c_float

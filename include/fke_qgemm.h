@@ -156,8 +156,10 @@ int fke_qgemm_f8_on_path(int path, const uint8_t* A, const uint8_t* B, void* C,
  * stream's slot of the library's split pool: a stream is given one of the
  * FKE_SPLIT_SLOTS slots of its GPU on its first split call (also while it
  * is being captured into a graph, whose kernels then keep that slot's
- * address) and keeps it; past FKE_SPLIT_SLOTS streams on one GPU, and on
- * hipStreamPerThread, calls run unsplit.  A graph captured on a stream must
+ * address) and keeps it; the next FKE_SPLIT_SMALL_SLOTS streams on that GPU
+ * get slots of FKE_SPLIT_SMALL_SLOT_BYTES, on which plans that need more run
+ * with fewer splits (the B [K,N] decode) or unsplit (the MFMA GEMM); past
+ * both, and on hipStreamPerThread, calls run unsplit.  A graph captured on a stream must
  * not be replayed while other work that uses the capture stream's slot (calls
  * on that stream, other graphs captured on it) can run at the same time.
  * fke_qgemm_i8_ws / fke_qgemm_f8_ws are the same calls on the caller's
@@ -172,9 +174,12 @@ int fke_qgemm_f8_on_path(int path, const uint8_t* A, const uint8_t* B, void* C,
  */
 #define FKE_SPLIT_SLOTS 16
 #define FKE_SPLIT_SLOT_BYTES (16u << 20)
+#define FKE_SPLIT_SMALL_SLOTS 48
+#define FKE_SPLIT_SMALL_SLOT_BYTES (2u << 20)
 size_t fke_qgemm_workspace_size(int M, int N, int K, int b_layout);
-/* Slots of the current GPU's split pool that streams hold (0..FKE_SPLIT_SLOTS),
- * or -1 without a device.  Host logic only; launches nothing. */
+/* Slots of the current GPU's split pool that streams hold (0..FKE_SPLIT_SLOTS
+ * + FKE_SPLIT_SMALL_SLOTS; the first FKE_SPLIT_SLOTS are the large ones), or
+ * -1 without a device.  Host logic only; launches nothing. */
 int fke_split_slots_in_use(void);
 int fke_qgemm_i8_ws(const int8_t* A, const int8_t* B, void* C, int M, int N, int K,
                     const float* scale_a, const float* scale_b, float sa, float sb,

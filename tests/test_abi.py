@@ -519,6 +519,10 @@ def test_split_pool_constants_match_header():
     scratch = re.search(r"#define FKE_W8A8_NOALLOC_SCRATCH_BYTES \((\d+)u << (\d+)\)", text)
     assert slots == _lib.SPLIT_SLOTS
     assert int(slot.group(1)) << int(slot.group(2)) == _lib.SPLIT_SLOT_BYTES
+    small = int(re.search(r"#define FKE_SPLIT_SMALL_SLOTS (\d+)", text).group(1))
+    small_b = re.search(r"#define FKE_SPLIT_SMALL_SLOT_BYTES \((\d+)u << (\d+)\)", text)
+    assert small == _lib.SPLIT_SMALL_SLOTS
+    assert int(small_b.group(1)) << int(small_b.group(2)) == _lib.SPLIT_SMALL_SLOT_BYTES
     assert int(scratch.group(1)) << int(scratch.group(2)) == _lib.W8A8_NOALLOC_SCRATCH_BYTES
     assert _lib.lib().fke_split_slots_in_use() == -1  # no device here
 
