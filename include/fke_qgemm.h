@@ -168,8 +168,10 @@ int fke_qgemm_f8_on_path(int path, const uint8_t* A, const uint8_t* B, void* C,
  * same bits whatever the workspace.  FP8 sums each split in fp32 and adds the
  * splits in order, so the bits depend on the number of splits: a workspace of
  * at least fke_qgemm_workspace_size bytes gives the bits of fke_qgemm_f8
- * (eager or captured), a smaller one other bits (within the same FP8 error
- * bounds, and the same from call to call).  Calls that can overlap in time
+ * (eager or captured) on a stream holding a large pool slot, a smaller one
+ * other bits (within the same FP8 error bounds, and the same from call to
+ * call); on a stream holding a small slot fke_qgemm_f8 gives the bits of a
+ * FKE_SPLIT_SMALL_SLOT_BYTES workspace, eager or captured alike.  Calls that can overlap in time
  * must not share a workspace.  Other kernel families ignore it.
  */
 #define FKE_SPLIT_SLOTS 16
