@@ -230,11 +230,11 @@ hipError_t launch_t(const GemmArgs& p, hipStream_t stream) {
 // workgroup then runs its K loop again with them cleared.  The epilogue is
 // the generic kernel's.
 // ===========================================================================
-constexpr int WT = 128;               // tile edge
+constexpr int WT = 128;               // tile rows (and columns of the wide tile)
 constexpr int WKC = 64;               // K bytes per stage
 constexpr int WNS = 4;                // ring stages (64 KiB of LDS)
-constexpr int WOP = WT * WKC;         // bytes of one operand's stage (8 KiB)
-constexpr int WCP = WOP / (4 * 256);  // 4-byte copies per wave, operand and stage (8)
+constexpr int WOP = WT * WKC;         // bytes of A's stage (8 KiB)
+constexpr int WCP = WOP / (4 * 256);  // 4-byte copies per wave and stage of A (8)
 static_assert(WCP == 8 && WNS == 4, "copy and wait counts below");
 
 typedef int w2i __attribute__((ext_vector_type(2)));
@@ -254,44 +254,64 @@ __device__ __forceinline__ w2i w_rdtr(const w_lds* a) {
     return r;
 }
 
-template <int EL, int BL, int OUT>
+// BN: tile columns, 128 or 64 (the narrow tile doubles the workgroups of
+// shapes with few 128x128 tiles); wave w takes columns (w % 2) BN / 2 ...
+template <int EL, int BL, int OUT, int BN>
 __global__ __launch_bounds__(256) void gemm_words_kernel(GemmArgs p) {
     constexpr bool F8 = EL == ELEM_F8, KN = BL == FKE_B_KN;
+    static_assert(BN == 128 || BN == 64, "tile columns");
+    constexpr int NJ = BN / 32;                  // 16-column blocks per wave
+    constexpr int WOPB = BN * WKC;               // bytes of B's stage
+    constexpr int WCPB = WOPB / (4 * 256);       // 4-byte copies per wave and stage of B (8 or 4)
     using Acc = typename std::conditional<F8, w4f, w4i>::type;
-    __shared__ __attribute__((aligned(1024))) uint8_t ring[WNS][2][WOP];
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[WNS][WOP + WOPB];
     __shared__ int nan_seen;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
     const int M = p.M, N = p.N, K = p.K;
-    const int m0 = blockIdx.y * WT, n0 = blockIdx.x * WT;
+    const int m0 = blockIdx.y * WT, n0 = blockIdx.x * BN;
     const int nst = (K + WKC - 1) / WKC;
     if constexpr (F8) {
         if (tid == 0) nan_seen = 0;
         __syncthreads();  // before any wave can set it (no copy is in flight yet)
     }
 
-    // Copy i of wave w, 64-byte rows (A; B [N,K]): stage bytes 256 (8w + i) +
-    // 4l = row r = 4 (8w + i) + l / 16, physical chunk (l % 16) / 4, word
-    // l % 4, holding logical chunk ((l % 16) / 4) ^ (i & 3).  B [K,N]: stage
-    // bytes 256 (8w + i) + 4l = k row kr = 2 (8w + i) + l / 32, physical chunk
+    // Copy i of wave w, 64-byte rows (A; B [N,K]): stage bytes 256 (c w + i)
+    // + 4l, c = the wave's copies, = row r = 4 (c w + i) + l / 16, physical
+    // chunk (l % 16) / 4, word l % 4, holding logical chunk ((l % 16) / 4) ^
+    // (i & 3) (c is a multiple of 4).  B [K,N], 128-byte rows: stage bytes
+    // 256 (8w + i) + 4l = k row kr = 2 (8w + i) + l / 32, physical chunk
     // (l % 32) / 4, word l % 4, holding logical chunk ((l % 32) / 4) ^ (kr &
-    // 7).  Offsets are 32-bit (M K and N K below 2^31); bit 31 set reads zero.
+    // 7); 64-byte rows: k row kr = 4 (4w + i) + l / 16, physical chunk (l %
+    // 16) / 4, holding logical chunk ((l % 16) / 4) ^ ((kr >> 2) & 1).
+    // Offsets are 32-bit (M K and N K below 2^31); bit 31 set reads zero.
     const int lr = lane >> 4, pc = (lane & 15) >> 2, dw = lane & 3;
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, M * K);
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.B, N * K);
-    uint32_t arow[WCP], brow[WCP];
-    int bkr[WCP];
+    uint32_t arow[WCP], brow[WCPB];
+    int bkr[WCPB];
 #pragma unroll
     for (int i = 0; i < WCP; ++i) {
         const int r = 4 * (WCP * wave + i) + lr;
         arow[i] = m0 + r < M ? static_cast<uint32_t>((m0 + r) * K) : 0x80000000u;
+    }
+#pragma unroll
+    for (int i = 0; i < WCPB; ++i) {
         if constexpr (KN) {
-            const int kr = 2 * (WCP * wave + i) + (lane >> 5);
-            const int col = n0 + 16 * (((lane & 31) >> 2) ^ (kr & 7)) + 4 * dw;
+            int kr, c;
+            if constexpr (BN == 128) {
+                kr = 2 * (WCPB * wave + i) + (lane >> 5);
+                c = ((lane & 31) >> 2) ^ (kr & 7);
+            } else {
+                kr = 4 * (WCPB * wave + i) + lr;
+                c = pc ^ ((kr >> 2) & 1);
+            }
+            const int col = n0 + 16 * c + 4 * dw;
             bkr[i] = kr;
             brow[i] = col < N ? static_cast<uint32_t>(col) : 0x80000000u;
         } else {
+            const int r = 4 * (WCPB * wave + i) + lr;
             bkr[i] = 0;
             brow[i] = n0 + r < N ? static_cast<uint32_t>((n0 + r) * K) : 0x80000000u;
         }
@@ -304,47 +324,56 @@ __global__ __launch_bounds__(256) void gemm_words_kernel(GemmArgs p) {
 #pragma unroll
         for (int i = 0; i < WCP; ++i) {
             const int kb = k0 + kof[i & 3];
-            const int dst = (WCP * wave + i) * 256;
-            dma4(ra, kb < K ? arow[i] + static_cast<uint32_t>(kb) : 0x80000000u, 0, &ring[slot][0][dst]);
+            dma4(ra, kb < K ? arow[i] + static_cast<uint32_t>(kb) : 0x80000000u, 0,
+                 &ring[slot][(WCP * wave + i) * 256]);
+        }
+#pragma unroll
+        for (int i = 0; i < WCPB; ++i) {
+            uint8_t* dst = &ring[slot][WOP + (WCPB * wave + i) * 256];
             if constexpr (KN) {
                 const int k = k0 + bkr[i];
-                dma4(rb, k < K ? brow[i] + static_cast<uint32_t>(k * N) : 0x80000000u, 0, &ring[slot][1][dst]);
+                dma4(rb, k < K ? brow[i] + static_cast<uint32_t>(k * N) : 0x80000000u, 0, dst);
             } else {
-                dma4(rb, kb < K ? brow[i] + static_cast<uint32_t>(kb) : 0x80000000u, 0, &ring[slot][1][dst]);
+                const int kb = k0 + kof[i & 3];
+                dma4(rb, kb < K ? brow[i] + static_cast<uint32_t>(kb) : 0x80000000u, 0, dst);
             }
         }
     };
 
     // Fragment reads: lane (g, rr) = (lane / 16, lane % 16); A and B [N,K]:
-    // logical chunk g of row 16 x + rr of the wave's 64 rows.  B [K,N]: two
+    // logical chunk g of row 16 x + rr of the wave's rows.  B [K,N]: two
     // transposing reads, k rows 16g + 8t + b (b = rr / 2) at the 8-byte half
     // rr % 2 of the wave's column block x.
     const int g = lane >> 4, rr = lane & 15;
-    uint32_t fa[4], fb[4][2];
+    uint32_t fa[4], fb[NJ][2];
 #pragma unroll
     for (int x = 0; x < 4; ++x) {
         const int ar = wm * 64 + 16 * x + rr;
         fa[x] = static_cast<uint32_t>(ar * WKC + 16 * (g ^ ((ar >> 2) & 3)));
+    }
+#pragma unroll
+    for (int x = 0; x < NJ; ++x) {
         if constexpr (KN) {
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
                 const int kr = 16 * g + 8 * t + (rr >> 1);
-                fb[x][t] = static_cast<uint32_t>(WOP + kr * WT + 16 * ((4 * wn + x) ^ (kr & 7)) + 8 * (rr & 1));
+                const int c = NJ * wn + x, sw = BN == 128 ? (kr & 7) : ((kr >> 2) & 1);
+                fb[x][t] = static_cast<uint32_t>(WOP + kr * BN + 16 * (c ^ sw) + 8 * (rr & 1));
             }
         } else {
-            const int br = wn * 64 + 16 * x + rr;
+            const int br = wn * (BN / 2) + 16 * x + rr;
             fb[x][0] = fb[x][1] = static_cast<uint32_t>(WOP + br * WKC + 16 * (g ^ ((br >> 2) & 3)));
         }
     }
-    const w_lds* const lring = (const w_lds*)(&ring[0][0][0]);
+    const w_lds* const lring = (const w_lds*)(&ring[0][0]);
 
-    Acc acc[4][4];
+    Acc acc[4][NJ];
     auto k_loop = [&](auto sanc) __attribute__((always_inline)) {
         constexpr bool SAN = decltype(sanc)::value;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = Acc{0, 0, 0, 0};
+            for (int j = 0; j < NJ; ++j) acc[i][j] = Acc{0, 0, 0, 0};
 #pragma unroll
         for (int s = 0; s < WNS - 1; ++s)
             if (s < nst) issue(s);
@@ -355,50 +384,57 @@ __global__ __launch_bounds__(256) void gemm_words_kernel(GemmArgs p) {
             // s - 1, whose slot takes stage s + WNS - 1.
             const int later = min(nst - 1 - s, WNS - 2);
             if (later == 0) wait_vm<0>();
-            else if (later == 1) wait_vm<2 * WCP>();
-            else wait_vm<4 * WCP>();
+            else if (later == 1) wait_vm<WCP + WCPB>();
+            else wait_vm<2 * (WCP + WCPB)>();
             barrier();
             if (s + WNS - 1 < nst) issue(s + WNS - 1);
-            const w_lds* st = lring + (s % WNS) * 2 * WOP;
-            w4i af[4], bf[4];
+            const w_lds* st = lring + (s % WNS) * (WOP + WOPB);
+            w4i af[4], bf[NJ];
 #pragma unroll
             for (int x = 0; x < 4; ++x) af[x] = w_rd128(st + fa[x]);
             if constexpr (KN) {
-                w2i t0[4], t1[4];
+                w2i t0[NJ], t1[NJ];
 #pragma unroll
-                for (int x = 0; x < 4; ++x) {
+                for (int x = 0; x < NJ; ++x) {
                     t0[x] = w_rdtr(st + fb[x][0]);
                     t1[x] = w_rdtr(st + fb[x][1]);
                 }
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
-                for (int x = 0; x < 4; ++x) {
-                    asm volatile("" : "+v"(af[x]), "+v"(t0[x]), "+v"(t1[x]));
+                for (int x = 0; x < 4; ++x) asm volatile("" : "+v"(af[x]));
+#pragma unroll
+                for (int x = 0; x < NJ; ++x) {
+                    asm volatile("" : "+v"(t0[x]), "+v"(t1[x]));
                     bf[x] = w4i{t0[x][0], t0[x][1], t1[x][0], t1[x][1]};
                 }
             } else {
 #pragma unroll
-                for (int x = 0; x < 4; ++x) bf[x] = w_rd128(st + fb[x][0]);
+                for (int x = 0; x < NJ; ++x) bf[x] = w_rd128(st + fb[x][0]);
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
-                for (int x = 0; x < 4; ++x) asm volatile("" : "+v"(af[x]), "+v"(bf[x]));
+                for (int x = 0; x < 4; ++x) asm volatile("" : "+v"(af[x]));
+#pragma unroll
+                for (int x = 0; x < NJ; ++x) asm volatile("" : "+v"(bf[x]));
             }
             if constexpr (F8) {
                 if constexpr (SAN) {
 #pragma unroll
                     for (int x = 0; x < 4; ++x)
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) {
+                        for (int e = 0; e < 4; ++e)
                             af[x][e] = static_cast<int>(e4m3_sanitize(static_cast<uint32_t>(af[x][e])));
+#pragma unroll
+                    for (int x = 0; x < NJ; ++x)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
                             bf[x][e] = static_cast<int>(e4m3_sanitize(static_cast<uint32_t>(bf[x][e])));
-                        }
                 }
                 const w4i z = {0, 0, 0, 0};
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const w8i a8 = __builtin_shufflevector(af[i], z, 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
-                    for (int j = 0; j < 4; ++j)
+                    for (int j = 0; j < NJ; ++j)
                         acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
                             a8, __builtin_shufflevector(bf[j], z, 0, 1, 2, 3, 4, 5, 6, 7), acc[i][j], 0, 0, 0, 0, 0, 0);
                 }
@@ -406,7 +442,7 @@ __global__ __launch_bounds__(256) void gemm_words_kernel(GemmArgs p) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
 #pragma unroll
-                    for (int j = 0; j < 4; ++j)
+                    for (int j = 0; j < NJ; ++j)
                         acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
             }
         }
@@ -421,7 +457,7 @@ __global__ __launch_bounds__(256) void gemm_words_kernel(GemmArgs p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < NJ; ++j)
 #pragma unroll
                 for (int v = 0; v < 4; ++v) bad |= __builtin_isnan(acc[i][j][v]);
         if (__builtin_amdgcn_ballot_w64(bad) != 0 && lane == 0) nan_seen = 1;
@@ -438,8 +474,8 @@ __global__ __launch_bounds__(256) void gemm_words_kernel(GemmArgs p) {
             if (m >= M) continue;
             const float sam = p.scale_a ? p.scale_a[m] : p.sa;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int n = n0 + wn * 64 + 16 * j + rr;
+            for (int j = 0; j < NJ; ++j) {
+                const int n = n0 + wn * (BN / 2) + 16 * j + rr;
                 if (n >= N) continue;
                 // (FP8 calls carry no scale vectors: s = fp32(sa * sb))
                 const float s = sam * (p.scale_b ? p.scale_b[n] : p.sb);
@@ -469,25 +505,33 @@ bool words_supports(const GemmArgs& p, int elem) {
 }
 
 namespace {
-template <int EL, int BL>
+template <int EL, int BL, int BN>
 const void* words_kernel(int out) {
     if constexpr (EL == ELEM_I8)
-        if (out == FKE_OUT_I32) return reinterpret_cast<const void*>(&gemm_words_kernel<EL, BL, FKE_OUT_I32>);
-    return out == FKE_OUT_F32 ? reinterpret_cast<const void*>(&gemm_words_kernel<EL, BL, FKE_OUT_F32>)
-                              : reinterpret_cast<const void*>(&gemm_words_kernel<EL, BL, FKE_OUT_BF16>);
+        if (out == FKE_OUT_I32) return reinterpret_cast<const void*>(&gemm_words_kernel<EL, BL, FKE_OUT_I32, BN>);
+    return out == FKE_OUT_F32 ? reinterpret_cast<const void*>(&gemm_words_kernel<EL, BL, FKE_OUT_F32, BN>)
+                              : reinterpret_cast<const void*>(&gemm_words_kernel<EL, BL, FKE_OUT_BF16, BN>);
+}
+template <int BN>
+const void* words_kernel_for(int elem, bool kn, int out) {
+    return elem == ELEM_I8 ? (kn ? words_kernel<ELEM_I8, FKE_B_KN, BN>(out) : words_kernel<ELEM_I8, FKE_B_NK, BN>(out))
+                           : (kn ? words_kernel<ELEM_F8, FKE_B_KN, BN>(out) : words_kernel<ELEM_F8, FKE_B_NK, BN>(out));
 }
 }  // namespace
 
+// 128x128 tiles, or 128x64 while those still number at most one per CU
+// (decode-sized M): twice the workgroups, each streaming half the columns,
+// each re-reading its A rows.  Same box, bf16 out + bias, 14336 x 4100:
+// B [N,K] M = 16 34.0 against 48.4 us, B [K,N] M = 64 42.0 against 58.9; at
+// M = 256 (224 wide tiles) 63.1 against 60.0 on the wide tile.
 hipError_t launch_words(const GemmArgs& p, int elem, hipStream_t s) {
     if (!words_supports(p, elem)) return hipErrorInvalidValue;
     GemmArgs a = p;
     void* args[] = {&a};
-    const dim3 grid((p.N + WT - 1) / WT, (p.M + WT - 1) / WT);
-    const bool kn = p.b_layout == FKE_B_KN;
-    const void* f = elem == ELEM_I8 ? (kn ? words_kernel<ELEM_I8, FKE_B_KN>(p.out_dtype)
-                                          : words_kernel<ELEM_I8, FKE_B_NK>(p.out_dtype))
-                                    : (kn ? words_kernel<ELEM_F8, FKE_B_KN>(p.out_dtype)
-                                          : words_kernel<ELEM_F8, FKE_B_NK>(p.out_dtype));
+    const int64_t rows = (p.M + WT - 1) / WT, wide = (p.N + WT - 1) / WT * rows;
+    const bool kn = p.b_layout == FKE_B_KN, narrow = 2 * wide <= device_cus();
+    const void* f = narrow ? words_kernel_for<64>(elem, kn, p.out_dtype) : words_kernel_for<128>(elem, kn, p.out_dtype);
+    const dim3 grid(narrow ? (p.N + 63) / 64 : (p.N + WT - 1) / WT, static_cast<unsigned>(rows));
     return hipLaunchKernel(f, grid, dim3(256), args, 0, s);
 }
 

@@ -1529,14 +1529,18 @@ def test_gemv_rows_dword_form(oracle, dev, M, N, K, shift):
 
 
 # INT8 and FP8 whose K (and N, for B [K,N]) is a multiple of 4 but not of 16,
-# or whose operands are only 4-byte aligned: the word kernel (128x128 tiles
-# on the matrix cores, 4-byte copies), through the automatic path.  B [K,N]
+# or whose operands are only 4-byte aligned: the word kernel (128x128 tiles,
+# 128x64 where those number at most half the CUs, on the matrix cores, 4-byte
+# copies), through the automatic path.  B [K,N]
 # from 33 rows (below, the [K,N] decode's 4-byte form takes such shapes).
 WORDS_CASES = [(5, 14336, 4100, 0, "nk"), (6, 1000, 68, 0, "nk"), (64, 64, 100, 0, "nk"), (129, 257, 4, 0, "nk"),
                (300, 520, 4104, 0, "nk"), (256, 4096, 4096, 4, "nk"), (200, 1030, 1028, 4, "nk"),
                (1024, 1024, 4100, 0, "nk"), (33, 4100, 4100, 0, "kn"), (64, 64, 100, 0, "kn"),
                (129, 260, 4, 0, "kn"), (300, 520, 4104, 0, "kn"), (256, 4096, 4096, 4, "kn"),
-               (200, 1028, 1028, 4, "kn"), (1024, 1024, 4100, 0, "kn")]
+               (200, 1028, 1028, 4, "kn"), (1024, 1024, 4100, 0, "kn"),
+               # 256 tiles of 128x128: the wide tile (128 or fewer take 128x64 tiles)
+               (2048, 2048, 100, 0, "nk"), (2048, 2064, 68, 4, "nk"), (2048, 2048, 100, 0, "kn"),
+               (2048, 2064, 132, 4, "kn")]
 
 
 def _words_path(L, M, N, K, shift, layout, f8=False):
