@@ -280,13 +280,14 @@ GemmArgs make_swiglu_args(const void* A, const void* W, void* H, int M, int I, i
 
 // Decode with B [K,N]: the transposing kernels, but where the row kernel's
 // 4-byte form would stream the weights more than once (past 4 rows) the MFMA
-// GEMM if it takes the shape, and past 20 rows the word kernel.  Same box,
-// N = 14340, K = 4096, bf16 out: row kernel / word kernel M = 16 40.0 / 48.4
-// us, M = 32 75.9 / 51.8 (FP8 43.8 / 57.8 and 80.5 / 61.1).
+// GEMM if it takes the shape, and past 8 rows the word kernel.  Same box,
+// N = 14340, K = 4096, bf16 out: row kernel / word kernel M = 8 23.7 / 36.0
+// us, M = 12 40.3 / 36.1, M = 16 39.9 / 36.0 (FP8 26.7 / 40.3 and 43.7 /
+// 40.3).
 bool kn_decode_pays(const GemmArgs& p, int elem) {
     if (!fke::gemv_kn_supports(p, elem)) return false;
     if (!fke::gemv_kn_yields_to_mfma(p)) return true;
-    return !(fke::mfma_supports(p, elem) || (p.M > 20 && fke::words_supports(p, elem)));
+    return !(fke::mfma_supports(p, elem) || (p.M > 8 && fke::words_supports(p, elem)));
 }
 
 int pick_i8(const GemmArgs& p) {

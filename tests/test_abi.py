@@ -317,8 +317,8 @@ def test_path_unavailable_for_shape_is_rejected():
     (4, 4096, 64, 1, _lib.PATH_GEMV),
     (4, 4104, 4096, 1, _lib.PATH_GEMV),      # B [K,N] with N % 16 != 0: the row kernel's 4-byte form
     (1, 4104, 4096, 1, _lib.PATH_GEMV),
-    (20, 4104, 4096, 1, _lib.PATH_GEMV),
-    (21, 4104, 4096, 1, _lib.PATH_MFMA),     # past 20 rows the word kernel
+    (8, 4104, 4096, 1, _lib.PATH_GEMV),
+    (9, 4104, 4096, 1, _lib.PATH_MFMA),      # past 8 rows the word kernel
     (5, 14336, 4000, 1, _lib.PATH_MFMA),     # past 4 rows the MFMA GEMM where it can (K % 16 == 0, N % 16 == 0)
     (4, 14336, 4000, 1, _lib.PATH_GEMV),     # one row group: the 4-byte form
     (33, 4104, 4096, 1, _lib.PATH_MFMA),     # past 32 rows: the word kernel (N % 4 == 0, K % 4 == 0)
@@ -368,7 +368,8 @@ def test_dispatch_unaligned_pointer_falls_back():
     (4, 14336, 4000, 1, _lib.PATH_GEMV),      # K % 64 != 0: the row kernel's 4-byte form (K % 4 == 0)
     (4, 14336, 4004, 1, _lib.PATH_GEMV),      # K % 16 != 0 (K % 4 == 0): the 4-byte form too
     (16, 14336, 4000, 1, _lib.PATH_MFMA),     # past 4 rows the MFMA GEMM where it can
-    (16, 14336, 4004, 1, _lib.PATH_GEMV),     # and the 4-byte form where it cannot
+    (8, 14336, 4004, 1, _lib.PATH_GEMV),      # and the 4-byte form where it cannot, to 8 rows
+    (16, 14336, 4004, 1, _lib.PATH_MFMA),     # then the word kernel
     (4, 14336, 4002, 1, _lib.PATH_GENERIC),   # K % 4 != 0
     (64, 14336, 4100, 1, _lib.PATH_MFMA),     # past 32 rows, K % 16 != 0: the word kernel (both layouts)
     (1, 14336, 4100, 0, _lib.PATH_GEMV),      # one row, B [N,K]: the row kernel's 4-byte form

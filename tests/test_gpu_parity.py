@@ -412,12 +412,12 @@ def dev_at(x, shift):
 # B [K,N] whose N or K is only a multiple of 4, or whose operands are only
 # 4-byte aligned: the row kernel's 4-byte form (one split when the plan gives
 # one, a ragged last 1024-column block, K not a multiple of 128; past one row,
-# workgroups of 2 or 4 activation rows, the last group part empty; past 20
+# workgroups of 2 or 4 activation rows, the last group part empty; past 8
 # rows the word kernel takes these shapes).
 KN_DW_CASES = [(1, 1000, 4096, 0), (1, 14340, 4096, 0), (1, 4100, 4100, 0), (1, 2052, 100, 0), (1, 14336, 4000, 0),
                (1, 14336, 4096, 4), (1, 1024, 4, 4), (2, 14340, 4096, 0), (3, 4100, 4100, 4), (4, 1000, 4096, 0),
-               (5, 2052, 100, 0), (8, 14336, 4096, 4), (16, 14340, 4096, 0), (17, 4100, 1028, 4),
-               (20, 14340, 4096, 0)]
+               (5, 2052, 100, 0), (8, 14336, 4096, 4), (6, 14340, 4096, 0), (7, 4100, 1028, 4),
+               (8, 14340, 4096, 0)]
 
 
 @pytest.mark.parametrize("M,N,K,shift", KN_DW_CASES)
