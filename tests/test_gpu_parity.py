@@ -664,7 +664,8 @@ def test_fp8_dropin_launcher_decode(oracle, dev, M):
     A, B, sa, sb = f8_inputs(oracle, M, N, K, 7600 + M, "kn", with_nan_codes=True)
     ref = oracle.ref_kernel_gemm_f8(A, B, sa, sb)
     C = torch.empty((M, N), dtype=torch.float32, device="cuda")
-    st = _lib.lib().fke_launch_fp8_gemm_scaled(dev_t(A).data_ptr(), dev_t(B).data_ptr(), C.data_ptr(), sa, sb,
+    dA, dB = dev_t(A), dev_t(B)  # held: a temporary's memory could be reused for the next operand
+    st = _lib.lib().fke_launch_fp8_gemm_scaled(dA.data_ptr(), dB.data_ptr(), C.data_ptr(), sa, sb,
                                                M, N, K, None)
     _lib.check(st, "fke_launch_fp8_gemm_scaled")
     torch.cuda.synchronize()
@@ -683,10 +684,36 @@ def test_fp8_dropin_launcher_batch_on_the_split_decode(oracle, dev):
     A, B, sa, sb = f8_inputs(oracle, M, N, K, 7700, "kn", with_nan_codes=True)
     ref = oracle.f8_gemm(A, B, sa, sb, b_layout=oracle.B_KN, nthreads=NTH)  # the sequential sum, threaded
     C = torch.empty((M, N), dtype=torch.float32, device="cuda")
-    _lib.check(L.fke_launch_fp8_gemm_scaled(dev_t(A).data_ptr(), dev_t(B).data_ptr(), C.data_ptr(), sa, sb, M, N, K,
+    dA, dB = dev_t(A), dev_t(B)  # held: a temporary's memory could be reused for the next operand
+    _lib.check(L.fke_launch_fp8_gemm_scaled(dA.data_ptr(), dB.data_ptr(), C.data_ptr(), sa, sb, M, N, K,
                                             None), "fke_launch_fp8_gemm_scaled")
     torch.cuda.synchronize()
     assert_fp8_close(C.cpu().numpy(), ref, "f32", f"drop-in batch M={M}")
+
+
+@pytest.mark.parametrize("M,N,K,want", [(1, 1000, 100, "gemv"), (7, 4100, 1028, "gemv"), (64, 1000, 100, "mfma"),
+                                        (300, 4100, 4100, "mfma"), (37, 50, 131, "generic")])
+def test_fp8_dropin_launcher_odd_shapes(oracle, dev, M, N, K, want):
+    """The drop-in fke_launch_fp8_gemm_scaled (B [K,N]: the reference
+    launcher, which takes any shape) where N or K is only a multiple of 4
+    (the [K,N] decode's 4-byte form up to 8 rows, the word kernel above) or
+    neither (the generic kernel), against the reference's sequential sum with
+    0x7F / 0xFF codes."""
+    say("fp8 drop-in odd shape", M, N, K, want)
+    L = _lib.lib()
+    path = {"gemv": _lib.PATH_GEMV, "mfma": _lib.PATH_MFMA, "generic": _lib.PATH_GENERIC}[want]
+    assert L.fke_select_path_f8(4096, 4096, 4096, M, N, K, _lib.OUT_F32, _lib.B_KN) == path
+    A, B, sa, sb = f8_inputs(oracle, M, N, K, 7800 + M + N + K, "kn", with_nan_codes=True)
+    ref = oracle.f8_gemm(A, B, sa, sb, b_layout=oracle.B_KN, nthreads=NTH)
+    C = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    dA, dB = dev_t(A), dev_t(B)  # held: a temporary's memory could be reused for the next operand
+    _lib.check(L.fke_launch_fp8_gemm_scaled(dA.data_ptr(), dB.data_ptr(), C.data_ptr(), sa, sb, M, N, K,
+                                            None), "fke_launch_fp8_gemm_scaled")
+    torch.cuda.synchronize()
+    if want == "generic":  # the reference's own order: the same bits
+        assert np.array_equal(C.cpu().numpy().view(np.uint32), ref.view(np.uint32)), "generic FP8 not bit-exact"
+    else:
+        assert_fp8_close(C.cpu().numpy(), ref, "f32", f"drop-in odd M={M} N={N} K={K}")
 
 
 @pytest.mark.parametrize("M", list(range(1, 17)))
