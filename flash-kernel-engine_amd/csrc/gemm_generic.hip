@@ -212,14 +212,16 @@ hipError_t launch_t(const GemmArgs& p, hipStream_t stream) {
 // multiple of 4 (K / 4 packed words per row, src/quantized_gemm.cu:28-37);
 // its FP8 kernel any shape with B [K,N] (src/quantized_gemm.cu:99-118).
 // 128x128 output tile per 256-thread workgroup, wave w the 64x64 block
-// (w / 2, w % 2).  K runs in stages of 64 bytes through a ring of WNS stages
+// (w / 2, w % 2), or 128x64 with 64x32 blocks (launch_words says when).  K
+// runs in stages of 64 bytes through a ring of WNS stages
 // in LDS, copied with 4-byte LDS-DMA loads (buffer_load_dword ... lds: lane
 // l's word lands at 4l of the instruction's 256 bytes), so no registers hold
 // the stages in flight; words past M, N or K read zero through the buffer
 // range (a word is all in or all out).  Stage rows of A and of B [N,K] are 64
 // k bytes, logical 16-byte chunk c of row r at physical chunk c ^ ((r >> 2) &
-// 3); B [K,N] is 64 k rows of 128 column bytes, chunk c of k row r at c ^ (r
-// & 7), read with the transposing ds_read_b64_tr_b8.  Either way a 16-lane
+// 3); B [K,N] is 64 k rows of the tile's column bytes, chunk c of k row r at
+// c ^ (r & 7) (128 bytes) or c ^ ((r >> 2) & 1) (64 bytes), read with the
+// transposing ds_read_b64_tr_b8.  Either way a 16-lane
 // fragment read covers the 64 banks once.  Lane (g, r) of a fragment holds k
 // bytes 16g .. 16g + 15 of row (column) r: INT8 multiplies them with
 // v_mfma_i32_16x16x64_i8 (exact int32 sums); FP8 with
@@ -232,7 +234,7 @@ hipError_t launch_t(const GemmArgs& p, hipStream_t stream) {
 // ===========================================================================
 constexpr int WT = 128;               // tile rows (and columns of the wide tile)
 constexpr int WKC = 64;               // K bytes per stage
-constexpr int WNS = 4;                // ring stages (64 KiB of LDS)
+constexpr int WNS = 4;                // ring stages (64 / 48 KiB of LDS for the wide / narrow tile)
 constexpr int WOP = WT * WKC;         // bytes of A's stage (8 KiB)
 constexpr int WCP = WOP / (4 * 256);  // 4-byte copies per wave and stage of A (8)
 static_assert(WCP == 8 && WNS == 4, "copy and wait counts below");
