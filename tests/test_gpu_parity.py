@@ -1625,3 +1625,49 @@ def test_words_kernel_fp8(oracle, dev, M, N, K, shift, layout, nan_codes):
         torch.cuda.synchronize()
         got = host(C) if out == "f32" else oracle.bf16_to_f32(host(C))
         assert_fp8_close(got, ref, out, f"words fp8 M={M} N={N} K={K} shift={shift} {layout} nan={nan_codes}")
+
+
+def _random_word_cases(n, seed):
+    """Shapes whose N and K are multiples of 4 only (now and then of 16),
+    with operands 0, 4, 8 or 12 bytes past 16-byte alignment: the 4-byte
+    forms of the decode kernels, the word kernel and, where aligned, the
+    16-byte families."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for _ in range(n):
+        M = int(rng.choice([1, 2, 3, 4, 5, 7, 8, 9, 12, 16, 17, 20, 21, 32, 33, 64, 100, 129, 200]))
+        N = 4 * int(rng.integers(1, 600))
+        K = 4 * int(rng.integers(1, 650))
+        layout = str(rng.choice(["nk", "kn"]))
+        shift = int(rng.choice([0, 4, 8, 12]))
+        cases.append((M, N, K, layout, shift))
+    return cases
+
+
+@pytest.mark.parametrize("M,N,K,layout,shift", _random_word_cases(30, 20261203))
+def test_auto_dispatch_random_word_shapes(oracle, dev, M, N, K, layout, shift):
+    """Seeded shapes of 4-byte multiples through the automatic dispatch: INT8
+    bit-exact (bf16 out with bias, and int32), FP8 (0x7F / 0xFF codes in one
+    case of three) within the bounds of the sequential sum."""
+    say("auto random, 4-byte shapes", M, N, K, layout, shift)
+    L = _lib.lib()
+    bl, obl = (_lib.B_KN, oracle.B_KN) if layout == "kn" else (_lib.B_NK, oracle.B_NK)
+    A, B, sa, sb, bias = inputs_i8(oracle, M, N, K, 5200 + M + N + K, layout)
+    acc = oracle.w8a8_acc(A, B, obl, nthreads=NTH)
+    (ba, pa), (bb, pb) = dev_at(A, shift), dev_at(B, shift)
+    dsa, dsb, dbias = dev_t(sa), dev_t(sb), dev_t(bias)
+    for out, code in (("bf16", _lib.OUT_BF16), ("i32", _lib.OUT_I32)):
+        C = torch.empty((M, N), dtype=OUT_T[out], device=dev)
+        _lib.check(L.fke_qgemm_i8(pa, pb, C.data_ptr(), M, N, K, dsa.data_ptr(), dsb.data_ptr(), 1.0, 1.0,
+                                  dbias.data_ptr(), code, bl, torch.cuda.current_stream().cuda_stream), "fke_qgemm_i8")
+        torch.cuda.synchronize()
+        want = acc if out == "i32" else oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, out)
+        assert_same(host(C), want, f"random words {out} {M, N, K, layout, shift}")
+    A8, B8, fa, fb = f8_inputs(oracle, M, N, K, 5300 + M + N + K, layout, with_nan_codes=(M + N) % 3 == 0)
+    ref = oracle.f8_gemm(A8, B8, fa, fb, b_layout=obl, nthreads=NTH)
+    (ba8, pa8), (bb8, pb8) = dev_at(A8, shift), dev_at(B8, shift)
+    C = torch.empty((M, N), dtype=torch.float32, device=dev)
+    _lib.check(L.fke_qgemm_f8(pa8, pb8, C.data_ptr(), M, N, K, fa, fb, None, _lib.OUT_F32, bl,
+                              torch.cuda.current_stream().cuda_stream), "fke_qgemm_f8")
+    torch.cuda.synchronize()
+    assert_fp8_close(host(C), ref, "f32", f"random words fp8 {M, N, K, layout, shift}")
