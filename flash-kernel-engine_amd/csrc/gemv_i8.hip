@@ -196,7 +196,8 @@ __global__ __launch_bounds__(ROWS_WAVES * 64) void gemv_rows_kernel(GemmArgs p) 
     static_assert(!DW || !FULLK, "4-byte loads: K is not a multiple of 4096 bytes of 16-byte chunks");
     static_assert(!SWI || NB == 2, "SwiGLU streams one gate and one up row");
     static_assert(MT * NB <= 64, "one storing lane per output");
-    static_assert(!F8 || (MT == 1 && NB == 1 && !SWI && OUT != FKE_OUT_I32), "FP8: M = 1, fp32 or bf16 out");
+    static_assert(!F8 || (!SWI && OUT != FKE_OUT_I32 && (DW || (MT == 1 && NB == 1))),
+                  "FP8: fp32 or bf16 out; M = 1 with 16-byte loads");
     using Acc = typename std::conditional<F8, float, int32_t>::type;
     const int lane = threadIdx.x & 63;
     const int NO = SWI ? p.N >> 1 : p.N;           // output columns
@@ -270,21 +271,35 @@ __global__ __launch_bounds__(ROWS_WAVES * 64) void gemv_rows_kernel(GemmArgs p) 
             for (int u = 0; u < 16; ++u)
                 a[m][u] = __builtin_bit_cast(int, __builtin_amdgcn_raw_buffer_load_b32(ra[m], off[u], 0, 0));
         if constexpr (F8) {
+            // each output: the lane's words in order, the 4 products of a word in k order
 #pragma unroll
             for (int u = 0; u < 16; ++u) {
-                uint32_t aw = static_cast<uint32_t>(a[0][u]), bw = static_cast<uint32_t>(b[0][u]);
-                if constexpr (clear) {
-                    aw = e4m3_sanitize(aw);
-                    bw = e4m3_sanitize(bw);
+                float bf[NB][4];
+#pragma unroll
+                for (int q = 0; q < NB; ++q) {
+                    uint32_t bw = static_cast<uint32_t>(b[q][u]);
+                    if constexpr (clear) bw = e4m3_sanitize(bw);
+                    const v2f lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(bw), false);
+                    const v2f hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(bw), true);
+                    bf[q][0] = lo.x;
+                    bf[q][1] = lo.y;
+                    bf[q][2] = hi.x;
+                    bf[q][3] = hi.y;
                 }
-                const v2f alo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(aw), false);
-                const v2f ahi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(aw), true);
-                const v2f blo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(bw), false);
-                const v2f bhi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(bw), true);
-                acc[0][0] = __builtin_fmaf(alo.x, blo.x, acc[0][0]);
-                acc[0][0] = __builtin_fmaf(alo.y, blo.y, acc[0][0]);
-                acc[0][0] = __builtin_fmaf(ahi.x, bhi.x, acc[0][0]);
-                acc[0][0] = __builtin_fmaf(ahi.y, bhi.y, acc[0][0]);
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    uint32_t aw = static_cast<uint32_t>(a[m][u]);
+                    if constexpr (clear) aw = e4m3_sanitize(aw);
+                    const v2f alo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(aw), false);
+                    const v2f ahi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(aw), true);
+#pragma unroll
+                    for (int q = 0; q < NB; ++q) {
+                        acc[q][m] = __builtin_fmaf(alo.x, bf[q][0], acc[q][m]);
+                        acc[q][m] = __builtin_fmaf(alo.y, bf[q][1], acc[q][m]);
+                        acc[q][m] = __builtin_fmaf(ahi.x, bf[q][2], acc[q][m]);
+                        acc[q][m] = __builtin_fmaf(ahi.y, bf[q][3], acc[q][m]);
+                    }
+                }
             }
         } else {
 #pragma unroll
@@ -361,7 +376,12 @@ __global__ __launch_bounds__(ROWS_WAVES * 64) void gemv_rows_kernel(GemmArgs p) 
     stream(std::false_type{});
     totals();
     if constexpr (F8) {
-        if (tot[0][0] != tot[0][0]) {  // uniform over the wave: replay with the codes cleared
+        bool nan = false;  // the totals are uniform over the wave, so is the replay
+#pragma unroll
+        for (int q = 0; q < NB; ++q)
+#pragma unroll
+            for (int m = 0; m < MT; ++m) nan |= tot[q][m] != tot[q][m];
+        if (nan) {  // replay with the codes cleared
             stream(std::true_type{});
             totals();
         }
@@ -1041,6 +1061,18 @@ hipError_t launch_rows(const GemmArgs& p, hipStream_t stream) {
     return hipLaunchKernel(f, grid, dim3(ROWS_WAVES * 64), args, 0, stream);
 }
 
+// FP8 with 4-byte loads, 2..4 rows: two weight rows per wave, as for INT8.
+template <int MT>
+hipError_t launch_rows_f8_dw(const GemmArgs& p, hipStream_t stream) {
+    GemmArgs a = p;
+    void* args[] = {&a};
+    const dim3 grid(((p.N + 1) / 2 + ROWS_WAVES - 1) / ROWS_WAVES);
+    const void* f = p.out_dtype == FKE_OUT_F32
+        ? reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_F32, false, 2, false, ELEM_F8, true>)
+        : reinterpret_cast<const void*>(&gemv_rows_kernel<MT, FKE_OUT_BF16, false, 2, false, ELEM_F8, true>);
+    return hipLaunchKernel(f, grid, dim3(ROWS_WAVES * 64), args, 0, stream);
+}
+
 // FP8 at M = 1: the row kernel on E4M3 codes (one weight row per wave).
 template <bool FULLK, bool DW = false>
 hipError_t launch_rows_f8(const GemmArgs& p, hipStream_t stream) {
@@ -1200,14 +1232,16 @@ hipError_t launch_gemv_i8(const GemmArgs& p, hipStream_t s) {
 // 14336: 10.8 against 12.7), the LDS-streamed kernel on E4M3 codes above.
 bool gemv_f8_supports(const GemmArgs& p) {
     const uintptr_t a = reinterpret_cast<uintptr_t>(p.A), b = reinterpret_cast<uintptr_t>(p.B);
-    if (p.M == 1 && rows_dw_ok(p)) return !p.swiglu && (p.out_dtype == FKE_OUT_F32 || p.out_dtype == FKE_OUT_BF16);
+    if (rows_dw_ok(p)) return !p.swiglu && (p.out_dtype == FKE_OUT_F32 || p.out_dtype == FKE_OUT_BF16);
     return p.M >= 1 && p.M <= FKE_GEMV_MAX_M && p.N >= 1 && p.K % 64 == 0 && p.b_layout == FKE_B_NK &&
            !p.swiglu && (p.out_dtype == FKE_OUT_F32 || p.out_dtype == FKE_OUT_BF16) && ((a | b) & 15) == 0 &&
            (p.M == 1 || lds_fits<512>(p));
 }
 
 hipError_t launch_gemv_f8(const GemmArgs& p, hipStream_t s) {
-    if (p.M == 1 && rows_dw_ok(p)) return launch_rows_f8<false, true>(p, s);
+    if (rows_dw_ok(p))
+        return p.M == 1 ? launch_rows_f8<false, true>(p, s)
+                        : p.M == 2 ? launch_rows_f8_dw<2>(p, s) : launch_rows_f8_dw<4>(p, s);
     if (p.M == 1) return p.K % 4096 == 0 ? launch_rows_f8<true>(p, s) : launch_rows_f8<false>(p, s);
     const bool big = lds_fits<1024>(p) && (pieces_even(p.K, 1024) || !pieces_even(p.K, 512));
     if (p.M > 32) return launch_lds_f8<512, 4, 4>(p, s);

@@ -372,8 +372,10 @@ def test_dispatch_unaligned_pointer_falls_back():
     (16, 14336, 4004, 1, _lib.PATH_MFMA),     # then the word kernel
     (4, 14336, 4002, 1, _lib.PATH_GENERIC),   # K % 4 != 0
     (64, 14336, 4100, 1, _lib.PATH_MFMA),     # past 32 rows, K % 16 != 0: the word kernel (both layouts)
-    (1, 14336, 4100, 0, _lib.PATH_GEMV),      # one row, B [N,K]: the row kernel's 4-byte form
-    (2, 14336, 4100, 0, _lib.PATH_MFMA),
+    (1, 14336, 4100, 0, _lib.PATH_GEMV),      # up to 4 rows, B [N,K]: the row kernel's 4-byte form
+    (4, 14336, 4100, 0, _lib.PATH_GEMV),
+    (4, 14336, 4112, 0, _lib.PATH_MFMA),      # past one row the MFMA GEMM where it can run
+    (5, 14336, 4100, 0, _lib.PATH_MFMA),      # past 4 rows the word kernel
     (64, 14336, 4100, 0, _lib.PATH_MFMA),
     (64, 14338, 4100, 1, _lib.PATH_GENERIC),  # N % 4 != 0 with B [K,N]
     (8192, 8192, 8192, 0, _lib.PATH_MFMA),

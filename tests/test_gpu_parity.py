@@ -1515,18 +1515,18 @@ def test_fp8_auto_dispatch_random_shapes(oracle, dev, M, N, K, layout, out):
     assert_fp8_close(got, ref, out, f"auto {M, N, K, layout}")
 
 
-# B [N,K] up to 4 rows (FP8: one) whose K is a multiple of 4 but not of 64, or
-# whose operands are only 4-byte aligned: the row kernel's 4-byte form (past
-# one row only where the MFMA GEMM cannot run: K % 16 != 0 or unaligned).
+# B [N,K] up to 4 rows whose K is a multiple of 4 but not of 64, or whose
+# operands are only 4-byte aligned: the row kernel's 4-byte form (past one
+# row only where the MFMA GEMM cannot run: K % 16 != 0 or unaligned).
 ROWS_DW_CASES = [(1, 14336, 4100, 0), (2, 1000, 68, 0), (3, 4100, 4, 4), (4, 14336, 4108, 0), (1, 4096, 4096, 4),
                  (4, 2048, 1028, 4), (1, 14336, 4000, 0)]
 
 
 @pytest.mark.parametrize("M,N,K,shift", ROWS_DW_CASES)
 def test_gemv_rows_dword_form(oracle, dev, M, N, K, shift):
-    """INT8 bit-exact on every output type; FP8 at M = 1 (0x7F / 0xFF codes
-    included) within the bounds of the sequential sum; A and B `shift` bytes
-    past 16-byte alignment."""
+    """INT8 bit-exact on every output type; FP8 (0x7F / 0xFF codes included)
+    within the bounds of the sequential sum; A and B `shift` bytes past
+    16-byte alignment."""
     say("gemv rows, 4-byte loads", M, N, K, shift)
     L = _lib.lib()
     assert L.fke_select_path_i8(4096 + shift, 4096 + shift, 4096, M, N, K, _lib.OUT_BF16, _lib.B_NK) == _lib.PATH_GEMV
@@ -1542,17 +1542,15 @@ def test_gemv_rows_dword_form(oracle, dev, M, N, K, shift):
         torch.cuda.synchronize()
         want = acc if out == "i32" else oracle_out(oracle, acc, sa, sb, 1.0, 1.0, bias, out)
         assert_same(host(C), want, f"rows dword {out} M={M} N={N} K={K} shift={shift}")
-    if M == 1:
-        assert L.fke_select_path_f8(4096 + shift, 4096 + shift, 4096, M, N, K, _lib.OUT_BF16, _lib.B_NK) == \
-            _lib.PATH_GEMV
-        A8, B8, fa, fb = f8_inputs(oracle, M, N, K, 9650 + N + K, "nk", with_nan_codes=True)
-        ref = oracle.f8_gemm(A8, B8, fa, fb, b_layout=oracle.B_NK, nthreads=NTH)
-        (ba, pa), (bb, pb) = dev_at(A8, shift), dev_at(B8, shift)
-        C = torch.empty((M, N), dtype=torch.float32, device=dev)
-        _lib.check(L.fke_qgemm_f8(pa, pb, C.data_ptr(), M, N, K, fa, fb, None, _lib.OUT_F32, _lib.B_NK,
-                                  torch.cuda.current_stream().cuda_stream), "fke_qgemm_f8")
-        torch.cuda.synchronize()
-        assert_fp8_close(host(C), ref, "f32", f"rows dword fp8 N={N} K={K} shift={shift}")
+    assert L.fke_select_path_f8(4096 + shift, 4096 + shift, 4096, M, N, K, _lib.OUT_BF16, _lib.B_NK) == _lib.PATH_GEMV
+    A8, B8, fa, fb = f8_inputs(oracle, M, N, K, 9650 + 3 * M + N + K, "nk", with_nan_codes=True)
+    ref = oracle.f8_gemm(A8, B8, fa, fb, b_layout=oracle.B_NK, nthreads=NTH)
+    (ba, pa), (bb, pb) = dev_at(A8, shift), dev_at(B8, shift)
+    C = torch.empty((M, N), dtype=torch.float32, device=dev)
+    _lib.check(L.fke_qgemm_f8(pa, pb, C.data_ptr(), M, N, K, fa, fb, None, _lib.OUT_F32, _lib.B_NK,
+                              torch.cuda.current_stream().cuda_stream), "fke_qgemm_f8")
+    torch.cuda.synchronize()
+    assert_fp8_close(host(C), ref, "f32", f"rows dword fp8 M={M} N={N} K={K} shift={shift}")
 
 
 # INT8 and FP8 whose K (and N, for B [K,N]) is a multiple of 4 but not of 16,
