@@ -213,7 +213,7 @@ hipError_t launch_t(const GemmArgs& p, hipStream_t stream) {
 // its FP8 kernel any shape with B [K,N] (src/quantized_gemm.cu:99-118).
 // 128x128 output tile per 256-thread workgroup, wave w the 64x64 block
 // (w / 2, w % 2), or 128x64 with 64x32 blocks (launch_words says when).  K
-// runs in stages of 64 bytes through a ring of WNS stages
+// runs in stages of 64 bytes through a ring of 3 (INT8) or 4 (FP8) stages
 // in LDS, copied with 4-byte LDS-DMA loads (buffer_load_dword ... lds: lane
 // l's word lands at 4l of the instruction's 256 bytes), so no registers hold
 // the stages in flight; words past M, N or K read zero through the buffer
@@ -234,10 +234,19 @@ hipError_t launch_t(const GemmArgs& p, hipStream_t stream) {
 // ===========================================================================
 constexpr int WT = 128;               // tile rows (and columns of the wide tile)
 constexpr int WKC = 64;               // K bytes per stage
-constexpr int WNS = 4;                // ring stages (64 / 48 KiB of LDS for the wide / narrow tile)
 constexpr int WOP = WT * WKC;         // bytes of A's stage (8 KiB)
 constexpr int WCP = WOP / (4 * 256);  // 4-byte copies per wave and stage of A (8)
-static_assert(WCP == 8 && WNS == 4, "copy and wait counts below");
+static_assert(WCP == 8, "copy and wait counts below");
+// Ring stages: INT8 3 (48 / 36 KiB of LDS for the wide / narrow tile, 138
+// registers: three workgroups per CU), FP8 4 (its replay's registers allow
+// two workgroups per CU either way, and the deeper ring keeps more in
+// flight).  Same box, bf16 out: INT8 4096 x 11008 x 4100 401.9 against 443.5
+// us with 4 stages, 16 x 14336 x 4100 32.8 against 34.1; FP8 B [K,N] 64 x
+// 14336 x 4100 45.8 with 4 stages against 48.2 with 3.
+template <int EL>
+constexpr int words_stages() {
+    return EL == ELEM_F8 ? 4 : 3;
+}
 
 typedef int w2i __attribute__((ext_vector_type(2)));
 typedef int w4i __attribute__((ext_vector_type(4)));
@@ -265,6 +274,8 @@ __global__ __launch_bounds__(256) void gemm_words_kernel(GemmArgs p) {
     constexpr int NJ = BN / 32;                  // 16-column blocks per wave
     constexpr int WOPB = BN * WKC;               // bytes of B's stage
     constexpr int WCPB = WOPB / (4 * 256);       // 4-byte copies per wave and stage of B (8 or 4)
+    constexpr int WNS = words_stages<EL>();
+    static_assert(WNS >= 3 && WNS <= 4, "the waits below count at most two later stages");
     using Acc = typename std::conditional<F8, w4f, w4i>::type;
     __shared__ __attribute__((aligned(1024))) uint8_t ring[WNS][WOP + WOPB];
     __shared__ int nan_seen;
