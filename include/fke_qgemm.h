@@ -341,8 +341,12 @@ int fke_select_path_half(const void* A, const void* B, const void* C, int M, int
 /* The workgroup tile FKE_PATH_MFMA runs for this shape (any operand type) on
  * a GPU of `cus` CUs (<= 0: the current device's, 256 without a device), as
  * the FKE_PATH_MFMA_* value that pins it, or -1 for bad arguments; swiglu !=
- * 0 for the fused SwiGLU GEMM with N = 2I.  Host logic only; launches
- * nothing. */
+ * 0 for the fused SwiGLU GEMM with N = 2I.  From the shape alone: where the
+ * MFMA GEMM cannot run the call (K, or N with B [K,N], not a multiple of 16
+ * bytes, or operands not 16-byte aligned), FKE_PATH_MFMA runs the word
+ * kernel instead (128x128 or 128x64 tiles, no K split) or refuses it, and
+ * neither this tile nor fke_select_mfma_split's plan applies.  Host logic
+ * only; launches nothing. */
 int fke_select_mfma_tile(int M, int N, int K, int b_layout, int swiglu, int cus);
 /* The K split FKE_PATH_MFMA takes for an 8-bit GEMM of this shape (INT8 and
  * FP8, not SwiGLU) on `cus` CUs (<= 0: the current device's): the number of
