@@ -267,10 +267,16 @@ __device__ __forceinline__ w2i w_rdtr(const w_lds* a) {
 
 // BN: tile columns, 128 or 64 (the narrow tile doubles the workgroups of
 // shapes with few 128x128 tiles); wave w takes columns (w % 2) BN / 2 ...
-template <int EL, int BL, int OUT, int BN>
+// SWI (INT8, B [N,K] = [gate; up], N = 2I): tile column c < BN / 2 is gate
+// row o0 + c and column BN / 2 + c up row I + o0 + c, o0 the tile's first
+// of its BN / 2 outputs, so the waves with w % 2 = 0 hold gate sums and
+// those with w % 2 = 1 the matching up sums; the up values meet the gate
+// values in LDS and each output is swiglu_pair of the two epilogue values.
+template <int EL, int BL, int OUT, int BN, bool SWI = false>
 __global__ __launch_bounds__(256) void gemm_words_kernel(GemmArgs p) {
     constexpr bool F8 = EL == ELEM_F8, KN = BL == FKE_B_KN;
     static_assert(BN == 128 || BN == 64, "tile columns");
+    static_assert(!SWI || (EL == ELEM_I8 && !KN && OUT != FKE_OUT_I32), "SwiGLU: INT8, B [N,K], float out");
     constexpr int NJ = BN / 32;                  // 16-column blocks per wave
     constexpr int WOPB = BN * WKC;               // bytes of B's stage
     constexpr int WCPB = WOPB / (4 * 256);       // 4-byte copies per wave and stage of B (8 or 4)
@@ -323,6 +329,11 @@ __global__ __launch_bounds__(256) void gemm_words_kernel(GemmArgs p) {
             const int col = n0 + 16 * c + 4 * dw;
             bkr[i] = kr;
             brow[i] = col < N ? static_cast<uint32_t>(col) : 0x80000000u;
+        } else if constexpr (SWI) {
+            const int r = 4 * (WCPB * wave + i) + lr, half = BN / 2, I = N >> 1;
+            const int o = blockIdx.x * half + (r < half ? r : r - half);  // the row's output
+            bkr[i] = 0;
+            brow[i] = o < I ? static_cast<uint32_t>((r < half ? o : I + o) * K) : 0x80000000u;
         } else {
             const int r = 4 * (WCPB * wave + i) + lr;
             bkr[i] = 0;
@@ -479,6 +490,52 @@ __global__ __launch_bounds__(256) void gemm_words_kernel(GemmArgs p) {
     }
 
     // Lane (g, c) of block (i, j) holds rows 16i + 4g + v, column 16j + c of the wave's block.
+    if constexpr (SWI) {
+        // the up waves' epilogue values, [wm][64 rows][BN / 2 outputs] fp32, in the ring's first bytes
+        static_assert(2 * 64 * (BN / 2) * 4 <= WNS * (WOP + WOPB), "the exchange fits the ring");
+        float* const xu = reinterpret_cast<float*>(&ring[0][0]);
+        const int I = N >> 1, o0 = blockIdx.x * (BN / 2);
+        __syncthreads();  // every wave is done with the ring
+        if (wn == 1) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int row = 16 * i + 4 * g + v, m = m0 + wm * 64 + row;
+                    const float sam = m < M ? (p.scale_a ? p.scale_a[m] : p.sa) : 0.0f;
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j) {
+                        const int col = 16 * j + rr, o = o0 + col;
+                        float y = 0.0f;
+                        if (m < M && o < I)
+                            y = epilogue_value(static_cast<float>(acc[i][j][v]),
+                                               sam * (p.scale_b ? p.scale_b[I + o] : p.sb), p.bias, I + o);
+                        xu[(wm * 64 + row) * (BN / 2) + col] = y;
+                    }
+                }
+        }
+        __syncthreads();
+        if (wn == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int row = 16 * i + 4 * g + v, m = m0 + wm * 64 + row;
+                    if (m >= M) continue;
+                    const float sam = p.scale_a ? p.scale_a[m] : p.sa;
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j) {
+                        const int col = 16 * j + rr, o = o0 + col;
+                        if (o >= I) continue;
+                        const float yg = epilogue_value(static_cast<float>(acc[i][j][v]),
+                                                        sam * (p.scale_b ? p.scale_b[o] : p.sb), p.bias, o);
+                        store_out<OUT>(p.C, static_cast<size_t>(m) * I + o,
+                                       swiglu_pair(yg, xu[(wm * 64 + row) * (BN / 2) + col]), 0);
+                    }
+                }
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -509,7 +566,8 @@ bool words_supports(const GemmArgs& p, int elem) {
     const uintptr_t a = reinterpret_cast<uintptr_t>(p.A), b = reinterpret_cast<uintptr_t>(p.B);
     if (elem != ELEM_I8 && elem != ELEM_F8) return false;
     if (elem == ELEM_F8 && p.out_dtype == FKE_OUT_I32) return false;
-    if (p.M < 1 || p.N < 1 || p.K < 4 || p.K % 4 != 0 || p.swiglu) return false;
+    if (p.M < 1 || p.N < 1 || p.K < 4 || p.K % 4 != 0) return false;
+    if (p.swiglu && (elem != ELEM_I8 || p.b_layout != FKE_B_NK || p.out_dtype == FKE_OUT_I32 || p.N % 2)) return false;
     if (p.b_layout != FKE_B_NK && (p.b_layout != FKE_B_KN || p.N % 4 != 0)) return false;
     if ((a | b) & 3) return false;
     if ((static_cast<int64_t>(p.M) + WT - 1) / WT > 65535) return false;  // grid y
@@ -536,15 +594,28 @@ const void* words_kernel_for(int elem, bool kn, int out) {
 // (decode-sized M): twice the workgroups, each streaming half the columns,
 // each re-reading its A rows.  Same box, bf16 out + bias, 14336 x 4100:
 // B [N,K] M = 16 34.0 against 48.4 us, B [K,N] M = 64 42.0 against 58.9; at
-// M = 256 (224 wide tiles) 63.1 against 60.0 on the wide tile.
+// M = 256 (224 wide tiles) 63.1 against 60.0 on the wide tile.  A SwiGLU
+// tile's BN columns are BN / 2 outputs.
 hipError_t launch_words(const GemmArgs& p, int elem, hipStream_t s) {
     if (!words_supports(p, elem)) return hipErrorInvalidValue;
     GemmArgs a = p;
     void* args[] = {&a};
-    const int64_t rows = (p.M + WT - 1) / WT, wide = (p.N + WT - 1) / WT * rows;
+    const int cols = p.swiglu ? p.N / 2 : p.N;  // output columns
+    const int per = p.swiglu ? WT / 2 : WT;     // output columns of a wide tile
+    const int64_t rows = (p.M + WT - 1) / WT, wide = (cols + per - 1) / per * rows;
     const bool kn = p.b_layout == FKE_B_KN, narrow = 2 * wide <= device_cus();
-    const void* f = narrow ? words_kernel_for<64>(elem, kn, p.out_dtype) : words_kernel_for<128>(elem, kn, p.out_dtype);
-    const dim3 grid(narrow ? (p.N + 63) / 64 : (p.N + WT - 1) / WT, static_cast<unsigned>(rows));
+    const void* f;
+    if (p.swiglu) {
+        const bool f32 = p.out_dtype == FKE_OUT_F32;
+        f = narrow ? (f32 ? reinterpret_cast<const void*>(&gemm_words_kernel<ELEM_I8, FKE_B_NK, FKE_OUT_F32, 64, true>)
+                          : reinterpret_cast<const void*>(&gemm_words_kernel<ELEM_I8, FKE_B_NK, FKE_OUT_BF16, 64, true>))
+                   : (f32 ? reinterpret_cast<const void*>(&gemm_words_kernel<ELEM_I8, FKE_B_NK, FKE_OUT_F32, 128, true>)
+                          : reinterpret_cast<const void*>(&gemm_words_kernel<ELEM_I8, FKE_B_NK, FKE_OUT_BF16, 128, true>));
+    } else {
+        f = narrow ? words_kernel_for<64>(elem, kn, p.out_dtype) : words_kernel_for<128>(elem, kn, p.out_dtype);
+    }
+    const int tile_cols = narrow ? per / 2 : per;
+    const dim3 grid((cols + tile_cols - 1) / tile_cols, static_cast<unsigned>(rows));
     return hipLaunchKernel(f, grid, dim3(256), args, 0, s);
 }
 

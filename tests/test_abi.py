@@ -144,7 +144,7 @@ def test_swiglu_rejects_bad_arguments():
                                          None, 0, None) == INVALID
     assert L.fke_qgemm_i8_swiglu_on_path(_lib.PATH_GEMV, P, P, P, 513, 64, 4096, None, None, 1.0, 1.0,
                                          None, 0, None) == INVALID
-    assert L.fke_qgemm_i8_swiglu_on_path(_lib.PATH_MFMA, P, P, P, 64, 64, 100, None, None, 1.0, 1.0,
+    assert L.fke_qgemm_i8_swiglu_on_path(_lib.PATH_MFMA, P, P, P, 64, 64, 102, None, None, 1.0, 1.0,
                                          None, 0, None) == INVALID
 
 
@@ -157,7 +157,9 @@ def test_swiglu_rejects_bad_arguments():
     (64, 14336, 4096, _lib.PATH_MFMA),     # the 128x128 ring (SwiGLU pairs need 128 columns)
     (128, 14336, 4096, _lib.PATH_MFMA),
     (4096, 14336, 4096, _lib.PATH_MFMA),
-    (64, 64, 100, _lib.PATH_GENERIC),
+    (64, 64, 100, _lib.PATH_MFMA),         # K % 16 != 0, K % 4 == 0: the word kernel's SwiGLU form
+    (64, 64, 102, _lib.PATH_GENERIC),      # K % 4 != 0
+    (4, 64, 100, _lib.PATH_GEMV),          # up to 4 rows: the row kernel's 4-byte form
     (2, 300000, 4096, _lib.PATH_GEMV),     # row kernel: 64-bit row bases
     (8, 300000, 4096, _lib.PATH_GEMV),     # LDS-streamed kernel: buffer bases per workgroup
     (8, 600000, 2048, _lib.PATH_GENERIC),  # K < 4096 and 2I*K past the skinny kernel's 32-bit offsets

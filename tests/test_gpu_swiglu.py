@@ -181,6 +181,8 @@ CASES = [
     (17, 130, 256, "mfma_128x128"), (256, 128, 128, "mfma_128x128"), (513, 333, 384, "mfma_128x128"),
     (17, 130, 256, "mfma_128x128_ring4"), (300, 200, 640, "mfma_128x128_ring4"), (513, 333, 384, "mfma_128x128_ring4"),
     (33, 40, 100, "generic"), (7, 9, 77, "generic"), (1, 5, 3, "generic"), (70, 100, 256, "generic"),
+    # K % 16 != 0 (K % 4 == 0): the word kernel's SwiGLU form, 128x64 tiles and (I = 1100, M = 1024) 128x128
+    (9, 300, 100, "mfma"), (70, 100, 1028, "mfma"), (300, 200, 68, "mfma"), (1024, 1100, 100, "mfma"),
 ]
 
 
