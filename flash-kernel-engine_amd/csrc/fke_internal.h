@@ -36,7 +36,7 @@ constexpr int elem_bytes(int elem) { return elem >= ELEM_F16 ? 2 : 1; }
 hipError_t launch_generic(const GemmArgs& p, int elem, hipStream_t stream);
 // INT8 / FP8 on the matrix cores with K % 4 == 0, 4-byte-aligned A / B and,
 // for B [K,N], N % 4 == 0 (the shapes the MFMA GEMM's 16-byte copies cannot
-// take); no SwiGLU.
+// take); the SwiGLU GEMM too (INT8, B [N,K], float out).
 bool words_supports(const GemmArgs& p, int elem);
 hipError_t launch_words(const GemmArgs& p, int elem, hipStream_t stream);
 hipError_t launch_gemv_i8(const GemmArgs& p, hipStream_t stream);
